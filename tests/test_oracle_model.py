@@ -1,0 +1,126 @@
+"""Pin the oracle's IntQwen3 restatement and GEMMs.
+
+* GEMMs: naive loops / plain int64 products (the reference's
+  tests/test_ops.py:52-78 restated).
+* Model: tokens, logits and demo chain hashes written by the reference's own
+  IntQwen3(backend="reference") on seeded random-init artifacts
+  (tests/golden/model_*.json), including batch invariance with right-padded
+  co-prompts and the split-prefill path.
+"""
+
+import json
+import os
+
+import numpy as np
+import pytest
+
+from idempotent_llm_amd import artifact as art
+from idempotent_llm_amd.hashchain import chain_hashes, token_chain
+from oracle import gemm
+from oracle.model import IntQwen3Oracle
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+I64 = np.int64
+
+
+def test_int_gemm_matches_naive_loop():
+    rng = np.random.default_rng(0)
+    a = rng.integers(-128, 128, (7, 33)).astype(np.int8)
+    b = rng.integers(-128, 128, (33, 5)).astype(np.int8)
+    got = gemm.int_gemm(a, b)
+    assert got.dtype == np.int32
+    for i in range(7):
+        for j in range(5):
+            assert int(got[i, j]) == sum(int(a[i, k]) * int(b[k, j]) for k in range(33))
+
+
+def test_exact_f32_chunked_gemm_worst_case():
+    # all -128 operands: every partial sum reaches the f32 exactness limit
+    a = np.full((3, 3072), -128, np.int8)
+    b = np.full((3072, 4), -128, np.int8)
+    got = gemm.exact_matmul_f32(a, b.astype(np.float32))
+    assert (got == 3072 * 128 * 128).all()
+    rng = np.random.default_rng(1)
+    a = rng.integers(-128, 128, (5, 2048)).astype(np.int8)
+    b = rng.integers(-128, 128, (2048, 9)).astype(np.int8)
+    want = a.astype(I64) @ b.astype(I64)
+    assert np.array_equal(gemm.exact_matmul_f32(a, b.astype(np.float32)), want)
+
+
+def test_u8_and_u16_tricks_exact():
+    rng = np.random.default_rng(7)
+    p = rng.integers(0, 129, (9, 21)).astype(np.int32)
+    v = rng.integers(-128, 128, (21, 6)).astype(np.int8)
+    assert np.array_equal(gemm.int_gemm_u8i8(p, v), p.astype(I64) @ v.astype(I64))
+    p = rng.integers(0, (1 << 14) + 1, (9, 300)).astype(np.int32)
+    v = rng.integers(-128, 128, (300, 6)).astype(np.int8)
+    got = gemm.int_gemm_u16i8(p, v)
+    assert got.dtype == I64
+    assert np.array_equal(got, p.astype(I64) @ v.astype(I64))
+
+
+def _load(name):
+    with open(os.path.join(HERE, "golden", f"model_{name}.json")) as f:
+        return json.load(f)
+
+
+@pytest.fixture(scope="module", params=["tiny", "mid"])
+def case(request, tmp_path_factory):
+    rec = _load(request.param)
+    d = str(tmp_path_factory.mktemp(request.param))
+    art.make_artifact(d, rec["dims"], rec["seed"])
+    assert art.artifact_digest(d) == rec["artifact_sha256"], "artifact generator drifted"
+    return rec, IntQwen3Oracle(d)
+
+
+def test_prefill_logits(case):
+    rec, m = case
+    ids = np.array(rec["prompt"], dtype=I64)[None]
+    pos = np.arange(ids.shape[1], dtype=I64)[None]
+    logits, xm, xk, _ = m.forward(ids, pos)
+    assert logits.dtype == np.int32
+    assert chain_hashes(logits[0]) == rec["prefill_chain"]
+    assert logits[0, -1].tolist() == rec["prefill_last_row"]
+    assert xm[0, :, 0].tolist() == rec["prefill_xm"] and xk[0, :, 0].tolist() == rec["prefill_xk"]
+
+
+def test_generate_b1(case):
+    rec, m = case
+    ids = np.array(rec["prompt"], dtype=I64)[None]
+    toks, steps = m.generate(ids, len(rec["b1_tokens"]))
+    assert toks[0].tolist() == rec["b1_tokens"]
+    assert chain_hashes([s[0] for s in steps]) == rec["b1_logit_chain"]
+    assert token_chain(toks[0]) == rec["b1_token_chain"]
+
+
+def test_generate_padded_batch(case):
+    rec, m = case
+    ids = np.array(rec["batch_ids"], dtype=I64)
+    valid = np.array(rec["batch_valid"], dtype=bool)
+    toks, steps = m.generate(ids, len(rec["b1_tokens"]), chunk_valid=valid)
+    assert toks.tolist() == rec["batch_tokens"]
+    for b in range(ids.shape[0]):
+        assert chain_hashes([s[b] for s in steps]) == rec["batch_row_chains"][b]
+    assert rec["batch_row_chains"][0] == rec["b1_logit_chain"]   # batch invariance
+
+
+def test_split_prefill(case):
+    rec, m = case
+    ids = np.array(rec["prompt"], dtype=I64)
+    T = len(ids)
+    half = T // 2
+    pos = np.arange(T, dtype=I64)[None]
+    full, _, _, _ = m.forward(ids[None], pos)
+    _, _, _, cache = m.forward(ids[None, :half], pos[:, :half])
+    rows = []
+    for t in range(half, T):
+        lg, _, _, cache = m.forward(ids[None, t:t + 1], np.array([[t]], I64), cache)
+        rows.append(lg[0, 0])
+    assert chain_hashes(rows) == rec["split_tail_chain"]
+    assert chain_hashes(rows) == chain_hashes(full[0, half:])   # prefill/decode invariance
+
+
+def test_greedy_pick_ties(case):
+    rec, m = case
+    rows = np.array(rec["tie_rows"], dtype=np.int32)
+    assert m.greedy_pick(rows).tolist() == rec["tie_picks"]
