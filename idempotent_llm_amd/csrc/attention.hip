@@ -1,0 +1,414 @@
+// Integer GQA attention over the int8 KV cache (gfx950).
+//
+// Semantics (bit-exact): scores = q8 . k8 (int32); DI-Softmax with the TRUE
+// row max over visible slots (ops/di_softmax.py:33-61 — DI-Exp is not
+// multiplicative, so no online rescaling); probabilities
+// p = round_half_away_div(exp << 14, max(sum exp, 1)) in [0, 2^14]; context
+// = sum_s p_s * v_s exactly in int64 (model.py:363-402 and the hi/lo GEMM of
+// backends.py:152-164 produce the same integer). Slot s is visible to the
+// query at absolute slot S_past + t iff s <= S_past + t and valid[b][s]
+// (model.py:259-266).
+//
+// Cache layout in HBM: K [B][n_kv][cap][128] (row per slot) and V stored
+// transposed, V^T [B][n_kv][128][cap], so that both the MFMA B-fragments of
+// P.V (16 consecutive slots per lane) and the decode reduction over slots
+// read slot-contiguous bytes. cap % 16 == 0.
+//
+// Prefill (k_attn_prefill): block = 64 queries of one head, 4 waves of 16.
+// Scores are computed transposed, S^T = K . Q^T, with v_mfma_i32_16x16x64_i8:
+// lane l then holds ONE query (l % 16) and 16 slots of each 64-slot tile, so
+// the row max, the denominator and the DI-Exp / normalisation divisors are
+// per-lane scalars. Three passes over the key tiles (max, denominator,
+// normalise + P.V) recompute S^T on MFMA. P.V uses the same fragments: the
+// 15-bit p is split as p = 128*hi + lo, and sum p.v =
+// 128*(sum (hi-64).v + 64*colsum(v)) + sum lo.v, both products on i8 MFMA
+// (hi-64 in [-64, 64], lo in [0, 127]).
+//
+// Decode (k_attn_decode): block = one (batch row, kv head), all q heads of
+// its group; scores live in LDS (or a global scratch when they do not fit);
+// every reduction is an exact integer max/sum.
+
+#include "common.h"
+
+using namespace di;
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+namespace {
+
+constexpr i64 NEG_SENTINEL = INT64_MIN + 1;
+
+__device__ __forceinline__ v4i mfma16(v4i a, v4i b, v4i c) {
+  return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
+}
+
+struct PrefillArgs {
+  const int8_t* q8;      // [B][n_q][T][128]
+  const int64_t* tpos;   // [B][n_q][T]
+  const int8_t* kc;      // [B][n_kv][cap][128]
+  const int8_t* vc;      // [B][n_kv][128][cap]
+  const uint8_t* valid;  // [B][valid_stride]
+  int64_t* out;          // [B][T][n_q * 128]
+  int T, S, S_past, n_q, n_kv;
+  i64 cap, valid_stride;
+};
+
+constexpr int KS_STRIDE = 128 + 16;
+constexpr int VS_STRIDE = 64 + 16;
+
+__global__ __launch_bounds__(256) void k_attn_prefill(PrefillArgs a) {
+  __shared__ __attribute__((aligned(16))) int8_t Ks[64 * KS_STRIDE];
+  __shared__ __attribute__((aligned(16))) int8_t Vs[128 * VS_STRIDE];
+  __shared__ uint8_t vflag[64];
+  const int qt = gridDim.x - 1 - blockIdx.x;  // heaviest (latest) query tiles first
+  const int h = blockIdx.y, b = blockIdx.z;
+  const int group = a.n_q / a.n_kv;
+  const int kvh = h / group;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int qi = lane & 15, g = lane >> 4;
+  const int t = qt * 64 + wave * 16 + qi;  // this lane's query
+  const bool tok = t < a.T;
+  const i64 qrow = ((i64)b * a.n_q + h) * a.T + (tok ? t : 0);
+  v4i qf0 = v4i{0, 0, 0, 0}, qf1 = v4i{0, 0, 0, 0};
+  if (tok) {
+    qf0 = *(const v4i*)(a.q8 + qrow * 128 + g * 16);
+    qf1 = *(const v4i*)(a.q8 + qrow * 128 + 64 + g * 16);
+  }
+  const i64 tpos = tok ? a.tpos[qrow] : 1;
+  const Recip Rt = make_recip(tpos);
+  const i64 limit = (i64)a.S_past + t;  // last visible slot of this query
+  const int kend = min(a.S, a.S_past + qt * 64 + 64);
+  const int ntiles = (kend + 63) / 64;
+  const int8_t* kbase = a.kc + ((i64)b * a.n_kv + kvh) * a.cap * 128;
+  const int8_t* vbase = a.vc + ((i64)b * a.n_kv + kvh) * 128 * a.cap;
+  const uint8_t* vrow = a.valid + (i64)b * a.valid_stride;
+
+  auto load_k = [&](int s0) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int c = tid + i * 256;
+      const int key = c >> 3, dc = (c & 7) * 16;
+      v4i v = v4i{0, 0, 0, 0};
+      if (s0 + key < a.S) v = *(const v4i*)(kbase + (i64)(s0 + key) * 128 + dc);
+      *(v4i*)&Ks[key * KS_STRIDE + dc] = v;
+    }
+    if (tid < 64) vflag[tid] = (s0 + tid < a.S) ? vrow[s0 + tid] : 0;
+  };
+  auto load_v = [&](int s0) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int c = tid + i * 256;
+      const int d = c >> 2, blk = c & 3;
+      v4i v = v4i{0, 0, 0, 0};
+      if (s0 + blk * 16 < a.cap) v = *(const v4i*)(vbase + (i64)d * a.cap + s0 + blk * 16);
+      // slot 16*blk + 4*gg + r -> position 16*gg + 4*blk + r
+#pragma unroll
+      for (int gg = 0; gg < 4; ++gg) *(int*)&Vs[d * VS_STRIDE + 16 * gg + 4 * blk] = v[gg];
+    }
+  };
+  // S^T for 4 blocks of 16 slots: st[blk][r] = score(slot s0+16blk+4g+r, query t)
+  auto scores = [&](v4i (&st)[4]) {
+#pragma unroll
+    for (int blk = 0; blk < 4; ++blk) {
+      const int8_t* kr = &Ks[(blk * 16 + qi) * KS_STRIDE + g * 16];
+      const v4i k0 = *(const v4i*)kr;
+      const v4i k1 = *(const v4i*)(kr + 64);
+      v4i acc = v4i{0, 0, 0, 0};
+      acc = mfma16(k0, qf0, acc);
+      st[blk] = mfma16(k1, qf1, acc);
+    }
+  };
+  auto visible = [&](int s0, int blk, int r) -> bool {
+    const int key = blk * 16 + g * 4 + r;
+    const int s = s0 + key;
+    return s < a.S && (i64)s <= limit && vflag[key] != 0;
+  };
+
+  // ---- pass 1: row max over visible slots
+  i64 mx = NEG_SENTINEL;
+  for (int it = 0; it < ntiles; ++it) {
+    const int s0 = it * 64;
+    __syncthreads();
+    load_k(s0);
+    __syncthreads();
+    v4i st[4];
+    scores(st);
+#pragma unroll
+    for (int blk = 0; blk < 4; ++blk)
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        if (visible(s0, blk, r)) mx = imax(mx, (i64)st[blk][r]);
+  }
+  mx = group4_max(mx);
+  if (mx == NEG_SENTINEL) mx = 0;  // no visible slot: max := 0, every p = 0
+
+  // ---- pass 2: denominator
+  i64 den = 0;
+  for (int it = 0; it < ntiles; ++it) {
+    const int s0 = it * 64;
+    __syncthreads();
+    load_k(s0);
+    __syncthreads();
+    v4i st[4];
+    scores(st);
+#pragma unroll
+    for (int blk = 0; blk < 4; ++blk)
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        if (visible(s0, blk, r)) den = wadd(den, di_exp_r(wsub((i64)st[blk][r], mx), tpos, Rt));
+  }
+  den = imax(group4_sum(den), 1);
+  const Recip Rd = make_recip(den);
+
+  // ---- pass 3: p, then P.V on MFMA with the hi/lo split
+  v4i ohi[8], olo[8];
+  int csum[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    ohi[j] = v4i{0, 0, 0, 0};
+    olo[j] = v4i{0, 0, 0, 0};
+    csum[j] = 0;
+  }
+  for (int it = 0; it < ntiles; ++it) {
+    const int s0 = it * 64;
+    __syncthreads();
+    load_k(s0);
+    load_v(s0);
+    __syncthreads();
+    v4i st[4];
+    scores(st);
+    v4i phi, plo;
+#pragma unroll
+    for (int blk = 0; blk < 4; ++blk) {
+      unsigned whi = 0, wlo = 0;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        i64 p = 0;
+        if (visible(s0, blk, r)) {
+          const i64 ex = di_exp_r(wsub((i64)st[blk][r], mx), tpos, Rt);
+          p = to_i32(rhad_r(shl(ex, 14), Rd));
+        }
+        const int hi = (int)(p >> 7);
+        const int lo = (int)(p - ((i64)hi << 7));
+        whi |= (unsigned)(uint8_t)(int8_t)(hi - 64) << (8 * r);
+        wlo |= (unsigned)(uint8_t)(int8_t)lo << (8 * r);
+      }
+      phi[blk] = (int)whi;
+      plo[blk] = (int)wlo;
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const v4i vb = *(const v4i*)&Vs[(j * 16 + qi) * VS_STRIDE + g * 16];
+      ohi[j] = mfma16(phi, vb, ohi[j]);
+      olo[j] = mfma16(plo, vb, olo[j]);
+      int cs = csum[j];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) cs = __builtin_amdgcn_sdot4(vb[q], 0x01010101, cs, false);
+      csum[j] = cs;
+    }
+  }
+  // write: lane holds O[query 4g + r][d = 16j + qi]
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const i64 cs = group4_sum((i64)csum[j]);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int tq = qt * 64 + wave * 16 + g * 4 + r;
+      if (tq < a.T) {
+        const i64 v = (i64)ohi[j][r] * 128 + cs * 8192 + (i64)olo[j][r];
+        a.out[((i64)b * a.T + tq) * (a.n_q * 128) + h * 128 + j * 16 + qi] = v;
+      }
+    }
+  }
+}
+
+struct DecodeArgs {
+  const int8_t* q8;      // [B][n_q][128]
+  const int64_t* tpos;   // [B][n_q]
+  const int8_t* kc;      // [B][n_kv][cap][128]
+  const int8_t* vc;      // [B][n_kv][128][cap]
+  const uint8_t* valid;  // [B][valid_stride]
+  int64_t* out;          // [B][n_q * 128]
+  int32_t* scratch;      // [B][n_q][S] when scores do not fit in LDS, else null
+  const int64_t* s_dev;  // optional device bound on the scanned slots
+  int S, n_q, n_kv;
+  i64 cap, valid_stride;
+};
+
+constexpr int MAXG = 8;
+constexpr i64 DECODE_LDS_BYTES = 48 * 1024;
+
+template <int G>
+__global__ __launch_bounds__(256) void k_attn_decode(DecodeArgs a) {
+  extern __shared__ __attribute__((aligned(16))) int32_t sh_scores[];
+  __shared__ i64 red[16];
+  __shared__ i64 pv_acc[G][128];
+  const int kvh = blockIdx.x, b = blockIdx.y;
+  const int tid = threadIdx.x, lane = tid & 63;
+  int S = a.S;
+  if (a.s_dev) {
+    const i64 sd = a.s_dev[0];
+    S = (int)imax(0, imin((i64)S, sd));
+  }
+  const int Spad = (a.S + 15) & ~15;
+  int32_t* sc = a.scratch ? a.scratch + ((i64)b * a.n_q + kvh * G) * Spad : sh_scores;
+  const int8_t* kbase = a.kc + ((i64)b * a.n_kv + kvh) * a.cap * 128;
+  const int8_t* vbase = a.vc + ((i64)b * a.n_kv + kvh) * 128 * a.cap;
+  const uint8_t* vrow = a.valid + (i64)b * a.valid_stride;
+
+  // ---- pass 1: scores (8 lanes per slot, 16 bytes each) and row max
+  const int sub = lane & 7;
+  v4i qv[G];
+#pragma unroll
+  for (int hh = 0; hh < G; ++hh)
+    qv[hh] = *(const v4i*)(a.q8 + ((i64)b * a.n_q + kvh * G + hh) * 128 + sub * 16);
+  i64 mx[G];
+#pragma unroll
+  for (int hh = 0; hh < G; ++hh) mx[hh] = NEG_SENTINEL;
+  const int keys_per_iter = 256 / 8;
+  for (int s0 = 0; s0 < S; s0 += keys_per_iter) {
+    const int s = s0 + (tid >> 3);
+    const bool in = s < S;
+    v4i kv = v4i{0, 0, 0, 0};
+    if (in) kv = *(const v4i*)(kbase + (i64)s * 128 + sub * 16);
+    const bool vis = in && vrow[s] != 0;
+#pragma unroll
+    for (int hh = 0; hh < G; ++hh) {
+      int d = 0;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) d = __builtin_amdgcn_sdot4(kv[q], qv[hh][q], d, false);
+      d += __shfl_xor(d, 1, 64);
+      d += __shfl_xor(d, 2, 64);
+      d += __shfl_xor(d, 4, 64);
+      if (in && sub == 0) sc[hh * Spad + s] = d;
+      if (vis) mx[hh] = imax(mx[hh], (i64)d);
+    }
+  }
+#pragma unroll
+  for (int hh = 0; hh < G; ++hh) {
+    mx[hh] = block_max(mx[hh], red);
+    if (mx[hh] == NEG_SENTINEL) mx[hh] = 0;
+  }
+  __syncthreads();
+  // ---- pass 2: denominators
+  i64 tp[G], den[G];
+#pragma unroll
+  for (int hh = 0; hh < G; ++hh) {
+    tp[hh] = a.tpos[(i64)b * a.n_q + kvh * G + hh];
+    den[hh] = 0;
+  }
+#pragma unroll
+  for (int hh = 0; hh < G; ++hh) {
+    const Recip R = make_recip(tp[hh]);
+    i64 acc = 0;
+    for (int s = tid; s < S; s += 256)
+      if (vrow[s] != 0) acc = wadd(acc, di_exp_r(wsub((i64)sc[hh * Spad + s], mx[hh]), tp[hh], R));
+    den[hh] = imax(block_sum(acc, red), 1);
+  }
+  // ---- pass 3: probabilities (in place of the scores)
+#pragma unroll
+  for (int hh = 0; hh < G; ++hh) {
+    const Recip R = make_recip(tp[hh]);
+    const Recip Rd = make_recip(den[hh]);
+    for (int s = tid; s < Spad; s += 256) {
+      i64 p = 0;
+      if (s < S && vrow[s] != 0) {
+        const i64 ex = di_exp_r(wsub((i64)sc[hh * Spad + s], mx[hh]), tp[hh], R);
+        p = to_i32(rhad_r(shl(ex, 14), Rd));
+      }
+      sc[hh * Spad + s] = (int32_t)p;
+    }
+  }
+  __syncthreads();
+  // ---- P.V: thread (d, half) sums its half of the slot range
+  const int d = tid & 127, half = tid >> 7;
+  const int nchunk = Spad / 16;
+  const int cbeg = half * ((nchunk + 1) / 2), cend = min(nchunk, cbeg + (nchunk + 1) / 2);
+  i64 acc[G];
+#pragma unroll
+  for (int hh = 0; hh < G; ++hh) acc[hh] = 0;
+  const int8_t* vr = vbase + (i64)d * a.cap;
+  for (int c = cbeg; c < cend; ++c) {
+    if (c * 16 >= S) break;
+    const v4i vv = *(const v4i*)(vr + c * 16);
+#pragma unroll
+    for (int hh = 0; hh < G; ++hh) {
+      const int32_t* pp = sc + hh * Spad + c * 16;
+      i64 sacc = 0;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int w = vv[q];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int v8 = (int)(int8_t)((w >> (8 * r)) & 0xff);
+          sacc += (i64)pp[q * 4 + r] * v8;
+        }
+      }
+      acc[hh] += sacc;
+    }
+  }
+  if (half == 1)
+#pragma unroll
+    for (int hh = 0; hh < G; ++hh) pv_acc[hh][d] = acc[hh];
+  __syncthreads();
+  if (half == 0)
+#pragma unroll
+    for (int hh = 0; hh < G; ++hh)
+      a.out[(i64)b * a.n_q * 128 + (kvh * G + hh) * 128 + d] = acc[hh] + pv_acc[hh][d];
+}
+
+}  // namespace
+
+extern "C" {
+
+int detllm_attn_prefill(const int8_t* q8, const int64_t* tpos, const int8_t* kc, const int8_t* vc,
+                        const uint8_t* valid, int64_t valid_stride, int B, int T, int S_past,
+                        int n_q, int n_kv, int64_t cap, int64_t* out, hipStream_t s) {
+  if (B <= 0 || T <= 0) return DI_OK;
+  const i64 S = (i64)S_past + T;
+  if (n_q <= 0 || n_kv <= 0 || n_q % n_kv || S_past < 0 || S > cap || cap % 16 != 0 ||
+      valid_stride < S)
+    return DI_EINVAL;
+  if (S > 131071) return DI_ERANGE;  // int32 MFMA accumulators of P.V
+  PrefillArgs a{q8, tpos, kc, vc, valid, out, T, (int)S, S_past, n_q, n_kv, cap, valid_stride};
+  hipLaunchKernelGGL(k_attn_prefill, dim3((T + 63) / 64, n_q, B), dim3(256), 0, s, a);
+  DI_LAUNCH_CHECK();
+  return DI_OK;
+}
+
+// Decode (one query per batch row). S: slots to scan (<= cap); s_dev:
+// optional device scalar that further bounds it (graph replay). scratch may
+// be null when n_q/n_kv * ceil16(S) * 4 bytes fit in 48 KiB of LDS.
+int detllm_attn_decode(const int8_t* q8, const int64_t* tpos, const int8_t* kc, const int8_t* vc,
+                       const uint8_t* valid, int64_t valid_stride, int B, int S, int n_q, int n_kv,
+                       int64_t cap, const int64_t* s_dev, int32_t* scratch, int64_t* out,
+                       hipStream_t s) {
+  if (B <= 0) return DI_OK;
+  if (n_q <= 0 || n_kv <= 0 || n_q % n_kv || S < 0 || S > cap || cap % 16 != 0 ||
+      valid_stride < S)
+    return DI_EINVAL;
+  const int G = n_q / n_kv;
+  if (G > MAXG) return DI_ENOSYS;
+  const i64 Spad = ((i64)S + 15) & ~15;
+  const i64 lds = (i64)G * Spad * 4;
+  size_t dyn = 0;
+  if (lds <= DECODE_LDS_BYTES) {
+    dyn = (size_t)lds;
+    scratch = nullptr;
+  } else if (!scratch) {
+    return DI_ERANGE;
+  }
+  DecodeArgs a{q8, tpos, kc, vc, valid, out, scratch, s_dev, S, n_q, n_kv, cap, valid_stride};
+  const dim3 grid(n_kv, B);
+  switch (G) {
+    case 1: hipLaunchKernelGGL(k_attn_decode<1>, grid, dim3(256), dyn, s, a); break;
+    case 2: hipLaunchKernelGGL(k_attn_decode<2>, grid, dim3(256), dyn, s, a); break;
+    case 4: hipLaunchKernelGGL(k_attn_decode<4>, grid, dim3(256), dyn, s, a); break;
+    case 8: hipLaunchKernelGGL(k_attn_decode<8>, grid, dim3(256), dyn, s, a); break;
+    default: return DI_ENOSYS;
+  }
+  DI_LAUNCH_CHECK();
+  return DI_OK;
+}
+
+}  // extern "C"

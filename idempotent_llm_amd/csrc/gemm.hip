@@ -1,0 +1,310 @@
+// Exact int8 x int8 -> int32 GEMMs on CDNA4 i8 MFMA (gfx950), plus the
+// integer arg-max of greedy decoding.
+//
+// Layout: C[M,N] = A[M,K] . B[N,K]^T with both operands K-contiguous ("NT").
+// The model keeps every weight matrix in this [out, in] layout (a load-time
+// integer permutation of the artifact's [in, out] ``w8t``), so a lane's
+// 16-byte load is directly one MFMA operand fragment.
+//
+// Exactness: every partial sum is an int32 integer sum of int8 products;
+// |sum| <= K * 128 * 128 < 2^31 for K <= 131071, so no accumulation order
+// can change the result (the reference's backends.py:1-11 argument).
+//
+// MFMA fragment convention (v_mfma_i32_16x16x64_i8): lane l supplies row (A)
+// or column (B) l % 16 and a 16-byte K slice chosen by l / 16; the product
+// sums over all 64 K values, so A and B only have to agree on which K value
+// sits in which slot. The 16x16 int32 result lands as C[4*(l/16) + r][l % 16]
+// in element r of lane l.
+//
+// Kernels:
+//   k_gemm_nt   — 128x128x64 block tiles, 4 waves of 64x64, LDS double
+//                 buffer; for M > 64 (prefill).
+//   k_gemv_nt   — M <= 64 (decode): each block owns 16 output columns and a
+//                 K range; weight fragments stream straight from HBM into
+//                 MFMA operands; optional K split writes int32 partials that
+//                 the consuming row kernel sums (exact integer addition).
+//   k_argmax_*  — greedy_pick (model.py:482-490): argmax of logits * head_m
+//                 in int64 with the lowest-id tie-break.
+
+#include "common.h"
+
+using namespace di;
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+namespace {
+
+__device__ __forceinline__ v4i mfma16(v4i a, v4i b, v4i c) {
+  return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ v4i zero4() { return v4i{0, 0, 0, 0}; }
+
+constexpr int TBM = 128, TBN = 128, TBK = 64, TPAD = 16;
+
+__global__ __launch_bounds__(256) void k_gemm_nt(const int8_t* __restrict__ A,
+                                                 const int8_t* __restrict__ B,
+                                                 int32_t* __restrict__ C, int M, int N, int K,
+                                                 i64 sA, i64 sB, i64 sC, int tiles_n) {
+  __shared__ __attribute__((aligned(16))) int8_t As[2][TBM][TBK + TPAD];
+  __shared__ __attribute__((aligned(16))) int8_t Bs[2][TBN][TBK + TPAD];
+  const int bz = blockIdx.z;
+  A += bz * sA;
+  B += bz * sB;
+  C += bz * sC;
+  const int tm = blockIdx.x / tiles_n, tn = blockIdx.x % tiles_n;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int r16 = lane & 15, kq = (lane >> 4) * 16;
+
+  v4i ra[2], rb[2];
+  auto gload = [&](int k0) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int c = tid + i * 256;
+      const int row = c >> 2, kc = (c & 3) * 16;
+      const int gk = k0 + kc;
+      const int ga = tm * TBM + row, gb = tn * TBN + row;
+      ra[i] = (ga < M && gk < K) ? *(const v4i*)(A + (i64)ga * K + gk) : zero4();
+      rb[i] = (gb < N && gk < K) ? *(const v4i*)(B + (i64)gb * K + gk) : zero4();
+    }
+  };
+  auto sstore = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int c = tid + i * 256;
+      const int row = c >> 2, kc = (c & 3) * 16;
+      *(v4i*)&As[buf][row][kc] = ra[i];
+      *(v4i*)&Bs[buf][row][kc] = rb[i];
+    }
+  };
+
+  v4i acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = zero4();
+
+  const int nk = (K + TBK - 1) / TBK;
+  gload(0);
+  sstore(0);
+  __syncthreads();
+  for (int kt = 0; kt < nk; ++kt) {
+    const int buf = kt & 1;
+    if (kt + 1 < nk) gload((kt + 1) * TBK);
+    v4i af[4], bf[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) af[i] = *(const v4i*)&As[buf][wm * 64 + i * 16 + r16][kq];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) bf[j] = *(const v4i*)&Bs[buf][wn * 64 + j * 16 + r16][kq];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[i][j] = mfma16(af[i], bf[j], acc[i][j]);
+    if (kt + 1 < nk) sstore(buf ^ 1);
+    __syncthreads();
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int row = tm * TBM + wm * 64 + i * 16 + (lane >> 4) * 4 + r;
+        const int col = tn * TBN + wn * 64 + j * 16 + r16;
+        if (row < M && col < N) C[(i64)row * N + col] = acc[i][j][r];
+      }
+}
+
+template <int MB>
+__global__ __launch_bounds__(256) void k_gemv_nt(const int8_t* __restrict__ A,
+                                                 const int8_t* __restrict__ B,
+                                                 int32_t* __restrict__ C, int M, int N, int K,
+                                                 int kchunk, i64 split_stride) {
+  __shared__ int32_t red[3][MB * 4][64];
+  const int n0 = blockIdx.x * 16;
+  const int ks = blockIdx.y;
+  const int kbeg = ks * kchunk;
+  const int kend = min(K, kbeg + kchunk);
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int r16 = lane & 15, kq = (lane >> 4) * 16;
+  const int col = n0 + r16;
+  const bool colok = col < N;
+  const int8_t* brow = B + (i64)(colok ? col : 0) * K;
+  v4i acc[MB];
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb) acc[mb] = zero4();
+#pragma unroll 4
+  for (int k0 = kbeg + wave * 64; k0 < kend; k0 += 256) {
+    const int kk = k0 + kq;
+    const bool kok = kk < kend;
+    const v4i b = (colok && kok) ? *(const v4i*)(brow + kk) : zero4();
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) {
+      const int row = mb * 16 + r16;
+      const v4i a = (row < M && kok) ? *(const v4i*)(A + (i64)row * K + kk) : zero4();
+      acc[mb] = mfma16(a, b, acc[mb]);
+    }
+  }
+  if (wave > 0) {
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) red[wave - 1][mb * 4 + r][lane] = acc[mb][r];
+  }
+  __syncthreads();
+  if (wave == 0) {
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int32_t s = acc[mb][r] + red[0][mb * 4 + r][lane] + red[1][mb * 4 + r][lane] +
+                          red[2][mb * 4 + r][lane];
+        const int row = mb * 16 + (lane >> 4) * 4 + r;
+        if (row < M && colok) C[ks * split_stride + (i64)row * N + col] = s;
+      }
+  }
+}
+
+__global__ void k_transpose_i8(const int8_t* __restrict__ src, int8_t* __restrict__ dst, int R,
+                               int Cc, i64 sS, i64 sD) {
+  __shared__ int8_t tile[64][65];
+  src += blockIdx.z * sS;
+  dst += blockIdx.z * sD;
+  const int r0 = blockIdx.y * 64, c0 = blockIdx.x * 64;
+  for (int i = threadIdx.x; i < 64 * 64; i += blockDim.x) {
+    const int rr = i >> 6, cc = i & 63;
+    if (r0 + rr < R && c0 + cc < Cc) tile[rr][cc] = src[(i64)(r0 + rr) * Cc + c0 + cc];
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < 64 * 64; i += blockDim.x) {
+    const int cc = i >> 6, rr = i & 63;
+    if (r0 + rr < R && c0 + cc < Cc) dst[(i64)(c0 + cc) * R + r0 + rr] = tile[rr][cc];
+  }
+}
+
+struct Best {
+  i64 v;
+  i64 i;
+};
+
+__device__ __forceinline__ Best better(Best a, Best b) {
+  return (a.v > b.v || (a.v == b.v && a.i < b.i)) ? a : b;
+}
+
+__device__ __forceinline__ Best block_best(Best x, i64* sv, i64* si) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    Best y{shfl_xor64(x.v, o), shfl_xor64(x.i, o)};
+    x = better(x, y);
+  }
+  const int w = threadIdx.x >> 6;
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) {
+    sv[w] = x.v;
+    si[w] = x.i;
+  }
+  __syncthreads();
+  Best r{sv[0], si[0]};
+  for (int i = 1; i < (int)(blockDim.x >> 6); ++i) r = better(r, Best{sv[i], si[i]});
+  return r;
+}
+
+__global__ __launch_bounds__(256) void k_argmax_partial(const int32_t* __restrict__ logits,
+                                                        const int64_t* __restrict__ head_m, int V,
+                                                        int chunk, int64_t* pv, int64_t* pi) {
+  __shared__ i64 sv[4], si[4];
+  const int r = blockIdx.y, ch = blockIdx.x, nch = gridDim.x;
+  const int beg = ch * chunk, end = min(V, beg + chunk);
+  Best b{INT64_MIN, (i64)V};
+  const int32_t* row = logits + (i64)r * V;
+  for (int i = beg + threadIdx.x; i < end; i += blockDim.x) {
+    b = better(b, Best{wmul((i64)row[i], head_m[i]), (i64)i});
+  }
+  b = block_best(b, sv, si);
+  if (threadIdx.x == 0) {
+    pv[(i64)r * nch + ch] = b.v;
+    pi[(i64)r * nch + ch] = b.i;
+  }
+}
+
+__global__ __launch_bounds__(256) void k_argmax_final(const int64_t* pv, const int64_t* pi,
+                                                      int nch, int64_t* out) {
+  __shared__ i64 sv[4], si[4];
+  const int r = blockIdx.x;
+  Best b{INT64_MIN, INT64_MAX};
+  for (int i = threadIdx.x; i < nch; i += blockDim.x)
+    b = better(b, Best{pv[(i64)r * nch + i], pi[(i64)r * nch + i]});
+  b = block_best(b, sv, si);
+  if (threadIdx.x == 0) out[r] = b.i;
+}
+
+}  // namespace
+
+extern "C" {
+
+// C[b] = A[b] . B[b]^T; A [batch][M][K], B [batch][N][K], C [batch][M][N]
+// (contiguous per batch, batch strides sA, sB, sC in elements). K % 16 == 0.
+int detllm_igemm_nt(const int8_t* A, const int8_t* B, int32_t* C, int M, int N, int K, int batch,
+                    int64_t sA, int64_t sB, int64_t sC, hipStream_t s) {
+  if (M <= 0 || N <= 0 || batch <= 0) return DI_OK;
+  if (K <= 0 || (K % 16) != 0 || K > 131071 || !A || !B || !C) return DI_EINVAL;
+  const int tiles_m = (M + TBM - 1) / TBM, tiles_n = (N + TBN - 1) / TBN;
+  if ((i64)tiles_m * tiles_n > 0x7fffffff || batch > 65535) return DI_ERANGE;
+  hipLaunchKernelGGL(k_gemm_nt, dim3(tiles_m * tiles_n, 1, batch), dim3(256), 0, s, A, B, C, M,
+                     N, K, (i64)sA, (i64)sB, (i64)sC, tiles_n);
+  DI_LAUNCH_CHECK();
+  return DI_OK;
+}
+
+// Skinny GEMM for M <= 64: writes ksplit int32 partials C[ks][M][N]
+// (split_stride elements apart); ksplit = 1 gives the plain product.
+int detllm_igemv_nt(const int8_t* A, const int8_t* B, int32_t* C, int M, int N, int K,
+                    int ksplit, int64_t split_stride, hipStream_t s) {
+  if (M <= 0 || N <= 0) return DI_OK;
+  if (M > 64 || K <= 0 || (K % 16) != 0 || K > 131071 || ksplit < 1 || !A || !B || !C)
+    return DI_EINVAL;
+  if (ksplit > 1 && split_stride < (int64_t)M * N) return DI_EINVAL;
+  int kchunk = (K + ksplit - 1) / ksplit;
+  kchunk = (kchunk + 63) / 64 * 64;
+  const int nsp = (K + kchunk - 1) / kchunk;
+  if (nsp != ksplit) return DI_EINVAL;  // caller must size partial buffers to ksplit
+  dim3 grid((N + 15) / 16, ksplit);
+  const int mb = (M + 15) / 16;
+  switch (mb) {
+    case 1: hipLaunchKernelGGL(k_gemv_nt<1>, grid, dim3(256), 0, s, A, B, C, M, N, K, kchunk, (i64)split_stride); break;
+    case 2: hipLaunchKernelGGL(k_gemv_nt<2>, grid, dim3(256), 0, s, A, B, C, M, N, K, kchunk, (i64)split_stride); break;
+    case 3: hipLaunchKernelGGL(k_gemv_nt<3>, grid, dim3(256), 0, s, A, B, C, M, N, K, kchunk, (i64)split_stride); break;
+    default: hipLaunchKernelGGL(k_gemv_nt<4>, grid, dim3(256), 0, s, A, B, C, M, N, K, kchunk, (i64)split_stride); break;
+  }
+  DI_LAUNCH_CHECK();
+  return DI_OK;
+}
+
+// dst[b] = src[b]^T for int8 [R][C] matrices
+int detllm_transpose_i8(const int8_t* src, int8_t* dst, int R, int Cc, int batch, int64_t sS,
+                        int64_t sD, hipStream_t s) {
+  if (R <= 0 || Cc <= 0 || batch <= 0) return DI_OK;
+  if (!src || !dst || batch > 65535 || (R + 63) / 64 > 65535) return DI_EINVAL;
+  hipLaunchKernelGGL(k_transpose_i8, dim3((Cc + 63) / 64, (R + 63) / 64, batch), dim3(256), 0, s,
+                     src, dst, R, Cc, (i64)sS, (i64)sD);
+  DI_LAUNCH_CHECK();
+  return DI_OK;
+}
+
+// greedy_pick: out[r] = lowest v maximising logits[r][v] * head_m[v].
+// Scratch: pv, pi of R * nchunk int64 each; nchunk = ceil(V / chunk).
+int detllm_greedy_pick(const int32_t* logits, const int64_t* head_m, int R, int V, int chunk,
+                       int64_t* pv, int64_t* pi, int64_t* out, hipStream_t s) {
+  if (R <= 0) return DI_OK;
+  if (V <= 0 || chunk <= 0 || !logits || !head_m || !pv || !pi || !out) return DI_EINVAL;
+  const int nch = (V + chunk - 1) / chunk;
+  hipLaunchKernelGGL(k_argmax_partial, dim3(nch, R), dim3(256), 0, s, logits, head_m, V, chunk,
+                     pv, pi);
+  DI_LAUNCH_CHECK();
+  hipLaunchKernelGGL(k_argmax_final, dim3(R), dim3(256), 0, s, pv, pi, nch, out);
+  DI_LAUNCH_CHECK();
+  return DI_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,235 @@
+// Integer semantics of DetLLM's numerical path, for host and device code.
+//
+// Every helper reproduces torch's CPU integer kernels, which the reference's
+// CPU backend runs on (src/detllm/intmath.py:7-17 fixes the rounding rules):
+//   * int64 add / sub / mul wrap modulo 2^64 (done on uint64 here, so the
+//     C++ code has no signed-overflow UB);
+//   * a << k is the unsigned shift, 0 when k >= 64 or k < 0;
+//   * a >> k is arithmetic, k clamped to 63 (sign fill) when k >= 63 or k < 0;
+//   * floor division rounds toward -inf;
+//   * int64 -> int32 truncates modulo 2^32.
+//
+// Division by a row-invariant divisor uses a precomputed reciprocal
+// r = floor((2^64 - 1) / d): q0 = mulhi64(n, r) satisfies
+// floor(n/d) - 1 <= q0 <= floor(n/d) for every n < 2^64, because
+// n*r/2^64 = n/d - n*(1 + ((2^64-1) mod d))/(d*2^64) and the subtracted term
+// is below 1; one compare-and-increment makes it exact. This is the
+// reciprocal-with-correction family of Granlund & Montgomery, "Division by
+// Invariant Integers using Multiplication" (PLDI 1994), in its simplest
+// one-correction form. Tested exhaustively near multiples of d on the host.
+#pragma once
+
+#include <stdint.h>
+
+#if defined(__HIPCC__) || defined(__HIP__)
+#include <hip/hip_runtime.h>
+#define DI_HD __host__ __device__ __forceinline__
+#else
+#define DI_HD static inline
+#endif
+
+typedef int64_t i64;
+typedef uint64_t u64;
+
+namespace di {
+
+DI_HD i64 wadd(i64 a, i64 b) { return (i64)((u64)a + (u64)b); }
+DI_HD i64 wsub(i64 a, i64 b) { return (i64)((u64)a - (u64)b); }
+DI_HD i64 wmul(i64 a, i64 b) { return (i64)((u64)a * (u64)b); }
+DI_HD i64 wneg(i64 a) { return (i64)(0ull - (u64)a); }
+DI_HD i64 wabs(i64 a) { return a < 0 ? wneg(a) : a; }  // |INT64_MIN| stays INT64_MIN
+DI_HD i64 imax(i64 a, i64 b) { return a > b ? a : b; }
+DI_HD i64 imin(i64 a, i64 b) { return a < b ? a : b; }
+
+// torch.bitwise_left_shift / bitwise_right_shift on int64
+DI_HD i64 shl(i64 a, i64 k) { return (k < 0 || k >= 64) ? 0 : (i64)((u64)a << k); }
+DI_HD i64 shr(i64 a, i64 k) { return a >> ((k < 0 || k >= 63) ? 63 : k); }
+
+DI_HD int clz64(u64 a) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  return __clzll((long long)a);
+#else
+  return a ? __builtin_clzll(a) : 64;
+#endif
+}
+
+DI_HD u64 mulhi64(u64 a, u64 b) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  return __umul64hi(a, b);
+#else
+  return (u64)(((unsigned __int128)a * b) >> 64);
+#endif
+}
+
+// int_prims.py:47-55 (_ilog2_loop): floor(log2 a) for a >= 2, else 0
+DI_HD i64 ilog2(i64 a) { return a < 2 ? 0 : 63 - clz64((u64)a); }
+
+// int_prims.py:31-44 (_isqrt_loop): 32 steps of the bitwise method from 2^62;
+// negative inputs give 0
+DI_HD i64 isqrt(i64 n) {
+  i64 rem = n, c = 0, d = (i64)1 << 62;
+#pragma unroll
+  for (int i = 0; i < 32; ++i) {
+    i64 t = wadd(c, d);
+    bool ge = rem >= t;
+    rem = ge ? wsub(rem, t) : rem;
+    c = (c >> 1) + (ge ? d : 0);
+    d >>= 2;
+  }
+  return c;
+}
+
+// c10::div_floor_integer semantics for b != 0
+DI_HD i64 floor_div(i64 a, i64 b) {
+  if (b == -1) return wneg(a);
+  i64 q = a / b;
+  i64 r = a - q * b;
+  if (r != 0 && ((r < 0) != (b < 0))) q -= 1;
+  return q;
+}
+
+// intmath.py:62-80 tensor branch: sign(a) * floor((|a| + floor(b/2)) / b)
+DI_HD i64 rhad(i64 a, i64 b) {
+  i64 mag = wabs(a);
+  i64 q = floor_div(wadd(mag, floor_div(b, 2)), b);
+  return a < 0 ? wneg(q) : q;
+}
+
+// intmath.py:120-147 — rshift_round / rshift_round_t: k == 0 is the identity
+DI_HD i64 rshift_round(i64 a, i64 k) {
+  if (k == 0) return a;
+  i64 kp = k < 1 ? 1 : k;
+  return shr(wadd(a, shl(1, kp - 1)), kp);
+}
+
+DI_HD i64 clamp_i8(i64 a) { return a < -128 ? -128 : (a > 127 ? 127 : a); }
+
+// ---- division by a row-invariant positive divisor ----------------------
+struct Recip {
+  u64 d;
+  u64 r;
+};
+
+DI_HD Recip make_recip(i64 d) {  // d >= 1
+  Recip R;
+  R.d = (u64)d;
+  R.r = ~0ull / (u64)d;
+  return R;
+}
+
+DI_HD u64 udiv(u64 n, const Recip& R) {
+  u64 q = mulhi64(n, R.r);
+  u64 rem = n - q * R.d;
+  return q + (rem >= R.d ? 1 : 0);
+}
+
+// floor(a / d) for signed a and invariant d >= 1
+DI_HD i64 floor_div_r(i64 a, const Recip& R) {
+  if (a >= 0) return (i64)udiv((u64)a, R);
+  u64 m = 0ull - (u64)a;  // |a| as unsigned (2^63 for INT64_MIN)
+  return wneg((i64)(udiv(m - 1, R) + 1));
+}
+
+// rhad(a, d) for invariant d >= 1 (bit-identical to rhad above)
+DI_HD i64 rhad_r(i64 a, const Recip& R) {
+  i64 mag = wabs(a);
+  i64 q = floor_div_r(wadd(mag, (i64)(R.d >> 1)), R);
+  return a < 0 ? wneg(q) : q;
+}
+
+// ---- dyadic helpers (src/detllm/dyadic.py) -----------------------------
+
+// dyadic.py:45-49
+DI_HD i64 scaled_round_div(i64 num, i64 den, i64 e) {
+  i64 d = shl(den, imax(-e, 0));
+  if (d == 0) d = 1;  // unreachable on the model path (den = 127, |e| < 50)
+  return rhad(shl(num, imax(e, 0)), d);
+}
+
+// dyadic.py:75-90 (bits = 16)
+DI_HD void norm_scale(i64 m, i64 k, i64* m_out, i64* k_out) {
+  i64 sh = 15 - ilog2(imax(m, 1));
+  i64 m2 = rshift_round(shl(m, imax(sh, 0)), imax(-sh, 0));
+  if (m2 >= 65536) {
+    m2 = rshift_round(m2, 1);
+    sh -= 1;
+  }
+  *m_out = m2;
+  *k_out = wadd(k, sh);
+}
+
+// dyadic.py:52-72 (bits = 16)
+DI_HD void fit_dyadic_ratio(i64 num, i64 den, i64* m_out, i64* e_out) {
+  i64 L = ilog2(num) - ilog2(den);
+  i64 e = 15 - L;
+  i64 m = scaled_round_div(num, den, e);
+  i64 adj = (m >= 65536 ? -1 : 0) + (m < 32768 ? 1 : 0);
+  e += adj;
+  if (adj != 0) m = scaled_round_div(num, den, e);
+  if (m >= 65536) {
+    m = rshift_round(m, 1);
+    e -= 1;
+  }
+  *m_out = m;
+  *e_out = e;
+}
+
+// DI-Exp per-row constant (ops/di_exp.py:29-31; model.py:355-358)
+DI_HD i64 di_exp_tpos(i64 m, i64 k) {
+  i64 m_f = wsub(wadd(m, shr(m, 1)), shr(m, 4));
+  if (m_f == 0) m_f = 1;  // m is a normalised mantissa on the model path
+  return imax(rhad(shl(1, k), m_f), 1);
+}
+
+// ops/di_exp.py:33-36 for x <= 0 in the positive domain (fused_attn.py:11-22):
+// neg = -x; q = neg // tpos; rem = neg - q*tpos;
+// result = (tpos - ((rem + 1) >> 1)) >> min(q, 62).
+// For x > 0 (never on the path) the generic form below is used.
+DI_HD i64 di_exp_generic(i64 x, i64 tpos) {
+  i64 t = wneg(tpos);
+  i64 q = floor_div(x, t);
+  i64 r = wsub(x, wmul(q, t));
+  i64 unshifted = wsub(shr(r, 1), t);
+  return shr(unshifted, imin(q, 62));
+}
+
+DI_HD i64 di_exp_r(i64 x, i64 tpos, const Recip& R) {
+  if (x > 0) return di_exp_generic(x, tpos);
+  u64 neg = 0ull - (u64)x;
+  u64 q = udiv(neg, R);
+  u64 rem = neg - q * R.d;
+  i64 unshifted = wsub(tpos, (i64)((rem + 1) >> 1));
+  return shr(unshifted, q > 62 ? 62 : (i64)q);
+}
+
+// round_half_away_div(num << 7, den) for 0 <= num <= den, den >= 1: the
+// quotient is at most 128, so 8 restoring steps are exact. Larger operands
+// (never produced on the model path) take the generic form.
+DI_HD i64 sigmoid_div(i64 num, i64 den) {
+  if (num >= 0 && den >= num && den < ((i64)1 << 48)) {
+    u64 n = ((u64)num << 7) + ((u64)den >> 1);
+    const u64 d = (u64)den;
+    i64 q = 0;
+#pragma unroll
+    for (int b = 7; b >= 0; --b) {
+      const u64 db = d << b;
+      if (n >= db) {
+        n -= db;
+        q |= (i64)1 << b;
+      }
+    }
+    return q;
+  }
+  return rhad(shl(num, 7), den);
+}
+
+// ops/di_swiglu.py:39-58 on one element (tpos/R per row)
+DI_HD i64 swiglu_elem(i64 g, i64 u, i64 tpos, const Recip& R) {
+  const i64 E = di_exp_r(wneg(wabs(g)), tpos, R);
+  const i64 den = imax(wadd(tpos, E), 1);
+  const i64 num = g >= 0 ? tpos : E;
+  const i64 sig = sigmoid_div(num, den);
+  return wmul(wmul(g, sig), u);
+}
+
+}  // namespace di

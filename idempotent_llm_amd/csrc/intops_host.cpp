@@ -1,0 +1,49 @@
+// Host (CPU) build of intops.h for the CPU test suite: batch wrappers that let
+// tests compare the exact same integer routines the kernels use against the
+// numpy oracle and brute force, without a GPU.
+#include "intops.h"
+
+using namespace di;
+
+extern "C" {
+
+void di_host_rhad_r(const int64_t* a, const int64_t* d, int64_t n, int64_t* out) {
+  for (int64_t i = 0; i < n; ++i) out[i] = rhad_r(a[i], make_recip(d[i]));
+}
+void di_host_rhad(const int64_t* a, const int64_t* d, int64_t n, int64_t* out) {
+  for (int64_t i = 0; i < n; ++i) out[i] = rhad(a[i], d[i]);
+}
+void di_host_floor_div_r(const int64_t* a, const int64_t* d, int64_t n, int64_t* out) {
+  for (int64_t i = 0; i < n; ++i) out[i] = floor_div_r(a[i], make_recip(d[i]));
+}
+void di_host_di_exp(const int64_t* x, const int64_t* tpos, int64_t n, int64_t* out) {
+  for (int64_t i = 0; i < n; ++i) out[i] = di_exp_r(x[i], tpos[i], make_recip(tpos[i]));
+}
+void di_host_di_exp_tpos(const int64_t* m, const int64_t* k, int64_t n, int64_t* out) {
+  for (int64_t i = 0; i < n; ++i) out[i] = di_exp_tpos(m[i], k[i]);
+}
+void di_host_sigmoid_div(const int64_t* num, const int64_t* den, int64_t n, int64_t* out) {
+  for (int64_t i = 0; i < n; ++i) out[i] = sigmoid_div(num[i], den[i]);
+}
+void di_host_swiglu(const int64_t* g, const int64_t* u, const int64_t* tpos, int64_t n,
+                    int64_t* out) {
+  for (int64_t i = 0; i < n; ++i) out[i] = swiglu_elem(g[i], u[i], tpos[i], make_recip(tpos[i]));
+}
+void di_host_scalar(int op, const int64_t* a, const int64_t* b, const int64_t* c, int64_t n,
+                    int64_t* o1, int64_t* o2) {
+  for (int64_t i = 0; i < n; ++i) {
+    int64_t x = 0, y = 0;
+    switch (op) {
+      case 0: o1[i] = isqrt(a[i]); break;
+      case 1: o1[i] = ilog2(a[i]); break;
+      case 2: norm_scale(a[i], b[i], &x, &y); o1[i] = x; o2[i] = y; break;
+      case 3: fit_dyadic_ratio(a[i], b[i], &x, &y); o1[i] = x; o2[i] = y; break;
+      default: o1[i] = scaled_round_div(a[i], b[i], c[i]); break;
+    }
+  }
+}
+void di_host_rshift_round(const int64_t* a, const int64_t* k, int64_t n, int64_t* out) {
+  for (int64_t i = 0; i < n; ++i) out[i] = rshift_round(a[i], k[i]);
+}
+
+}  // extern "C"

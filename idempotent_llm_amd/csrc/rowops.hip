@@ -1,0 +1,962 @@
+// Row kernels of the integer forward pass: per-row (per-token) reductions
+// fused with the dyadic requantisations around them.
+//
+// A row of C <= 4096 values is held in registers by one 256-thread block:
+// thread t owns columns t, t+256, ... (coalesced loads/stores); columns past C
+// hold 0, which is neutral for every max|x| and sum. All arithmetic goes
+// through intops.h, which reproduces the reference's torch-CPU semantics.
+//
+// Fused model kernels (one launch per edge of the layer graph):
+//   k_residual_normq  — [embedding gather | GEMM requant_i32_common(tb)] +
+//                       residual_add/renorm + DI-RMSNorm + smoothing + int8 quant
+//                       (dyadic.py:108-120, :174-206; di_rmsnorm.py:33-52;
+//                        model.py:187-198, :246-249, :410-415, :424-427)
+//   k_swiglu_quant    — requant_i32_common(14) x2 + DI-SwiGLU + quant_i8
+//                       (model.py:416-423; di_swiglu.py:39-58)
+//   k_merge_rowcol    — attention-output merge: requant_i8_rowcol
+//                       (model.py:404-409; dyadic.py:123-139)
+//   k_qkv_epilogue    — per (token, head): requant_i32_common(16) + QK-norm +
+//                       RoPE + QK-smoothing + Q int8 quant + score-scale /
+//                       DI-Exp constant; K/V static int8 quant into the cache
+//                       (model.py:200-216, :303-340, :351-358)
+// Op-level kernels (the same device functions, one reference function each)
+// back the op API used by the parity tests.
+
+#include "common.h"
+
+using namespace di;
+
+namespace {
+
+constexpr int RT = DI_ROW_THREADS;
+
+template <int VPT>
+__device__ __forceinline__ i64 row_absmax(const i64 (&v)[VPT], i64* red) {
+  i64 g = 0;
+#pragma unroll
+  for (int j = 0; j < VPT; ++j) g = imax(g, wabs(v[j]));
+  return block_max(g, red);
+}
+
+// ops/di_rmsnorm.py:33-52: v (<= C valid columns, 0 elsewhere) -> y (int32 values)
+template <int VPT>
+__device__ __forceinline__ void rmsnorm_row(i64 (&v)[VPT], int C, i64* red) {
+  const i64 g = row_absmax(v, red);
+  const i64 sh = 25 - ilog2(imax(g, 1));
+  const i64 up = imax(sh, 0), down = imax(-sh, 0);
+  i64 ss = 0;
+#pragma unroll
+  for (int j = 0; j < VPT; ++j) {
+    const i64 xp = shl(rshift_round(v[j], down), up);
+    v[j] = xp;
+    ss = wadd(ss, wmul(xp, xp));
+  }
+  ss = block_sum(ss, red);
+  const i64 mean = rhad(ss, (i64)C);
+  const Recip R = make_recip(imax(isqrt(mean), 1));
+#pragma unroll
+  for (int j = 0; j < VPT; ++j) v[j] = to_i32(rhad_r(shl(v[j], 20), R));
+}
+
+// dyadic.py:93-105
+template <int VPT>
+__device__ __forceinline__ void quant_row(const i64 (&v)[VPT], i64 m_in, i64 k_in, int C,
+                                          i64* red, int8_t* out, i64* m_out, i64* k_out) {
+  i64 m, k;
+  norm_scale(m_in, k_in, &m, &k);
+  const i64 a = imax(row_absmax(v, red), 1);
+  const Recip R = make_recip(a);
+#pragma unroll
+  for (int j = 0; j < VPT; ++j) {
+    const int c = threadIdx.x + j * RT;
+    if (c < C) out[c] = (int8_t)clamp_i8(rhad_r(wmul(v[j], 127), R));
+  }
+  if (threadIdx.x == 0) {
+    i64 mo, e;
+    fit_dyadic_ratio(wmul(a, m), 127, &mo, &e);
+    *m_out = mo;
+    *k_out = wadd(k, e);
+  }
+}
+
+// dyadic.py:108-120: v holds P on entry, y (int32 values) on exit; returns k_out
+template <int VPT>
+__device__ __forceinline__ i64 requant_common_row(i64 (&v)[VPT], const i64* col_m, i64 row_k,
+                                                  i64 col_k, int tb, int C, i64* red) {
+#pragma unroll
+  for (int j = 0; j < VPT; ++j) {
+    const int c = threadIdx.x + j * RT;
+    v[j] = c < C ? wmul(v[j], col_m[c]) : 0;
+  }
+  const i64 a = imax(row_absmax(v, red), 1);
+  const i64 sh = imax(ilog2(a) - (tb - 1), 0);
+#pragma unroll
+  for (int j = 0; j < VPT; ++j) v[j] = to_i32(rshift_round(v[j], sh));
+  return wsub(wadd(row_k, col_k), sh);
+}
+
+// dyadic.py:174-184
+template <int VPT>
+__device__ __forceinline__ i64 residual_renorm_row(i64 (&h)[VPT], i64 k_res, i64* red) {
+  const i64 g = row_absmax(h, red);
+  const i64 lg = ilog2(imax(g, 1));
+  const i64 sh_down = imax(lg - 29, 0);
+  i64 sh_up = g > 0 ? imax(26 - lg, 0) : 0;
+  if (sh_down > 0) sh_up = 0;
+#pragma unroll
+  for (int j = 0; j < VPT; ++j) h[j] = to_i32(shl(rshift_round(h[j], sh_down), sh_up));
+  return wadd(wsub(k_res, sh_down), sh_up);
+}
+
+// dyadic.py:193-206
+template <int VPT>
+__device__ __forceinline__ i64 residual_add_row(i64 (&h)[VPT], i64 k_res, const i64 (&d)[VPT],
+                                                i64 dm, i64 dk, i64* red) {
+  const i64 rel = wsub(dk, k_res);
+  const i64 down = imax(rel, 0), up = imax(wneg(rel), 0);
+#pragma unroll
+  for (int j = 0; j < VPT; ++j) h[j] = wadd(h[j], shl(rshift_round(wmul(d[j], dm), down), up));
+  return residual_renorm_row(h, k_res, red);
+}
+
+template <int VPT>
+__device__ __forceinline__ void load_row_i32_sum(i64 (&v)[VPT], const int32_t* P, int nsplit,
+                                                 i64 split_stride, i64 off, int C) {
+#pragma unroll
+  for (int j = 0; j < VPT; ++j) {
+    const int c = threadIdx.x + j * RT;
+    if (c < C) {
+      uint32_t s = 0;
+      for (int k = 0; k < nsplit; ++k) s += (uint32_t)P[k * split_stride + off + c];
+      v[j] = (i64)(int32_t)s;
+    } else {
+      v[j] = 0;
+    }
+  }
+}
+
+// =====================================================================
+// Fused model kernels
+// =====================================================================
+
+struct ResNormArgs {
+  int C;
+  int mode;  // 0: embedding gather (residual_from_delta); 1: GEMM residual add
+  i64 vocab;
+  const int64_t* ids;
+  const int8_t* e8;
+  const int64_t* em;
+  const int64_t* ek;
+  const int32_t* P;
+  int nsplit;
+  i64 split_stride;
+  const int64_t* row_m;
+  const int64_t* row_k;
+  const int64_t* col_m;
+  i64 col_k;
+  int tb;
+  int32_t* h;
+  int64_t* k_res;
+  const int64_t* sm_m;  // null: no smoothing multiply
+  i64 sm_k;
+  int8_t* x8;  // null: no norm-quant
+  int64_t* xm;
+  int64_t* xk;
+};
+
+template <int VPT>
+__global__ __launch_bounds__(RT) void k_residual_normq(ResNormArgs a) {
+  __shared__ i64 red[16];
+  const int r = blockIdx.x;
+  const int C = a.C;
+  const i64 off = (i64)r * C;
+  i64 h[VPT], d[VPT];
+  i64 kr;
+  if (a.mode == 0) {
+    i64 id = a.ids[r];
+    id = id < 0 ? 0 : (id >= a.vocab ? a.vocab - 1 : id);  // memory safety only
+    const i64 dm = a.em[id];
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) {
+      const int c = threadIdx.x + j * RT;
+      h[j] = c < C ? wmul((i64)a.e8[id * C + c], dm) : 0;
+    }
+    kr = residual_renorm_row(h, a.ek[id], red);
+  } else {
+    load_row_i32_sum(d, a.P, a.nsplit, a.split_stride, off, C);
+    const i64 dk = requant_common_row(d, a.col_m, a.row_k[r], a.col_k, a.tb, C, red);
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) {
+      const int c = threadIdx.x + j * RT;
+      h[j] = c < C ? (i64)a.h[off + c] : 0;
+    }
+    kr = residual_add_row(h, a.k_res[r], d, a.row_m[r], dk, red);
+  }
+#pragma unroll
+  for (int j = 0; j < VPT; ++j) {
+    const int c = threadIdx.x + j * RT;
+    if (c < C) a.h[off + c] = (int32_t)h[j];
+  }
+  if (threadIdx.x == 0) a.k_res[r] = kr;
+  if (a.x8 == nullptr) return;
+  rmsnorm_row(h, C, red);
+  i64 kq = 20;
+  if (a.sm_m != nullptr) {
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) {
+      const int c = threadIdx.x + j * RT;
+      h[j] = c < C ? wmul(h[j], a.sm_m[c]) : 0;
+    }
+    kq += a.sm_k;
+  }
+  quant_row(h, 1, kq, C, red, a.x8 + off, a.xm + r, a.xk + r);
+}
+
+struct SwigluArgs {
+  int I;
+  const int32_t* P;  // [nsplit][R][2I]: gate | up
+  int nsplit;
+  i64 split_stride;
+  const int64_t* xm;
+  const int64_t* xk;
+  const int64_t* gate_m;
+  i64 gate_k;
+  const int64_t* up_m;
+  i64 up_k;
+  const int64_t* ds_m;
+  i64 ds_k;
+  int8_t* y8;
+  int64_t* ym;
+  int64_t* yk;
+};
+
+template <int VPT>
+__global__ __launch_bounds__(RT) void k_swiglu_quant(SwigluArgs a) {
+  __shared__ i64 red[16];
+  const int r = blockIdx.x;
+  const int I = a.I;
+  i64 g[VPT], u[VPT];
+  load_row_i32_sum(g, a.P, a.nsplit, a.split_stride, (i64)r * 2 * I, I);
+  load_row_i32_sum(u, a.P, a.nsplit, a.split_stride, (i64)r * 2 * I + I, I);
+  const i64 xm = a.xm[r], xk = a.xk[r];
+  const i64 gk = requant_common_row(g, a.gate_m, xk, a.gate_k, 14, I, red);
+  const i64 uk = requant_common_row(u, a.up_m, xk, a.up_k, 14, I, red);
+  const i64 tpos = di_exp_tpos(xm, gk);
+  const Recip R = make_recip(tpos);
+#pragma unroll
+  for (int j = 0; j < VPT; ++j) {
+    const int c = threadIdx.x + j * RT;
+    g[j] = c < I ? wmul(swiglu_elem(g[j], u[j], tpos, R), a.ds_m[c]) : 0;
+  }
+  const i64 ym = wmul(xm, xm);
+  const i64 yk = wadd(wadd(wadd(gk, uk), 7), a.ds_k);
+  quant_row(g, ym, yk, I, red, a.y8 + (i64)r * I, a.ym + r, a.yk + r);
+}
+
+struct MergeArgs {
+  int C;
+  const int64_t* attn;  // [nsplit][R][C]
+  int nsplit;
+  i64 split_stride;
+  const int64_t* os_m;
+  i64 os_k;
+  const int64_t* col_m;
+  i64 col_k;
+  int8_t* a8;
+  int64_t* am;
+  int64_t* ak;
+};
+
+template <int VPT>
+__global__ __launch_bounds__(RT) void k_merge_rowcol(MergeArgs a) {
+  __shared__ i64 red[16];
+  const int r = blockIdx.x;
+  const int C = a.C;
+  const i64 off = (i64)r * C;
+  i64 v[VPT];
+#pragma unroll
+  for (int j = 0; j < VPT; ++j) {
+    const int c = threadIdx.x + j * RT;
+    i64 s = 0;
+    if (c < C) {
+      for (int k = 0; k < a.nsplit; ++k) s = wadd(s, a.attn[k * a.split_stride + off + c]);
+      s = wmul(wmul(s, a.os_m[c]), a.col_m[c]);
+    }
+    v[j] = s;
+  }
+  const i64 a1 = imax(row_absmax(v, red), 1);
+  const i64 sh = imax(ilog2(a1) - 45, 0);
+#pragma unroll
+  for (int j = 0; j < VPT; ++j) v[j] = rshift_round(v[j], sh);
+  const i64 a2 = imax(row_absmax(v, red), 1);
+  const Recip R = make_recip(a2);
+#pragma unroll
+  for (int j = 0; j < VPT; ++j) {
+    const int c = threadIdx.x + j * RT;
+    if (c < C) a.a8[off + c] = (int8_t)clamp_i8(rhad_r(wmul(v[j], 127), R));
+  }
+  if (threadIdx.x == 0) {
+    i64 mo, e;
+    fit_dyadic_ratio(a2, 127, &mo, &e);
+    a.am[r] = mo;
+    a.ak[r] = wsub(wadd(wadd(a.os_k, a.col_k), e), sh);
+  }
+}
+
+// ---------------------------------------------------------------------
+// Q/K/V epilogue: one wave per (token row, head slot). Lane l owns channels
+// l and l + 64, which is exactly the rotate_half pairing of RoPE.
+// ---------------------------------------------------------------------
+struct QKVArgs {
+  int T;
+  int n_q, n_kv;
+  const int32_t* P;  // [nsplit][R][(n_q + 2 n_kv) * 128]
+  int nsplit;
+  i64 split_stride;
+  const int64_t* xm;
+  const int64_t* xk;
+  const int64_t* positions;  // [R]
+  const int64_t* q_m;
+  const int64_t* k_m;
+  const int64_t* v_m;
+  i64 q_k, k_k, v_k;
+  const int64_t* q_norm_m;
+  const int64_t* k_norm_m;
+  i64 q_norm_k, k_norm_k;
+  const int64_t* qs_m;  // [n_kv * 128]
+  i64 qs_k;
+  const int64_t* kq_m;  // [n_kv * 128]
+  const int64_t* kq_k;
+  const int64_t* ks_m;  // [n_kv]
+  const int64_t* ks_k;
+  const int64_t* vq_m;
+  const int64_t* vq_k;
+  const int16_t* cos_t;
+  const int16_t* sin_t;
+  i64 max_pos;
+  int8_t* q8;      // [B][n_q][T][128]
+  int64_t* tpos;   // [B][n_q][T]
+  int64_t* dbg;    // optional [B][n_q][T][4]: qm, qk, sm, sk
+  int8_t* kcache;  // [B][n_kv][cap][128]
+  int8_t* vcache;  // [B][n_kv][128][cap]  (V stored transposed)
+  i64 cap;
+  const int64_t* slot_base_dev;  // optional device scalar (graph replay)
+  i64 slot_base;
+};
+
+__device__ __forceinline__ void wave_rmsnorm128(i64& a, i64& b) {
+  // ops/di_rmsnorm.py:33-52 over 128 channels held two per lane
+  const i64 g = wave_max(imax(wabs(a), wabs(b)));
+  const i64 sh = 25 - ilog2(imax(g, 1));
+  const i64 up = imax(sh, 0), down = imax(-sh, 0);
+  a = shl(rshift_round(a, down), up);
+  b = shl(rshift_round(b, down), up);
+  const i64 ss = wave_sum(wadd(wmul(a, a), wmul(b, b)));
+  const Recip R = make_recip(imax(isqrt(rhad(ss, 128)), 1));
+  a = to_i32(rhad_r(shl(a, 20), R));
+  b = to_i32(rhad_r(shl(b, 20), R));
+}
+
+__global__ __launch_bounds__(RT) void k_qkv_epilogue(QKVArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int slotw = blockIdx.y * 4 + (threadIdx.x >> 6);
+  const int n_heads = a.n_q + 2 * a.n_kv;
+  if (slotw >= n_heads) return;
+  const int r = blockIdx.x;  // token row = b * T + t
+  const int b = r / a.T, t = r - b * a.T;
+  const int NQKV = n_heads * 128;
+  const i64 off = (i64)r * NQKV + (i64)slotw * 128;
+  i64 p0 = 0, p1 = 0;
+  {
+    uint32_t s0 = 0, s1 = 0;
+    for (int k = 0; k < a.nsplit; ++k) {
+      s0 += (uint32_t)a.P[k * a.split_stride + off + lane];
+      s1 += (uint32_t)a.P[k * a.split_stride + off + lane + 64];
+    }
+    p0 = (int32_t)s0;
+    p1 = (int32_t)s1;
+  }
+  const i64 xk = a.xk[r];
+  const i64 xm = a.xm[r];
+  const int group = a.n_q / a.n_kv;
+  const i64 base = a.slot_base_dev ? a.slot_base_dev[0] : a.slot_base;
+  const i64 slot = base + t;
+
+  if (slotw >= a.n_q + a.n_kv) {
+    // ---- V head: requant_i8_static(Pv, xm, xk, v_m, v_k, vq_m[h], vq_k[h])
+    const int h = slotw - a.n_q - a.n_kv;
+    const i64 shift = wsub(wadd(xk, a.v_k), a.vq_k[h]);
+    const i64 up = imax(wneg(shift), 0), down = imax(shift, 0);
+    i64 den = shl(a.vq_m[h], down);
+    if (den <= 0) den = 1;  // static scales are positive mantissas in artifacts
+    const i64 n0 = shl(wmul(wmul(p0, a.v_m[h * 128 + lane]), xm), up);
+    const i64 n1 = shl(wmul(wmul(p1, a.v_m[h * 128 + lane + 64]), xm), up);
+    const Recip R = make_recip(den);
+    int8_t* vrow = a.vcache + ((i64)b * a.n_kv + h) * 128 * a.cap;
+    if (slot >= 0 && slot < a.cap) {
+      vrow[(i64)lane * a.cap + slot] = (int8_t)clamp_i8(rhad_r(n0, R));
+      vrow[(i64)(lane + 64) * a.cap + slot] = (int8_t)clamp_i8(rhad_r(n1, R));
+    }
+    return;
+  }
+  const bool is_q = slotw < a.n_q;
+  const int h = is_q ? slotw : slotw - a.n_q;
+  const int64_t* wm = is_q ? a.q_m + (i64)h * 128 : a.k_m + (i64)h * 128;
+  const i64 wk = is_q ? a.q_k : a.k_k;
+  // requant_i32_common(tb = 16) per (token, head)   (model.py:207-211)
+  i64 y0 = wmul(p0, wm[lane]), y1 = wmul(p1, wm[lane + 64]);
+  {
+    const i64 am = imax(wave_max(imax(wabs(y0), wabs(y1))), 1);
+    const i64 sh = imax(ilog2(am) - 15, 0);
+    y0 = to_i32(rshift_round(y0, sh));
+    y1 = to_i32(rshift_round(y1, sh));
+  }
+  (void)wk;  // (m, k) of the requant are dropped by _qk_head_pipeline
+  // di_rmsnorm_gamma  (model.py:212)
+  wave_rmsnorm128(y0, y1);
+  const int64_t* gam = is_q ? a.q_norm_m : a.k_norm_m;
+  y0 = wmul(y0, gam[lane]);
+  y1 = wmul(y1, gam[lane + 64]);
+  // apply_int_rope at this token's position   (model.py:213-215; rope.py:38-55)
+  i64 pos = a.positions[r];
+  pos = pos < 0 ? 0 : (pos >= a.max_pos ? a.max_pos - 1 : pos);
+  const i64 c0 = a.cos_t[pos * 128 + lane], c1 = a.cos_t[pos * 128 + lane + 64];
+  const i64 s0 = a.sin_t[pos * 128 + lane], s1 = a.sin_t[pos * 128 + lane + 64];
+  const i64 r0 = rshift_round(wadd(wmul(y0, c0), wmul(wneg(y1), s0)), 14);
+  const i64 r1 = rshift_round(wadd(wmul(y1, c1), wmul(y0, s1)), 14);
+  if (!is_q) {
+    // K: requant_i8_static(kk, 1, k_rowk, 1, 0, kq_m, kq_k)   (model.py:326-329)
+    const i64 rowk = 20 + a.k_norm_k;
+    int8_t* krow = a.kcache + (((i64)b * a.n_kv + h) * a.cap + slot) * 128;
+    i64 outv[2];
+    const i64 rv[2] = {r0, r1};
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const int c = lane + 64 * q;
+      const i64 shift = wsub(rowk, a.kq_k[h * 128 + c]);
+      const i64 up = imax(wneg(shift), 0), down = imax(shift, 0);
+      i64 den = shl(a.kq_m[h * 128 + c], down);
+      if (den <= 0) den = 1;
+      outv[q] = clamp_i8(rhad(shl(rv[q], up), den));
+    }
+    if (slot >= 0 && slot < a.cap) {
+      krow[lane] = (int8_t)outv[0];
+      krow[lane + 64] = (int8_t)outv[1];
+    }
+    return;
+  }
+  // Q: QK smoothing (model.py:317-320) then quant_i8_pertoken (model.py:322-323)
+  const int kvh = h / group;
+  const i64 q0 = wmul(r0, a.qs_m[kvh * 128 + lane]);
+  const i64 q1 = wmul(r1, a.qs_m[kvh * 128 + lane + 64]);
+  const i64 qkk = 20 + a.q_norm_k + a.qs_k;
+  i64 m, k;
+  norm_scale(1, qkk, &m, &k);
+  const i64 am = imax(wave_max(imax(wabs(q0), wabs(q1))), 1);
+  const Recip R = make_recip(am);
+  const i64 qrow = (((i64)b * a.n_q + h) * a.T + t);
+  a.q8[qrow * 128 + lane] = (int8_t)clamp_i8(rhad_r(wmul(q0, 127), R));
+  a.q8[qrow * 128 + lane + 64] = (int8_t)clamp_i8(rhad_r(wmul(q1, 127), R));
+  if (lane == 0) {
+    i64 qm, e;
+    fit_dyadic_ratio(wmul(am, m), 127, &qm, &e);
+    const i64 qk = wadd(k, e);
+    // score scale: norm_scale(qm * ks_m[h//g], qk + ks_k[h//g])   (model.py:351-353)
+    i64 sm, sk;
+    norm_scale(wmul(qm, a.ks_m[kvh]), wadd(qk, a.ks_k[kvh]), &sm, &sk);
+    a.tpos[qrow] = di_exp_tpos(sm, sk);
+    if (a.dbg) {
+      a.dbg[qrow * 4 + 0] = qm;
+      a.dbg[qrow * 4 + 1] = qk;
+      a.dbg[qrow * 4 + 2] = sm;
+      a.dbg[qrow * 4 + 3] = sk;
+    }
+  }
+}
+
+// =====================================================================
+// Op-level row kernels (one reference function each)
+// =====================================================================
+
+template <int VPT>
+__device__ __forceinline__ void load_row64(i64 (&v)[VPT], const int64_t* x, i64 off, int C) {
+#pragma unroll
+  for (int j = 0; j < VPT; ++j) {
+    const int c = threadIdx.x + j * RT;
+    v[j] = c < C ? x[off + c] : 0;
+  }
+}
+
+template <int VPT>
+__global__ __launch_bounds__(RT) void k_op_quant(const int64_t* x, const int64_t* m,
+                                                 const int64_t* k, int C, int8_t* x8,
+                                                 int64_t* mo, int64_t* ko) {
+  __shared__ i64 red[16];
+  const int r = blockIdx.x;
+  i64 v[VPT];
+  load_row64(v, x, (i64)r * C, C);
+  quant_row(v, m[r], k[r], C, red, x8 + (i64)r * C, mo + r, ko + r);
+}
+
+template <int VPT>
+__global__ __launch_bounds__(RT) void k_op_requant_common(const int64_t* P, const int64_t* row_k,
+                                                          const int64_t* col_m, int G, i64 col_k,
+                                                          int tb, int C, int32_t* y,
+                                                          int64_t* ko) {
+  __shared__ i64 red[16];
+  const int r = blockIdx.x;
+  i64 v[VPT];
+  load_row64(v, P, (i64)r * C, C);
+  const i64 k = requant_common_row(v, col_m + (i64)(r % G) * C, row_k[r], col_k, tb, C, red);
+#pragma unroll
+  for (int j = 0; j < VPT; ++j) {
+    const int c = threadIdx.x + j * RT;
+    if (c < C) y[(i64)r * C + c] = (int32_t)v[j];
+  }
+  if (threadIdx.x == 0) ko[r] = k;
+}
+
+template <int VPT>
+__global__ __launch_bounds__(RT) void k_op_rowcol(const int64_t* P, const int64_t* row_m,
+                                                  const int64_t* row_k, const int64_t* col_m,
+                                                  i64 col_k, int C, int8_t* y8, int64_t* mo,
+                                                  int64_t* ko) {
+  __shared__ i64 red[16];
+  const int r = blockIdx.x;
+  i64 v[VPT];
+  load_row64(v, P, (i64)r * C, C);
+#pragma unroll
+  for (int j = 0; j < VPT; ++j) {
+    const int c = threadIdx.x + j * RT;
+    v[j] = c < C ? wmul(v[j], col_m[c]) : 0;
+  }
+  const i64 a1 = imax(row_absmax(v, red), 1);
+  const i64 sh = imax(ilog2(a1) - 45, 0);
+#pragma unroll
+  for (int j = 0; j < VPT; ++j) v[j] = rshift_round(v[j], sh);
+  const i64 a2 = imax(row_absmax(v, red), 1);
+  const Recip R = make_recip(a2);
+#pragma unroll
+  for (int j = 0; j < VPT; ++j) {
+    const int c = threadIdx.x + j * RT;
+    if (c < C) y8[(i64)r * C + c] = (int8_t)clamp_i8(rhad_r(wmul(v[j], 127), R));
+  }
+  if (threadIdx.x == 0) {
+    i64 m, e;
+    fit_dyadic_ratio(wmul(a2, row_m[r]), 127, &m, &e);
+    mo[r] = m;
+    ko[r] = wsub(wadd(wadd(row_k[r], col_k), e), sh);
+  }
+}
+
+// mode 0: residual_renorm(h64, k); 1: residual_add(h, k, d, dm, dk)
+template <int VPT>
+__global__ __launch_bounds__(RT) void k_op_residual(int mode, const int64_t* h_in,
+                                                    const int64_t* k_res, const int64_t* d,
+                                                    const int64_t* dm, const int64_t* dk, int C,
+                                                    int32_t* h_out, int64_t* k_out) {
+  __shared__ i64 red[16];
+  const int r = blockIdx.x;
+  i64 h[VPT];
+  load_row64(h, h_in, (i64)r * C, C);
+  i64 k;
+  if (mode == 0) {
+    k = residual_renorm_row(h, k_res[r], red);
+  } else {
+    i64 dv[VPT];
+    load_row64(dv, d, (i64)r * C, C);
+    k = residual_add_row(h, k_res[r], dv, dm[r], dk[r], red);
+  }
+#pragma unroll
+  for (int j = 0; j < VPT; ++j) {
+    const int c = threadIdx.x + j * RT;
+    if (c < C) h_out[(i64)r * C + c] = (int32_t)h[j];
+  }
+  if (threadIdx.x == 0) k_out[r] = k;
+}
+
+template <int VPT>
+__global__ __launch_bounds__(RT) void k_op_rmsnorm(const int64_t* x, const int64_t* gamma_m,
+                                                   int C, int32_t* y32, int64_t* y64) {
+  __shared__ i64 red[16];
+  const int r = blockIdx.x;
+  i64 v[VPT];
+  load_row64(v, x, (i64)r * C, C);
+  rmsnorm_row(v, C, red);
+#pragma unroll
+  for (int j = 0; j < VPT; ++j) {
+    const int c = threadIdx.x + j * RT;
+    if (c < C) {
+      if (gamma_m) y64[(i64)r * C + c] = wmul(v[j], gamma_m[c]);
+      else y32[(i64)r * C + c] = (int32_t)v[j];
+    }
+  }
+}
+
+template <int VPT>
+__global__ __launch_bounds__(RT) void k_op_softmax(const int64_t* x, const int64_t* m,
+                                                   const int64_t* k, const uint8_t* valid,
+                                                   int has_clip, i64 clip_c, int p_out_bits,
+                                                   int C, int32_t* probs) {
+  // ops/di_softmax.py:33-61
+  __shared__ i64 red[16];
+  const int r = blockIdx.x;
+  const i64 off = (i64)r * C;
+  const i64 NEG = INT64_MIN + 1;
+  i64 v[VPT];
+  bool ok[VPT];
+  i64 mx = NEG;
+  bool anyv = false;
+#pragma unroll
+  for (int j = 0; j < VPT; ++j) {
+    const int c = threadIdx.x + j * RT;
+    ok[j] = c < C && valid[off + c] != 0;
+    v[j] = c < C ? x[off + c] : 0;
+    if (ok[j]) {
+      mx = imax(mx, v[j]);
+      anyv = true;
+    }
+  }
+  mx = block_max(mx, red);
+  const i64 any = block_max(anyv ? 1 : 0, red);
+  if (!any) mx = 0;
+  const i64 mm = m[r], kk = k[r];
+  const i64 tpos = di_exp_tpos(mm, kk);
+  const Recip Rt = make_recip(tpos);
+  i64 cint = 0;
+  if (has_clip) cint = rhad(wmul(clip_c, shl(1, kk)), mm);
+  i64 den = 0;
+#pragma unroll
+  for (int j = 0; j < VPT; ++j) {
+    i64 xd = ok[j] ? wsub(v[j], mx) : 0;
+    if (has_clip) xd = imax(xd, wneg(cint));
+    const i64 e = ok[j] ? di_exp_r(xd, tpos, Rt) : 0;
+    v[j] = e;
+    den = wadd(den, e);
+  }
+  den = imax(block_sum(den, red), 1);
+  const Recip Rd = make_recip(den);
+#pragma unroll
+  for (int j = 0; j < VPT; ++j) {
+    const int c = threadIdx.x + j * RT;
+    if (c < C) probs[off + c] = (int32_t)to_i32(rhad_r(shl(v[j], p_out_bits - 1), Rd));
+  }
+}
+
+__global__ void k_op_di_exp(const int64_t* x, const int64_t* m, const int64_t* k, int C,
+                            i64 n, int64_t* res, int64_t* tpos_out) {
+  // ops/di_exp.py:21-37, row constants recomputed per element
+  for (i64 i = blockIdx.x * (i64)blockDim.x + threadIdx.x; i < n;
+       i += (i64)gridDim.x * blockDim.x) {
+    const i64 r = i / C;
+    const i64 tpos = di_exp_tpos(m[r], k[r]);
+    const Recip R = make_recip(tpos);
+    res[i] = di_exp_r(x[i], tpos, R);
+    if (i % C == 0) tpos_out[r] = tpos;
+  }
+}
+
+__global__ void k_op_swiglu(const int64_t* gate, const int64_t* gm, const int64_t* gk,
+                            const int64_t* up, const int64_t* um, const int64_t* uk, int C,
+                            i64 n, int64_t* y, int64_t* ym, int64_t* yk) {
+  for (i64 i = blockIdx.x * (i64)blockDim.x + threadIdx.x; i < n;
+       i += (i64)gridDim.x * blockDim.x) {
+    const i64 r = i / C;
+    const i64 tpos = di_exp_tpos(gm[r], gk[r]);
+    const Recip R = make_recip(tpos);
+    y[i] = swiglu_elem(gate[i], up[i], tpos, R);
+    if (i % C == 0) {
+      ym[r] = wmul(gm[r], um[r]);
+      yk[r] = wadd(wadd(gk[r], uk[r]), 7);
+    }
+  }
+}
+
+__global__ void k_op_rope(const int64_t* x, const int64_t* pos, const int16_t* cos_t,
+                          const int16_t* sin_t, i64 max_pos, i64 rows, int64_t* y) {
+  // ops/rope.py:38-55 on rows of 128 channels
+  const i64 r = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (r >= rows) return;
+  i64 p = pos[r];
+  p = p < 0 ? 0 : (p >= max_pos ? max_pos - 1 : p);
+  const i64 x0 = x[r * 128 + lane], x1 = x[r * 128 + lane + 64];
+  y[r * 128 + lane] = rshift_round(
+      wadd(wmul(x0, (i64)cos_t[p * 128 + lane]), wmul(wneg(x1), (i64)sin_t[p * 128 + lane])), 14);
+  y[r * 128 + lane + 64] = rshift_round(
+      wadd(wmul(x1, (i64)cos_t[p * 128 + lane + 64]), wmul(x0, (i64)sin_t[p * 128 + lane + 64])),
+      14);
+}
+
+__global__ void k_op_static(const int64_t* P, const int64_t* row_m, const int64_t* row_k,
+                            const int64_t* col_m, const int64_t* col_k, const int64_t* s_m,
+                            const int64_t* s_k, i64 n, int8_t* y8) {
+  // dyadic.py:142-163 with every operand materialised per element
+  for (i64 i = blockIdx.x * (i64)blockDim.x + threadIdx.x; i < n;
+       i += (i64)gridDim.x * blockDim.x) {
+    const i64 num = wmul(wmul(P[i], col_m[i]), row_m[i]);
+    const i64 shift = wsub(wadd(row_k[i], col_k[i]), s_k[i]);
+    const i64 up = imax(wneg(shift), 0), down = imax(shift, 0);
+    i64 den = shl(s_m[i], down);
+    if (den <= 0) den = 1;
+    y8[i] = (int8_t)clamp_i8(rhad(shl(num, up), den));
+  }
+}
+
+// op: 0 isqrt, 1 ilog2, 2 norm_scale, 3 fit_dyadic_ratio, 4 scaled_round_div
+__global__ void k_op_scalar(int op, const int64_t* a, const int64_t* b, const int64_t* c, i64 n,
+                            int64_t* o1, int64_t* o2) {
+  for (i64 i = blockIdx.x * (i64)blockDim.x + threadIdx.x; i < n;
+       i += (i64)gridDim.x * blockDim.x) {
+    i64 x, y;
+    switch (op) {
+      case 0: o1[i] = isqrt(a[i]); break;
+      case 1: o1[i] = ilog2(a[i]); break;
+      case 2: norm_scale(a[i], b[i], &x, &y); o1[i] = x; o2[i] = y; break;
+      case 3: fit_dyadic_ratio(a[i], b[i], &x, &y); o1[i] = x; o2[i] = y; break;
+      default: o1[i] = scaled_round_div(a[i], b[i], c[i]); break;
+    }
+  }
+}
+
+inline int pick_vpt(int C) {
+  const int need = (C + RT - 1) / RT;
+  if (need <= 1) return 1;
+  if (need <= 2) return 2;
+  if (need <= 4) return 4;
+  if (need <= 8) return 8;
+  if (need <= 12) return 12;
+  if (need <= 16) return 16;
+  return 0;
+}
+
+inline int grid_for(i64 n) {
+  i64 g = (n + 255) / 256;
+  return (int)(g < 65536 ? (g < 1 ? 1 : g) : 65536);
+}
+
+}  // namespace
+
+#define DI_VPT_DISPATCH(vpt, KERNEL, GRID, STREAM, ...)                                  \
+  switch (vpt) {                                                                         \
+    case 1: hipLaunchKernelGGL(KERNEL<1>, GRID, dim3(RT), 0, STREAM, __VA_ARGS__); break;   \
+    case 2: hipLaunchKernelGGL(KERNEL<2>, GRID, dim3(RT), 0, STREAM, __VA_ARGS__); break;   \
+    case 4: hipLaunchKernelGGL(KERNEL<4>, GRID, dim3(RT), 0, STREAM, __VA_ARGS__); break;   \
+    case 8: hipLaunchKernelGGL(KERNEL<8>, GRID, dim3(RT), 0, STREAM, __VA_ARGS__); break;   \
+    case 12: hipLaunchKernelGGL(KERNEL<12>, GRID, dim3(RT), 0, STREAM, __VA_ARGS__); break; \
+    case 16: hipLaunchKernelGGL(KERNEL<16>, GRID, dim3(RT), 0, STREAM, __VA_ARGS__); break; \
+    default: return DI_ERANGE;                                                            \
+  }
+
+extern "C" {
+
+// ---------------------------------------------------------------- model path
+
+int detllm_embed_normq(const int64_t* ids, int R, int C, int64_t vocab, const int8_t* e8,
+                       const int64_t* em, const int64_t* ek, int32_t* h, int64_t* k_res,
+                       const int64_t* sm_m, int64_t sm_k, int8_t* x8, int64_t* xm, int64_t* xk,
+                       hipStream_t s) {
+  if (R <= 0) return DI_OK;
+  if (C <= 0 || vocab <= 0 || !ids || !e8 || !em || !ek || !h || !k_res) return DI_EINVAL;
+  ResNormArgs a{};
+  a.C = C; a.mode = 0; a.vocab = vocab; a.ids = ids; a.e8 = e8; a.em = em; a.ek = ek;
+  a.h = h; a.k_res = k_res; a.sm_m = sm_m; a.sm_k = sm_k; a.x8 = x8; a.xm = xm; a.xk = xk;
+  const int vpt = pick_vpt(C);
+  DI_VPT_DISPATCH(vpt, k_residual_normq, dim3(R), s, a);
+  DI_LAUNCH_CHECK();
+  return DI_OK;
+}
+
+int detllm_residual_normq(const int32_t* P, int nsplit, int64_t split_stride, int R, int C,
+                          const int64_t* row_m, const int64_t* row_k, const int64_t* col_m,
+                          int64_t col_k, int tb, int32_t* h, int64_t* k_res, const int64_t* sm_m,
+                          int64_t sm_k, int8_t* x8, int64_t* xm, int64_t* xk, hipStream_t s) {
+  if (R <= 0) return DI_OK;
+  if (C <= 0 || nsplit < 1 || !P || !row_m || !row_k || !col_m || !h || !k_res) return DI_EINVAL;
+  ResNormArgs a{};
+  a.C = C; a.mode = 1; a.P = P; a.nsplit = nsplit; a.split_stride = split_stride;
+  a.row_m = row_m; a.row_k = row_k; a.col_m = col_m; a.col_k = col_k; a.tb = tb;
+  a.h = h; a.k_res = k_res; a.sm_m = sm_m; a.sm_k = sm_k; a.x8 = x8; a.xm = xm; a.xk = xk;
+  const int vpt = pick_vpt(C);
+  DI_VPT_DISPATCH(vpt, k_residual_normq, dim3(R), s, a);
+  DI_LAUNCH_CHECK();
+  return DI_OK;
+}
+
+int detllm_swiglu_quant(const int32_t* P, int nsplit, int64_t split_stride, int R, int I,
+                        const int64_t* xm, const int64_t* xk, const int64_t* gate_m,
+                        int64_t gate_k, const int64_t* up_m, int64_t up_k, const int64_t* ds_m,
+                        int64_t ds_k, int8_t* y8, int64_t* ym, int64_t* yk, hipStream_t s) {
+  if (R <= 0) return DI_OK;
+  if (I <= 0 || nsplit < 1 || !P || !xm || !xk || !gate_m || !up_m || !ds_m || !y8 || !ym || !yk)
+    return DI_EINVAL;
+  SwigluArgs a{};
+  a.I = I; a.P = P; a.nsplit = nsplit; a.split_stride = split_stride; a.xm = xm; a.xk = xk;
+  a.gate_m = gate_m; a.gate_k = gate_k; a.up_m = up_m; a.up_k = up_k; a.ds_m = ds_m;
+  a.ds_k = ds_k; a.y8 = y8; a.ym = ym; a.yk = yk;
+  const int vpt = pick_vpt(I);
+  DI_VPT_DISPATCH(vpt, k_swiglu_quant, dim3(R), s, a);
+  DI_LAUNCH_CHECK();
+  return DI_OK;
+}
+
+int detllm_merge_rowcol(const int64_t* attn, int nsplit, int64_t split_stride, int R, int C,
+                        const int64_t* os_m, int64_t os_k, const int64_t* col_m, int64_t col_k,
+                        int8_t* a8, int64_t* am, int64_t* ak, hipStream_t s) {
+  if (R <= 0) return DI_OK;
+  if (C <= 0 || nsplit < 1 || !attn || !os_m || !col_m || !a8 || !am || !ak) return DI_EINVAL;
+  MergeArgs a{};
+  a.C = C; a.attn = attn; a.nsplit = nsplit; a.split_stride = split_stride; a.os_m = os_m;
+  a.os_k = os_k; a.col_m = col_m; a.col_k = col_k; a.a8 = a8; a.am = am; a.ak = ak;
+  const int vpt = pick_vpt(C);
+  DI_VPT_DISPATCH(vpt, k_merge_rowcol, dim3(R), s, a);
+  DI_LAUNCH_CHECK();
+  return DI_OK;
+}
+
+int detllm_qkv_epilogue(const int32_t* P, int nsplit, int64_t split_stride, int B, int T,
+                        int n_q, int n_kv, const int64_t* xm, const int64_t* xk,
+                        const int64_t* positions, const int64_t* q_m, int64_t q_k,
+                        const int64_t* k_m, int64_t k_k, const int64_t* v_m, int64_t v_k,
+                        const int64_t* q_norm_m, int64_t q_norm_k, const int64_t* k_norm_m,
+                        int64_t k_norm_k, const int64_t* qs_m, int64_t qs_k,
+                        const int64_t* kq_m, const int64_t* kq_k, const int64_t* ks_m,
+                        const int64_t* ks_k, const int64_t* vq_m, const int64_t* vq_k,
+                        const int16_t* cos_t, const int16_t* sin_t, int64_t max_pos,
+                        int8_t* q8, int64_t* tpos, int64_t* dbg, int8_t* kcache,
+                        int8_t* vcache, int64_t cap, const int64_t* slot_base_dev,
+                        int64_t slot_base, hipStream_t s) {
+  if (B <= 0 || T <= 0) return DI_OK;
+  if (n_q <= 0 || n_kv <= 0 || n_q % n_kv != 0 || nsplit < 1 || cap <= 0 || max_pos <= 0)
+    return DI_EINVAL;
+  if (!slot_base_dev && (slot_base < 0 || slot_base + T > cap)) return DI_ERANGE;
+  QKVArgs a{};
+  a.T = T; a.n_q = n_q; a.n_kv = n_kv; a.P = P; a.nsplit = nsplit; a.split_stride = split_stride;
+  a.xm = xm; a.xk = xk; a.positions = positions; a.q_m = q_m; a.k_m = k_m; a.v_m = v_m;
+  a.q_k = q_k; a.k_k = k_k; a.v_k = v_k; a.q_norm_m = q_norm_m; a.k_norm_m = k_norm_m;
+  a.q_norm_k = q_norm_k; a.k_norm_k = k_norm_k; a.qs_m = qs_m; a.qs_k = qs_k; a.kq_m = kq_m;
+  a.kq_k = kq_k; a.ks_m = ks_m; a.ks_k = ks_k; a.vq_m = vq_m; a.vq_k = vq_k; a.cos_t = cos_t;
+  a.sin_t = sin_t; a.max_pos = max_pos; a.q8 = q8; a.tpos = tpos; a.dbg = dbg;
+  a.kcache = kcache; a.vcache = vcache; a.cap = cap; a.slot_base_dev = slot_base_dev;
+  a.slot_base = slot_base;
+  const int heads = n_q + 2 * n_kv;
+  hipLaunchKernelGGL(k_qkv_epilogue, dim3(B * T, (heads + 3) / 4), dim3(RT), 0, s, a);
+  DI_LAUNCH_CHECK();
+  return DI_OK;
+}
+
+// ---------------------------------------------------------------- op level
+
+int detllm_op_quant_i8_pertoken(const int64_t* x, const int64_t* m, const int64_t* k, int R,
+                                int C, int8_t* x8, int64_t* mo, int64_t* ko, hipStream_t s) {
+  if (R <= 0) return DI_OK;
+  const int vpt = pick_vpt(C);
+  DI_VPT_DISPATCH(vpt, k_op_quant, dim3(R), s, x, m, k, C, x8, mo, ko);
+  DI_LAUNCH_CHECK();
+  return DI_OK;
+}
+
+int detllm_op_requant_i32_common(const int64_t* P, const int64_t* row_k, const int64_t* col_m,
+                                 int G, int64_t col_k, int tb, int R, int C, int32_t* y,
+                                 int64_t* ko, hipStream_t s) {
+  if (R <= 0) return DI_OK;
+  if (G < 1) return DI_EINVAL;
+  const int vpt = pick_vpt(C);
+  DI_VPT_DISPATCH(vpt, k_op_requant_common, dim3(R), s, P, row_k, col_m, G, col_k, tb, C, y, ko);
+  DI_LAUNCH_CHECK();
+  return DI_OK;
+}
+
+int detllm_op_requant_i8_rowcol(const int64_t* P, const int64_t* row_m, const int64_t* row_k,
+                                const int64_t* col_m, int64_t col_k, int R, int C, int8_t* y8,
+                                int64_t* mo, int64_t* ko, hipStream_t s) {
+  if (R <= 0) return DI_OK;
+  const int vpt = pick_vpt(C);
+  DI_VPT_DISPATCH(vpt, k_op_rowcol, dim3(R), s, P, row_m, row_k, col_m, col_k, C, y8, mo, ko);
+  DI_LAUNCH_CHECK();
+  return DI_OK;
+}
+
+int detllm_op_requant_i8_static(const int64_t* P, const int64_t* row_m, const int64_t* row_k,
+                                const int64_t* col_m, const int64_t* col_k, const int64_t* s_m,
+                                const int64_t* s_k, int64_t n, int8_t* y8, hipStream_t s) {
+  if (n <= 0) return DI_OK;
+  hipLaunchKernelGGL(k_op_static, dim3(grid_for(n)), dim3(256), 0, s, P, row_m, row_k, col_m,
+                     col_k, s_m, s_k, n, y8);
+  DI_LAUNCH_CHECK();
+  return DI_OK;
+}
+
+int detllm_op_residual(int mode, const int64_t* h, const int64_t* k_res, const int64_t* d,
+                       const int64_t* dm, const int64_t* dk, int R, int C, int32_t* h_out,
+                       int64_t* k_out, hipStream_t s) {
+  if (R <= 0) return DI_OK;
+  if (mode != 0 && mode != 1) return DI_EINVAL;
+  const int vpt = pick_vpt(C);
+  DI_VPT_DISPATCH(vpt, k_op_residual, dim3(R), s, mode, h, k_res, d, dm, dk, C, h_out, k_out);
+  DI_LAUNCH_CHECK();
+  return DI_OK;
+}
+
+int detllm_op_rmsnorm(const int64_t* x, const int64_t* gamma_m, int R, int C, int32_t* y32,
+                      int64_t* y64, hipStream_t s) {
+  if (R <= 0) return DI_OK;
+  const int vpt = pick_vpt(C);
+  DI_VPT_DISPATCH(vpt, k_op_rmsnorm, dim3(R), s, x, gamma_m, C, y32, y64);
+  DI_LAUNCH_CHECK();
+  return DI_OK;
+}
+
+int detllm_op_softmax(const int64_t* x, const int64_t* m, const int64_t* k, const uint8_t* valid,
+                      int has_clip, int64_t clip_c, int p_out_bits, int R, int C, int32_t* probs,
+                      hipStream_t s) {
+  if (R <= 0) return DI_OK;
+  if (p_out_bits < 1 || p_out_bits > 62) return DI_EINVAL;
+  const int vpt = pick_vpt(C);
+  DI_VPT_DISPATCH(vpt, k_op_softmax, dim3(R), s, x, m, k, valid, has_clip, clip_c, p_out_bits, C,
+                  probs);
+  DI_LAUNCH_CHECK();
+  return DI_OK;
+}
+
+int detllm_op_di_exp(const int64_t* x, const int64_t* m, const int64_t* k, int R, int C,
+                     int64_t* res, int64_t* tpos, hipStream_t s) {
+  const i64 n = (i64)R * C;
+  if (n <= 0) return DI_OK;
+  hipLaunchKernelGGL(k_op_di_exp, dim3(grid_for(n)), dim3(256), 0, s, x, m, k, C, n, res, tpos);
+  DI_LAUNCH_CHECK();
+  return DI_OK;
+}
+
+int detllm_op_swiglu(const int64_t* gate, const int64_t* gm, const int64_t* gk,
+                     const int64_t* up, const int64_t* um, const int64_t* uk, int R, int C,
+                     int64_t* y, int64_t* ym, int64_t* yk, hipStream_t s) {
+  const i64 n = (i64)R * C;
+  if (n <= 0) return DI_OK;
+  hipLaunchKernelGGL(k_op_swiglu, dim3(grid_for(n)), dim3(256), 0, s, gate, gm, gk, up, um, uk,
+                     C, n, y, ym, yk);
+  DI_LAUNCH_CHECK();
+  return DI_OK;
+}
+
+int detllm_op_rope(const int64_t* x, const int64_t* pos, const int16_t* cos_t,
+                   const int16_t* sin_t, int64_t max_pos, int64_t rows, int64_t* y,
+                   hipStream_t s) {
+  if (rows <= 0) return DI_OK;
+  if (max_pos <= 0) return DI_EINVAL;
+  hipLaunchKernelGGL(k_op_rope, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, s, x, pos, cos_t,
+                     sin_t, max_pos, rows, y);
+  DI_LAUNCH_CHECK();
+  return DI_OK;
+}
+
+int detllm_op_scalar(int op, const int64_t* a, const int64_t* b, const int64_t* c, int64_t n,
+                     int64_t* o1, int64_t* o2, hipStream_t s) {
+  if (n <= 0) return DI_OK;
+  if (op < 0 || op > 4) return DI_EINVAL;
+  hipLaunchKernelGGL(k_op_scalar, dim3(grid_for(n)), dim3(256), 0, s, op, a, b, c, n, o1, o2);
+  DI_LAUNCH_CHECK();
+  return DI_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,377 @@
+"""IntQwen3 on the "rocm" backend: the reference runtime API
+(``src/detllm/model.py:105-531``) driving fused gfx950 HIP kernels.
+
+Public surface (same names, argument meaning and return values as the
+reference): ``IntQwen3(artifact_dir, backend)``, ``.forward(ids, positions,
+cache=None, chunk_valid=None, guard=False) -> (logits, row_m, row_k, cache)``,
+``.generate(ids, max_new, guard=False, chunk_valid=None, stop_at_eos=False,
+use_graph=False) -> (tokens, step_logits)``, ``.greedy_pick(logits_row)``,
+``KVCache``, ``LayerWeights``. Batching/masking model as in model.py:8-17:
+right padding, a validity flag per cache slot, explicit positions, K/V
+quantised once when produced.
+
+One layer is 9 launches, each fusing everything between two GEMMs
+(model.py:288-428):
+
+  x8 --GEMM[q|k|v]--> qkv_epilogue (per-head requant, QK-norm, RoPE,
+      smoothing, Q int8 + DI-Exp constant, K/V int8 into the cache)
+     --> attention (prefill: MFMA 3-pass; decode: per (row, kv-head))
+     --> merge_rowcol (attention-output requant to int8)
+     --GEMM[o]--> residual_normq (requant, residual add, RMSNorm, MLP quant)
+     --GEMM[gate|up]--> swiglu_quant
+     --GEMM[down]--> residual_normq (... next layer's attention quant)
+
+Memory layout in HBM (all integer; built once at load by integer
+permutation of the artifact's tensors): weights as [out, in] int8 with
+q|k|v and gate|up concatenated along out; per-channel mantissas int64; the
+KV cache as K [B, n_kv, cap, 128] and V^T [B, n_kv, 128, cap] int8 per layer
+plus a [B, cap] validity mask; cap is a multiple of 256.
+"""
+
+from __future__ import annotations
+
+import json
+import os
+from dataclasses import dataclass
+
+import torch
+
+from ._lib import call
+from .backends import canonical_backend, gemm_nt
+from .guard import NoFloatMode
+
+I64 = torch.int64
+P_OUT_BITS = 15
+OUT_FRAC_BITS = 20
+GREEDY_CHUNK = 2048
+
+
+@dataclass
+class LayerWeights:
+    """Per-layer device tensors in kernel layout (model.py:41-64 contents)."""
+    idx: int
+    wqkv: torch.Tensor   # [(n_q + 2 n_kv) * hd, H] int8
+    wo: torch.Tensor     # [H, n_q * hd]
+    wgu: torch.Tensor    # [2 I, H]
+    wd: torch.Tensor     # [H, I]
+    q_m: torch.Tensor; q_k: int
+    k_m: torch.Tensor; k_k: int
+    v_m: torch.Tensor; v_k: int
+    o_m: torch.Tensor; o_k: int
+    gate_m: torch.Tensor; gate_k: int
+    up_m: torch.Tensor; up_k: int
+    down_m: torch.Tensor; down_k: int
+    q_norm_m: torch.Tensor; q_norm_k: int
+    k_norm_m: torch.Tensor; k_norm_k: int
+    qs_m: torch.Tensor; qs_k: int
+    as_m: torch.Tensor; as_k: int
+    ms_m: torch.Tensor; ms_k: int
+    ds_m: torch.Tensor; ds_k: int
+    os_m: torch.Tensor; os_k: int
+    kq_m: torch.Tensor; kq_k: torch.Tensor
+    ks_m: torch.Tensor; ks_k: torch.Tensor
+    vq_m: torch.Tensor; vq_k: torch.Tensor
+    attn_out_col_m: torch.Tensor
+    attn_out_col_k: int
+
+
+class KVCache:
+    """int8 K/V cache (model.py:67-102 semantics): ``length`` filled slots,
+    contents of filled slots never move, buffers grow geometrically (or to a
+    bucketed static capacity for graphed decode, graphed.py:36-93)."""
+
+    def __init__(self):
+        self.k8: list = []        # per layer [B, n_kv, cap, hd]
+        self.v8: list = []        # per layer V^T [B, n_kv, hd, cap]
+        self.valid_buf = None     # [B, cap] bool
+        self.length = 0
+        self.cap = 0
+        self.static_cap = 0
+        self.len_idx = None       # [1] int64 device: slot written by a graphed step
+        self.nslots = None        # [1] int64 device: slots visible to a graphed step
+
+    @property
+    def valid(self):
+        return None if self.valid_buf is None else self.valid_buf[:, :self.length]
+
+    def seq_len(self) -> int:
+        return self.length
+
+    def _alloc(self, B, n_layers, n_kv, hd, cap, device):
+        self.k8 = [torch.zeros(B, n_kv, cap, hd, dtype=torch.int8, device=device)
+                   for _ in range(n_layers)]
+        self.v8 = [torch.zeros(B, n_kv, hd, cap, dtype=torch.int8, device=device)
+                   for _ in range(n_layers)]
+        self.valid_buf = torch.zeros(B, cap, dtype=torch.bool, device=device)
+        self.cap = cap
+
+    def reserve(self, model: "IntQwen3", B: int, need: int):
+        if not self.k8:
+            cap = max(256, (need + 255) // 256 * 256)
+            self._alloc(B, model.n_layers, model.n_kv, model.hd, cap, model.device)
+        elif need > self.cap:
+            self.resize(max((need + 255) // 256 * 256, 2 * self.cap))
+
+    def resize(self, cap: int):
+        """Reallocate at capacity ``cap`` (multiple of 16), copying the filled
+        prefix verbatim (model.py:93-102, graphed.py:76-93)."""
+        assert cap % 16 == 0
+        L = self.length
+        for li in range(len(self.k8)):
+            B, n_kv, _, hd = self.k8[li].shape
+            nk = self.k8[li].new_zeros(B, n_kv, cap, hd)
+            nk[:, :, :L] = self.k8[li][:, :, :L]
+            nv = self.v8[li].new_zeros(B, n_kv, hd, cap)
+            nv[..., :L] = self.v8[li][..., :L]
+            self.k8[li], self.v8[li] = nk, nv
+        valid = torch.zeros(self.valid_buf.shape[0], cap, dtype=torch.bool,
+                            device=self.valid_buf.device)
+        n = min(cap, self.valid_buf.shape[1])
+        valid[:, :n] = self.valid_buf[:, :n]
+        self.valid_buf = valid
+        self.cap = cap
+
+
+class IntQwen3:
+    def __init__(self, artifact_dir: str, backend: str = "rocm"):
+        from safetensors.torch import load_file
+        self.backend = canonical_backend(backend)
+        if self.backend != "rocm":
+            raise ValueError(f"backend {backend!r} is served by detllm itself; this package "
+                             "implements the 'rocm' backend")
+        if not torch.cuda.is_available():
+            raise RuntimeError("the rocm backend needs a gfx950 GPU (torch.cuda unavailable)")
+        self.device = torch.device("cuda")
+        with open(os.path.join(artifact_dir, "config.json")) as f:
+            self.cfg = json.load(f)
+        tensors = load_file(os.path.join(artifact_dir, "model.safetensors"))
+        for name, t in tensors.items():   # model.py:117-119
+            assert t.dtype in (torch.int8, torch.int16, torch.int32, torch.int64), \
+                f"float tensor in artifact: {name} {t.dtype}"
+        c = self.cfg
+        self.n_layers = c["n_layers"]; self.hidden = c["hidden"]
+        self.n_q = c["n_q_heads"]; self.n_kv = c["n_kv_heads"]; self.hd = c["head_dim"]
+        self.vocab = c["vocab"]; self.inter = c["intermediate"]
+        assert self.hd == 128, "the rocm kernels are specialised to head_dim 128"
+        assert self.n_q % self.n_kv == 0 and self.n_q // self.n_kv in (1, 2, 4, 8)
+        assert self.hidden % 16 == 0 and self.inter % 16 == 0
+        assert self.hd * 127 * 127 < 2 ** 31 and self.inter * 127 * 127 < 2 ** 31
+        dev = self.device
+        g = lambda n: tensors[n].to(dev)
+        gt = lambda n: tensors[n].t().contiguous().to(dev)   # [in, out] -> [out, in]
+        self.embed_e8 = g("embed.e8"); self.embed_m = g("embed.m"); self.embed_k = g("embed.k")
+        self.head_w = gt("head.w8t")                       # [V, H]
+        self.head_m = g("head.m"); self.head_k = c["head"]["k"]
+        self.rope_cos = g("rope.cos").contiguous(); self.rope_sin = g("rope.sin").contiguous()
+        self.max_pos = self.rope_cos.shape[0]
+        group = self.n_q // self.n_kv
+        self.layers: list[LayerWeights] = []
+        for i in range(self.n_layers):
+            p = f"layers.{i}."
+            Lc = c["layers"][i]
+            wqkv = torch.cat([tensors[p + "q.w8t"], tensors[p + "k.w8t"], tensors[p + "v.w8t"]],
+                             dim=1).t().contiguous().to(dev)
+            wgu = torch.cat([tensors[p + "gate.w8t"], tensors[p + "up.w8t"]],
+                            dim=1).t().contiguous().to(dev)
+            vq_m = tensors[p + "vq_m"].to(I64); vq_k = tensors[p + "vq_k"].to(I64)
+            # model.py:165-176: merged attention-output column scale
+            vk_shared = int(vq_k.max())
+            aligned = torch.bitwise_left_shift(vq_m, vk_shared - vq_k)
+            col_m = aligned.repeat_interleave(group).repeat_interleave(self.hd)
+            self.layers.append(LayerWeights(
+                idx=i, wqkv=wqkv, wo=gt(p + "o.w8t"), wgu=wgu, wd=gt(p + "down.w8t"),
+                q_m=g(p + "q.m"), q_k=int(Lc["q"]["k"]), k_m=g(p + "k.m"), k_k=int(Lc["k"]["k"]),
+                v_m=g(p + "v.m"), v_k=int(Lc["v"]["k"]), o_m=g(p + "o.m"), o_k=int(Lc["o"]["k"]),
+                gate_m=g(p + "gate.m"), gate_k=int(Lc["gate"]["k"]),
+                up_m=g(p + "up.m"), up_k=int(Lc["up"]["k"]),
+                down_m=g(p + "down.m"), down_k=int(Lc["down"]["k"]),
+                q_norm_m=g(p + "q_norm.m"), q_norm_k=int(Lc["q_norm_k"]),
+                k_norm_m=g(p + "k_norm.m"), k_norm_k=int(Lc["k_norm_k"]),
+                qs_m=g(p + "qs_m").reshape(-1).contiguous(), qs_k=int(Lc["qs_k"]),
+                as_m=g(p + "as_m"), as_k=int(Lc["as_k"]), ms_m=g(p + "ms_m"), ms_k=int(Lc["ms_k"]),
+                ds_m=g(p + "ds_m"), ds_k=int(Lc["ds_k"]), os_m=g(p + "os_m"), os_k=int(Lc["os_k"]),
+                kq_m=g(p + "kq_m").reshape(-1).contiguous(),
+                kq_k=g(p + "kq_k").reshape(-1).contiguous(),
+                ks_m=g(p + "ks_m"), ks_k=g(p + "ks_k"), vq_m=vq_m.to(dev), vq_k=vq_k.to(dev),
+                attn_out_col_m=col_m.to(dev), attn_out_col_k=vk_shared + (P_OUT_BITS - 1)))
+        del tensors
+        self._greedy_scratch = {}
+
+    # reference-layout view of the LM head (model.py:136)
+    @property
+    def head_w8t(self) -> torch.Tensor:
+        return self.head_w.t()
+
+    # -- GEMM dispatch ---------------------------------------------------------
+    @staticmethod
+    def _ksplit(N: int, K: int) -> int:
+        blocks = (N + 15) // 16
+        ks = max(1, min(K // 256, -(-1024 // blocks)))
+        kchunk = -(-K // ks)
+        kchunk = -(-kchunk // 64) * 64
+        return -(-K // kchunk)
+
+    def _gemm(self, x: torch.Tensor, w: torch.Tensor):
+        R, K = x.shape
+        N = w.shape[0]
+        ks = self._ksplit(N, K) if R <= 64 else 1
+        P = gemm_nt(x, w, ksplit=ks)
+        return P, ks, R * N
+
+    # -- forward (model.py:220-286) ------------------------------------------------
+    def forward(self, ids: torch.Tensor, positions: torch.Tensor, cache: KVCache | None = None,
+                chunk_valid: torch.Tensor | None = None, guard: bool = False):
+        """ids, positions: int64 [B, T]; chunk_valid: bool [B, T] (True = real).
+
+        Returns (logits int32 [B, T, vocab], logit_row_m, logit_row_k, cache)."""
+        if guard:
+            with NoFloatMode():
+                return self._forward(ids, positions, cache, chunk_valid)
+        return self._forward(ids, positions, cache, chunk_valid)
+
+    def _forward(self, ids, positions, cache, chunk_valid, head_rows=None):
+        dev = self.device
+        ids = ids.to(device=dev, dtype=I64)
+        positions = positions.to(device=dev, dtype=I64)
+        B, T = ids.shape
+        if chunk_valid is None:
+            chunk_valid = torch.ones(B, T, dtype=torch.bool, device=dev)
+        chunk_valid = chunk_valid.to(dev)
+        if cache is None:
+            cache = KVCache()
+        static = cache.static_cap > 0
+        S_past = cache.length
+        if static:
+            assert T == 1, "graphed (static-capacity) mode decodes one token per row"
+            S = cache.static_cap
+        else:
+            S = S_past + T
+            cache.reserve(self, B, S)
+            cache.valid_buf[:, S_past:S] = chunk_valid
+        H, R = self.hidden, B * T
+        h = torch.empty(R, H, dtype=torch.int32, device=dev)
+        k_res = torch.empty(R, dtype=I64, device=dev)
+        x8 = torch.empty(R, H, dtype=torch.int8, device=dev)
+        xm = torch.empty(R, dtype=I64, device=dev)
+        xk = torch.empty(R, dtype=I64, device=dev)
+        L0 = self.layers[0]
+        call("detllm_embed_normq", ids.contiguous().view(-1), R, H, self.vocab, self.embed_e8,
+             self.embed_m,
+             self.embed_k, h, k_res, L0.as_m, L0.as_k, x8, xm, xk)
+        pos = positions.contiguous().view(-1)
+        for li, L in enumerate(self.layers):
+            nxt = self.layers[li + 1] if li + 1 < self.n_layers else None
+            self._layer(L, nxt, B, T, h, k_res, x8, xm, xk, pos, cache, S_past, S, static)
+        if not static:
+            cache.length = S
+        if head_rows is not None:
+            xh = x8.view(B, T, H)[torch.arange(B, device=dev), head_rows].contiguous()
+            logits = gemm_nt(xh, self.head_w)[0]
+            return logits, xm.view(B, T, 1), xk.view(B, T, 1), cache
+        logits = gemm_nt(x8, self.head_w)[0].view(B, T, self.vocab)
+        return logits, xm.view(B, T, 1), xk.view(B, T, 1), cache
+
+    def _layer(self, L: LayerWeights, nxt, B, T, h, k_res, x8, xm, xk, pos, cache: KVCache,
+               S_past, S, static):
+        dev = self.device
+        R, H, nq, nkv, hd, I_ = B * T, self.hidden, self.n_q, self.n_kv, self.hd, self.inter
+        li = L.idx
+        P, ns, st = self._gemm(x8, L.wqkv)
+        q8 = torch.empty(B, nq, T, hd, dtype=torch.int8, device=dev)
+        tpos = torch.empty(B, nq, T, dtype=I64, device=dev)
+        call("detllm_qkv_epilogue", P, ns, st, B, T, nq, nkv, xm, xk, pos,
+             L.q_m, L.q_k, L.k_m, L.k_k, L.v_m, L.v_k, L.q_norm_m, L.q_norm_k,
+             L.k_norm_m, L.k_norm_k, L.qs_m, L.qs_k, L.kq_m, L.kq_k, L.ks_m, L.ks_k,
+             L.vq_m, L.vq_k, self.rope_cos, self.rope_sin, self.max_pos, q8, tpos, None,
+             cache.k8[li], cache.v8[li], cache.cap, cache.len_idx if static else None,
+             0 if static else S_past)
+        attn = torch.empty(R, nq * hd, dtype=I64, device=dev)
+        valid = cache.valid_buf.view(torch.uint8)
+        if T == 1:
+            G = nq // nkv
+            Spad = (S + 15) // 16 * 16
+            scratch = None
+            if G * Spad * 4 > 48 * 1024:
+                scratch = torch.empty(B, nq, Spad, dtype=torch.int32, device=dev)
+            call("detllm_attn_decode", q8, tpos, cache.k8[li], cache.v8[li], valid, cache.cap,
+                 B, S, nq, nkv, cache.cap, cache.nslots if static else None, scratch, attn)
+        else:
+            call("detllm_attn_prefill", q8, tpos, cache.k8[li], cache.v8[li], valid, cache.cap,
+                 B, T, S_past, nq, nkv, cache.cap, attn)
+        a8 = torch.empty(R, nq * hd, dtype=torch.int8, device=dev)
+        am = torch.empty(R, dtype=I64, device=dev)
+        ak = torch.empty(R, dtype=I64, device=dev)
+        call("detllm_merge_rowcol", attn, 1, 0, R, nq * hd, L.os_m, L.os_k, L.attn_out_col_m,
+             L.attn_out_col_k, a8, am, ak)
+        P, ns, st = self._gemm(a8, L.wo)
+        call("detllm_residual_normq", P, ns, st, R, H, am, ak, L.o_m, L.o_k, 20, h, k_res,
+             L.ms_m, L.ms_k, x8, xm, xk)
+        P, ns, st = self._gemm(x8, L.wgu)
+        y8 = torch.empty(R, I_, dtype=torch.int8, device=dev)
+        ym = torch.empty(R, dtype=I64, device=dev)
+        yk = torch.empty(R, dtype=I64, device=dev)
+        call("detllm_swiglu_quant", P, ns, st, R, I_, xm, xk, L.gate_m, L.gate_k, L.up_m,
+             L.up_k, L.ds_m, L.ds_k, y8, ym, yk)
+        P, ns, st = self._gemm(y8, L.wd)
+        sm_m, sm_k = (nxt.as_m, nxt.as_k) if nxt is not None else (None, 0)
+        call("detllm_residual_normq", P, ns, st, R, H, ym, yk, L.down_m, L.down_k, 20, h, k_res,
+             sm_m, sm_k, x8, xm, xk)
+
+    # -- decoding (model.py:482-531) ------------------------------------------------
+    def greedy_pick(self, logits_row: torch.Tensor) -> torch.Tensor:
+        """Integer argmax of logits*head_m (int64) with the lowest-id tie-break."""
+        lr = logits_row.to(device=self.device, dtype=torch.int32).contiguous()
+        R = lr.shape[0]
+        nch = -(-self.vocab // GREEDY_CHUNK)
+        key = R
+        sc = self._greedy_scratch.get(key)
+        if sc is None or torch.cuda.is_current_stream_capturing():
+            sc = (torch.empty(R, nch, dtype=I64, device=self.device),
+                  torch.empty(R, nch, dtype=I64, device=self.device))
+            if not torch.cuda.is_current_stream_capturing():
+                self._greedy_scratch[key] = sc
+        out = torch.empty(R, dtype=I64, device=self.device)
+        call("detllm_greedy_pick", lr, self.head_m, R, self.vocab, GREEDY_CHUNK, sc[0], sc[1],
+             out)
+        return out
+
+    @torch.no_grad()
+    def generate(self, ids: torch.Tensor, max_new: int, guard: bool = False,
+                 chunk_valid: torch.Tensor | None = None, stop_at_eos: bool = False,
+                 use_graph: bool = False):
+        """Greedy generation; ids int64 [B, T0] right-padded (pads False in
+        chunk_valid). Returns (tokens [B, max_new], step_logits list of [B, V])."""
+        dev = self.device
+        ids = ids.to(dev)
+        B, T0 = ids.shape
+        if chunk_valid is None:
+            chunk_valid = torch.ones(B, T0, dtype=torch.bool, device=dev)
+        chunk_valid = chunk_valid.to(dev)
+        positions = torch.arange(T0, device=dev).expand(B, T0)
+        lens = chunk_valid.sum(dim=1)
+        last = (lens - 1).clamp(min=0)
+        if guard:
+            with NoFloatMode():
+                first, _, _, cache = self._forward(ids, positions, None, chunk_valid, last)
+        else:
+            first, _, _, cache = self._forward(ids, positions, None, chunk_valid, last)
+        step_logits = [first]
+        cur = self.greedy_pick(first)
+        out = [cur]
+        if use_graph and max_new > 1:
+            from .graphed import GraphedDecode
+            gd = GraphedDecode(self, cache, lens)
+            for _ in range(1, max_new):
+                lg = gd.step(cur).clone()
+                step_logits.append(lg)
+                cur = self.greedy_pick(lg)
+                out.append(cur)
+            return torch.stack(out, dim=1), step_logits
+        ones = torch.ones(B, 1, dtype=torch.bool, device=dev)
+        for step in range(1, max_new):
+            pos = (lens + step - 1).unsqueeze(1)
+            lg, _, _, cache = self.forward(cur.unsqueeze(1), pos, cache, ones, guard)
+            step_logits.append(lg[:, 0])
+            cur = self.greedy_pick(lg[:, 0])
+            out.append(cur)
+        return torch.stack(out, dim=1), step_logits

@@ -1,0 +1,205 @@
+/*
+ * detllm_hip.h — C ABI of libdetllm_hip.so, the MI355X (gfx950) "rocm"
+ * backend of DetLLM's integer forward pass.
+ *
+ * Conventions (every entry point):
+ *   - pointers are DEVICE pointers owned by the caller (torch allocator);
+ *     nothing is allocated, freed, synchronised or read back on the host,
+ *     so every call is safe inside hipGraph stream capture;
+ *   - shapes are explicit ints, arrays are dense row-major;
+ *   - work is enqueued on the given hipStream_t;
+ *   - return 0 on success, > 0 = hipError_t of a failed launch,
+ *     < 0 = argument error (-22 EINVAL, -34 ERANGE, -38 ENOSYS).
+ *   - all arithmetic is integer and bit-identical to the reference CPU
+ *     ("reference") backend: int64 wraps, torch shift clamping, floor
+ *     division, round_half_away_div / rshift_round rounding
+ *     (src/detllm/intmath.py:7-17).
+ *
+ * Reference interfaces each entry replaces are cited as file:line in
+ * rishabh135/idempotent_llm. The reference has no FFI: its boundary is the
+ * Python function named in each citation; the Python mirror in
+ * idempotent_llm_amd/ binds these symbols through ctypes.
+ */
+#ifndef DETLLM_HIP_H
+#define DETLLM_HIP_H
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---------------------------------------------------------------- GEMM -- */
+
+/* int_gemm(a, b, backend) — src/detllm/backends.py:88-135 (batched form
+ * :127-134). C[b] = A[b] . B[b]^T: A [batch][M][K], B [batch][N][K] (the
+ * artifact's [K][N] w8t transposed), C [batch][M][N] int32; batch strides in
+ * elements. K % 16 == 0, K <= 131071. i8 MFMA, 128x128 block tiles. */
+int detllm_igemm_nt(const int8_t* A, const int8_t* B, int32_t* C, int M, int N, int K,
+                    int batch, int64_t sA, int64_t sB, int64_t sC, hipStream_t s);
+
+/* int_gemm for M <= 64 (decode GEMV) — backends.py:88-135 (2-D path :115-119,
+ * decode fast path :121-126). Writes ksplit int32 partials C[k][M][N],
+ * split_stride elements apart, whose integer sum is the product (ksplit = 1:
+ * the product itself). */
+int detllm_igemv_nt(const int8_t* A, const int8_t* B, int32_t* C, int M, int N, int K,
+                    int ksplit, int64_t split_stride, hipStream_t s);
+
+/* Device transpose of int8 [R][C] matrices (operand layout for int_gemm's
+ * [K][N] right-hand side; backends.py:115-119 consumes b as [K][N]). */
+int detllm_transpose_i8(const int8_t* src, int8_t* dst, int R, int C, int batch,
+                        int64_t sS, int64_t sD, hipStream_t s);
+
+/* IntQwen3.greedy_pick — src/detllm/model.py:482-490: out[r] = lowest v
+ * maximising logits[r][v] * head_m[v] (int64). pv/pi: R * ceil(V/chunk)
+ * int64 scratch each. */
+int detllm_greedy_pick(const int32_t* logits, const int64_t* head_m, int R, int V, int chunk,
+                       int64_t* pv, int64_t* pi, int64_t* out, hipStream_t s);
+
+/* ------------------------------------------------- fused layer kernels -- */
+
+/* Embedding lookup + residual_from_delta + _norm_quant —
+ * model.py:246-249 (dyadic.py:187-190, :174-184) fused with model.py:187-198
+ * for the first layer's attention input (sm_m = as_m of layer 0; null skips
+ * the smoothing multiply; x8 null skips the norm-quant). h [R][C] int32,
+ * k_res/xm/xk [R] int64, x8 [R][C] int8. Ids outside [0, vocab) are clamped
+ * (the reference raises IndexError; a device kernel cannot). */
+int detllm_embed_normq(const int64_t* ids, int R, int C, int64_t vocab, const int8_t* e8,
+                       const int64_t* em, const int64_t* ek, int32_t* h, int64_t* k_res,
+                       const int64_t* sm_m, int64_t sm_k, int8_t* x8, int64_t* xm, int64_t* xk,
+                       hipStream_t s);
+
+/* requant_i32_common(P, row_m, row_k, col_m, col_k, tb) + residual_add +
+ * _norm_quant(sm_m, sm_k) — model.py:410-415 / :424-427, :303, :284
+ * (dyadic.py:108-120, :193-206; ops/di_rmsnorm.py:33-52; dyadic.py:93-105).
+ * P: nsplit int32 partials [nsplit][R][C]; h/k_res updated in place. */
+int detllm_residual_normq(const int32_t* P, int nsplit, int64_t split_stride, int R, int C,
+                          const int64_t* row_m, const int64_t* row_k, const int64_t* col_m,
+                          int64_t col_k, int tb, int32_t* h, int64_t* k_res,
+                          const int64_t* sm_m, int64_t sm_k, int8_t* x8, int64_t* xm,
+                          int64_t* xk, hipStream_t s);
+
+/* gate/up requant_i32_common(14) x2 + di_swiglu + quant_i8_pertoken(y*ds_m)
+ * — model.py:416-423 (ops/di_swiglu.py:39-58). P: [nsplit][R][2I] with gate
+ * in columns [0, I) and up in [I, 2I). */
+int detllm_swiglu_quant(const int32_t* P, int nsplit, int64_t split_stride, int R, int I,
+                        const int64_t* xm, const int64_t* xk, const int64_t* gate_m,
+                        int64_t gate_k, const int64_t* up_m, int64_t up_k, const int64_t* ds_m,
+                        int64_t ds_k, int8_t* y8, int64_t* ym, int64_t* yk, hipStream_t s);
+
+/* Attention-output merge: requant_i8_rowcol(attn * os_m, 1, os_k, col_m,
+ * col_k) — model.py:404-409 (dyadic.py:123-139). attn: [nsplit][R][C] int64
+ * partial context sums. */
+int detllm_merge_rowcol(const int64_t* attn, int nsplit, int64_t split_stride, int R, int C,
+                        const int64_t* os_m, int64_t os_k, const int64_t* col_m, int64_t col_k,
+                        int8_t* a8, int64_t* am, int64_t* ak, hipStream_t s);
+
+/* Q/K/V epilogue per (token, head) — model.py:200-216 (_qk_head_pipeline),
+ * :303-340 (QK smoothing, Q quant_i8_pertoken, K/V requant_i8_static, cache
+ * write) and :351-358 (score scale norm_scale + DI-Exp constant tpos).
+ * P: [nsplit][B*T][(n_q + 2 n_kv) * 128] int32 (q | k | v columns).
+ * Outputs: q8 [B][n_q][T][128], tpos [B][n_q][T]; optional dbg
+ * [B][n_q][T][4] = (qm, qk, sm, sk); K into kcache [B][n_kv][cap][128] and
+ * V into vcache [B][n_kv][128][cap] (transposed) at slot base + t, where base
+ * is *slot_base_dev when non-null (graph replay) else slot_base. */
+int detllm_qkv_epilogue(const int32_t* P, int nsplit, int64_t split_stride, int B, int T,
+                        int n_q, int n_kv, const int64_t* xm, const int64_t* xk,
+                        const int64_t* positions, const int64_t* q_m, int64_t q_k,
+                        const int64_t* k_m, int64_t k_k, const int64_t* v_m, int64_t v_k,
+                        const int64_t* q_norm_m, int64_t q_norm_k, const int64_t* k_norm_m,
+                        int64_t k_norm_k, const int64_t* qs_m, int64_t qs_k,
+                        const int64_t* kq_m, const int64_t* kq_k, const int64_t* ks_m,
+                        const int64_t* ks_k, const int64_t* vq_m, const int64_t* vq_k,
+                        const int16_t* cos_t, const int16_t* sin_t, int64_t max_pos,
+                        int8_t* q8, int64_t* tpos, int64_t* dbg, int8_t* kcache,
+                        int8_t* vcache, int64_t cap, const int64_t* slot_base_dev,
+                        int64_t slot_base, hipStream_t s);
+
+/* ------------------------------------------------------------ attention -- */
+
+/* Prefill/chunk attention — model.py:382-402 (_attn_scores :469-474,
+ * di_softmax ops/di_softmax.py:33-61, _attn_context :476-478 with
+ * int_gemm_u16i8 backends.py:152-164). Queries t in [0, T) sit at slots
+ * S_past + t; slot s is visible iff s <= S_past + t and valid[b][s].
+ * out [B][T][n_q*128] int64 = exact sum_s p_s v_s. cap % 16 == 0,
+ * S_past + T <= min(cap, 131071). */
+int detllm_attn_prefill(const int8_t* q8, const int64_t* tpos, const int8_t* kcache,
+                        const int8_t* vcache, const uint8_t* valid, int64_t valid_stride, int B,
+                        int T, int S_past, int n_q, int n_kv, int64_t cap, int64_t* out,
+                        hipStream_t s);
+
+/* Decode attention (one query per row) — model.py:347-381 and the fused
+ * Triton kernel ops/fused_attn.py:47-142 it replaces. Scans S slots (further
+ * bounded by *s_dev when non-null); scratch [B][n_q][ceil16(S)] int32 is
+ * required only when n_q/n_kv * ceil16(S) * 4 > 48 KiB. out [B][n_q*128]. */
+int detllm_attn_decode(const int8_t* q8, const int64_t* tpos, const int8_t* kcache,
+                       const int8_t* vcache, const uint8_t* valid, int64_t valid_stride, int B,
+                       int S, int n_q, int n_kv, int64_t cap, const int64_t* s_dev,
+                       int32_t* scratch, int64_t* out, hipStream_t s);
+
+/* ------------------------------------------- operator-level entry points -- */
+/* One reference function each (rows = leading dims flattened, C = last dim). */
+
+/* dyadic.quant_i8_pertoken — src/detllm/dyadic.py:93-105 */
+int detllm_op_quant_i8_pertoken(const int64_t* x, const int64_t* m, const int64_t* k, int R,
+                                int C, int8_t* x8, int64_t* mo, int64_t* ko, hipStream_t s);
+
+/* dyadic.requant_i32_common — dyadic.py:108-120 (col_m [G][C], row r uses
+ * group r % G) */
+int detllm_op_requant_i32_common(const int64_t* P, const int64_t* row_k, const int64_t* col_m,
+                                 int G, int64_t col_k, int tb, int R, int C, int32_t* y,
+                                 int64_t* ko, hipStream_t s);
+
+/* dyadic.requant_i8_rowcol — dyadic.py:123-139 */
+int detllm_op_requant_i8_rowcol(const int64_t* P, const int64_t* row_m, const int64_t* row_k,
+                                const int64_t* col_m, int64_t col_k, int R, int C, int8_t* y8,
+                                int64_t* mo, int64_t* ko, hipStream_t s);
+
+/* dyadic.requant_i8_static — dyadic.py:142-163 (operands materialised per
+ * element) */
+int detllm_op_requant_i8_static(const int64_t* P, const int64_t* row_m, const int64_t* row_k,
+                                const int64_t* col_m, const int64_t* col_k, const int64_t* s_m,
+                                const int64_t* s_k, int64_t n, int8_t* y8, hipStream_t s);
+
+/* dyadic.residual_renorm (mode 0) / residual_add (mode 1) — dyadic.py:174-206 */
+int detllm_op_residual(int mode, const int64_t* h, const int64_t* k_res, const int64_t* d,
+                       const int64_t* dm, const int64_t* dk, int R, int C, int32_t* h_out,
+                       int64_t* k_out, hipStream_t s);
+
+/* ops.di_rmsnorm (gamma_m null, int32 out) / di_rmsnorm_gamma (int64 out) —
+ * src/detllm/ops/di_rmsnorm.py:33-64 */
+int detllm_op_rmsnorm(const int64_t* x, const int64_t* gamma_m, int R, int C, int32_t* y32,
+                      int64_t* y64, hipStream_t s);
+
+/* ops.di_softmax — src/detllm/ops/di_softmax.py:33-61 */
+int detllm_op_softmax(const int64_t* x, const int64_t* m, const int64_t* k, const uint8_t* valid,
+                      int has_clip, int64_t clip_c, int p_out_bits, int R, int C, int32_t* probs,
+                      hipStream_t s);
+
+/* ops.di_exp — src/detllm/ops/di_exp.py:21-37 */
+int detllm_op_di_exp(const int64_t* x, const int64_t* m, const int64_t* k, int R, int C,
+                     int64_t* res, int64_t* tpos, hipStream_t s);
+
+/* ops.di_swiglu — src/detllm/ops/di_swiglu.py:39-58 */
+int detllm_op_swiglu(const int64_t* gate, const int64_t* gm, const int64_t* gk,
+                     const int64_t* up, const int64_t* um, const int64_t* uk, int R, int C,
+                     int64_t* y, int64_t* ym, int64_t* yk, hipStream_t s);
+
+/* ops.apply_int_rope — src/detllm/ops/rope.py:38-55 (head_dim 128) */
+int detllm_op_rope(const int64_t* x, const int64_t* pos, const int16_t* cos_t,
+                   const int16_t* sin_t, int64_t max_pos, int64_t rows, int64_t* y,
+                   hipStream_t s);
+
+/* Elementwise primitives: op 0 isqrt (intmath.py:180-202, int_prims.py:31-44),
+ * 1 ilog2_floor (intmath.py:164-177, int_prims.py:47-55), 2 norm_scale
+ * (dyadic.py:75-90), 3 fit_dyadic_ratio (dyadic.py:52-72), 4
+ * scaled_round_div (dyadic.py:45-49). */
+int detllm_op_scalar(int op, const int64_t* a, const int64_t* b, const int64_t* c, int64_t n,
+                     int64_t* o1, int64_t* o2, hipStream_t s);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DETLLM_HIP_H */

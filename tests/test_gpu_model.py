@@ -1,0 +1,127 @@
+"""GPU parity of the full IntQwen3 rocm runtime: logits, tokens and the demo
+chain hashes must equal those the reference's CPU backend wrote
+(tests/golden/model_*.json) — eager, graph-captured, right-padded batches,
+split prefill, greedy ties — plus the determinism invariances of the
+reference's tests/test_determinism.py, all exact."""
+
+import json
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from idempotent_llm_amd import artifact as art
+from idempotent_llm_amd.hashchain import chain_hashes, token_chain
+
+pytestmark = pytest.mark.gpu
+HERE = os.path.dirname(os.path.abspath(__file__))
+I64 = torch.int64
+
+
+def _load(name):
+    with open(os.path.join(HERE, "golden", f"model_{name}.json")) as f:
+        return json.load(f)
+
+
+@pytest.fixture(scope="module", params=["tiny", "mid"])
+def case(request, tmp_path_factory):
+    if not torch.cuda.is_available():
+        pytest.skip("needs a GPU")
+    from idempotent_llm_amd.model import IntQwen3
+    rec = _load(request.param)
+    d = str(tmp_path_factory.mktemp(request.param))
+    art.make_artifact(d, rec["dims"], rec["seed"])
+    assert art.artifact_digest(d) == rec["artifact_sha256"], "artifact generator drifted"
+    print(f"[model case {request.param}]", flush=True)
+    return rec, IntQwen3(d, backend="rocm"), d
+
+
+def _ids(rec):
+    return torch.tensor(rec["prompt"], dtype=I64, device="cuda")
+
+
+def test_prefill_logits_and_guard(case):
+    rec, m, _ = case
+    ids = _ids(rec)[None]
+    pos = torch.arange(ids.shape[1], device="cuda")[None]
+    logits, xm, xk, _ = m.forward(ids, pos, guard=True)
+    assert logits.dtype == torch.int32
+    assert chain_hashes(logits[0]) == rec["prefill_chain"]
+    assert logits[0, -1].tolist() == rec["prefill_last_row"]
+    assert xm[0, :, 0].tolist() == rec["prefill_xm"]
+    assert xk[0, :, 0].tolist() == rec["prefill_xk"]
+
+
+def test_generate_b1_eager(case):
+    rec, m, _ = case
+    toks, steps = m.generate(_ids(rec)[None], len(rec["b1_tokens"]))
+    assert toks[0].tolist() == rec["b1_tokens"]
+    assert chain_hashes([s[0] for s in steps]) == rec["b1_logit_chain"]
+    assert token_chain(toks[0]) == rec["b1_token_chain"]
+
+
+def test_generate_b1_graphed(case):
+    rec, m, _ = case
+    toks, steps = m.generate(_ids(rec)[None], len(rec["b1_tokens"]), use_graph=True)
+    assert toks[0].tolist() == rec["b1_tokens"]
+    assert chain_hashes([s[0] for s in steps]) == rec["b1_logit_chain"]
+
+
+@pytest.mark.parametrize("use_graph", [False, True])
+def test_padded_batch(case, use_graph):
+    rec, m, _ = case
+    ids = torch.tensor(rec["batch_ids"], dtype=I64, device="cuda")
+    valid = torch.tensor(rec["batch_valid"], dtype=torch.bool, device="cuda")
+    toks, steps = m.generate(ids, len(rec["b1_tokens"]), chunk_valid=valid, use_graph=use_graph)
+    assert toks.tolist() == rec["batch_tokens"]
+    for b in range(ids.shape[0]):
+        assert chain_hashes([s[b] for s in steps]) == rec["batch_row_chains"][b]
+
+
+def test_split_prefill(case):
+    rec, m, _ = case
+    ids = _ids(rec)
+    T = ids.shape[0]
+    half = T // 2
+    pos = torch.arange(T, device="cuda")[None]
+    full, _, _, _ = m.forward(ids[None], pos)
+    _, _, _, cache = m.forward(ids[None, :half], pos[:, :half])
+    rows = []
+    for t in range(half, T):
+        lg, _, _, cache = m.forward(ids[None, t:t + 1], torch.tensor([[t]], device="cuda"), cache)
+        rows.append(lg[0, 0])
+    assert chain_hashes(rows) == rec["split_tail_chain"]
+    for t in range(half, T):
+        assert torch.equal(rows[t - half], full[0, t])
+
+
+def test_greedy_pick_ties(case):
+    rec, m, _ = case
+    rows = torch.tensor(rec["tie_rows"], dtype=torch.int32, device="cuda")
+    assert m.greedy_pick(rows).tolist() == rec["tie_picks"]
+
+
+def test_run_to_run(case):
+    rec, m, _ = case
+    base_t, base_l = m.generate(_ids(rec)[None], 8, use_graph=True)
+    for _ in range(3):
+        t, lg = m.generate(_ids(rec)[None], 8, use_graph=True)
+        assert torch.equal(t, base_t)
+        for a, b in zip(lg, base_l):
+            assert torch.equal(a, b)
+
+
+def test_graph_growth_matches_oracle(case):
+    """Prompt in bucket 256, decode past 256 slots: the graph is re-captured
+    after the cache grows; every step equals the oracle (graphed.py:76-93)."""
+    rec, m, d = case
+    if rec["dims"]["hidden"] != 256:
+        pytest.skip("tiny model only (oracle speed)")
+    from oracle.model import IntQwen3Oracle
+    steps = 250
+    ids = _ids(rec)[None]
+    tg, lg = m.generate(ids, steps, use_graph=True)
+    te, le = IntQwen3Oracle(d).generate(ids.cpu().numpy(), steps)
+    assert tg.cpu().numpy().tolist() == te.tolist()
+    assert chain_hashes(lg) == chain_hashes(le)

@@ -1,0 +1,220 @@
+"""GPU parity of every op-level HIP kernel (through the C-ABI) against the
+golden vectors written from the reference CPU path, the oracle and closed
+forms. Zero tolerance: every comparison is exact equality."""
+
+import math
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import dyadic as ody
+from oracle import gemm as ogemm
+from oracle import intmath as oim
+from oracle import ops as oops
+
+pytestmark = pytest.mark.gpu
+HERE = os.path.dirname(os.path.abspath(__file__))
+I64 = np.int64
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _need_gpu():
+    if not torch.cuda.is_available():
+        pytest.skip("needs a GPU")
+    from idempotent_llm_amd import _lib
+    _lib.load()   # fails loudly if the HIP library is missing
+
+
+@pytest.fixture(scope="module")
+def D():
+    return dict(np.load(os.path.join(HERE, "golden", "dyadic.npz")))
+
+
+@pytest.fixture(scope="module")
+def O():
+    return dict(np.load(os.path.join(HERE, "golden", "ops.npz")))
+
+
+def g(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def eq(got, want):
+    got = got.cpu().numpy() if isinstance(got, torch.Tensor) else np.asarray(got)
+    want = np.asarray(want)
+    assert got.shape == want.shape, (got.shape, want.shape)
+    assert np.array_equal(got.astype(I64), want.astype(I64))
+
+
+def test_isqrt_ilog2_vs_closed_forms():
+    from idempotent_llm_amd import dyadic as dd
+    rnd = np.random.default_rng(0)
+    v = np.concatenate([rnd.integers(0, 1 << 62, 200000, dtype=I64),
+                        np.arange(0, 70000, dtype=I64),
+                        np.array([0, 1, 2, 3, 4, (1 << 31) - 1, 1 << 31, (1 << 52) + 7,
+                                  (1 << 62) - 1], I64)])
+    got = dd.isqrt(g(v)).cpu().numpy()
+    assert got.tolist() == [math.isqrt(int(x)) for x in v]
+    w = np.concatenate([rnd.integers(1, 1 << 62, 200000, dtype=I64),
+                        np.arange(1, 1 << 16, dtype=I64),
+                        np.array([1, 2, 3, (1 << 62) + 123, (1 << 63) - 1], I64)])
+    got = dd.ilog2_floor(g(w)).cpu().numpy()
+    assert got.tolist() == [int(x).bit_length() - 1 for x in w]
+    x = rnd.integers(0, 1 << 50, (17, 33, 5), dtype=I64)
+    eq(dd.isqrt(g(x)), oim.isqrt(x))
+
+
+def test_dyadic_scalars(D):
+    from idempotent_llm_amd import dyadic as dd
+    eq(dd.scaled_round_div(g(D["srd_num"]), g(D["srd_den"]), g(D["srd_e"])), D["srd_out"])
+    m, e = dd.fit_dyadic_ratio(g(D["fit_num"]), g(D["fit_den"]))
+    eq(m, D["fit_m"]); eq(e, D["fit_e"])
+    m, e = dd.fit_dyadic_ratio(g(D["fit_num"]), 127)
+    eq(m, D["fit127_m"]); eq(e, D["fit127_e"])
+    m2, k2 = dd.norm_scale(g(D["ns_m"]), g(D["ns_k"]))
+    eq(m2, D["ns_m2"]); eq(k2, D["ns_k2"])
+
+
+def test_quant_i8_pertoken(D):
+    from idempotent_llm_amd import dyadic as dd
+    for p in ("q", "q64"):
+        x8, mo, ko = dd.quant_i8_pertoken(g(D[p + "_x"]), g(D[p + "_m"]), g(D[p + "_k"]))
+        assert x8.dtype == torch.int8
+        eq(x8, D[p + "_x8"]); eq(mo, D[p + "_mo"]); eq(ko, D[p + "_ko"])
+
+
+def test_requant_i32_common(D):
+    from idempotent_llm_amd import dyadic as dd
+    for tb in (12, 14, 16, 20):
+        y, m, k = dd.requant_i32_common(g(D["rq_P"]), g(D["rq_rm"]), g(D["rq_rk"]),
+                                        g(D["rq_cm"]), 24, target_bits=tb)
+        assert y.dtype == torch.int32
+        eq(y, D[f"rq{tb}_y"]); eq(m, D[f"rq{tb}_m"]); eq(k, D[f"rq{tb}_k"])
+
+
+def test_requant_i32_common_grouped_cols():
+    # per-(head, channel) column scales as in _qk_head_pipeline (model.py:207-211)
+    from idempotent_llm_amd import dyadic as dd
+    rnd = np.random.default_rng(3)
+    P = rnd.integers(-(1 << 24), 1 << 24, (2, 5, 4, 128)).astype(np.int32)
+    rm = rnd.integers(1 << 15, 1 << 16, (2, 5, 1, 1), dtype=I64)
+    rk = rnd.integers(10, 40, (2, 5, 1, 1), dtype=I64)
+    cm = rnd.integers(1 << 14, 1 << 16, (4, 128), dtype=I64)
+    y, m, k = dd.requant_i32_common(g(P), g(rm), g(rk), g(cm), 24, target_bits=16)
+    wy, wm, wk = ody.requant_i32_common(P, rm, rk, cm, 24, 16)
+    eq(y, wy); eq(k, wk)
+
+
+def test_requant_i8_rowcol(D):
+    from idempotent_llm_amd import dyadic as dd
+    y8, m, k = dd.requant_i8_rowcol(g(D["rq_P"]), g(D["rq_rm"]), g(D["rq_rk"]), g(D["rq_cm"]), 24)
+    eq(y8, D["rc_y8"]); eq(m, D["rc_m"]); eq(k, D["rc_k"])
+    y8, m, k = dd.requant_i8_rowcol(g(D["rc64_P"]), g(D["rc64_rm"]), g(D["rc64_rk"]),
+                                    g(D["rc64_cm"]), 30)
+    eq(y8, D["rc64_y8"]); eq(m, D["rc64_m"]); eq(k, D["rc64_k"])
+
+
+def test_requant_i8_static(D):
+    from idempotent_llm_amd import dyadic as dd
+    eq(dd.requant_i8_static(g(D["rs_P"]), g(D["rs_rm"]), g(D["rs_rk"]), g(D["rs_cm"]), 24,
+                            g(D["rs_sm"]), g(D["rs_sk"])), D["rs_y8"])
+    eq(dd.requant_i8_static(g(D["rsk_x"]), 1, 31, 1, 0, g(D["rsk_m"]), g(D["rsk_k"])),
+       D["rsk_y8"])
+    eq(dd.requant_i8_static(g(D["rq_P"]), 1, 0, g(D["rq_cm"]), 20, 1, 0), D["rs0_y8"])
+
+
+def test_residual(D):
+    from idempotent_llm_amd import dyadic as dd
+    h, k = dd.residual_renorm(g(D["rr_h64"]), g(D["rr_k"]))
+    eq(h, D["rr_h"]); eq(k, D["rr_k2"])
+    h, k = dd.residual_from_delta(g(D["rf_d"]), g(D["rf_dm"]), g(D["rf_dk"]))
+    eq(h, D["rf_h"]); eq(k, D["rf_k"])
+    h3, k3 = dd.residual_add(h, k, g(D["ra_d"]), g(D["ra_dm"]), g(D["ra_dk"]))
+    eq(h3, D["ra_h"]); eq(k3, D["ra_k"])
+
+
+def test_di_exp(O):
+    from idempotent_llm_amd import ops
+    res, tpos = ops.di_exp(g(O["exp_x"]), g(O["exp_m"]), g(O["exp_k"]))
+    eq(res, O["exp_res"]); eq(tpos, O["exp_tpos"])
+
+
+def test_di_softmax(O):
+    from idempotent_llm_amd import ops
+    args = (g(O["sm_x"]), g(O["sm_m"]), g(O["sm_k"]), g(O["sm_valid"]))
+    eq(ops.di_softmax(*args), O["sm_p15"])
+    eq(ops.di_softmax(*args, p_out_bits=8), O["sm_p8"])
+    eq(ops.di_softmax(*args, clip_c=15), O["sm_pc15"])
+    z = ops.di_softmax(args[0], args[1], args[2], torch.zeros_like(args[3]))
+    assert int(z.abs().max()) == 0
+
+
+def test_di_rmsnorm(O):
+    from idempotent_llm_amd import ops
+    for n in (1024, 128, 3072):
+        eq(ops.di_rmsnorm(g(O[f"rms{n}_x"])), O[f"rms{n}_y"])
+    eq(ops.di_rmsnorm(g(O["rms64_x"])), O["rms64_y"])
+    y, k = ops.di_rmsnorm_gamma(g(O["rmsg_x"]), g(O["rmsg_gm"]), 13)
+    eq(y, O["rmsg_y"]); assert k == int(O["rmsg_k"])
+
+
+def test_di_swiglu(O):
+    from idempotent_llm_amd import ops
+    y, m, k = ops.di_swiglu(g(O["sw_g"]), g(O["sw_gm"]), g(O["sw_gk"]), g(O["sw_u"]),
+                            g(O["sw_um"]), g(O["sw_uk"]))
+    eq(y, O["sw_y"]); eq(m, O["sw_ym"]); eq(k, O["sw_yk"])
+
+
+def test_rope(O):
+    from idempotent_llm_amd import ops
+    cos_t, sin_t = oops.build_rope_tables(128, 4096, 1e6)
+    eq(ops.apply_int_rope(g(O["rope_x"]), g(cos_t), g(sin_t), g(O["rope_pos"])), O["rope_y"])
+
+
+@pytest.mark.parametrize("M,K,N", [(7, 33, 5), (1, 1024, 4096), (8, 3072, 1024), (64, 1024, 3072),
+                                   (65, 1024, 3072), (200, 128, 300), (512, 2048, 1024)])
+def test_int_gemm_exact(M, K, N):
+    from idempotent_llm_amd.backends import int_gemm
+    rnd = np.random.default_rng(M * 7 + K + N)
+    a = rnd.integers(-128, 128, (M, K)).astype(np.int8)
+    b = rnd.integers(-128, 128, (K, N)).astype(np.int8)
+    got = int_gemm(g(a), g(b), "rocm")
+    assert got.dtype == torch.int32
+    eq(got, a.astype(I64) @ b.astype(I64))
+
+
+def test_int_gemm_extremes_and_batched():
+    from idempotent_llm_amd.backends import int_gemm, int_gemm_u8i8, int_gemm_u16i8
+    a = np.full((70, 3072), -128, np.int8)
+    b = np.full((3072, 40), -128, np.int8)
+    eq(int_gemm(g(a), g(b), "rocm"), np.full((70, 40), 3072 * 128 * 128))
+    rnd = np.random.default_rng(9)
+    a = rnd.integers(-128, 128, (3, 4, 37, 128)).astype(np.int8)
+    b = rnd.integers(-128, 128, (3, 4, 128, 45)).astype(np.int8)
+    eq(int_gemm(g(a), g(b), "rocm"), a.astype(I64) @ b.astype(I64))
+    p = rnd.integers(0, 129, (9, 21)).astype(np.int32)
+    v = rnd.integers(-128, 128, (21, 6)).astype(np.int8)
+    eq(int_gemm_u8i8(g(p), g(v), "rocm"), p.astype(I64) @ v.astype(I64))
+    p = rnd.integers(0, (1 << 14) + 1, (9, 300)).astype(np.int32)
+    v = rnd.integers(-128, 128, (300, 6)).astype(np.int8)
+    eq(int_gemm_u16i8(g(p), g(v), "rocm"), ogemm.int_gemm_u16i8(p, v))
+
+
+def test_config0_gemm_requant():
+    """[64,1024] x [1024,3072] then requant_i8_static(P,1,0,m,20,1,0)
+    and the rowcol variant, bit-identical to the CPU path."""
+    from idempotent_llm_amd import artifact as art
+    from idempotent_llm_amd import dyadic as dd
+    from idempotent_llm_amd.backends import int_gemm
+    A = art.rand_i8(0, "c0.A", (64, 1024))
+    W = art.rand_i8(0, "c0.W", (1024, 3072))
+    m = art.uniform_int(0, "c0.m", (3072,), 1 << 14, 1 << 15)
+    P = int_gemm(g(A), g(W), "rocm")
+    Pw = ogemm.int_gemm(A, W)
+    eq(P, Pw)
+    eq(dd.requant_i8_static(P, 1, 0, g(m), 20, 1, 0), ody.requant_i8_static(Pw, 1, 0, m, 20, 1, 0))
+    y8, mo, ko = dd.requant_i8_rowcol(P, 1, 0, g(m), 20)
+    wy, wm, wk = ody.requant_i8_rowcol(Pw, np.ones((64, 1), I64), np.zeros((64, 1), I64), m, 20)
+    eq(y8, wy); eq(mo, wm); eq(ko, wk)

@@ -1,0 +1,181 @@
+"""CPU checks of intops.h — the integer routines every HIP kernel shares —
+through its host build (libdetllm_intops_host.so).
+
+Pinned against Python's exact integer arithmetic (division by invariant
+divisors near multiples of d, at int64 extremes) and against the oracle,
+which is itself pinned to the reference's golden vectors."""
+
+import ctypes
+import os
+import random
+
+import numpy as np
+import pytest
+
+from oracle import dyadic as ody
+from oracle import intmath as oim
+from oracle import ops as oops
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HOST = os.path.join(ROOT, "idempotent_llm_amd", "libdetllm_intops_host.so")
+I64 = np.int64
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not os.path.exists(HOST):
+        from idempotent_llm_amd.build import build_host_shim
+        build_host_shim()
+    return ctypes.CDLL(HOST)
+
+
+def _p(a):
+    return a.ctypes.data_as(ctypes.c_void_p)
+
+
+def _call2(lib, name, a, b):
+    a = np.ascontiguousarray(a, I64)
+    b = np.ascontiguousarray(b, I64)
+    out = np.empty_like(a)
+    getattr(lib, name)(_p(a), _p(b), ctypes.c_int64(a.size), _p(out))
+    return out
+
+
+def _py_floor_div(a, d):
+    return a // d
+
+
+def _py_rhad(a, d):
+    q = (abs(a) + d // 2) // d
+    return -q if a < 0 else q
+
+
+def _wrap(v):
+    v &= (1 << 64) - 1
+    return v - (1 << 64) if v >= 1 << 63 else v
+
+
+def _divisor_cases(seed=0, n=40000):
+    rnd = random.Random(seed)
+    A, D = [], []
+    ds = [1, 2, 3, 7, 127, 128, 1 << 20, (1 << 31) - 1, 1 << 31, (1 << 32) + 1,
+          (1 << 47) - 3, (1 << 62) + 11, (1 << 63) - 1]
+    ds += [rnd.randrange(1, 1 << rnd.randrange(1, 63)) for _ in range(200)]
+    for d in ds:
+        for _ in range(n // len(ds)):
+            kind = rnd.randrange(4)
+            if kind == 0:       # near a multiple of d
+                q = rnd.randrange(0, max(1, ((1 << 63) - 1) // d))
+                a = q * d + rnd.choice([-1, 0, 1, d // 2, d // 2 + 1, (d - 1) // 2])
+            elif kind == 1:
+                a = rnd.randrange(-(1 << 63), 1 << 63)
+            elif kind == 2:
+                a = rnd.randrange(-(1 << 24), 1 << 24)
+            else:
+                a = rnd.choice([0, 1, -1, (1 << 63) - 1, -(1 << 63) + 1, -(1 << 63)])
+            a = max(-(1 << 63), min((1 << 63) - 1, a))
+            A.append(a)
+            D.append(d)
+    return np.array(A, dtype=I64), np.array(D, dtype=I64)
+
+
+def test_floor_div_by_reciprocal_exact(lib):
+    A, D = _divisor_cases(1)
+    got = _call2(lib, "di_host_floor_div_r", A, D)
+    want = [_py_floor_div(int(a), int(d)) for a, d in zip(A, D)]
+    assert got.tolist() == want
+
+
+def test_rhad_by_reciprocal_matches_generic_and_python(lib):
+    A, D = _divisor_cases(2)
+    got_r = _call2(lib, "di_host_rhad_r", A, D)
+    got = _call2(lib, "di_host_rhad", A, D)
+    # the reference's formula on wrapping int64: mag + half may wrap
+    want = []
+    for a, d in zip(A.tolist(), D.tolist()):
+        mag = _wrap(abs(a)) if a != -(1 << 63) else -(1 << 63)
+        s = _wrap(mag + d // 2)
+        q = s // d
+        want.append(_wrap(-q) if a < 0 else q)
+    assert got.tolist() == want
+    assert got_r.tolist() == want
+
+
+def test_rshift_round_matches_oracle(lib):
+    rnd = np.random.default_rng(3)
+    a = np.concatenate([rnd.integers(-(1 << 62), 1 << 62, 20000, dtype=I64),
+                        np.array([0, -1, 1, (1 << 63) - 1, -(1 << 63)], I64)])
+    k = rnd.integers(0, 70, a.size, dtype=I64)
+    got = _call2(lib, "di_host_rshift_round", a, k)
+    assert np.array_equal(got, oim.rshift_round_t(a, k))
+
+
+def test_di_exp_matches_oracle(lib):
+    rnd = np.random.default_rng(4)
+    rows = 64
+    m = rnd.integers(1 << 15, 1 << 16, (rows, 1), dtype=I64)
+    k = rnd.integers(5, 62, (rows, 1), dtype=I64)
+    x = -rnd.integers(0, 1 << 40, (rows, 300), dtype=I64)
+    x[:, 0] = 0
+    want, tpos = oops.di_exp(x, m, k)
+    t = _call2(lib, "di_host_di_exp_tpos", m.ravel(), k.ravel())
+    assert np.array_equal(t, tpos.ravel())
+    got = _call2(lib, "di_host_di_exp", x.ravel(), np.broadcast_to(tpos, x.shape).ravel())
+    assert np.array_equal(got.reshape(x.shape), want)
+
+
+def test_sigmoid_div_matches_rhad(lib):
+    rnd = np.random.default_rng(5)
+    den = rnd.integers(1, 1 << 50, 20000, dtype=I64)
+    num = (den * rnd.integers(0, 1001, den.size) // 1000).astype(I64)
+    num[:5] = den[:5]
+    num[5:10] = 0
+    got = _call2(lib, "di_host_sigmoid_div", num, den)
+    assert np.array_equal(got, oim.rhad(oim.shl(num, 7), den))
+
+
+def test_swiglu_elem_matches_oracle(lib):
+    rnd = np.random.default_rng(6)
+    rows, C = 16, 777
+    gate = rnd.integers(-(1 << 14), (1 << 14) + 1, (rows, C), dtype=I64)
+    up = rnd.integers(-(1 << 14), (1 << 14) + 1, (rows, C), dtype=I64)
+    gm = rnd.integers(1 << 15, 1 << 16, (rows, 1), dtype=I64)
+    gk = rnd.integers(10, 40, (rows, 1), dtype=I64)
+    y, _, _ = oops.di_swiglu(gate, gm, gk, up, gm, gk)
+    tpos = oops.di_exp_tpos(gm, gk)
+    g = np.ascontiguousarray(gate.ravel())
+    u = np.ascontiguousarray(up.ravel())
+    t = np.ascontiguousarray(np.broadcast_to(tpos, gate.shape).ravel())
+    out = np.empty_like(g)
+    lib.di_host_swiglu(_p(g), _p(u), _p(t), ctypes.c_int64(g.size), _p(out))
+    assert np.array_equal(out.reshape(gate.shape), y)
+
+
+def _scalar(lib, op, a, b=None, c=None):
+    a = np.ascontiguousarray(a, I64)
+    b = np.ascontiguousarray(b if b is not None else np.zeros_like(a), I64)
+    c = np.ascontiguousarray(c if c is not None else np.zeros_like(a), I64)
+    o1 = np.empty_like(a)
+    o2 = np.empty_like(a)
+    lib.di_host_scalar(ctypes.c_int(op), _p(a), _p(b), _p(c), ctypes.c_int64(a.size), _p(o1),
+                       _p(o2))
+    return o1, o2
+
+
+def test_scalar_ops_match_oracle(lib, golden_dir):
+    D = dict(np.load(os.path.join(golden_dir, "dyadic.npz")))
+    rnd = np.random.default_rng(7)
+    v = np.concatenate([rnd.integers(-(1 << 62), 1 << 62, 20000, dtype=I64),
+                        np.arange(-5, 70000, dtype=I64)])
+    assert np.array_equal(_scalar(lib, 0, v)[0], oim.isqrt(v))
+    assert np.array_equal(_scalar(lib, 1, v)[0], oim.ilog2(v))
+    m2, k2 = _scalar(lib, 2, D["ns_m"], D["ns_k"])
+    assert np.array_equal(m2, D["ns_m2"]) and np.array_equal(k2, D["ns_k2"])
+    m, e = _scalar(lib, 3, D["fit_num"], D["fit_den"])
+    assert np.array_equal(m, D["fit_m"]) and np.array_equal(e, D["fit_e"])
+    out, _ = _scalar(lib, 4, D["srd_num"], D["srd_den"], D["srd_e"])
+    assert np.array_equal(out, D["srd_out"])
+    m, e = _scalar(lib, 3, D["fit_num"], np.full_like(D["fit_num"], 127))
+    assert np.array_equal(m, D["fit127_m"]) and np.array_equal(e, D["fit127_e"])
+    wm, we = ody.norm_scale(D["ns_m"], D["ns_k"])
+    assert np.array_equal(wm, m2) and np.array_equal(we, k2)

@@ -1,0 +1,95 @@
+"""The C-ABI library loads without a GPU and exports every symbol that
+include/detllm_hip.h declares; the Python binding covers each with the
+header's arity. Also the host-side API checks that need no GPU."""
+
+import ctypes
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "detllm_hip.h")
+LIB = os.path.join(ROOT, "idempotent_llm_amd", "libdetllm_hip.so")
+
+
+def _declarations():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    decls = {}
+    for m in re.finditer(r"int\s+(detllm_\w+)\s*\(([^;]*?)\)\s*;", text, flags=re.S):
+        params = [p for p in m.group(2).split(",") if p.strip()]
+        decls[m.group(1)] = len(params)
+    return decls
+
+
+def test_header_declares_entry_points():
+    decls = _declarations()
+    assert len(decls) >= 20
+    assert "detllm_igemm_nt" in decls and "detllm_attn_decode" in decls
+
+
+@pytest.mark.skipif(not os.path.exists(LIB), reason="library not built (run build())")
+def test_library_exports_every_declared_symbol():
+    lib = ctypes.CDLL(LIB)
+    missing = [n for n in _declarations() if not hasattr(lib, n)]
+    assert not missing, missing
+
+
+def test_python_binding_matches_header_arity():
+    from idempotent_llm_amd._lib import SIGNATURES
+    decls = _declarations()
+    assert set(SIGNATURES) == set(decls)
+    for name, n in decls.items():
+        assert len(SIGNATURES[name]) == n, name
+        assert SIGNATURES[name][-1] == "s", name   # every entry takes a stream last
+
+
+def test_backend_names():
+    # the reference's tests/test_ops.py:33-48, extended by "rocm"
+    from idempotent_llm_amd.backends import BACKENDS, canonical_backend
+    assert canonical_backend("cpu") == "reference"
+    assert canonical_backend("hip") == "rocm"
+    for name in BACKENDS:
+        assert canonical_backend(name) == name
+    for bad in ("mps", "metal", "CPU", "reference ", "ROCM"):
+        with pytest.raises(ValueError):
+            canonical_backend(bad)
+
+
+def test_int_gemm_rejects_non_int8_and_other_backends():
+    import torch
+
+    from idempotent_llm_amd.backends import int_gemm
+    a = torch.zeros(2, 3, dtype=torch.int8)
+    with pytest.raises(AssertionError):
+        int_gemm(a.to(torch.int32), torch.zeros(3, 2, dtype=torch.int8), "rocm")
+    with pytest.raises(AssertionError):
+        int_gemm(a, torch.zeros(4, 2, dtype=torch.int8), "rocm")
+    with pytest.raises(ValueError):
+        int_gemm(a, torch.zeros(3, 2, dtype=torch.int8), "reference")
+
+
+def test_guard_fires_on_float():
+    import torch
+
+    from idempotent_llm_amd.guard import FloatLeakError, NoFloatMode
+    with pytest.raises(FloatLeakError):
+        with NoFloatMode():
+            torch.ones(3).float() * 2.0
+    with NoFloatMode():
+        (torch.ones(3, dtype=torch.int64) * 2).sum()
+
+
+def test_model_requires_gpu_loudly(tmp_path):
+    import torch
+
+    from idempotent_llm_amd import artifact as art
+    from idempotent_llm_amd.model import IntQwen3
+    if torch.cuda.is_available():
+        pytest.skip("GPU present")
+    d = art.make_artifact(str(tmp_path), art.TINY, seed=1)
+    with pytest.raises(RuntimeError):
+        IntQwen3(d, backend="rocm")
+    with pytest.raises(ValueError):
+        IntQwen3(d, backend="cpu")
