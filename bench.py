@@ -1,0 +1,266 @@
+"""Decode throughput of the integer Qwen3-0.6B-shaped forward pass on one MI355X.
+
+Usage: python bench.py [--gpus 1] [--steps 64] [--warmup 10] [--no-cpu]
+
+Workload (the configuration the headline metric is quoted on): the full
+Qwen3-0.6B-shaped random-init integer artifact (28 layers, hidden 1024,
+16q/8kv x 128, FFN 3072, vocab 151936; seed 3), seeded random prompts of 128
+ids in [100, 50000), greedy decode through the graph-captured step, timed as
+the reference's scripts/bench.py:31-43 does: 10 warm-up steps, then K steps,
+tok/s = B * K / seconds. A "step" is one decode step of the whole batch
+(graph replay of 28 layers + LM head, then the on-device greedy pick).
+
+``value`` is batch-8 decode tok/s; batch 1, prefill (2048 tokens) and the
+int8 GEMM TOPS at the prefill shapes are reported beside it. ``roofline``
+describes the kernel that dominates the decode step (the skinny int8 GEMM
+``k_gemv_nt``): algorithmic bytes per launch (weights + activations + int32
+outputs) over its average launch duration, timed with HIP events on the
+stream it runs on. ``cpu_baseline`` times the numpy CPU restatement of the
+reference path (``oracle/``) on this host for a few decode steps.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import tempfile
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, GB/s
+I8_PEAK_TOPS = 5000.0          # MI355X dense int8 MFMA, TOP/s
+A100_B8_TOKS = 783.3           # reference's published A100 batch-8 decode tok/s
+PROMPT_LEN = 128
+PREFILL_LEN = 2048
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def _prompts(B: int, T: int, vocab: int):
+    import numpy as np
+    from idempotent_llm_amd import artifact as art
+    rows = [art.prompt_ids(30 + b, T, vocab) for b in range(B)]
+    return np.stack(rows)
+
+
+def decode_bench(model, B: int, steps: int, warmup: int):
+    """Reference methodology (scripts/bench.py:31-43) on the rocm backend.
+    Returns (tok/s, ms/step, tokens [B, steps])."""
+    import torch
+    from idempotent_llm_amd.graphed import GraphedDecode
+    ids = torch.from_numpy(_prompts(B, PROMPT_LEN, model.vocab)).cuda()
+    pos = torch.arange(PROMPT_LEN, device="cuda").expand(B, PROMPT_LEN)
+    lens = torch.full((B,), PROMPT_LEN, dtype=torch.int64, device="cuda")
+    logits, _, _, cache = model.forward(ids, pos)
+    gd = GraphedDecode(model, cache, lens)
+    cur = model.greedy_pick(logits[:, -1])
+    for _ in range(warmup):
+        cur = model.greedy_pick(gd.step(cur))
+    torch.cuda.synchronize()
+    toks = torch.empty(B, steps, dtype=torch.int64, device="cuda")
+    t0 = time.perf_counter()
+    for i in range(steps):
+        cur = model.greedy_pick(gd.step(cur))
+        toks[:, i] = cur
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    return B * steps / dt, 1e3 * dt / steps, toks.cpu()
+
+
+def prefill_bench(model, T: int):
+    import torch
+    ids = torch.from_numpy(_prompts(1, T, model.vocab)).cuda()
+    pos = torch.arange(T, device="cuda")[None]
+    model.forward(ids, pos)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    model.forward(ids, pos)
+    torch.cuda.synchronize()
+    return T / (time.perf_counter() - t0)
+
+
+def _graph_time_us(fn, reps: int, launches: int) -> float:
+    """Average duration of one launch of ``fn``'s kernels: the launches are
+    recorded into a HIP graph and the graph replayed ``reps`` times between
+    two events on the capturing stream."""
+    import torch
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        fn()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            fn()
+        g.replay()
+        s.synchronize()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record(s)
+        for _ in range(reps):
+            g.replay()
+        e1.record(s)
+        e1.synchronize()
+    torch.cuda.current_stream().wait_stream(s)
+    return 1e3 * e0.elapsed_time(e1) / (reps * launches)
+
+
+def gemv_roofline(model, B: int):
+    """The decode step's skinny GEMMs (q|k|v, o, gate|up, down per layer and
+    the LM head) with the model's own weights and K splits: algorithmic bytes
+    per launch / average launch duration."""
+    import torch
+    from idempotent_llm_amd.backends import gemm_nt
+    dev = "cuda"
+    H, I_ = model.hidden, model.inter
+    nqd = model.n_q * model.hd
+    x_h = torch.randint(-127, 128, (B, H), dtype=torch.int8, device=dev)
+    x_a = torch.randint(-127, 128, (B, nqd), dtype=torch.int8, device=dev)
+    x_i = torch.randint(-127, 128, (B, I_), dtype=torch.int8, device=dev)
+    jobs = []
+    for L in model.layers:
+        for x, w in ((x_h, L.wqkv), (x_a, L.wo), (x_h, L.wgu), (x_i, L.wd)):
+            N, K = w.shape
+            ks = model._ksplit(N, K)
+            jobs.append((x, w, torch.empty(ks, B, N, dtype=torch.int32, device=dev), ks))
+    N, K = model.head_w.shape
+    jobs.append((x_h, model.head_w, torch.empty(1, B, N, dtype=torch.int32, device=dev), 1))
+    nbytes = sum(w.numel() + x.numel() + 4 * B * w.shape[0] for x, w, _, _ in jobs)
+
+    def run():
+        for x, w, out, ks in jobs:
+            gemm_nt(x, w, out=out, ksplit=ks)
+
+    us = _graph_time_us(run, 20, len(jobs))
+    per_launch = nbytes / len(jobs)
+    achieved = per_launch / (us * 1e-6) / 1e9
+    return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+            "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+            "kernel": "k_gemv_nt<1>", "batch": B, "launches_per_step": len(jobs),
+            "bytes_per_launch": int(per_launch), "avg_launch_us": round(us, 3)}
+
+
+def gemm_tops(T: int = PREFILL_LEN):
+    """int8 GEMM TOP/s at the prefill shapes (T tokens): q|k|v, o, gate|up, down."""
+    import torch
+    from idempotent_llm_amd.backends import gemm_nt
+    dev = "cuda"
+    shapes = {"qkv": (T, 4096, 1024), "o": (T, 1024, 2048), "gate_up": (T, 6144, 1024),
+              "down": (T, 1024, 3072)}
+    res = {}
+    tot_ops = tot_us = 0.0
+    for name, (M, N, K) in shapes.items():
+        a = torch.randint(-127, 128, (M, K), dtype=torch.int8, device=dev)
+        w = torch.randint(-127, 128, (N, K), dtype=torch.int8, device=dev)
+        out = torch.empty(1, M, N, dtype=torch.int32, device=dev)
+        us = _graph_time_us(lambda: gemm_nt(a, w, out=out), 50, 1)
+        ops = 2.0 * M * N * K
+        tops = ops / (us * 1e-6) / 1e12
+        res[name] = {"M": M, "N": N, "K": K, "us": round(us, 2), "tops": round(tops, 1),
+                     "frac_peak": round(tops / I8_PEAK_TOPS, 4)}
+        tot_ops += ops
+        tot_us += us
+    tops = tot_ops / (tot_us * 1e-6) / 1e12
+    res["all"] = {"tops": round(tops, 1), "frac_peak": round(tops / I8_PEAK_TOPS, 4)}
+    return res
+
+
+def cpu_baseline(art_dir: str, steps: int = 3):
+    """Decode tok/s of the numpy CPU restatement (oracle/) at batch 1: prefill
+    of the 128-token prompt (untimed), then ``steps`` timed decode steps."""
+    import numpy as np
+    from oracle.model import IntQwen3Oracle
+    o = IntQwen3Oracle(art_dir)
+    ids = _prompts(1, PROMPT_LEN, o.vocab)
+    pos = np.arange(PROMPT_LEN, dtype=np.int64)[None]
+    logits, _, _, cache = o.forward(ids, pos)
+    cur = o.greedy_pick(logits[:, -1])
+    t0 = time.perf_counter()
+    for i in range(steps):
+        lg, _, _, cache = o.forward(cur[:, None], np.array([[PROMPT_LEN + i]]), cache)
+        cur = o.greedy_pick(lg[:, 0])
+    dt = time.perf_counter() - t0
+    cores = len(os.sched_getaffinity(0))
+    omp = os.environ.get("OMP_NUM_THREADS")
+    if omp and omp.isdigit():
+        cores = min(cores, int(omp))
+    return {"value": round(steps / dt, 4), "unit": "tok/s", "cores": cores, "kind": "port",
+            "sample": f"batch 1, {steps} decode steps after a {PROMPT_LEN}-token prefill "
+                      f"(prefill untimed), full 28-layer model, numpy oracle"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=64)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--batch", type=int, default=8)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-extras", action="store_true",
+                    help="decode only (no prefill/GEMM/roofline legs)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}): the integer "
+              "forward pass here is built and measured on a single MI355X", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from idempotent_llm_amd import artifact as art
+    from idempotent_llm_amd.model import IntQwen3
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+
+    with tempfile.TemporaryDirectory(prefix="detllm_bench_") as d:
+        t0 = time.perf_counter()
+        art.make_artifact(d, art.QWEN3_0_6B, seed=3)
+        log(f"artifact generated in {time.perf_counter() - t0:.1f}s")
+        model = IntQwen3(d, backend="rocm")
+        log("model loaded")
+        B = args.batch
+        tps, ms, toks = decode_bench(model, B, args.steps, args.warmup)
+        log(f"decode b{B}: {tps:.1f} tok/s ({ms:.3f} ms/step)")
+        tps1, ms1, toks1 = decode_bench(model, 1, args.steps, args.warmup)
+        log(f"decode b1: {tps1:.1f} tok/s ({ms1:.3f} ms/step)")
+        invariant = bool(torch.equal(toks[0], toks1[0]))
+        extras = {}
+        roof = None
+        if not args.no_extras:
+            extras["prefill_tok_s_2048"] = round(prefill_bench(model, PREFILL_LEN), 1)
+            log(f"prefill 2048: {extras['prefill_tok_s_2048']} tok/s")
+            extras["int8_gemm_prefill"] = gemm_tops()
+            log(f"gemm: {extras['int8_gemm_prefill']['all']}")
+            roof = gemv_roofline(model, B)
+            log(f"roofline: {roof}")
+        del model
+        torch.cuda.empty_cache()
+        cpu = None
+        if not args.no_cpu:
+            cpu = cpu_baseline(d)
+            log(f"cpu baseline: {cpu}")
+
+    line = {
+        "metric": "decode tok/s at batch 1/8 + int8 GEMM TOPS (% peak); bit-exact vs CPU",
+        "value": round(tps, 2), "unit": "tok/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": round(tps / A100_B8_TOKS, 3) if B == 8 else None,
+        "dtype": "int8", "data": "synthetic (seeded random-init integer artifact and prompts)",
+        "config": {"workload": f"c3: Qwen3-0.6B-shaped integer decode, batch {B}, "
+                               f"{PROMPT_LEN}-token prompt, hipGraph step + greedy pick",
+                   "global_batch": B, "seq_len": PROMPT_LEN, "parallelism": "none (1 GPU)",
+                   "vs_baseline_ref": "A100 batch-8 int8 final 783.3 tok/s"},
+        "batch1": {"value": round(tps1, 2), "unit": "tok/s", "ms_per_step": round(ms1, 4)},
+        "batch_invariant_row0": invariant,
+        "roofline": roof,
+        "cpu_baseline": cpu,
+        **extras,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()
