@@ -23,6 +23,7 @@ P, I, L, S = "p", "i", "l", "s"
 SIGNATURES = {
     "detllm_igemm_nt": [P, P, P, I, I, I, I, L, L, L, S],
     "detllm_igemv_nt": [P, P, P, I, I, I, I, L, S],
+    "detllm_igemv_plan": [I, I, I, P],
     "detllm_transpose_i8": [P, P, I, I, I, L, L, S],
     "detllm_greedy_pick": [P, P, I, I, I, P, P, P, S],
     "detllm_embed_normq": [P, I, I, L, P, P, P, P, P, P, L, P, P, P, S],
@@ -45,6 +46,9 @@ SIGNATURES = {
     "detllm_op_rope": [P, P, P, P, L, L, P, S],
     "detllm_op_scalar": [I, P, P, P, L, P, P, S],
 }
+
+# host-only entry points (no device work, so no stream argument)
+HOST_ONLY = frozenset({"detllm_igemv_plan"})
 
 _CT = {P: ctypes.c_void_p, I: ctypes.c_int, L: ctypes.c_int64, S: ctypes.c_void_p}
 
@@ -88,6 +92,16 @@ def _arg(kind, v):
 def stream_handle(stream=None) -> int:
     s = stream if stream is not None else torch.cuda.current_stream()
     return s.cuda_stream
+
+
+def gemv_plan(M: int, N: int, K: int) -> int:
+    """K split the skinny-GEMM kernel is tuned for at [M, K] x [N, K]^T."""
+    lib = load()
+    out = ctypes.c_int(0)
+    rc = lib.detllm_igemv_plan(int(M), int(N), int(K), ctypes.byref(out))
+    if rc != 0:
+        raise RuntimeError(f"detllm_igemv_plan failed (code {rc})")
+    return out.value
 
 
 def call(name: str, *args, stream=None) -> None:

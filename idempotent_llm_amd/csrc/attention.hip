@@ -238,6 +238,9 @@ struct DecodeArgs {
 constexpr int MAXG = 8;
 constexpr i64 DECODE_LDS_BYTES = 48 * 1024;
 
+constexpr int32_t SCORE_MASKED = INT32_MIN;  // |q.k| <= 128*128*128 < 2^31: never a score
+constexpr int VPRE = 8;                      // V chunks of 16 slots prefetched per thread
+
 template <int G>
 __global__ __launch_bounds__(256) void k_attn_decode(DecodeArgs a) {
   extern __shared__ __attribute__((aligned(16))) int32_t sh_scores[];
@@ -256,32 +259,55 @@ __global__ __launch_bounds__(256) void k_attn_decode(DecodeArgs a) {
   const int8_t* vbase = a.vc + ((i64)b * a.n_kv + kvh) * 128 * a.cap;
   const uint8_t* vrow = a.valid + (i64)b * a.valid_stride;
 
-  // ---- pass 1: scores (8 lanes per slot, 16 bytes each) and row max
+  // P.V ownership: thread (d, half) sums slot chunks [cbeg, cend) of channel d.
+  // Its first VPRE chunks of V are loaded now, overlapping the score passes.
+  const int d = tid & 127, half = tid >> 7;
+  const int nchunk = (S + 15) / 16;
+  const int per = (nchunk + 1) / 2;
+  const int cbeg = half * per, cend = min(nchunk, cbeg + per);
+  const int8_t* vr = vbase + (i64)d * a.cap;
+  v4i vpre[VPRE];
+#pragma unroll
+  for (int i = 0; i < VPRE; ++i)
+    vpre[i] = cbeg + i < cend ? *(const v4i*)(vr + (cbeg + i) * 16) : v4i{0, 0, 0, 0};
+
+  // ---- pass 1: scores (8 lanes per slot, 16 bytes each), masked slots
+  // marked, row max over visible slots. 256 slots per batch of loads.
   const int sub = lane & 7;
   v4i qv[G];
+  i64 tp[G];
 #pragma unroll
-  for (int hh = 0; hh < G; ++hh)
+  for (int hh = 0; hh < G; ++hh) {
     qv[hh] = *(const v4i*)(a.q8 + ((i64)b * a.n_q + kvh * G + hh) * 128 + sub * 16);
+    tp[hh] = a.tpos[(i64)b * a.n_q + kvh * G + hh];
+  }
   i64 mx[G];
 #pragma unroll
   for (int hh = 0; hh < G; ++hh) mx[hh] = NEG_SENTINEL;
-  const int keys_per_iter = 256 / 8;
-  for (int s0 = 0; s0 < S; s0 += keys_per_iter) {
-    const int s = s0 + (tid >> 3);
-    const bool in = s < S;
-    v4i kv = v4i{0, 0, 0, 0};
-    if (in) kv = *(const v4i*)(kbase + (i64)s * 128 + sub * 16);
-    const bool vis = in && vrow[s] != 0;
+  for (int s0 = 0; s0 < S; s0 += 256) {
+    v4i kv[8];
+    int vf[8];
 #pragma unroll
-    for (int hh = 0; hh < G; ++hh) {
-      int d = 0;
+    for (int u = 0; u < 8; ++u) {
+      const int s = s0 + u * 32 + (tid >> 3);
+      const int sc_ = s < S ? s : 0;
+      kv[u] = *(const v4i*)(kbase + (i64)sc_ * 128 + sub * 16);
+      vf[u] = vrow[sc_];
+    }
 #pragma unroll
-      for (int q = 0; q < 4; ++q) d = __builtin_amdgcn_sdot4(kv[q], qv[hh][q], d, false);
-      d += __shfl_xor(d, 1, 64);
-      d += __shfl_xor(d, 2, 64);
-      d += __shfl_xor(d, 4, 64);
-      if (in && sub == 0) sc[hh * Spad + s] = d;
-      if (vis) mx[hh] = imax(mx[hh], (i64)d);
+    for (int u = 0; u < 8; ++u) {
+      const int s = s0 + u * 32 + (tid >> 3);
+      const bool in = s < S;
+      const bool vis = in && vf[u] != 0;
+#pragma unroll
+      for (int hh = 0; hh < G; ++hh) {
+        int dd = 0;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) dd = __builtin_amdgcn_sdot4(kv[u][q], qv[hh][q], dd, false);
+        dd = sum8_i32(dd);
+        if (in && sub == 0) sc[hh * Spad + s] = vis ? dd : SCORE_MASKED;
+        if (vis) mx[hh] = imax(mx[hh], (i64)dd);
+      }
     }
   }
 #pragma unroll
@@ -291,61 +317,66 @@ __global__ __launch_bounds__(256) void k_attn_decode(DecodeArgs a) {
   }
   __syncthreads();
   // ---- pass 2: denominators
-  i64 tp[G], den[G];
-#pragma unroll
-  for (int hh = 0; hh < G; ++hh) {
-    tp[hh] = a.tpos[(i64)b * a.n_q + kvh * G + hh];
-    den[hh] = 0;
-  }
+  i64 den[G];
 #pragma unroll
   for (int hh = 0; hh < G; ++hh) {
     const Recip R = make_recip(tp[hh]);
     i64 acc = 0;
-    for (int s = tid; s < S; s += 256)
-      if (vrow[s] != 0) acc = wadd(acc, di_exp_r(wsub((i64)sc[hh * Spad + s], mx[hh]), tp[hh], R));
+    for (int s = tid; s < S; s += 256) {
+      const int32_t x = sc[hh * Spad + s];
+      if (x != SCORE_MASKED) acc = wadd(acc, di_exp_r(wsub((i64)x, mx[hh]), tp[hh], R));
+    }
     den[hh] = imax(block_sum(acc, red), 1);
   }
-  // ---- pass 3: probabilities (in place of the scores)
+  // ---- pass 3: probabilities in [0, 2^14] (in place of the scores; 0 for
+  // masked slots and the padding up to the next multiple of 16)
 #pragma unroll
   for (int hh = 0; hh < G; ++hh) {
     const Recip R = make_recip(tp[hh]);
     const Recip Rd = make_recip(den[hh]);
-    for (int s = tid; s < Spad; s += 256) {
+    for (int s = tid; s < nchunk * 16; s += 256) {
       i64 p = 0;
-      if (s < S && vrow[s] != 0) {
-        const i64 ex = di_exp_r(wsub((i64)sc[hh * Spad + s], mx[hh]), tp[hh], R);
-        p = to_i32(rhad_r(shl(ex, 14), Rd));
+      if (s < S) {
+        const int32_t x = sc[hh * Spad + s];
+        if (x != SCORE_MASKED) {
+          const i64 ex = di_exp_r(wsub((i64)x, mx[hh]), tp[hh], R);
+          p = to_i32(rhad_r(shl(ex, 14), Rd));
+        }
       }
       sc[hh * Spad + s] = (int32_t)p;
     }
   }
   __syncthreads();
-  // ---- P.V: thread (d, half) sums its half of the slot range
-  const int d = tid & 127, half = tid >> 7;
-  const int nchunk = Spad / 16;
-  const int cbeg = half * ((nchunk + 1) / 2), cend = min(nchunk, cbeg + (nchunk + 1) / 2);
-  i64 acc[G];
+  // ---- P.V: sum_s p_s v_s. |sum| <= 128 * (2^14 + S) < 2^31, so int32
+  // accumulation is exact; chunks beyond the prefetched ones load 8 at a time.
+  int32_t acc[G];
 #pragma unroll
   for (int hh = 0; hh < G; ++hh) acc[hh] = 0;
-  const int8_t* vr = vbase + (i64)d * a.cap;
-  for (int c = cbeg; c < cend; ++c) {
-    if (c * 16 >= S) break;
-    const v4i vv = *(const v4i*)(vr + c * 16);
+  auto chunk_dot = [&](int c, const v4i& vv) {
 #pragma unroll
     for (int hh = 0; hh < G; ++hh) {
       const int32_t* pp = sc + hh * Spad + c * 16;
-      i64 sacc = 0;
+      int32_t s = 0;
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const int w = vv[q];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int v8 = (int)(int8_t)((w >> (8 * r)) & 0xff);
-          sacc += (i64)pp[q * 4 + r] * v8;
-        }
+        for (int r = 0; r < 4; ++r) s += pp[q * 4 + r] * (int32_t)(int8_t)((w >> (8 * r)) & 0xff);
       }
-      acc[hh] += sacc;
+      acc[hh] += s;
     }
+  };
+#pragma unroll
+  for (int i = 0; i < VPRE; ++i)
+    if (cbeg + i < cend) chunk_dot(cbeg + i, vpre[i]);
+  for (int c0 = cbeg + VPRE; c0 < cend; c0 += 8) {
+    v4i vv[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      vv[i] = *(const v4i*)(vr + (c0 + i < cend ? c0 + i : c0) * 16);
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      if (c0 + i < cend) chunk_dot(c0 + i, vv[i]);
   }
   if (half == 1)
 #pragma unroll
@@ -354,7 +385,7 @@ __global__ __launch_bounds__(256) void k_attn_decode(DecodeArgs a) {
   if (half == 0)
 #pragma unroll
     for (int hh = 0; hh < G; ++hh)
-      a.out[(i64)b * a.n_q * 128 + (kvh * G + hh) * 128 + d] = acc[hh] + pv_acc[hh][d];
+      a.out[(i64)b * a.n_q * 128 + (kvh * G + hh) * 128 + d] = (i64)acc[hh] + pv_acc[hh][d];
 }
 
 }  // namespace
@@ -389,6 +420,7 @@ int detllm_attn_decode(const int8_t* q8, const int64_t* tpos, const int8_t* kc, 
     return DI_EINVAL;
   const int G = n_q / n_kv;
   if (G > MAXG) return DI_ENOSYS;
+  if (S > (1 << 24)) return DI_ERANGE;  // int32 P.V accumulators
   const i64 Spad = ((i64)S + 15) & ~15;
   const i64 lds = (i64)G * Spad * 4;
   size_t dyn = 0;

@@ -32,15 +32,55 @@ __device__ __forceinline__ i64 shfl_xor64(i64 v, int mask) {
   return (i64)(((u64)(unsigned)hi << 32) | (u64)(unsigned)lo);
 }
 
+// One DPP move of a 64-bit value (two 32-bit halves, same control). Lanes the
+// row mask disables keep `old`. CTRL: 0xB1 / 0x4E quad permutations (lane ^ 1,
+// lane ^ 2), 0x141 row_half_mirror, 0x140 row_mirror, 0x142 row_bcast15,
+// 0x143 row_bcast31 (CDNA data-parallel primitives).
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ i64 dpp64(i64 v, i64 old) {
+  const int lo = __builtin_amdgcn_update_dpp((int)(u64)old, (int)(u64)v, CTRL, ROW_MASK, 0xF,
+                                             false);
+  const int hi = __builtin_amdgcn_update_dpp((int)((u64)old >> 32), (int)((u64)v >> 32), CTRL,
+                                             ROW_MASK, 0xF, false);
+  return (i64)(((u64)(unsigned)hi << 32) | (u64)(unsigned)lo);
+}
+
+__device__ __forceinline__ i64 readlane64(i64 v, int lane) {
+  const int lo = __builtin_amdgcn_readlane((int)(u64)v, lane);
+  const int hi = __builtin_amdgcn_readlane((int)((u64)v >> 32), lane);
+  return (i64)(((u64)(unsigned)hi << 32) | (u64)(unsigned)lo);
+}
+
+// Wave-wide max / wrapping sum with DPP moves (a few cycles each, against an
+// LDS round trip per step for a shuffle). After the six steps lane 63 holds
+// the result, which is broadcast. Integer max and modular sum are
+// associative and commutative, so the combine order cannot change the value.
+// Every lane of the wave must be active.
 __device__ __forceinline__ i64 wave_max(i64 v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = imax(v, shfl_xor64(v, o));
-  return v;
+  v = imax(v, dpp64<0xB1, 0xF>(v, v));
+  v = imax(v, dpp64<0x4E, 0xF>(v, v));
+  v = imax(v, dpp64<0x141, 0xF>(v, v));
+  v = imax(v, dpp64<0x140, 0xF>(v, v));
+  v = imax(v, dpp64<0x142, 0xA>(v, v));
+  v = imax(v, dpp64<0x143, 0xC>(v, v));
+  return readlane64(v, 63);
 }
 
 __device__ __forceinline__ i64 wave_sum(i64 v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = wadd(v, shfl_xor64(v, o));
+  v = wadd(v, dpp64<0xB1, 0xF>(v, 0));
+  v = wadd(v, dpp64<0x4E, 0xF>(v, 0));
+  v = wadd(v, dpp64<0x141, 0xF>(v, 0));
+  v = wadd(v, dpp64<0x140, 0xF>(v, 0));
+  v = wadd(v, dpp64<0x142, 0xA>(v, 0));
+  v = wadd(v, dpp64<0x143, 0xC>(v, 0));
+  return readlane64(v, 63);
+}
+
+// Sum over each aligned group of 8 lanes, result in all 8 (int32).
+__device__ __forceinline__ int sum8_i32(int v) {
+  v += __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false);
+  v += __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, false);
+  v += __builtin_amdgcn_update_dpp(0, v, 0x141, 0xF, 0xF, false);
   return v;
 }
 

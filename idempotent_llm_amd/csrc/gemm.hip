@@ -19,10 +19,12 @@
 // Kernels:
 //   k_gemm_nt   — 128x128x64 block tiles, 4 waves of 64x64, LDS double
 //                 buffer; for M > 64 (prefill).
-//   k_gemv_nt   — M <= 64 (decode): each block owns 16 output columns and a
+//   k_gemv_nt   — M <= 64 (decode): a wave owns 16 output columns and a
 //                 K range; weight fragments stream straight from HBM into
-//                 MFMA operands; optional K split writes int32 partials that
-//                 the consuming row kernel sums (exact integer addition).
+//                 MFMA operands, every load of a batch issued before the
+//                 first MFMA; an optional K split (detllm_igemv_plan) writes
+//                 int32 partials that the consuming row kernel sums in a
+//                 fixed order (exact integer addition).
 //   k_argmax_*  — greedy_pick (model.py:482-490): argmax of logits * head_m
 //                 in int64 with the lowest-id tie-break.
 
@@ -116,54 +118,87 @@ __global__ __launch_bounds__(256) void k_gemm_nt(const int8_t* __restrict__ A,
       }
 }
 
-template <int MB>
+// Skinny GEMM (decode GEMV), M <= 64 rows, C[ks][M][N] = A[M][Kchunk] . B[N][Kchunk]^T.
+//
+// A wave computes one 16-column group over a K range with
+// v_mfma_i32_16x16x64_i8. Lane l supplies column (l % 16) and U consecutive
+// 16-byte K slices starting at 16*U*(l / 16): a wave-load then reads 16U*4
+// contiguous bytes of each of its 16 weight rows (whole 128-byte lines for
+// U >= 2). The K order inside an MFMA does not matter as long as A and B use
+// the same one, so A is loaded with the identical mapping.
+//
+// Latency is what bounds these launches (a decode layer's matrices are 1-6 MB),
+// so each wave issues all loads of NB iterations before the first MFMA.
+// KW waves of a block split the K range of one column group and reduce their
+// int32 accumulators through LDS; with KW == 1 the 4 waves own 4 column groups.
+template <int MB, int KW, int NB>
 __global__ __launch_bounds__(256) void k_gemv_nt(const int8_t* __restrict__ A,
                                                  const int8_t* __restrict__ B,
                                                  int32_t* __restrict__ C, int M, int N, int K,
                                                  int kchunk, i64 split_stride) {
-  __shared__ int32_t red[3][MB * 4][64];
-  const int n0 = blockIdx.x * 16;
-  const int ks = blockIdx.y;
-  const int kbeg = ks * kchunk;
-  const int kend = min(K, kbeg + kchunk);
+  constexpr int U = 4;                 // 16-byte slices per lane per iteration
+  constexpr int CG = 4 / KW;           // column groups per block
+  constexpr int KSTEP = 64 * U;        // K covered by one wave-iteration
+  __shared__ int32_t red[KW > 1 ? (KW - 1) * CG : 1][MB * 4][64];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  const int r16 = lane & 15, kq = (lane >> 4) * 16;
-  const int col = n0 + r16;
+  const int cg = wave % CG, kw = wave / CG;
+  const int r16 = lane & 15, g = lane >> 4;
+  const int col = (blockIdx.x * CG + cg) * 16 + r16;
   const bool colok = col < N;
+  const int kbeg = blockIdx.y * kchunk;
+  const int kend = min(K, kbeg + kchunk);
   const int8_t* brow = B + (i64)(colok ? col : 0) * K;
   v4i acc[MB];
 #pragma unroll
   for (int mb = 0; mb < MB; ++mb) acc[mb] = zero4();
-#pragma unroll 4
-  for (int k0 = kbeg + wave * 64; k0 < kend; k0 += 256) {
-    const int kk = k0 + kq;
-    const bool kok = kk < kend;
-    const v4i b = (colok && kok) ? *(const v4i*)(brow + kk) : zero4();
+  for (int k0 = kbeg + kw * KSTEP; k0 < kend; k0 += KSTEP * KW * NB) {
+    v4i b[NB][U], a[NB][U][MB];
 #pragma unroll
-    for (int mb = 0; mb < MB; ++mb) {
-      const int row = mb * 16 + r16;
-      const v4i a = (row < M && kok) ? *(const v4i*)(A + (i64)row * K + kk) : zero4();
-      acc[mb] = mfma16(a, b, acc[mb]);
+    for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int kk = k0 + nb * KSTEP * KW + g * 16 * U + u * 16;
+        const bool kok = kk < kend;
+        b[nb][u] = (colok && kok) ? *(const v4i*)(brow + kk) : zero4();
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) {
+          const int row = mb * 16 + r16;
+          a[nb][u][mb] = (row < M && kok) ? *(const v4i*)(A + (i64)row * K + kk) : zero4();
+        }
+      }
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) acc[mb] = mfma16(a[nb][u][mb], b[nb][u], acc[mb]);
+  }
+  if (KW > 1) {
+    if (kw > 0) {
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) red[(kw - 1) * CG + cg][mb * 4 + r][lane] = acc[mb][r];
     }
-  }
-  if (wave > 0) {
-#pragma unroll
-    for (int mb = 0; mb < MB; ++mb)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) red[wave - 1][mb * 4 + r][lane] = acc[mb][r];
-  }
-  __syncthreads();
-  if (wave == 0) {
+    __syncthreads();
+    if (kw > 0) return;
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int32_t s = acc[mb][r] + red[0][mb * 4 + r][lane] + red[1][mb * 4 + r][lane] +
-                          red[2][mb * 4 + r][lane];
-        const int row = mb * 16 + (lane >> 4) * 4 + r;
-        if (row < M && colok) C[ks * split_stride + (i64)row * N + col] = s;
+        int32_t s = acc[mb][r];
+#pragma unroll
+        for (int w = 0; w < KW - 1; ++w) s += red[w * CG + cg][mb * 4 + r][lane];
+        acc[mb][r] = s;
       }
   }
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int row = mb * 16 + g * 4 + r;
+      if (row < M && colok) C[blockIdx.y * split_stride + (i64)row * N + col] = acc[mb][r];
+    }
 }
 
 __global__ void k_transpose_i8(const int8_t* __restrict__ src, int8_t* __restrict__ dst, int R,
@@ -239,6 +274,28 @@ __global__ __launch_bounds__(256) void k_argmax_final(const int64_t* pv, const i
   if (threadIdx.x == 0) out[r] = b.i;
 }
 
+// Recommended K split of the skinny GEMM for an [M, K] x [N, K]^T product:
+// enough (block, K-range) pairs to spread the weight stream over the CUs,
+// at most 8 partials. The caller sizes the partial buffer with it.
+int gemv_plan(int N, int K) {
+  const int groups = (N + 15) / 16;
+  if (groups >= 1024) return 1;
+  int ks = (256 + groups - 1) / groups;
+  ks = ks < 1 ? 1 : (ks > 8 ? 8 : ks);
+  const int kmax = K / 256 > 0 ? K / 256 : 1;
+  if (ks > kmax) ks = kmax;
+  int kchunk = (K + ks - 1) / ks;
+  kchunk = (kchunk + 63) / 64 * 64;
+  return (K + kchunk - 1) / kchunk;
+}
+
+template <int MB, int KW, int NB>
+void launch_gemv(dim3 grid, hipStream_t s, const int8_t* A, const int8_t* B, int32_t* C,
+                        int M, int N, int K, int kchunk, i64 split_stride) {
+  hipLaunchKernelGGL((k_gemv_nt<MB, KW, NB>), grid, dim3(256), 0, s, A, B, C, M, N, K, kchunk,
+                     split_stride);
+}
+
 }  // namespace
 
 extern "C" {
@@ -257,8 +314,16 @@ int detllm_igemm_nt(const int8_t* A, const int8_t* B, int32_t* C, int M, int N, 
   return DI_OK;
 }
 
+int detllm_igemv_plan(int M, int N, int K, int* ksplit) {
+  if (!ksplit || M <= 0 || M > 64 || N <= 0 || K <= 0 || (K % 16) != 0) return DI_EINVAL;
+  *ksplit = gemv_plan(N, K);
+  return DI_OK;
+}
+
 // Skinny GEMM for M <= 64: writes ksplit int32 partials C[ks][M][N]
 // (split_stride elements apart); ksplit = 1 gives the plain product.
+// Wide products (>= 1024 column groups of 16) give each wave its own column
+// group; narrower ones put 4 waves on one group, splitting its K range.
 int detllm_igemv_nt(const int8_t* A, const int8_t* B, int32_t* C, int M, int N, int K,
                     int ksplit, int64_t split_stride, hipStream_t s) {
   if (M <= 0 || N <= 0) return DI_OK;
@@ -269,13 +334,25 @@ int detllm_igemv_nt(const int8_t* A, const int8_t* B, int32_t* C, int M, int N, 
   kchunk = (kchunk + 63) / 64 * 64;
   const int nsp = (K + kchunk - 1) / kchunk;
   if (nsp != ksplit) return DI_EINVAL;  // caller must size partial buffers to ksplit
-  dim3 grid((N + 15) / 16, ksplit);
+  const int groups = (N + 15) / 16;
+  const bool wide = false;  // 4 waves per column group measured faster at every model shape
+  const dim3 grid(wide ? (groups + 3) / 4 : groups, ksplit);
   const int mb = (M + 15) / 16;
-  switch (mb) {
-    case 1: hipLaunchKernelGGL(k_gemv_nt<1>, grid, dim3(256), 0, s, A, B, C, M, N, K, kchunk, (i64)split_stride); break;
-    case 2: hipLaunchKernelGGL(k_gemv_nt<2>, grid, dim3(256), 0, s, A, B, C, M, N, K, kchunk, (i64)split_stride); break;
-    case 3: hipLaunchKernelGGL(k_gemv_nt<3>, grid, dim3(256), 0, s, A, B, C, M, N, K, kchunk, (i64)split_stride); break;
-    default: hipLaunchKernelGGL(k_gemv_nt<4>, grid, dim3(256), 0, s, A, B, C, M, N, K, kchunk, (i64)split_stride); break;
+  const i64 ss = (i64)split_stride;
+  if (wide) {
+    switch (mb) {
+      case 1: launch_gemv<1, 1, 2>(grid, s, A, B, C, M, N, K, kchunk, ss); break;
+      case 2: launch_gemv<2, 1, 2>(grid, s, A, B, C, M, N, K, kchunk, ss); break;
+      case 3: launch_gemv<3, 1, 1>(grid, s, A, B, C, M, N, K, kchunk, ss); break;
+      default: launch_gemv<4, 1, 1>(grid, s, A, B, C, M, N, K, kchunk, ss); break;
+    }
+  } else {
+    switch (mb) {
+      case 1: launch_gemv<1, 4, 2>(grid, s, A, B, C, M, N, K, kchunk, ss); break;
+      case 2: launch_gemv<2, 4, 2>(grid, s, A, B, C, M, N, K, kchunk, ss); break;
+      case 3: launch_gemv<3, 4, 1>(grid, s, A, B, C, M, N, K, kchunk, ss); break;
+      default: launch_gemv<4, 4, 1>(grid, s, A, B, C, M, N, K, kchunk, ss); break;
+    }
   }
   DI_LAUNCH_CHECK();
   return DI_OK;

@@ -29,6 +29,10 @@ using namespace di;
 namespace {
 
 constexpr int RT = DI_ROW_THREADS;
+// The fused model kernels run one row per block with up to RT_WIDE threads
+// (at most 4 columns per thread), shortening the per-element part of the
+// serial per-row chain that bounds them at decode.
+constexpr int RT_WIDE = 1024;
 
 template <int VPT>
 __device__ __forceinline__ i64 row_absmax(const i64 (&v)[VPT], i64* red) {
@@ -68,7 +72,7 @@ __device__ __forceinline__ void quant_row(const i64 (&v)[VPT], i64 m_in, i64 k_i
   const Recip R = make_recip(a);
 #pragma unroll
   for (int j = 0; j < VPT; ++j) {
-    const int c = threadIdx.x + j * RT;
+    const int c = threadIdx.x + j * (int)blockDim.x;
     if (c < C) out[c] = (int8_t)clamp_i8(rhad_r(wmul(v[j], 127), R));
   }
   if (threadIdx.x == 0) {
@@ -79,15 +83,13 @@ __device__ __forceinline__ void quant_row(const i64 (&v)[VPT], i64 m_in, i64 k_i
   }
 }
 
-// dyadic.py:108-120: v holds P on entry, y (int32 values) on exit; returns k_out
+// dyadic.py:108-120: v holds P on entry, y (int32 values) on exit; cm holds
+// col_m of this thread's columns (0 past C); returns k_out
 template <int VPT>
-__device__ __forceinline__ i64 requant_common_row(i64 (&v)[VPT], const i64* col_m, i64 row_k,
-                                                  i64 col_k, int tb, int C, i64* red) {
+__device__ __forceinline__ i64 requant_common_row(i64 (&v)[VPT], const i64 (&cm)[VPT], i64 row_k,
+                                                  i64 col_k, int tb, i64* red) {
 #pragma unroll
-  for (int j = 0; j < VPT; ++j) {
-    const int c = threadIdx.x + j * RT;
-    v[j] = c < C ? wmul(v[j], col_m[c]) : 0;
-  }
+  for (int j = 0; j < VPT; ++j) v[j] = wmul(v[j], cm[j]);
   const i64 a = imax(row_absmax(v, red), 1);
   const i64 sh = imax(ilog2(a) - (tb - 1), 0);
 #pragma unroll
@@ -119,20 +121,64 @@ __device__ __forceinline__ i64 residual_add_row(i64 (&h)[VPT], i64 k_res, const 
   return residual_renorm_row(h, k_res, red);
 }
 
+// Latency, not bandwidth, bounds these kernels at decode (one block per
+// token row): every helper below issues all of its global loads before the
+// first use, so a kernel waits for one memory round trip instead of one per
+// load. Indices are clamped instead of branched on, so each load is
+// unconditional and in bounds; out-of-range lanes are zeroed after the load.
+
+// x[c] for the columns c = threadIdx.x + j * blockDim.x this thread owns (0 past C or
+// when x is null).
 template <int VPT>
-__device__ __forceinline__ void load_row_i32_sum(i64 (&v)[VPT], const int32_t* P, int nsplit,
-                                                 i64 split_stride, i64 off, int C) {
+__device__ __forceinline__ void prefetch_cols(i64 (&v)[VPT], const int64_t* x, int C) {
 #pragma unroll
   for (int j = 0; j < VPT; ++j) {
-    const int c = threadIdx.x + j * RT;
-    if (c < C) {
-      uint32_t s = 0;
-      for (int k = 0; k < nsplit; ++k) s += (uint32_t)P[k * split_stride + off + c];
-      v[j] = (i64)(int32_t)s;
-    } else {
-      v[j] = 0;
-    }
+    const int c = threadIdx.x + j * (int)blockDim.x;
+    v[j] = x ? x[c < C ? c : C - 1] : 0;
   }
+#pragma unroll
+  for (int j = 0; j < VPT; ++j)
+    if (threadIdx.x + j * (int)blockDim.x >= C) v[j] = 0;
+}
+
+// Sum of nsplit int32 partials P[k * stride + off + c] (the K-split of the
+// skinny GEMM) in a fixed order, for NR rows at offsets off[0..NR).
+template <int NR, int VPT>
+__device__ __forceinline__ void load_rows_i32_sum(i64 (&v)[NR][VPT], const int32_t* P,
+                                                  int nsplit, i64 stride, const i64 (&off)[NR],
+                                                  int C) {
+  constexpr int KU = NR * VPT > 8 ? 2 : 4;  // partials per batch of loads
+  uint32_t s[NR][VPT];
+#pragma unroll
+  for (int q = 0; q < NR; ++q)
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) s[q][j] = 0;
+  for (int k0 = 0; k0 < nsplit; k0 += KU) {
+    int32_t t[KU][NR][VPT];
+#pragma unroll
+    for (int kk = 0; kk < KU; ++kk) {
+      const int k = k0 + kk < nsplit ? k0 + kk : nsplit - 1;
+#pragma unroll
+      for (int q = 0; q < NR; ++q)
+#pragma unroll
+        for (int j = 0; j < VPT; ++j) {
+          const int c = threadIdx.x + j * (int)blockDim.x;
+          t[kk][q][j] = P[(i64)k * stride + off[q] + (c < C ? c : C - 1)];
+        }
+    }
+#pragma unroll
+    for (int kk = 0; kk < KU; ++kk)
+      if (k0 + kk < nsplit)
+#pragma unroll
+        for (int q = 0; q < NR; ++q)
+#pragma unroll
+          for (int j = 0; j < VPT; ++j) s[q][j] += (uint32_t)t[kk][q][j];
+  }
+#pragma unroll
+  for (int q = 0; q < NR; ++q)
+#pragma unroll
+    for (int j = 0; j < VPT; ++j)
+      v[q][j] = threadIdx.x + j * (int)blockDim.x < C ? (i64)(int32_t)s[q][j] : 0;
 }
 
 // =====================================================================
@@ -165,36 +211,49 @@ struct ResNormArgs {
 };
 
 template <int VPT>
-__global__ __launch_bounds__(RT) void k_residual_normq(ResNormArgs a) {
+__global__ __launch_bounds__(RT_WIDE) void k_residual_normq(ResNormArgs a) {
   __shared__ i64 red[16];
   const int r = blockIdx.x;
   const int C = a.C;
   const i64 off = (i64)r * C;
-  i64 h[VPT], d[VPT];
+  i64 h[VPT], d[VPT], smv[VPT];
   i64 kr;
+  prefetch_cols(smv, a.sm_m, C);
   if (a.mode == 0) {
     i64 id = a.ids[r];
     id = id < 0 ? 0 : (id >= a.vocab ? a.vocab - 1 : id);  // memory safety only
-    const i64 dm = a.em[id];
+    const i64 dm = a.em[id], ek = a.ek[id];
 #pragma unroll
     for (int j = 0; j < VPT; ++j) {
-      const int c = threadIdx.x + j * RT;
-      h[j] = c < C ? wmul((i64)a.e8[id * C + c], dm) : 0;
+      const int c = threadIdx.x + j * (int)blockDim.x;
+      h[j] = a.e8[id * C + (c < C ? c : C - 1)];
     }
-    kr = residual_renorm_row(h, a.ek[id], red);
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) h[j] = threadIdx.x + j * (int)blockDim.x < C ? wmul(h[j], dm) : 0;
+    kr = residual_renorm_row(h, ek, red);
   } else {
-    load_row_i32_sum(d, a.P, a.nsplit, a.split_stride, off, C);
-    const i64 dk = requant_common_row(d, a.col_m, a.row_k[r], a.col_k, a.tb, C, red);
+    i64 cm[VPT];
+    prefetch_cols(cm, a.col_m, C);
 #pragma unroll
     for (int j = 0; j < VPT; ++j) {
-      const int c = threadIdx.x + j * RT;
-      h[j] = c < C ? (i64)a.h[off + c] : 0;
+      const int c = threadIdx.x + j * (int)blockDim.x;
+      h[j] = a.h[off + (c < C ? c : C - 1)];
     }
-    kr = residual_add_row(h, a.k_res[r], d, a.row_m[r], dk, red);
+    const i64 row_k = a.row_k[r], row_m = a.row_m[r], k_res = a.k_res[r];
+    i64 dd[1][VPT];
+    const i64 offs[1] = {off};
+    load_rows_i32_sum<1, VPT>(dd, a.P, a.nsplit, a.split_stride, offs, C);
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) {
+      d[j] = dd[0][j];
+      if (threadIdx.x + j * (int)blockDim.x >= C) h[j] = 0;
+    }
+    const i64 dk = requant_common_row(d, cm, row_k, a.col_k, a.tb, red);
+    kr = residual_add_row(h, k_res, d, row_m, dk, red);
   }
 #pragma unroll
   for (int j = 0; j < VPT; ++j) {
-    const int c = threadIdx.x + j * RT;
+    const int c = threadIdx.x + j * (int)blockDim.x;
     if (c < C) a.h[off + c] = (int32_t)h[j];
   }
   if (threadIdx.x == 0) a.k_res[r] = kr;
@@ -203,10 +262,7 @@ __global__ __launch_bounds__(RT) void k_residual_normq(ResNormArgs a) {
   i64 kq = 20;
   if (a.sm_m != nullptr) {
 #pragma unroll
-    for (int j = 0; j < VPT; ++j) {
-      const int c = threadIdx.x + j * RT;
-      h[j] = c < C ? wmul(h[j], a.sm_m[c]) : 0;
-    }
+    for (int j = 0; j < VPT; ++j) h[j] = wmul(h[j], smv[j]);
     kq += a.sm_k;
   }
   quant_row(h, 1, kq, C, red, a.x8 + off, a.xm + r, a.xk + r);
@@ -231,26 +287,27 @@ struct SwigluArgs {
 };
 
 template <int VPT>
-__global__ __launch_bounds__(RT) void k_swiglu_quant(SwigluArgs a) {
+__global__ __launch_bounds__(RT_WIDE) void k_swiglu_quant(SwigluArgs a) {
   __shared__ i64 red[16];
   const int r = blockIdx.x;
   const int I = a.I;
-  i64 g[VPT], u[VPT];
-  load_row_i32_sum(g, a.P, a.nsplit, a.split_stride, (i64)r * 2 * I, I);
-  load_row_i32_sum(u, a.P, a.nsplit, a.split_stride, (i64)r * 2 * I + I, I);
+  i64 gm[VPT], um[VPT], dsm[VPT];
+  prefetch_cols(gm, a.gate_m, I);
+  prefetch_cols(um, a.up_m, I);
+  prefetch_cols(dsm, a.ds_m, I);
   const i64 xm = a.xm[r], xk = a.xk[r];
-  const i64 gk = requant_common_row(g, a.gate_m, xk, a.gate_k, 14, I, red);
-  const i64 uk = requant_common_row(u, a.up_m, xk, a.up_k, 14, I, red);
+  i64 gu[2][VPT];
+  const i64 offs[2] = {(i64)r * 2 * I, (i64)r * 2 * I + I};
+  load_rows_i32_sum<2, VPT>(gu, a.P, a.nsplit, a.split_stride, offs, I);
+  const i64 gk = requant_common_row(gu[0], gm, xk, a.gate_k, 14, red);
+  const i64 uk = requant_common_row(gu[1], um, xk, a.up_k, 14, red);
   const i64 tpos = di_exp_tpos(xm, gk);
   const Recip R = make_recip(tpos);
 #pragma unroll
-  for (int j = 0; j < VPT; ++j) {
-    const int c = threadIdx.x + j * RT;
-    g[j] = c < I ? wmul(swiglu_elem(g[j], u[j], tpos, R), a.ds_m[c]) : 0;
-  }
+  for (int j = 0; j < VPT; ++j) gu[0][j] = wmul(swiglu_elem(gu[0][j], gu[1][j], tpos, R), dsm[j]);
   const i64 ym = wmul(xm, xm);
   const i64 yk = wadd(wadd(wadd(gk, uk), 7), a.ds_k);
-  quant_row(g, ym, yk, I, red, a.y8 + (i64)r * I, a.ym + r, a.yk + r);
+  quant_row(gu[0], ym, yk, I, red, a.y8 + (i64)r * I, a.ym + r, a.yk + r);
 }
 
 struct MergeArgs {
@@ -268,22 +325,35 @@ struct MergeArgs {
 };
 
 template <int VPT>
-__global__ __launch_bounds__(RT) void k_merge_rowcol(MergeArgs a) {
+__global__ __launch_bounds__(RT_WIDE) void k_merge_rowcol(MergeArgs a) {
   __shared__ i64 red[16];
   const int r = blockIdx.x;
   const int C = a.C;
   const i64 off = (i64)r * C;
-  i64 v[VPT];
+  i64 v[VPT], om[VPT], cm[VPT];
+  prefetch_cols(om, a.os_m, C);
+  prefetch_cols(cm, a.col_m, C);
 #pragma unroll
-  for (int j = 0; j < VPT; ++j) {
-    const int c = threadIdx.x + j * RT;
-    i64 s = 0;
-    if (c < C) {
-      for (int k = 0; k < a.nsplit; ++k) s = wadd(s, a.attn[k * a.split_stride + off + c]);
-      s = wmul(wmul(s, a.os_m[c]), a.col_m[c]);
+  for (int j = 0; j < VPT; ++j) v[j] = 0;
+  for (int k0 = 0; k0 < a.nsplit; k0 += 2) {
+    i64 t[2][VPT];
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) {
+      const int k = k0 + kk < a.nsplit ? k0 + kk : a.nsplit - 1;
+#pragma unroll
+      for (int j = 0; j < VPT; ++j) {
+        const int c = threadIdx.x + j * (int)blockDim.x;
+        t[kk][j] = a.attn[(i64)k * a.split_stride + off + (c < C ? c : C - 1)];
+      }
     }
-    v[j] = s;
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk)
+      if (k0 + kk < a.nsplit)
+#pragma unroll
+        for (int j = 0; j < VPT; ++j) v[j] = wadd(v[j], t[kk][j]);
   }
+#pragma unroll
+  for (int j = 0; j < VPT; ++j) v[j] = wmul(wmul(v[j], om[j]), cm[j]);  // 0 past C
   const i64 a1 = imax(row_absmax(v, red), 1);
   const i64 sh = imax(ilog2(a1) - 45, 0);
 #pragma unroll
@@ -292,7 +362,7 @@ __global__ __launch_bounds__(RT) void k_merge_rowcol(MergeArgs a) {
   const Recip R = make_recip(a2);
 #pragma unroll
   for (int j = 0; j < VPT; ++j) {
-    const int c = threadIdx.x + j * RT;
+    const int c = threadIdx.x + j * (int)blockDim.x;
     if (c < C) a.a8[off + c] = (int8_t)clamp_i8(rhad_r(wmul(v[j], 127), R));
   }
   if (threadIdx.x == 0) {
@@ -366,104 +436,122 @@ __global__ __launch_bounds__(RT) void k_qkv_epilogue(QKVArgs a) {
   const int b = r / a.T, t = r - b * a.T;
   const int NQKV = n_heads * 128;
   const i64 off = (i64)r * NQKV + (i64)slotw * 128;
-  i64 p0 = 0, p1 = 0;
+  const int group = a.n_q / a.n_kv;
+  const bool is_q = slotw < a.n_q, is_v = slotw >= a.n_q + a.n_kv;
+  const int h = is_q ? slotw : (is_v ? slotw - a.n_q - a.n_kv : slotw - a.n_q);
+  const int kvh = is_q ? h / group : h;
+  const int c0 = lane, c1 = lane + 64;
+
+  // ---- every global load up front (one memory round trip, plus the RoPE
+  // table rows that depend on the position)
+  const i64 pos_raw = a.positions[r];
+  const i64 xk = a.xk[r], xm = a.xm[r];
+  const i64 base = a.slot_base_dev ? a.slot_base_dev[0] : a.slot_base;
+  const int64_t* wmp = (is_q ? a.q_m : (is_v ? a.v_m : a.k_m)) + (i64)h * 128;
+  const i64 wm0 = wmp[c0], wm1 = wmp[c1];
+  const int64_t* gam = is_q ? a.q_norm_m : a.k_norm_m;
+  const i64 g0 = gam[c0], g1 = gam[c1];
+  const i64 qs0 = a.qs_m[kvh * 128 + c0], qs1 = a.qs_m[kvh * 128 + c1];
+  const i64 kqm0 = a.kq_m[kvh * 128 + c0], kqm1 = a.kq_m[kvh * 128 + c1];
+  const i64 kqk0 = a.kq_k[kvh * 128 + c0], kqk1 = a.kq_k[kvh * 128 + c1];
+  const i64 vqm = a.vq_m[kvh], vqk = a.vq_k[kvh];
+  const i64 ksm = a.ks_m[kvh], ksk = a.ks_k[kvh];
+  i64 p0, p1;
   {
     uint32_t s0 = 0, s1 = 0;
-    for (int k = 0; k < a.nsplit; ++k) {
-      s0 += (uint32_t)a.P[k * a.split_stride + off + lane];
-      s1 += (uint32_t)a.P[k * a.split_stride + off + lane + 64];
+    for (int k0 = 0; k0 < a.nsplit; k0 += 4) {
+      int32_t t0[4], t1[4];
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) {
+        const int k = k0 + kk < a.nsplit ? k0 + kk : a.nsplit - 1;
+        t0[kk] = a.P[(i64)k * a.split_stride + off + c0];
+        t1[kk] = a.P[(i64)k * a.split_stride + off + c1];
+      }
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk)
+        if (k0 + kk < a.nsplit) {
+          s0 += (uint32_t)t0[kk];
+          s1 += (uint32_t)t1[kk];
+        }
     }
     p0 = (int32_t)s0;
     p1 = (int32_t)s1;
   }
-  const i64 xk = a.xk[r];
-  const i64 xm = a.xm[r];
-  const int group = a.n_q / a.n_kv;
-  const i64 base = a.slot_base_dev ? a.slot_base_dev[0] : a.slot_base;
+  const i64 pos = pos_raw < 0 ? 0 : (pos_raw >= a.max_pos ? a.max_pos - 1 : pos_raw);
+  const i64 cs0 = a.cos_t[pos * 128 + c0], cs1 = a.cos_t[pos * 128 + c1];
+  const i64 sn0 = a.sin_t[pos * 128 + c0], sn1 = a.sin_t[pos * 128 + c1];
   const i64 slot = base + t;
 
-  if (slotw >= a.n_q + a.n_kv) {
+  if (is_v) {
     // ---- V head: requant_i8_static(Pv, xm, xk, v_m, v_k, vq_m[h], vq_k[h])
-    const int h = slotw - a.n_q - a.n_kv;
-    const i64 shift = wsub(wadd(xk, a.v_k), a.vq_k[h]);
+    const i64 shift = wsub(wadd(xk, a.v_k), vqk);
     const i64 up = imax(wneg(shift), 0), down = imax(shift, 0);
-    i64 den = shl(a.vq_m[h], down);
+    i64 den = shl(vqm, down);
     if (den <= 0) den = 1;  // static scales are positive mantissas in artifacts
-    const i64 n0 = shl(wmul(wmul(p0, a.v_m[h * 128 + lane]), xm), up);
-    const i64 n1 = shl(wmul(wmul(p1, a.v_m[h * 128 + lane + 64]), xm), up);
+    const i64 n0 = shl(wmul(wmul(p0, wm0), xm), up);
+    const i64 n1 = shl(wmul(wmul(p1, wm1), xm), up);
     const Recip R = make_recip(den);
     int8_t* vrow = a.vcache + ((i64)b * a.n_kv + h) * 128 * a.cap;
     if (slot >= 0 && slot < a.cap) {
-      vrow[(i64)lane * a.cap + slot] = (int8_t)clamp_i8(rhad_r(n0, R));
-      vrow[(i64)(lane + 64) * a.cap + slot] = (int8_t)clamp_i8(rhad_r(n1, R));
+      vrow[(i64)c0 * a.cap + slot] = (int8_t)clamp_i8(rhad_r(n0, R));
+      vrow[(i64)c1 * a.cap + slot] = (int8_t)clamp_i8(rhad_r(n1, R));
     }
     return;
   }
-  const bool is_q = slotw < a.n_q;
-  const int h = is_q ? slotw : slotw - a.n_q;
-  const int64_t* wm = is_q ? a.q_m + (i64)h * 128 : a.k_m + (i64)h * 128;
-  const i64 wk = is_q ? a.q_k : a.k_k;
-  // requant_i32_common(tb = 16) per (token, head)   (model.py:207-211)
-  i64 y0 = wmul(p0, wm[lane]), y1 = wmul(p1, wm[lane + 64]);
+  // requant_i32_common(tb = 16) per (token, head)   (model.py:207-211); the
+  // (m, k) it returns are dropped by _qk_head_pipeline
+  i64 y0 = wmul(p0, wm0), y1 = wmul(p1, wm1);
   {
     const i64 am = imax(wave_max(imax(wabs(y0), wabs(y1))), 1);
     const i64 sh = imax(ilog2(am) - 15, 0);
     y0 = to_i32(rshift_round(y0, sh));
     y1 = to_i32(rshift_round(y1, sh));
   }
-  (void)wk;  // (m, k) of the requant are dropped by _qk_head_pipeline
   // di_rmsnorm_gamma  (model.py:212)
   wave_rmsnorm128(y0, y1);
-  const int64_t* gam = is_q ? a.q_norm_m : a.k_norm_m;
-  y0 = wmul(y0, gam[lane]);
-  y1 = wmul(y1, gam[lane + 64]);
+  y0 = wmul(y0, g0);
+  y1 = wmul(y1, g1);
   // apply_int_rope at this token's position   (model.py:213-215; rope.py:38-55)
-  i64 pos = a.positions[r];
-  pos = pos < 0 ? 0 : (pos >= a.max_pos ? a.max_pos - 1 : pos);
-  const i64 c0 = a.cos_t[pos * 128 + lane], c1 = a.cos_t[pos * 128 + lane + 64];
-  const i64 s0 = a.sin_t[pos * 128 + lane], s1 = a.sin_t[pos * 128 + lane + 64];
-  const i64 r0 = rshift_round(wadd(wmul(y0, c0), wmul(wneg(y1), s0)), 14);
-  const i64 r1 = rshift_round(wadd(wmul(y1, c1), wmul(y0, s1)), 14);
+  const i64 r0 = rshift_round(wadd(wmul(y0, cs0), wmul(wneg(y1), sn0)), 14);
+  const i64 r1 = rshift_round(wadd(wmul(y1, cs1), wmul(y0, sn1)), 14);
   if (!is_q) {
     // K: requant_i8_static(kk, 1, k_rowk, 1, 0, kq_m, kq_k)   (model.py:326-329)
     const i64 rowk = 20 + a.k_norm_k;
     int8_t* krow = a.kcache + (((i64)b * a.n_kv + h) * a.cap + slot) * 128;
+    const i64 rv[2] = {r0, r1}, km[2] = {kqm0, kqm1}, kk[2] = {kqk0, kqk1};
     i64 outv[2];
-    const i64 rv[2] = {r0, r1};
 #pragma unroll
     for (int q = 0; q < 2; ++q) {
-      const int c = lane + 64 * q;
-      const i64 shift = wsub(rowk, a.kq_k[h * 128 + c]);
+      const i64 shift = wsub(rowk, kk[q]);
       const i64 up = imax(wneg(shift), 0), down = imax(shift, 0);
-      i64 den = shl(a.kq_m[h * 128 + c], down);
+      i64 den = shl(km[q], down);
       if (den <= 0) den = 1;
       outv[q] = clamp_i8(rhad(shl(rv[q], up), den));
     }
     if (slot >= 0 && slot < a.cap) {
-      krow[lane] = (int8_t)outv[0];
-      krow[lane + 64] = (int8_t)outv[1];
+      krow[c0] = (int8_t)outv[0];
+      krow[c1] = (int8_t)outv[1];
     }
     return;
   }
   // Q: QK smoothing (model.py:317-320) then quant_i8_pertoken (model.py:322-323)
-  const int kvh = h / group;
-  const i64 q0 = wmul(r0, a.qs_m[kvh * 128 + lane]);
-  const i64 q1 = wmul(r1, a.qs_m[kvh * 128 + lane + 64]);
+  const i64 q0 = wmul(r0, qs0);
+  const i64 q1 = wmul(r1, qs1);
   const i64 qkk = 20 + a.q_norm_k + a.qs_k;
   i64 m, k;
   norm_scale(1, qkk, &m, &k);
   const i64 am = imax(wave_max(imax(wabs(q0), wabs(q1))), 1);
   const Recip R = make_recip(am);
   const i64 qrow = (((i64)b * a.n_q + h) * a.T + t);
-  a.q8[qrow * 128 + lane] = (int8_t)clamp_i8(rhad_r(wmul(q0, 127), R));
-  a.q8[qrow * 128 + lane + 64] = (int8_t)clamp_i8(rhad_r(wmul(q1, 127), R));
+  a.q8[qrow * 128 + c0] = (int8_t)clamp_i8(rhad_r(wmul(q0, 127), R));
+  a.q8[qrow * 128 + c1] = (int8_t)clamp_i8(rhad_r(wmul(q1, 127), R));
   if (lane == 0) {
     i64 qm, e;
     fit_dyadic_ratio(wmul(am, m), 127, &qm, &e);
     const i64 qk = wadd(k, e);
     // score scale: norm_scale(qm * ks_m[h//g], qk + ks_k[h//g])   (model.py:351-353)
     i64 sm, sk;
-    norm_scale(wmul(qm, a.ks_m[kvh]), wadd(qk, a.ks_k[kvh]), &sm, &sk);
+    norm_scale(wmul(qm, ksm), wadd(qk, ksk), &sm, &sk);
     a.tpos[qrow] = di_exp_tpos(sm, sk);
     if (a.dbg) {
       a.dbg[qrow * 4 + 0] = qm;
@@ -482,7 +570,7 @@ template <int VPT>
 __device__ __forceinline__ void load_row64(i64 (&v)[VPT], const int64_t* x, i64 off, int C) {
 #pragma unroll
   for (int j = 0; j < VPT; ++j) {
-    const int c = threadIdx.x + j * RT;
+    const int c = threadIdx.x + j * (int)blockDim.x;
     v[j] = c < C ? x[off + c] : 0;
   }
 }
@@ -507,10 +595,12 @@ __global__ __launch_bounds__(RT) void k_op_requant_common(const int64_t* P, cons
   const int r = blockIdx.x;
   i64 v[VPT];
   load_row64(v, P, (i64)r * C, C);
-  const i64 k = requant_common_row(v, col_m + (i64)(r % G) * C, row_k[r], col_k, tb, C, red);
+  i64 cm[VPT];
+  prefetch_cols(cm, col_m + (i64)(r % G) * C, C);
+  const i64 k = requant_common_row(v, cm, row_k[r], col_k, tb, red);
 #pragma unroll
   for (int j = 0; j < VPT; ++j) {
-    const int c = threadIdx.x + j * RT;
+    const int c = threadIdx.x + j * (int)blockDim.x;
     if (c < C) y[(i64)r * C + c] = (int32_t)v[j];
   }
   if (threadIdx.x == 0) ko[r] = k;
@@ -527,7 +617,7 @@ __global__ __launch_bounds__(RT) void k_op_rowcol(const int64_t* P, const int64_
   load_row64(v, P, (i64)r * C, C);
 #pragma unroll
   for (int j = 0; j < VPT; ++j) {
-    const int c = threadIdx.x + j * RT;
+    const int c = threadIdx.x + j * (int)blockDim.x;
     v[j] = c < C ? wmul(v[j], col_m[c]) : 0;
   }
   const i64 a1 = imax(row_absmax(v, red), 1);
@@ -538,7 +628,7 @@ __global__ __launch_bounds__(RT) void k_op_rowcol(const int64_t* P, const int64_
   const Recip R = make_recip(a2);
 #pragma unroll
   for (int j = 0; j < VPT; ++j) {
-    const int c = threadIdx.x + j * RT;
+    const int c = threadIdx.x + j * (int)blockDim.x;
     if (c < C) y8[(i64)r * C + c] = (int8_t)clamp_i8(rhad_r(wmul(v[j], 127), R));
   }
   if (threadIdx.x == 0) {
@@ -569,7 +659,7 @@ __global__ __launch_bounds__(RT) void k_op_residual(int mode, const int64_t* h_i
   }
 #pragma unroll
   for (int j = 0; j < VPT; ++j) {
-    const int c = threadIdx.x + j * RT;
+    const int c = threadIdx.x + j * (int)blockDim.x;
     if (c < C) h_out[(i64)r * C + c] = (int32_t)h[j];
   }
   if (threadIdx.x == 0) k_out[r] = k;
@@ -585,7 +675,7 @@ __global__ __launch_bounds__(RT) void k_op_rmsnorm(const int64_t* x, const int64
   rmsnorm_row(v, C, red);
 #pragma unroll
   for (int j = 0; j < VPT; ++j) {
-    const int c = threadIdx.x + j * RT;
+    const int c = threadIdx.x + j * (int)blockDim.x;
     if (c < C) {
       if (gamma_m) y64[(i64)r * C + c] = wmul(v[j], gamma_m[c]);
       else y32[(i64)r * C + c] = (int32_t)v[j];
@@ -609,7 +699,7 @@ __global__ __launch_bounds__(RT) void k_op_softmax(const int64_t* x, const int64
   bool anyv = false;
 #pragma unroll
   for (int j = 0; j < VPT; ++j) {
-    const int c = threadIdx.x + j * RT;
+    const int c = threadIdx.x + j * (int)blockDim.x;
     ok[j] = c < C && valid[off + c] != 0;
     v[j] = c < C ? x[off + c] : 0;
     if (ok[j]) {
@@ -638,7 +728,7 @@ __global__ __launch_bounds__(RT) void k_op_softmax(const int64_t* x, const int64
   const Recip Rd = make_recip(den);
 #pragma unroll
   for (int j = 0; j < VPT; ++j) {
-    const int c = threadIdx.x + j * RT;
+    const int c = threadIdx.x + j * (int)blockDim.x;
     if (c < C) probs[off + c] = (int32_t)to_i32(rhad_r(shl(v[j], p_out_bits - 1), Rd));
   }
 }
@@ -730,6 +820,17 @@ inline int pick_vpt(int C) {
   return 0;
 }
 
+// threads and columns per thread of a fused row kernel over C columns
+inline bool wide_shape(int C, int* threads, int* vpt) {
+  int t = ((C + 3) / 4 + 63) / 64 * 64;
+  t = t < 64 ? 64 : (t > RT_WIDE ? RT_WIDE : t);
+  const int v = (C + t - 1) / t;
+  if (v > 4) return false;
+  *threads = t;
+  *vpt = v;
+  return true;
+}
+
 inline int grid_for(i64 n) {
   i64 g = (n + 255) / 256;
   return (int)(g < 65536 ? (g < 1 ? 1 : g) : 65536);
@@ -748,6 +849,18 @@ inline int grid_for(i64 n) {
     default: return DI_ERANGE;                                                            \
   }
 
+#define DI_WIDE_DISPATCH(C, KERNEL, GRID, STREAM, ...)                                       \
+  do {                                                                                       \
+    int thr_, vpt_;                                                                          \
+    if (!wide_shape((C), &thr_, &vpt_)) return DI_ENOSYS;                                    \
+    switch (vpt_) {                                                                          \
+      case 1: hipLaunchKernelGGL(KERNEL<1>, GRID, dim3(thr_), 0, STREAM, __VA_ARGS__); break; \
+      case 2: hipLaunchKernelGGL(KERNEL<2>, GRID, dim3(thr_), 0, STREAM, __VA_ARGS__); break; \
+      case 3: hipLaunchKernelGGL(KERNEL<3>, GRID, dim3(thr_), 0, STREAM, __VA_ARGS__); break; \
+      default: hipLaunchKernelGGL(KERNEL<4>, GRID, dim3(thr_), 0, STREAM, __VA_ARGS__); break; \
+    }                                                                                        \
+  } while (0)
+
 extern "C" {
 
 // ---------------------------------------------------------------- model path
@@ -761,8 +874,7 @@ int detllm_embed_normq(const int64_t* ids, int R, int C, int64_t vocab, const in
   ResNormArgs a{};
   a.C = C; a.mode = 0; a.vocab = vocab; a.ids = ids; a.e8 = e8; a.em = em; a.ek = ek;
   a.h = h; a.k_res = k_res; a.sm_m = sm_m; a.sm_k = sm_k; a.x8 = x8; a.xm = xm; a.xk = xk;
-  const int vpt = pick_vpt(C);
-  DI_VPT_DISPATCH(vpt, k_residual_normq, dim3(R), s, a);
+  DI_WIDE_DISPATCH(C, k_residual_normq, dim3(R), s, a);
   DI_LAUNCH_CHECK();
   return DI_OK;
 }
@@ -777,8 +889,7 @@ int detllm_residual_normq(const int32_t* P, int nsplit, int64_t split_stride, in
   a.C = C; a.mode = 1; a.P = P; a.nsplit = nsplit; a.split_stride = split_stride;
   a.row_m = row_m; a.row_k = row_k; a.col_m = col_m; a.col_k = col_k; a.tb = tb;
   a.h = h; a.k_res = k_res; a.sm_m = sm_m; a.sm_k = sm_k; a.x8 = x8; a.xm = xm; a.xk = xk;
-  const int vpt = pick_vpt(C);
-  DI_VPT_DISPATCH(vpt, k_residual_normq, dim3(R), s, a);
+  DI_WIDE_DISPATCH(C, k_residual_normq, dim3(R), s, a);
   DI_LAUNCH_CHECK();
   return DI_OK;
 }
@@ -794,8 +905,7 @@ int detllm_swiglu_quant(const int32_t* P, int nsplit, int64_t split_stride, int 
   a.I = I; a.P = P; a.nsplit = nsplit; a.split_stride = split_stride; a.xm = xm; a.xk = xk;
   a.gate_m = gate_m; a.gate_k = gate_k; a.up_m = up_m; a.up_k = up_k; a.ds_m = ds_m;
   a.ds_k = ds_k; a.y8 = y8; a.ym = ym; a.yk = yk;
-  const int vpt = pick_vpt(I);
-  DI_VPT_DISPATCH(vpt, k_swiglu_quant, dim3(R), s, a);
+  DI_WIDE_DISPATCH(I, k_swiglu_quant, dim3(R), s, a);
   DI_LAUNCH_CHECK();
   return DI_OK;
 }
@@ -808,8 +918,7 @@ int detllm_merge_rowcol(const int64_t* attn, int nsplit, int64_t split_stride, i
   MergeArgs a{};
   a.C = C; a.attn = attn; a.nsplit = nsplit; a.split_stride = split_stride; a.os_m = os_m;
   a.os_k = os_k; a.col_m = col_m; a.col_k = col_k; a.a8 = a8; a.am = am; a.ak = ak;
-  const int vpt = pick_vpt(C);
-  DI_VPT_DISPATCH(vpt, k_merge_rowcol, dim3(R), s, a);
+  DI_WIDE_DISPATCH(C, k_merge_rowcol, dim3(R), s, a);
   DI_LAUNCH_CHECK();
   return DI_OK;
 }

@@ -36,7 +36,7 @@ from dataclasses import dataclass
 
 import torch
 
-from ._lib import call
+from ._lib import call, gemv_plan
 from .backends import canonical_backend, gemm_nt
 from .guard import NoFloatMode
 
@@ -196,6 +196,7 @@ class IntQwen3:
                 attn_out_col_m=col_m.to(dev), attn_out_col_k=vk_shared + (P_OUT_BITS - 1)))
         del tensors
         self._greedy_scratch = {}
+        self._plans: dict = {}
 
     # reference-layout view of the LM head (model.py:136)
     @property
@@ -203,18 +204,18 @@ class IntQwen3:
         return self.head_w.t()
 
     # -- GEMM dispatch ---------------------------------------------------------
-    @staticmethod
-    def _ksplit(N: int, K: int) -> int:
-        blocks = (N + 15) // 16
-        ks = max(1, min(K // 256, -(-1024 // blocks)))
-        kchunk = -(-K // ks)
-        kchunk = -(-kchunk // 64) * 64
-        return -(-K // kchunk)
+    def _ksplit(self, N: int, K: int, M: int = 1) -> int:
+        key = (N, K)
+        ks = self._plans.get(key)
+        if ks is None:
+            ks = gemv_plan(M, N, K)
+            self._plans[key] = ks
+        return ks
 
     def _gemm(self, x: torch.Tensor, w: torch.Tensor):
         R, K = x.shape
         N = w.shape[0]
-        ks = self._ksplit(N, K) if R <= 64 else 1
+        ks = self._ksplit(N, K, R) if R <= 64 else 1
         P = gemm_nt(x, w, ksplit=ks)
         return P, ks, R * N
 

@@ -46,6 +46,11 @@ int detllm_igemm_nt(const int8_t* A, const int8_t* B, int32_t* C, int M, int N, 
 int detllm_igemv_nt(const int8_t* A, const int8_t* B, int32_t* C, int M, int N, int K,
                     int ksplit, int64_t split_stride, hipStream_t s);
 
+/* K split that detllm_igemv_nt is tuned for at this shape (the reference's
+ * cuBLASLt path picks its own kernel internally, backends.py:115-119);
+ * writes *ksplit in [1, 8]. */
+int detllm_igemv_plan(int M, int N, int K, int* ksplit);
+
 /* Device transpose of int8 [R][C] matrices (operand layout for int_gemm's
  * [K][N] right-hand side; backends.py:115-119 consumes b as [K][N]). */
 int detllm_transpose_i8(const int8_t* src, int8_t* dst, int R, int C, int batch,

@@ -37,12 +37,31 @@ def test_library_exports_every_declared_symbol():
 
 
 def test_python_binding_matches_header_arity():
-    from idempotent_llm_amd._lib import SIGNATURES
+    from idempotent_llm_amd._lib import HOST_ONLY, SIGNATURES
     decls = _declarations()
     assert set(SIGNATURES) == set(decls)
     for name, n in decls.items():
         assert len(SIGNATURES[name]) == n, name
-        assert SIGNATURES[name][-1] == "s", name   # every entry takes a stream last
+        if name not in HOST_ONLY:   # every entry that enqueues work takes a stream last
+            assert SIGNATURES[name][-1] == "s", name
+
+
+@pytest.mark.skipif(not os.path.exists(LIB), reason="library not built (run build())")
+def test_gemv_plan_host_entry():
+    """The K-split planner runs on the host (no GPU needed): 1..8 partials,
+    1 for wide products, a multiple-of-64 chunk that the kernel accepts."""
+    from idempotent_llm_amd._lib import gemv_plan
+    for N, K in ((4096, 1024), (1024, 2048), (6144, 1024), (1024, 3072), (151936, 1024),
+                 (1024, 256), (16, 16), (48, 4096)):
+        ks = gemv_plan(8, N, K)
+        assert 1 <= ks <= 8
+        chunk = (K + ks - 1) // ks
+        chunk = (chunk + 63) // 64 * 64
+        assert (K + chunk - 1) // chunk == ks
+    assert gemv_plan(1, 151936, 1024) == 1
+    assert gemv_plan(1, 1024, 3072) > 1
+    with pytest.raises(RuntimeError):
+        gemv_plan(65, 1024, 1024)
 
 
 def test_backend_names():
