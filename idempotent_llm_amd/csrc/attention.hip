@@ -244,7 +244,8 @@ constexpr int VPRE = 8;                      // V chunks of 16 slots prefetched 
 template <int G>
 __global__ __launch_bounds__(256) void k_attn_decode(DecodeArgs a) {
   extern __shared__ __attribute__((aligned(16))) int32_t sh_scores[];
-  __shared__ i64 red[16];
+  __shared__ i64 red_buf[32];
+  BlockRed red{red_buf, 0};
   __shared__ i64 pv_acc[G][128];
   const int kvh = blockIdx.x, b = blockIdx.y;
   const int tid = threadIdx.x, lane = tid & 63;
@@ -312,7 +313,7 @@ __global__ __launch_bounds__(256) void k_attn_decode(DecodeArgs a) {
   }
 #pragma unroll
   for (int hh = 0; hh < G; ++hh) {
-    mx[hh] = block_max(mx[hh], red);
+    mx[hh] = red.max(mx[hh]);
     if (mx[hh] == NEG_SENTINEL) mx[hh] = 0;
   }
   __syncthreads();
@@ -326,7 +327,7 @@ __global__ __launch_bounds__(256) void k_attn_decode(DecodeArgs a) {
       const int32_t x = sc[hh * Spad + s];
       if (x != SCORE_MASKED) acc = wadd(acc, di_exp_r(wsub((i64)x, mx[hh]), tp[hh], R));
     }
-    den[hh] = imax(block_sum(acc, red), 1);
+    den[hh] = imax(red.sum(acc), 1);
   }
   // ---- pass 3: probabilities in [0, 2^14] (in place of the scores; 0 for
   // masked slots and the padding up to the next multiple of 16)

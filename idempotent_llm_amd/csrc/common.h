@@ -94,31 +94,80 @@ __device__ __forceinline__ i64 group4_sum(i64 v) {
   return wadd(v, shfl_xor64(v, 32));
 }
 
-// Block-wide reductions (blockDim.x a multiple of 64, <= 1024). `red` is a
-// __shared__ i64[16]; the leading barrier makes back-to-back calls safe.
-__device__ __forceinline__ i64 block_max(i64 v, i64* red) {
-  v = wave_max(v);
-  const int w = threadIdx.x >> 6;
-  __syncthreads();
-  if ((threadIdx.x & 63) == 0) red[w] = v;
-  __syncthreads();
-  i64 r = red[0];
-  const int nw = blockDim.x >> 6;
-  for (int i = 1; i < nw; ++i) r = imax(r, red[i]);
-  return r;
+// floor(sqrt(n)) for a wave-uniform n: the same integer as isqrt (intops.h,
+// int_prims.py:31-44; 0 for n <= 0), found by a 64-way search instead of 32
+// serial bit steps. Invariant: the root lies in [lo, lo + 64 * sub); lane l
+// tests lo + l * sub, and the highest passing lane (the test is monotone)
+// becomes the new lo. sub = 2^26, 2^20, 2^14, 2^8, 2^2, 1 covers [0, 2^32),
+// which holds every root of a non-negative int64; candidates stay below 2^32,
+// so their squares fit in uint64. Every lane of the wave must be active.
+__device__ __forceinline__ i64 isqrt_wave(i64 n) {
+  if (n <= 0) return 0;
+  const u64 un = (u64)n;
+  const u64 lane = threadIdx.x & 63;
+  u64 lo = 0;
+#pragma unroll
+  for (int sh = 26; sh >= -4; sh -= 6) {
+    const int s = sh < 0 ? 0 : sh;
+    const u64 cand = lo + (lane << s);
+    const bool ok = cand * cand <= un;
+    const u64 mask = __ballot(ok);
+    lo += (u64)(63 - clz64(mask)) << s;
+  }
+  return (i64)lo;
 }
 
-__device__ __forceinline__ i64 block_sum(i64 v, i64* red) {
-  v = wave_sum(v);
-  const int w = threadIdx.x >> 6;
-  __syncthreads();
-  if ((threadIdx.x & 63) == 0) red[w] = v;
-  __syncthreads();
-  i64 r = red[0];
-  const int nw = blockDim.x >> 6;
-  for (int i = 1; i < nw; ++i) r = wadd(r, red[i]);
-  return r;
-}
+// Block-wide reductions (blockDim.x a multiple of 64, <= 1024), one barrier
+// each: every wave's lane 63 publishes its DPP partial, and calls alternate
+// between two 16-entry slots of `buf`, so a call never overwrites a slot that
+// a slower thread may still be reading (the call in between has a barrier
+// that every thread passes only after its reads). Max and wrapping sum are
+// associative and commutative: any combine order gives the same integer.
+struct BlockRed {
+  i64* buf;  // __shared__ i64[32]
+  int k;
+
+  template <bool MAX>
+  __device__ __forceinline__ i64 reduce(i64 v) {
+    v = wave_part<MAX>(v);
+    i64* slot = buf + (k & 1) * 16;
+    ++k;
+    if ((threadIdx.x & 63) == 63) slot[threadIdx.x >> 6] = v;
+    __syncthreads();
+    const int nw = blockDim.x >> 6;
+    i64 r = MAX ? INT64_MIN : 0;
+    for (int i = 0; i < nw; i += 4) {
+      const i64 a0 = slot[i], a1 = slot[i + 1], a2 = slot[i + 2], a3 = slot[i + 3];
+      const i64 id = MAX ? INT64_MIN : 0;
+      const i64 b1 = i + 1 < nw ? a1 : id, b2 = i + 2 < nw ? a2 : id, b3 = i + 3 < nw ? a3 : id;
+      r = MAX ? imax(imax(r, a0), imax(imax(b1, b2), b3)) : wadd(wadd(r, a0), wadd(wadd(b1, b2), b3));
+    }
+    return r;
+  }
+  __device__ __forceinline__ i64 max(i64 v) { return reduce<true>(v); }
+  __device__ __forceinline__ i64 sum(i64 v) { return reduce<false>(v); }
+
+  // DPP reduction leaving the wave's result in lane 63 (no broadcast)
+  template <bool MAX>
+  static __device__ __forceinline__ i64 wave_part(i64 v) {
+    if (MAX) {
+      v = imax(v, dpp64<0xB1, 0xF>(v, v));
+      v = imax(v, dpp64<0x4E, 0xF>(v, v));
+      v = imax(v, dpp64<0x141, 0xF>(v, v));
+      v = imax(v, dpp64<0x140, 0xF>(v, v));
+      v = imax(v, dpp64<0x142, 0xA>(v, v));
+      v = imax(v, dpp64<0x143, 0xC>(v, v));
+    } else {
+      v = wadd(v, dpp64<0xB1, 0xF>(v, 0));
+      v = wadd(v, dpp64<0x4E, 0xF>(v, 0));
+      v = wadd(v, dpp64<0x141, 0xF>(v, 0));
+      v = wadd(v, dpp64<0x140, 0xF>(v, 0));
+      v = wadd(v, dpp64<0x142, 0xA>(v, 0));
+      v = wadd(v, dpp64<0x143, 0xC>(v, 0));
+    }
+    return v;
+  }
+};
 
 __device__ __forceinline__ i64 to_i32(i64 v) { return (i64)(int32_t)(uint32_t)(u64)v; }
 

@@ -137,6 +137,16 @@ DI_HD i64 rhad_r(i64 a, const Recip& R) {
   return a < 0 ? wneg(q) : q;
 }
 
+// rhad(a, 2^k) for k >= 0: the same integer as rhad(a, 1 << k) above (floor
+// division by a positive power of two is an arithmetic shift, including the
+// wrapped |INT64_MIN| case).
+DI_HD i64 rhad_pow2(i64 a, int k) {
+  if (k == 0) return a;
+  const i64 mag = wabs(a);
+  const i64 q = shr(wadd(mag, (i64)1 << (k - 1)), k);
+  return a < 0 ? wneg(q) : q;
+}
+
 // ---- dyadic helpers (src/detllm/dyadic.py) -----------------------------
 
 // dyadic.py:45-49
@@ -166,6 +176,45 @@ DI_HD void fit_dyadic_ratio(i64 num, i64 den, i64* m_out, i64* e_out) {
   i64 adj = (m >= 65536 ? -1 : 0) + (m < 32768 ? 1 : 0);
   e += adj;
   if (adj != 0) m = scaled_round_div(num, den, e);
+  if (m >= 65536) {
+    m = rshift_round(m, 1);
+    e -= 1;
+  }
+  *m_out = m;
+  *e_out = e;
+}
+
+// fit_dyadic_ratio(num, 127): every requantisation to int8 fits its output
+// scale against 127. Same integer as the generic routine; the divisions by
+// 127 * 2^s use the constant reciprocal floor((2^64 - 1) / 127) whenever no
+// operand of the generic path wraps (num < 2^56, shifts below 56), else the
+// generic path runs.
+DI_HD i64 srd127(i64 num, i64 e) {
+  // scaled_round_div(num, 127, e) for 0 < num < 2^56, |e| < 56 and no wrap of
+  // num << e: rhad(x, 127 * 2^s) = floor(floor((x + h) / 2^s) / 127) with
+  // h = floor(127 * 2^s / 2).
+  const Recip R127{127ull, 0x0204081020408102ull};
+  if (e >= 0) {
+    const u64 x = (u64)num << e;
+    return (i64)udiv(x + 63, R127);
+  }
+  const int s = (int)(-e);
+  const u64 h = (127ull << s) >> 1;
+  return (i64)udiv(((u64)num + h) >> s, R127);
+}
+
+DI_HD void fit_dyadic_ratio_127(i64 num, i64* m_out, i64* e_out) {
+  const i64 lg = ilog2(num);
+  if (num <= 0 || lg >= 56) {
+    fit_dyadic_ratio(num, 127, m_out, e_out);
+    return;
+  }
+  // e = 15 - (lg - 6) in [-34, 21]; num << e < 2^(lg + e + 1) <= 2^22: no wrap
+  i64 e = 21 - lg;
+  i64 m = srd127(num, e);
+  const i64 adj = (m >= 65536 ? -1 : 0) + (m < 32768 ? 1 : 0);
+  e += adj;
+  if (adj != 0) m = srd127(num, e);
   if (m >= 65536) {
     m = rshift_round(m, 1);
     e -= 1;

@@ -38,6 +38,8 @@ void di_host_scalar(int op, const int64_t* a, const int64_t* b, const int64_t* c
       case 1: o1[i] = ilog2(a[i]); break;
       case 2: norm_scale(a[i], b[i], &x, &y); o1[i] = x; o2[i] = y; break;
       case 3: fit_dyadic_ratio(a[i], b[i], &x, &y); o1[i] = x; o2[i] = y; break;
+      case 5: fit_dyadic_ratio_127(a[i], &x, &y); o1[i] = x; o2[i] = y; break;
+      case 6: o1[i] = rhad_pow2(a[i], (int)b[i]); break;
       default: o1[i] = scaled_round_div(a[i], b[i], c[i]); break;
     }
   }

@@ -35,16 +35,16 @@ constexpr int RT = DI_ROW_THREADS;
 constexpr int RT_WIDE = 1024;
 
 template <int VPT>
-__device__ __forceinline__ i64 row_absmax(const i64 (&v)[VPT], i64* red) {
+__device__ __forceinline__ i64 row_absmax(const i64 (&v)[VPT], BlockRed& red) {
   i64 g = 0;
 #pragma unroll
   for (int j = 0; j < VPT; ++j) g = imax(g, wabs(v[j]));
-  return block_max(g, red);
+  return red.max(g);
 }
 
 // ops/di_rmsnorm.py:33-52: v (<= C valid columns, 0 elsewhere) -> y (int32 values)
 template <int VPT>
-__device__ __forceinline__ void rmsnorm_row(i64 (&v)[VPT], int C, i64* red) {
+__device__ __forceinline__ void rmsnorm_row(i64 (&v)[VPT], int C, BlockRed& red) {
   const i64 g = row_absmax(v, red);
   const i64 sh = 25 - ilog2(imax(g, 1));
   const i64 up = imax(sh, 0), down = imax(-sh, 0);
@@ -55,9 +55,9 @@ __device__ __forceinline__ void rmsnorm_row(i64 (&v)[VPT], int C, i64* red) {
     v[j] = xp;
     ss = wadd(ss, wmul(xp, xp));
   }
-  ss = block_sum(ss, red);
-  const i64 mean = rhad(ss, (i64)C);
-  const Recip R = make_recip(imax(isqrt(mean), 1));
+  ss = red.sum(ss);
+  const i64 mean = (C & (C - 1)) == 0 ? rhad_pow2(ss, (int)ilog2(C)) : rhad(ss, (i64)C);
+  const Recip R = make_recip(imax(isqrt_wave(mean), 1));
 #pragma unroll
   for (int j = 0; j < VPT; ++j) v[j] = to_i32(rhad_r(shl(v[j], 20), R));
 }
@@ -65,7 +65,7 @@ __device__ __forceinline__ void rmsnorm_row(i64 (&v)[VPT], int C, i64* red) {
 // dyadic.py:93-105
 template <int VPT>
 __device__ __forceinline__ void quant_row(const i64 (&v)[VPT], i64 m_in, i64 k_in, int C,
-                                          i64* red, int8_t* out, i64* m_out, i64* k_out) {
+                                          BlockRed& red, int8_t* out, i64* m_out, i64* k_out) {
   i64 m, k;
   norm_scale(m_in, k_in, &m, &k);
   const i64 a = imax(row_absmax(v, red), 1);
@@ -77,7 +77,7 @@ __device__ __forceinline__ void quant_row(const i64 (&v)[VPT], i64 m_in, i64 k_i
   }
   if (threadIdx.x == 0) {
     i64 mo, e;
-    fit_dyadic_ratio(wmul(a, m), 127, &mo, &e);
+    fit_dyadic_ratio_127(wmul(a, m), &mo, &e);
     *m_out = mo;
     *k_out = wadd(k, e);
   }
@@ -87,7 +87,7 @@ __device__ __forceinline__ void quant_row(const i64 (&v)[VPT], i64 m_in, i64 k_i
 // col_m of this thread's columns (0 past C); returns k_out
 template <int VPT>
 __device__ __forceinline__ i64 requant_common_row(i64 (&v)[VPT], const i64 (&cm)[VPT], i64 row_k,
-                                                  i64 col_k, int tb, i64* red) {
+                                                  i64 col_k, int tb, BlockRed& red) {
 #pragma unroll
   for (int j = 0; j < VPT; ++j) v[j] = wmul(v[j], cm[j]);
   const i64 a = imax(row_absmax(v, red), 1);
@@ -99,7 +99,7 @@ __device__ __forceinline__ i64 requant_common_row(i64 (&v)[VPT], const i64 (&cm)
 
 // dyadic.py:174-184
 template <int VPT>
-__device__ __forceinline__ i64 residual_renorm_row(i64 (&h)[VPT], i64 k_res, i64* red) {
+__device__ __forceinline__ i64 residual_renorm_row(i64 (&h)[VPT], i64 k_res, BlockRed& red) {
   const i64 g = row_absmax(h, red);
   const i64 lg = ilog2(imax(g, 1));
   const i64 sh_down = imax(lg - 29, 0);
@@ -113,7 +113,7 @@ __device__ __forceinline__ i64 residual_renorm_row(i64 (&h)[VPT], i64 k_res, i64
 // dyadic.py:193-206
 template <int VPT>
 __device__ __forceinline__ i64 residual_add_row(i64 (&h)[VPT], i64 k_res, const i64 (&d)[VPT],
-                                                i64 dm, i64 dk, i64* red) {
+                                                i64 dm, i64 dk, BlockRed& red) {
   const i64 rel = wsub(dk, k_res);
   const i64 down = imax(rel, 0), up = imax(wneg(rel), 0);
 #pragma unroll
@@ -212,7 +212,8 @@ struct ResNormArgs {
 
 template <int VPT>
 __global__ __launch_bounds__(RT_WIDE) void k_residual_normq(ResNormArgs a) {
-  __shared__ i64 red[16];
+  __shared__ i64 red_buf[32];
+  BlockRed red{red_buf, 0};
   const int r = blockIdx.x;
   const int C = a.C;
   const i64 off = (i64)r * C;
@@ -288,7 +289,8 @@ struct SwigluArgs {
 
 template <int VPT>
 __global__ __launch_bounds__(RT_WIDE) void k_swiglu_quant(SwigluArgs a) {
-  __shared__ i64 red[16];
+  __shared__ i64 red_buf[32];
+  BlockRed red{red_buf, 0};
   const int r = blockIdx.x;
   const int I = a.I;
   i64 gm[VPT], um[VPT], dsm[VPT];
@@ -326,7 +328,8 @@ struct MergeArgs {
 
 template <int VPT>
 __global__ __launch_bounds__(RT_WIDE) void k_merge_rowcol(MergeArgs a) {
-  __shared__ i64 red[16];
+  __shared__ i64 red_buf[32];
+  BlockRed red{red_buf, 0};
   const int r = blockIdx.x;
   const int C = a.C;
   const i64 off = (i64)r * C;
@@ -367,7 +370,7 @@ __global__ __launch_bounds__(RT_WIDE) void k_merge_rowcol(MergeArgs a) {
   }
   if (threadIdx.x == 0) {
     i64 mo, e;
-    fit_dyadic_ratio(a2, 127, &mo, &e);
+    fit_dyadic_ratio_127(a2, &mo, &e);
     a.am[r] = mo;
     a.ak[r] = wsub(wadd(wadd(a.os_k, a.col_k), e), sh);
   }
@@ -422,7 +425,7 @@ __device__ __forceinline__ void wave_rmsnorm128(i64& a, i64& b) {
   a = shl(rshift_round(a, down), up);
   b = shl(rshift_round(b, down), up);
   const i64 ss = wave_sum(wadd(wmul(a, a), wmul(b, b)));
-  const Recip R = make_recip(imax(isqrt(rhad(ss, 128)), 1));
+  const Recip R = make_recip(imax(isqrt_wave(rhad_pow2(ss, 7)), 1));
   a = to_i32(rhad_r(shl(a, 20), R));
   b = to_i32(rhad_r(shl(b, 20), R));
 }
@@ -547,7 +550,7 @@ __global__ __launch_bounds__(RT) void k_qkv_epilogue(QKVArgs a) {
   a.q8[qrow * 128 + c1] = (int8_t)clamp_i8(rhad_r(wmul(q1, 127), R));
   if (lane == 0) {
     i64 qm, e;
-    fit_dyadic_ratio(wmul(am, m), 127, &qm, &e);
+    fit_dyadic_ratio_127(wmul(am, m), &qm, &e);
     const i64 qk = wadd(k, e);
     // score scale: norm_scale(qm * ks_m[h//g], qk + ks_k[h//g])   (model.py:351-353)
     i64 sm, sk;
@@ -579,7 +582,8 @@ template <int VPT>
 __global__ __launch_bounds__(RT) void k_op_quant(const int64_t* x, const int64_t* m,
                                                  const int64_t* k, int C, int8_t* x8,
                                                  int64_t* mo, int64_t* ko) {
-  __shared__ i64 red[16];
+  __shared__ i64 red_buf[32];
+  BlockRed red{red_buf, 0};
   const int r = blockIdx.x;
   i64 v[VPT];
   load_row64(v, x, (i64)r * C, C);
@@ -591,7 +595,8 @@ __global__ __launch_bounds__(RT) void k_op_requant_common(const int64_t* P, cons
                                                           const int64_t* col_m, int G, i64 col_k,
                                                           int tb, int C, int32_t* y,
                                                           int64_t* ko) {
-  __shared__ i64 red[16];
+  __shared__ i64 red_buf[32];
+  BlockRed red{red_buf, 0};
   const int r = blockIdx.x;
   i64 v[VPT];
   load_row64(v, P, (i64)r * C, C);
@@ -611,7 +616,8 @@ __global__ __launch_bounds__(RT) void k_op_rowcol(const int64_t* P, const int64_
                                                   const int64_t* row_k, const int64_t* col_m,
                                                   i64 col_k, int C, int8_t* y8, int64_t* mo,
                                                   int64_t* ko) {
-  __shared__ i64 red[16];
+  __shared__ i64 red_buf[32];
+  BlockRed red{red_buf, 0};
   const int r = blockIdx.x;
   i64 v[VPT];
   load_row64(v, P, (i64)r * C, C);
@@ -633,7 +639,7 @@ __global__ __launch_bounds__(RT) void k_op_rowcol(const int64_t* P, const int64_
   }
   if (threadIdx.x == 0) {
     i64 m, e;
-    fit_dyadic_ratio(wmul(a2, row_m[r]), 127, &m, &e);
+    fit_dyadic_ratio_127(wmul(a2, row_m[r]), &m, &e);
     mo[r] = m;
     ko[r] = wsub(wadd(wadd(row_k[r], col_k), e), sh);
   }
@@ -645,7 +651,8 @@ __global__ __launch_bounds__(RT) void k_op_residual(int mode, const int64_t* h_i
                                                     const int64_t* k_res, const int64_t* d,
                                                     const int64_t* dm, const int64_t* dk, int C,
                                                     int32_t* h_out, int64_t* k_out) {
-  __shared__ i64 red[16];
+  __shared__ i64 red_buf[32];
+  BlockRed red{red_buf, 0};
   const int r = blockIdx.x;
   i64 h[VPT];
   load_row64(h, h_in, (i64)r * C, C);
@@ -668,7 +675,8 @@ __global__ __launch_bounds__(RT) void k_op_residual(int mode, const int64_t* h_i
 template <int VPT>
 __global__ __launch_bounds__(RT) void k_op_rmsnorm(const int64_t* x, const int64_t* gamma_m,
                                                    int C, int32_t* y32, int64_t* y64) {
-  __shared__ i64 red[16];
+  __shared__ i64 red_buf[32];
+  BlockRed red{red_buf, 0};
   const int r = blockIdx.x;
   i64 v[VPT];
   load_row64(v, x, (i64)r * C, C);
@@ -689,7 +697,8 @@ __global__ __launch_bounds__(RT) void k_op_softmax(const int64_t* x, const int64
                                                    int has_clip, i64 clip_c, int p_out_bits,
                                                    int C, int32_t* probs) {
   // ops/di_softmax.py:33-61
-  __shared__ i64 red[16];
+  __shared__ i64 red_buf[32];
+  BlockRed red{red_buf, 0};
   const int r = blockIdx.x;
   const i64 off = (i64)r * C;
   const i64 NEG = INT64_MIN + 1;
@@ -707,8 +716,8 @@ __global__ __launch_bounds__(RT) void k_op_softmax(const int64_t* x, const int64
       anyv = true;
     }
   }
-  mx = block_max(mx, red);
-  const i64 any = block_max(anyv ? 1 : 0, red);
+  mx = red.max(mx);
+  const i64 any = red.max(anyv ? 1 : 0);
   if (!any) mx = 0;
   const i64 mm = m[r], kk = k[r];
   const i64 tpos = di_exp_tpos(mm, kk);
@@ -724,7 +733,7 @@ __global__ __launch_bounds__(RT) void k_op_softmax(const int64_t* x, const int64
     v[j] = e;
     den = wadd(den, e);
   }
-  den = imax(block_sum(den, red), 1);
+  den = imax(red.sum(den), 1);
   const Recip Rd = make_recip(den);
 #pragma unroll
   for (int j = 0; j < VPT; ++j) {
@@ -793,7 +802,9 @@ __global__ void k_op_static(const int64_t* P, const int64_t* row_m, const int64_
   }
 }
 
-// op: 0 isqrt, 1 ilog2, 2 norm_scale, 3 fit_dyadic_ratio, 4 scaled_round_div
+// op: 0 isqrt, 1 ilog2, 2 norm_scale, 3 fit_dyadic_ratio, 4 scaled_round_div,
+// 5 fit_dyadic_ratio(a, 127) through the constant-127 path the kernels use
+// (6, the wave-parallel isqrt, runs in k_op_isqrt_wave)
 __global__ void k_op_scalar(int op, const int64_t* a, const int64_t* b, const int64_t* c, i64 n,
                             int64_t* o1, int64_t* o2) {
   for (i64 i = blockIdx.x * (i64)blockDim.x + threadIdx.x; i < n;
@@ -804,8 +815,29 @@ __global__ void k_op_scalar(int op, const int64_t* a, const int64_t* b, const in
       case 1: o1[i] = ilog2(a[i]); break;
       case 2: norm_scale(a[i], b[i], &x, &y); o1[i] = x; o2[i] = y; break;
       case 3: fit_dyadic_ratio(a[i], b[i], &x, &y); o1[i] = x; o2[i] = y; break;
+      case 5: fit_dyadic_ratio_127(a[i], &x, &y); o1[i] = x; o2[i] = y; break;
       default: o1[i] = scaled_round_div(a[i], b[i], c[i]); break;
     }
+  }
+}
+
+// isqrt_wave on every element: each wave walks its 64 elements one at a time
+// (the search needs the whole wave; indices are clamped so every lane stays
+// active).
+__global__ void k_op_isqrt_wave(const int64_t* a, i64 n, int64_t* o) {
+  const i64 lane = threadIdx.x & 63;
+  const i64 wave0 = (blockIdx.x * (i64)blockDim.x + threadIdx.x) - lane;
+  const i64 stride = (i64)gridDim.x * blockDim.x;
+  for (i64 base = wave0; base < n; base += stride) {
+    const i64 i = base + lane < n ? base + lane : n - 1;
+    const i64 mine = a[i];
+    i64 res = 0;
+    for (int j = 0; j < 64; ++j) {
+      const i64 nj = readlane64(mine, j);
+      const i64 r = isqrt_wave(nj);
+      if (lane == j) res = r;
+    }
+    if (base + lane < n) o[base + lane] = res;
   }
 }
 
@@ -1062,8 +1094,11 @@ int detllm_op_rope(const int64_t* x, const int64_t* pos, const int16_t* cos_t,
 int detllm_op_scalar(int op, const int64_t* a, const int64_t* b, const int64_t* c, int64_t n,
                      int64_t* o1, int64_t* o2, hipStream_t s) {
   if (n <= 0) return DI_OK;
-  if (op < 0 || op > 4) return DI_EINVAL;
-  hipLaunchKernelGGL(k_op_scalar, dim3(grid_for(n)), dim3(256), 0, s, op, a, b, c, n, o1, o2);
+  if (op < 0 || op > 6) return DI_EINVAL;
+  if (op == 6)
+    hipLaunchKernelGGL(k_op_isqrt_wave, dim3(grid_for(n)), dim3(256), 0, s, a, n, o1);
+  else
+    hipLaunchKernelGGL(k_op_scalar, dim3(grid_for(n)), dim3(256), 0, s, op, a, b, c, n, o1, o2);
   DI_LAUNCH_CHECK();
   return DI_OK;
 }

@@ -155,6 +155,8 @@ class IntQwen3:
         assert self.hd == 128, "the rocm kernels are specialised to head_dim 128"
         assert self.n_q % self.n_kv == 0 and self.n_q // self.n_kv in (1, 2, 4, 8)
         assert self.hidden % 16 == 0 and self.inter % 16 == 0
+        assert self.hidden <= 4096 and self.inter <= 4096 and self.n_q * self.hd <= 4096, \
+            "the fused row kernels hold a row of at most 4096 columns in one block"
         assert self.hd * 127 * 127 < 2 ** 31 and self.inter * 127 * 127 < 2 ** 31
         dev = self.device
         g = lambda n: tensors[n].to(dev)

@@ -199,7 +199,9 @@ int detllm_op_rope(const int64_t* x, const int64_t* pos, const int16_t* cos_t,
 /* Elementwise primitives: op 0 isqrt (intmath.py:180-202, int_prims.py:31-44),
  * 1 ilog2_floor (intmath.py:164-177, int_prims.py:47-55), 2 norm_scale
  * (dyadic.py:75-90), 3 fit_dyadic_ratio (dyadic.py:52-72), 4
- * scaled_round_div (dyadic.py:45-49). */
+ * scaled_round_div (dyadic.py:45-49); and the device forms the fused kernels
+ * use for the same functions: 5 fit_dyadic_ratio(a, 127) (constant-divisor
+ * path), 6 isqrt by the wave-parallel search. */
 int detllm_op_scalar(int op, const int64_t* a, const int64_t* b, const int64_t* c, int64_t n,
                      int64_t* o1, int64_t* o2, hipStream_t s);
 

@@ -8,7 +8,7 @@ reference's contiguous int8 ``[B, n_kv, S, hd]`` per layer with a ``valid``
 slot mask; the reference's static-capacity / graphed variants compute the same
 bits by construction (graphed.py:12-20), so only the dynamic form is restated.
 
-Pinned: tests/golden/tiny_model.npz — logits, tokens and demo chain hashes
+Pinned: tests/golden/model_tiny.json and model_mid.json — logits, tokens and demo chain hashes
 written by running the reference's own ``IntQwen3(backend="reference")`` on a
 seeded random-init artifact (tests/golden/make_golden.py).
 """

@@ -4,7 +4,7 @@ Pinned: tests/golden/ops.npz (vectors written from the reference CPU path by
 tests/golden/make_golden.py) plus the exact special cases the reference's
 tests/test_ops.py holds (exp(0) = tpos and tail -> 0 :123-134; masked
 invariance and all-masked rows :164-181; RMSNorm scale invariance and zero
-rows :202-212), restated in tests/test_oracle_ops.py.
+rows :202-212), restated in tests/test_oracle_golden.py.
 """
 
 from __future__ import annotations

@@ -66,6 +66,33 @@ def test_isqrt_ilog2_vs_closed_forms():
     eq(dd.isqrt(g(x)), oim.isqrt(x))
 
 
+def test_device_fast_paths_vs_closed_forms(D):
+    """The forms the fused kernels run: the wave-parallel isqrt (op 6) is
+    floor(sqrt) (math.isqrt) and fit_dyadic_ratio(., 127) by the constant-127
+    path (op 5) equals the reference's golden vectors and the generic form."""
+    from idempotent_llm_amd._lib import call
+    rnd = np.random.default_rng(5)
+    v = np.concatenate([rnd.integers(0, 1 << 62, 100000, dtype=I64),
+                        (I64(1) << rnd.integers(0, 62, 5000).astype(I64)) - 1,
+                        np.arange(-3, 70000, dtype=I64),
+                        np.array([(1 << 63) - 1, (1 << 62) - 1, 1 << 62, 3037000499 ** 2,
+                                  3037000499 ** 2 - 1, -(1 << 63)], I64)])
+    x = g(v)
+    out = torch.empty_like(x)
+    call("detllm_op_scalar", 6, x, None, None, x.numel(), out, None)
+    assert out.cpu().numpy().tolist() == [math.isqrt(int(t)) if t > 0 else 0 for t in v]
+    num = np.concatenate([D["fit_num"], rnd.integers(1, 1 << 62, 50000, dtype=I64)])
+    xn = g(num)
+    m5, e5 = torch.empty_like(xn), torch.empty_like(xn)
+    call("detllm_op_scalar", 5, xn, None, None, xn.numel(), m5, e5)
+    den = g(np.full_like(num, 127))
+    m3, e3 = torch.empty_like(xn), torch.empty_like(xn)
+    call("detllm_op_scalar", 3, xn, den, None, xn.numel(), m3, e3)
+    eq(m5, m3.cpu().numpy()); eq(e5, e3.cpu().numpy())
+    n0 = D["fit_num"].size
+    eq(m5[:n0], D["fit127_m"]); eq(e5[:n0], D["fit127_e"])
+
+
 def test_dyadic_scalars(D):
     from idempotent_llm_amd import dyadic as dd
     eq(dd.scaled_round_div(g(D["srd_num"]), g(D["srd_den"]), g(D["srd_e"])), D["srd_out"])

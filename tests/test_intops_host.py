@@ -179,3 +179,36 @@ def test_scalar_ops_match_oracle(lib, golden_dir):
     assert np.array_equal(m, D["fit127_m"]) and np.array_equal(e, D["fit127_e"])
     wm, we = ody.norm_scale(D["ns_m"], D["ns_k"])
     assert np.array_equal(wm, m2) and np.array_equal(we, k2)
+
+
+def test_fit127_fast_path_matches_generic_and_golden(lib, golden_dir):
+    """fit_dyadic_ratio(num, 127) through the constant-127 reciprocal path
+    (what every fused kernel runs) equals the generic routine and the
+    reference's golden vectors, across the fast-path boundary (2^56) and at
+    the adjustment edges (mantissas near 2^15 and 2^16)."""
+    D = dict(np.load(os.path.join(golden_dir, "dyadic.npz")))
+    m, e = _scalar(lib, 5, D["fit_num"])
+    assert np.array_equal(m, D["fit127_m"]) and np.array_equal(e, D["fit127_e"])
+    rnd = np.random.default_rng(11)
+    num = np.concatenate([
+        rnd.integers(1, 1 << 62, 50000, dtype=I64),
+        (I64(1) << rnd.integers(0, 62, 20000).astype(I64)) + rnd.integers(-3, 4, 20000),
+        np.arange(1, 5000, dtype=I64),
+        np.array([(1 << 56) - 1, 1 << 56, (1 << 56) + 1, (1 << 55) + 12345, 127, 254, 127 << 20,
+                  (127 << 20) - 1, (1 << 63) - 1], I64)])
+    num = num[num > 0]
+    fm, fe = _scalar(lib, 5, num)
+    gm, ge = _scalar(lib, 3, num, np.full_like(num, 127))
+    assert np.array_equal(fm, gm) and np.array_equal(fe, ge)
+    om, oe = ody.fit_dyadic_ratio(num, 127)
+    assert np.array_equal(fm, om) and np.array_equal(fe, oe)
+
+
+def test_rhad_pow2_matches_rhad(lib):
+    rnd = np.random.default_rng(12)
+    a = np.concatenate([rnd.integers(-(1 << 63), (1 << 63) - 1, 40000, dtype=I64, endpoint=True),
+                        np.array([-(1 << 63), (1 << 63) - 1, 0, 1, -1, 511, 512, -512, 513], I64)])
+    for k in (0, 1, 7, 10, 20, 40, 62):
+        got, _ = _scalar(lib, 6, a, np.full_like(a, k))
+        want = _call2(lib, "di_host_rhad", a, np.full_like(a, 1 << k))
+        assert np.array_equal(got, want), k
