@@ -159,7 +159,11 @@ def gemm_tops(T: int = PREFILL_LEN):
         a = torch.randint(-127, 128, (M, K), dtype=torch.int8, device=dev)
         w = torch.randint(-127, 128, (N, K), dtype=torch.int8, device=dev)
         out = torch.empty(1, M, N, dtype=torch.int32, device=dev)
-        us = _graph_time_us(lambda: gemm_nt(a, w, out=out), 50, 1)
+        def run(a=a, w=w, out=out):
+            for _ in range(20):
+                gemm_nt(a, w, out=out)
+
+        us = _graph_time_us(run, 10, 20)
         ops = 2.0 * M * N * K
         tops = ops / (us * 1e-6) / 1e12
         res[name] = {"M": M, "N": N, "K": K, "us": round(us, 2), "tops": round(tops, 1),

@@ -17,8 +17,10 @@
 // in element r of lane l.
 //
 // Kernels:
-//   k_gemm_nt   — 128x128x64 block tiles, 4 waves of 64x64, LDS double
-//                 buffer; for M > 64 (prefill).
+//   k_gemm_nt2  — M > 64, K % 128 == 0 (prefill): 32x32x32 MFMA, direct-to-LDS
+//                 operand ring with swizzled rows, XCD-blocked tile order.
+//   k_gemm_nt   — other M > 64 shapes: 128x128x64 block tiles, 4 waves of
+//                 64x64, LDS double buffer.
 //   k_gemv_nt   — M <= 64 (decode): a wave owns 16 output columns and a
 //                 K range; weight fragments stream straight from HBM into
 //                 MFMA operands, every load of a batch issued before the
@@ -116,6 +118,165 @@ __global__ __launch_bounds__(256) void k_gemm_nt(const int8_t* __restrict__ A,
         const int col = tn * TBN + wn * 64 + j * 16 + r16;
         if (row < M && col < N) C[(i64)row * N + col] = acc[i][j][r];
       }
+}
+
+// ---------------------------------------------------------------------------
+// k_gemm_nt2 — the prefill GEMM (M > 64, K % 128 == 0), on the full-rate
+// v_mfma_i32_32x32x32_i8 (the 16x16x64 form issues at about half its rate
+// on gfx950).
+//
+// Operands stream into LDS with direct-to-LDS loads (global_load_lds_dwordx4:
+// lane l's 16 bytes land at base + 16 l) through an S-stage ring of 128-byte
+// K slices. A load instruction covers 8 operand rows x 128 bytes, i.e. 8 whole
+// cache lines. In LDS each slice is row-major (128 bytes per row) with the
+// 16-byte chunks of row r permuted, physical chunk = logical chunk ^
+// ((r / 2) % 8), so the MFMA operand reads (32 rows, one chunk each) hit
+// distinct banks; the loader lanes fetch the logical chunk that belongs at
+// their physical position. Rows past M / N are clamped to the last row (valid
+// memory; their results are never stored). Waits are explicit: each wave
+// waits for its own loads of the slice it is about to use (vmcnt), then one
+// barrier makes every wave's part visible and frees the slot that the next
+// issue overwrites. Tiles are ordered so that each XCD (blocks are dispatched
+// round-robin over the 8 XCDs) owns one contiguous block of the tile grid,
+// keeping its share of A and B in its own L2.
+// ---------------------------------------------------------------------------
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+typedef __attribute__((address_space(1))) void* gbl_ptr_t;
+typedef int v16i __attribute__((ext_vector_type(16)));
+
+__device__ __forceinline__ v16i mfma32(v4i a, v4i b, v16i c) {
+  return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c, 0, 0, 0);
+}
+
+// s_waitcnt with vmcnt = n (n < 64) and no wait on the other counters
+template <int n>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(n >= 0 && n < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((n & 0xF) | ((n >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
+__device__ __forceinline__ int g2_swz(int row) { return (row >> 1) & 7; }
+
+// tile order: XCD x (= blockIdx % 8) owns block (x / 4, x % 4) of a 2 x 4
+// split of the tile grid when the grid divides evenly, else row-major order
+__device__ __forceinline__ void g2_tile(int bid, int tiles_m, int tiles_n, int& tm, int& tn) {
+  if ((tiles_m & 1) != 0 || (tiles_n & 3) != 0) {
+    tm = bid / tiles_n;
+    tn = bid - tm * tiles_n;
+    return;
+  }
+  const int xcd = bid & 7, j = bid >> 3;
+  const int bm = tiles_m >> 1, bn = tiles_n >> 2;
+  tm = (xcd >> 2) * bm + j / bn;
+  tn = (xcd & 3) * bn + j % bn;
+}
+
+constexpr int G2_BK = 128;
+
+template <int BM, int BN, int S, int MINB>
+__global__ __launch_bounds__(256, MINB) void k_gemm_nt2(const int8_t* __restrict__ A,
+                                                        const int8_t* __restrict__ B,
+                                                        int32_t* __restrict__ C, int M, int N,
+                                                        int K, i64 sA, i64 sB, i64 sC,
+                                                        int tiles_m, int tiles_n) {
+  constexpr int ROWS = BM + BN;       // 128-byte rows per slice: A rows, then B rows
+  constexpr int NI = ROWS / 8;        // load instructions per slice (8 rows each)
+  static_assert(NI % 4 == 0, "loads per wave");
+  constexpr int LPW = NI / 4;
+  constexpr int STAGE = ROWS * G2_BK;
+  constexpr int WA = BM / 64, WB = BN / 64;  // 32x32 blocks per wave (2 x 2 waves)
+  __shared__ __attribute__((aligned(1024))) int8_t lds[S * STAGE];
+
+  const int bz = blockIdx.z;
+  A += bz * sA;
+  B += bz * sB;
+  C += bz * sC;
+  int tm, tn;
+  g2_tile(blockIdx.x, tiles_m, tiles_n, tm, tn);
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int wm = wave >> 1, wn = wave & 1;
+
+  // this wave's loads: instruction i covers slice rows 8i..8i+7; lane l takes
+  // row 8i + l/8 at physical chunk l%8, i.e. logical chunk (l%8) ^ swz(row)
+  const int8_t* src[LPW];
+  int dst_off[LPW];
+#pragma unroll
+  for (int j = 0; j < LPW; ++j) {
+    const int ins = wave * LPW + j;
+    const int srow = ins * 8 + (lane >> 3);
+    const int lch = (lane & 7) ^ g2_swz(srow);
+    if (srow < BM) {
+      const int row = min(tm * BM + srow, M - 1);
+      src[j] = A + (i64)row * K + lch * 16;
+    } else {
+      const int col = min(tn * BN + (srow - BM), N - 1);
+      src[j] = B + (i64)col * K + lch * 16;
+    }
+    dst_off[j] = __builtin_amdgcn_readfirstlane(ins * 1024);
+  }
+  auto issue = [&](int kt) {
+    int8_t* base = lds + (kt % S) * STAGE;
+#pragma unroll
+    for (int j = 0; j < LPW; ++j)
+      __builtin_amdgcn_global_load_lds((gbl_ptr_t)(src[j] + (i64)kt * G2_BK),
+                                       (lds_ptr_t)(base + dst_off[j]), 16, 0, 0);
+  };
+
+  // MFMA operands: lane l reads row l%32 of a 32-row block, logical chunk
+  // 2s + l/32 of sub-slice s (32 K values); A and B use the same K order
+  const int r32 = lane & 31, half = lane >> 5;
+  v16i acc[WA][WB];
+#pragma unroll
+  for (int i = 0; i < WA; ++i)
+#pragma unroll
+    for (int j = 0; j < WB; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
+
+  const int nk = K / G2_BK;
+#pragma unroll
+  for (int s = 0; s < S - 1; ++s)
+    if (s < nk) issue(s);
+  for (int kt = 0; kt < nk; ++kt) {
+    // slices issued after kt so far: min(S - 2, nk - 1 - kt)
+    const int after = min(S - 2, nk - 1 - kt);
+    if (after >= 2) wait_vmcnt<2 * LPW>();
+    else if (after == 1) wait_vmcnt<LPW>();
+    else wait_vmcnt<0>();
+    __builtin_amdgcn_s_barrier();
+    if (kt + S - 1 < nk) issue(kt + S - 1);
+    const int8_t* base = lds + (kt % S) * STAGE;
+#pragma unroll
+    for (int s = 0; s < G2_BK / 32; ++s) {
+      v4i af[WA], bf[WB];
+#pragma unroll
+      for (int i = 0; i < WA; ++i) {
+        const int r = (wm * WA + i) * 32 + r32;
+        af[i] = *(const v4i*)(base + r * G2_BK + ((2 * s + half) ^ g2_swz(r)) * 16);
+      }
+#pragma unroll
+      for (int j = 0; j < WB; ++j) {
+        const int r = BM + (wn * WB + j) * 32 + r32;
+        bf[j] = *(const v4i*)(base + r * G2_BK + ((2 * s + half) ^ g2_swz(r)) * 16);
+      }
+#pragma unroll
+      for (int i = 0; i < WA; ++i)
+#pragma unroll
+        for (int j = 0; j < WB; ++j) acc[i][j] = mfma32(af[i], bf[j], acc[i][j]);
+    }
+  }
+  // 32x32 result block: lane l, element r -> row 8(r/4) + 4(l/32) + r%4, col l%32
+#pragma unroll
+  for (int i = 0; i < WA; ++i)
+#pragma unroll
+    for (int j = 0; j < WB; ++j) {
+      const int col = tn * BN + (wn * WB + j) * 32 + r32;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int row = tm * BM + (wm * WA + i) * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
+        if (row < M && col < N) C[(i64)row * N + col] = acc[i][j][r];
+      }
+    }
 }
 
 // Skinny GEMM (decode GEMV), M <= 64 rows, C[ks][M][N] = A[M][Kchunk] . B[N][Kchunk]^T.
@@ -306,8 +467,28 @@ int detllm_igemm_nt(const int8_t* A, const int8_t* B, int32_t* C, int M, int N, 
                     int64_t sA, int64_t sB, int64_t sC, hipStream_t s) {
   if (M <= 0 || N <= 0 || batch <= 0) return DI_OK;
   if (K <= 0 || (K % 16) != 0 || K > 131071 || !A || !B || !C) return DI_EINVAL;
+  if (batch > 65535) return DI_ERANGE;
+  if (M > 64 && K % G2_BK == 0) {
+    // 128x128 tiles (2 slices, 2 blocks per CU) while they give at least two
+    // tiles per CU; otherwise 128x64 tiles (3 slices) for more parallelism
+    const i64 t128 = (i64)((M + 127) / 128) * ((N + 127) / 128) * batch;
+    const int tm = (M + 127) / 128;
+    if (t128 >= 512) {
+      const int tn = (N + 127) / 128;
+      if ((i64)tm * tn > 0x7fffffff) return DI_ERANGE;
+      hipLaunchKernelGGL((k_gemm_nt2<128, 128, 2, 2>), dim3(tm * tn, 1, batch), dim3(256), 0, s,
+                         A, B, C, M, N, K, (i64)sA, (i64)sB, (i64)sC, tm, tn);
+    } else {
+      const int tn = (N + 63) / 64;
+      if ((i64)tm * tn > 0x7fffffff) return DI_ERANGE;
+      hipLaunchKernelGGL((k_gemm_nt2<128, 64, 3, 2>), dim3(tm * tn, 1, batch), dim3(256), 0, s,
+                         A, B, C, M, N, K, (i64)sA, (i64)sB, (i64)sC, tm, tn);
+    }
+    DI_LAUNCH_CHECK();
+    return DI_OK;
+  }
   const int tiles_m = (M + TBM - 1) / TBM, tiles_n = (N + TBN - 1) / TBN;
-  if ((i64)tiles_m * tiles_n > 0x7fffffff || batch > 65535) return DI_ERANGE;
+  if ((i64)tiles_m * tiles_n > 0x7fffffff) return DI_ERANGE;
   hipLaunchKernelGGL(k_gemm_nt, dim3(tiles_m * tiles_n, 1, batch), dim3(256), 0, s, A, B, C, M,
                      N, K, (i64)sA, (i64)sB, (i64)sC, tiles_n);
   DI_LAUNCH_CHECK();

@@ -201,7 +201,9 @@ def test_rope(O):
 
 
 @pytest.mark.parametrize("M,K,N", [(7, 33, 5), (1, 1024, 4096), (8, 3072, 1024), (64, 1024, 3072),
-                                   (65, 1024, 3072), (200, 128, 300), (512, 2048, 1024)])
+                                   (65, 1024, 3072), (200, 128, 300), (512, 2048, 1024),
+                                   (2048, 1024, 4096), (2048, 3072, 1024), (2048, 1024, 6144),
+                                   (1000, 2048, 1000), (129, 64, 130), (300, 192, 64)])
 def test_int_gemm_exact(M, K, N):
     from idempotent_llm_amd.backends import int_gemm
     rnd = np.random.default_rng(M * 7 + K + N)
@@ -209,7 +211,7 @@ def test_int_gemm_exact(M, K, N):
     b = rnd.integers(-128, 128, (K, N)).astype(np.int8)
     got = int_gemm(g(a), g(b), "rocm")
     assert got.dtype == torch.int32
-    eq(got, a.astype(I64) @ b.astype(I64))
+    eq(got, ogemm.int_gemm(a, b))   # exact: float64 BLAS on int8 operands, |sum| < 2^53
 
 
 def test_int_gemm_extremes_and_batched():
@@ -221,6 +223,13 @@ def test_int_gemm_extremes_and_batched():
     a = rnd.integers(-128, 128, (3, 4, 37, 128)).astype(np.int8)
     b = rnd.integers(-128, 128, (3, 4, 128, 45)).astype(np.int8)
     eq(int_gemm(g(a), g(b), "rocm"), a.astype(I64) @ b.astype(I64))
+    # batched through the pipelined prefill kernel (M > 64, K % 64 == 0)
+    a = rnd.integers(-128, 128, (2, 3, 200, 256)).astype(np.int8)
+    b = rnd.integers(-128, 128, (2, 3, 256, 96)).astype(np.int8)
+    eq(int_gemm(g(a), g(b), "rocm"), a.astype(I64) @ b.astype(I64))
+    a = np.full((300, 1024), -128, np.int8)
+    b = np.full((1024, 200), -128, np.int8)
+    eq(int_gemm(g(a), g(b), "rocm"), np.full((300, 200), 1024 * 128 * 128))
     p = rnd.integers(0, 129, (9, 21)).astype(np.int32)
     v = rnd.integers(-128, 128, (21, 6)).astype(np.int8)
     eq(int_gemm_u8i8(g(p), g(v), "rocm"), p.astype(I64) @ v.astype(I64))
