@@ -29,6 +29,7 @@
 // every reduction is an exact integer max/sum.
 
 #include "common.h"
+#include "qkv_epilogue.h"
 
 using namespace di;
 
@@ -241,13 +242,16 @@ constexpr i64 DECODE_LDS_BYTES = 48 * 1024;
 constexpr int32_t SCORE_MASKED = INT32_MIN;  // |q.k| <= 128*128*128 < 2^31: never a score
 constexpr int VPRE = 8;                      // V chunks of 16 slots prefetched per thread
 
+// Attention of one (batch row b, kv head kvh) over its G query heads, whose
+// int8 rows sit at qsrc[hh * 128] and DI-Exp constants at tsrc[hh] (global
+// memory or LDS). 256 threads.
 template <int G>
-__global__ __launch_bounds__(256) void k_attn_decode(DecodeArgs a) {
-  extern __shared__ __attribute__((aligned(16))) int32_t sh_scores[];
+__device__ __forceinline__ void decode_body(const DecodeArgs& a, int kvh, int b,
+                                            const int8_t* qsrc, const int64_t* tsrc,
+                                            int32_t* sh_scores) {
   __shared__ i64 red_buf[32];
   BlockRed red{red_buf, 0};
   __shared__ i64 pv_acc[G][128];
-  const int kvh = blockIdx.x, b = blockIdx.y;
   const int tid = threadIdx.x, lane = tid & 63;
   int S = a.S;
   if (a.s_dev) {
@@ -279,8 +283,8 @@ __global__ __launch_bounds__(256) void k_attn_decode(DecodeArgs a) {
   i64 tp[G];
 #pragma unroll
   for (int hh = 0; hh < G; ++hh) {
-    qv[hh] = *(const v4i*)(a.q8 + ((i64)b * a.n_q + kvh * G + hh) * 128 + sub * 16);
-    tp[hh] = a.tpos[(i64)b * a.n_q + kvh * G + hh];
+    qv[hh] = *(const v4i*)(qsrc + hh * 128 + sub * 16);
+    tp[hh] = tsrc[hh];
   }
   i64 mx[G];
 #pragma unroll
@@ -389,6 +393,34 @@ __global__ __launch_bounds__(256) void k_attn_decode(DecodeArgs a) {
       a.out[(i64)b * a.n_q * 128 + (kvh * G + hh) * 128 + d] = (i64)acc[hh] + pv_acc[hh][d];
 }
 
+template <int G>
+__global__ __launch_bounds__(256) void k_attn_decode(DecodeArgs a) {
+  extern __shared__ __attribute__((aligned(16))) int32_t sh_scores[];
+  const int kvh = blockIdx.x, b = blockIdx.y;
+  const i64 q0 = (i64)b * a.n_q + kvh * G;
+  decode_body<G>(a, kvh, b, a.q8 + q0 * 128, a.tpos + q0, sh_scores);
+}
+
+// Decode step with the Q/K/V epilogue fused in (G <= 2): waves 0..G-1 finish
+// the block's query heads into LDS, wave G writes the key head and wave G + 1
+// the value head of this step's slot into the cache; after one barrier the
+// block attends over every slot, the new one included.
+template <int G>
+__global__ __launch_bounds__(256) void k_qkv_attn_decode(DecodeArgs a, QKVArgs qa) {
+  static_assert(G + 2 <= 4, "one wave per head slot");
+  extern __shared__ __attribute__((aligned(16))) int32_t sh_scores[];
+  __shared__ __attribute__((aligned(16))) int8_t q_lds[G][128];
+  __shared__ int64_t t_lds[G];
+  const int kvh = blockIdx.x, b = blockIdx.y, w = threadIdx.x >> 6;
+  int slotw = -1;
+  if (w < G) slotw = kvh * G + w;
+  else if (w == G) slotw = qa.n_q + kvh;
+  else if (w == G + 1) slotw = qa.n_q + qa.n_kv + kvh;
+  if (slotw >= 0) qkv_head(qa, b, slotw, w < G ? q_lds[w] : nullptr, w < G ? &t_lds[w] : nullptr);
+  __syncthreads();
+  decode_body<G>(a, kvh, b, &q_lds[0][0], t_lds, sh_scores);
+}
+
 }  // namespace
 
 extern "C" {
@@ -440,6 +472,59 @@ int detllm_attn_decode(const int8_t* q8, const int64_t* tpos, const int8_t* kc, 
     case 8: hipLaunchKernelGGL(k_attn_decode<8>, grid, dim3(256), dyn, s, a); break;
     default: return DI_ENOSYS;
   }
+  DI_LAUNCH_CHECK();
+  return DI_OK;
+}
+
+// Fused decode step for one query token per row: the Q/K/V epilogue of
+// detllm_qkv_epilogue (T = 1) followed by detllm_attn_decode, one launch.
+int detllm_qkv_attn_decode(const int32_t* P, int nsplit, int64_t split_stride, int B, int n_q,
+                           int n_kv, const int64_t* xm, const int64_t* xk,
+                           const int64_t* positions, const int64_t* q_m, int64_t q_k,
+                           const int64_t* k_m, int64_t k_k, const int64_t* v_m, int64_t v_k,
+                           const int64_t* q_norm_m, int64_t q_norm_k, const int64_t* k_norm_m,
+                           int64_t k_norm_k, const int64_t* qs_m, int64_t qs_k,
+                           const int64_t* kq_m, const int64_t* kq_k, const int64_t* ks_m,
+                           const int64_t* ks_k, const int64_t* vq_m, const int64_t* vq_k,
+                           const int16_t* cos_t, const int16_t* sin_t, int64_t max_pos,
+                           int8_t* kcache, int8_t* vcache, int64_t cap,
+                           const int64_t* slot_base_dev, int64_t slot_base,
+                           const uint8_t* valid, int64_t valid_stride, int S,
+                           const int64_t* s_dev, int32_t* scratch, int64_t* out,
+                           hipStream_t s) {
+  if (B <= 0) return DI_OK;
+  if (n_q <= 0 || n_kv <= 0 || n_q % n_kv || nsplit < 1 || S < 1 || S > cap || cap % 16 != 0 ||
+      valid_stride < S || max_pos <= 0 || !P || !out)
+    return DI_EINVAL;
+  if (!slot_base_dev && (slot_base < 0 || slot_base + 1 > cap)) return DI_ERANGE;
+  const int G = n_q / n_kv;
+  if (G > 2) return DI_ENOSYS;  // one wave per head slot of the block
+  const i64 Spad = ((i64)S + 15) & ~15;
+  const i64 lds = (i64)G * Spad * 4;
+  size_t dyn = 0;
+  if (lds <= DECODE_LDS_BYTES) {
+    dyn = (size_t)lds;
+    scratch = nullptr;
+  } else if (!scratch) {
+    return DI_ERANGE;
+  }
+  QKVArgs qa{};
+  qa.T = 1; qa.n_q = n_q; qa.n_kv = n_kv; qa.P = P; qa.nsplit = nsplit;
+  qa.split_stride = split_stride; qa.xm = xm; qa.xk = xk; qa.positions = positions;
+  qa.q_m = q_m; qa.k_m = k_m; qa.v_m = v_m; qa.q_k = q_k; qa.k_k = k_k; qa.v_k = v_k;
+  qa.q_norm_m = q_norm_m; qa.k_norm_m = k_norm_m; qa.q_norm_k = q_norm_k;
+  qa.k_norm_k = k_norm_k; qa.qs_m = qs_m; qa.qs_k = qs_k; qa.kq_m = kq_m; qa.kq_k = kq_k;
+  qa.ks_m = ks_m; qa.ks_k = ks_k; qa.vq_m = vq_m; qa.vq_k = vq_k; qa.cos_t = cos_t;
+  qa.sin_t = sin_t; qa.max_pos = max_pos; qa.q8 = nullptr; qa.tpos = nullptr; qa.dbg = nullptr;
+  qa.kcache = kcache; qa.vcache = vcache; qa.cap = cap; qa.slot_base_dev = slot_base_dev;
+  qa.slot_base = slot_base;
+  DecodeArgs a{nullptr, nullptr, kcache, vcache, valid, out, scratch, s_dev, S, n_q, n_kv, cap,
+               valid_stride};
+  const dim3 grid(n_kv, B);
+  if (G == 1)
+    hipLaunchKernelGGL(k_qkv_attn_decode<1>, grid, dim3(256), dyn, s, a, qa);
+  else
+    hipLaunchKernelGGL(k_qkv_attn_decode<2>, grid, dim3(256), dyn, s, a, qa);
   DI_LAUNCH_CHECK();
   return DI_OK;
 }

@@ -1,0 +1,203 @@
+// Q/K/V epilogue of one (token row, head slot), shared by the standalone
+// epilogue kernel (prefill) and the fused decode attention kernel.
+//
+// One wave per (token row r, head slot): slots [0, n_q) are query heads,
+// [n_q, n_q + n_kv) key heads, then value heads. Lane l owns channels l and
+// l + 64, which is exactly the rotate_half pairing of RoPE. Reference:
+// model.py:200-216 (_qk_head_pipeline), :303-340 (QK smoothing, Q
+// quant_i8_pertoken, K/V requant_i8_static, cache write), :351-358 (score
+// scale and DI-Exp constant).
+#pragma once
+
+#include "common.h"
+
+namespace di {
+
+struct QKVArgs {
+  int T;
+  int n_q, n_kv;
+  const int32_t* P;  // [nsplit][R][(n_q + 2 n_kv) * 128]
+  int nsplit;
+  i64 split_stride;
+  const int64_t* xm;
+  const int64_t* xk;
+  const int64_t* positions;  // [R]
+  const int64_t* q_m;
+  const int64_t* k_m;
+  const int64_t* v_m;
+  i64 q_k, k_k, v_k;
+  const int64_t* q_norm_m;
+  const int64_t* k_norm_m;
+  i64 q_norm_k, k_norm_k;
+  const int64_t* qs_m;  // [n_kv * 128]
+  i64 qs_k;
+  const int64_t* kq_m;  // [n_kv * 128]
+  const int64_t* kq_k;
+  const int64_t* ks_m;  // [n_kv]
+  const int64_t* ks_k;
+  const int64_t* vq_m;
+  const int64_t* vq_k;
+  const int16_t* cos_t;
+  const int16_t* sin_t;
+  i64 max_pos;
+  int8_t* q8;      // [B][n_q][T][128]
+  int64_t* tpos;   // [B][n_q][T]
+  int64_t* dbg;    // optional [B][n_q][T][4]: qm, qk, sm, sk
+  int8_t* kcache;  // [B][n_kv][cap][128]
+  int8_t* vcache;  // [B][n_kv][128][cap]  (V stored transposed)
+  i64 cap;
+  const int64_t* slot_base_dev;  // optional device scalar (graph replay)
+  i64 slot_base;
+};
+
+__device__ __forceinline__ void wave_rmsnorm128(i64& a, i64& b) {
+  // ops/di_rmsnorm.py:33-52 over 128 channels held two per lane
+  const i64 g = wave_max(imax(wabs(a), wabs(b)));
+  const i64 sh = 25 - ilog2(imax(g, 1));
+  const i64 up = imax(sh, 0), down = imax(-sh, 0);
+  a = shl(rshift_round(a, down), up);
+  b = shl(rshift_round(b, down), up);
+  const i64 ss = wave_sum(wadd(wmul(a, a), wmul(b, b)));
+  const Recip R = make_recip(imax(isqrt_wave(rhad_pow2(ss, 7)), 1));
+  a = to_i32(rhad_r(shl(a, 20), R));
+  b = to_i32(rhad_r(shl(b, 20), R));
+}
+
+// The whole wave must be active. K and V go to the cache; a query head's
+// int8 row goes to q8_out[0..128) and its DI-Exp constant to *tpos_out
+// (global memory for the standalone kernel, LDS for the fused one).
+__device__ __forceinline__ void qkv_head(const QKVArgs& a, int r, int slotw, int8_t* q8_out,
+                                         int64_t* tpos_out) {
+  const int lane = threadIdx.x & 63;
+  const int n_heads = a.n_q + 2 * a.n_kv;
+
+  const int b = r / a.T, t = r - b * a.T;
+  const int NQKV = n_heads * 128;
+  const i64 off = (i64)r * NQKV + (i64)slotw * 128;
+  const int group = a.n_q / a.n_kv;
+  const bool is_q = slotw < a.n_q, is_v = slotw >= a.n_q + a.n_kv;
+  const int h = is_q ? slotw : (is_v ? slotw - a.n_q - a.n_kv : slotw - a.n_q);
+  const int kvh = is_q ? h / group : h;
+  const int c0 = lane, c1 = lane + 64;
+
+  // ---- every global load up front (one memory round trip, plus the RoPE
+  // table rows that depend on the position)
+  const i64 pos_raw = a.positions[r];
+  const i64 xk = a.xk[r], xm = a.xm[r];
+  const i64 base = a.slot_base_dev ? a.slot_base_dev[0] : a.slot_base;
+  const int64_t* wmp = (is_q ? a.q_m : (is_v ? a.v_m : a.k_m)) + (i64)h * 128;
+  const i64 wm0 = wmp[c0], wm1 = wmp[c1];
+  const int64_t* gam = is_q ? a.q_norm_m : a.k_norm_m;
+  const i64 g0 = gam[c0], g1 = gam[c1];
+  const i64 qs0 = a.qs_m[kvh * 128 + c0], qs1 = a.qs_m[kvh * 128 + c1];
+  const i64 kqm0 = a.kq_m[kvh * 128 + c0], kqm1 = a.kq_m[kvh * 128 + c1];
+  const i64 kqk0 = a.kq_k[kvh * 128 + c0], kqk1 = a.kq_k[kvh * 128 + c1];
+  const i64 vqm = a.vq_m[kvh], vqk = a.vq_k[kvh];
+  const i64 ksm = a.ks_m[kvh], ksk = a.ks_k[kvh];
+  i64 p0, p1;
+  {
+    uint32_t s0 = 0, s1 = 0;
+    for (int k0 = 0; k0 < a.nsplit; k0 += 4) {
+      int32_t t0[4], t1[4];
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) {
+        const int k = k0 + kk < a.nsplit ? k0 + kk : a.nsplit - 1;
+        t0[kk] = a.P[(i64)k * a.split_stride + off + c0];
+        t1[kk] = a.P[(i64)k * a.split_stride + off + c1];
+      }
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk)
+        if (k0 + kk < a.nsplit) {
+          s0 += (uint32_t)t0[kk];
+          s1 += (uint32_t)t1[kk];
+        }
+    }
+    p0 = (int32_t)s0;
+    p1 = (int32_t)s1;
+  }
+  const i64 pos = pos_raw < 0 ? 0 : (pos_raw >= a.max_pos ? a.max_pos - 1 : pos_raw);
+  const i64 cs0 = a.cos_t[pos * 128 + c0], cs1 = a.cos_t[pos * 128 + c1];
+  const i64 sn0 = a.sin_t[pos * 128 + c0], sn1 = a.sin_t[pos * 128 + c1];
+  const i64 slot = base + t;
+
+  if (is_v) {
+    // ---- V head: requant_i8_static(Pv, xm, xk, v_m, v_k, vq_m[h], vq_k[h])
+    const i64 shift = wsub(wadd(xk, a.v_k), vqk);
+    const i64 up = imax(wneg(shift), 0), down = imax(shift, 0);
+    i64 den = shl(vqm, down);
+    if (den <= 0) den = 1;  // static scales are positive mantissas in artifacts
+    const i64 n0 = shl(wmul(wmul(p0, wm0), xm), up);
+    const i64 n1 = shl(wmul(wmul(p1, wm1), xm), up);
+    const Recip R = make_recip(den);
+    int8_t* vrow = a.vcache + ((i64)b * a.n_kv + h) * 128 * a.cap;
+    if (slot >= 0 && slot < a.cap) {
+      vrow[(i64)c0 * a.cap + slot] = (int8_t)clamp_i8(rhad_r(n0, R));
+      vrow[(i64)c1 * a.cap + slot] = (int8_t)clamp_i8(rhad_r(n1, R));
+    }
+    return;
+  }
+  // requant_i32_common(tb = 16) per (token, head)   (model.py:207-211); the
+  // (m, k) it returns are dropped by _qk_head_pipeline
+  i64 y0 = wmul(p0, wm0), y1 = wmul(p1, wm1);
+  {
+    const i64 am = imax(wave_max(imax(wabs(y0), wabs(y1))), 1);
+    const i64 sh = imax(ilog2(am) - 15, 0);
+    y0 = to_i32(rshift_round(y0, sh));
+    y1 = to_i32(rshift_round(y1, sh));
+  }
+  // di_rmsnorm_gamma  (model.py:212)
+  wave_rmsnorm128(y0, y1);
+  y0 = wmul(y0, g0);
+  y1 = wmul(y1, g1);
+  // apply_int_rope at this token's position   (model.py:213-215; rope.py:38-55)
+  const i64 r0 = rshift_round(wadd(wmul(y0, cs0), wmul(wneg(y1), sn0)), 14);
+  const i64 r1 = rshift_round(wadd(wmul(y1, cs1), wmul(y0, sn1)), 14);
+  if (!is_q) {
+    // K: requant_i8_static(kk, 1, k_rowk, 1, 0, kq_m, kq_k)   (model.py:326-329)
+    const i64 rowk = 20 + a.k_norm_k;
+    int8_t* krow = a.kcache + (((i64)b * a.n_kv + h) * a.cap + slot) * 128;
+    const i64 rv[2] = {r0, r1}, km[2] = {kqm0, kqm1}, kk[2] = {kqk0, kqk1};
+    i64 outv[2];
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const i64 shift = wsub(rowk, kk[q]);
+      const i64 up = imax(wneg(shift), 0), down = imax(shift, 0);
+      i64 den = shl(km[q], down);
+      if (den <= 0) den = 1;
+      outv[q] = clamp_i8(rhad(shl(rv[q], up), den));
+    }
+    if (slot >= 0 && slot < a.cap) {
+      krow[c0] = (int8_t)outv[0];
+      krow[c1] = (int8_t)outv[1];
+    }
+    return;
+  }
+  // Q: QK smoothing (model.py:317-320) then quant_i8_pertoken (model.py:322-323)
+  const i64 q0 = wmul(r0, qs0);
+  const i64 q1 = wmul(r1, qs1);
+  const i64 qkk = 20 + a.q_norm_k + a.qs_k;
+  i64 m, k;
+  norm_scale(1, qkk, &m, &k);
+  const i64 am = imax(wave_max(imax(wabs(q0), wabs(q1))), 1);
+  const Recip R = make_recip(am);
+  const i64 qrow = (((i64)b * a.n_q + h) * a.T + t);
+  q8_out[c0] = (int8_t)clamp_i8(rhad_r(wmul(q0, 127), R));
+  q8_out[c1] = (int8_t)clamp_i8(rhad_r(wmul(q1, 127), R));
+  if (lane == 0) {
+    i64 qm, e;
+    fit_dyadic_ratio_127(wmul(am, m), &qm, &e);
+    const i64 qk = wadd(k, e);
+    // score scale: norm_scale(qm * ks_m[h//g], qk + ks_k[h//g])   (model.py:351-353)
+    i64 sm, sk;
+    norm_scale(wmul(qm, ksm), wadd(qk, ksk), &sm, &sk);
+    *tpos_out = di_exp_tpos(sm, sk);
+    if (a.dbg) {
+      a.dbg[qrow * 4 + 0] = qm;
+      a.dbg[qrow * 4 + 1] = qk;
+      a.dbg[qrow * 4 + 2] = sm;
+      a.dbg[qrow * 4 + 3] = sk;
+    }
+  }
+}
+
+}  // namespace di

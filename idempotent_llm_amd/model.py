@@ -280,6 +280,34 @@ class IntQwen3:
         R, H, nq, nkv, hd, I_ = B * T, self.hidden, self.n_q, self.n_kv, self.hd, self.inter
         li = L.idx
         P, ns, st = self._gemm(x8, L.wqkv)
+        attn = torch.empty(R, nq * hd, dtype=I64, device=dev)
+        valid = cache.valid_buf.view(torch.uint8)
+        if T == 1 and nq // nkv <= 2:
+            # decode: Q/K/V epilogue and attention in one launch
+            scratch = self._decode_scratch(B, S)
+            call("detllm_qkv_attn_decode", P, ns, st, B, nq, nkv, xm, xk, pos,
+                 L.q_m, L.q_k, L.k_m, L.k_k, L.v_m, L.v_k, L.q_norm_m, L.q_norm_k,
+                 L.k_norm_m, L.k_norm_k, L.qs_m, L.qs_k, L.kq_m, L.kq_k, L.ks_m, L.ks_k,
+                 L.vq_m, L.vq_k, self.rope_cos, self.rope_sin, self.max_pos,
+                 cache.k8[li], cache.v8[li], cache.cap, cache.len_idx if static else None,
+                 0 if static else S_past, valid, cache.cap, S,
+                 cache.nslots if static else None, scratch, attn)
+        else:
+            self._attention(L, B, T, P, ns, st, xm, xk, pos, cache, S_past, S, static, attn)
+        self._after_attention(L, nxt, B, T, attn, h, k_res, x8, xm, xk)
+
+    def _decode_scratch(self, B, S):
+        """Global score scratch of the decode attention when the scores of a
+        (row, kv-head) do not fit its 48 KiB of LDS."""
+        G = self.n_q // self.n_kv
+        Spad = (S + 15) // 16 * 16
+        if G * Spad * 4 <= 48 * 1024:
+            return None
+        return torch.empty(B, self.n_q, Spad, dtype=torch.int32, device=self.device)
+
+    def _attention(self, L, B, T, P, ns, st, xm, xk, pos, cache, S_past, S, static, attn):
+        dev = self.device
+        nq, nkv, hd, li = self.n_q, self.n_kv, self.hd, L.idx
         q8 = torch.empty(B, nq, T, hd, dtype=torch.int8, device=dev)
         tpos = torch.empty(B, nq, T, dtype=I64, device=dev)
         call("detllm_qkv_epilogue", P, ns, st, B, T, nq, nkv, xm, xk, pos,
@@ -288,19 +316,18 @@ class IntQwen3:
              L.vq_m, L.vq_k, self.rope_cos, self.rope_sin, self.max_pos, q8, tpos, None,
              cache.k8[li], cache.v8[li], cache.cap, cache.len_idx if static else None,
              0 if static else S_past)
-        attn = torch.empty(R, nq * hd, dtype=I64, device=dev)
         valid = cache.valid_buf.view(torch.uint8)
         if T == 1:
-            G = nq // nkv
-            Spad = (S + 15) // 16 * 16
-            scratch = None
-            if G * Spad * 4 > 48 * 1024:
-                scratch = torch.empty(B, nq, Spad, dtype=torch.int32, device=dev)
             call("detllm_attn_decode", q8, tpos, cache.k8[li], cache.v8[li], valid, cache.cap,
-                 B, S, nq, nkv, cache.cap, cache.nslots if static else None, scratch, attn)
+                 B, S, nq, nkv, cache.cap, cache.nslots if static else None,
+                 self._decode_scratch(B, S), attn)
         else:
             call("detllm_attn_prefill", q8, tpos, cache.k8[li], cache.v8[li], valid, cache.cap,
                  B, T, S_past, nq, nkv, cache.cap, attn)
+
+    def _after_attention(self, L, nxt, B, T, attn, h, k_res, x8, xm, xk):
+        dev = self.device
+        R, H, nq, hd, I_ = B * T, self.hidden, self.n_q, self.hd, self.inter
         a8 = torch.empty(R, nq * hd, dtype=torch.int8, device=dev)
         am = torch.empty(R, dtype=I64, device=dev)
         ak = torch.empty(R, dtype=I64, device=dev)

@@ -143,6 +143,28 @@ int detllm_attn_decode(const int8_t* q8, const int64_t* tpos, const int8_t* kcac
                        int S, int n_q, int n_kv, int64_t cap, const int64_t* s_dev,
                        int32_t* scratch, int64_t* out, hipStream_t s);
 
+/* One decode step's attention block with the Q/K/V epilogue fused in (one
+ * query token per row; n_q / n_kv <= 2): detllm_qkv_epilogue with T = 1 —
+ * model.py:200-216, :303-358 — followed by detllm_attn_decode — model.py:347-381
+ * and ops/fused_attn.py:47-142 — in one launch. Arguments as in those two
+ * entry points (P [nsplit][B][(n_q + 2 n_kv) * 128]; the step's slot is
+ * *slot_base_dev or slot_base; S slots are scanned, bounded by *s_dev when
+ * non-null). out [B][n_q * 128] int64. */
+int detllm_qkv_attn_decode(const int32_t* P, int nsplit, int64_t split_stride, int B, int n_q,
+                           int n_kv, const int64_t* xm, const int64_t* xk,
+                           const int64_t* positions, const int64_t* q_m, int64_t q_k,
+                           const int64_t* k_m, int64_t k_k, const int64_t* v_m, int64_t v_k,
+                           const int64_t* q_norm_m, int64_t q_norm_k, const int64_t* k_norm_m,
+                           int64_t k_norm_k, const int64_t* qs_m, int64_t qs_k,
+                           const int64_t* kq_m, const int64_t* kq_k, const int64_t* ks_m,
+                           const int64_t* ks_k, const int64_t* vq_m, const int64_t* vq_k,
+                           const int16_t* cos_t, const int16_t* sin_t, int64_t max_pos,
+                           int8_t* kcache, int8_t* vcache, int64_t cap,
+                           const int64_t* slot_base_dev, int64_t slot_base,
+                           const uint8_t* valid, int64_t valid_stride, int S,
+                           const int64_t* s_dev, int32_t* scratch, int64_t* out,
+                           hipStream_t s);
+
 /* ------------------------------------------- operator-level entry points -- */
 /* One reference function each (rows = leading dims flattened, C = last dim). */
 
