@@ -28,6 +28,7 @@ SIGNATURES = {
     "detllm_greedy_pick": [P, P, I, I, I, P, P, P, S],
     "detllm_embed_normq": [P, I, I, L, P, P, P, P, P, P, L, P, P, P, S],
     "detllm_residual_normq": [P, I, L, I, I, P, P, P, L, I, P, P, P, L, P, P, P, S],
+    "detllm_norm_quant": [P, I, I, P, L, P, P, P, S],
     "detllm_swiglu_quant": [P, I, L, I, I, P, P, P, L, P, L, P, L, P, P, P, S],
     "detllm_merge_rowcol": [P, I, L, I, I, P, L, P, L, P, P, P, S],
     "detllm_qkv_epilogue": [P, I, L, I, I, I, I, P, P, P, P, L, P, L, P, L, P, L, P, L, P, L,

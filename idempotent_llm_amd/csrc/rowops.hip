@@ -188,7 +188,8 @@ __device__ __forceinline__ void load_rows_i32_sum(i64 (&v)[NR][VPT], const int32
 
 struct ResNormArgs {
   int C;
-  int mode;  // 0: embedding gather (residual_from_delta); 1: GEMM residual add
+  int mode;  // 0: embedding gather (residual_from_delta); 1: GEMM residual add;
+             // 2: norm-quant of the given rows only
   i64 vocab;
   const int64_t* ids;
   const int8_t* e8;
@@ -221,7 +222,18 @@ __global__ __launch_bounds__(RT_WIDE) void k_residual_normq(ResNormArgs a) {
   i64 h[VPT], d[VPT], smv[VPT];
   i64 kr;
   prefetch_cols(smv, a.sm_m, C);
-  if (a.mode == 0) {
+  if (a.mode == 2) {
+    // _norm_quant of a given residual row: h is read, not written
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) {
+      const int c = threadIdx.x + j * (int)blockDim.x;
+      h[j] = a.h[off + (c < C ? c : C - 1)];
+    }
+#pragma unroll
+    for (int j = 0; j < VPT; ++j)
+      if (threadIdx.x + j * (int)blockDim.x >= C) h[j] = 0;
+    kr = 0;
+  } else if (a.mode == 0) {
     i64 id = a.ids[r];
     id = id < 0 ? 0 : (id >= a.vocab ? a.vocab - 1 : id);  // memory safety only
     const i64 dm = a.em[id], ek = a.ek[id];
@@ -253,12 +265,14 @@ __global__ __launch_bounds__(RT_WIDE) void k_residual_normq(ResNormArgs a) {
     const i64 dk = requant_common_row(d, cm, row_k, a.col_k, a.tb, red);
     kr = residual_add_row(h, k_res, d, row_m, dk, red);
   }
+  if (a.mode != 2) {
 #pragma unroll
-  for (int j = 0; j < VPT; ++j) {
-    const int c = threadIdx.x + j * (int)blockDim.x;
-    if (c < C) a.h[off + c] = (int32_t)h[j];
+    for (int j = 0; j < VPT; ++j) {
+      const int c = threadIdx.x + j * (int)blockDim.x;
+      if (c < C) a.h[off + c] = (int32_t)h[j];
+    }
+    if (threadIdx.x == 0) a.k_res[r] = kr;
   }
-  if (threadIdx.x == 0) a.k_res[r] = kr;
   if (a.x8 == nullptr) return;
   rmsnorm_row(h, C, red);
   i64 kq = 20;
@@ -742,6 +756,18 @@ int detllm_residual_normq(const int32_t* P, int nsplit, int64_t split_stride, in
   a.C = C; a.mode = 1; a.P = P; a.nsplit = nsplit; a.split_stride = split_stride;
   a.row_m = row_m; a.row_k = row_k; a.col_m = col_m; a.col_k = col_k; a.tb = tb;
   a.h = h; a.k_res = k_res; a.sm_m = sm_m; a.sm_k = sm_k; a.x8 = x8; a.xm = xm; a.xk = xk;
+  DI_WIDE_DISPATCH(C, k_residual_normq, dim3(R), s, a);
+  DI_LAUNCH_CHECK();
+  return DI_OK;
+}
+
+int detllm_norm_quant(const int32_t* h, int R, int C, const int64_t* sm_m, int64_t sm_k,
+                      int8_t* x8, int64_t* xm, int64_t* xk, hipStream_t s) {
+  if (R <= 0) return DI_OK;
+  if (C <= 0 || !h || !x8 || !xm || !xk) return DI_EINVAL;
+  ResNormArgs a{};
+  a.C = C; a.mode = 2; a.h = const_cast<int32_t*>(h); a.sm_m = sm_m; a.sm_k = sm_k;
+  a.x8 = x8; a.xm = xm; a.xk = xk;
   DI_WIDE_DISPATCH(C, k_residual_normq, dim3(R), s, a);
   DI_LAUNCH_CHECK();
   return DI_OK;

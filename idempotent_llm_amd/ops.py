@@ -95,5 +95,19 @@ def apply_int_rope(x: torch.Tensor, cos_t: torch.Tensor, sin_t: torch.Tensor,
     return y
 
 
+def di_linear(x8: torch.Tensor, xm, xk, w8_t: torch.Tensor, wm, wk):
+    """ops/di_matmul.py:22-31: exact int8 GEMM, scales passed through."""
+    from .backends import int_gemm
+    return int_gemm(x8, w8_t, "rocm"), xm, xk, wm, wk
+
+
+def di_matmul(x: torch.Tensor, xm, xk, w8_t: torch.Tensor, wm, wk):
+    """ops/di_matmul.py:34-40: quantise per token, GEMM, requantise to int8."""
+    from .dyadic import quant_i8_pertoken, requant_i8_rowcol
+    x8, qm, qk = quant_i8_pertoken(x, xm, xk)
+    P, rm, rk, cm, ck = di_linear(x8, qm, qk, w8_t, wm, wk)
+    return requant_i8_rowcol(P, rm, rk, cm, ck)
+
+
 __all__ = ["di_exp", "di_softmax", "di_rmsnorm", "di_rmsnorm_gamma", "di_swiglu",
-           "apply_int_rope"]
+           "apply_int_rope", "di_linear", "di_matmul"]

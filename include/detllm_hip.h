@@ -85,6 +85,12 @@ int detllm_residual_normq(const int32_t* P, int nsplit, int64_t split_stride, in
                           const int64_t* sm_m, int64_t sm_k, int8_t* x8, int64_t* xm,
                           int64_t* xk, hipStream_t s);
 
+/* IntQwen3._norm_quant — model.py:187-198: di_rmsnorm(h) (ops/di_rmsnorm.py:33-52),
+ * optional smoothing multiply by sm_m (null: none) with k 20 + sm_k, then
+ * quant_i8_pertoken (dyadic.py:93-105). h [R][C] int32 is only read. */
+int detllm_norm_quant(const int32_t* h, int R, int C, const int64_t* sm_m, int64_t sm_k,
+                      int8_t* x8, int64_t* xm, int64_t* xk, hipStream_t s);
+
 /* gate/up requant_i32_common(14) x2 + di_swiglu + quant_i8_pertoken(y*ds_m)
  * — model.py:416-423 (ops/di_swiglu.py:39-58). P: [nsplit][R][2I] with gate
  * in columns [0, I) and up in [I, 2I). */

@@ -254,3 +254,18 @@ def test_config0_gemm_requant():
     y8, mo, ko = dd.requant_i8_rowcol(P, 1, 0, g(m), 20)
     wy, wm, wk = ody.requant_i8_rowcol(Pw, np.ones((64, 1), I64), np.zeros((64, 1), I64), m, 20)
     eq(y8, wy); eq(mo, wm); eq(ko, wk)
+
+
+def test_di_matmul_composition():
+    """ops/di_matmul.py:34-40 (quant_i8_pertoken -> int_gemm ->
+    requant_i8_rowcol) on the device equals the oracle's composition."""
+    from idempotent_llm_amd import ops as dops
+    rnd = np.random.default_rng(21)
+    x = rnd.integers(-(1 << 30), 1 << 30, (37, 256)).astype(I64)
+    xm = rnd.integers(1 << 15, 1 << 16, (37, 1)).astype(I64)
+    xk = rnd.integers(20, 40, (37, 1)).astype(I64)
+    w = rnd.integers(-127, 128, (256, 96)).astype(np.int8)
+    wm = rnd.integers(1 << 14, 1 << 16, (96,)).astype(I64)
+    y8, m, k = dops.di_matmul(g(x), g(xm), g(xk), g(w), g(wm), 24)
+    oy, om, ok = oops.di_matmul(x, xm, xk, w, wm, 24)
+    eq(y8, oy); eq(m, om); eq(k, ok)
