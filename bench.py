@@ -111,12 +111,11 @@ def _graph_time_us(fn, reps: int, launches: int) -> float:
     return 1e3 * e0.elapsed_time(e1) / (reps * launches)
 
 
-def gemv_roofline(model, B: int):
+def decode_gemv_jobs(model, B: int):
     """The decode step's skinny GEMMs (q|k|v, o, gate|up, down per layer and
-    the LM head) with the model's own weights and K splits: algorithmic bytes
-    per launch / average launch duration."""
+    the LM head) with the model's own weights and K splits, on random int8
+    activations: [(x, w, out, ksplit)], and their algorithmic bytes."""
     import torch
-    from idempotent_llm_amd.backends import gemm_nt
     dev = "cuda"
     H, I_ = model.hidden, model.inter
     nqd = model.n_q * model.hd
@@ -132,6 +131,25 @@ def gemv_roofline(model, B: int):
     N, K = model.head_w.shape
     jobs.append((x_h, model.head_w, torch.empty(1, B, N, dtype=torch.int32, device=dev), 1))
     nbytes = sum(w.numel() + x.numel() + 4 * B * w.shape[0] for x, w, _, _ in jobs)
+    return jobs, nbytes
+
+
+def _traffic():
+    """HBM bytes per k_gemv_nt launch measured by rocprofv3 FETCH_SIZE and
+    WRITE_SIZE passes over `bench.py --kernel-probe` (profiles/), or None."""
+    path = os.path.join(ROOT, "profiles", "gemv_traffic.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        rec = json.load(f)
+    return rec.get("bytes_per_launch")
+
+
+def gemv_roofline(model, B: int):
+    """Algorithmic bytes per launch / average launch duration of the decode
+    step's skinny GEMMs, timed over a graph of the step's launches."""
+    from idempotent_llm_amd.backends import gemm_nt
+    jobs, nbytes = decode_gemv_jobs(model, B)
 
     def run():
         for x, w, out, ks in jobs:
@@ -141,9 +159,117 @@ def gemv_roofline(model, B: int):
     per_launch = nbytes / len(jobs)
     achieved = per_launch / (us * 1e-6) / 1e9
     return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
-            "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-            "kernel": "k_gemv_nt<1>", "batch": B, "launches_per_step": len(jobs),
+            "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": _traffic(),
+            "kernel": "k_gemv_nt<1,4,2>", "batch": B, "launches_per_step": len(jobs),
             "bytes_per_launch": int(per_launch), "avg_launch_us": round(us, 3)}
+
+
+def kernel_probe(model, B: int, reps: int = 3):
+    """Eager launches for counter passes (rocprofv3 --pmc): a plain device copy
+    of known size (the calibration of FETCH_SIZE / WRITE_SIZE), then the decode
+    step's skinny GEMMs."""
+    import torch
+    from idempotent_llm_amd.backends import gemm_nt
+    n = 256 << 20
+    src = torch.empty(n, dtype=torch.int8, device="cuda").fill_(1)
+    dst = torch.empty_like(src)
+    jobs, nbytes = decode_gemv_jobs(model, B)
+    for _ in range(reps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    for _ in range(reps):
+        for x, w, out, ks in jobs:
+            gemm_nt(x, w, out=out, ksplit=ks)
+    torch.cuda.synchronize()
+    log(f"kernel probe: copy {n} B x {reps}, {len(jobs)} GEMV launches x {reps} "
+        f"({nbytes / len(jobs):.0f} algorithmic B per launch)")
+
+
+def c4_decode_bench(model, steps: int = 128, warmup: int = 10):
+    """Config c4's batch: 32 prompts of seeded lengths in [16, 1024],
+    right-padded, prefill, then graphed decode; tok/s = 32 * steps / s."""
+    import torch
+    from idempotent_llm_amd import artifact as art
+    from idempotent_llm_amd.graphed import GraphedDecode
+    lens = art.uniform_int(4, "c4.lens", (32,), 16, 1025)
+    prompts = [art.uniform_int(4, f"c4.prompt.{i}", (int(n),), 100, 50000)
+               for i, n in enumerate(lens)]
+    ids, valid = art.right_pad(prompts)
+    B, T = ids.shape
+    ids = torch.from_numpy(ids).cuda()
+    valid = torch.from_numpy(valid).cuda()
+    pos = torch.arange(T, device="cuda").expand(B, T)
+    vlens = valid.sum(dim=1)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    logits, _, _, cache = model._forward(ids, pos, None, valid, (vlens - 1).clamp(min=0))
+    torch.cuda.synchronize()
+    t_pre = time.perf_counter() - t0
+    gd = GraphedDecode(model, cache, vlens)
+    cur = model.greedy_pick(logits)
+    for _ in range(warmup):
+        cur = model.greedy_pick(gd.step(cur))
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        cur = model.greedy_pick(gd.step(cur))
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    return {"batch": B, "prompt_tokens": int(lens.sum()), "padded_len": T,
+            "prefill_s": round(t_pre, 4), "decode_tok_s": round(B * steps / dt, 1),
+            "ms_per_step": round(1e3 * dt / steps, 4),
+            "slots": [T + warmup, T + warmup + steps]}
+
+
+def c1_c2_bench():
+    """Config c1 (MLP block on 2048 tokens: norm-quant, gate|up GEMM, SwiGLU +
+    quant, down GEMM, residual requant) and c2 (GQA attention prefill, 2048
+    tokens, 16 q heads) device times with HIP events over graph replays."""
+    import torch
+    from idempotent_llm_amd import artifact as art
+    from idempotent_llm_amd._lib import call
+    from idempotent_llm_amd.backends import gemm_nt
+    T, H, I = 2048, 1024, 3072
+    dev = "cuda"
+    h = torch.from_numpy(art.gauss_int(1, "c1.h", (T, H), 1 << 12).astype("int32")).to(dev)
+    k_res = torch.full((T,), 24, dtype=torch.int64, device=dev)
+    wgu = torch.randint(-127, 128, (2 * I, H), dtype=torch.int8, device=dev)
+    wd = torch.randint(-127, 128, (H, I), dtype=torch.int8, device=dev)
+    gm = torch.randint(1 << 14, 1 << 15, (I,), dtype=torch.int64, device=dev)
+    dm = torch.randint(1 << 14, 1 << 15, (H,), dtype=torch.int64, device=dev)
+    ones_h = torch.ones(H, dtype=torch.int64, device=dev)
+    ones_i = torch.ones(I, dtype=torch.int64, device=dev)
+    x8 = torch.empty(T, H, dtype=torch.int8, device=dev)
+    y8 = torch.empty(T, I, dtype=torch.int8, device=dev)
+    xm, xk, ym, yk = (torch.empty(T, dtype=torch.int64, device=dev) for _ in range(4))
+    P1 = torch.empty(1, T, 2 * I, dtype=torch.int32, device=dev)
+    P2 = torch.empty(1, T, H, dtype=torch.int32, device=dev)
+    h_work = h.clone()
+
+    def mlp():
+        call("detllm_norm_quant", h, T, H, ones_h, 0, x8, xm, xk)
+        gemm_nt(x8, wgu, out=P1)
+        call("detllm_swiglu_quant", P1, 1, 0, T, I, xm, xk, gm, 20, gm, 20, ones_i, 0, y8, ym, yk)
+        gemm_nt(y8, wd, out=P2)
+        call("detllm_residual_normq", P2, 1, 0, T, H, ym, yk, dm, 20, 20, h_work, k_res, None, 0,
+             None, None, None)
+
+    us1 = _graph_time_us(mlp, 10, 1)
+    ops1 = 2.0 * T * H * I * 3
+    # c2: one prefill attention launch over a 2048-slot cache
+    q8 = torch.randint(-127, 128, (1, 16, T, 128), dtype=torch.int8, device=dev)
+    tpos = torch.full((1, 16, T), 1 << 12, dtype=torch.int64, device=dev)
+    kc = torch.randint(-127, 128, (1, 8, T, 128), dtype=torch.int8, device=dev)
+    vc = torch.randint(-127, 128, (1, 8, 128, T), dtype=torch.int8, device=dev)
+    valid = torch.ones(1, T, dtype=torch.uint8, device=dev)
+    out = torch.empty(1, T, 16 * 128, dtype=torch.int64, device=dev)
+    us2 = _graph_time_us(lambda: call("detllm_attn_prefill", q8, tpos, kc, vc, valid, T, 1, T,
+                                      0, 16, 8, T, out), 10, 1)
+    ops2 = 2.0 * 2 * 16 * (T * (T + 1) // 2) * 128
+    return ({"us": round(us1, 2), "gemm_tops": round(ops1 / (us1 * 1e-6) / 1e12, 1),
+             "tokens_per_s": round(T / (us1 * 1e-6), 1)},
+            {"us": round(us2, 2), "tops": round(ops2 / (us2 * 1e-6) / 1e12, 1),
+             "algorithmic_ops": int(ops2)})
 
 
 def gemm_tops(T: int = PREFILL_LEN):
@@ -208,6 +334,9 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-extras", action="store_true",
                     help="decode only (no prefill/GEMM/roofline legs)")
+    ap.add_argument("--kernel-probe", action="store_true",
+                    help="only launch a known-size copy and the decode GEMVs eagerly "
+                         "(for rocprofv3 --pmc counter passes), then exit")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}): the integer "
@@ -226,6 +355,9 @@ def main():
         model = IntQwen3(d, backend="rocm")
         log("model loaded")
         B = args.batch
+        if args.kernel_probe:
+            kernel_probe(model, B)
+            return
         tps, ms, toks = decode_bench(model, B, args.steps, args.warmup)
         log(f"decode b{B}: {tps:.1f} tok/s ({ms:.3f} ms/step)")
         tps1, ms1, toks1 = decode_bench(model, 1, args.steps, args.warmup)
@@ -240,6 +372,12 @@ def main():
             log(f"gemm: {extras['int8_gemm_prefill']['all']}")
             roof = gemv_roofline(model, B)
             log(f"roofline: {roof}")
+            extras["c4_batch32"] = c4_decode_bench(model)
+            log(f"c4: {extras['c4_batch32']}")
+            c1, c2 = c1_c2_bench()
+            extras["c1_mlp_block_2048"] = c1
+            extras["c2_attention_prefill_2048"] = c2
+            log(f"c1: {c1} c2: {c2}")
         del model
         torch.cuda.empty_cache()
         cpu = None
