@@ -76,7 +76,7 @@ __global__ __launch_bounds__(256) void k_attn_prefill(PrefillArgs a) {
     qf1 = *(const v4i*)(a.q8 + qrow * 128 + 64 + g * 16);
   }
   const i64 tpos = tok ? a.tpos[qrow] : 1;
-  const Recip Rt = make_recip(tpos);
+  const ExpR Et = make_exp(tpos);
   const i64 limit = (i64)a.S_past + t;  // last visible slot of this query
   const int kend = min(a.S, a.S_past + qt * 64 + 64);
   const int ntiles = (kend + 63) / 64;
@@ -84,27 +84,63 @@ __global__ __launch_bounds__(256) void k_attn_prefill(PrefillArgs a) {
   const int8_t* vbase = a.vc + ((i64)b * a.n_kv + kvh) * 128 * a.cap;
   const uint8_t* vrow = a.valid + (i64)b * a.valid_stride;
 
-  auto load_k = [&](int s0) {
+  // Tiles of 64 slots move global -> registers -> LDS; the next tile's loads
+  // are issued before the current tile's MFMAs and DI-Exp work, so their
+  // latency overlaps the compute.
+  v4i kreg[2], vreg[2];
+  int freg = 0;
+  auto gload_k = [&](int s0) {
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       const int c = tid + i * 256;
       const int key = c >> 3, dc = (c & 7) * 16;
-      v4i v = v4i{0, 0, 0, 0};
-      if (s0 + key < a.S) v = *(const v4i*)(kbase + (i64)(s0 + key) * 128 + dc);
-      *(v4i*)&Ks[key * KS_STRIDE + dc] = v;
+      kreg[i] = v4i{0, 0, 0, 0};
+      if (s0 + key < a.S) kreg[i] = *(const v4i*)(kbase + (i64)(s0 + key) * 128 + dc);
     }
-    if (tid < 64) vflag[tid] = (s0 + tid < a.S) ? vrow[s0 + tid] : 0;
+    if (tid < 64) freg = (s0 + tid < a.S) ? vrow[s0 + tid] : 0;
   };
-  auto load_v = [&](int s0) {
+  auto sstore_k = [&]() {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int c = tid + i * 256;
+      const int key = c >> 3, dc = (c & 7) * 16;
+      *(v4i*)&Ks[key * KS_STRIDE + dc] = kreg[i];
+    }
+    if (tid < 64) vflag[tid] = (uint8_t)freg;
+  };
+  auto gload_v = [&](int s0) {
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       const int c = tid + i * 256;
       const int d = c >> 2, blk = c & 3;
-      v4i v = v4i{0, 0, 0, 0};
-      if (s0 + blk * 16 < a.cap) v = *(const v4i*)(vbase + (i64)d * a.cap + s0 + blk * 16);
+      vreg[i] = v4i{0, 0, 0, 0};
+      if (s0 + blk * 16 < a.cap) vreg[i] = *(const v4i*)(vbase + (i64)d * a.cap + s0 + blk * 16);
+    }
+  };
+  auto sstore_v = [&]() {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int c = tid + i * 256;
+      const int d = c >> 2, blk = c & 3;
       // slot 16*blk + 4*gg + r -> position 16*gg + 4*blk + r
 #pragma unroll
-      for (int gg = 0; gg < 4; ++gg) *(int*)&Vs[d * VS_STRIDE + 16 * gg + 4 * blk] = v[gg];
+      for (int gg = 0; gg < 4; ++gg) *(int*)&Vs[d * VS_STRIDE + 16 * gg + 4 * blk] = vreg[i][gg];
+    }
+  };
+  // one pass over the key tiles: body(s0) runs with tile s0 in LDS
+  auto pass = [&](bool with_v, auto&& body) {
+    gload_k(0);
+    if (with_v) gload_v(0);
+    for (int it = 0; it < ntiles; ++it) {
+      __syncthreads();
+      sstore_k();
+      if (with_v) sstore_v();
+      __syncthreads();
+      if (it + 1 < ntiles) {
+        gload_k((it + 1) * 64);
+        if (with_v) gload_v((it + 1) * 64);
+      }
+      body(it * 64);
     }
   };
   // S^T for 4 blocks of 16 slots: st[blk][r] = score(slot s0+16blk+4g+r, query t)
@@ -127,11 +163,7 @@ __global__ __launch_bounds__(256) void k_attn_prefill(PrefillArgs a) {
 
   // ---- pass 1: row max over visible slots
   i64 mx = NEG_SENTINEL;
-  for (int it = 0; it < ntiles; ++it) {
-    const int s0 = it * 64;
-    __syncthreads();
-    load_k(s0);
-    __syncthreads();
+  pass(false, [&](int s0) {
     v4i st[4];
     scores(st);
 #pragma unroll
@@ -139,25 +171,21 @@ __global__ __launch_bounds__(256) void k_attn_prefill(PrefillArgs a) {
 #pragma unroll
       for (int r = 0; r < 4; ++r)
         if (visible(s0, blk, r)) mx = imax(mx, (i64)st[blk][r]);
-  }
+  });
   mx = group4_max(mx);
   if (mx == NEG_SENTINEL) mx = 0;  // no visible slot: max := 0, every p = 0
 
   // ---- pass 2: denominator
   i64 den = 0;
-  for (int it = 0; it < ntiles; ++it) {
-    const int s0 = it * 64;
-    __syncthreads();
-    load_k(s0);
-    __syncthreads();
+  pass(false, [&](int s0) {
     v4i st[4];
     scores(st);
 #pragma unroll
     for (int blk = 0; blk < 4; ++blk)
 #pragma unroll
       for (int r = 0; r < 4; ++r)
-        if (visible(s0, blk, r)) den = wadd(den, di_exp_r(wsub((i64)st[blk][r], mx), tpos, Rt));
-  }
+        if (visible(s0, blk, r)) den = wadd(den, di_exp_neg((u64)wsub(mx, (i64)st[blk][r]), Et));
+  });
   den = imax(group4_sum(den), 1);
   const Recip Rd = make_recip(den);
 
@@ -170,12 +198,7 @@ __global__ __launch_bounds__(256) void k_attn_prefill(PrefillArgs a) {
     olo[j] = v4i{0, 0, 0, 0};
     csum[j] = 0;
   }
-  for (int it = 0; it < ntiles; ++it) {
-    const int s0 = it * 64;
-    __syncthreads();
-    load_k(s0);
-    load_v(s0);
-    __syncthreads();
+  pass(true, [&](int s0) {
     v4i st[4];
     scores(st);
     v4i phi, plo;
@@ -186,7 +209,7 @@ __global__ __launch_bounds__(256) void k_attn_prefill(PrefillArgs a) {
       for (int r = 0; r < 4; ++r) {
         i64 p = 0;
         if (visible(s0, blk, r)) {
-          const i64 ex = di_exp_r(wsub((i64)st[blk][r], mx), tpos, Rt);
+          const i64 ex = di_exp_neg((u64)wsub(mx, (i64)st[blk][r]), Et);
           p = to_i32(rhad_r(shl(ex, 14), Rd));
         }
         const int hi = (int)(p >> 7);
@@ -207,7 +230,7 @@ __global__ __launch_bounds__(256) void k_attn_prefill(PrefillArgs a) {
       for (int q = 0; q < 4; ++q) cs = __builtin_amdgcn_sdot4(vb[q], 0x01010101, cs, false);
       csum[j] = cs;
     }
-  }
+  });
   // write: lane holds O[query 4g + r][d = 16j + qi]
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
@@ -325,11 +348,11 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, int kvh, int b,
   i64 den[G];
 #pragma unroll
   for (int hh = 0; hh < G; ++hh) {
-    const Recip R = make_recip(tp[hh]);
+    const ExpR E = make_exp(tp[hh]);
     i64 acc = 0;
     for (int s = tid; s < S; s += 256) {
       const int32_t x = sc[hh * Spad + s];
-      if (x != SCORE_MASKED) acc = wadd(acc, di_exp_r(wsub((i64)x, mx[hh]), tp[hh], R));
+      if (x != SCORE_MASKED) acc = wadd(acc, di_exp_neg((u64)wsub(mx[hh], (i64)x), E));
     }
     den[hh] = imax(red.sum(acc), 1);
   }
@@ -337,14 +360,14 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, int kvh, int b,
   // masked slots and the padding up to the next multiple of 16)
 #pragma unroll
   for (int hh = 0; hh < G; ++hh) {
-    const Recip R = make_recip(tp[hh]);
+    const ExpR E = make_exp(tp[hh]);
     const Recip Rd = make_recip(den[hh]);
     for (int s = tid; s < nchunk * 16; s += 256) {
       i64 p = 0;
       if (s < S) {
         const int32_t x = sc[hh * Spad + s];
         if (x != SCORE_MASKED) {
-          const i64 ex = di_exp_r(wsub((i64)x, mx[hh]), tp[hh], R);
+          const i64 ex = di_exp_neg((u64)wsub(mx[hh], (i64)x), E);
           p = to_i32(rhad_r(shl(ex, 14), Rd));
         }
       }

@@ -251,6 +251,77 @@ DI_HD i64 di_exp_r(i64 x, i64 tpos, const Recip& R) {
   return shr(unshifted, q > 62 ? 62 : (i64)q);
 }
 
+DI_HD uint32_t mulhi32(uint32_t a, uint32_t b) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  return __umulhi(a, b);
+#else
+  return (uint32_t)(((u64)a * b) >> 32);
+#endif
+}
+
+// DI-Exp with a row-invariant constant tpos, for non-positive arguments x =
+// -neg (every argument on the model path: x = score - row max, or -|gate|).
+// When tpos < 2^31 and neg < 2^32 the whole computation fits 32 bits: q =
+// floor(neg / tpos) from the 32-bit reciprocal r = floor((2^32 - 1) / tpos)
+// (mulhi32(neg, r) is floor(neg / tpos) or one less, by the argument given for
+// the 64-bit reciprocal above, with 2^32 for 2^64), rem = neg - q tpos <
+// tpos, unshifted = tpos - ((rem + 1) >> 1) in [tpos / 2, tpos], and the
+// result unshifted >> min(q, 62) is 0 once q >= 31. Otherwise the 64-bit form
+// runs. Bit-identical to di_exp_r(-neg, tpos, R).
+struct ExpR {
+  i64 tpos;
+  Recip R;
+  uint32_t t32, r32;
+  bool fast;
+};
+
+DI_HD ExpR make_exp(i64 tpos) {  // tpos >= 1
+  ExpR E;
+  E.tpos = tpos;
+  E.R = make_recip(tpos);
+  E.fast = tpos < ((i64)1 << 31);
+  E.t32 = (uint32_t)tpos;
+  E.r32 = E.fast ? 0xFFFFFFFFu / E.t32 : 0u;
+  return E;
+}
+
+DI_HD i64 di_exp_neg(u64 neg, const ExpR& E) {
+  if (E.fast && neg <= 0xFFFFFFFFull) {
+    const uint32_t n = (uint32_t)neg;
+    uint32_t q = mulhi32(n, E.r32);
+    uint32_t rem = n - q * E.t32;
+    if (rem >= E.t32) {
+      q += 1;
+      rem -= E.t32;
+    }
+    const uint32_t unshifted = E.t32 - ((rem + 1) >> 1);
+    return q >= 31 ? 0 : (i64)(unshifted >> q);
+  }
+  return di_exp_r(wneg((i64)neg), E.tpos, E.R);
+}
+
+// round_half_away_div(num << 7, den) for 0 <= num <= den < 2^31, in 32 bits:
+// one step for the integer bit, seven doubling steps (t < den < 2^31, so 2t
+// fits), then the half-divisor rounding term. Same integer as sigmoid_div.
+DI_HD i64 sigmoid_div32(uint32_t num, uint32_t den) {
+  uint32_t t = num, q = 0;
+  if (t >= den) {
+    t -= den;
+    q = 1;
+  }
+#pragma unroll
+  for (int b = 0; b < 7; ++b) {
+    t <<= 1;
+    q <<= 1;
+    if (t >= den) {
+      t -= den;
+      q |= 1;
+    }
+  }
+  if (t + (den >> 1) >= den) q += 1;
+  return (i64)q;
+}
+
 // round_half_away_div(num << 7, den) for 0 <= num <= den, den >= 1: the
 // quotient is at most 128, so 8 restoring steps are exact. Larger operands
 // (never produced on the model path) take the generic form.
@@ -279,6 +350,21 @@ DI_HD i64 swiglu_elem(i64 g, i64 u, i64 tpos, const Recip& R) {
   const i64 num = g >= 0 ? tpos : E;
   const i64 sig = sigmoid_div(num, den);
   return wmul(wmul(g, sig), u);
+}
+
+// swiglu_elem with the row's DI-Exp context: 32-bit DI-Exp and sigmoid
+// division when tpos < 2^30 (then E <= tpos and den = tpos + E < 2^31) and g
+// is an int32 value; otherwise the 64-bit form. Same integer.
+DI_HD i64 swiglu_elem_e(i64 g, i64 u, const ExpR& E) {
+  if (E.tpos < ((i64)1 << 30) && g >= INT32_MIN && g <= INT32_MAX) {
+    const u64 mag = (u64)(g < 0 ? -g : g);
+    const i64 e = di_exp_neg(mag, E);
+    const uint32_t den = (uint32_t)imax(E.tpos + e, 1);
+    const uint32_t num = (uint32_t)(g >= 0 ? E.tpos : e);
+    const i64 sig = sigmoid_div32(num, den);
+    return wmul((i64)(int32_t)g * sig, u);
+  }
+  return swiglu_elem(g, u, E.tpos, E.R);
 }
 
 }  // namespace di

@@ -44,6 +44,16 @@ void di_host_scalar(int op, const int64_t* a, const int64_t* b, const int64_t* c
     }
   }
 }
+void di_host_di_exp_neg(const int64_t* neg, const int64_t* tpos, int64_t n, int64_t* out) {
+  for (int64_t i = 0; i < n; ++i) out[i] = di_exp_neg((u64)neg[i], make_exp(tpos[i]));
+}
+void di_host_swiglu_e(const int64_t* g, const int64_t* u, const int64_t* tpos, int64_t n,
+                      int64_t* out) {
+  for (int64_t i = 0; i < n; ++i) out[i] = swiglu_elem_e(g[i], u[i], make_exp(tpos[i]));
+}
+void di_host_sigmoid_div32(const int64_t* num, const int64_t* den, int64_t n, int64_t* out) {
+  for (int64_t i = 0; i < n; ++i) out[i] = sigmoid_div32((uint32_t)num[i], (uint32_t)den[i]);
+}
 void di_host_rshift_round(const int64_t* a, const int64_t* k, int64_t n, int64_t* out) {
   for (int64_t i = 0; i < n; ++i) out[i] = rshift_round(a[i], k[i]);
 }

@@ -318,10 +318,9 @@ __global__ __launch_bounds__(RT_WIDE) void k_swiglu_quant(SwigluArgs a) {
   load_rows_i32_sum<2, VPT>(gu, a.P, a.nsplit, a.split_stride, offs, I);
   const i64 gk = requant_common_row(gu[0], gm, xk, a.gate_k, 14, red);
   const i64 uk = requant_common_row(gu[1], um, xk, a.up_k, 14, red);
-  const i64 tpos = di_exp_tpos(xm, gk);
-  const Recip R = make_recip(tpos);
+  const ExpR E = make_exp(di_exp_tpos(xm, gk));
 #pragma unroll
-  for (int j = 0; j < VPT; ++j) gu[0][j] = wmul(swiglu_elem(gu[0][j], gu[1][j], tpos, R), dsm[j]);
+  for (int j = 0; j < VPT; ++j) gu[0][j] = wmul(swiglu_elem_e(gu[0][j], gu[1][j], E), dsm[j]);
   const i64 ym = wmul(xm, xm);
   const i64 yk = wadd(wadd(wadd(gk, uk), 7), a.ds_k);
   quant_row(gu[0], ym, yk, I, red, a.y8 + (i64)r * I, a.ym + r, a.yk + r);
@@ -555,8 +554,7 @@ __global__ __launch_bounds__(RT) void k_op_softmax(const int64_t* x, const int64
   const i64 any = red.max(anyv ? 1 : 0);
   if (!any) mx = 0;
   const i64 mm = m[r], kk = k[r];
-  const i64 tpos = di_exp_tpos(mm, kk);
-  const Recip Rt = make_recip(tpos);
+  const ExpR Et = make_exp(di_exp_tpos(mm, kk));
   i64 cint = 0;
   if (has_clip) cint = rhad(wmul(clip_c, shl(1, kk)), mm);
   i64 den = 0;
@@ -564,7 +562,9 @@ __global__ __launch_bounds__(RT) void k_op_softmax(const int64_t* x, const int64
   for (int j = 0; j < VPT; ++j) {
     i64 xd = ok[j] ? wsub(v[j], mx) : 0;
     if (has_clip) xd = imax(xd, wneg(cint));
-    const i64 e = ok[j] ? di_exp_r(xd, tpos, Rt) : 0;
+    // xd <= 0 for every visible slot (x <= row max, clip only raises it)
+    const i64 e = !ok[j] ? 0 : (xd <= 0 ? di_exp_neg((u64)wneg(xd), Et)
+                                        : di_exp_r(xd, Et.tpos, Et.R));
     v[j] = e;
     den = wadd(den, e);
   }
@@ -583,10 +583,9 @@ __global__ void k_op_di_exp(const int64_t* x, const int64_t* m, const int64_t* k
   for (i64 i = blockIdx.x * (i64)blockDim.x + threadIdx.x; i < n;
        i += (i64)gridDim.x * blockDim.x) {
     const i64 r = i / C;
-    const i64 tpos = di_exp_tpos(m[r], k[r]);
-    const Recip R = make_recip(tpos);
-    res[i] = di_exp_r(x[i], tpos, R);
-    if (i % C == 0) tpos_out[r] = tpos;
+    const ExpR E = make_exp(di_exp_tpos(m[r], k[r]));
+    res[i] = x[i] <= 0 ? di_exp_neg((u64)wneg(x[i]), E) : di_exp_r(x[i], E.tpos, E.R);
+    if (i % C == 0) tpos_out[r] = E.tpos;
   }
 }
 
@@ -596,9 +595,7 @@ __global__ void k_op_swiglu(const int64_t* gate, const int64_t* gm, const int64_
   for (i64 i = blockIdx.x * (i64)blockDim.x + threadIdx.x; i < n;
        i += (i64)gridDim.x * blockDim.x) {
     const i64 r = i / C;
-    const i64 tpos = di_exp_tpos(gm[r], gk[r]);
-    const Recip R = make_recip(tpos);
-    y[i] = swiglu_elem(gate[i], up[i], tpos, R);
+    y[i] = swiglu_elem_e(gate[i], up[i], make_exp(di_exp_tpos(gm[r], gk[r])));
     if (i % C == 0) {
       ym[r] = wmul(gm[r], um[r]);
       yk[r] = wadd(wadd(gk[r], uk[r]), 7);

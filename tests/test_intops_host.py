@@ -212,3 +212,62 @@ def test_rhad_pow2_matches_rhad(lib):
         got, _ = _scalar(lib, 6, a, np.full_like(a, k))
         want = _call2(lib, "di_host_rhad", a, np.full_like(a, 1 << k))
         assert np.array_equal(got, want), k
+
+
+def _call2_3(lib, name, a, b, c=None):
+    a = np.ascontiguousarray(a, I64)
+    b = np.ascontiguousarray(b, I64)
+    out = np.empty_like(a)
+    if c is None:
+        getattr(lib, name)(_p(a), _p(b), ctypes.c_int64(a.size), _p(out))
+    else:
+        c = np.ascontiguousarray(c, I64)
+        getattr(lib, name)(_p(a), _p(b), _p(c), ctypes.c_int64(a.size), _p(out))
+    return out
+
+
+def test_di_exp_neg_32bit_path_matches_generic(lib):
+    """The 32-bit DI-Exp (tpos < 2^31, neg < 2^32) equals the 64-bit form
+    di_exp_r(-neg) for tpos on both sides of 2^31, neg near multiples of tpos
+    and across the 2^32 boundary."""
+    rnd = np.random.default_rng(31)
+    tp = np.concatenate([np.arange(1, 300, dtype=I64),
+                         rnd.integers(1, 1 << 31, 3000, dtype=I64),
+                         np.array([(1 << 31) - 1, 1 << 31, (1 << 31) + 1, 1 << 40], I64)])
+    tpos = np.repeat(tp, 40)
+    k = rnd.integers(0, 70, tpos.size)
+    jitter = rnd.integers(-2, 3, tpos.size)
+    neg = np.clip(tpos * k + jitter, 0, None).astype(I64)
+    neg[::7] = rnd.integers(0, 1 << 33, neg[::7].size)
+    neg[::11] = (1 << 32) - 1 - rnd.integers(0, 3, neg[::11].size)
+    got = _call2_3(lib, "di_host_di_exp_neg", neg, tpos)
+    want = _call2_3(lib, "di_host_di_exp", -neg, tpos)
+    assert np.array_equal(got, want)   # di_host_di_exp is pinned to the oracle above
+
+
+def test_sigmoid_div32_matches_64bit(lib):
+    rnd = np.random.default_rng(32)
+    den = np.concatenate([rnd.integers(1, 1 << 31, 50000, dtype=I64),
+                          np.array([1, 2, 3, 127, 128, 255, (1 << 31) - 1], I64)])
+    num = (rnd.random(den.size) * (den + 1)).astype(I64)
+    num = np.minimum(num, den)
+    num[::5] = den[::5]
+    num[::9] = 0
+    got = _call2_3(lib, "di_host_sigmoid_div32", num, den)
+    want = _call2_3(lib, "di_host_sigmoid_div", num, den)
+    assert np.array_equal(got, want)
+    py = [((int(a) << 7) + int(b) // 2) // int(b) for a, b in zip(num[:2000], den[:2000])]
+    assert got[:2000].tolist() == py
+
+
+def test_swiglu_elem_fast_path_matches_generic(lib):
+    rnd = np.random.default_rng(33)
+    n = 60000
+    g = np.concatenate([rnd.integers(-(1 << 15), 1 << 15, n // 2),
+                        rnd.integers(-(1 << 31), 1 << 31, n // 2)]).astype(I64)
+    u = rnd.integers(-(1 << 15), 1 << 15, n).astype(I64)
+    tpos = np.concatenate([rnd.integers(1, 1 << 20, n // 3), rnd.integers(1, 1 << 30, n // 3),
+                           rnd.integers(1 << 29, 1 << 33, n - 2 * (n // 3))]).astype(I64)
+    got = _call2_3(lib, "di_host_swiglu_e", g, u, tpos)
+    want = _call2_3(lib, "di_host_swiglu", g, u, tpos)
+    assert np.array_equal(got, want)
