@@ -173,18 +173,20 @@ __device__ __forceinline__ void g2_tile(int bid, int tiles_m, int tiles_n, int& 
 
 constexpr int G2_BK = 128;
 
-template <int BM, int BN, int S, int MINB>
-__global__ __launch_bounds__(256, MINB) void k_gemm_nt2(const int8_t* __restrict__ A,
+template <int BM, int BN, int S, int WGM, int WGN, int MINB>
+__global__ __launch_bounds__(64 * WGM * WGN, MINB) void k_gemm_nt2(const int8_t* __restrict__ A,
                                                         const int8_t* __restrict__ B,
                                                         int32_t* __restrict__ C, int M, int N,
                                                         int K, i64 sA, i64 sB, i64 sC,
                                                         int tiles_m, int tiles_n) {
   constexpr int ROWS = BM + BN;       // 128-byte rows per slice: A rows, then B rows
+  constexpr int NW = WGM * WGN;       // waves, WGM x WGN over the tile
   constexpr int NI = ROWS / 8;        // load instructions per slice (8 rows each)
-  static_assert(NI % 4 == 0, "loads per wave");
-  constexpr int LPW = NI / 4;
+  static_assert(NI % NW == 0, "loads per wave");
+  constexpr int LPW = NI / NW;
   constexpr int STAGE = ROWS * G2_BK;
-  constexpr int WA = BM / 64, WB = BN / 64;  // 32x32 blocks per wave (2 x 2 waves)
+  constexpr int WA = BM / 32 / WGM, WB = BN / 32 / WGN;  // 32x32 blocks per wave
+  static_assert(WA >= 1 && WB >= 1, "wave tile");
   __shared__ __attribute__((aligned(1024))) int8_t lds[S * STAGE];
 
   const int bz = blockIdx.z;
@@ -194,7 +196,7 @@ __global__ __launch_bounds__(256, MINB) void k_gemm_nt2(const int8_t* __restrict
   int tm, tn;
   g2_tile(blockIdx.x, tiles_m, tiles_n, tm, tn);
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = wave / WGN, wn = wave % WGN;
 
   // this wave's loads: instruction i covers slice rows 8i..8i+7; lane l takes
   // row 8i + l/8 at physical chunk l%8, i.e. logical chunk (l%8) ^ swz(row)
@@ -240,7 +242,9 @@ __global__ __launch_bounds__(256, MINB) void k_gemm_nt2(const int8_t* __restrict
   for (int kt = 0; kt < nk; ++kt) {
     // slices issued after kt so far: min(S - 2, nk - 1 - kt)
     const int after = min(S - 2, nk - 1 - kt);
-    if (after >= 2) wait_vmcnt<2 * LPW>();
+    static_assert(S <= 5 && 3 * LPW < 64, "vmcnt range");
+    if (after >= 3) wait_vmcnt<3 * LPW>();
+    else if (after == 2) wait_vmcnt<2 * LPW>();
     else if (after == 1) wait_vmcnt<LPW>();
     else wait_vmcnt<0>();
     __builtin_amdgcn_s_barrier();
@@ -469,19 +473,20 @@ int detllm_igemm_nt(const int8_t* A, const int8_t* B, int32_t* C, int M, int N, 
   if (K <= 0 || (K % 16) != 0 || K > 131071 || !A || !B || !C) return DI_EINVAL;
   if (batch > 65535) return DI_ERANGE;
   if (M > 64 && K % G2_BK == 0) {
-    // 128x128 tiles (2 slices, 2 blocks per CU) while they give at least two
-    // tiles per CU; otherwise 128x64 tiles (3 slices) for more parallelism
+    // 128x128 tiles (4 waves, 2 slices, 2 blocks per CU) while they give at
+    // least two tiles per CU; otherwise 128x64 tiles for more parallelism,
+    // on 8 waves (4 x 2, one 32x32 block each) and a 4-slice ring
     const i64 t128 = (i64)((M + 127) / 128) * ((N + 127) / 128) * batch;
     const int tm = (M + 127) / 128;
     if (t128 >= 512) {
       const int tn = (N + 127) / 128;
       if ((i64)tm * tn > 0x7fffffff) return DI_ERANGE;
-      hipLaunchKernelGGL((k_gemm_nt2<128, 128, 2, 2>), dim3(tm * tn, 1, batch), dim3(256), 0, s,
+      hipLaunchKernelGGL((k_gemm_nt2<128, 128, 2, 2, 2, 2>), dim3(tm * tn, 1, batch), dim3(256), 0, s,
                          A, B, C, M, N, K, (i64)sA, (i64)sB, (i64)sC, tm, tn);
     } else {
       const int tn = (N + 63) / 64;
       if ((i64)tm * tn > 0x7fffffff) return DI_ERANGE;
-      hipLaunchKernelGGL((k_gemm_nt2<128, 64, 3, 2>), dim3(tm * tn, 1, batch), dim3(256), 0, s,
+      hipLaunchKernelGGL((k_gemm_nt2<128, 64, 4, 4, 2, 1>), dim3(tm * tn, 1, batch), dim3(512), 0, s,
                          A, B, C, M, N, K, (i64)sA, (i64)sB, (i64)sC, tm, tn);
     }
     DI_LAUNCH_CHECK();
