@@ -273,7 +273,10 @@ def c1_c2_bench():
 
 
 def gemm_tops(T: int = PREFILL_LEN):
-    """int8 GEMM TOP/s at the prefill shapes (T tokens): q|k|v, o, gate|up, down."""
+    """int8 GEMM TOP/s at the prefill shapes (T tokens): q|k|v, o, gate|up, down.
+    Beside each, the same product through torch._int_mm (hipBLASLt on ROCm, the
+    vendor library) on the same inputs, timed the same way, as a yardstick;
+    `equal` records that both give the same int32 matrix."""
     import torch
     from idempotent_llm_amd.backends import gemm_nt
     dev = "cuda"
@@ -294,6 +297,19 @@ def gemm_tops(T: int = PREFILL_LEN):
         tops = ops / (us * 1e-6) / 1e12
         res[name] = {"M": M, "N": N, "K": K, "us": round(us, 2), "tops": round(tops, 1),
                      "frac_peak": round(tops / I8_PEAK_TOPS, 4)}
+        wt = w.t()
+        try:
+            ref = torch._int_mm(a, wt)
+            def run_vendor(a=a, wt=wt):
+                for _ in range(20):
+                    torch._int_mm(a, wt)
+
+            vus = _graph_time_us(run_vendor, 10, 20)
+            res[name]["vendor_int_mm"] = {"us": round(vus, 2),
+                                          "tops": round(ops / (vus * 1e-6) / 1e12, 1),
+                                          "equal": bool(torch.equal(out[0], ref))}
+        except RuntimeError as e:   # no int8 GEMM in this torch build
+            res[name]["vendor_int_mm"] = {"error": str(e)[:120]}
         tot_ops += ops
         tot_us += us
     tops = tot_ops / (tot_us * 1e-6) / 1e12
@@ -337,6 +353,8 @@ def main():
     ap.add_argument("--kernel-probe", action="store_true",
                     help="only launch a known-size copy and the decode GEMVs eagerly "
                          "(for rocprofv3 --pmc counter passes), then exit")
+    ap.add_argument("--gemm-probe", action="store_true",
+                    help="only time the prefill-shape int8 GEMMs (no model), print them, exit")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}): the integer "
@@ -347,6 +365,9 @@ def main():
     from idempotent_llm_amd import artifact as art
     from idempotent_llm_amd.model import IntQwen3
     assert torch.cuda.is_available(), "bench.py needs a GPU"
+    if args.gemm_probe:
+        print(json.dumps(gemm_tops()), flush=True)
+        return
 
     with tempfile.TemporaryDirectory(prefix="detllm_bench_") as d:
         t0 = time.perf_counter()
