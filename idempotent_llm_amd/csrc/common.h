@@ -147,6 +147,49 @@ struct BlockRed {
   __device__ __forceinline__ i64 max(i64 v) { return reduce<true>(v); }
   __device__ __forceinline__ i64 sum(i64 v) { return reduce<false>(v); }
 
+  // Block maxima of one or two 32-bit unsigned values (one barrier). A row
+  // shift that depends only on the bit length of max |x| reduces bit lengths
+  // (bitlen_abs below) here instead of 64-bit magnitudes.
+  __device__ __forceinline__ uint32_t max_u32(uint32_t v) {
+    uint32_t b = 0;
+    max2_u32(v, b);
+    return v;
+  }
+  __device__ __forceinline__ void max2_u32(uint32_t& a, uint32_t& b) {
+    a = wave_max_u32(a);
+    b = wave_max_u32(b);
+    uint32_t* slot = (uint32_t*)(buf + (k & 1) * 16);
+    ++k;
+    if ((threadIdx.x & 63) == 63) {
+      slot[threadIdx.x >> 6] = a;
+      slot[16 + (threadIdx.x >> 6)] = b;
+    }
+    __syncthreads();
+    const int nw = blockDim.x >> 6;
+    uint32_t ra = 0, rb = 0;
+    for (int i = 0; i < nw; i += 4) {  // 4 reads in flight; entries past nw ignored
+      const uint32_t a0 = slot[i], a1 = slot[i + 1], a2 = slot[i + 2], a3 = slot[i + 3];
+      const uint32_t b0 = slot[16 + i], b1 = slot[17 + i], b2 = slot[18 + i], b3 = slot[19 + i];
+      ra = ::max(ra, ::max(::max(a0, i + 1 < nw ? a1 : 0u),
+                           ::max(i + 2 < nw ? a2 : 0u, i + 3 < nw ? a3 : 0u)));
+      rb = ::max(rb, ::max(::max(b0, i + 1 < nw ? b1 : 0u),
+                           ::max(i + 2 < nw ? b2 : 0u, i + 3 < nw ? b3 : 0u)));
+    }
+    a = ra;
+    b = rb;
+  }
+
+  // DPP maximum of a 32-bit unsigned value, result in lane 63 (no broadcast)
+  static __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+    v = ::max(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0xB1, 0xF, 0xF, false));
+    v = ::max(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x4E, 0xF, 0xF, false));
+    v = ::max(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x141, 0xF, 0xF, false));
+    v = ::max(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x140, 0xF, 0xF, false));
+    v = ::max(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x142, 0xA, 0xF, false));
+    v = ::max(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x143, 0xC, 0xF, false));
+    return v;
+  }
+
   // DPP reduction leaving the wave's result in lane 63 (no broadcast)
   template <bool MAX>
   static __device__ __forceinline__ i64 wave_part(i64 v) {
@@ -168,6 +211,18 @@ struct BlockRed {
     return v;
   }
 };
+
+// Bit length of |x| (0 for x == 0): ilog2(max(max_j |x_j|, 1)) is
+// max(max_j bitlen_abs(x_j) - 1, 0). |INT64_MIN| wraps to a negative int64,
+// as torch's abs does, and never wins a maximum of magnitudes (every amax
+// here is clamped to >= 1 first), so it counts as 0 too.
+__device__ __forceinline__ uint32_t bitlen_abs(i64 x) {
+  const i64 a = wabs(x);
+  return a > 0 ? 64u - (uint32_t)clz64((u64)a) : 0u;
+}
+
+// ilog2(max(m, 1)) from the bit length of m >= 0
+__device__ __forceinline__ i64 ilog2_from_bitlen(uint32_t len) { return len > 1 ? len - 1 : 0; }
 
 __device__ __forceinline__ i64 to_i32(i64 v) { return (i64)(int32_t)(uint32_t)(u64)v; }
 

@@ -50,10 +50,15 @@ struct QKVArgs {
   i64 slot_base;
 };
 
+// ilog2(max(max |x|, 1)) over the wave's 128 channels (two per lane)
+__device__ __forceinline__ i64 wave_ilog2_absmax(i64 a, i64 b) {
+  const uint32_t L = BlockRed::wave_max_u32(::max(bitlen_abs(a), bitlen_abs(b)));
+  return ilog2_from_bitlen((uint32_t)__builtin_amdgcn_readlane((int)L, 63));
+}
+
 __device__ __forceinline__ void wave_rmsnorm128(i64& a, i64& b) {
   // ops/di_rmsnorm.py:33-52 over 128 channels held two per lane
-  const i64 g = wave_max(imax(wabs(a), wabs(b)));
-  const i64 sh = 25 - ilog2(imax(g, 1));
+  const i64 sh = 25 - wave_ilog2_absmax(a, b);
   const i64 up = imax(sh, 0), down = imax(-sh, 0);
   a = shl(rshift_round(a, down), up);
   b = shl(rshift_round(b, down), up);
@@ -140,8 +145,7 @@ __device__ __forceinline__ void qkv_head(const QKVArgs& a, int r, int slotw, int
   // (m, k) it returns are dropped by _qk_head_pipeline
   i64 y0 = wmul(p0, wm0), y1 = wmul(p1, wm1);
   {
-    const i64 am = imax(wave_max(imax(wabs(y0), wabs(y1))), 1);
-    const i64 sh = imax(ilog2(am) - 15, 0);
+    const i64 sh = imax(wave_ilog2_absmax(y0, y1) - 15, 0);
     y0 = to_i32(rshift_round(y0, sh));
     y1 = to_i32(rshift_round(y1, sh));
   }

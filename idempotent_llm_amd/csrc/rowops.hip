@@ -43,11 +43,19 @@ __device__ __forceinline__ i64 row_absmax(const i64 (&v)[VPT], BlockRed& red) {
   return red.max(g);
 }
 
+// ilog2(max(max_j |v_j|, 1)) over the row, from a 32-bit bit-length maximum
+template <int VPT>
+__device__ __forceinline__ i64 row_ilog2_absmax(const i64 (&v)[VPT], BlockRed& red) {
+  uint32_t L = 0;
+#pragma unroll
+  for (int j = 0; j < VPT; ++j) L = ::max(L, bitlen_abs(v[j]));
+  return ilog2_from_bitlen(red.max_u32(L));
+}
+
 // ops/di_rmsnorm.py:33-52: v (<= C valid columns, 0 elsewhere) -> y (int32 values)
 template <int VPT>
 __device__ __forceinline__ void rmsnorm_row(i64 (&v)[VPT], int C, BlockRed& red) {
-  const i64 g = row_absmax(v, red);
-  const i64 sh = 25 - ilog2(imax(g, 1));
+  const i64 sh = 25 - row_ilog2_absmax(v, red);
   const i64 up = imax(sh, 0), down = imax(-sh, 0);
   i64 ss = 0;
 #pragma unroll
@@ -91,20 +99,49 @@ __device__ __forceinline__ i64 requant_common_row(i64 (&v)[VPT], const i64 (&cm)
                                                   i64 col_k, int tb, BlockRed& red) {
 #pragma unroll
   for (int j = 0; j < VPT; ++j) v[j] = wmul(v[j], cm[j]);
-  const i64 a = imax(row_absmax(v, red), 1);
-  const i64 sh = imax(ilog2(a) - (tb - 1), 0);
+  const i64 sh = imax(row_ilog2_absmax(v, red) - (tb - 1), 0);
 #pragma unroll
   for (int j = 0; j < VPT; ++j) v[j] = to_i32(rshift_round(v[j], sh));
   return wsub(wadd(row_k, col_k), sh);
 }
 
+// requant_common_row on two rows at once (gate and up of the same token):
+// both bit-length maxima share one barrier. Returns the two k_out.
+template <int VPT>
+__device__ __forceinline__ void requant_common_row2(i64 (&v0)[VPT], const i64 (&cm0)[VPT],
+                                                    i64 col_k0, i64 (&v1)[VPT],
+                                                    const i64 (&cm1)[VPT], i64 col_k1, i64 row_k,
+                                                    int tb, BlockRed& red, i64* k0, i64* k1) {
+  uint32_t L0 = 0, L1 = 0;
+#pragma unroll
+  for (int j = 0; j < VPT; ++j) {
+    v0[j] = wmul(v0[j], cm0[j]);
+    v1[j] = wmul(v1[j], cm1[j]);
+    L0 = ::max(L0, bitlen_abs(v0[j]));
+    L1 = ::max(L1, bitlen_abs(v1[j]));
+  }
+  red.max2_u32(L0, L1);
+  const i64 sh0 = imax(ilog2_from_bitlen(L0) - (tb - 1), 0);
+  const i64 sh1 = imax(ilog2_from_bitlen(L1) - (tb - 1), 0);
+#pragma unroll
+  for (int j = 0; j < VPT; ++j) {
+    v0[j] = to_i32(rshift_round(v0[j], sh0));
+    v1[j] = to_i32(rshift_round(v1[j], sh1));
+  }
+  *k0 = wsub(wadd(row_k, col_k0), sh0);
+  *k1 = wsub(wadd(row_k, col_k1), sh1);
+}
+
 // dyadic.py:174-184
 template <int VPT>
 __device__ __forceinline__ i64 residual_renorm_row(i64 (&h)[VPT], i64 k_res, BlockRed& red) {
-  const i64 g = row_absmax(h, red);
-  const i64 lg = ilog2(imax(g, 1));
+  uint32_t L = 0;
+#pragma unroll
+  for (int j = 0; j < VPT; ++j) L = ::max(L, bitlen_abs(h[j]));
+  L = red.max_u32(L);                       // g = max |h| > 0  <=>  L > 0
+  const i64 lg = ilog2_from_bitlen(L);      // ilog2(max(g, 1))
   const i64 sh_down = imax(lg - 29, 0);
-  i64 sh_up = g > 0 ? imax(26 - lg, 0) : 0;
+  i64 sh_up = L > 0 ? imax(26 - lg, 0) : 0;
   if (sh_down > 0) sh_up = 0;
 #pragma unroll
   for (int j = 0; j < VPT; ++j) h[j] = to_i32(shl(rshift_round(h[j], sh_down), sh_up));
@@ -316,8 +353,8 @@ __global__ __launch_bounds__(RT_WIDE) void k_swiglu_quant(SwigluArgs a) {
   i64 gu[2][VPT];
   const i64 offs[2] = {(i64)r * 2 * I, (i64)r * 2 * I + I};
   load_rows_i32_sum<2, VPT>(gu, a.P, a.nsplit, a.split_stride, offs, I);
-  const i64 gk = requant_common_row(gu[0], gm, xk, a.gate_k, 14, red);
-  const i64 uk = requant_common_row(gu[1], um, xk, a.up_k, 14, red);
+  i64 gk, uk;
+  requant_common_row2(gu[0], gm, a.gate_k, gu[1], um, a.up_k, xk, 14, red, &gk, &uk);
   const ExpR E = make_exp(di_exp_tpos(xm, gk));
 #pragma unroll
   for (int j = 0; j < VPT; ++j) gu[0][j] = wmul(swiglu_elem_e(gu[0][j], gu[1][j], E), dsm[j]);
@@ -371,8 +408,7 @@ __global__ __launch_bounds__(RT_WIDE) void k_merge_rowcol(MergeArgs a) {
   }
 #pragma unroll
   for (int j = 0; j < VPT; ++j) v[j] = wmul(wmul(v[j], om[j]), cm[j]);  // 0 past C
-  const i64 a1 = imax(row_absmax(v, red), 1);
-  const i64 sh = imax(ilog2(a1) - 45, 0);
+  const i64 sh = imax(row_ilog2_absmax(v, red) - 45, 0);
 #pragma unroll
   for (int j = 0; j < VPT; ++j) v[j] = rshift_round(v[j], sh);
   const i64 a2 = imax(row_absmax(v, red), 1);
@@ -460,8 +496,7 @@ __global__ __launch_bounds__(RT) void k_op_rowcol(const int64_t* P, const int64_
     const int c = threadIdx.x + j * (int)blockDim.x;
     v[j] = c < C ? wmul(v[j], col_m[c]) : 0;
   }
-  const i64 a1 = imax(row_absmax(v, red), 1);
-  const i64 sh = imax(ilog2(a1) - 45, 0);
+  const i64 sh = imax(row_ilog2_absmax(v, red) - 45, 0);
 #pragma unroll
   for (int j = 0; j < VPT; ++j) v[j] = rshift_round(v[j], sh);
   const i64 a2 = imax(row_absmax(v, red), 1);
