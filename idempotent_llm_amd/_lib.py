@@ -23,6 +23,7 @@ P, I, L, S = "p", "i", "l", "s"
 SIGNATURES = {
     "detllm_igemm_nt": [P, P, P, I, I, I, I, L, L, L, S],
     "detllm_igemv_nt": [P, P, P, I, I, I, I, L, S],
+    "detllm_igemv_nt_pf": [P, P, P, I, I, I, I, L, P, L, P, L, P, L, P, L, S],
     "detllm_igemv_plan": [I, I, I, P],
     "detllm_transpose_i8": [P, P, I, I, I, L, L, S],
     "detllm_greedy_pick": [P, P, I, I, I, P, P, P, S],

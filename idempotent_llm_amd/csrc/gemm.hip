@@ -296,11 +296,39 @@ __global__ __launch_bounds__(64 * WGM * WGN, MINB) void k_gemm_nt2(const int8_t*
 // so each wave issues all loads of NB iterations before the first MFMA.
 // KW waves of a block split the K range of one column group and reduce their
 // int32 accumulators through LDS; with KW == 1 the 4 waves own 4 column groups.
+// Up to four byte ranges that the kernels after this launch read (their
+// per-column scale vectors): each thread of the first K split touches one
+// 128-byte line of them, so they are fetched into the memory-side cache while
+// this launch streams its weights and the next launch finds them there.
+// A performance hint only: the loaded words are discarded (stored to `sink`
+// only when it is non-null, which keeps the loads), results do not change.
+struct Prefetch {
+  const int8_t* p[4];
+  i64 n[4];  // bytes; 0 = unused
+  int32_t* sink;
+};
+
+__device__ __forceinline__ void prefetch_lines(const Prefetch& pf, i64 t) {
+  int32_t v = 0;
+  bool hit = false;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const i64 lines = (pf.n[i] + 127) >> 7;
+    if (t >= 0 && t < lines) {  // offset 128 t < n, and n is a multiple of 4
+      v = *(const int32_t*)(pf.p[i] + (t << 7));
+      hit = true;
+    }
+    t -= lines;
+  }
+  if (hit && pf.sink) *pf.sink = v;
+}
+
 template <int MB, int KW, int NB>
 __global__ __launch_bounds__(256) void k_gemv_nt(const int8_t* __restrict__ A,
                                                  const int8_t* __restrict__ B,
                                                  int32_t* __restrict__ C, int M, int N, int K,
-                                                 int kchunk, i64 split_stride) {
+                                                 int kchunk, i64 split_stride, Prefetch pf) {
+  if (blockIdx.y == 0) prefetch_lines(pf, (i64)blockIdx.x * blockDim.x + threadIdx.x);
   constexpr int U = 4;                 // 16-byte slices per lane per iteration
   constexpr int CG = 4 / KW;           // column groups per block
   constexpr int KSTEP = 64 * U;        // K covered by one wave-iteration
@@ -456,9 +484,35 @@ int gemv_plan(int N, int K) {
 
 template <int MB, int KW, int NB>
 void launch_gemv(dim3 grid, hipStream_t s, const int8_t* A, const int8_t* B, int32_t* C,
-                        int M, int N, int K, int kchunk, i64 split_stride) {
+                        int M, int N, int K, int kchunk, i64 split_stride, const Prefetch& pf) {
   hipLaunchKernelGGL((k_gemv_nt<MB, KW, NB>), grid, dim3(256), 0, s, A, B, C, M, N, K, kchunk,
-                     split_stride);
+                     split_stride, pf);
+}
+
+// Skinny GEMM for M <= 64: writes ksplit int32 partials C[ks][M][N]
+// (split_stride elements apart); ksplit = 1 gives the plain product. Four
+// waves share one 16-column group and split its K range (measured faster than
+// a column group per wave at every model shape).
+int igemv(const int8_t* A, const int8_t* B, int32_t* C, int M, int N, int K, int ksplit,
+          int64_t split_stride, const Prefetch& pf, hipStream_t s) {
+  if (M <= 0 || N <= 0) return DI_OK;
+  if (M > 64 || K <= 0 || (K % 16) != 0 || K > 131071 || ksplit < 1 || !A || !B || !C)
+    return DI_EINVAL;
+  if (ksplit > 1 && split_stride < (int64_t)M * N) return DI_EINVAL;
+  int kchunk = (K + ksplit - 1) / ksplit;
+  kchunk = (kchunk + 63) / 64 * 64;
+  const int nsp = (K + kchunk - 1) / kchunk;
+  if (nsp != ksplit) return DI_EINVAL;  // caller must size partial buffers to ksplit
+  const dim3 grid((N + 15) / 16, ksplit);
+  const i64 ss = (i64)split_stride;
+  switch ((M + 15) / 16) {
+    case 1: launch_gemv<1, 4, 2>(grid, s, A, B, C, M, N, K, kchunk, ss, pf); break;
+    case 2: launch_gemv<2, 4, 2>(grid, s, A, B, C, M, N, K, kchunk, ss, pf); break;
+    case 3: launch_gemv<3, 4, 1>(grid, s, A, B, C, M, N, K, kchunk, ss, pf); break;
+    default: launch_gemv<4, 4, 1>(grid, s, A, B, C, M, N, K, kchunk, ss, pf); break;
+  }
+  DI_LAUNCH_CHECK();
+  return DI_OK;
 }
 
 }  // namespace
@@ -506,42 +560,29 @@ int detllm_igemv_plan(int M, int N, int K, int* ksplit) {
   return DI_OK;
 }
 
-// Skinny GEMM for M <= 64: writes ksplit int32 partials C[ks][M][N]
-// (split_stride elements apart); ksplit = 1 gives the plain product.
-// Wide products (>= 1024 column groups of 16) give each wave its own column
-// group; narrower ones put 4 waves on one group, splitting its K range.
+// Skinny GEMM for M <= 64 (igemv above).
 int detllm_igemv_nt(const int8_t* A, const int8_t* B, int32_t* C, int M, int N, int K,
                     int ksplit, int64_t split_stride, hipStream_t s) {
-  if (M <= 0 || N <= 0) return DI_OK;
-  if (M > 64 || K <= 0 || (K % 16) != 0 || K > 131071 || ksplit < 1 || !A || !B || !C)
-    return DI_EINVAL;
-  if (ksplit > 1 && split_stride < (int64_t)M * N) return DI_EINVAL;
-  int kchunk = (K + ksplit - 1) / ksplit;
-  kchunk = (kchunk + 63) / 64 * 64;
-  const int nsp = (K + kchunk - 1) / kchunk;
-  if (nsp != ksplit) return DI_EINVAL;  // caller must size partial buffers to ksplit
-  const int groups = (N + 15) / 16;
-  const bool wide = false;  // 4 waves per column group measured faster at every model shape
-  const dim3 grid(wide ? (groups + 3) / 4 : groups, ksplit);
-  const int mb = (M + 15) / 16;
-  const i64 ss = (i64)split_stride;
-  if (wide) {
-    switch (mb) {
-      case 1: launch_gemv<1, 1, 2>(grid, s, A, B, C, M, N, K, kchunk, ss); break;
-      case 2: launch_gemv<2, 1, 2>(grid, s, A, B, C, M, N, K, kchunk, ss); break;
-      case 3: launch_gemv<3, 1, 1>(grid, s, A, B, C, M, N, K, kchunk, ss); break;
-      default: launch_gemv<4, 1, 1>(grid, s, A, B, C, M, N, K, kchunk, ss); break;
-    }
-  } else {
-    switch (mb) {
-      case 1: launch_gemv<1, 4, 2>(grid, s, A, B, C, M, N, K, kchunk, ss); break;
-      case 2: launch_gemv<2, 4, 2>(grid, s, A, B, C, M, N, K, kchunk, ss); break;
-      case 3: launch_gemv<3, 4, 1>(grid, s, A, B, C, M, N, K, kchunk, ss); break;
-      default: launch_gemv<4, 4, 1>(grid, s, A, B, C, M, N, K, kchunk, ss); break;
-    }
+  const Prefetch none{};
+  return igemv(A, B, C, M, N, K, ksplit, split_stride, none, s);
+}
+
+// detllm_igemv_nt that also pulls up to four byte ranges, which the next
+// kernels read, into the memory-side cache (see Prefetch); same results.
+int detllm_igemv_nt_pf(const int8_t* A, const int8_t* B, int32_t* C, int M, int N, int K,
+                       int ksplit, int64_t split_stride, const void* pf0, int64_t n0,
+                       const void* pf1, int64_t n1, const void* pf2, int64_t n2,
+                       const void* pf3, int64_t n3, hipStream_t s) {
+  const void* ps[4] = {pf0, pf1, pf2, pf3};
+  const int64_t ns[4] = {n0, n1, n2, n3};
+  Prefetch pf{};
+  for (int i = 0; i < 4; ++i) {
+    if (ns[i] < 0 || (ns[i] > 0 && (!ps[i] || (ns[i] & 3) != 0 || ((uintptr_t)ps[i] & 3) != 0)))
+      return DI_EINVAL;
+    pf.p[i] = (const int8_t*)ps[i];
+    pf.n[i] = ps[i] ? ns[i] : 0;
   }
-  DI_LAUNCH_CHECK();
-  return DI_OK;
+  return igemv(A, B, C, M, N, K, ksplit, split_stride, pf, s);
 }
 
 // dst[b] = src[b]^T for int8 [R][C] matrices

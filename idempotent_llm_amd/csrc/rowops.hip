@@ -52,10 +52,12 @@ __device__ __forceinline__ i64 row_ilog2_absmax(const i64 (&v)[VPT], BlockRed& r
   return ilog2_from_bitlen(red.max_u32(L));
 }
 
-// ops/di_rmsnorm.py:33-52: v (<= C valid columns, 0 elsewhere) -> y (int32 values)
+// ops/di_rmsnorm.py:33-52: v (<= C valid columns, 0 elsewhere) -> y (int32
+// values). lg: ilog2(max(max |v|, 1)) when the caller already knows it, else
+// -1 (one more block reduction).
 template <int VPT>
-__device__ __forceinline__ void rmsnorm_row(i64 (&v)[VPT], int C, BlockRed& red) {
-  const i64 sh = 25 - row_ilog2_absmax(v, red);
+__device__ __forceinline__ void rmsnorm_row(i64 (&v)[VPT], int C, BlockRed& red, i64 lg = -1) {
+  const i64 sh = 25 - (lg >= 0 ? lg : row_ilog2_absmax(v, red));
   const i64 up = imax(sh, 0), down = imax(-sh, 0);
   i64 ss = 0;
 #pragma unroll
@@ -132,9 +134,14 @@ __device__ __forceinline__ void requant_common_row2(i64 (&v0)[VPT], const i64 (&
   *k1 = wsub(wadd(row_k, col_k1), sh1);
 }
 
-// dyadic.py:174-184
+// dyadic.py:174-184. *lg_out: ilog2(max(max |h|, 1)) of the renormalised
+// row when it follows from the reduction already done, else -1. Without a
+// down-shift it does: an exact up-shift by u adds u to every bit length (and
+// no shift leaves them), while rounding a down-shift may carry into the next
+// bit.
 template <int VPT>
-__device__ __forceinline__ i64 residual_renorm_row(i64 (&h)[VPT], i64 k_res, BlockRed& red) {
+__device__ __forceinline__ i64 residual_renorm_row(i64 (&h)[VPT], i64 k_res, BlockRed& red,
+                                                   i64* lg_out) {
   uint32_t L = 0;
 #pragma unroll
   for (int j = 0; j < VPT; ++j) L = ::max(L, bitlen_abs(h[j]));
@@ -145,18 +152,19 @@ __device__ __forceinline__ i64 residual_renorm_row(i64 (&h)[VPT], i64 k_res, Blo
   if (sh_down > 0) sh_up = 0;
 #pragma unroll
   for (int j = 0; j < VPT; ++j) h[j] = to_i32(shl(rshift_round(h[j], sh_down), sh_up));
+  *lg_out = sh_down > 0 ? -1 : ilog2_from_bitlen(L > 0 ? L + (uint32_t)sh_up : 0u);
   return wadd(wsub(k_res, sh_down), sh_up);
 }
 
 // dyadic.py:193-206
 template <int VPT>
 __device__ __forceinline__ i64 residual_add_row(i64 (&h)[VPT], i64 k_res, const i64 (&d)[VPT],
-                                                i64 dm, i64 dk, BlockRed& red) {
+                                                i64 dm, i64 dk, BlockRed& red, i64* lg_out) {
   const i64 rel = wsub(dk, k_res);
   const i64 down = imax(rel, 0), up = imax(wneg(rel), 0);
 #pragma unroll
   for (int j = 0; j < VPT; ++j) h[j] = wadd(h[j], shl(rshift_round(wmul(d[j], dm), down), up));
-  return residual_renorm_row(h, k_res, red);
+  return residual_renorm_row(h, k_res, red, lg_out);
 }
 
 // Latency, not bandwidth, bounds these kernels at decode (one block per
@@ -257,7 +265,7 @@ __global__ __launch_bounds__(RT_WIDE) void k_residual_normq(ResNormArgs a) {
   const int C = a.C;
   const i64 off = (i64)r * C;
   i64 h[VPT], d[VPT], smv[VPT];
-  i64 kr;
+  i64 kr, lg = -1;
   prefetch_cols(smv, a.sm_m, C);
   if (a.mode == 2) {
     // _norm_quant of a given residual row: h is read, not written
@@ -281,7 +289,7 @@ __global__ __launch_bounds__(RT_WIDE) void k_residual_normq(ResNormArgs a) {
     }
 #pragma unroll
     for (int j = 0; j < VPT; ++j) h[j] = threadIdx.x + j * (int)blockDim.x < C ? wmul(h[j], dm) : 0;
-    kr = residual_renorm_row(h, ek, red);
+    kr = residual_renorm_row(h, ek, red, &lg);
   } else {
     i64 cm[VPT];
     prefetch_cols(cm, a.col_m, C);
@@ -300,7 +308,7 @@ __global__ __launch_bounds__(RT_WIDE) void k_residual_normq(ResNormArgs a) {
       if (threadIdx.x + j * (int)blockDim.x >= C) h[j] = 0;
     }
     const i64 dk = requant_common_row(d, cm, row_k, a.col_k, a.tb, red);
-    kr = residual_add_row(h, k_res, d, row_m, dk, red);
+    kr = residual_add_row(h, k_res, d, row_m, dk, red, &lg);
   }
   if (a.mode != 2) {
 #pragma unroll
@@ -311,7 +319,7 @@ __global__ __launch_bounds__(RT_WIDE) void k_residual_normq(ResNormArgs a) {
     if (threadIdx.x == 0) a.k_res[r] = kr;
   }
   if (a.x8 == nullptr) return;
-  rmsnorm_row(h, C, red);
+  rmsnorm_row(h, C, red, lg);
   i64 kq = 20;
   if (a.sm_m != nullptr) {
 #pragma unroll
@@ -525,13 +533,13 @@ __global__ __launch_bounds__(RT) void k_op_residual(int mode, const int64_t* h_i
   const int r = blockIdx.x;
   i64 h[VPT];
   load_row64(h, h_in, (i64)r * C, C);
-  i64 k;
+  i64 k, lg;
   if (mode == 0) {
-    k = residual_renorm_row(h, k_res[r], red);
+    k = residual_renorm_row(h, k_res[r], red, &lg);
   } else {
     i64 dv[VPT];
     load_row64(dv, d, (i64)r * C, C);
-    k = residual_add_row(h, k_res[r], dv, dm[r], dk[r], red);
+    k = residual_add_row(h, k_res[r], dv, dm[r], dk[r], red, &lg);
   }
 #pragma unroll
   for (int j = 0; j < VPT; ++j) {

@@ -73,6 +73,23 @@ class LayerWeights:
     vq_m: torch.Tensor; vq_k: torch.Tensor
     attn_out_col_m: torch.Tensor
     attn_out_col_k: int
+    # the per-column scale vectors each row kernel reads, packed contiguously
+    # so the skinny GEMM before it can prefetch them as one range
+    pf_attn: torch.Tensor | None = None   # Q/K/V epilogue + attention-output merge
+    pf_o: torch.Tensor | None = None      # residual after o
+    pf_mlp: torch.Tensor | None = None    # SwiGLU
+
+
+def _pack(L: LayerWeights, names) -> torch.Tensor:
+    """Move the named int64 tensors of L into one buffer (views keep their
+    shapes and values); returns the buffer."""
+    ts = [getattr(L, n) for n in names]
+    buf = torch.cat([t.reshape(-1) for t in ts])
+    off = 0
+    for n, t in zip(names, ts):
+        setattr(L, n, buf[off:off + t.numel()].view(t.shape))
+        off += t.numel()
+    return buf
 
 
 class KVCache:
@@ -197,6 +214,12 @@ class IntQwen3:
                 ks_m=g(p + "ks_m"), ks_k=g(p + "ks_k"), vq_m=vq_m.to(dev), vq_k=vq_k.to(dev),
                 attn_out_col_m=col_m.to(dev), attn_out_col_k=vk_shared + (P_OUT_BITS - 1)))
         del tensors
+        for L in self.layers:
+            L.pf_attn = _pack(L, ["q_m", "k_m", "v_m", "q_norm_m", "k_norm_m", "qs_m", "kq_m",
+                                  "kq_k", "ks_m", "ks_k", "vq_m", "vq_k", "os_m",
+                                  "attn_out_col_m"])
+            L.pf_o = _pack(L, ["o_m", "ms_m"])
+            L.pf_mlp = _pack(L, ["gate_m", "up_m", "ds_m"])
         self._greedy_scratch = {}
         self._plans: dict = {}
 
@@ -214,11 +237,22 @@ class IntQwen3:
             self._plans[key] = ks
         return ks
 
-    def _gemm(self, x: torch.Tensor, w: torch.Tensor):
+    def _gemm(self, x: torch.Tensor, w: torch.Tensor, prefetch=(), split: bool = True):
+        """x . w^T as int32 partials [ks, R, N] (ks = 1 unless split and the
+        skinny GEMM's plan splits K). prefetch: up to four device tensors the
+        next kernels read; the skinny GEMM pulls them into the memory-side
+        cache while it streams w (a hint, results unchanged)."""
         R, K = x.shape
         N = w.shape[0]
-        ks = self._ksplit(N, K, R) if R <= 64 else 1
-        P = gemm_nt(x, w, ksplit=ks)
+        if R > 64:
+            return gemm_nt(x, w), 1, R * N
+        ks = self._ksplit(N, K, R) if split else 1
+        P = torch.empty(ks, R, N, dtype=torch.int32, device=self.device)
+        pf = []
+        for t in prefetch[:4]:
+            pf += [t, t.numel() * t.element_size()]
+        pf += [None, 0] * (4 - len(prefetch[:4]))
+        call("detllm_igemv_nt_pf", x, w, P, R, N, K, ks, R * N, *pf)
         return P, ks, R * N
 
     # -- forward (model.py:220-286) ------------------------------------------------
@@ -259,8 +293,7 @@ class IntQwen3:
         xk = torch.empty(R, dtype=I64, device=dev)
         L0 = self.layers[0]
         call("detllm_embed_normq", ids.contiguous().view(-1), R, H, self.vocab, self.embed_e8,
-             self.embed_m,
-             self.embed_k, h, k_res, L0.as_m, L0.as_k, x8, xm, xk)
+             self.embed_m, self.embed_k, h, k_res, L0.as_m, L0.as_k, x8, xm, xk)
         pos = positions.contiguous().view(-1)
         for li, L in enumerate(self.layers):
             nxt = self.layers[li + 1] if li + 1 < self.n_layers else None
@@ -269,9 +302,10 @@ class IntQwen3:
             cache.length = S
         if head_rows is not None:
             xh = x8.view(B, T, H)[torch.arange(B, device=dev), head_rows].contiguous()
-            logits = gemm_nt(xh, self.head_w)[0]
+            logits = self._gemm(xh, self.head_w, (self.head_m,), split=False)[0][0]
             return logits, xm.view(B, T, 1), xk.view(B, T, 1), cache
-        logits = gemm_nt(x8, self.head_w)[0].view(B, T, self.vocab)
+        logits = self._gemm(x8, self.head_w, (self.head_m,), split=False)[0][0].view(
+            B, T, self.vocab)
         return logits, xm.view(B, T, 1), xk.view(B, T, 1), cache
 
     def _layer(self, L: LayerWeights, nxt, B, T, h, k_res, x8, xm, xk, pos, cache: KVCache,
@@ -279,7 +313,7 @@ class IntQwen3:
         dev = self.device
         R, H, nq, nkv, hd, I_ = B * T, self.hidden, self.n_q, self.n_kv, self.hd, self.inter
         li = L.idx
-        P, ns, st = self._gemm(x8, L.wqkv)
+        P, ns, st = self._gemm(x8, L.wqkv, (L.pf_attn,))
         attn = torch.empty(R, nq * hd, dtype=I64, device=dev)
         valid = cache.valid_buf.view(torch.uint8)
         if T == 1 and nq // nkv <= 2:
@@ -333,16 +367,16 @@ class IntQwen3:
         ak = torch.empty(R, dtype=I64, device=dev)
         call("detllm_merge_rowcol", attn, 1, 0, R, nq * hd, L.os_m, L.os_k, L.attn_out_col_m,
              L.attn_out_col_k, a8, am, ak)
-        P, ns, st = self._gemm(a8, L.wo)
+        P, ns, st = self._gemm(a8, L.wo, (L.pf_o,))
         call("detllm_residual_normq", P, ns, st, R, H, am, ak, L.o_m, L.o_k, 20, h, k_res,
              L.ms_m, L.ms_k, x8, xm, xk)
-        P, ns, st = self._gemm(x8, L.wgu)
+        P, ns, st = self._gemm(x8, L.wgu, (L.pf_mlp,))
         y8 = torch.empty(R, I_, dtype=torch.int8, device=dev)
         ym = torch.empty(R, dtype=I64, device=dev)
         yk = torch.empty(R, dtype=I64, device=dev)
         call("detllm_swiglu_quant", P, ns, st, R, I_, xm, xk, L.gate_m, L.gate_k, L.up_m,
              L.up_k, L.ds_m, L.ds_k, y8, ym, yk)
-        P, ns, st = self._gemm(y8, L.wd)
+        P, ns, st = self._gemm(y8, L.wd, (L.down_m,) if nxt is None else (L.down_m, nxt.as_m))
         sm_m, sm_k = (nxt.as_m, nxt.as_k) if nxt is not None else (None, 0)
         call("detllm_residual_normq", P, ns, st, R, H, ym, yk, L.down_m, L.down_k, 20, h, k_res,
              sm_m, sm_k, x8, xm, xk)

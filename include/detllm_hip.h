@@ -46,6 +46,17 @@ int detllm_igemm_nt(const int8_t* A, const int8_t* B, int32_t* C, int M, int N, 
 int detllm_igemv_nt(const int8_t* A, const int8_t* B, int32_t* C, int M, int N, int K,
                     int ksplit, int64_t split_stride, hipStream_t s);
 
+/* detllm_igemv_nt plus a prefetch hint (no counterpart in the reference: a
+ * performance hint of this backend): up to four device byte ranges
+ * (pf_i, n_i; n_i a multiple of 4, 0 = unused) that the following kernels
+ * read are touched once per 128-byte line while the weights stream, so they
+ * sit in the memory-side cache when those kernels start. Results are those
+ * of detllm_igemv_nt. */
+int detllm_igemv_nt_pf(const int8_t* A, const int8_t* B, int32_t* C, int M, int N, int K,
+                       int ksplit, int64_t split_stride, const void* pf0, int64_t n0,
+                       const void* pf1, int64_t n1, const void* pf2, int64_t n2,
+                       const void* pf3, int64_t n3, hipStream_t s);
+
 /* K split that detllm_igemv_nt is tuned for at this shape (the reference's
  * cuBLASLt path picks its own kernel internally, backends.py:115-119);
  * writes *ksplit in [1, 8]. */

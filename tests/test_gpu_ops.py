@@ -269,3 +269,95 @@ def test_di_matmul_composition():
     y8, m, k = dops.di_matmul(g(x), g(xm), g(xk), g(w), g(wm), 24)
     oy, om, ok = oops.di_matmul(x, xm, xk, w, wm, 24)
     eq(y8, oy); eq(m, om); eq(k, ok)
+
+
+def _normq_oracle(P, row_m, row_k, col_m, col_k, h, k_res, sm_m, sm_k):
+    """model.py:410-415 (+ :187-198) on the oracle: requant_i32_common(20),
+    residual_add, then _norm_quant with optional smoothing."""
+    d, dm, dk = ody.requant_i32_common(P, row_m[:, None], row_k[:, None], col_m, col_k,
+                                       target_bits=20)
+    h2, k2 = ody.residual_add(h, k_res[:, None], d, dm, dk)
+    y = oops.di_rmsnorm(h2)
+    kq = np.full((P.shape[0], 1), 20, I64)
+    if sm_m is not None:
+        y = y.astype(I64) * sm_m.astype(I64)
+        kq = kq + sm_k
+    x8, xm, xk = ody.quant_i8_pertoken(y, np.ones_like(kq), kq)
+    return h2, k2[:, 0], x8, xm[:, 0], xk[:, 0]
+
+
+@pytest.mark.parametrize("C", [1024, 256, 3072])
+@pytest.mark.parametrize("smooth", [False, True])
+def test_residual_normq_renorm_branches(C, smooth):
+    """The fused residual + RMSNorm + quant kernel against the oracle on rows
+    chosen to take every renormalisation branch: the sum crosses 2^30 (down
+    shift, the RMSNorm maximum is reduced again), small rows (up shift, the
+    RMSNorm maximum follows from the renorm), rows left in [2^26, 2^30), a
+    zero row, and a row of one non-zero element."""
+    from idempotent_llm_amd._lib import call
+    print(f"[residual_normq branches C={C} smooth={smooth}]", flush=True)
+    rng = np.random.default_rng(C + smooth)
+    R = 8
+    scale = [2 ** 29 - 3, 2 ** 20, 2 ** 28, 0, 0, 2 ** 27, 2 ** 12, 2 ** 29]
+    h = np.stack([rng.integers(-s, s + 1, C) if s else np.zeros(C, I64) for s in scale])
+    h[4, C // 3] = 5
+    P = rng.integers(-(1 << 20), 1 << 20, (1, R, C)).astype(np.int32)
+    P[0, 3] = 0
+    P[0, 4] = 0
+    row_m = rng.integers(1 << 15, 1 << 16, R).astype(I64)
+    row_k = np.array([20, 24, 26, 20, 20, 30, 40, 19], I64)
+    k_res = np.array([24, 24, 24, 24, 24, 24, 24, 24], I64)
+    col_m = rng.integers(1 << 15, 1 << 16, C).astype(I64)
+    sm_m = rng.integers(1 << 15, 1 << 16, C).astype(I64) if smooth else None
+    want = _normq_oracle(P[0], row_m, row_k, col_m, 20, h.astype(np.int32), k_res, sm_m, 15)
+    hg = g(h.astype(np.int32))
+    kg = g(k_res.copy())
+    x8 = torch.empty(R, C, dtype=torch.int8, device="cuda")
+    xm = torch.empty(R, dtype=torch.int64, device="cuda")
+    xk = torch.empty(R, dtype=torch.int64, device="cuda")
+    call("detllm_residual_normq", g(P), 1, 0, R, C, g(row_m), g(row_k), g(col_m), 20, 20, hg,
+         kg, g(sm_m) if smooth else None, 15, x8, xm, xk)
+    for got, w in zip((hg, kg, x8, xm, xk), want):
+        eq(got, w)
+    # the rows do take the branches named above
+    d, dm, dk = ody.requant_i32_common(P[0], row_m[:, None], row_k[:, None], col_m, 20, 20)
+    rel = dk[:, 0] - k_res
+    dd = d.astype(I64) * dm
+    al = oim.shl(oim.rshift_round_t(dd, np.broadcast_to(np.maximum(rel, 0)[:, None], dd.shape)),
+                 np.broadcast_to(np.maximum(-rel, 0)[:, None], dd.shape))
+    top = np.abs(h.astype(I64) + al).max(axis=1)
+    assert (top >= 2 ** 30).any() and ((top > 0) & (top < 2 ** 26)).any()
+    assert ((top >= 2 ** 26) & (top < 2 ** 30)).any() and (top == 0).any()
+
+
+def test_igemv_prefetch_variant_same_product():
+    """detllm_igemv_nt_pf (skinny GEMM + prefetch hint) gives the product of
+    detllm_igemv_nt, with 0-4 ranges of any multiple-of-4 size; bad ranges are
+    argument errors."""
+    from idempotent_llm_amd._lib import call, gemv_plan
+    print("[igemv prefetch]", flush=True)
+    rng = np.random.default_rng(3)
+    M, N, K = 8, 1024, 3072
+    a = g(rng.integers(-128, 128, (M, K)).astype(np.int8))
+    w = g(rng.integers(-128, 128, (N, K)).astype(np.int8))
+    ks = gemv_plan(M, N, K)
+    ref = torch.empty(ks, M, N, dtype=torch.int32, device="cuda")
+    call("detllm_igemv_nt", a, w, ref, M, N, K, ks, M * N)
+    pfs = [g(rng.integers(0, 9, n).astype(np.int64)) for n in (1, 17, 3072, 40000)]
+    for nr in range(5):
+        out = torch.full((ks, M, N), -1, dtype=torch.int32, device="cuda")
+        args = []
+        for t in pfs[:nr]:
+            args += [t, t.numel() * 8]
+        args += [None, 0] * (4 - nr)
+        call("detllm_igemv_nt_pf", a, w, out, M, N, K, ks, M * N, *args)
+        assert torch.equal(out, ref)
+    want = ogemm.int_gemm(a.cpu().numpy(), w.cpu().numpy().T)
+    eq(ref.sum(0), want)
+    with pytest.raises(RuntimeError):   # size not a multiple of 4
+        call("detllm_igemv_nt_pf", a, w, ref, M, N, K, ks, M * N, pfs[0], 6, None, 0, None, 0,
+             None, 0)
+    with pytest.raises(RuntimeError):   # size without a pointer
+        call("detllm_igemv_nt_pf", a, w, ref, M, N, K, ks, M * N, None, 8, None, 0, None, 0,
+             None, 0)
+
