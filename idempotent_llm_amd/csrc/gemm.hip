@@ -527,12 +527,20 @@ int detllm_igemm_nt(const int8_t* A, const int8_t* B, int32_t* C, int M, int N, 
   if (K <= 0 || (K % 16) != 0 || K > 131071 || !A || !B || !C) return DI_EINVAL;
   if (batch > 65535) return DI_ERANGE;
   if (M > 64 && K % G2_BK == 0) {
-    // 128x128 tiles (4 waves, 2 slices, 2 blocks per CU) while they give at
-    // least two tiles per CU; otherwise 128x64 tiles for more parallelism,
+    // Tile by how many tiles the product gives for the 256 CUs (measured):
+    // 256x256 tiles on 8 waves (4 x 2, 64x128 each, 2 slices) from 192 of
+    // them; else 128x128 tiles (4 waves, 2 slices, 2 blocks per CU) while they
+    // give at least two tiles per CU; else 128x64 tiles for more parallelism,
     // on 8 waves (4 x 2, one 32x32 block each) and a 4-slice ring
+    const i64 t256 = (i64)((M + 255) / 256) * ((N + 255) / 256) * batch;
     const i64 t128 = (i64)((M + 127) / 128) * ((N + 127) / 128) * batch;
     const int tm = (M + 127) / 128;
-    if (t128 >= 512) {
+    if (t256 >= 192) {
+      const int tm2 = (M + 255) / 256, tn2 = (N + 255) / 256;
+      if ((i64)tm2 * tn2 > 0x7fffffff) return DI_ERANGE;
+      hipLaunchKernelGGL((k_gemm_nt2<256, 256, 2, 4, 2, 1>), dim3(tm2 * tn2, 1, batch), dim3(512),
+                         0, s, A, B, C, M, N, K, (i64)sA, (i64)sB, (i64)sC, tm2, tn2);
+    } else if (t128 >= 512) {
       const int tn = (N + 127) / 128;
       if ((i64)tm * tn > 0x7fffffff) return DI_ERANGE;
       hipLaunchKernelGGL((k_gemm_nt2<128, 128, 2, 2, 2, 2>), dim3(tm * tn, 1, batch), dim3(256), 0, s,
