@@ -263,19 +263,46 @@ constexpr int MAXG = 8;
 constexpr i64 DECODE_LDS_BYTES = 48 * 1024;
 
 constexpr int32_t SCORE_MASKED = INT32_MIN;  // |q.k| <= 128*128*128 < 2^31: never a score
-constexpr int VPRE = 8;                      // V chunks of 16 slots prefetched per thread
+constexpr int DEC_MAX_S = 131071;            // int32 MFMA accumulators of P.V
+constexpr int VPRE = 4;                      // 64-slot steps of V loaded before the scores
+
+// DPP max over each aligned row of 16 lanes (result in every lane of the row)
+__device__ __forceinline__ int32_t row16_max(int32_t v) {
+  v = ::max(v, __builtin_amdgcn_update_dpp(v, v, 0xB1, 0xF, 0xF, false));
+  v = ::max(v, __builtin_amdgcn_update_dpp(v, v, 0x4E, 0xF, 0xF, false));
+  v = ::max(v, __builtin_amdgcn_update_dpp(v, v, 0x141, 0xF, 0xF, false));
+  v = ::max(v, __builtin_amdgcn_update_dpp(v, v, 0x140, 0xF, 0xF, false));
+  return v;
+}
 
 // Attention of one (batch row b, kv head kvh) over its G query heads, whose
 // int8 rows sit at qsrc[hh * 128] and DI-Exp constants at tsrc[hh] (global
-// memory or LDS). 256 threads.
+// memory or LDS). 256 threads = 4 waves.
+//
+// Scores and P.V run on v_mfma_i32_16x16x64_i8 with the G query heads as the
+// 16 MFMA rows (rows >= G zero):
+//   * scores: C[hh][slot] = sum_d q[hh][d] k[slot][d]; a wave takes blocks of
+//     16 slots, B-fragment lane l = slot l % 16, bytes 16 (l / 16) (+ 64) of
+//     the slot's K row (two MFMAs over the 128 channels);
+//   * P.V with the prefill's exact hi/lo split of p in [0, 2^14]:
+//     p = 128 hi + lo, sum p v = 128 (sum (hi - 64) v + 64 colsum v) + sum lo v;
+//     A rows hh < G hold hi - 64 (resp. lo) of 64 consecutive slots, and row G
+//     of the hi product holds ones, so C_hi[G][d] = colsum v over exactly the
+//     slots of the B fragments; B-fragment lane l = channel l % 16, slots
+//     16 (l / 16) .. + 15 of V^T (slot-contiguous). Wave w owns channels
+//     32w .. 32w + 31 (two 16-channel blocks).
+// Slots past S read zero V fragments (16-slot chunks starting at or past S),
+// so their A values do not matter; the p of slots S .. ceil16(S) are 0.
+// |accumulators| <= 128 * 128 * S < 2^31 for S <= 131071.
 template <int G>
 __device__ __forceinline__ void decode_body(const DecodeArgs& a, int kvh, int b,
                                             const int8_t* qsrc, const int64_t* tsrc,
                                             int32_t* sh_scores) {
+  static_assert(G <= 8, "query heads per kv head");
   __shared__ i64 red_buf[32];
   BlockRed red{red_buf, 0};
-  __shared__ i64 pv_acc[G][128];
-  const int tid = threadIdx.x, lane = tid & 63;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int l16 = lane & 15, grp = lane >> 4;
   int S = a.S;
   if (a.s_dev) {
     const i64 sd = a.s_dev[0];
@@ -286,134 +313,165 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, int kvh, int b,
   const int8_t* kbase = a.kc + ((i64)b * a.n_kv + kvh) * a.cap * 128;
   const int8_t* vbase = a.vc + ((i64)b * a.n_kv + kvh) * 128 * a.cap;
   const uint8_t* vrow = a.valid + (i64)b * a.valid_stride;
+  const int nstep = (S + 63) / 64;  // 64-slot steps of P.V
 
-  // P.V ownership: thread (d, half) sums slot chunks [cbeg, cend) of channel d.
-  // Its first VPRE chunks of V are loaded now, overlapping the score passes.
-  const int d = tid & 127, half = tid >> 7;
-  const int nchunk = (S + 15) / 16;
-  const int per = (nchunk + 1) / 2;
-  const int cbeg = half * per, cend = min(nchunk, cbeg + per);
-  const int8_t* vr = vbase + (i64)d * a.cap;
-  v4i vpre[VPRE];
+  // V fragments of the first VPRE steps, loaded now to overlap the scores
+  const int8_t* vch[2];
+#pragma unroll
+  for (int nb = 0; nb < 2; ++nb) vch[nb] = vbase + (i64)(wave * 32 + nb * 16 + l16) * a.cap;
+  auto vfrag = [&](int st, int nb) -> v4i {
+    const int s0 = st * 64 + grp * 16;
+    return s0 < S ? *(const v4i*)(vch[nb] + s0) : v4i{0, 0, 0, 0};
+  };
+  v4i vpre[VPRE][2];
 #pragma unroll
   for (int i = 0; i < VPRE; ++i)
-    vpre[i] = cbeg + i < cend ? *(const v4i*)(vr + (cbeg + i) * 16) : v4i{0, 0, 0, 0};
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb) vpre[i][nb] = vfrag(i, nb);
 
-  // ---- pass 1: scores (8 lanes per slot, 16 bytes each), masked slots
-  // marked, row max over visible slots. 256 slots per batch of loads.
-  const int sub = lane & 7;
-  v4i qv[G];
-  i64 tp[G];
-#pragma unroll
-  for (int hh = 0; hh < G; ++hh) {
-    qv[hh] = *(const v4i*)(qsrc + hh * 128 + sub * 16);
-    tp[hh] = tsrc[hh];
+  // query fragments (row l16 = head) and the heads' DI-Exp constants
+  v4i qa0 = v4i{0, 0, 0, 0}, qa1 = v4i{0, 0, 0, 0};
+  if (l16 < G) {
+    qa0 = *(const v4i*)(qsrc + l16 * 128 + grp * 16);
+    qa1 = *(const v4i*)(qsrc + l16 * 128 + 64 + grp * 16);
   }
-  i64 mx[G];
+  ExpR E[G];
 #pragma unroll
-  for (int hh = 0; hh < G; ++hh) mx[hh] = NEG_SENTINEL;
-  for (int s0 = 0; s0 < S; s0 += 256) {
-    v4i kv[8];
-    int vf[8];
+  for (int hh = 0; hh < G; ++hh) E[hh] = make_exp(tsrc[hh]);
+
+  // ---- pass 1: scores on MFMA; masked slots marked; per-head row max.
+  // Lane (grp, l16) holds C[4 grp + r][slot l16] in element r.
+  int32_t mx[4] = {SCORE_MASKED, SCORE_MASKED, SCORE_MASKED, SCORE_MASKED};
+  const int nblk = (S + 15) / 16;
+  for (int blk0 = wave; blk0 < nblk; blk0 += 16) {
+    v4i kb[4][2];
+    int vf[4];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const int s = s0 + u * 32 + (tid >> 3);
+    for (int u = 0; u < 4; ++u) {
+      const int s = (blk0 + u * 4) * 16 + l16;
       const int sc_ = s < S ? s : 0;
-      kv[u] = *(const v4i*)(kbase + (i64)sc_ * 128 + sub * 16);
+      kb[u][0] = *(const v4i*)(kbase + (i64)sc_ * 128 + grp * 16);
+      kb[u][1] = *(const v4i*)(kbase + (i64)sc_ * 128 + 64 + grp * 16);
       vf[u] = vrow[sc_];
     }
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const int s = s0 + u * 32 + (tid >> 3);
-      const bool in = s < S;
-      const bool vis = in && vf[u] != 0;
+    for (int u = 0; u < 4; ++u) {
+      const int blk = blk0 + u * 4;
+      if (blk < nblk) {  // wave-uniform
+        v4i c = mfma16(qa0, kb[u][0], v4i{0, 0, 0, 0});
+        c = mfma16(qa1, kb[u][1], c);
+        const int s = blk * 16 + l16;
+        const bool vis = s < S && vf[u] != 0;
 #pragma unroll
-      for (int hh = 0; hh < G; ++hh) {
-        int dd = 0;
-#pragma unroll
-        for (int q = 0; q < 4; ++q) dd = __builtin_amdgcn_sdot4(kv[u][q], qv[hh][q], dd, false);
-        dd = sum8_i32(dd);
-        if (in && sub == 0) sc[hh * Spad + s] = vis ? dd : SCORE_MASKED;
-        if (vis) mx[hh] = imax(mx[hh], (i64)dd);
+        for (int r = 0; r < 4; ++r) {
+          const int hh = grp * 4 + r;
+          if (hh < G) {
+            if (s < S) sc[hh * Spad + s] = vis ? c[r] : SCORE_MASKED;
+            if (vis) mx[r] = ::max(mx[r], c[r]);
+          }
+        }
       }
     }
   }
+  i64 hmax[G];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) mx[r] = row16_max(mx[r]);
 #pragma unroll
   for (int hh = 0; hh < G; ++hh) {
-    mx[hh] = red.max(mx[hh]);
-    if (mx[hh] == NEG_SENTINEL) mx[hh] = 0;
+    // head hh lives in lanes 16 (hh / 4) .. + 15, element hh % 4
+    const int32_t mine = grp == hh / 4 ? mx[hh % 4] : SCORE_MASKED;
+    const i64 m = red.max((i64)mine);
+    hmax[hh] = m == (i64)SCORE_MASKED ? 0 : m;  // no visible slot: max := 0, every p = 0
   }
   __syncthreads();
   // ---- pass 2: denominators
   i64 den[G];
 #pragma unroll
   for (int hh = 0; hh < G; ++hh) {
-    const ExpR E = make_exp(tp[hh]);
     i64 acc = 0;
     for (int s = tid; s < S; s += 256) {
       const int32_t x = sc[hh * Spad + s];
-      if (x != SCORE_MASKED) acc = wadd(acc, di_exp_neg((u64)wsub(mx[hh], (i64)x), E));
+      if (x != SCORE_MASKED) acc = wadd(acc, di_exp_neg((u64)wsub(hmax[hh], (i64)x), E[hh]));
     }
     den[hh] = imax(red.sum(acc), 1);
   }
-  // ---- pass 3: probabilities in [0, 2^14] (in place of the scores; 0 for
-  // masked slots and the padding up to the next multiple of 16)
+  // ---- pass 3: p in [0, 2^14] as (hi - 64) | lo << 8 in place of the score
+  // (0 for masked slots and the padding up to the next multiple of 16, i.e.
+  // hi - 64 = -64, lo = 0)
+  const int nchunk = (S + 15) / 16;
 #pragma unroll
   for (int hh = 0; hh < G; ++hh) {
-    const ExpR E = make_exp(tp[hh]);
     const Recip Rd = make_recip(den[hh]);
     for (int s = tid; s < nchunk * 16; s += 256) {
       i64 p = 0;
       if (s < S) {
         const int32_t x = sc[hh * Spad + s];
         if (x != SCORE_MASKED) {
-          const i64 ex = di_exp_neg((u64)wsub(mx[hh], (i64)x), E);
+          const i64 ex = di_exp_neg((u64)wsub(hmax[hh], (i64)x), E[hh]);
           p = to_i32(rhad_r(shl(ex, 14), Rd));
         }
       }
-      sc[hh * Spad + s] = (int32_t)p;
+      const int hi = (int)(p >> 7), lo = (int)(p & 127);
+      sc[hh * Spad + s] = (int32_t)((uint32_t)(uint8_t)(int8_t)(hi - 64) | ((uint32_t)lo << 8));
     }
   }
   __syncthreads();
-  // ---- P.V: sum_s p_s v_s. |sum| <= 128 * (2^14 + S) < 2^31, so int32
-  // accumulation is exact; chunks beyond the prefetched ones load 8 at a time.
-  int32_t acc[G];
-#pragma unroll
-  for (int hh = 0; hh < G; ++hh) acc[hh] = 0;
-  auto chunk_dot = [&](int c, const v4i& vv) {
-#pragma unroll
-    for (int hh = 0; hh < G; ++hh) {
-      const int32_t* pp = sc + hh * Spad + c * 16;
-      int32_t s = 0;
+  // ---- P.V on MFMA
+  v4i chi[2] = {v4i{0, 0, 0, 0}, v4i{0, 0, 0, 0}}, clo[2] = {v4i{0, 0, 0, 0}, v4i{0, 0, 0, 0}};
+  auto pv_step = [&](int st, const v4i (&vb)[2]) {
+    v4i ahi = v4i{0, 0, 0, 0}, alo = v4i{0, 0, 0, 0};
+    const int s0 = st * 64 + grp * 16;
+    if (l16 < G && s0 < S) {
+      const int32_t* pp = sc + l16 * Spad + s0;  // 16 packed p of head l16
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        const int w = vv[q];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) s += pp[q * 4 + r] * (int32_t)(int8_t)((w >> (8 * r)) & 0xff);
+        const v4i w = *(const v4i*)(pp + 4 * q);
+        // bytes 0 of the four words -> hi - 64 fragment, bytes 1 -> lo
+        const uint32_t h01 = __builtin_amdgcn_perm((uint32_t)w[1], (uint32_t)w[0], 0x0c0c0400u);
+        const uint32_t h23 = __builtin_amdgcn_perm((uint32_t)w[3], (uint32_t)w[2], 0x04000c0cu);
+        const uint32_t l01 = __builtin_amdgcn_perm((uint32_t)w[1], (uint32_t)w[0], 0x0c0c0501u);
+        const uint32_t l23 = __builtin_amdgcn_perm((uint32_t)w[3], (uint32_t)w[2], 0x05010c0cu);
+        ahi[q] = (int)(h01 | h23);
+        alo[q] = (int)(l01 | l23);
       }
-      acc[hh] += s;
+    } else if (l16 == G) {
+      ahi = v4i{0x01010101, 0x01010101, 0x01010101, 0x01010101};  // colsum row
+    }
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb) {
+      chi[nb] = mfma16(ahi, vb[nb], chi[nb]);
+      clo[nb] = mfma16(alo, vb[nb], clo[nb]);
     }
   };
 #pragma unroll
   for (int i = 0; i < VPRE; ++i)
-    if (cbeg + i < cend) chunk_dot(cbeg + i, vpre[i]);
-  for (int c0 = cbeg + VPRE; c0 < cend; c0 += 8) {
-    v4i vv[8];
+    if (i < nstep) pv_step(i, vpre[i]);
+  for (int st0 = VPRE; st0 < nstep; st0 += 4) {
+    v4i vb[4][2];
 #pragma unroll
-    for (int i = 0; i < 8; ++i)
-      vv[i] = *(const v4i*)(vr + (c0 + i < cend ? c0 + i : c0) * 16);
+    for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int i = 0; i < 8; ++i)
-      if (c0 + i < cend) chunk_dot(c0 + i, vv[i]);
+      for (int nb = 0; nb < 2; ++nb) vb[i][nb] = st0 + i < nstep ? vfrag(st0 + i, nb) : v4i{0, 0, 0, 0};
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      if (st0 + i < nstep) pv_step(st0 + i, vb[i]);
   }
-  if (half == 1)
+  // lane (grp, l16), element r: head 4 grp + r, channel 32 wave + 16 nb + l16;
+  // the colsum of that channel sits in row G: lane 16 (G / 4) + l16, element G % 4
 #pragma unroll
-    for (int hh = 0; hh < G; ++hh) pv_acc[hh][d] = acc[hh];
-  __syncthreads();
-  if (half == 0)
+  for (int nb = 0; nb < 2; ++nb) {
+    const int cs_src = (G / 4) * 16 + l16;
+    const int32_t cs = __shfl(chi[nb][G % 4], cs_src, 64);
+    const int d = wave * 32 + nb * 16 + l16;
 #pragma unroll
-    for (int hh = 0; hh < G; ++hh)
-      a.out[(i64)b * a.n_q * 128 + (kvh * G + hh) * 128 + d] = (i64)acc[hh] + pv_acc[hh][d];
+    for (int r = 0; r < 4; ++r) {
+      const int hh = grp * 4 + r;
+      if (hh < G) {
+        const i64 v = ((i64)chi[nb][r] + 64 * (i64)cs) * 128 + (i64)clo[nb][r];
+        a.out[(i64)b * a.n_q * 128 + (kvh * G + hh) * 128 + d] = v;
+      }
+    }
+  }
 }
 
 template <int G>
@@ -476,7 +534,7 @@ int detllm_attn_decode(const int8_t* q8, const int64_t* tpos, const int8_t* kc, 
     return DI_EINVAL;
   const int G = n_q / n_kv;
   if (G > MAXG) return DI_ENOSYS;
-  if (S > (1 << 24)) return DI_ERANGE;  // int32 P.V accumulators
+  if (S > DEC_MAX_S) return DI_ERANGE;  // int32 MFMA accumulators of P.V
   const i64 Spad = ((i64)S + 15) & ~15;
   const i64 lds = (i64)G * Spad * 4;
   size_t dyn = 0;

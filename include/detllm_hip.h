@@ -152,9 +152,10 @@ int detllm_attn_prefill(const int8_t* q8, const int64_t* tpos, const int8_t* kca
                         hipStream_t s);
 
 /* Decode attention (one query per row) — model.py:347-381 and the fused
- * Triton kernel ops/fused_attn.py:47-142 it replaces. Scans S slots (further
- * bounded by *s_dev when non-null); scratch [B][n_q][ceil16(S)] int32 is
- * required only when n_q/n_kv * ceil16(S) * 4 > 48 KiB. out [B][n_q*128]. */
+ * Triton kernel ops/fused_attn.py:47-142 it replaces. Scans S <= 131071 slots
+ * (further bounded by *s_dev when non-null); scratch [B][n_q][ceil16(S)]
+ * int32 is required only when n_q/n_kv * ceil16(S) * 4 > 48 KiB.
+ * out [B][n_q*128]. */
 int detllm_attn_decode(const int8_t* q8, const int64_t* tpos, const int8_t* kcache,
                        const int8_t* vcache, const uint8_t* valid, int64_t valid_stride, int B,
                        int S, int n_q, int n_kv, int64_t cap, const int64_t* s_dev,
