@@ -31,18 +31,11 @@
 //                 in int64 with the lowest-id tie-break.
 
 #include "common.h"
+#include "gemv.h"
 
 using namespace di;
 
-typedef int v4i __attribute__((ext_vector_type(4)));
-
 namespace {
-
-__device__ __forceinline__ v4i mfma16(v4i a, v4i b, v4i c) {
-  return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
-}
-
-__device__ __forceinline__ v4i zero4() { return v4i{0, 0, 0, 0}; }
 
 constexpr int TBM = 128, TBN = 128, TBK = 64, TPAD = 16;
 
@@ -283,115 +276,13 @@ __global__ __launch_bounds__(64 * WGM * WGN, MINB) void k_gemm_nt2(const int8_t*
     }
 }
 
-// Skinny GEMM (decode GEMV), M <= 64 rows, C[ks][M][N] = A[M][Kchunk] . B[N][Kchunk]^T.
-//
-// A wave computes one 16-column group over a K range with
-// v_mfma_i32_16x16x64_i8. Lane l supplies column (l % 16) and U consecutive
-// 16-byte K slices starting at 16*U*(l / 16): a wave-load then reads 16U*4
-// contiguous bytes of each of its 16 weight rows (whole 128-byte lines for
-// U >= 2). The K order inside an MFMA does not matter as long as A and B use
-// the same one, so A is loaded with the identical mapping.
-//
-// Latency is what bounds these launches (a decode layer's matrices are 1-6 MB),
-// so each wave issues all loads of NB iterations before the first MFMA.
-// KW waves of a block split the K range of one column group and reduce their
-// int32 accumulators through LDS; with KW == 1 the 4 waves own 4 column groups.
-// Up to four byte ranges that the kernels after this launch read (their
-// per-column scale vectors): each thread of the first K split touches one
-// 128-byte line of them, so they are fetched into the memory-side cache while
-// this launch streams its weights and the next launch finds them there.
-// A performance hint only: the loaded words are discarded (stored to `sink`
-// only when it is non-null, which keeps the loads), results do not change.
-struct Prefetch {
-  const int8_t* p[4];
-  i64 n[4];  // bytes; 0 = unused
-  int32_t* sink;
-};
-
-__device__ __forceinline__ void prefetch_lines(const Prefetch& pf, i64 t) {
-  int32_t v = 0;
-  bool hit = false;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const i64 lines = (pf.n[i] + 127) >> 7;
-    if (t >= 0 && t < lines) {  // offset 128 t < n, and n is a multiple of 4
-      v = *(const int32_t*)(pf.p[i] + (t << 7));
-      hit = true;
-    }
-    t -= lines;
-  }
-  if (hit && pf.sink) *pf.sink = v;
-}
-
+// Skinny GEMM (decode GEMV), M <= 64 rows: the tile of gemv.h, one
+// 256-thread block per (column group, K range).
 template <int MB, int KW, int NB>
-__global__ __launch_bounds__(256) void k_gemv_nt(const int8_t* __restrict__ A,
-                                                 const int8_t* __restrict__ B,
-                                                 int32_t* __restrict__ C, int M, int N, int K,
-                                                 int kchunk, i64 split_stride, Prefetch pf) {
+__global__ __launch_bounds__(256) void k_gemv_nt(GemvArgs g, Prefetch pf) {
+  __shared__ GemvLds<MB, KW> lds;
   if (blockIdx.y == 0) prefetch_lines(pf, (i64)blockIdx.x * blockDim.x + threadIdx.x);
-  constexpr int U = 4;                 // 16-byte slices per lane per iteration
-  constexpr int CG = 4 / KW;           // column groups per block
-  constexpr int KSTEP = 64 * U;        // K covered by one wave-iteration
-  __shared__ int32_t red[KW > 1 ? (KW - 1) * CG : 1][MB * 4][64];
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  const int cg = wave % CG, kw = wave / CG;
-  const int r16 = lane & 15, g = lane >> 4;
-  const int col = (blockIdx.x * CG + cg) * 16 + r16;
-  const bool colok = col < N;
-  const int kbeg = blockIdx.y * kchunk;
-  const int kend = min(K, kbeg + kchunk);
-  const int8_t* brow = B + (i64)(colok ? col : 0) * K;
-  v4i acc[MB];
-#pragma unroll
-  for (int mb = 0; mb < MB; ++mb) acc[mb] = zero4();
-  for (int k0 = kbeg + kw * KSTEP; k0 < kend; k0 += KSTEP * KW * NB) {
-    v4i b[NB][U], a[NB][U][MB];
-#pragma unroll
-    for (int nb = 0; nb < NB; ++nb)
-#pragma unroll
-      for (int u = 0; u < U; ++u) {
-        const int kk = k0 + nb * KSTEP * KW + g * 16 * U + u * 16;
-        const bool kok = kk < kend;
-        b[nb][u] = (colok && kok) ? *(const v4i*)(brow + kk) : zero4();
-#pragma unroll
-        for (int mb = 0; mb < MB; ++mb) {
-          const int row = mb * 16 + r16;
-          a[nb][u][mb] = (row < M && kok) ? *(const v4i*)(A + (i64)row * K + kk) : zero4();
-        }
-      }
-#pragma unroll
-    for (int nb = 0; nb < NB; ++nb)
-#pragma unroll
-      for (int u = 0; u < U; ++u)
-#pragma unroll
-        for (int mb = 0; mb < MB; ++mb) acc[mb] = mfma16(a[nb][u][mb], b[nb][u], acc[mb]);
-  }
-  if (KW > 1) {
-    if (kw > 0) {
-#pragma unroll
-      for (int mb = 0; mb < MB; ++mb)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) red[(kw - 1) * CG + cg][mb * 4 + r][lane] = acc[mb][r];
-    }
-    __syncthreads();
-    if (kw > 0) return;
-#pragma unroll
-    for (int mb = 0; mb < MB; ++mb)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        int32_t s = acc[mb][r];
-#pragma unroll
-        for (int w = 0; w < KW - 1; ++w) s += red[w * CG + cg][mb * 4 + r][lane];
-        acc[mb][r] = s;
-      }
-  }
-#pragma unroll
-  for (int mb = 0; mb < MB; ++mb)
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int row = mb * 16 + g * 4 + r;
-      if (row < M && colok) C[blockIdx.y * split_stride + (i64)row * N + col] = acc[mb][r];
-    }
+  gemv_block<MB, KW, NB>(g, blockIdx.x, blockIdx.y, lds);
 }
 
 __global__ void k_transpose_i8(const int8_t* __restrict__ src, int8_t* __restrict__ dst, int R,
@@ -485,8 +376,8 @@ int gemv_plan(int N, int K) {
 template <int MB, int KW, int NB>
 void launch_gemv(dim3 grid, hipStream_t s, const int8_t* A, const int8_t* B, int32_t* C,
                         int M, int N, int K, int kchunk, i64 split_stride, const Prefetch& pf) {
-  hipLaunchKernelGGL((k_gemv_nt<MB, KW, NB>), grid, dim3(256), 0, s, A, B, C, M, N, K, kchunk,
-                     split_stride, pf);
+  const GemvArgs g{A, B, C, M, N, K, kchunk, split_stride};
+  hipLaunchKernelGGL((k_gemv_nt<MB, KW, NB>), grid, dim3(256), 0, s, g, pf);
 }
 
 // Skinny GEMM for M <= 64: writes ksplit int32 partials C[ks][M][N]
@@ -499,8 +390,7 @@ int igemv(const int8_t* A, const int8_t* B, int32_t* C, int M, int N, int K, int
   if (M > 64 || K <= 0 || (K % 16) != 0 || K > 131071 || ksplit < 1 || !A || !B || !C)
     return DI_EINVAL;
   if (ksplit > 1 && split_stride < (int64_t)M * N) return DI_EINVAL;
-  int kchunk = (K + ksplit - 1) / ksplit;
-  kchunk = (kchunk + 63) / 64 * 64;
+  const int kchunk = gemv_kchunk(K, ksplit);
   const int nsp = (K + kchunk - 1) / kchunk;
   if (nsp != ksplit) return DI_EINVAL;  // caller must size partial buffers to ksplit
   const dim3 grid((N + 15) / 16, ksplit);

@@ -258,10 +258,7 @@ struct ResNormArgs {
 };
 
 template <int VPT>
-__global__ __launch_bounds__(RT_WIDE) void k_residual_normq(ResNormArgs a) {
-  __shared__ i64 red_buf[32];
-  BlockRed red{red_buf, 0};
-  const int r = blockIdx.x;
+__device__ __forceinline__ void residual_normq_row(const ResNormArgs& a, int r, BlockRed& red) {
   const int C = a.C;
   const i64 off = (i64)r * C;
   i64 h[VPT], d[VPT], smv[VPT];
@@ -329,6 +326,13 @@ __global__ __launch_bounds__(RT_WIDE) void k_residual_normq(ResNormArgs a) {
   quant_row(h, 1, kq, C, red, a.x8 + off, a.xm + r, a.xk + r);
 }
 
+template <int VPT>
+__global__ __launch_bounds__(RT_WIDE) void k_residual_normq(ResNormArgs a) {
+  __shared__ i64 red_buf[32];
+  BlockRed red{red_buf, 0};
+  residual_normq_row<VPT>(a, blockIdx.x, red);
+}
+
 struct SwigluArgs {
   int I;
   const int32_t* P;  // [nsplit][R][2I]: gate | up
@@ -348,10 +352,7 @@ struct SwigluArgs {
 };
 
 template <int VPT>
-__global__ __launch_bounds__(RT_WIDE) void k_swiglu_quant(SwigluArgs a) {
-  __shared__ i64 red_buf[32];
-  BlockRed red{red_buf, 0};
-  const int r = blockIdx.x;
+__device__ __forceinline__ void swiglu_quant_row(const SwigluArgs& a, int r, BlockRed& red) {
   const int I = a.I;
   i64 gm[VPT], um[VPT], dsm[VPT];
   prefetch_cols(gm, a.gate_m, I);
@@ -371,6 +372,13 @@ __global__ __launch_bounds__(RT_WIDE) void k_swiglu_quant(SwigluArgs a) {
   quant_row(gu[0], ym, yk, I, red, a.y8 + (i64)r * I, a.ym + r, a.yk + r);
 }
 
+template <int VPT>
+__global__ __launch_bounds__(RT_WIDE) void k_swiglu_quant(SwigluArgs a) {
+  __shared__ i64 red_buf[32];
+  BlockRed red{red_buf, 0};
+  swiglu_quant_row<VPT>(a, blockIdx.x, red);
+}
+
 struct MergeArgs {
   int C;
   const int64_t* attn;  // [nsplit][R][C]
@@ -386,10 +394,7 @@ struct MergeArgs {
 };
 
 template <int VPT>
-__global__ __launch_bounds__(RT_WIDE) void k_merge_rowcol(MergeArgs a) {
-  __shared__ i64 red_buf[32];
-  BlockRed red{red_buf, 0};
-  const int r = blockIdx.x;
+__device__ __forceinline__ void merge_rowcol_row(const MergeArgs& a, int r, BlockRed& red) {
   const int C = a.C;
   const i64 off = (i64)r * C;
   i64 v[VPT], om[VPT], cm[VPT];
@@ -432,6 +437,13 @@ __global__ __launch_bounds__(RT_WIDE) void k_merge_rowcol(MergeArgs a) {
     a.am[r] = mo;
     a.ak[r] = wsub(wadd(wadd(a.os_k, a.col_k), e), sh);
   }
+}
+
+template <int VPT>
+__global__ __launch_bounds__(RT_WIDE) void k_merge_rowcol(MergeArgs a) {
+  __shared__ i64 red_buf[32];
+  BlockRed red{red_buf, 0};
+  merge_rowcol_row<VPT>(a, blockIdx.x, red);
 }
 
 __global__ __launch_bounds__(RT) void k_qkv_epilogue(QKVArgs a) {
