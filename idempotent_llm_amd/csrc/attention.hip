@@ -50,7 +50,7 @@ struct PrefillArgs {
   const int8_t* vc;      // [B][n_kv][128][cap]
   const uint8_t* valid;  // [B][valid_stride]
   int64_t* out;          // [B][T][n_q * 128]
-  int T, S, S_past, n_q, n_kv;
+  int T, S, S_past, n_q, n_kv, B;
   i64 cap, valid_stride;
 };
 
@@ -61,8 +61,18 @@ __global__ __launch_bounds__(256) void k_attn_prefill(PrefillArgs a) {
   __shared__ __attribute__((aligned(16))) int8_t Ks[64 * KS_STRIDE];
   __shared__ __attribute__((aligned(16))) int8_t Vs[128 * VS_STRIDE];
   __shared__ uint8_t vflag[64];
-  const int qt = gridDim.x - 1 - blockIdx.x;  // heaviest (latest) query tiles first
-  const int h = blockIdx.y, b = blockIdx.z;
+  // Causal work per query tile grows with its index. Blocks come in two
+  // halves of `pairs` blocks: the first half takes the heavy tiles
+  // (nqt - 1 - k), dispatched first, the second their light partners (k), so
+  // the two blocks a CU holds together add up to about the same work
+  // whatever k they have. The middle tile of an odd count appears once.
+  const int nqt = (a.T + 63) / 64, np = (nqt + 1) / 2;
+  const int pairs = np * a.n_q * a.B;
+  const int half = blockIdx.x >= pairs, p = blockIdx.x - half * pairs;
+  const int k = p % np, hb = p / np;
+  if (half && k == nqt - 1 - k) return;  // middle tile: done by the first half
+  const int qt = half ? k : nqt - 1 - k;
+  const int h = hb % a.n_q, b = hb / a.n_q;
   const int group = a.n_q / a.n_kv;
   const int kvh = h / group;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
@@ -515,8 +525,10 @@ int detllm_attn_prefill(const int8_t* q8, const int64_t* tpos, const int8_t* kc,
       valid_stride < S)
     return DI_EINVAL;
   if (S > 131071) return DI_ERANGE;  // int32 MFMA accumulators of P.V
-  PrefillArgs a{q8, tpos, kc, vc, valid, out, T, (int)S, S_past, n_q, n_kv, cap, valid_stride};
-  hipLaunchKernelGGL(k_attn_prefill, dim3((T + 63) / 64, n_q, B), dim3(256), 0, s, a);
+  PrefillArgs a{q8, tpos, kc, vc, valid, out, T, (int)S, S_past, n_q, n_kv, B, cap, valid_stride};
+  const i64 pairs = (i64)(((T + 63) / 64 + 1) / 2) * n_q * B;
+  if (2 * pairs > 0x7fffffff) return DI_ERANGE;
+  hipLaunchKernelGGL(k_attn_prefill, dim3((unsigned)(2 * pairs)), dim3(256), 0, s, a);
   DI_LAUNCH_CHECK();
   return DI_OK;
 }
