@@ -28,6 +28,8 @@
 // its group; scores live in LDS (or a global scratch when they do not fit);
 // every reduction is an exact integer max/sum.
 
+#include <type_traits>
+
 #include "common.h"
 #include "qkv_epilogue.h"
 
@@ -36,8 +38,6 @@ using namespace di;
 typedef int v4i __attribute__((ext_vector_type(4)));
 
 namespace {
-
-constexpr i64 NEG_SENTINEL = INT64_MIN + 1;
 
 __device__ __forceinline__ v4i mfma16(v4i a, v4i b, v4i c) {
   return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
@@ -54,13 +54,90 @@ struct PrefillArgs {
   i64 cap, valid_stride;
 };
 
-constexpr int KS_STRIDE = 128 + 16;
-constexpr int VS_STRIDE = 64 + 16;
+constexpr int PF_KBYTES = 64 * 128;       // K tile: 64 slot rows of 128 B
+constexpr int PF_VBYTES = 128 * 64;       // V^T tile: 128 dim rows of 64 B
+constexpr int PF_RING = 32 * 1024;        // 4 K stages, or 2 K+V stages
+constexpr int PF_CSUM = 128 * 4;          // column sums of V (int32 per dim)
+constexpr uint32_t PF_SMALL_T = 1u << 23;  // 24-bit DI-Exp below this tpos
+constexpr i64 PF_SMALL_DEN = (i64)1 << 30;  // float-estimated p below this den
 
-__global__ __launch_bounds__(256) void k_attn_prefill(PrefillArgs a) {
-  __shared__ __attribute__((aligned(16))) int8_t Ks[64 * KS_STRIDE];
-  __shared__ __attribute__((aligned(16))) int8_t Vs[128 * VS_STRIDE];
-  __shared__ uint8_t vflag[64];
+// 16-byte chunk swizzles of the LDS tiles (physical chunk = logical ^ swz).
+// K rows (128 B): the 16 rows one MFMA reads with a chunk (rows
+// 16(i/4) + 4 blk + i%4, i = 0..15) fall on distinct banks both 8 and 16
+// lanes at a time. V^T rows (64 B): dims 16 j + i, i = 0..15, likewise.
+__device__ __forceinline__ int pf_kswz(int row) {
+  return ((row ^ (row >> 5)) & 1) | (row & 2) | ((row >> 2) & 4);
+}
+__device__ __forceinline__ int pf_vswz(int d) { return ((d >> 1) ^ (d >> 3)) & 3; }
+
+// The 24-bit multiplier (full rate; the 32-bit multiplies issue at a quarter
+// of it). Written out because the compiler cannot see the operand bounds
+// across the loop blocks and would pick the 32-bit forms.
+__device__ __forceinline__ uint32_t mul_u24(uint32_t a, uint32_t b) {
+  uint32_t d;
+  asm("v_mul_u32_u24 %0, %1, %2" : "=v"(d) : "v"(a), "v"(b));
+  return d;
+}
+__device__ __forceinline__ uint32_t mulhi_u24(uint32_t a, uint32_t b) {
+  uint32_t d;
+  asm("v_mul_hi_u32_u24 %0, %1, %2" : "=v"(d) : "v"(a), "v"(b));
+  return d;
+}
+
+// DI-Exp of -n (ops/di_exp.py:27-37) for 0 <= n < 2^22 and 1 <= t < 2^23.
+// Every score difference qualifies: |q8 . k8| <= 2^21. q = floor(n / t) from
+// r24 = floor((2^24 - 1) / t) on the 24-bit multiplier is exact or one short
+// (n r24 / 2^24 lies in (n / t - 1/2, n / t)), fixed by one remainder step;
+// the result (t - ceil(rem / 2)) >> q is below 2^23, so the shift clamped to
+// 31 gives the same 0 as min(q, 62) for every q >= 23.
+__device__ __forceinline__ uint32_t pf_dexp24(uint32_t n, uint32_t t, uint32_t r24) {
+  uint32_t q = __builtin_amdgcn_alignbit(mulhi_u24(n, r24), mul_u24(n, r24), 24);
+  uint32_t rem = n - mul_u24(q, t);  // in [0, 2t)
+  if (rem >= t) {
+    q += 1;
+    rem -= t;
+  }
+  const uint32_t u = t - ((rem + 1) >> 1);
+  return u >> min(q, 31u);
+}
+
+// p = round_half_away_div(ex << 14, den) = floor((ex 2^14 + floor(den / 2)) /
+// den) for 0 <= ex <= den < 2^30, ex < 2^24. fma(ex, rf, 1/2) with rf =
+// fl(2^14 / den) is within 2^-10 (reciprocal) + 2^-10 (fma rounding) + 1/2
+// (versus floor(den / 2) / den) of the exact quotient, so its truncation q is
+// off by at most one either way; the remainder lies in [-den, 2 den), inside
+// the int32 range, so 32-bit wrapping arithmetic gives it exactly (q den mod
+// 2^32 from the 24-bit halves of den: q <= 2^14 + 1).
+__device__ __forceinline__ uint32_t pf_pdiv(uint32_t ex, float rf, uint32_t dlo, uint32_t dhi,
+                                            uint32_t den, uint32_t hd) {
+  uint32_t q = (uint32_t)fmaf((float)ex, rf, 0.5f);
+  const uint32_t qd = mul_u24(q, dlo) + (mul_u24(q, dhi) << 24);
+  const int32_t rem = (int32_t)((ex << 14) + hd - qd);
+  q += rem >= (int32_t)den ? 1u : 0u;
+  q -= rem < 0 ? 1u : 0u;
+  return q;
+}
+
+// Four probabilities (slot order = byte order) as the two MFMA operands of
+// the hi/lo split p = 128 hi + lo: bytes hi - 64 = (p - 8192) >> 7 in
+// [-64, 64] (byte 1 of 2p - 16384) and lo = p & 127.
+__device__ __forceinline__ void pf_pack(const uint32_t (&p)[4], int& whi, int& wlo) {
+  uint32_t y[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) y[r] = (p[r] << 1) - 16384u;
+  const uint32_t h01 = __builtin_amdgcn_perm(y[1], y[0], 0x0c0c0501u);
+  const uint32_t h23 = __builtin_amdgcn_perm(y[3], y[2], 0x05010c0cu);
+  const uint32_t l01 = __builtin_amdgcn_perm(p[1], p[0], 0x0c0c0400u);
+  const uint32_t l23 = __builtin_amdgcn_perm(p[3], p[2], 0x04000c0cu);
+  whi = (int)(h01 | h23);
+  wlo = (int)((l01 | l23) & 0x7f7f7f7fu);
+}
+
+__global__ __launch_bounds__(256, 2) void k_attn_prefill(PrefillArgs a) {
+  extern __shared__ __attribute__((aligned(1024))) int8_t smem[];
+  int8_t* const ring = smem;
+  int32_t* const csum_lds = (int32_t*)(smem + PF_RING);
+  u64* const vmask = (u64*)(smem + PF_RING + PF_CSUM);  // per key tile
   // Causal work per query tile grows with its index. Blocks come in two
   // halves of `pairs` blocks: the first half takes the heavy tiles
   // (nqt - 1 - k), dispatched first, the second their light partners (k), so
@@ -68,13 +145,12 @@ __global__ __launch_bounds__(256) void k_attn_prefill(PrefillArgs a) {
   // whatever k they have. The middle tile of an odd count appears once.
   const int nqt = (a.T + 63) / 64, np = (nqt + 1) / 2;
   const int pairs = np * a.n_q * a.B;
-  const int half = blockIdx.x >= pairs, p = blockIdx.x - half * pairs;
-  const int k = p % np, hb = p / np;
-  if (half && k == nqt - 1 - k) return;  // middle tile: done by the first half
-  const int qt = half ? k : nqt - 1 - k;
+  const int half = blockIdx.x >= pairs, pi = blockIdx.x - half * pairs;
+  const int kk = pi % np, hb = pi / np;
+  if (half && kk == nqt - 1 - kk) return;  // middle tile: done by the first half
+  const int qt = half ? kk : nqt - 1 - kk;
   const int h = hb % a.n_q, b = hb / a.n_q;
-  const int group = a.n_q / a.n_kv;
-  const int kvh = h / group;
+  const int kvh = h / (a.n_q / a.n_kv);
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int qi = lane & 15, g = lane >> 4;
   const int t = qt * 64 + wave * 16 + qi;  // this lane's query
@@ -86,165 +162,257 @@ __global__ __launch_bounds__(256) void k_attn_prefill(PrefillArgs a) {
     qf1 = *(const v4i*)(a.q8 + qrow * 128 + 64 + g * 16);
   }
   const i64 tpos = tok ? a.tpos[qrow] : 1;
-  const ExpR Et = make_exp(tpos);
-  const i64 limit = (i64)a.S_past + t;  // last visible slot of this query
+  const int limit = a.S_past + t;              // last visible slot of this query
+  const int wlim = a.S_past + qt * 64 + wave * 16;  // the smallest limit in the wave
   const int kend = min(a.S, a.S_past + qt * 64 + 64);
   const int ntiles = (kend + 63) / 64;
   const int8_t* kbase = a.kc + ((i64)b * a.n_kv + kvh) * a.cap * 128;
   const int8_t* vbase = a.vc + ((i64)b * a.n_kv + kvh) * 128 * a.cap;
   const uint8_t* vrow = a.valid + (i64)b * a.valid_stride;
 
-  // Tiles of 64 slots move global -> registers -> LDS; the next tile's loads
-  // are issued before the current tile's MFMAs and DI-Exp work, so their
-  // latency overlaps the compute.
-  v4i kreg[2], vreg[2];
-  int freg = 0;
-  auto gload_k = [&](int s0) {
+  // validity bitmask of every key tile (bit s - 64 i of tile i: slot s < S
+  // and valid), made once and read by all three passes
+  for (int i0 = wave; i0 < ntiles; i0 += 16) {
+    uint32_t f[4];
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int c = tid + i * 256;
-      const int key = c >> 3, dc = (c & 7) * 16;
-      kreg[i] = v4i{0, 0, 0, 0};
-      if (s0 + key < a.S) kreg[i] = *(const v4i*)(kbase + (i64)(s0 + key) * 128 + dc);
+    for (int u = 0; u < 4; ++u) {
+      const int s = (i0 + 4 * u) * 64 + lane;
+      const uint32_t v = vrow[s < a.S ? s : 0];  // unconditional: one wait for all four
+      f[u] = (i0 + 4 * u < ntiles && s < a.S) ? v : 0u;
     }
-    if (tid < 64) freg = (s0 + tid < a.S) ? vrow[s0 + tid] : 0;
-  };
-  auto sstore_k = [&]() {
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int c = tid + i * 256;
-      const int key = c >> 3, dc = (c & 7) * 16;
-      *(v4i*)&Ks[key * KS_STRIDE + dc] = kreg[i];
+    for (int u = 0; u < 4; ++u) {
+      const u64 m = __ballot(f[u] != 0);
+      if (lane == 0 && i0 + 4 * u < ntiles) vmask[i0 + 4 * u] = m;
     }
-    if (tid < 64) vflag[tid] = (uint8_t)freg;
-  };
-  auto gload_v = [&](int s0) {
+  }
+  wait_vmcnt<0>();  // query operands in registers before the ring's loads count
+
+  // Key tiles stream into an LDS ring with direct-to-LDS loads, issued
+  // STAGES - 1 tiles ahead. K: instruction j of wave w covers tile rows
+  // 8(2w + j) .. +7, lane l row 8(2w + j) + l/8 at physical chunk l % 8.
+  // V^T: dims 16(2w + j) + l/4 at physical chunk l % 4. Rows past the cache
+  // are clamped to its last row or chunk: valid memory whose slots are never
+  // visible (p = 0: their hi byte -64 and the +64 column-sum term cancel).
+  int krow[2], kchk[2], vdim[2], vchk[2];
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int c = tid + i * 256;
-      const int d = c >> 2, blk = c & 3;
-      vreg[i] = v4i{0, 0, 0, 0};
-      if (s0 + blk * 16 < a.cap) vreg[i] = *(const v4i*)(vbase + (i64)d * a.cap + s0 + blk * 16);
+  for (int j = 0; j < 2; ++j) {
+    const int ins = wave * 2 + j;
+    krow[j] = ins * 8 + (lane >> 3);
+    kchk[j] = ((lane & 7) ^ pf_kswz(krow[j])) * 16;
+    vdim[j] = ins * 16 + (lane >> 2);
+    vchk[j] = ((lane & 3) ^ pf_vswz(vdim[j])) * 16;
+  }
+  auto issue = [&](int tile, int8_t* st, bool with_v) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const i64 row = min((i64)tile * 64 + krow[j], a.cap - 1);
+      __builtin_amdgcn_global_load_lds((gbl_ptr_t)(kbase + row * 128 + kchk[j]),
+                                       (lds_ptr_t)(st + (wave * 2 + j) * 1024), 16, 0, 0);
     }
-  };
-  auto sstore_v = [&]() {
+    if (with_v) {
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int c = tid + i * 256;
-      const int d = c >> 2, blk = c & 3;
-      // slot 16*blk + 4*gg + r -> position 16*gg + 4*blk + r
-#pragma unroll
-      for (int gg = 0; gg < 4; ++gg) *(int*)&Vs[d * VS_STRIDE + 16 * gg + 4 * blk] = vreg[i][gg];
-    }
-  };
-  // one pass over the key tiles: body(s0) runs with tile s0 in LDS
-  auto pass = [&](bool with_v, auto&& body) {
-    gload_k(0);
-    if (with_v) gload_v(0);
-    for (int it = 0; it < ntiles; ++it) {
-      __syncthreads();
-      sstore_k();
-      if (with_v) sstore_v();
-      __syncthreads();
-      if (it + 1 < ntiles) {
-        gload_k((it + 1) * 64);
-        if (with_v) gload_v((it + 1) * 64);
+      for (int j = 0; j < 2; ++j) {
+        const i64 s = min((i64)tile * 64 + vchk[j], a.cap - 16);
+        __builtin_amdgcn_global_load_lds((gbl_ptr_t)(vbase + (i64)vdim[j] * a.cap + s),
+                                         (lds_ptr_t)(st + PF_KBYTES + (wave * 2 + j) * 1024),
+                                         16, 0, 0);
       }
-      body(it * 64);
     }
   };
-  // S^T for 4 blocks of 16 slots: st[blk][r] = score(slot s0+16blk+4g+r, query t)
-  auto scores = [&](v4i (&st)[4]) {
+  // one pass over the key tiles; body(it, stage) runs with tile it in LDS.
+  // Each wave waits for its own loads of the tile (vmcnt: loads complete in
+  // order), then one barrier publishes every wave's part and frees the
+  // stage that the next issue overwrites.
+  auto pass = [&](auto kv, auto&& body) {
+    constexpr bool KV = decltype(kv)::value;
+    constexpr int STAGE = KV ? PF_KBYTES + PF_VBYTES : PF_KBYTES;
+    constexpr int ST = PF_RING / STAGE;
+    constexpr int LPT = KV ? 4 : 2;  // loads per tile per wave
+    static_assert(ST >= 2 && ST <= 4, "ring stages");
+    __builtin_amdgcn_s_barrier();  // the previous pass is done with the ring
+#pragma unroll
+    for (int s = 0; s < ST - 1; ++s)
+      if (s < ntiles) issue(s, ring + s * STAGE, KV);
+    for (int it = 0; it < ntiles; ++it) {
+      const int after = min(ST - 2, ntiles - 1 - it);  // tiles issued after `it`
+      if (after >= 2) wait_vmcnt<2 * LPT>();
+      else if (after == 1) wait_vmcnt<LPT>();
+      else wait_vmcnt<0>();
+      __builtin_amdgcn_s_barrier();
+      if (it + ST - 1 < ntiles) issue(it + ST - 1, ring + ((it + ST - 1) % ST) * STAGE, KV);
+      body(it, ring + (it % ST) * STAGE);
+    }
+  };
+
+  // S^T = K . Q^T for one tile: MFMA block blk takes K rows
+  // 16(i/4) + 4 blk + i%4 as its rows i, so lane (qi, g) receives the scores
+  // of query qi for the 16 consecutive slots 16 g + 4 blk + r (blk, r < 4):
+  // st[blk][r]. Those are also the 16 bytes of its P operand for P.V, in
+  // the slot order of the V^T rows.
+  const int kr = 16 * (qi >> 2) + (qi & 3);
+  const int koff0 = kr * 128 + ((g ^ pf_kswz(kr)) << 4);
+  const int koff1 = kr * 128 + (((g + 4) ^ pf_kswz(kr)) << 4);
+  auto scores = [&](const int8_t* st_k, v4i (&st)[4]) {
 #pragma unroll
     for (int blk = 0; blk < 4; ++blk) {
-      const int8_t* kr = &Ks[(blk * 16 + qi) * KS_STRIDE + g * 16];
-      const v4i k0 = *(const v4i*)kr;
-      const v4i k1 = *(const v4i*)(kr + 64);
+      const v4i k0 = *(const v4i*)(st_k + koff0 + blk * 512);
+      const v4i k1 = *(const v4i*)(st_k + koff1 + blk * 512);
       v4i acc = v4i{0, 0, 0, 0};
       acc = mfma16(k0, qf0, acc);
       st[blk] = mfma16(k1, qf1, acc);
     }
   };
-  auto visible = [&](int s0, int blk, int r) -> bool {
-    const int key = blk * 16 + g * 4 + r;
-    const int s = s0 + key;
-    return s < a.S && (i64)s <= limit && vflag[key] != 0;
+  // tile `it` is visible in full to every query of the wave (wave-uniform)
+  auto full_tile = [&](int it, u64 vm) { return vm == ~0ull && it * 64 + 63 <= wlim; };
+  // this lane's visibility bits: bit 4 blk + r for slot 16 g + 4 blk + r
+  auto lane_bits = [&](int it, u64 vm) -> uint32_t {
+    const int e = limit - it * 64 - 16 * g;  // last visible offset in the lane's 16
+    const uint32_t cb = e >= 15 ? 0xFFFFu : (e < 0 ? 0u : (2u << e) - 1u);
+    return (uint32_t)(vm >> (16 * g)) & cb;
   };
 
-  // ---- pass 1: row max over visible slots
-  i64 mx = NEG_SENTINEL;
-  pass(false, [&](int s0) {
+  // ---- pass 1: row max over visible slots (scores are int32)
+  int mx = INT32_MIN;
+  pass(std::false_type{}, [&](int it, const int8_t* st_k) {
     v4i st[4];
-    scores(st);
+    scores(st_k, st);
+    const u64 vm = vmask[it];
+    if (full_tile(it, vm)) {
 #pragma unroll
-    for (int blk = 0; blk < 4; ++blk)
+      for (int blk = 0; blk < 4; ++blk)
 #pragma unroll
-      for (int r = 0; r < 4; ++r)
-        if (visible(s0, blk, r)) mx = imax(mx, (i64)st[blk][r]);
+        for (int r = 0; r < 4; ++r) mx = max(mx, st[blk][r]);
+    } else {
+      const uint32_t bits = lane_bits(it, vm);
+#pragma unroll
+      for (int blk = 0; blk < 4; ++blk)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if ((bits >> (4 * blk + r)) & 1u) mx = max(mx, st[blk][r]);
+    }
   });
-  mx = group4_max(mx);
-  if (mx == NEG_SENTINEL) mx = 0;  // no visible slot: max := 0, every p = 0
+  mx = max(mx, __shfl_xor(mx, 16));
+  mx = max(mx, __shfl_xor(mx, 32));
+  if (mx == INT32_MIN) mx = 0;  // no visible slot: max := 0, every p = 0
 
-  // ---- pass 2: denominator
+  // ---- pass 2: denominator. The 24-bit DI-Exp runs when every query of the
+  // wave has tpos < 2^23 (then every exp is below 2^23 and 16 of them sum in
+  // 32 bits); otherwise the general 64-bit form.
+  const bool fexp = __ballot(tpos >= (i64)PF_SMALL_T) == 0;
+  const uint32_t t32 = (uint32_t)tpos;
+  const uint32_t r24 = fexp ? 0xFFFFFFu / t32 : 0u;
+  const ExpR Et = make_exp(tpos);
   i64 den = 0;
-  pass(false, [&](int s0) {
+  pass(std::false_type{}, [&](int it, const int8_t* st_k) {
     v4i st[4];
-    scores(st);
+    scores(st_k, st);
+    const u64 vm = vmask[it];
+    const uint32_t bits = full_tile(it, vm) ? 0xFFFFu : lane_bits(it, vm);
+    if (fexp) {
+      uint32_t sum = 0;
 #pragma unroll
-    for (int blk = 0; blk < 4; ++blk)
+      for (int blk = 0; blk < 4; ++blk)
 #pragma unroll
-      for (int r = 0; r < 4; ++r)
-        if (visible(s0, blk, r)) den = wadd(den, di_exp_neg((u64)wsub(mx, (i64)st[blk][r]), Et));
+        for (int r = 0; r < 4; ++r) {
+          const uint32_t e = pf_dexp24((uint32_t)(mx - st[blk][r]), t32, r24);
+          sum += ((bits >> (4 * blk + r)) & 1u) ? e : 0u;
+        }
+      den += sum;
+    } else {
+#pragma unroll
+      for (int blk = 0; blk < 4; ++blk)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if ((bits >> (4 * blk + r)) & 1u)
+            den = wadd(den, di_exp_neg((u64)(uint32_t)(mx - st[blk][r]), Et));
+    }
   });
   den = imax(group4_sum(den), 1);
+  const bool fdiv = fexp && __ballot(den >= PF_SMALL_DEN) == 0;
+  const uint32_t d32 = (uint32_t)den, hd32 = d32 >> 1, dlo = d32 & 0xFFFFFFu, dhi = d32 >> 24;
+  const float rf = fdiv ? (float)(16384.0 / (double)d32) : 0.f;
   const Recip Rd = make_recip(den);
 
-  // ---- pass 3: p, then P.V on MFMA with the hi/lo split
-  v4i ohi[8], olo[8];
-  int csum[8];
+  // ---- pass 3: p, then P.V on MFMA with the hi/lo split; wave w also sums
+  // the V^T rows of dims 32w .. 32w + 31 (an all-ones A operand) for the
+  // +64 correction of the hi bytes
+  v4i ohi[8], olo[8], ocs[2];
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
     ohi[j] = v4i{0, 0, 0, 0};
     olo[j] = v4i{0, 0, 0, 0};
-    csum[j] = 0;
   }
-  pass(true, [&](int s0) {
+  ocs[0] = ocs[1] = v4i{0, 0, 0, 0};
+  const v4i ones = v4i{0x01010101, 0x01010101, 0x01010101, 0x01010101};
+  int voff[2];
+#pragma unroll
+  for (int par = 0; par < 2; ++par) {
+    const int d = 16 * par + qi;  // dims 16 j + qi: the swizzle depends on j % 2
+    voff[par] = PF_KBYTES + qi * 64 + ((g ^ pf_vswz(d)) << 4);
+  }
+  pass(std::true_type{}, [&](int it, const int8_t* stg) {
     v4i st[4];
-    scores(st);
+    scores(stg, st);
+    const u64 vm = vmask[it];
+    const uint32_t bits = full_tile(it, vm) ? 0xFFFFu : lane_bits(it, vm);
     v4i phi, plo;
+    auto put = [&](int blk, const uint32_t (&p)[4]) {
+      int whi, wlo;
+      pf_pack(p, whi, wlo);
+      phi[blk] = whi;
+      plo[blk] = wlo;
+    };
+    if (fdiv) {
 #pragma unroll
-    for (int blk = 0; blk < 4; ++blk) {
-      unsigned whi = 0, wlo = 0;
+      for (int blk = 0; blk < 4; ++blk) {
+        uint32_t p[4];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        i64 p = 0;
-        if (visible(s0, blk, r)) {
-          const i64 ex = di_exp_neg((u64)wsub(mx, (i64)st[blk][r]), Et);
-          p = to_i32(rhad_r(shl(ex, 14), Rd));
+        for (int r = 0; r < 4; ++r) {
+          const uint32_t e = pf_dexp24((uint32_t)(mx - st[blk][r]), t32, r24);
+          p[r] = pf_pdiv(((bits >> (4 * blk + r)) & 1u) ? e : 0u, rf, dlo, dhi, d32, hd32);
         }
-        const int hi = (int)(p >> 7);
-        const int lo = (int)(p - ((i64)hi << 7));
-        whi |= (unsigned)(uint8_t)(int8_t)(hi - 64) << (8 * r);
-        wlo |= (unsigned)(uint8_t)(int8_t)lo << (8 * r);
+        put(blk, p);
       }
-      phi[blk] = (int)whi;
-      plo[blk] = (int)wlo;
+    } else {
+#pragma unroll
+      for (int blk = 0; blk < 4; ++blk) {
+        uint32_t p[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          i64 pv = 0;
+          if ((bits >> (4 * blk + r)) & 1u) {
+            const i64 ex = di_exp_neg((u64)(uint32_t)(mx - st[blk][r]), Et);
+            pv = to_i32(rhad_r(shl(ex, 14), Rd));
+          }
+          p[r] = (uint32_t)pv;
+        }
+        put(blk, p);
+      }
     }
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      const v4i vb = *(const v4i*)&Vs[(j * 16 + qi) * VS_STRIDE + g * 16];
+      const v4i vb = *(const v4i*)(stg + voff[j & 1] + j * 1024);
       ohi[j] = mfma16(phi, vb, ohi[j]);
       olo[j] = mfma16(plo, vb, olo[j]);
-      int cs = csum[j];
+    }
 #pragma unroll
-      for (int q = 0; q < 4; ++q) cs = __builtin_amdgcn_sdot4(vb[q], 0x01010101, cs, false);
-      csum[j] = cs;
+    for (int c = 0; c < 2; ++c) {
+      const int j = 2 * wave + c;
+      const v4i vb = *(const v4i*)(stg + voff[c] + j * 1024);
+      ocs[c] = mfma16(ones, vb, ocs[c]);
     }
   });
+  // column sums: every row of ocs[c] holds sum_s v[s][32 wave + 16 c + qi]
+  if (g == 0) {
+    csum_lds[32 * wave + qi] = ocs[0][0];
+    csum_lds[32 * wave + 16 + qi] = ocs[1][0];
+  }
+  __syncthreads();
   // write: lane holds O[query 4g + r][d = 16j + qi]
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
-    const i64 cs = group4_sum((i64)csum[j]);
+    const i64 cs = csum_lds[16 * j + qi];
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int tq = qt * 64 + wave * 16 + g * 4 + r;
@@ -528,7 +696,8 @@ int detllm_attn_prefill(const int8_t* q8, const int64_t* tpos, const int8_t* kc,
   PrefillArgs a{q8, tpos, kc, vc, valid, out, T, (int)S, S_past, n_q, n_kv, B, cap, valid_stride};
   const i64 pairs = (i64)(((T + 63) / 64 + 1) / 2) * n_q * B;
   if (2 * pairs > 0x7fffffff) return DI_ERANGE;
-  hipLaunchKernelGGL(k_attn_prefill, dim3((unsigned)(2 * pairs)), dim3(256), 0, s, a);
+  const size_t lds = PF_RING + PF_CSUM + 8 * (size_t)((S + 63) / 64);  // + tile masks
+  hipLaunchKernelGGL(k_attn_prefill, dim3((unsigned)(2 * pairs)), dim3(256), lds, s, a);
   DI_LAUNCH_CHECK();
   return DI_OK;
 }

@@ -226,4 +226,16 @@ __device__ __forceinline__ i64 ilog2_from_bitlen(uint32_t len) { return len > 1 
 
 __device__ __forceinline__ i64 to_i32(i64 v) { return (i64)(int32_t)(uint32_t)(u64)v; }
 
+// Direct-to-LDS loads (global_load_lds_dwordx4: lane l's 16 bytes land at the
+// wave-uniform LDS base + 16 l) take these pointer types.
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+typedef __attribute__((address_space(1))) void* gbl_ptr_t;
+
+// s_waitcnt with vmcnt = n (n < 64) and no wait on the other counters
+template <int n>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(n >= 0 && n < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((n & 0xF) | ((n >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
 }  // namespace di

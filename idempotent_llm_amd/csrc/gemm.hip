@@ -133,19 +133,10 @@ __global__ __launch_bounds__(256) void k_gemm_nt(const int8_t* __restrict__ A,
 // round-robin over the 8 XCDs) owns one contiguous block of the tile grid,
 // keeping its share of A and B in its own L2.
 // ---------------------------------------------------------------------------
-typedef __attribute__((address_space(3))) void* lds_ptr_t;
-typedef __attribute__((address_space(1))) void* gbl_ptr_t;
 typedef int v16i __attribute__((ext_vector_type(16)));
 
 __device__ __forceinline__ v16i mfma32(v4i a, v4i b, v16i c) {
   return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c, 0, 0, 0);
-}
-
-// s_waitcnt with vmcnt = n (n < 64) and no wait on the other counters
-template <int n>
-__device__ __forceinline__ void wait_vmcnt() {
-  static_assert(n >= 0 && n < 64, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt((n & 0xF) | ((n >> 4) << 14) | (0x7 << 4) | (0xF << 8));
 }
 
 __device__ __forceinline__ int g2_swz(int row) { return (row >> 1) & 7; }

@@ -104,3 +104,90 @@ def test_fused_decode_group1():
     dims = dict(art.TINY, n_q_heads=2, n_kv_heads=2)
     print("[fused decode G=1]", flush=True)
     _run(dims, B=2, cap=256, S=100, slot=99, device_bounds=True, seed=9)
+
+
+# ------------------------------------------------------------ prefill kernel
+
+def _prefill_case(B, n_q, n_kv, T, S_past, cap, seed, sk_lo, sk_hi, zero_heads=(),
+                  extreme_rows=(), dead_prefix=0, p_valid=0.75):
+    """Random prefill inputs: q8/K/V bytes, per-row score scales (sm, sk) and
+    the DI-Exp constant tpos they give, a ragged validity mask. zero_heads get
+    q = 0 (every score 0: flat rows, the largest denominators); extreme_rows
+    (b, h, t) get q = -128 against K rows of -128 (scores of 2^21); batch row
+    1 has its first dead_prefix slots invalid (queries that see no slot)."""
+    from oracle import ops as oops
+    rng = np.random.default_rng(seed)
+    S = S_past + T
+    q8 = rng.integers(-128, 128, (B, n_q, T, 128), dtype=np.int8)
+    for h in zero_heads:
+        q8[:, h] = 0
+    kc = rng.integers(-128, 128, (B, n_kv, cap, 128), dtype=np.int8)
+    vc = rng.integers(-128, 128, (B, n_kv, 128, cap), dtype=np.int8)
+    for (b, h, t) in extreme_rows:
+        q8[b, h, t] = -128
+        kc[b, h // (n_q // n_kv), :S:7] = -128
+    sm = rng.integers(1 << 15, 1 << 16, (B, n_q, T, 1), dtype=np.int64)
+    sk = rng.integers(sk_lo, sk_hi + 1, (B, n_q, T, 1), dtype=np.int64)
+    tpos = oops.di_exp_tpos(sm, sk)
+    valid = rng.random((B, cap)) < p_valid
+    if B > 1 and dead_prefix:
+        valid[1, :dead_prefix] = False
+    return q8, kc, vc, valid, sm, sk, tpos
+
+
+def _prefill_oracle(q8, kc, vc, valid, sm, sk, S_past):
+    """model.py:382-402 on the CPU oracle: int8 scores, DI-Softmax over the
+    slots s <= S_past + t that are valid, exact p.v."""
+    from oracle import gemm as ogemm
+    from oracle import ops as oops
+    B, n_q, T, _ = q8.shape
+    n_kv = kc.shape[1]
+    S = S_past + T
+    vis = (np.arange(S)[None, :] <= (S_past + np.arange(T))[:, None])
+    out = np.zeros((B, T, n_q * 128), dtype=np.int64)
+    for b in range(B):
+        mask = vis & valid[b, None, :S]
+        for h in range(n_q):
+            kvh = h // (n_q // n_kv)
+            sc = ogemm.int_gemm(q8[b, h], np.ascontiguousarray(kc[b, kvh, :S].T))
+            p = oops.di_softmax(sc, sm[b, h], sk[b, h], mask)
+            out[b, :, h * 128:(h + 1) * 128] = ogemm.matmul_i64(
+                p, np.ascontiguousarray(vc[b, kvh, :, :S].T))
+    return out
+
+
+PREFILL_CASES = {
+    # B, n_q, n_kv, T, S_past, cap, seed, sk range, extras
+    "typical": (2, 4, 2, 150, 37, 192, 1, 29, 34, {}),
+    "wide_tpos": (2, 4, 2, 150, 37, 192, 2, 0, 62, dict(dead_prefix=40)),
+    "flat_big_den": (1, 4, 1, 200, 0, 208, 3, 46, 60, dict(zero_heads=(0, 2), p_valid=1.0)),
+    "extreme_scores": (2, 2, 2, 96, 5, 112, 4, 28, 40,
+                       dict(extreme_rows=((0, 0, 3), (1, 1, 95), (0, 1, 50)))),
+    "one_tile": (1, 2, 1, 64, 0, 64, 5, 30, 33, {}),
+    "single_query": (3, 2, 2, 1, 300, 304, 6, 25, 45, dict(dead_prefix=301)),
+}
+
+
+@pytest.mark.parametrize("name", list(PREFILL_CASES))
+def test_prefill_attention_vs_oracle(name):
+    """detllm_attn_prefill (model.py:382-402) against the oracle's
+    composition: int_gemm scores, di_softmax (ops/di_softmax.py:33-61) over
+    valid & causal slots, exact p.v; tpos from the oracle's di_exp_tpos.
+    Exact equality, including rows with no visible slot (all-zero context),
+    tpos from 1 to about 2^46 in one wave, and denominators beyond 2^32."""
+    from idempotent_llm_amd._lib import call
+    B, n_q, n_kv, T, S_past, cap, seed, lo, hi, extra = PREFILL_CASES[name]
+    print(f"[prefill attention {name}: B={B} n_q={n_q} n_kv={n_kv} T={T} S_past={S_past}]",
+          flush=True)
+    q8, kc, vc, valid, sm, sk, tpos = _prefill_case(B, n_q, n_kv, T, S_past, cap, seed, lo, hi,
+                                                    **extra)
+    want = _prefill_oracle(q8, kc, vc, valid, sm, sk, S_past)
+    d = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
+    out = torch.full((B, T, n_q * 128), -7, dtype=I64, device="cuda")
+    call("detllm_attn_prefill", d(q8), d(tpos[..., 0]), d(kc), d(vc), d(valid.astype(np.uint8)),
+         cap, B, T, S_past, n_q, n_kv, cap, out)
+    got = out.cpu().numpy()
+    bad = np.argwhere(got != want)
+    assert bad.size == 0, f"{len(bad)} mismatches, first at {bad[0].tolist()}"
+    if name == "flat_big_den":
+        assert tpos[0, 0].max() > (1 << 32)  # den = sum of exps >= tpos * visible slots
