@@ -58,8 +58,8 @@ constexpr int PF_KBYTES = 64 * 128;       // K tile: 64 slot rows of 128 B
 constexpr int PF_VBYTES = 128 * 64;       // V^T tile: 128 dim rows of 64 B
 constexpr int PF_RING = 32 * 1024;        // 4 K stages, or 2 K+V stages
 constexpr int PF_CSUM = 128 * 4;          // column sums of V (int32 per dim)
-constexpr uint32_t PF_SMALL_T = 1u << 23;  // 24-bit DI-Exp below this tpos
-constexpr i64 PF_SMALL_DEN = (i64)1 << 30;  // float-estimated p below this den
+constexpr uint32_t PF_SMALL_T = 1u << 23;  // estimated DI-Exp below this tpos
+constexpr i64 PF_SMALL_DEN = (i64)1 << 34;  // estimated p below this den
 
 // 16-byte chunk swizzles of the LDS tiles (physical chunk = logical ^ swz).
 // K rows (128 B): the 16 rows one MFMA reads with a chunk (rows
@@ -70,52 +70,49 @@ __device__ __forceinline__ int pf_kswz(int row) {
 }
 __device__ __forceinline__ int pf_vswz(int d) { return ((d >> 1) ^ (d >> 3)) & 3; }
 
-// The 24-bit multiplier (full rate; the 32-bit multiplies issue at a quarter
-// of it). Written out because the compiler cannot see the operand bounds
-// across the loop blocks and would pick the 32-bit forms.
-__device__ __forceinline__ uint32_t mul_u24(uint32_t a, uint32_t b) {
+// v_mad_u32_u24: a b + c with a, b < 2^24 (full rate; the 32-bit multiplies
+// issue at a quarter of it). Written out because the compiler cannot see the
+// operand bound across the loop blocks and would pick the 32-bit form.
+__device__ __forceinline__ uint32_t mad_u24(uint32_t a, uint32_t b, uint32_t c) {
   uint32_t d;
-  asm("v_mul_u32_u24 %0, %1, %2" : "=v"(d) : "v"(a), "v"(b));
-  return d;
-}
-__device__ __forceinline__ uint32_t mulhi_u24(uint32_t a, uint32_t b) {
-  uint32_t d;
-  asm("v_mul_hi_u32_u24 %0, %1, %2" : "=v"(d) : "v"(a), "v"(b));
+  asm("v_mad_u32_u24 %0, %1, %2, %3" : "=v"(d) : "v"(a), "v"(b), "v"(c));
   return d;
 }
 
-// DI-Exp of -n (ops/di_exp.py:27-37) for 0 <= n < 2^22 and 1 <= t < 2^23.
-// Every score difference qualifies: |q8 . k8| <= 2^21. q = floor(n / t) from
-// r24 = floor((2^24 - 1) / t) on the 24-bit multiplier is exact or one short
-// (n r24 / 2^24 lies in (n / t - 1/2, n / t)), fixed by one remainder step;
-// the result (t - ceil(rem / 2)) >> q is below 2^23, so the shift clamped to
-// 31 gives the same 0 as min(q, 62) for every q >= 23.
-__device__ __forceinline__ uint32_t pf_dexp24(uint32_t n, uint32_t t, uint32_t r24) {
-  uint32_t q = __builtin_amdgcn_alignbit(mulhi_u24(n, r24), mul_u24(n, r24), 24);
-  uint32_t rem = n - mul_u24(q, t);  // in [0, 2t)
-  if (rem >= t) {
-    q += 1;
-    rem -= t;
-  }
-  const uint32_t u = t - ((rem + 1) >> 1);
-  return u >> min(q, 31u);
+// Per-query constants of the estimated DI-Exp and division (fp64 runs at
+// the full vector rate on gfx950).
+struct PfFast {
+  double nrt;   // -fl(1 / t)
+  double kx;    // fl(mx fl(1 / t) + 1 + 2^-26)
+  uint32_t t;   // tpos < 2^23
+  uint32_t cx;  // t - mx (mod 2^32)
+  double r14;   // fl(2^14 / den)
+  double kp;    // fl(fl(floor(den / 2) / den) + 2^-36)
+};
+
+// DI-Exp of st - mx (ops/di_exp.py:27-37) for a visible score st <= mx and
+// t < 2^23. n = mx - st < 2^22 (|q8 . k8| <= 2^21). e = fma(st, -1/t, kx)
+// is n / t + 1 + 2^-26 within 2^-29 (rounding of 1/t, kx and the fma, all
+// below 2^-53 relative on values under 2^23), and every non-integer n / t is
+// at least 1/t > 2^-23 below the next integer, so truncating e gives
+// q1 = floor(n / t) + 1 exactly. With rem = n - q t, the result
+// (t - ceil(rem / 2)) >> q equals (2t - rem) >> (q + 1) = ((q + 2) t - n)
+// >> q1, where (q + 2) t - n = q1 t + (t - mx) + st lies in (0, 2t]; it is
+// below 2^24, so shifts of 24 and more (clamped to 31) give the same 0 as
+// min(q, 62) for every q >= 23.
+__device__ __forceinline__ uint32_t pf_dexp(int32_t st, const PfFast& F) {
+  const uint32_t q1 = (uint32_t)fma((double)st, F.nrt, F.kx);
+  const uint32_t m = mad_u24(q1, F.t, F.cx + (uint32_t)st);
+  return m >> min(q1, 31u);
 }
 
 // p = round_half_away_div(ex << 14, den) = floor((ex 2^14 + floor(den / 2)) /
-// den) for 0 <= ex <= den < 2^30, ex < 2^24. fma(ex, rf, 1/2) with rf =
-// fl(2^14 / den) is within 2^-10 (reciprocal) + 2^-10 (fma rounding) + 1/2
-// (versus floor(den / 2) / den) of the exact quotient, so its truncation q is
-// off by at most one either way; the remainder lies in [-den, 2 den), inside
-// the int32 range, so 32-bit wrapping arithmetic gives it exactly (q den mod
-// 2^32 from the 24-bit halves of den: q <= 2^14 + 1).
-__device__ __forceinline__ uint32_t pf_pdiv(uint32_t ex, float rf, uint32_t dlo, uint32_t dhi,
-                                            uint32_t den, uint32_t hd) {
-  uint32_t q = (uint32_t)fmaf((float)ex, rf, 0.5f);
-  const uint32_t qd = mul_u24(q, dlo) + (mul_u24(q, dhi) << 24);
-  const int32_t rem = (int32_t)((ex << 14) + hd - qd);
-  q += rem >= (int32_t)den ? 1u : 0u;
-  q -= rem < 0 ? 1u : 0u;
-  return q;
+// den) for 0 <= ex <= den < 2^34 (ex < 2^23): fma(ex, r14, kp) is the exact
+// quotient + 2^-36 within 2^-37 (r14 and the fma round at 2^-39 on values
+// below 2^15, kp at 2^-54), and a non-integer quotient is at least
+// 1/den > 2^-34 below the next integer, so truncation gives the floor.
+__device__ __forceinline__ uint32_t pf_pdiv(uint32_t ex, const PfFast& F) {
+  return (uint32_t)fma((double)ex, F.r14, F.kp);
 }
 
 // Four probabilities (slot order = byte order) as the two MFMA operands of
@@ -151,7 +148,8 @@ __global__ __launch_bounds__(256, 2) void k_attn_prefill(PrefillArgs a) {
   const int qt = half ? kk : nqt - 1 - kk;
   const int h = hb % a.n_q, b = hb / a.n_q;
   const int kvh = h / (a.n_q / a.n_kv);
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
   const int qi = lane & 15, g = lane >> 4;
   const int t = qt * 64 + wave * 16 + qi;  // this lane's query
   const bool tok = t < a.T;
@@ -296,27 +294,44 @@ __global__ __launch_bounds__(256, 2) void k_attn_prefill(PrefillArgs a) {
   mx = max(mx, __shfl_xor(mx, 32));
   if (mx == INT32_MIN) mx = 0;  // no visible slot: max := 0, every p = 0
 
-  // ---- pass 2: denominator. The 24-bit DI-Exp runs when every query of the
-  // wave has tpos < 2^23 (then every exp is below 2^23 and 16 of them sum in
-  // 32 bits); otherwise the general 64-bit form.
+  // ---- pass 2: denominator. The estimated DI-Exp runs when every query of
+  // the wave has tpos < 2^23 (then every exp is below 2^23 and 16 of them sum
+  // in 32 bits); otherwise the general 64-bit form. Masked slots enter the
+  // estimate as st = mx (a defined conversion) and are then dropped.
   const bool fexp = __ballot(tpos >= (i64)PF_SMALL_T) == 0;
-  const uint32_t t32 = (uint32_t)tpos;
-  const uint32_t r24 = fexp ? 0xFFFFFFu / t32 : 0u;
+  PfFast F;
+  F.t = (uint32_t)tpos;
+  F.cx = F.t - (uint32_t)mx;
+  {
+    const double rt = 1.0 / (double)F.t;
+    F.nrt = -rt;
+    F.kx = fma((double)mx, rt, 1.0 + 0x1p-26);
+  }
   const ExpR Et = make_exp(tpos);
   i64 den = 0;
   pass(std::false_type{}, [&](int it, const int8_t* st_k) {
     v4i st[4];
     scores(st_k, st);
     const u64 vm = vmask[it];
-    const uint32_t bits = full_tile(it, vm) ? 0xFFFFu : lane_bits(it, vm);
+    if (fexp && full_tile(it, vm)) {
+      uint32_t sum = 0;
+#pragma unroll
+      for (int blk = 0; blk < 4; ++blk)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) sum += pf_dexp(st[blk][r], F);
+      den += sum;
+      return;
+    }
+    const uint32_t bits = lane_bits(it, vm);
     if (fexp) {
       uint32_t sum = 0;
 #pragma unroll
       for (int blk = 0; blk < 4; ++blk)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const uint32_t e = pf_dexp24((uint32_t)(mx - st[blk][r]), t32, r24);
-          sum += ((bits >> (4 * blk + r)) & 1u) ? e : 0u;
+          const bool vis = (bits >> (4 * blk + r)) & 1u;
+          const uint32_t e = pf_dexp(vis ? st[blk][r] : mx, F);
+          sum += vis ? e : 0u;
         }
       den += sum;
     } else {
@@ -330,8 +345,8 @@ __global__ __launch_bounds__(256, 2) void k_attn_prefill(PrefillArgs a) {
   });
   den = imax(group4_sum(den), 1);
   const bool fdiv = fexp && __ballot(den >= PF_SMALL_DEN) == 0;
-  const uint32_t d32 = (uint32_t)den, hd32 = d32 >> 1, dlo = d32 & 0xFFFFFFu, dhi = d32 >> 24;
-  const float rf = fdiv ? (float)(16384.0 / (double)d32) : 0.f;
+  F.r14 = 16384.0 / (double)den;
+  F.kp = (double)(den >> 1) / (double)den + 0x1p-36;
   const Recip Rd = make_recip(den);
 
   // ---- pass 3: p, then P.V on MFMA with the hi/lo split; wave w also sums
@@ -355,7 +370,8 @@ __global__ __launch_bounds__(256, 2) void k_attn_prefill(PrefillArgs a) {
     v4i st[4];
     scores(stg, st);
     const u64 vm = vmask[it];
-    const uint32_t bits = full_tile(it, vm) ? 0xFFFFu : lane_bits(it, vm);
+    const bool full = full_tile(it, vm);
+    const uint32_t bits = full ? 0xFFFFu : lane_bits(it, vm);
     v4i phi, plo;
     auto put = [&](int blk, const uint32_t (&p)[4]) {
       int whi, wlo;
@@ -363,14 +379,23 @@ __global__ __launch_bounds__(256, 2) void k_attn_prefill(PrefillArgs a) {
       phi[blk] = whi;
       plo[blk] = wlo;
     };
-    if (fdiv) {
+    if (fdiv && full) {
+#pragma unroll
+      for (int blk = 0; blk < 4; ++blk) {
+        uint32_t p[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) p[r] = pf_pdiv(pf_dexp(st[blk][r], F), F);
+        put(blk, p);
+      }
+    } else if (fdiv) {
 #pragma unroll
       for (int blk = 0; blk < 4; ++blk) {
         uint32_t p[4];
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const uint32_t e = pf_dexp24((uint32_t)(mx - st[blk][r]), t32, r24);
-          p[r] = pf_pdiv(((bits >> (4 * blk + r)) & 1u) ? e : 0u, rf, dlo, dhi, d32, hd32);
+          const bool vis = (bits >> (4 * blk + r)) & 1u;
+          const uint32_t e = pf_dexp(vis ? st[blk][r] : mx, F);
+          p[r] = pf_pdiv(vis ? e : 0u, F);
         }
         put(blk, p);
       }
