@@ -54,21 +54,22 @@ struct PrefillArgs {
   i64 cap, valid_stride;
 };
 
-constexpr int PF_KBYTES = 64 * 128;       // K tile: 64 slot rows of 128 B
-constexpr int PF_VBYTES = 128 * 64;       // V^T tile: 128 dim rows of 64 B
-constexpr int PF_RING = 32 * 1024;        // 4 K stages, or 2 K+V stages
+constexpr int PF_KBYTES = 128 * 128;      // K tile: 128 slot rows of 128 B
+constexpr int PF_VBYTES = 128 * 128;      // V^T tile: 128 dim rows of 128 B
+constexpr int PF_RING = 64 * 1024;        // 4 K stages, or 2 K+V stages
 constexpr int PF_CSUM = 128 * 4;          // column sums of V (int32 per dim)
 constexpr uint32_t PF_SMALL_T = 1u << 23;  // estimated DI-Exp below this tpos
 constexpr i64 PF_SMALL_DEN = (i64)1 << 34;  // estimated p below this den
 
-// 16-byte chunk swizzles of the LDS tiles (physical chunk = logical ^ swz).
-// K rows (128 B): the 16 rows one MFMA reads with a chunk (rows
-// 16(i/4) + 4 blk + i%4, i = 0..15) fall on distinct banks both 8 and 16
-// lanes at a time. V^T rows (64 B): dims 16 j + i, i = 0..15, likewise.
-__device__ __forceinline__ int pf_kswz(int row) {
-  return ((row ^ (row >> 5)) & 1) | (row & 2) | ((row >> 2) & 4);
-}
-__device__ __forceinline__ int pf_vswz(int d) { return ((d >> 1) ^ (d >> 3)) & 3; }
+// 16-byte chunk swizzles of the LDS tiles (128-byte rows, physical chunk =
+// logical ^ swz). An MFMA operand read takes one chunk column of 16 rows per
+// 16 lanes: K rows 16(i/4) + 4 blk + i%4 and V^T rows (dims) 16 j + i for
+// i = 0..15. With swz = bits 0, 1 and 4 of the K row (i % 4 and i / 4 % 2)
+// and the low 3 bits of the V^T row, both reads run at the full LDS rate of
+// 16 bytes per lane (measured on gfx950; an unswizzled read takes 4 times as
+// long, swizzles on other row bits twice as long).
+__device__ __forceinline__ int pf_kswz(int row) { return (row & 3) | ((row >> 2) & 4); }
+__device__ __forceinline__ int pf_vswz(int d) { return d & 7; }
 
 // v_mad_u32_u24: a b + c with a, b < 2^24 (full rate; the 32-bit multiplies
 // issue at a quarter of it). Written out because the compiler cannot see the
@@ -131,18 +132,30 @@ __device__ __forceinline__ void pf_pack(const uint32_t (&p)[4], int& whi, int& w
 }
 
 __global__ __launch_bounds__(256, 2) void k_attn_prefill(PrefillArgs a) {
-  extern __shared__ __attribute__((aligned(1024))) int8_t smem[];
-  int8_t* const ring = smem;
-  int32_t* const csum_lds = (int32_t*)(smem + PF_RING);
-  u64* const vmask = (u64*)(smem + PF_RING + PF_CSUM);  // per key tile
-  // Causal work per query tile grows with its index. Blocks come in two
-  // halves of `pairs` blocks: the first half takes the heavy tiles
-  // (nqt - 1 - k), dispatched first, the second their light partners (k), so
-  // the two blocks a CU holds together add up to about the same work
-  // whatever k they have. The middle tile of an odd count appears once.
+  __shared__ __attribute__((aligned(1024))) int8_t ring[PF_RING];
+  extern __shared__ __attribute__((aligned(16))) int8_t dyn[];  // PF_CSUM + 8 per 64 slots
+  int32_t* const csum_lds = (int32_t*)dyn;
+  u64* const vmask = (u64*)(dyn + PF_CSUM);  // per 64-slot key tile
+  // Causal work per query tile grows with its index. Pair pi = (b, h, k)
+  // (k fastest) stands for the heavy tile nqt - 1 - k and its light partner
+  // k. Blocks are dispatched round-robin over the 8 XCDs (XCD = blockIdx % 8);
+  // when the pairs split evenly, XCD x takes the contiguous pairs
+  // [x pairs/8, (x + 1) pairs/8) — whole heads, so each XCD's L2 holds only
+  // its own heads' K and V — heavy tiles first, then the light ones, so the
+  // two blocks a CU holds together add up to about the same work. Otherwise
+  // the first half of the grid takes the heavy tiles and the second half the
+  // light ones. The middle tile of an odd count appears once.
   const int nqt = (a.T + 63) / 64, np = (nqt + 1) / 2;
   const int pairs = np * a.n_q * a.B;
-  const int half = blockIdx.x >= pairs, pi = blockIdx.x - half * pairs;
+  int half, pi;
+  if (pairs % 8 == 0) {
+    const int per = pairs / 8, j = blockIdx.x >> 3;
+    half = j >= per;
+    pi = (blockIdx.x & 7) * per + (j - half * per);
+  } else {
+    half = blockIdx.x >= pairs;
+    pi = blockIdx.x - half * pairs;
+  }
   const int kk = pi % np, hb = pi / np;
   if (half && kk == nqt - 1 - kk) return;  // middle tile: done by the first half
   const int qt = half ? kk : nqt - 1 - kk;
@@ -169,7 +182,9 @@ __global__ __launch_bounds__(256, 2) void k_attn_prefill(PrefillArgs a) {
   const uint8_t* vrow = a.valid + (i64)b * a.valid_stride;
 
   // validity bitmask of every key tile (bit s - 64 i of tile i: slot s < S
-  // and valid), made once and read by all three passes
+  // and valid), made once and read by all three passes for the tiles that
+  // are not valid in full; nfull = the first tile that is not
+  int nf = ntiles;
   for (int i0 = wave; i0 < ntiles; i0 += 16) {
     uint32_t f[4];
 #pragma unroll
@@ -180,45 +195,51 @@ __global__ __launch_bounds__(256, 2) void k_attn_prefill(PrefillArgs a) {
     }
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
+      const int i = i0 + 4 * u;
       const u64 m = __ballot(f[u] != 0);
-      if (lane == 0 && i0 + 4 * u < ntiles) vmask[i0 + 4 * u] = m;
+      if (lane == 0 && i < ntiles) vmask[i] = m;
+      if (i < ntiles && m != ~0ull) nf = min(nf, i);
     }
   }
+  if (lane == 0) csum_lds[wave] = nf;  // the column-sum area is free until the end
+  __syncthreads();
+  const int nfull = min(min(csum_lds[0], csum_lds[1]), min(csum_lds[2], csum_lds[3]));
   wait_vmcnt<0>();  // query operands in registers before the ring's loads count
 
-  // Key tiles stream into an LDS ring with direct-to-LDS loads, issued
-  // STAGES - 1 tiles ahead. K: instruction j of wave w covers tile rows
-  // 8(2w + j) .. +7, lane l row 8(2w + j) + l/8 at physical chunk l % 8.
-  // V^T: dims 16(2w + j) + l/4 at physical chunk l % 4. Rows past the cache
-  // are clamped to its last row or chunk: valid memory whose slots are never
-  // visible (p = 0: their hi byte -64 and the +64 column-sum term cancel).
-  int krow[2], kchk[2], vdim[2], vchk[2];
+  // Key tiles of 128 slots stream into an LDS ring with direct-to-LDS loads,
+  // issued STAGES - 1 tiles ahead; each tile is processed as two 64-slot
+  // halves (the 64-slot tiles `it` of the masks) between one barrier and the
+  // next. K: instruction j of wave w covers tile rows 8(4w + j) .. +7, lane l
+  // row 8(4w + j) + l/8 at physical chunk l % 8; V^T likewise with dims for
+  // rows. Buffer loads bounded by the (b, kv head) slice of each cache: slots
+  // past the cache read as 0 (K) or as the next V^T row / 0 (V); such slots
+  // are never visible (p = 0: their hi byte -64 and the +64 column-sum term
+  // cancel).
+  const int ntiles2 = (ntiles + 1) / 2;
+  const __amdgpu_buffer_rsrc_t krs =
+      __builtin_amdgcn_make_buffer_rsrc((void*)kbase, (short)0, (int)(a.cap * 128), 0x00020000);
+  const __amdgpu_buffer_rsrc_t vrs =
+      __builtin_amdgcn_make_buffer_rsrc((void*)vbase, (short)0, (int)(a.cap * 128), 0x00020000);
+  int koffl[4], voffl[4];
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int ins = wave * 2 + j;
-    krow[j] = ins * 8 + (lane >> 3);
-    kchk[j] = ((lane & 7) ^ pf_kswz(krow[j])) * 16;
-    vdim[j] = ins * 16 + (lane >> 2);
-    vchk[j] = ((lane & 3) ^ pf_vswz(vdim[j])) * 16;
+  for (int j = 0; j < 4; ++j) {
+    const int row = (wave * 4 + j) * 8 + (lane >> 3);
+    koffl[j] = row * 128 + ((lane & 7) ^ pf_kswz(row)) * 16;
+    voffl[j] = row * (int)a.cap + ((lane & 7) ^ pf_vswz(row)) * 16;
   }
   auto issue = [&](int tile, int8_t* st, bool with_v) {
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const i64 row = min((i64)tile * 64 + krow[j], a.cap - 1);
-      __builtin_amdgcn_global_load_lds((gbl_ptr_t)(kbase + row * 128 + kchk[j]),
-                                       (lds_ptr_t)(st + (wave * 2 + j) * 1024), 16, 0, 0);
-    }
+    for (int j = 0; j < 4; ++j)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(krs, (lds_ptr_t)(st + (wave * 4 + j) * 1024), 16,
+                                               koffl[j], tile * 128 * 128, 0, 0);
     if (with_v) {
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const i64 s = min((i64)tile * 64 + vchk[j], a.cap - 16);
-        __builtin_amdgcn_global_load_lds((gbl_ptr_t)(vbase + (i64)vdim[j] * a.cap + s),
-                                         (lds_ptr_t)(st + PF_KBYTES + (wave * 2 + j) * 1024),
-                                         16, 0, 0);
-      }
+      for (int j = 0; j < 4; ++j)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            vrs, (lds_ptr_t)(st + PF_KBYTES + (wave * 4 + j) * 1024), 16, voffl[j], tile * 128, 0, 0);
     }
   };
-  // one pass over the key tiles; body(it, stage) runs with tile it in LDS.
+  // one pass over the key tiles; body(it2, stage) runs with tile it2 in LDS.
   // Each wave waits for its own loads of the tile (vmcnt: loads complete in
   // order), then one barrier publishes every wave's part and frees the
   // stage that the next issue overwrites.
@@ -226,24 +247,24 @@ __global__ __launch_bounds__(256, 2) void k_attn_prefill(PrefillArgs a) {
     constexpr bool KV = decltype(kv)::value;
     constexpr int STAGE = KV ? PF_KBYTES + PF_VBYTES : PF_KBYTES;
     constexpr int ST = PF_RING / STAGE;
-    constexpr int LPT = KV ? 4 : 2;  // loads per tile per wave
-    static_assert(ST >= 2 && ST <= 4, "ring stages");
+    constexpr int LPT = KV ? 8 : 4;  // loads per tile per wave
+    static_assert(ST >= 2 && ST <= 4 && 2 * LPT < 64, "ring stages");
     __builtin_amdgcn_s_barrier();  // the previous pass is done with the ring
 #pragma unroll
     for (int s = 0; s < ST - 1; ++s)
-      if (s < ntiles) issue(s, ring + s * STAGE, KV);
-    for (int it = 0; it < ntiles; ++it) {
-      const int after = min(ST - 2, ntiles - 1 - it);  // tiles issued after `it`
+      if (s < ntiles2) issue(s, ring + s * STAGE, KV);
+    for (int it2 = 0; it2 < ntiles2; ++it2) {
+      const int after = min(ST - 2, ntiles2 - 1 - it2);  // tiles issued after it2
       if (after >= 2) wait_vmcnt<2 * LPT>();
       else if (after == 1) wait_vmcnt<LPT>();
       else wait_vmcnt<0>();
       __builtin_amdgcn_s_barrier();
-      if (it + ST - 1 < ntiles) issue(it + ST - 1, ring + ((it + ST - 1) % ST) * STAGE, KV);
-      body(it, ring + (it % ST) * STAGE);
+      if (it2 + ST - 1 < ntiles2) issue(it2 + ST - 1, ring + ((it2 + ST - 1) % ST) * STAGE, KV);
+      body(it2, ring + (it2 % ST) * STAGE);
     }
   };
 
-  // S^T = K . Q^T for one tile: MFMA block blk takes K rows
+  // S^T = K . Q^T for one 64-slot half: MFMA block blk takes K rows
   // 16(i/4) + 4 blk + i%4 as its rows i, so lane (qi, g) receives the scores
   // of query qi for the 16 consecutive slots 16 g + 4 blk + r (blk, r < 4):
   // st[blk][r]. Those are also the 16 bytes of its P operand for P.V, in
@@ -251,18 +272,38 @@ __global__ __launch_bounds__(256, 2) void k_attn_prefill(PrefillArgs a) {
   const int kr = 16 * (qi >> 2) + (qi & 3);
   const int koff0 = kr * 128 + ((g ^ pf_kswz(kr)) << 4);
   const int koff1 = kr * 128 + (((g + 4) ^ pf_kswz(kr)) << 4);
-  auto scores = [&](const int8_t* st_k, v4i (&st)[4]) {
+  auto load_k = [&](const int8_t* st_k, v4i (&kf)[8]) {
 #pragma unroll
     for (int blk = 0; blk < 4; ++blk) {
-      const v4i k0 = *(const v4i*)(st_k + koff0 + blk * 512);
-      const v4i k1 = *(const v4i*)(st_k + koff1 + blk * 512);
-      v4i acc = v4i{0, 0, 0, 0};
-      acc = mfma16(k0, qf0, acc);
-      st[blk] = mfma16(k1, qf1, acc);
+      kf[2 * blk] = *(const v4i*)(st_k + koff0 + blk * 512);
+      kf[2 * blk + 1] = *(const v4i*)(st_k + koff1 + blk * 512);
     }
   };
+  // both halves' K operands read at once (one LDS latency), then their
+  // score MFMAs: the first 64 dims of all 8 blocks, then the second 64 — the
+  // two MFMAs of a block are 8 issues apart, so none waits on the previous
+  // one's result — overlapping the first half's VALU work; then
+  // fn(st, it, half) per half that holds key slots
+  auto halves = [&](const int8_t* stg, int it2, auto&& fn) {
+    v4i ka[8], kb[8], sa[4], sb[4];
+    load_k(stg, ka);
+    load_k(stg + 64 * 128, kb);
+    __builtin_amdgcn_sched_barrier(0);
+    const v4i z = v4i{0, 0, 0, 0};
+#pragma unroll
+    for (int blk = 0; blk < 4; ++blk) sa[blk] = mfma16(ka[2 * blk], qf0, z);
+#pragma unroll
+    for (int blk = 0; blk < 4; ++blk) sb[blk] = mfma16(kb[2 * blk], qf0, z);
+#pragma unroll
+    for (int blk = 0; blk < 4; ++blk) sa[blk] = mfma16(ka[2 * blk + 1], qf1, sa[blk]);
+#pragma unroll
+    for (int blk = 0; blk < 4; ++blk) sb[blk] = mfma16(kb[2 * blk + 1], qf1, sb[blk]);
+    __builtin_amdgcn_sched_barrier(0);
+    fn(sa, 2 * it2, 0);
+    if (2 * it2 + 1 < ntiles) fn(sb, 2 * it2 + 1, 1);
+  };
   // tile `it` is visible in full to every query of the wave (wave-uniform)
-  auto full_tile = [&](int it, u64 vm) { return vm == ~0ull && it * 64 + 63 <= wlim; };
+  auto full_tile = [&](int it) { return it < nfull && it * 64 + 63 <= wlim; };
   // this lane's visibility bits: bit 4 blk + r for slot 16 g + 4 blk + r
   auto lane_bits = [&](int it, u64 vm) -> uint32_t {
     const int e = limit - it * 64 - 16 * g;  // last visible offset in the lane's 16
@@ -272,24 +313,21 @@ __global__ __launch_bounds__(256, 2) void k_attn_prefill(PrefillArgs a) {
 
   // ---- pass 1: row max over visible slots (scores are int32)
   int mx = INT32_MIN;
-  pass(std::false_type{}, [&](int it, const int8_t* st_k) {
-    v4i st[4];
-    scores(st_k, st);
-    const u64 vm = vmask[it];
-    if (full_tile(it, vm)) {
+  pass(std::false_type{}, [&](int it2, const int8_t* stg) { halves(stg, it2, [&](const v4i (&st)[4], int it, int) {
+    if (full_tile(it)) {
 #pragma unroll
       for (int blk = 0; blk < 4; ++blk)
 #pragma unroll
         for (int r = 0; r < 4; ++r) mx = max(mx, st[blk][r]);
     } else {
-      const uint32_t bits = lane_bits(it, vm);
+      const uint32_t bits = lane_bits(it, vmask[it]);
 #pragma unroll
       for (int blk = 0; blk < 4; ++blk)
 #pragma unroll
         for (int r = 0; r < 4; ++r)
           if ((bits >> (4 * blk + r)) & 1u) mx = max(mx, st[blk][r]);
     }
-  });
+  }); });
   mx = max(mx, __shfl_xor(mx, 16));
   mx = max(mx, __shfl_xor(mx, 32));
   if (mx == INT32_MIN) mx = 0;  // no visible slot: max := 0, every p = 0
@@ -309,11 +347,8 @@ __global__ __launch_bounds__(256, 2) void k_attn_prefill(PrefillArgs a) {
   }
   const ExpR Et = make_exp(tpos);
   i64 den = 0;
-  pass(std::false_type{}, [&](int it, const int8_t* st_k) {
-    v4i st[4];
-    scores(st_k, st);
-    const u64 vm = vmask[it];
-    if (fexp && full_tile(it, vm)) {
+  pass(std::false_type{}, [&](int it2, const int8_t* stg) { halves(stg, it2, [&](const v4i (&st)[4], int it, int) {
+    if (fexp && full_tile(it)) {
       uint32_t sum = 0;
 #pragma unroll
       for (int blk = 0; blk < 4; ++blk)
@@ -322,7 +357,7 @@ __global__ __launch_bounds__(256, 2) void k_attn_prefill(PrefillArgs a) {
       den += sum;
       return;
     }
-    const uint32_t bits = lane_bits(it, vm);
+    const uint32_t bits = lane_bits(it, vmask[it]);
     if (fexp) {
       uint32_t sum = 0;
 #pragma unroll
@@ -342,7 +377,7 @@ __global__ __launch_bounds__(256, 2) void k_attn_prefill(PrefillArgs a) {
           if ((bits >> (4 * blk + r)) & 1u)
             den = wadd(den, di_exp_neg((u64)(uint32_t)(mx - st[blk][r]), Et));
     }
-  });
+  }); });
   den = imax(group4_sum(den), 1);
   const bool fdiv = fexp && __ballot(den >= PF_SMALL_DEN) == 0;
   F.r14 = 16384.0 / (double)den;
@@ -360,18 +395,21 @@ __global__ __launch_bounds__(256, 2) void k_attn_prefill(PrefillArgs a) {
   }
   ocs[0] = ocs[1] = v4i{0, 0, 0, 0};
   const v4i ones = v4i{0x01010101, 0x01010101, 0x01010101, 0x01010101};
+  // V^T operand of half `hf`: dim 16 j + qi, slots 64 hf + 16 g .. + 15
+  // (the swizzle of dim 16 j + qi does not depend on j)
   int voff[2];
 #pragma unroll
-  for (int par = 0; par < 2; ++par) {
-    const int d = 16 * par + qi;  // dims 16 j + qi: the swizzle depends on j % 2
-    voff[par] = PF_KBYTES + qi * 64 + ((g ^ pf_vswz(d)) << 4);
-  }
-  pass(std::true_type{}, [&](int it, const int8_t* stg) {
-    v4i st[4];
-    scores(stg, st);
-    const u64 vm = vmask[it];
-    const bool full = full_tile(it, vm);
-    const uint32_t bits = full ? 0xFFFFu : lane_bits(it, vm);
+  for (int hf = 0; hf < 2; ++hf) voff[hf] = PF_KBYTES + qi * 128 + (((4 * hf + g) ^ pf_vswz(qi)) << 4);
+  pass(std::true_type{}, [&](int it2, const int8_t* stg) { halves(stg, it2, [&](const v4i (&st)[4], int it, int hf) {
+    v4i vf[8], vc[2];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) vf[j] = *(const v4i*)(stg + voff[hf] + j * 2048);
+#pragma unroll
+    for (int c = 0; c < 2; ++c) vc[c] = *(const v4i*)(stg + voff[hf] + (2 * wave + c) * 2048);
+    __builtin_amdgcn_sched_barrier(0);
+    const bool full = full_tile(it);
+    uint32_t bits = 0xFFFFu;
+    if (!full) bits = lane_bits(it, vmask[it]);
     v4i phi, plo;
     auto put = [&](int blk, const uint32_t (&p)[4]) {
       int whi, wlo;
@@ -417,17 +455,12 @@ __global__ __launch_bounds__(256, 2) void k_attn_prefill(PrefillArgs a) {
     }
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      const v4i vb = *(const v4i*)(stg + voff[j & 1] + j * 1024);
-      ohi[j] = mfma16(phi, vb, ohi[j]);
-      olo[j] = mfma16(plo, vb, olo[j]);
+      ohi[j] = mfma16(phi, vf[j], ohi[j]);
+      olo[j] = mfma16(plo, vf[j], olo[j]);
     }
 #pragma unroll
-    for (int c = 0; c < 2; ++c) {
-      const int j = 2 * wave + c;
-      const v4i vb = *(const v4i*)(stg + voff[c] + j * 1024);
-      ocs[c] = mfma16(ones, vb, ocs[c]);
-    }
-  });
+    for (int c = 0; c < 2; ++c) ocs[c] = mfma16(ones, vc[c], ocs[c]);
+  }); });
   // column sums: every row of ocs[c] holds sum_s v[s][32 wave + 16 c + qi]
   if (g == 0) {
     csum_lds[32 * wave + qi] = ocs[0][0];
@@ -718,10 +751,11 @@ int detllm_attn_prefill(const int8_t* q8, const int64_t* tpos, const int8_t* kc,
       valid_stride < S)
     return DI_EINVAL;
   if (S > 131071) return DI_ERANGE;  // int32 MFMA accumulators of P.V
+  if (cap > ((i64)1 << 24)) return DI_ERANGE;  // 32-bit buffer offsets of a cache slice
   PrefillArgs a{q8, tpos, kc, vc, valid, out, T, (int)S, S_past, n_q, n_kv, B, cap, valid_stride};
   const i64 pairs = (i64)(((T + 63) / 64 + 1) / 2) * n_q * B;
   if (2 * pairs > 0x7fffffff) return DI_ERANGE;
-  const size_t lds = PF_RING + PF_CSUM + 8 * (size_t)((S + 63) / 64);  // + tile masks
+  const size_t lds = PF_CSUM + 8 * (size_t)((S + 63) / 64);  // column sums, tile masks
   hipLaunchKernelGGL(k_attn_prefill, dim3((unsigned)(2 * pairs)), dim3(256), lds, s, a);
   DI_LAUNCH_CHECK();
   return DI_OK;

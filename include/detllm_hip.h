@@ -145,7 +145,7 @@ int detllm_qkv_epilogue(const int32_t* P, int nsplit, int64_t split_stride, int 
  * int_gemm_u16i8 backends.py:152-164). Queries t in [0, T) sit at slots
  * S_past + t; slot s is visible iff s <= S_past + t and valid[b][s].
  * out [B][T][n_q*128] int64 = exact sum_s p_s v_s. cap % 16 == 0,
- * S_past + T <= min(cap, 131071). */
+ * cap <= 2^24, S_past + T <= min(cap, 131071). */
 int detllm_attn_prefill(const int8_t* q8, const int64_t* tpos, const int8_t* kcache,
                         const int8_t* vcache, const uint8_t* valid, int64_t valid_stride, int B,
                         int T, int S_past, int n_q, int n_kv, int64_t cap, int64_t* out,
