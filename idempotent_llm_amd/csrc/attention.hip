@@ -84,26 +84,27 @@ __device__ __forceinline__ uint32_t mad_u24(uint32_t a, uint32_t b, uint32_t c) 
 // the full vector rate on gfx950).
 struct PfFast {
   double nrt;   // -fl(1 / t)
-  double kx;    // fl(mx fl(1 / t) + 1 + 2^-26)
+  double kx;    // fl(t fl(1 / t) + 1 + 2^-26)
   uint32_t t;   // tpos < 2^23
-  uint32_t cx;  // t - mx (mod 2^32)
+  int32_t cx;   // t - mx: the score MFMAs of passes 2 and 3 start from it
   double r14;   // fl(2^14 / den)
   double kp;    // fl(fl(floor(den / 2) / den) + 2^-36)
 };
 
 // DI-Exp of st - mx (ops/di_exp.py:27-37) for a visible score st <= mx and
-// t < 2^23. n = mx - st < 2^22 (|q8 . k8| <= 2^21). e = fma(st, -1/t, kx)
-// is n / t + 1 + 2^-26 within 2^-29 (rounding of 1/t, kx and the fma, all
-// below 2^-53 relative on values under 2^23), and every non-integer n / t is
-// at least 1/t > 2^-23 below the next integer, so truncating e gives
-// q1 = floor(n / t) + 1 exactly. With rem = n - q t, the result
-// (t - ceil(rem / 2)) >> q equals (2t - rem) >> (q + 1) = ((q + 2) t - n)
-// >> q1, where (q + 2) t - n = q1 t + (t - mx) + st lies in (0, 2t]; it is
-// below 2^24, so shifts of 24 and more (clamped to 31) give the same 0 as
-// min(q, 62) for every q >= 23.
-__device__ __forceinline__ uint32_t pf_dexp(int32_t st, const PfFast& F) {
-  const uint32_t q1 = (uint32_t)fma((double)st, F.nrt, F.kx);
-  const uint32_t m = mad_u24(q1, F.t, F.cx + (uint32_t)st);
+// t < 2^23, from sp = st + t - mx (the MFMA adds t - mx for free).
+// n = mx - st < 2^22 (|q8 . k8| <= 2^21) and |sp| < 2^23. e = fma(sp, -1/t,
+// kx) is 2 - sp / t + 2^-26 = n / t + 1 + 2^-26 within 2^-29 (roundings of
+// 1/t, kx and the fma, each below 2^-53 relative on values under 2^24), and
+// every non-integer n / t is at least 1/t > 2^-23 below the next integer, so
+// truncating e gives q1 = floor(n / t) + 1 exactly. With rem = n - q t, the
+// result (t - ceil(rem / 2)) >> q equals (2t - rem) >> (q + 1) = (q1 t + sp)
+// >> q1, where q1 t + sp = (q + 2) t - n lies in (0, 2t]; it is below 2^24,
+// so shifts of 24 and more (clamped to 31) give the same 0 as min(q, 62)
+// for every q >= 23.
+__device__ __forceinline__ uint32_t pf_dexp(int32_t sp, const PfFast& F) {
+  const uint32_t q1 = (uint32_t)fma((double)sp, F.nrt, F.kx);
+  const uint32_t m = mad_u24(q1, F.t, (uint32_t)sp);
   return m >> min(q1, 31u);
 }
 
@@ -280,16 +281,16 @@ __global__ __launch_bounds__(256, 2) void k_attn_prefill(PrefillArgs a) {
     }
   };
   // both halves' K operands read at once (one LDS latency), then their
-  // score MFMAs: the first 64 dims of all 8 blocks, then the second 64 — the
+  // score MFMAs from accumulator z: the first 64 dims of all 8 blocks, then
+  // the second 64 — the
   // two MFMAs of a block are 8 issues apart, so none waits on the previous
   // one's result — overlapping the first half's VALU work; then
   // fn(st, it, half) per half that holds key slots
-  auto halves = [&](const int8_t* stg, int it2, auto&& fn) {
+  auto halves = [&](const int8_t* stg, int it2, const v4i z, auto&& fn) {
     v4i ka[8], kb[8], sa[4], sb[4];
     load_k(stg, ka);
     load_k(stg + 64 * 128, kb);
     __builtin_amdgcn_sched_barrier(0);
-    const v4i z = v4i{0, 0, 0, 0};
 #pragma unroll
     for (int blk = 0; blk < 4; ++blk) sa[blk] = mfma16(ka[2 * blk], qf0, z);
 #pragma unroll
@@ -313,7 +314,7 @@ __global__ __launch_bounds__(256, 2) void k_attn_prefill(PrefillArgs a) {
 
   // ---- pass 1: row max over visible slots (scores are int32)
   int mx = INT32_MIN;
-  pass(std::false_type{}, [&](int it2, const int8_t* stg) { halves(stg, it2, [&](const v4i (&st)[4], int it, int) {
+  pass(std::false_type{}, [&](int it2, const int8_t* stg) { halves(stg, it2, v4i{0, 0, 0, 0}, [&](const v4i (&st)[4], int it, int) {
     if (full_tile(it)) {
 #pragma unroll
       for (int blk = 0; blk < 4; ++blk)
@@ -339,15 +340,18 @@ __global__ __launch_bounds__(256, 2) void k_attn_prefill(PrefillArgs a) {
   const bool fexp = __ballot(tpos >= (i64)PF_SMALL_T) == 0;
   PfFast F;
   F.t = (uint32_t)tpos;
-  F.cx = F.t - (uint32_t)mx;
+  F.cx = (int32_t)(F.t - (uint32_t)mx);
   {
     const double rt = 1.0 / (double)F.t;
     F.nrt = -rt;
-    F.kx = fma((double)mx, rt, 1.0 + 0x1p-26);
+    F.kx = fma((double)F.t, rt, 1.0 + 0x1p-26);
   }
+  // fast path: scores arrive as st + t - mx; the general path subtracts it
+  const int32_t soff = fexp ? F.cx : 0;
+  const v4i cinit = v4i{soff, soff, soff, soff};
   const ExpR Et = make_exp(tpos);
   i64 den = 0;
-  pass(std::false_type{}, [&](int it2, const int8_t* stg) { halves(stg, it2, [&](const v4i (&st)[4], int it, int) {
+  pass(std::false_type{}, [&](int it2, const int8_t* stg) { halves(stg, it2, cinit, [&](const v4i (&st)[4], int it, int) {
     if (fexp && full_tile(it)) {
       uint32_t sum = 0;
 #pragma unroll
@@ -365,7 +369,7 @@ __global__ __launch_bounds__(256, 2) void k_attn_prefill(PrefillArgs a) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const bool vis = (bits >> (4 * blk + r)) & 1u;
-          const uint32_t e = pf_dexp(vis ? st[blk][r] : mx, F);
+          const uint32_t e = pf_dexp(vis ? st[blk][r] : (int32_t)F.t, F);
           sum += vis ? e : 0u;
         }
       den += sum;
@@ -375,7 +379,7 @@ __global__ __launch_bounds__(256, 2) void k_attn_prefill(PrefillArgs a) {
 #pragma unroll
         for (int r = 0; r < 4; ++r)
           if ((bits >> (4 * blk + r)) & 1u)
-            den = wadd(den, di_exp_neg((u64)(uint32_t)(mx - st[blk][r]), Et));
+            den = wadd(den, di_exp_neg((u64)(uint32_t)(mx - (st[blk][r] - soff)), Et));
     }
   }); });
   den = imax(group4_sum(den), 1);
@@ -400,7 +404,7 @@ __global__ __launch_bounds__(256, 2) void k_attn_prefill(PrefillArgs a) {
   int voff[2];
 #pragma unroll
   for (int hf = 0; hf < 2; ++hf) voff[hf] = PF_KBYTES + qi * 128 + (((4 * hf + g) ^ pf_vswz(qi)) << 4);
-  pass(std::true_type{}, [&](int it2, const int8_t* stg) { halves(stg, it2, [&](const v4i (&st)[4], int it, int hf) {
+  pass(std::true_type{}, [&](int it2, const int8_t* stg) { halves(stg, it2, cinit, [&](const v4i (&st)[4], int it, int hf) {
     v4i vf[8], vc[2];
 #pragma unroll
     for (int j = 0; j < 8; ++j) vf[j] = *(const v4i*)(stg + voff[hf] + j * 2048);
@@ -432,7 +436,7 @@ __global__ __launch_bounds__(256, 2) void k_attn_prefill(PrefillArgs a) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const bool vis = (bits >> (4 * blk + r)) & 1u;
-          const uint32_t e = pf_dexp(vis ? st[blk][r] : mx, F);
+          const uint32_t e = pf_dexp(vis ? st[blk][r] : (int32_t)F.t, F);
           p[r] = pf_pdiv(vis ? e : 0u, F);
         }
         put(blk, p);
@@ -445,7 +449,7 @@ __global__ __launch_bounds__(256, 2) void k_attn_prefill(PrefillArgs a) {
         for (int r = 0; r < 4; ++r) {
           i64 pv = 0;
           if ((bits >> (4 * blk + r)) & 1u) {
-            const i64 ex = di_exp_neg((u64)(uint32_t)(mx - st[blk][r]), Et);
+            const i64 ex = di_exp_neg((u64)(uint32_t)(mx - (st[blk][r] - soff)), Et);
             pv = to_i32(rhad_r(shl(ex, 14), Rd));
           }
           p[r] = (uint32_t)pv;

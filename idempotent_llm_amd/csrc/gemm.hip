@@ -114,9 +114,10 @@ __global__ __launch_bounds__(256) void k_gemm_nt(const int8_t* __restrict__ A,
 }
 
 // ---------------------------------------------------------------------------
-// k_gemm_nt2 — the prefill GEMM (M > 64, K % 128 == 0), on the full-rate
-// v_mfma_i32_32x32x32_i8 (the 16x16x64 form issues at about half its rate
-// on gfx950).
+// k_gemm_nt2 — the prefill GEMM (M > 64, K % 128 == 0), on
+// v_mfma_i32_32x32x32_i8: both i8 forms run at the same rate on gfx950
+// (measured, about 4.4 POP/s), but a 32x32x32 tile needs half the operand
+// bytes per multiply-add of a 16x16x64 one, so half the LDS reads.
 //
 // Operands stream into LDS with direct-to-LDS loads (global_load_lds_dwordx4:
 // lane l's 16 bytes land at base + 16 l) through an S-stage ring of 128-byte

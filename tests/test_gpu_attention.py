@@ -109,7 +109,7 @@ def test_fused_decode_group1():
 # ------------------------------------------------------------ prefill kernel
 
 def _prefill_case(B, n_q, n_kv, T, S_past, cap, seed, sk_lo, sk_hi, zero_heads=(),
-                  extreme_rows=(), dead_prefix=0, p_valid=0.75):
+                  extreme_rows=(), dead_prefix=0, p_valid=0.75, sm_lo=1 << 15):
     """Random prefill inputs: q8/K/V bytes, per-row score scales (sm, sk) and
     the DI-Exp constant tpos they give, a ragged validity mask. zero_heads get
     q = 0 (every score 0: flat rows, the largest denominators); extreme_rows
@@ -126,7 +126,7 @@ def _prefill_case(B, n_q, n_kv, T, S_past, cap, seed, sk_lo, sk_hi, zero_heads=(
     for (b, h, t) in extreme_rows:
         q8[b, h, t] = -128
         kc[b, h // (n_q // n_kv), :S:7] = -128
-    sm = rng.integers(1 << 15, 1 << 16, (B, n_q, T, 1), dtype=np.int64)
+    sm = rng.integers(sm_lo, 1 << 16, (B, n_q, T, 1), dtype=np.int64)
     sk = rng.integers(sk_lo, sk_hi + 1, (B, n_q, T, 1), dtype=np.int64)
     tpos = oops.di_exp_tpos(sm, sk)
     valid = rng.random((B, cap)) < p_valid
@@ -165,6 +165,10 @@ PREFILL_CASES = {
                        dict(extreme_rows=((0, 0, 3), (1, 1, 95), (0, 1, 50)))),
     "one_tile": (1, 2, 1, 64, 0, 64, 5, 30, 33, {}),
     "single_query": (3, 2, 2, 1, 300, 304, 6, 25, 45, dict(dead_prefix=301)),
+    # tpos just below 2^23 on every row, flat rows over 4096 slots: sums of
+    # exps beyond 2^34 next to small ones
+    "big_tpos_long_rows": (1, 2, 1, 64, 4032, 4096, 7, 39, 39,
+                           dict(zero_heads=(0,), sm_lo=60000, p_valid=1.0)),
 }
 
 
@@ -191,3 +195,5 @@ def test_prefill_attention_vs_oracle(name):
     assert bad.size == 0, f"{len(bad)} mismatches, first at {bad[0].tolist()}"
     if name == "flat_big_den":
         assert tpos[0, 0].max() > (1 << 32)  # den = sum of exps >= tpos * visible slots
+    if name == "big_tpos_long_rows":
+        assert tpos.max() < (1 << 23) and tpos.min() * 4033 > (1 << 34)
