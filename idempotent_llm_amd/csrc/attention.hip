@@ -71,51 +71,13 @@ constexpr i64 PF_SMALL_DEN = (i64)1 << 34;  // estimated p below this den
 __device__ __forceinline__ int pf_kswz(int row) { return (row & 3) | ((row >> 2) & 4); }
 __device__ __forceinline__ int pf_vswz(int d) { return d & 7; }
 
-// v_mad_u32_u24: a b + c with a, b < 2^24 (full rate; the 32-bit multiplies
-// issue at a quarter of it). Written out because the compiler cannot see the
-// operand bound across the loop blocks and would pick the 32-bit form.
-__device__ __forceinline__ uint32_t mad_u24(uint32_t a, uint32_t b, uint32_t c) {
-  uint32_t d;
-  asm("v_mad_u32_u24 %0, %1, %2, %3" : "=v"(d) : "v"(a), "v"(b), "v"(c));
-  return d;
-}
-
-// Per-query constants of the estimated DI-Exp and division (fp64 runs at
-// the full vector rate on gfx950).
+// Per-query constants of the estimated DI-Exp and division (intops.h).
 struct PfFast {
-  double nrt;   // -fl(1 / t)
-  double kx;    // fl(t fl(1 / t) + 1 + 2^-26)
-  uint32_t t;   // tpos < 2^23
-  int32_t cx;   // t - mx: the score MFMAs of passes 2 and 3 start from it
-  double r14;   // fl(2^14 / den)
-  double kp;    // fl(fl(floor(den / 2) / den) + 2^-36)
+  ExpEst E;    // tpos < 2^23
+  double kx;   // dexp_sp_const(E)
+  int32_t cx;  // t - mx: the score MFMAs of passes 2 and 3 start from it
+  DivEst D;    // make_divest(den, 2^14): p = rhad(ex << 14, den), den < 2^34
 };
-
-// DI-Exp of st - mx (ops/di_exp.py:27-37) for a visible score st <= mx and
-// t < 2^23, from sp = st + t - mx (the MFMA adds t - mx for free).
-// n = mx - st < 2^22 (|q8 . k8| <= 2^21) and |sp| < 2^23. e = fma(sp, -1/t,
-// kx) is 2 - sp / t + 2^-26 = n / t + 1 + 2^-26 within 2^-29 (roundings of
-// 1/t, kx and the fma, each below 2^-53 relative on values under 2^24), and
-// every non-integer n / t is at least 1/t > 2^-23 below the next integer, so
-// truncating e gives q1 = floor(n / t) + 1 exactly. With rem = n - q t, the
-// result (t - ceil(rem / 2)) >> q equals (2t - rem) >> (q + 1) = (q1 t + sp)
-// >> q1, where q1 t + sp = (q + 2) t - n lies in (0, 2t]; it is below 2^24,
-// so shifts of 24 and more (clamped to 31) give the same 0 as min(q, 62)
-// for every q >= 23.
-__device__ __forceinline__ uint32_t pf_dexp(int32_t sp, const PfFast& F) {
-  const uint32_t q1 = (uint32_t)fma((double)sp, F.nrt, F.kx);
-  const uint32_t m = mad_u24(q1, F.t, (uint32_t)sp);
-  return m >> min(q1, 31u);
-}
-
-// p = round_half_away_div(ex << 14, den) = floor((ex 2^14 + floor(den / 2)) /
-// den) for 0 <= ex <= den < 2^34 (ex < 2^23): fma(ex, r14, kp) is the exact
-// quotient + 2^-36 within 2^-37 (r14 and the fma round at 2^-39 on values
-// below 2^15, kp at 2^-54), and a non-integer quotient is at least
-// 1/den > 2^-34 below the next integer, so truncation gives the floor.
-__device__ __forceinline__ uint32_t pf_pdiv(uint32_t ex, const PfFast& F) {
-  return (uint32_t)fma((double)ex, F.r14, F.kp);
-}
 
 // Four probabilities (slot order = byte order) as the two MFMA operands of
 // the hi/lo split p = 128 hi + lo: bytes hi - 64 = (p - 8192) >> 7 in
@@ -339,13 +301,9 @@ __global__ __launch_bounds__(256, 2) void k_attn_prefill(PrefillArgs a) {
   // estimate as st = mx (a defined conversion) and are then dropped.
   const bool fexp = __ballot(tpos >= (i64)PF_SMALL_T) == 0;
   PfFast F;
-  F.t = (uint32_t)tpos;
-  F.cx = (int32_t)(F.t - (uint32_t)mx);
-  {
-    const double rt = 1.0 / (double)F.t;
-    F.nrt = -rt;
-    F.kx = fma((double)F.t, rt, 1.0 + 0x1p-26);
-  }
+  F.E = make_expest(tpos);
+  F.kx = dexp_sp_const(F.E);
+  F.cx = (int32_t)(F.E.t - (uint32_t)mx);
   // fast path: scores arrive as st + t - mx; the general path subtracts it
   const int32_t soff = fexp ? F.cx : 0;
   const v4i cinit = v4i{soff, soff, soff, soff};
@@ -357,7 +315,7 @@ __global__ __launch_bounds__(256, 2) void k_attn_prefill(PrefillArgs a) {
 #pragma unroll
       for (int blk = 0; blk < 4; ++blk)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) sum += pf_dexp(st[blk][r], F);
+        for (int r = 0; r < 4; ++r) sum += dexp_est_sp(st[blk][r], F.E, F.kx);
       den += sum;
       return;
     }
@@ -369,7 +327,7 @@ __global__ __launch_bounds__(256, 2) void k_attn_prefill(PrefillArgs a) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const bool vis = (bits >> (4 * blk + r)) & 1u;
-          const uint32_t e = pf_dexp(vis ? st[blk][r] : (int32_t)F.t, F);
+          const uint32_t e = dexp_est_sp(vis ? st[blk][r] : (int32_t)F.E.t, F.E, F.kx);
           sum += vis ? e : 0u;
         }
       den += sum;
@@ -384,8 +342,7 @@ __global__ __launch_bounds__(256, 2) void k_attn_prefill(PrefillArgs a) {
   }); });
   den = imax(group4_sum(den), 1);
   const bool fdiv = fexp && __ballot(den >= PF_SMALL_DEN) == 0;
-  F.r14 = 16384.0 / (double)den;
-  F.kp = (double)(den >> 1) / (double)den + 0x1p-36;
+  F.D = make_divest(den, 16384.0);
   const Recip Rd = make_recip(den);
 
   // ---- pass 3: p, then P.V on MFMA with the hi/lo split; wave w also sums
@@ -426,7 +383,7 @@ __global__ __launch_bounds__(256, 2) void k_attn_prefill(PrefillArgs a) {
       for (int blk = 0; blk < 4; ++blk) {
         uint32_t p[4];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) p[r] = pf_pdiv(pf_dexp(st[blk][r], F), F);
+        for (int r = 0; r < 4; ++r) p[r] = rhad_est((double)dexp_est_sp(st[blk][r], F.E, F.kx), F.D);
         put(blk, p);
       }
     } else if (fdiv) {
@@ -436,8 +393,8 @@ __global__ __launch_bounds__(256, 2) void k_attn_prefill(PrefillArgs a) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const bool vis = (bits >> (4 * blk + r)) & 1u;
-          const uint32_t e = pf_dexp(vis ? st[blk][r] : (int32_t)F.t, F);
-          p[r] = pf_pdiv(vis ? e : 0u, F);
+          const uint32_t e = dexp_est_sp(vis ? st[blk][r] : (int32_t)F.E.t, F.E, F.kx);
+          p[r] = rhad_est((double)(vis ? e : 0u), F.D);
         }
         put(blk, p);
       }

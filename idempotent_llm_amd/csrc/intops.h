@@ -19,6 +19,7 @@
 // one-correction form. Tested exhaustively near multiples of d on the host.
 #pragma once
 
+#include <math.h>
 #include <stdint.h>
 
 #if defined(__HIPCC__) || defined(__HIP__)
@@ -365,6 +366,129 @@ DI_HD i64 swiglu_elem_e(i64 g, i64 u, const ExpR& E) {
     return wmul((i64)(int32_t)g * sig, u);
   }
   return swiglu_elem(g, u, E.tpos, E.R);
+}
+
+// ---- exact integers from biased fp64 estimates -------------------------
+//
+// fp64 runs at the full vector rate on gfx950, while a 64-bit integer
+// division or reciprocal multiply costs tens of instructions. Each helper
+// below computes an integer quotient as the truncation of one fp64 estimate
+// that carries a bias large enough to cover every rounding error of the
+// estimate and small enough to stay below the gap to the next integer, so
+// the truncation is exact. Callers check the stated operand bounds (a
+// wave-uniform test per row) and otherwise take the integer routines above.
+// fma and the fp64 division are IEEE-correctly rounded on the device and on
+// the host, so the host build of these helpers is the device arithmetic.
+
+// v_mad_u32_u24: a b + c (mod 2^32) for a, b < 2^24, full rate on gfx950
+// (the 32-bit multiplies issue at a quarter of it). Written out on the
+// device because the compiler does not always see the operand bounds.
+DI_HD uint32_t mad_u24(uint32_t a, uint32_t b, uint32_t c) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  uint32_t d;
+  asm("v_mad_u32_u24 %0, %1, %2, %3" : "=v"(d) : "v"(a), "v"(b), "v"(c));
+  return d;
+#else
+  return a * b + c;
+#endif
+}
+
+// rhad(m s, d) = floor((m s + floor(d/2)) / d) for an exact integer m >= 0, a
+// scale s (a power of two or 127) and a row-invariant d >= 1, from r = fl(s/d)
+// and k = fl((floor(d/2) + 1/2) / d): fma(m, r, k) = v + 1/(2d) + err with
+// v = (m s + floor(d/2)) / d and |err| <= (2 m s + d + 2) 2^-53 / d (one
+// relative rounding each on r, k and the fma). When 2 m s + d < 2^51,
+// |err| < 1/(2d); v is a multiple of 1/d, at most (d - 1)/d above floor(v),
+// so the estimate lies in (v, floor(v) + 1) and truncates to floor(v).
+// Quotients below 2^32.
+struct DivEst {
+  double r;
+  double k;
+};
+
+DI_HD DivEst make_divest(i64 d, double s) {  // 1 <= d < 2^51
+  DivEst D;
+  D.r = s / (double)d;
+  D.k = ((double)(d >> 1) + 0.5) / (double)d;
+  return D;
+}
+
+DI_HD uint32_t rhad_est(double m, const DivEst& D) { return (uint32_t)fma(m, D.r, D.k); }
+
+// sign(a) rhad(|a| s, d) for |a| s bounded as above, as a signed int32
+DI_HD int32_t rhad_est_signed(i64 a, const DivEst& D) {
+  const uint32_t q = rhad_est((double)(a < 0 ? -a : a), D);
+  return a < 0 ? -(int32_t)q : (int32_t)q;
+}
+
+// sigmoid division round_half_away_div(num << 7, den) (ops/di_swiglu.py:
+// 52-55) for 0 <= num <= den < 2^31, den >= 1: the quotient v = (128 num +
+// floor(den/2)) / den is at most 128.5; fl((128 num + floor(den/2) + 1/2) /
+// den) = v + 1/(2 den) within 2^-53 129 < 1/(2 den) (the numerator is exact),
+// so it truncates to floor(v) as above.
+DI_HD uint32_t sigmoid_est(uint32_t num, uint32_t den) {
+  return (uint32_t)(fma((double)num, 128.0, (double)(den >> 1) + 0.5) / (double)den);
+}
+
+// DI-Exp of -n (ops/di_exp.py:27-37) for 0 <= n < 2^22 and a row-invariant
+// 1 <= t < 2^23: e = fma(n, fl(1/t), 1 + 2^-26) is n/t + 1 + 2^-26 within
+// 2^-30 (the rounding of 1/t and of the fma, on values below 2^23), and a
+// non-integer n/t is at least 1/t > 2^-23 below the next integer, so e
+// truncates to q1 = floor(n/t) + 1. With rem = n - q t, the result
+// (t - ceil(rem/2)) >> q is (2t - rem) >> (q + 1) = (q1 t + t - n) >> q1,
+// where q1 t + t - n = (q + 2) t - n lies in (0, 2t] below 2^24, so any shift
+// of 24 or more (clamped to 31) gives the 0 that min(q, 62) gives for
+// q >= 23.
+struct ExpEst {
+  double rt;   // fl(1 / t)
+  uint32_t t;  // tpos
+};
+
+DI_HD ExpEst make_expest(i64 tpos) {  // 1 <= tpos < 2^23
+  ExpEst E;
+  E.t = (uint32_t)tpos;
+  E.rt = 1.0 / (double)tpos;
+  return E;
+}
+
+// di_exp_tpos with the division rhad(2^k, m_f) from the estimate when
+// 0 <= k <= 46 and 1 <= m_f < 2^31 (2 * 2^k + m_f < 2^51, quotient < 2^32
+// for m_f >= 2^15; smaller m_f takes the integer path); same integer.
+DI_HD i64 di_exp_tpos_fast(i64 m, i64 k) {
+  const i64 m_f = wsub(wadd(m, shr(m, 1)), shr(m, 4));
+  if (k >= 0 && k <= 46 && m_f >= ((i64)1 << 15) && m_f < ((i64)1 << 31))
+    return imax((i64)rhad_est((double)((i64)1 << k), make_divest(m_f, 1.0)), 1);
+  return di_exp_tpos(m, k);
+}
+
+DI_HD uint32_t dexp_est(uint32_t n, const ExpEst& E) {
+  const uint32_t q1 = (uint32_t)fma((double)n, E.rt, 1.0 + 0x1p-26);
+  const uint32_t m = mad_u24(q1, E.t, E.t - n);
+  return m >> (q1 < 31u ? q1 : 31u);
+}
+
+// dexp_est of n = mx - st taken from sp = st + t - mx (attention adds t - mx
+// to the scores for free in the MFMA accumulator): |sp| < 2^23, and
+// fma(sp, -fl(1/t), fl(t fl(1/t) + 1 + 2^-26)) = 2 - sp/t + 2^-26 =
+// n/t + 1 + 2^-26 within 2^-29 (roundings of 1/t, of the constant and of the
+// fma on values below 2^24), so the same truncation argument holds, and
+// q1 t + sp = q1 t + t - n.
+DI_HD double dexp_sp_const(const ExpEst& E) { return fma((double)E.t, E.rt, 1.0 + 0x1p-26); }
+
+DI_HD uint32_t dexp_est_sp(int32_t sp, const ExpEst& E, double kx) {
+  const uint32_t q1 = (uint32_t)fma((double)sp, -E.rt, kx);
+  const uint32_t m = mad_u24(q1, E.t, (uint32_t)sp);
+  return m >> (q1 < 31u ? q1 : 31u);
+}
+
+// ops/di_swiglu.py:39-58 on one element for |g|, |u| <= 2^14 (gate and up
+// after requant_i32_common(14)) and tpos < 2^23: |g| < 2^22 for dexp_est,
+// E <= tpos and den = tpos + E < 2^24 for sigmoid_est, g * sig (sig <= 128)
+// fits int32 and g * sig * u int64. Same integer as swiglu_elem.
+DI_HD i64 swiglu_elem_est(int32_t g, int32_t u, const ExpEst& E) {
+  const uint32_t e = dexp_est((uint32_t)(g < 0 ? -g : g), E);
+  const uint32_t sig = sigmoid_est(g >= 0 ? E.t : e, E.t + e);
+  return (i64)(g * (int32_t)sig) * (i64)u;
 }
 
 }  // namespace di

@@ -40,6 +40,7 @@ void di_host_scalar(int op, const int64_t* a, const int64_t* b, const int64_t* c
       case 3: fit_dyadic_ratio(a[i], b[i], &x, &y); o1[i] = x; o2[i] = y; break;
       case 5: fit_dyadic_ratio_127(a[i], &x, &y); o1[i] = x; o2[i] = y; break;
       case 6: o1[i] = rhad_pow2(a[i], (int)b[i]); break;
+      case 7: o1[i] = di_exp_tpos_fast(a[i], b[i]); break;
       default: o1[i] = scaled_round_div(a[i], b[i], c[i]); break;
     }
   }
@@ -56,6 +57,34 @@ void di_host_sigmoid_div32(const int64_t* num, const int64_t* den, int64_t n, in
 }
 void di_host_rshift_round(const int64_t* a, const int64_t* k, int64_t n, int64_t* out) {
   for (int64_t i = 0; i < n; ++i) out[i] = rshift_round(a[i], k[i]);
+}
+
+void di_host_rhad_est(const int64_t* m, const int64_t* d, const double* sc, int64_t n,
+                      int64_t* out) {
+  for (int64_t i = 0; i < n; ++i) out[i] = rhad_est((double)m[i], make_divest(d[i], sc[i]));
+}
+void di_host_sigmoid_est(const int64_t* num, const int64_t* den, int64_t n, int64_t* out) {
+  for (int64_t i = 0; i < n; ++i) out[i] = sigmoid_est((uint32_t)num[i], (uint32_t)den[i]);
+}
+// Mismatches of dexp_est(n) and dexp_est_sp(t - n) against the integer DI-Exp
+// for every n in [n_lo, n_hi) at one tpos.
+int64_t di_host_dexp_est_mismatches(int64_t tpos, int64_t n_lo, int64_t n_hi) {
+  const ExpR R = make_exp(tpos);
+  const ExpEst E = make_expest(tpos);
+  const double kx = dexp_sp_const(E);
+  int64_t bad = 0;
+  for (int64_t n = n_lo; n < n_hi; ++n) {
+    const int64_t want = di_exp_r(-n, tpos, R.R);
+    bad += (int64_t)dexp_est((uint32_t)n, E) != want;
+    bad += (int64_t)dexp_est_sp((int32_t)(tpos - n), E, kx) != want;
+  }
+  return bad;
+}
+
+void di_host_swiglu_est(const int64_t* g, const int64_t* u, const int64_t* tpos, int64_t n,
+                        int64_t* out) {
+  for (int64_t i = 0; i < n; ++i)
+    out[i] = swiglu_elem_est((int32_t)g[i], (int32_t)u[i], make_expest(tpos[i]));
 }
 
 }  // extern "C"

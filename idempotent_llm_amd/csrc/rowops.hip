@@ -73,18 +73,29 @@ __device__ __forceinline__ void rmsnorm_row(i64 (&v)[VPT], int C, BlockRed& red,
   for (int j = 0; j < VPT; ++j) v[j] = to_i32(rhad_r(shl(v[j], 20), R));
 }
 
-// dyadic.py:93-105
+// dyadic.py:93-105. The quotients rhad(127 x, a) with |x| <= a come from the
+// fp64 estimate (intops.h rhad_est) when a < 2^43 (then 2 * 127 |x| + a <
+// 2^51 and no 127 x wraps), else from the 64-bit reciprocal.
 template <int VPT>
 __device__ __forceinline__ void quant_row(const i64 (&v)[VPT], i64 m_in, i64 k_in, int C,
                                           BlockRed& red, int8_t* out, i64* m_out, i64* k_out) {
   i64 m, k;
   norm_scale(m_in, k_in, &m, &k);
   const i64 a = imax(row_absmax(v, red), 1);
-  const Recip R = make_recip(a);
+  if (a < ((i64)1 << 43)) {
+    const DivEst D = make_divest(a, 127.0);
 #pragma unroll
-  for (int j = 0; j < VPT; ++j) {
-    const int c = threadIdx.x + j * (int)blockDim.x;
-    if (c < C) out[c] = (int8_t)clamp_i8(rhad_r(wmul(v[j], 127), R));
+    for (int j = 0; j < VPT; ++j) {
+      const int c = threadIdx.x + j * (int)blockDim.x;
+      if (c < C) out[c] = (int8_t)rhad_est_signed(v[j], D);
+    }
+  } else {
+    const Recip R = make_recip(a);
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) {
+      const int c = threadIdx.x + j * (int)blockDim.x;
+      if (c < C) out[c] = (int8_t)clamp_i8(rhad_r(wmul(v[j], 127), R));
+    }
   }
   if (threadIdx.x == 0) {
     i64 mo, e;
@@ -364,9 +375,19 @@ __device__ __forceinline__ void swiglu_quant_row(const SwigluArgs& a, int r, Blo
   load_rows_i32_sum<2, VPT>(gu, a.P, a.nsplit, a.split_stride, offs, I);
   i64 gk, uk;
   requant_common_row2(gu[0], gm, a.gate_k, gu[1], um, a.up_k, xk, 14, red, &gk, &uk);
-  const ExpR E = make_exp(di_exp_tpos(xm, gk));
+  const i64 tp = di_exp_tpos_fast(xm, gk);
+  if (tp < ((i64)1 << 23)) {
+    // requant_i32_common(14) leaves |g|, |u| <= 2^14 (the shift brings the
+    // row's largest magnitude to at most 2^14)
+    const ExpEst Ee = make_expest(tp);
 #pragma unroll
-  for (int j = 0; j < VPT; ++j) gu[0][j] = wmul(swiglu_elem_e(gu[0][j], gu[1][j], E), dsm[j]);
+    for (int j = 0; j < VPT; ++j)
+      gu[0][j] = wmul(swiglu_elem_est((int32_t)gu[0][j], (int32_t)gu[1][j], Ee), dsm[j]);
+  } else {
+    const ExpR E = make_exp(tp);
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) gu[0][j] = wmul(swiglu_elem_e(gu[0][j], gu[1][j], E), dsm[j]);
+  }
   const i64 ym = wmul(xm, xm);
   const i64 yk = wadd(wadd(wadd(gk, uk), 7), a.ds_k);
   quant_row(gu[0], ym, yk, I, red, a.y8 + (i64)r * I, a.ym + r, a.yk + r);

@@ -271,3 +271,116 @@ def test_swiglu_elem_fast_path_matches_generic(lib):
     got = _call2_3(lib, "di_host_swiglu_e", g, u, tpos)
     want = _call2_3(lib, "di_host_swiglu", g, u, tpos)
     assert np.array_equal(got, want)
+
+
+# ------------------------------------------- exact integers from fp64 estimates
+
+def _rhad_est_cases(seed=11):
+    rnd = random.Random(seed)
+    M, D, S = [], [], []
+    scales = [1.0, 127.0, float(1 << 14), float(1 << 20)]
+    ds = [1, 2, 3, 5, 127, 128, 255, 4097, (1 << 20) + 1, (1 << 31) - 1, (1 << 34) - 3,
+          (1 << 40) + 7, (1 << 47) - 1]
+    ds += [rnd.randrange(1, 1 << rnd.randrange(1, 48)) for _ in range(300)]
+    for d in ds:
+        for s in scales:
+            si = int(s)
+            # m s + d/2 < 2^32 d (quotient below 2^32) and 2 m s + d < 2^51
+            mmax = min(((1 << 51) - d) // (2 * si), ((1 << 32) * d - d // 2) // si - 1)
+            if mmax < 0:
+                continue
+            for _ in range(24):
+                kind = rnd.randrange(4)
+                if kind == 0:   # numerator at / next to a multiple of d
+                    q = rnd.randrange(0, max(1, mmax * si // d + 1))
+                    tgt = q * d - d // 2 + rnd.choice([-1, 0, 1])
+                    m = max(0, min(mmax, tgt // si + rnd.choice([0, 1])))
+                elif kind == 1:
+                    m = rnd.randrange(0, mmax + 1)
+                elif kind == 2:
+                    m = mmax - rnd.randrange(0, min(mmax, 16) + 1)
+                else:
+                    m = rnd.randrange(0, min(mmax, 4 * d) + 1)
+                M.append(m)
+                D.append(d)
+                S.append(s)
+    return np.array(M, I64), np.array(D, I64), np.array(S, np.float64)
+
+
+def test_rhad_est_exact(lib):
+    """rhad_est (fp64 estimate, intops.h) equals floor((m s + floor(d/2)) / d)
+    in exact integer arithmetic across divisor magnitudes 1..2^47, the scales
+    the kernels use, numerators at multiples of d and at the stated bound."""
+    M, D, S = _rhad_est_cases()
+    out = np.empty_like(M)
+    lib.di_host_rhad_est(_p(M), _p(D), _p(S), ctypes.c_int64(M.size), _p(out))
+    want = [(int(m) * int(s) + int(d) // 2) // int(d) for m, d, s in zip(M, D, S)]
+    assert out.tolist() == want
+
+
+def test_sigmoid_est_matches_restoring_division(lib):
+    """sigmoid_est == round_half_away_div(num << 7, den) for num <= den < 2^31,
+    including every num for small den and ties."""
+    rnd = random.Random(5)
+    num, den = [], []
+    for d in range(1, 300):
+        for n in range(0, d + 1):
+            num.append(n)
+            den.append(d)
+    for _ in range(200000):
+        d = rnd.randrange(1, 1 << rnd.randrange(1, 32))
+        d = min(d, (1 << 31) - 1)
+        num.append(rnd.choice([0, d, d - 1, d // 2, rnd.randrange(0, d + 1)]))
+        den.append(d)
+    num = np.array(num, I64)
+    den = np.array(den, I64)
+    got = _call2(lib, "di_host_sigmoid_est", num, den)
+    want = [(int(n) * 128 + int(d) // 2) // int(d) for n, d in zip(num, den)]
+    assert got.tolist() == want
+
+
+@pytest.mark.parametrize("tpos", [1, 2, 3, 7, 100, 4095, 4096, 46341, 65537, 360626,
+                                  (1 << 22) + 1, (1 << 23) - 1])
+def test_dexp_est_exhaustive(lib, tpos):
+    """dexp_est(n) and dexp_est_sp(t - n) equal the integer DI-Exp (di_exp_r,
+    pinned to the oracle above) for every n < 2^22 at tpos up to 2^23 - 1."""
+    lib.di_host_dexp_est_mismatches.restype = ctypes.c_int64
+    bad = lib.di_host_dexp_est_mismatches(ctypes.c_int64(tpos), ctypes.c_int64(0),
+                                          ctypes.c_int64(1 << 22))
+    assert bad == 0
+
+
+def test_di_exp_tpos_fast_matches_oracle(lib):
+    """di_exp_tpos_fast (division by m_f from the fp64 estimate where its
+    bounds hold) equals the oracle's DI-Exp constant for mantissas across
+    and beyond the normalised range and shifts k from -3 to 66."""
+    rnd = np.random.default_rng(17)
+    m = np.concatenate([rnd.integers(1 << 15, 1 << 16, 40000, dtype=I64),
+                        rnd.integers(1, 1 << 40, 10000, dtype=I64),
+                        np.array([1, 2, 10, 32767, 32768, 65535, 65536, (1 << 31) - 1], I64)])
+    k = rnd.integers(-3, 67, m.size, dtype=I64)
+    k[:70] = np.arange(-3, 67)
+    got, _ = _scalar(lib, 7, m, k)
+    assert np.array_equal(got, oops.di_exp_tpos(m, k))
+
+
+def test_swiglu_elem_est_matches_oracle(lib):
+    """The fused kernel's SwiGLU element (dexp_est + sigmoid_est) equals the
+    oracle's di_swiglu (ops/di_swiglu.py:39-58) for |g|, |u| <= 2^14 and
+    tpos < 2^23: every g in [-2^14, 2^14] at a few row scales, random pairs
+    elsewhere; tpos comes from the oracle's constant for each (gm, gk)."""
+    rnd = np.random.default_rng(41)
+    full = np.arange(-(1 << 14), (1 << 14) + 1, dtype=I64)
+    n = 200000
+    g = np.concatenate([full] * 4 + [rnd.integers(-(1 << 14), (1 << 14) + 1, n, dtype=I64)])
+    gm = np.concatenate([np.full(full.size, m, I64) for m in (32768, 40000, 50000, 65535)]
+                        + [rnd.integers(1 << 15, 1 << 16, n, dtype=I64)])
+    gk = np.concatenate([np.full(full.size, k, I64) for k in (15, 28, 31, 38)]
+                        + [rnd.integers(0, 39, n, dtype=I64)])
+    tpos = oops.di_exp_tpos(gm, gk)
+    keep = tpos < (1 << 23)
+    g, gm, gk, tpos = g[keep], gm[keep], gk[keep], tpos[keep]
+    u = rnd.integers(-(1 << 14), (1 << 14) + 1, g.size, dtype=I64)
+    got = _call2_3(lib, "di_host_swiglu_est", g, u, tpos)
+    want, _, _ = oops.di_swiglu(g, gm, gk, u, np.ones_like(u), np.zeros_like(u))
+    assert g.size > 150000 and np.array_equal(got, want)
