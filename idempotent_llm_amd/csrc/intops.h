@@ -421,6 +421,28 @@ DI_HD int32_t rhad_est_signed(i64 a, const DivEst& D) {
   return a < 0 ? -(int32_t)q : (int32_t)q;
 }
 
+// clamp_i8(rhad(n, d)) for 2 |n| + d < 2^51: estimates at or above 255
+// (quotients of 255 or more) saturate before the conversion and clamp like
+// the integer quotient would.
+DI_HD int rhad_est_i8(i64 n, const DivEst& D) {
+  const double e = fmin(fma((double)(n < 0 ? -n : n), D.r, D.k), 255.0);
+  const int q = (int)(uint32_t)e;
+  const int sq = n < 0 ? -q : q;
+  return sq < -128 ? -128 : (sq > 127 ? 127 : sq);
+}
+
+// rhad(s |a|, d) signed, for s |a| + d < 2^53 and quotients below 2^31: the
+// estimate may be one off once 2 s |a| + d reaches 2^51, so its truncation
+// q0 is corrected with the exact remainder s |a| + floor(d/2) - q0 d (all
+// terms below 2^54 as int64).
+DI_HD int32_t rhad_est_corr_signed(i64 a, int s, i64 d, const DivEst& D) {
+  const i64 n = (a < 0 ? -a : a) * (i64)s + (d >> 1);
+  i64 q = (i64)(uint32_t)fma((double)(a < 0 ? -a : a), D.r, D.k);
+  const i64 rem = n - q * d;
+  q += (rem >= d ? 1 : 0) - (rem < 0 ? 1 : 0);
+  return a < 0 ? -(int32_t)q : (int32_t)q;
+}
+
 // sigmoid division round_half_away_div(num << 7, den) (ops/di_swiglu.py:
 // 52-55) for 0 <= num <= den < 2^31, den >= 1: the quotient v = (128 num +
 // floor(den/2)) / den is at most 128.5; fl((128 num + floor(den/2) + 1/2) /

@@ -87,4 +87,15 @@ void di_host_swiglu_est(const int64_t* g, const int64_t* u, const int64_t* tpos,
     out[i] = swiglu_elem_est((int32_t)g[i], (int32_t)u[i], make_expest(tpos[i]));
 }
 
+// op 0: rhad_est_signed(a, divest(d, s)); 1: rhad_est_i8(a, divest(d, 1));
+// 2: rhad_est_corr_signed(a, s, d, divest(d, s))
+void di_host_rhad_est_op(int op, const int64_t* a, const int64_t* d, const int64_t* sc,
+                         int64_t n, int64_t* out) {
+  for (int64_t i = 0; i < n; ++i) {
+    const DivEst D = make_divest(d[i], op == 1 ? 1.0 : (double)sc[i]);
+    out[i] = op == 0 ? rhad_est_signed(a[i], D)
+                     : (op == 1 ? rhad_est_i8(a[i], D) : rhad_est_corr_signed(a[i], (int)sc[i], d[i], D));
+  }
+}
+
 }  // extern "C"

@@ -63,9 +63,17 @@ __device__ __forceinline__ void wave_rmsnorm128(i64& a, i64& b) {
   a = shl(rshift_round(a, down), up);
   b = shl(rshift_round(b, down), up);
   const i64 ss = wave_sum(wadd(wmul(a, a), wmul(b, b)));
-  const Recip R = make_recip(imax(isqrt_wave(rhad_pow2(ss, 7)), 1));
-  a = to_i32(rhad_r(shl(a, 20), R));
-  b = to_i32(rhad_r(shl(b, 20), R));
+  const i64 rms = imax(isqrt_wave(rhad_pow2(ss, 7)), 1);
+  if (rms > ((i64)1 << 16)) {
+    // |a|, |b| <= 2^26 after the shift: rhad_est as in rmsnorm_row
+    const DivEst D = make_divest(rms, 1048576.0);
+    a = rhad_est_signed(a, D);
+    b = rhad_est_signed(b, D);
+  } else {
+    const Recip R = make_recip(rms);
+    a = to_i32(rhad_r(shl(a, 20), R));
+    b = to_i32(rhad_r(shl(b, 20), R));
+  }
 }
 
 // The whole wave must be active. K and V go to the cache; a query head's
@@ -133,11 +141,21 @@ __device__ __forceinline__ void qkv_head(const QKVArgs& a, int r, int slotw, int
     if (den <= 0) den = 1;  // static scales are positive mantissas in artifacts
     const i64 n0 = shl(wmul(wmul(p0, wm0), xm), up);
     const i64 n1 = shl(wmul(wmul(p1, wm1), xm), up);
-    const Recip R = make_recip(den);
     int8_t* vrow = a.vcache + ((i64)b * a.n_kv + h) * 128 * a.cap;
+    int8_t o0, o1;
+    const i64 lim = (i64)1 << 49;  // 2 |n| + den < 2^51 for rhad_est_i8
+    if (den < lim && n0 > -lim && n0 < lim && n1 > -lim && n1 < lim) {
+      const DivEst D = make_divest(den, 1.0);
+      o0 = (int8_t)rhad_est_i8(n0, D);
+      o1 = (int8_t)rhad_est_i8(n1, D);
+    } else {
+      const Recip R = make_recip(den);
+      o0 = (int8_t)clamp_i8(rhad_r(n0, R));
+      o1 = (int8_t)clamp_i8(rhad_r(n1, R));
+    }
     if (slot >= 0 && slot < a.cap) {
-      vrow[(i64)c0 * a.cap + slot] = (int8_t)clamp_i8(rhad_r(n0, R));
-      vrow[(i64)c1 * a.cap + slot] = (int8_t)clamp_i8(rhad_r(n1, R));
+      vrow[(i64)c0 * a.cap + slot] = o0;
+      vrow[(i64)c1 * a.cap + slot] = o1;
     }
     return;
   }
@@ -168,7 +186,12 @@ __device__ __forceinline__ void qkv_head(const QKVArgs& a, int r, int slotw, int
       const i64 up = imax(wneg(shift), 0), down = imax(shift, 0);
       i64 den = shl(km[q], down);
       if (den <= 0) den = 1;
-      outv[q] = clamp_i8(rhad(shl(rv[q], up), den));
+      const i64 n = shl(rv[q], up);
+      const i64 lim = (i64)1 << 49;  // 2 |n| + den < 2^51 for rhad_est_i8
+      if (den < lim && n > -lim && n < lim)
+        outv[q] = rhad_est_i8(n, make_divest(den, 1.0));
+      else
+        outv[q] = clamp_i8(rhad(n, den));
     }
     if (slot >= 0 && slot < a.cap) {
       krow[c0] = (int8_t)outv[0];
@@ -183,10 +206,16 @@ __device__ __forceinline__ void qkv_head(const QKVArgs& a, int r, int slotw, int
   i64 m, k;
   norm_scale(1, qkk, &m, &k);
   const i64 am = imax(wave_max(imax(wabs(q0), wabs(q1))), 1);
-  const Recip R = make_recip(am);
   const i64 qrow = (((i64)b * a.n_q + h) * a.T + t);
-  q8_out[c0] = (int8_t)clamp_i8(rhad_r(wmul(q0, 127), R));
-  q8_out[c1] = (int8_t)clamp_i8(rhad_r(wmul(q1, 127), R));
+  if (am < ((i64)1 << 43)) {  // as in quant_row: no 127 q wraps, 255 am < 2^51
+    const DivEst D = make_divest(am, 127.0);
+    q8_out[c0] = (int8_t)rhad_est_signed(q0, D);
+    q8_out[c1] = (int8_t)rhad_est_signed(q1, D);
+  } else {
+    const Recip R = make_recip(am);
+    q8_out[c0] = (int8_t)clamp_i8(rhad_r(wmul(q0, 127), R));
+    q8_out[c1] = (int8_t)clamp_i8(rhad_r(wmul(q1, 127), R));
+  }
   if (lane == 0) {
     i64 qm, e;
     fit_dyadic_ratio_127(wmul(am, m), &qm, &e);

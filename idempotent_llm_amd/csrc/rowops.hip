@@ -68,9 +68,18 @@ __device__ __forceinline__ void rmsnorm_row(i64 (&v)[VPT], int C, BlockRed& red,
   }
   ss = red.sum(ss);
   const i64 mean = (C & (C - 1)) == 0 ? rhad_pow2(ss, (int)ilog2(C)) : rhad(ss, (i64)C);
-  const Recip R = make_recip(imax(isqrt_wave(mean), 1));
+  const i64 rms = imax(isqrt_wave(mean), 1);
+  if (rms > ((i64)1 << 16)) {
+    // the shift leaves |xp| <= 2^26, so 2 |xp| 2^20 + rms < 2^51 and the
+    // quotient is below 2^31: rhad_est, and to_i32 keeps it
+    const DivEst D = make_divest(rms, 1048576.0);
 #pragma unroll
-  for (int j = 0; j < VPT; ++j) v[j] = to_i32(rhad_r(shl(v[j], 20), R));
+    for (int j = 0; j < VPT; ++j) v[j] = rhad_est_signed(v[j], D);
+  } else {
+    const Recip R = make_recip(rms);
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) v[j] = to_i32(rhad_r(shl(v[j], 20), R));
+  }
 }
 
 // dyadic.py:93-105. The quotients rhad(127 x, a) with |x| <= a come from the
@@ -446,11 +455,31 @@ __device__ __forceinline__ void merge_rowcol_row(const MergeArgs& a, int r, Bloc
 #pragma unroll
   for (int j = 0; j < VPT; ++j) v[j] = rshift_round(v[j], sh);
   const i64 a2 = imax(row_absmax(v, red), 1);
-  const Recip R = make_recip(a2);
+  if (a2 < ((i64)1 << 46)) {
+    // |v| <= a2 < 2^46 (the pre-shift leaves at most 46 bits): 127 |v| does
+    // not wrap and 127 |v| + a2 < 2^53; the plain estimate is exact below
+    // 2^43, the corrected one above
+    const DivEst D = make_divest(a2, 127.0);
+    if (a2 < ((i64)1 << 43)) {
 #pragma unroll
-  for (int j = 0; j < VPT; ++j) {
-    const int c = threadIdx.x + j * (int)blockDim.x;
-    if (c < C) a.a8[off + c] = (int8_t)clamp_i8(rhad_r(wmul(v[j], 127), R));
+      for (int j = 0; j < VPT; ++j) {
+        const int c = threadIdx.x + j * (int)blockDim.x;
+        if (c < C) a.a8[off + c] = (int8_t)rhad_est_signed(v[j], D);
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < VPT; ++j) {
+        const int c = threadIdx.x + j * (int)blockDim.x;
+        if (c < C) a.a8[off + c] = (int8_t)rhad_est_corr_signed(v[j], 127, a2, D);
+      }
+    }
+  } else {
+    const Recip R = make_recip(a2);
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) {
+      const int c = threadIdx.x + j * (int)blockDim.x;
+      if (c < C) a.a8[off + c] = (int8_t)clamp_i8(rhad_r(wmul(v[j], 127), R));
+    }
   }
   if (threadIdx.x == 0) {
     i64 mo, e;

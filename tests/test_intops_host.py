@@ -384,3 +384,72 @@ def test_swiglu_elem_est_matches_oracle(lib):
     got = _call2_3(lib, "di_host_swiglu_est", g, u, tpos)
     want, _, _ = oops.di_swiglu(g, gm, gk, u, np.ones_like(u), np.zeros_like(u))
     assert g.size > 150000 and np.array_equal(got, want)
+
+
+def _est_op(lib, op, a, d, s):
+    a, d, s = (np.ascontiguousarray(x, I64) for x in (a, d, s))
+    out = np.empty_like(a)
+    lib.di_host_rhad_est_op(ctypes.c_int(op), _p(a), _p(d), _p(s), ctypes.c_int64(a.size), _p(out))
+    return out
+
+
+def test_rhad_est_signed_i8_and_corrected(lib):
+    """The signed, int8-clamped and remainder-corrected fp64-estimate
+    divisions of the row kernels against exact rhad (Python integers) at
+    their stated bounds: quantisation (s = 127, |a| <= d < 2^43), RMSNorm
+    (s = 2^20, |a| <= 2^26), static requant (s = 1, |a|, d < 2^49, clamped),
+    merge (s = 127, |a| <= d < 2^46, corrected)."""
+    rnd = random.Random(23)
+
+    def rh(a, d):
+        q = (abs(a) + d // 2) // d
+        return -q if a < 0 else q
+
+    def near_ties(d, s, amax, n):
+        out = []
+        for _ in range(n):
+            q = rnd.randrange(0, 128)
+            t = (q * d - d // 2) // s + rnd.choice([-1, 0, 1])
+            a = max(-amax, min(amax, t * rnd.choice([1, -1])))
+            out.append(a)
+        return out
+
+    # quantisation: |a| <= d < 2^43
+    A, D = [], []
+    for _ in range(4000):
+        d = rnd.randrange(1, 1 << rnd.randrange(1, 43))
+        for a in near_ties(d, 127, d, 3) + [rnd.randrange(-d, d + 1), d, -d, 0]:
+            A.append(a)
+            D.append(d)
+    got = _est_op(lib, 0, A, D, [127] * len(A))
+    assert got.tolist() == [rh(127 * a, d) for a, d in zip(A, D)]
+    # RMSNorm: |a| <= 2^26, d in (2^16, 2^26]
+    A, D = [], []
+    for _ in range(20000):
+        d = rnd.randrange((1 << 16) + 1, (1 << 26) + 1)
+        a = rnd.choice([rnd.randrange(-(1 << 26), (1 << 26) + 1), (1 << 26), -(1 << 26),
+                        ((rnd.randrange(0, 1 << 15) * d - d // 2) >> 20) + rnd.choice([-1, 0, 1])])
+        A.append(a)
+        D.append(d)
+    got = _est_op(lib, 0, A, D, [1 << 20] * len(A))
+    assert got.tolist() == [rh(a << 20, d) for a, d in zip(A, D)]
+    # static requant to int8, clamped: |a|, d < 2^49
+    A, D = [], []
+    for _ in range(20000):
+        d = rnd.randrange(1, 1 << rnd.randrange(1, 49))
+        q = rnd.choice([rnd.randrange(0, 300), rnd.randrange(0, 1 << 20)])
+        a = q * d - d // 2 + rnd.choice([-1, 0, 1, rnd.randrange(0, d)])
+        a = max(-(1 << 49) + 1, min((1 << 49) - 1, a * rnd.choice([1, -1])))
+        A.append(a)
+        D.append(d)
+    got = _est_op(lib, 1, A, D, [1] * len(A))
+    assert got.tolist() == [max(-128, min(127, rh(a, d))) for a, d in zip(A, D)]
+    # merge: |a| <= d < 2^46 with the correction step
+    A, D = [], []
+    for _ in range(6000):
+        d = rnd.randrange(1 << 40, 1 << 46)
+        for a in near_ties(d, 127, d, 3) + [rnd.randrange(-d, d + 1), d, -d]:
+            A.append(a)
+            D.append(d)
+    got = _est_op(lib, 2, A, D, [127] * len(A))
+    assert got.tolist() == [rh(127 * a, d) for a, d in zip(A, D)]
