@@ -532,9 +532,12 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, int kvh, int b,
     qa0 = *(const v4i*)(qsrc + l16 * 128 + grp * 16);
     qa1 = *(const v4i*)(qsrc + l16 * 128 + 64 + grp * 16);
   }
-  ExpR E[G];
+  // per head: the fp64-estimate DI-Exp (intops.h dexp_est) when tpos < 2^23
+  // (every score difference is below 2^22: |q8 . k8| <= 2^21), else the
+  // integer form
+  i64 tph[G];
 #pragma unroll
-  for (int hh = 0; hh < G; ++hh) E[hh] = make_exp(tsrc[hh]);
+  for (int hh = 0; hh < G; ++hh) tph[hh] = tsrc[hh];
 
   // ---- pass 1: scores on MFMA; masked slots marked; per-head row max.
   // Lane (grp, l16) holds C[4 grp + r][slot l16] in element r.
@@ -586,9 +589,18 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, int kvh, int b,
 #pragma unroll
   for (int hh = 0; hh < G; ++hh) {
     i64 acc = 0;
-    for (int s = tid; s < S; s += 256) {
-      const int32_t x = sc[hh * Spad + s];
-      if (x != SCORE_MASKED) acc = wadd(acc, di_exp_neg((u64)wsub(hmax[hh], (i64)x), E[hh]));
+    if (tph[hh] < ((i64)1 << 23)) {
+      const ExpEst Ee = make_expest(tph[hh]);
+      for (int s = tid; s < S; s += 256) {
+        const int32_t x = sc[hh * Spad + s];
+        if (x != SCORE_MASKED) acc += dexp_est((uint32_t)(hmax[hh] - x), Ee);
+      }
+    } else {
+      const ExpR E = make_exp(tph[hh]);
+      for (int s = tid; s < S; s += 256) {
+        const int32_t x = sc[hh * Spad + s];
+        if (x != SCORE_MASKED) acc = wadd(acc, di_exp_neg((u64)wsub(hmax[hh], (i64)x), E));
+      }
     }
     den[hh] = imax(red.sum(acc), 1);
   }
@@ -598,18 +610,36 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, int kvh, int b,
   const int nchunk = (S + 15) / 16;
 #pragma unroll
   for (int hh = 0; hh < G; ++hh) {
-    const Recip Rd = make_recip(den[hh]);
-    for (int s = tid; s < nchunk * 16; s += 256) {
-      i64 p = 0;
-      if (s < S) {
-        const int32_t x = sc[hh * Spad + s];
-        if (x != SCORE_MASKED) {
-          const i64 ex = di_exp_neg((u64)wsub(hmax[hh], (i64)x), E[hh]);
-          p = to_i32(rhad_r(shl(ex, 14), Rd));
-        }
-      }
+    auto put = [&](int s, i64 p) {
       const int hi = (int)(p >> 7), lo = (int)(p & 127);
       sc[hh * Spad + s] = (int32_t)((uint32_t)(uint8_t)(int8_t)(hi - 64) | ((uint32_t)lo << 8));
+    };
+    if (tph[hh] < ((i64)1 << 23) && den[hh] < ((i64)1 << 34)) {
+      // exps below 2^23, den < 2^34: p = rhad(ex 2^14, den) from rhad_est
+      const ExpEst Ee = make_expest(tph[hh]);
+      const DivEst D = make_divest(den[hh], 16384.0);
+      for (int s = tid; s < nchunk * 16; s += 256) {
+        i64 p = 0;
+        if (s < S) {
+          const int32_t x = sc[hh * Spad + s];
+          if (x != SCORE_MASKED) p = rhad_est((double)dexp_est((uint32_t)(hmax[hh] - x), Ee), D);
+        }
+        put(s, p);
+      }
+    } else {
+      const ExpR E = make_exp(tph[hh]);
+      const Recip Rd = make_recip(den[hh]);
+      for (int s = tid; s < nchunk * 16; s += 256) {
+        i64 p = 0;
+        if (s < S) {
+          const int32_t x = sc[hh * Spad + s];
+          if (x != SCORE_MASKED) {
+            const i64 ex = di_exp_neg((u64)wsub(hmax[hh], (i64)x), E);
+            p = to_i32(rhad_r(shl(ex, 14), Rd));
+          }
+        }
+        put(s, p);
+      }
     }
   }
   __syncthreads();

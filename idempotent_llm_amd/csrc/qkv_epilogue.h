@@ -223,7 +223,7 @@ __device__ __forceinline__ void qkv_head(const QKVArgs& a, int r, int slotw, int
     // score scale: norm_scale(qm * ks_m[h//g], qk + ks_k[h//g])   (model.py:351-353)
     i64 sm, sk;
     norm_scale(wmul(qm, ksm), wadd(qk, ksk), &sm, &sk);
-    *tpos_out = di_exp_tpos(sm, sk);
+    *tpos_out = di_exp_tpos_fast(sm, sk);
     if (a.dbg) {
       a.dbg[qrow * 4 + 0] = qm;
       a.dbg[qrow * 4 + 1] = qk;

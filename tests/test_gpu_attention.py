@@ -197,3 +197,40 @@ def test_prefill_attention_vs_oracle(name):
         assert tpos[0, 0].max() > (1 << 32)  # den = sum of exps >= tpos * visible slots
     if name == "big_tpos_long_rows":
         assert tpos.max() < (1 << 23) and tpos.min() * 4033 > (1 << 34)
+
+
+# ------------------------------------------------------------- decode kernel
+
+DECODE_CASES = {
+    # B, n_q, n_kv, S, cap, seed, sk range, extras  (one query at slot S - 1)
+    "typical": (3, 4, 2, 300, 320, 11, 29, 34, {}),
+    "wide_tpos": (2, 4, 2, 200, 208, 12, 0, 62, dict(dead_prefix=200)),
+    "big_tpos_long_rows": (1, 2, 1, 4096, 4096, 13, 39, 39,
+                           dict(zero_heads=(0,), sm_lo=60000, p_valid=1.0)),
+    "single_slot": (2, 2, 2, 1, 16, 14, 25, 45, {}),
+}
+
+
+@pytest.mark.parametrize("name", list(DECODE_CASES))
+def test_decode_attention_vs_oracle(name):
+    """detllm_attn_decode (ops/fused_attn.py:47-142 semantics) against the
+    oracle composition for one query per row at slot S - 1 (every valid slot
+    below S visible): ragged masks, rows with no visible slot, tpos from 1 to
+    about 2^46, flat rows whose denominators pass 2^34."""
+    from idempotent_llm_amd._lib import call
+    B, n_q, n_kv, S, cap, seed, lo, hi, extra = DECODE_CASES[name]
+    print(f"[decode attention {name}: B={B} n_q={n_q} n_kv={n_kv} S={S}]", flush=True)
+    q8, kc, vc, valid, sm, sk, tpos = _prefill_case(B, n_q, n_kv, 1, S - 1, cap, seed, lo, hi,
+                                                    **extra)
+    want = _prefill_oracle(q8, kc, vc, valid, sm, sk, S - 1)[:, 0]
+    d = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
+    G = n_q // n_kv
+    Spad = (S + 15) // 16 * 16
+    scratch = (torch.empty(B, n_q, Spad, dtype=torch.int32, device="cuda")
+               if G * Spad * 4 > 48 * 1024 else None)
+    out = torch.full((B, n_q * 128), -7, dtype=I64, device="cuda")
+    call("detllm_attn_decode", d(q8[:, :, 0]), d(tpos[:, :, 0, 0]), d(kc), d(vc),
+         d(valid.astype(np.uint8)), cap, B, S, n_q, n_kv, cap, None, scratch, out)
+    got = out.cpu().numpy()
+    bad = np.argwhere(got != want)
+    assert bad.size == 0, f"{len(bad)} mismatches, first at {bad[0].tolist()}"
