@@ -256,7 +256,18 @@ def c1_c2_bench():
 
     us1 = _graph_time_us(mlp, 10, 1)
     ops1 = 2.0 * T * H * I * 3
-    # c2: one prefill attention launch over a 2048-slot cache
+    return ({"us": round(us1, 2), "gemm_tops": round(ops1 / (us1 * 1e-6) / 1e12, 1),
+             "tokens_per_s": round(T / (us1 * 1e-6), 1)}, c2_bench())
+
+
+def c2_bench():
+    """Config c2: one GQA attention prefill launch (2048 queries, 16 q heads,
+    8 kv heads, over a 2048-slot cache), device time with HIP events over
+    graph replays."""
+    import torch
+    from idempotent_llm_amd._lib import call
+    T = 2048
+    dev = "cuda"
     q8 = torch.randint(-127, 128, (1, 16, T, 128), dtype=torch.int8, device=dev)
     tpos = torch.full((1, 16, T), 1 << 12, dtype=torch.int64, device=dev)
     kc = torch.randint(-127, 128, (1, 8, T, 128), dtype=torch.int8, device=dev)
@@ -266,10 +277,8 @@ def c1_c2_bench():
     us2 = _graph_time_us(lambda: call("detllm_attn_prefill", q8, tpos, kc, vc, valid, T, 1, T,
                                       0, 16, 8, T, out), 10, 1)
     ops2 = 2.0 * 2 * 16 * (T * (T + 1) // 2) * 128
-    return ({"us": round(us1, 2), "gemm_tops": round(ops1 / (us1 * 1e-6) / 1e12, 1),
-             "tokens_per_s": round(T / (us1 * 1e-6), 1)},
-            {"us": round(us2, 2), "tops": round(ops2 / (us2 * 1e-6) / 1e12, 1),
-             "algorithmic_ops": int(ops2)})
+    return {"us": round(us2, 2), "tops": round(ops2 / (us2 * 1e-6) / 1e12, 1),
+            "algorithmic_ops": int(ops2)}
 
 
 def gemm_tops(T: int = PREFILL_LEN):
@@ -355,6 +364,10 @@ def main():
                          "(for rocprofv3 --pmc counter passes), then exit")
     ap.add_argument("--gemm-probe", action="store_true",
                     help="only time the prefill-shape int8 GEMMs (no model), print them, exit")
+    ap.add_argument("--attn-probe", action="store_true",
+                    help="only time the c2 attention prefill (no model), print it, exit")
+    ap.add_argument("--prefill-probe", action="store_true",
+                    help="only time 2048-token prefills of the model, print them, exit")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}): the integer "
@@ -368,6 +381,9 @@ def main():
     if args.gemm_probe:
         print(json.dumps(gemm_tops()), flush=True)
         return
+    if args.attn_probe:
+        print(json.dumps({"c2_attention_prefill_2048": c2_bench()}), flush=True)
+        return
 
     with tempfile.TemporaryDirectory(prefix="detllm_bench_") as d:
         t0 = time.perf_counter()
@@ -375,6 +391,10 @@ def main():
         log(f"artifact generated in {time.perf_counter() - t0:.1f}s")
         model = IntQwen3(d, backend="rocm")
         log("model loaded")
+        if args.prefill_probe:
+            tps = [round(prefill_bench(model, PREFILL_LEN), 1) for _ in range(3)]
+            print(json.dumps({"prefill_tok_s_2048": tps}), flush=True)
+            return
         B = args.batch
         if args.kernel_probe:
             kernel_probe(model, B)
