@@ -346,8 +346,8 @@ __device__ __forceinline__ void residual_normq_row(const ResNormArgs& a, int r, 
   quant_row(h, 1, kq, C, red, a.x8 + off, a.xm + r, a.xk + r);
 }
 
-template <int VPT>
-__global__ __launch_bounds__(RT_WIDE) void k_residual_normq(ResNormArgs a) {
+template <int VPT, int NT = RT_WIDE>
+__global__ __launch_bounds__(NT) void k_residual_normq(ResNormArgs a) {
   __shared__ i64 red_buf[32];
   BlockRed red{red_buf, 0};
   residual_normq_row<VPT>(a, blockIdx.x, red);
@@ -402,8 +402,8 @@ __device__ __forceinline__ void swiglu_quant_row(const SwigluArgs& a, int r, Blo
   quant_row(gu[0], ym, yk, I, red, a.y8 + (i64)r * I, a.ym + r, a.yk + r);
 }
 
-template <int VPT>
-__global__ __launch_bounds__(RT_WIDE) void k_swiglu_quant(SwigluArgs a) {
+template <int VPT, int NT = RT_WIDE>
+__global__ __launch_bounds__(NT) void k_swiglu_quant(SwigluArgs a) {
   __shared__ i64 red_buf[32];
   BlockRed red{red_buf, 0};
   swiglu_quant_row<VPT>(a, blockIdx.x, red);
@@ -489,8 +489,8 @@ __device__ __forceinline__ void merge_rowcol_row(const MergeArgs& a, int r, Bloc
   }
 }
 
-template <int VPT>
-__global__ __launch_bounds__(RT_WIDE) void k_merge_rowcol(MergeArgs a) {
+template <int VPT, int NT = RT_WIDE>
+__global__ __launch_bounds__(NT) void k_merge_rowcol(MergeArgs a) {
   __shared__ i64 red_buf[32];
   BlockRed red{red_buf, 0};
   merge_rowcol_row<VPT>(a, blockIdx.x, red);
@@ -830,6 +830,25 @@ inline int grid_for(i64 n) {
     }                                                                                        \
   } while (0)
 
+// Row kernels over many rows (prefill, R > 64) run 256-thread blocks with up
+// to 16 columns per thread: the per-row work (reductions, scale fits,
+// divisors) is then shared by 4 waves instead of up to 16, and more rows fit
+// on a CU at once. Decode-sized calls keep the wide blocks, which shorten
+// the per-row serial chain.
+#define DI_ROWS_DISPATCH(R, C, KERNEL, GRID, STREAM, ...)                                       \
+  do {                                                                                          \
+    if ((R) > 64) {                                                                             \
+      const int v_ = ((C) + 255) / 256;                                                         \
+      if (v_ <= 4) hipLaunchKernelGGL((KERNEL<4, 256>), GRID, dim3(256), 0, STREAM, __VA_ARGS__);   \
+      else if (v_ <= 8) hipLaunchKernelGGL((KERNEL<8, 256>), GRID, dim3(256), 0, STREAM, __VA_ARGS__); \
+      else if (v_ <= 12) hipLaunchKernelGGL((KERNEL<12, 256>), GRID, dim3(256), 0, STREAM, __VA_ARGS__); \
+      else if (v_ <= 16) hipLaunchKernelGGL((KERNEL<16, 256>), GRID, dim3(256), 0, STREAM, __VA_ARGS__); \
+      else return DI_ENOSYS;                                                                    \
+    } else {                                                                                    \
+      DI_WIDE_DISPATCH(C, KERNEL, GRID, STREAM, __VA_ARGS__);                                   \
+    }                                                                                           \
+  } while (0)
+
 extern "C" {
 
 // ---------------------------------------------------------------- model path
@@ -843,7 +862,7 @@ int detllm_embed_normq(const int64_t* ids, int R, int C, int64_t vocab, const in
   ResNormArgs a{};
   a.C = C; a.mode = 0; a.vocab = vocab; a.ids = ids; a.e8 = e8; a.em = em; a.ek = ek;
   a.h = h; a.k_res = k_res; a.sm_m = sm_m; a.sm_k = sm_k; a.x8 = x8; a.xm = xm; a.xk = xk;
-  DI_WIDE_DISPATCH(C, k_residual_normq, dim3(R), s, a);
+  DI_ROWS_DISPATCH(R, C, k_residual_normq, dim3(R), s, a);
   DI_LAUNCH_CHECK();
   return DI_OK;
 }
@@ -858,7 +877,7 @@ int detllm_residual_normq(const int32_t* P, int nsplit, int64_t split_stride, in
   a.C = C; a.mode = 1; a.P = P; a.nsplit = nsplit; a.split_stride = split_stride;
   a.row_m = row_m; a.row_k = row_k; a.col_m = col_m; a.col_k = col_k; a.tb = tb;
   a.h = h; a.k_res = k_res; a.sm_m = sm_m; a.sm_k = sm_k; a.x8 = x8; a.xm = xm; a.xk = xk;
-  DI_WIDE_DISPATCH(C, k_residual_normq, dim3(R), s, a);
+  DI_ROWS_DISPATCH(R, C, k_residual_normq, dim3(R), s, a);
   DI_LAUNCH_CHECK();
   return DI_OK;
 }
@@ -870,7 +889,7 @@ int detllm_norm_quant(const int32_t* h, int R, int C, const int64_t* sm_m, int64
   ResNormArgs a{};
   a.C = C; a.mode = 2; a.h = const_cast<int32_t*>(h); a.sm_m = sm_m; a.sm_k = sm_k;
   a.x8 = x8; a.xm = xm; a.xk = xk;
-  DI_WIDE_DISPATCH(C, k_residual_normq, dim3(R), s, a);
+  DI_ROWS_DISPATCH(R, C, k_residual_normq, dim3(R), s, a);
   DI_LAUNCH_CHECK();
   return DI_OK;
 }
@@ -886,7 +905,7 @@ int detllm_swiglu_quant(const int32_t* P, int nsplit, int64_t split_stride, int 
   a.I = I; a.P = P; a.nsplit = nsplit; a.split_stride = split_stride; a.xm = xm; a.xk = xk;
   a.gate_m = gate_m; a.gate_k = gate_k; a.up_m = up_m; a.up_k = up_k; a.ds_m = ds_m;
   a.ds_k = ds_k; a.y8 = y8; a.ym = ym; a.yk = yk;
-  DI_WIDE_DISPATCH(I, k_swiglu_quant, dim3(R), s, a);
+  DI_ROWS_DISPATCH(R, I, k_swiglu_quant, dim3(R), s, a);
   DI_LAUNCH_CHECK();
   return DI_OK;
 }
@@ -899,7 +918,7 @@ int detllm_merge_rowcol(const int64_t* attn, int nsplit, int64_t split_stride, i
   MergeArgs a{};
   a.C = C; a.attn = attn; a.nsplit = nsplit; a.split_stride = split_stride; a.os_m = os_m;
   a.os_k = os_k; a.col_m = col_m; a.col_k = col_k; a.a8 = a8; a.am = am; a.ak = ak;
-  DI_WIDE_DISPATCH(C, k_merge_rowcol, dim3(R), s, a);
+  DI_ROWS_DISPATCH(R, C, k_merge_rowcol, dim3(R), s, a);
   DI_LAUNCH_CHECK();
   return DI_OK;
 }
