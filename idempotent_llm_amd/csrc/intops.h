@@ -503,6 +503,19 @@ DI_HD uint32_t dexp_est_sp(int32_t sp, const ExpEst& E, double kx) {
   return m >> (q1 < 31u ? q1 : 31u);
 }
 
+// floor(sqrt(n)) for 0 <= n < 2^62 (int_prims.py:31-44 isqrt, negative n
+// give 0): fp64 sqrt of fl(n) is within 2^-21 of sqrt(n) (relative 2^-53
+// on n, one rounding of the square root), so its truncation is the integer
+// root or one off either way; one exact integer step each way settles it
+// ((r + 1)^2 <= 2^62 stays in range).
+DI_HD i64 isqrt_est(i64 n) {
+  if (n <= 0) return 0;
+  i64 r = (i64)sqrt((double)n);
+  if (r * r > n) r -= 1;
+  if ((r + 1) * (r + 1) <= n) r += 1;
+  return r;
+}
+
 // ops/di_swiglu.py:39-58 on one element for |g|, |u| <= 2^14 (gate and up
 // after requant_i32_common(14)) and tpos < 2^23: |g| < 2^22 for dexp_est,
 // E <= tpos and den = tpos + E < 2^24 for sigmoid_est, g * sig (sig <= 128)

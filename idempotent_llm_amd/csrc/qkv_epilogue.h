@@ -234,3 +234,235 @@ __device__ __forceinline__ void qkv_head(const QKVArgs& a, int r, int slotw, int
 }
 
 }  // namespace di
+
+namespace di {
+
+// ---- prefill layout: one wave per (head slot, 4 consecutive token rows) ----
+//
+// Lane (g, j) = (lane / 16, lane % 16) handles token row r0 + g and the
+// channels c_i = 4j + i and c_{i+4} = 64 + 4j + i (i < 4), so RoPE partners
+// (c, c + 64) share a lane and every reduction over a row's 128 channels is a
+// 16-lane DPP row reduction. Compared with the one-wave-per-(row, head)
+// layout above, the per-row scalar chains (scale fits, divisors) run for four
+// rows at once and each head's scale vectors are loaded once per four rows.
+// Same arithmetic and the same integers as qkv_head.
+
+__device__ __forceinline__ i64 row16_max64(i64 v) {
+  v = imax(v, dpp64<0xB1, 0xF>(v, v));
+  v = imax(v, dpp64<0x4E, 0xF>(v, v));
+  v = imax(v, dpp64<0x141, 0xF>(v, v));
+  return imax(v, dpp64<0x140, 0xF>(v, v));
+}
+__device__ __forceinline__ i64 row16_sum64(i64 v) {
+  v = wadd(v, dpp64<0xB1, 0xF>(v, 0));
+  v = wadd(v, dpp64<0x4E, 0xF>(v, 0));
+  v = wadd(v, dpp64<0x141, 0xF>(v, 0));
+  return wadd(v, dpp64<0x140, 0xF>(v, 0));
+}
+__device__ __forceinline__ uint32_t row16_max_u32(uint32_t v) {
+  v = ::max(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0xB1, 0xF, 0xF, false));
+  v = ::max(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x4E, 0xF, 0xF, false));
+  v = ::max(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x141, 0xF, 0xF, false));
+  return ::max(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x140, 0xF, 0xF, false));
+}
+
+// The whole wave must be active. Rows r >= R compute on row R - 1 and store
+// nothing.
+__device__ __forceinline__ void qkv_rows4(const QKVArgs& a, int R, int r0, int slotw) {
+  const int lane = threadIdx.x & 63, g = lane >> 4, j = lane & 15;
+  const int n_heads = a.n_q + 2 * a.n_kv;
+  const bool rok = r0 + g < R;
+  const int r = rok ? r0 + g : R - 1;
+  const int b = r / a.T, t = r - b * a.T;
+  const i64 off = (i64)r * (n_heads * 128) + (i64)slotw * 128;
+  const int group = a.n_q / a.n_kv;
+  const bool is_q = slotw < a.n_q, is_v = slotw >= a.n_q + a.n_kv;
+  const int h = is_q ? slotw : (is_v ? slotw - a.n_q - a.n_kv : slotw - a.n_q);
+  const int kvh = is_q ? h / group : h;
+  int c[8];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    c[i] = 4 * j + i;
+    c[i + 4] = 64 + 4 * j + i;
+  }
+
+  // ---- loads
+  const i64 pos_raw = a.positions[r];
+  const i64 xk = a.xk[r], xm = a.xm[r];
+  const i64 base = a.slot_base_dev ? a.slot_base_dev[0] : a.slot_base;
+  const int64_t* wmp = (is_q ? a.q_m : (is_v ? a.v_m : a.k_m)) + (i64)h * 128;
+  i64 wm[8], p[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) wm[i] = wmp[c[i]];
+  {
+    uint32_t s[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    for (int k = 0; k < a.nsplit; ++k) {
+      const int32_t* pk = a.P + (i64)k * a.split_stride + off;
+      const int4 lo = *(const int4*)(pk + 4 * j);
+      const int4 hi = *(const int4*)(pk + 64 + 4 * j);
+      s[0] += (uint32_t)lo.x; s[1] += (uint32_t)lo.y; s[2] += (uint32_t)lo.z; s[3] += (uint32_t)lo.w;
+      s[4] += (uint32_t)hi.x; s[5] += (uint32_t)hi.y; s[6] += (uint32_t)hi.z; s[7] += (uint32_t)hi.w;
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) p[i] = (int32_t)s[i];
+  }
+  const i64 slot = base + t;
+  const bool sok = rok && slot >= 0 && slot < a.cap;
+
+  if (is_v) {
+    // V head: requant_i8_static(Pv, xm, xk, v_m, v_k, vq_m[h], vq_k[h])
+    const i64 vqm = a.vq_m[kvh], vqk = a.vq_k[kvh];
+    const i64 shift = wsub(wadd(xk, a.v_k), vqk);
+    const i64 up = imax(wneg(shift), 0), down = imax(shift, 0);
+    i64 den = shl(vqm, down);
+    if (den <= 0) den = 1;
+    i64 n[8];
+    bool fast = den < ((i64)1 << 49);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      n[i] = shl(wmul(wmul(p[i], wm[i]), xm), up);
+      fast = fast && n[i] > -((i64)1 << 49) && n[i] < ((i64)1 << 49);
+    }
+    int8_t o[8];
+    if (fast) {
+      const DivEst D = make_divest(den, 1.0);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) o[i] = (int8_t)rhad_est_i8(n[i], D);
+    } else {
+      const Recip Rr = make_recip(den);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) o[i] = (int8_t)clamp_i8(rhad_r(n[i], Rr));
+    }
+    if (sok) {
+      int8_t* vrow = a.vcache + ((i64)b * a.n_kv + h) * 128 * a.cap + slot;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) vrow[(i64)c[i] * a.cap] = o[i];
+    }
+    return;
+  }
+  const int64_t* gam = is_q ? a.q_norm_m : a.k_norm_m;
+  i64 gm[8], cs[8], sn[8];
+  const i64 pos = pos_raw < 0 ? 0 : (pos_raw >= a.max_pos ? a.max_pos - 1 : pos_raw);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    gm[i] = gam[c[i]];
+    cs[i] = a.cos_t[pos * 128 + c[i]];
+    sn[i] = a.sin_t[pos * 128 + c[i]];
+  }
+  // requant_i32_common(tb = 16) per (token, head)   (model.py:207-211)
+  i64 y[8];
+  uint32_t L = 0;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    y[i] = wmul(p[i], wm[i]);
+    L = ::max(L, bitlen_abs(y[i]));
+  }
+  {
+    const i64 sh = imax(ilog2_from_bitlen(row16_max_u32(L)) - 15, 0);
+    L = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      y[i] = to_i32(rshift_round(y[i], sh));
+      L = ::max(L, bitlen_abs(y[i]));
+    }
+  }
+  // di_rmsnorm over the 128 channels (model.py:212)
+  {
+    const i64 sh = 25 - ilog2_from_bitlen(row16_max_u32(L));
+    const i64 up = imax(sh, 0), down = imax(-sh, 0);
+    i64 ss = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      y[i] = shl(rshift_round(y[i], down), up);
+      ss = wadd(ss, wmul(y[i], y[i]));
+    }
+    const i64 rms = imax(isqrt_est(rhad_pow2(row16_sum64(ss), 7)), 1);
+    if (rms > ((i64)1 << 16)) {  // |y| <= 2^26 after the shift: rhad_est
+      const DivEst D = make_divest(rms, 1048576.0);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) y[i] = rhad_est_signed(y[i], D);
+    } else {
+      const Recip Rr = make_recip(rms);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) y[i] = to_i32(rhad_r(shl(y[i], 20), Rr));
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 8; ++i) y[i] = wmul(y[i], gm[i]);
+  // apply_int_rope at this token's position   (model.py:213-215; rope.py:38-55)
+  i64 rv[8];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    rv[i] = rshift_round(wadd(wmul(y[i], cs[i]), wmul(wneg(y[i + 4]), sn[i])), 14);
+    rv[i + 4] = rshift_round(wadd(wmul(y[i + 4], cs[i + 4]), wmul(y[i], sn[i + 4])), 14);
+  }
+  if (!is_q) {
+    // K: requant_i8_static(kk, 1, k_rowk, 1, 0, kq_m, kq_k)   (model.py:326-329)
+    const i64 rowk = 20 + a.k_norm_k;
+    uint32_t w[2] = {0, 0};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const i64 km = a.kq_m[kvh * 128 + c[i]], kk = a.kq_k[kvh * 128 + c[i]];
+      const i64 shift = wsub(rowk, kk);
+      const i64 up = imax(wneg(shift), 0), down = imax(shift, 0);
+      i64 den = shl(km, down);
+      if (den <= 0) den = 1;
+      const i64 n = shl(rv[i], up);
+      const i64 lim = (i64)1 << 49;  // 2 |n| + den < 2^51 for rhad_est_i8
+      const int o = (den < lim && n > -lim && n < lim) ? rhad_est_i8(n, make_divest(den, 1.0))
+                                                       : (int)clamp_i8(rhad(n, den));
+      w[i >> 2] |= (uint32_t)(uint8_t)(int8_t)o << (8 * (i & 3));
+    }
+    if (sok) {
+      int8_t* krow = a.kcache + (((i64)b * a.n_kv + h) * a.cap + slot) * 128;
+      *(uint32_t*)(krow + 4 * j) = w[0];
+      *(uint32_t*)(krow + 64 + 4 * j) = w[1];
+    }
+    return;
+  }
+  // Q: QK smoothing (model.py:317-320) then quant_i8_pertoken (model.py:322-323)
+  i64 q[8], amx = 0;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    q[i] = wmul(rv[i], a.qs_m[kvh * 128 + c[i]]);
+    amx = imax(amx, wabs(q[i]));
+  }
+  const i64 qkk = 20 + a.q_norm_k + a.qs_k;
+  i64 m, k;
+  norm_scale(1, qkk, &m, &k);
+  const i64 am = imax(row16_max64(amx), 1);
+  const i64 qrow = ((i64)b * a.n_q + h) * a.T + t;
+  uint32_t w[2] = {0, 0};
+  if (am < ((i64)1 << 43)) {  // as in quant_row: no 127 q wraps, 255 am < 2^51
+    const DivEst D = make_divest(am, 127.0);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) w[i >> 2] |= (uint32_t)(uint8_t)(int8_t)rhad_est_signed(q[i], D) << (8 * (i & 3));
+  } else {
+    const Recip Rr = make_recip(am);
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      w[i >> 2] |= (uint32_t)(uint8_t)(int8_t)clamp_i8(rhad_r(wmul(q[i], 127), Rr)) << (8 * (i & 3));
+  }
+  if (rok) {
+    *(uint32_t*)(a.q8 + qrow * 128 + 4 * j) = w[0];
+    *(uint32_t*)(a.q8 + qrow * 128 + 64 + 4 * j) = w[1];
+  }
+  if (j == 0 && rok) {
+    const i64 ksm = a.ks_m[kvh], ksk = a.ks_k[kvh];
+    i64 qm, e;
+    fit_dyadic_ratio_127(wmul(am, m), &qm, &e);
+    const i64 qk = wadd(k, e);
+    // score scale: norm_scale(qm * ks_m[h//g], qk + ks_k[h//g])   (model.py:351-353)
+    i64 sm, sk;
+    norm_scale(wmul(qm, ksm), wadd(qk, ksk), &sm, &sk);
+    a.tpos[qrow] = di_exp_tpos_fast(sm, sk);
+    if (a.dbg) {
+      a.dbg[qrow * 4 + 0] = qm;
+      a.dbg[qrow * 4 + 1] = qk;
+      a.dbg[qrow * 4 + 2] = sm;
+      a.dbg[qrow * 4 + 3] = sk;
+    }
+  }
+}
+
+}  // namespace di

@@ -505,6 +505,16 @@ __global__ __launch_bounds__(RT) void k_qkv_epilogue(QKVArgs a) {
   qkv_head(a, r, slotw, a.q8 + qrow * 128, a.tpos + qrow);
 }
 
+// Many token rows (prefill): one wave per (head slot, 4 rows), head-major so
+// a block's waves share a head's scale vectors.
+__global__ __launch_bounds__(RT) void k_qkv_epilogue_rows(QKVArgs a, int R, int ngroups) {
+  const int heads = a.n_q + 2 * a.n_kv;
+  const int wg = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (wg >= heads * ngroups) return;  // whole waves only
+  const int slotw = wg / ngroups, grp = wg - slotw * ngroups;
+  qkv_rows4(a, R, grp * 4, slotw);
+}
+
 // =====================================================================
 // Op-level row kernels (one reference function each)
 // =====================================================================
@@ -949,7 +959,17 @@ int detllm_qkv_epilogue(const int32_t* P, int nsplit, int64_t split_stride, int 
   a.kcache = kcache; a.vcache = vcache; a.cap = cap; a.slot_base_dev = slot_base_dev;
   a.slot_base = slot_base;
   const int heads = n_q + 2 * n_kv;
-  hipLaunchKernelGGL(k_qkv_epilogue, dim3(B * T, (heads + 3) / 4), dim3(RT), 0, s, a);
+  const int R = B * T;
+  // the rows layout reads P 16 bytes at a time
+  if (R > 64 && (nsplit == 1 || split_stride % 4 == 0) && ((uintptr_t)P & 15) == 0) {
+    const int ngroups = (R + 3) / 4;
+    const i64 waves = (i64)ngroups * heads;
+    if ((waves + 3) / 4 > 0x7fffffff) return DI_ERANGE;
+    hipLaunchKernelGGL(k_qkv_epilogue_rows, dim3((unsigned)((waves + 3) / 4)), dim3(RT), 0, s, a,
+                       R, ngroups);
+  } else {
+    hipLaunchKernelGGL(k_qkv_epilogue, dim3(R, (heads + 3) / 4), dim3(RT), 0, s, a);
+  }
   DI_LAUNCH_CHECK();
   return DI_OK;
 }

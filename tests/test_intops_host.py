@@ -453,3 +453,18 @@ def test_rhad_est_signed_i8_and_corrected(lib):
             D.append(d)
     got = _est_op(lib, 2, A, D, [127] * len(A))
     assert got.tolist() == [rh(127 * a, d) for a, d in zip(A, D)]
+
+
+def test_isqrt_est_matches_oracle(lib):
+    """isqrt_est (fp64 square root + one integer step each way) equals the
+    oracle's isqrt (int_prims.py bitwise method) below 2^62: random values at
+    every magnitude, perfect squares and their neighbours."""
+    rnd = np.random.default_rng(29)
+    r = rnd.integers(0, 1 << 31, 30000, dtype=I64)
+    sq = r * r
+    v = np.concatenate([sq, sq - 1, sq + 1, sq + 2 * r, sq + 2 * r + 1,
+                        (rnd.random(30000) * 2.0 ** rnd.integers(0, 62, 30000)).astype(I64),
+                        np.arange(-3, 5000, dtype=I64)])
+    v = v[(v < (1 << 62))]
+    got, _ = _scalar(lib, 8, v)
+    assert np.array_equal(got, oim.isqrt(v))
