@@ -414,25 +414,28 @@ int detllm_igemm_nt(const int8_t* A, const int8_t* B, int32_t* C, int M, int N, 
     // them; else 128x128 tiles (4 waves, 2 slices, 2 blocks per CU) while they
     // give at least two tiles per CU; else 128x64 tiles for more parallelism,
     // on 8 waves (4 x 2, one 32x32 block each) and a 4-slice ring
-    const i64 t256 = (i64)((M + 255) / 256) * ((N + 255) / 256) * batch;
-    const i64 t128 = (i64)((M + 127) / 128) * ((N + 127) / 128) * batch;
-    const int tm = (M + 127) / 128;
-    if (t256 >= 192) {
-      const int tm2 = (M + 255) / 256, tn2 = (N + 255) / 256;
-      if ((i64)tm2 * tn2 > 0x7fffffff) return DI_ERANGE;
-      hipLaunchKernelGGL((k_gemm_nt2<256, 256, 2, 4, 2, 1>), dim3(tm2 * tn2, 1, batch), dim3(512),
-                         0, s, A, B, C, M, N, K, (i64)sA, (i64)sB, (i64)sC, tm2, tn2);
-    } else if (t128 >= 512) {
-      const int tn = (N + 127) / 128;
-      if ((i64)tm * tn > 0x7fffffff) return DI_ERANGE;
-      hipLaunchKernelGGL((k_gemm_nt2<128, 128, 2, 2, 2, 2>), dim3(tm * tn, 1, batch), dim3(256), 0, s,
-                         A, B, C, M, N, K, (i64)sA, (i64)sB, (i64)sC, tm, tn);
-    } else {
-      const int tn = (N + 63) / 64;
-      if ((i64)tm * tn > 0x7fffffff) return DI_ERANGE;
-      hipLaunchKernelGGL((k_gemm_nt2<128, 64, 4, 4, 2, 1>), dim3(tm * tn, 1, batch), dim3(512), 0, s,
-                         A, B, C, M, N, K, (i64)sA, (i64)sB, (i64)sC, tm, tn);
-    }
+    // Tile shape: the largest whose tile count nearly fills the 256 CUs (one
+    // tile per CU at M = 2048: 256x192 for gate|up, 256x128 for q|k|v,
+    // 128x64 for o and down), with at most 1/16 of its columns padding.
+    auto tiles = [&](int bm, int bn) { return (i64)((M + bm - 1) / bm) * ((N + bn - 1) / bn) * batch; };
+    auto fits = [&](int bm, int bn) {
+      const i64 tn = (N + bn - 1) / bn;
+      return tiles(bm, bn) >= 224 && (tn * bn - N) * 16 <= N;
+    };
+#define DI_GEMM2(BM, BN, S, WGM, WGN, MINB)                                                      \
+  do {                                                                                          \
+    const int tm_ = (M + BM - 1) / BM, tn_ = (N + BN - 1) / BN;                                 \
+    if ((i64)tm_ * tn_ > 0x7fffffff) return DI_ERANGE;                                          \
+    hipLaunchKernelGGL((k_gemm_nt2<BM, BN, S, WGM, WGN, MINB>), dim3(tm_ * tn_, 1, batch),     \
+                       dim3(64 * WGM * WGN), 0, s, A, B, C, M, N, K, (i64)sA, (i64)sB, (i64)sC, \
+                       tm_, tn_);                                                               \
+  } while (0)
+    if (fits(256, 256)) DI_GEMM2(256, 256, 2, 4, 2, 1);
+    else if (fits(256, 192)) DI_GEMM2(256, 192, 2, 4, 2, 1);
+    else if (fits(256, 128)) DI_GEMM2(256, 128, 3, 4, 2, 1);
+    else if (tiles(128, 128) >= 512) DI_GEMM2(128, 128, 2, 2, 2, 2);
+    else DI_GEMM2(128, 64, 4, 4, 2, 1);
+#undef DI_GEMM2
     DI_LAUNCH_CHECK();
     return DI_OK;
   }
