@@ -414,14 +414,12 @@ int detllm_igemm_nt(const int8_t* A, const int8_t* B, int32_t* C, int M, int N, 
     // them; else 128x128 tiles (4 waves, 2 slices, 2 blocks per CU) while they
     // give at least two tiles per CU; else 128x64 tiles for more parallelism,
     // on 8 waves (4 x 2, one 32x32 block each) and a 4-slice ring
-    // Tile shape: the largest whose tile count nearly fills the 256 CUs (one
-    // tile per CU at M = 2048: 256x192 for gate|up, 256x128 for q|k|v,
-    // 128x64 for o and down), with at most 1/16 of its columns padding.
+    // Tile shape by tile count (a sweep of shapes over the four M = 2048
+    // products picked these): 256x256 only for large products (c4 prefill),
+    // 128x192 (two blocks per CU) where it divides N (gate|up), 128x128 (two
+    // per CU) at >= 448 tiles (q|k|v), else 128x64 with a 4-slice ring (o,
+    // down).
     auto tiles = [&](int bm, int bn) { return (i64)((M + bm - 1) / bm) * ((N + bn - 1) / bn) * batch; };
-    auto fits = [&](int bm, int bn) {
-      const i64 tn = (N + bn - 1) / bn;
-      return tiles(bm, bn) >= 224 && (tn * bn - N) * 16 <= N;
-    };
 #define DI_GEMM2(BM, BN, S, WGM, WGN, MINB)                                                      \
   do {                                                                                          \
     const int tm_ = (M + BM - 1) / BM, tn_ = (N + BN - 1) / BN;                                 \
@@ -430,10 +428,9 @@ int detllm_igemm_nt(const int8_t* A, const int8_t* B, int32_t* C, int M, int N, 
                        dim3(64 * WGM * WGN), 0, s, A, B, C, M, N, K, (i64)sA, (i64)sB, (i64)sC, \
                        tm_, tn_);                                                               \
   } while (0)
-    if (fits(256, 256)) DI_GEMM2(256, 256, 2, 4, 2, 1);
-    else if (fits(256, 192)) DI_GEMM2(256, 192, 2, 4, 2, 1);
-    else if (fits(256, 128)) DI_GEMM2(256, 128, 3, 4, 2, 1);
-    else if (tiles(128, 128) >= 512) DI_GEMM2(128, 128, 2, 2, 2, 2);
+    if (tiles(256, 256) >= 448) DI_GEMM2(256, 256, 2, 4, 2, 1);
+    else if (N % 192 == 0 && tiles(128, 192) >= 448) DI_GEMM2(128, 192, 2, 2, 2, 2);
+    else if (tiles(128, 128) >= 448) DI_GEMM2(128, 128, 2, 2, 2, 2);
     else DI_GEMM2(128, 64, 4, 4, 2, 1);
 #undef DI_GEMM2
     DI_LAUNCH_CHECK();

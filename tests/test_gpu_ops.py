@@ -204,7 +204,8 @@ def test_rope(O):
                                    (65, 1024, 3072), (200, 128, 300), (512, 2048, 1024),
                                    (2048, 1024, 4096), (2048, 3072, 1024), (2048, 1024, 6144),
                                    (1000, 2048, 1000), (129, 64, 130), (300, 192, 64),
-                                   (3000, 512, 9000), (2100, 1024, 4096)])
+                                   (3000, 512, 9000), (2100, 1024, 4096), (1900, 256, 6144),
+                                   (9000, 256, 1100)])
 def test_int_gemm_exact(M, K, N):
     from idempotent_llm_amd.backends import int_gemm
     rnd = np.random.default_rng(M * 7 + K + N)
