@@ -491,10 +491,20 @@ __device__ __forceinline__ int32_t row16_max(int32_t v) {
 // Slots past S read zero V fragments (16-slot chunks starting at or past S),
 // so their A values do not matter; the p of slots S .. ceil16(S) are 0.
 // |accumulators| <= 128 * 128 * S < 2^31 for S <= 131071.
+// K rows and validity flags of a wave's first 16-slot blocks, loaded before
+// the fused kernel's Q/K/V epilogue so that their latency hides behind it;
+// the slot the epilogue writes is taken from LDS instead.
+struct KPre {
+  v4i kb[4][2];
+  int vf[4];
+  const int8_t* k_new;  // LDS, 128 bytes
+  i64 new_slot;         // -1: none
+};
+
 template <int G>
 __device__ __forceinline__ void decode_body(const DecodeArgs& a, int kvh, int b,
                                             const int8_t* qsrc, const int64_t* tsrc,
-                                            int32_t* sh_scores) {
+                                            int32_t* sh_scores, const KPre* pre = nullptr) {
   static_assert(G <= 8, "query heads per kv head");
   __shared__ i64 red_buf[32];
   BlockRed red{red_buf, 0};
@@ -546,13 +556,26 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, int kvh, int b,
   for (int blk0 = wave; blk0 < nblk; blk0 += 16) {
     v4i kb[4][2];
     int vf[4];
+    if (pre && blk0 == wave) {
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int s = (blk0 + u * 4) * 16 + l16;
-      const int sc_ = s < S ? s : 0;
-      kb[u][0] = *(const v4i*)(kbase + (i64)sc_ * 128 + grp * 16);
-      kb[u][1] = *(const v4i*)(kbase + (i64)sc_ * 128 + 64 + grp * 16);
-      vf[u] = vrow[sc_];
+      for (int u = 0; u < 4; ++u) {
+        kb[u][0] = pre->kb[u][0];
+        kb[u][1] = pre->kb[u][1];
+        vf[u] = pre->vf[u];
+        if ((blk0 + u * 4) * 16 + l16 == pre->new_slot) {
+          kb[u][0] = *(const v4i*)(pre->k_new + grp * 16);
+          kb[u][1] = *(const v4i*)(pre->k_new + 64 + grp * 16);
+        }
+      }
+    } else {
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int s = (blk0 + u * 4) * 16 + l16;
+        const int sc_ = s < S ? s : 0;
+        kb[u][0] = *(const v4i*)(kbase + (i64)sc_ * 128 + grp * 16);
+        kb[u][1] = *(const v4i*)(kbase + (i64)sc_ * 128 + 64 + grp * 16);
+        vf[u] = vrow[sc_];
+      }
     }
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
@@ -724,9 +747,31 @@ __global__ __launch_bounds__(256) void k_qkv_attn_decode(DecodeArgs a, QKVArgs q
   if (w < G) slotw = kvh * G + w;
   else if (w == G) slotw = qa.n_q + kvh;
   else if (w == G + 1) slotw = qa.n_q + qa.n_kv + kvh;
-  if (slotw >= 0) qkv_head(qa, b, slotw, w < G ? q_lds[w] : nullptr, w < G ? &t_lds[w] : nullptr);
+  __shared__ __attribute__((aligned(16))) int8_t k_new[128];
+  // prefetch this wave's first K blocks of the scores pass (slots below the
+  // host bound a.S <= cap; the pass masks slots at or past the scanned count)
+  KPre pre;
+  {
+    const int lane = threadIdx.x & 63, l16 = lane & 15, grp = lane >> 4;
+    const int8_t* kbase = a.kc + ((i64)b * a.n_kv + kvh) * a.cap * 128;
+    const uint8_t* vrow = a.valid + (i64)b * a.valid_stride;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int s = (w + u * 4) * 16 + l16;
+      const int sc_ = s < a.S ? s : 0;
+      pre.kb[u][0] = *(const v4i*)(kbase + (i64)sc_ * 128 + grp * 16);
+      pre.kb[u][1] = *(const v4i*)(kbase + (i64)sc_ * 128 + 64 + grp * 16);
+      pre.vf[u] = vrow[sc_];
+    }
+    const i64 base = qa.slot_base_dev ? qa.slot_base_dev[0] : qa.slot_base;
+    pre.new_slot = (base >= 0 && base < qa.cap) ? base : -1;  // T = 1: slot = base
+    pre.k_new = k_new;
+  }
+  if (slotw >= 0)
+    qkv_head(qa, b, slotw, w < G ? q_lds[w] : nullptr, w < G ? &t_lds[w] : nullptr,
+             w == G ? k_new : nullptr);
   __syncthreads();
-  decode_body<G>(a, kvh, b, &q_lds[0][0], t_lds, sh_scores);
+  decode_body<G>(a, kvh, b, &q_lds[0][0], t_lds, sh_scores, &pre);
 }
 
 }  // namespace

@@ -80,7 +80,7 @@ __device__ __forceinline__ void wave_rmsnorm128(i64& a, i64& b) {
 // int8 row goes to q8_out[0..128) and its DI-Exp constant to *tpos_out
 // (global memory for the standalone kernel, LDS for the fused one).
 __device__ __forceinline__ void qkv_head(const QKVArgs& a, int r, int slotw, int8_t* q8_out,
-                                         int64_t* tpos_out) {
+                                         int64_t* tpos_out, int8_t* k_lds = nullptr) {
   const int lane = threadIdx.x & 63;
   const int n_heads = a.n_q + 2 * a.n_kv;
 
@@ -196,6 +196,10 @@ __device__ __forceinline__ void qkv_head(const QKVArgs& a, int r, int slotw, int
     if (slot >= 0 && slot < a.cap) {
       krow[c0] = (int8_t)outv[0];
       krow[c1] = (int8_t)outv[1];
+    }
+    if (k_lds) {  // the new K row for the fused attention (it may have prefetched the old one)
+      k_lds[c0] = (int8_t)outv[0];
+      k_lds[c1] = (int8_t)outv[1];
     }
     return;
   }
