@@ -114,10 +114,14 @@ class KVCache:
     def seq_len(self) -> int:
         return self.length
 
+    # Slots at or past the filled length are never read as data: scores of
+    # such slots are masked, and their V bytes enter P.V only with p = 0 (the
+    # hi/lo split's colsum term cancels them exactly), so the buffers are not
+    # zero-filled.
     def _alloc(self, B, n_layers, n_kv, hd, cap, device):
-        self.k8 = [torch.zeros(B, n_kv, cap, hd, dtype=torch.int8, device=device)
+        self.k8 = [torch.empty(B, n_kv, cap, hd, dtype=torch.int8, device=device)
                    for _ in range(n_layers)]
-        self.v8 = [torch.zeros(B, n_kv, hd, cap, dtype=torch.int8, device=device)
+        self.v8 = [torch.empty(B, n_kv, hd, cap, dtype=torch.int8, device=device)
                    for _ in range(n_layers)]
         self.valid_buf = torch.zeros(B, cap, dtype=torch.bool, device=device)
         self.cap = cap
@@ -136,9 +140,9 @@ class KVCache:
         L = self.length
         for li in range(len(self.k8)):
             B, n_kv, _, hd = self.k8[li].shape
-            nk = self.k8[li].new_zeros(B, n_kv, cap, hd)
+            nk = self.k8[li].new_empty(B, n_kv, cap, hd)
             nk[:, :, :L] = self.k8[li][:, :, :L]
-            nv = self.v8[li].new_zeros(B, n_kv, hd, cap)
+            nv = self.v8[li].new_empty(B, n_kv, hd, cap)
             nv[..., :L] = self.v8[li][..., :L]
             self.k8[li], self.v8[li] = nk, nv
         valid = torch.zeros(self.valid_buf.shape[0], cap, dtype=torch.bool,
