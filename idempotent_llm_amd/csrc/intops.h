@@ -452,6 +452,31 @@ DI_HD uint32_t sigmoid_est(uint32_t num, uint32_t den) {
   return (uint32_t)(fma((double)num, 128.0, (double)(den >> 1) + 0.5) / (double)den);
 }
 
+// 1 / x in single precision: v_rcp_f32 (1 ulp) on the device, the correctly
+// rounded quotient on the host
+DI_HD float rcp_f32(float x) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  return __builtin_amdgcn_rcpf(x);
+#else
+  return 1.0f / x;
+#endif
+}
+
+// sigmoid_est for 0 <= num <= den < 2^24 without a double division:
+// N = 128 num + floor(den/2) < 2^32 and v = N / den <= 128.5. fl(N), the
+// reciprocal of the exactly represented den and the product are each within
+// a relative 2^-23, so q = trunc(fl(fl(N) rcp(den))) is within 129 * 3 *
+// 2^-23 < 1 of v: floor(v) - 1 <= q <= floor(v) + 1, and one remainder step
+// (q den <= 129 * 2^24 < 2^32 by the exact 24-bit multiply; N - q den lies in
+// (-den, 2 den)) gives floor(v), the same integer as sigmoid_est.
+DI_HD uint32_t sigmoid_est24(uint32_t num, uint32_t den) {
+  const uint32_t N = num * 128u + (den >> 1);
+  uint32_t q = (uint32_t)((float)N * rcp_f32((float)den));
+  const int32_t rem = (int32_t)(N - mad_u24(q, den, 0u));
+  q += (rem >= (int32_t)den ? 1u : 0u) - (rem < 0 ? 1u : 0u);
+  return q;
+}
+
 // DI-Exp of -n (ops/di_exp.py:27-37) for 0 <= n < 2^22 and a row-invariant
 // 1 <= t < 2^23: e = fma(n, fl(1/t), 1 + 2^-26) is n/t + 1 + 2^-26 within
 // 2^-30 (the rounding of 1/t and of the fma, on values below 2^23), and a
@@ -518,11 +543,11 @@ DI_HD i64 isqrt_est(i64 n) {
 
 // ops/di_swiglu.py:39-58 on one element for |g|, |u| <= 2^14 (gate and up
 // after requant_i32_common(14)) and tpos < 2^23: |g| < 2^22 for dexp_est,
-// E <= tpos and den = tpos + E < 2^24 for sigmoid_est, g * sig (sig <= 128)
+// E <= tpos and den = tpos + E < 2^24 for sigmoid_est24, g * sig (sig <= 128)
 // fits int32 and g * sig * u int64. Same integer as swiglu_elem.
 DI_HD i64 swiglu_elem_est(int32_t g, int32_t u, const ExpEst& E) {
   const uint32_t e = dexp_est((uint32_t)(g < 0 ? -g : g), E);
-  const uint32_t sig = sigmoid_est(g >= 0 ? E.t : e, E.t + e);
+  const uint32_t sig = sigmoid_est24(g >= 0 ? E.t : e, E.t + e);
   return (i64)(g * (int32_t)sig) * (i64)u;
 }
 

@@ -67,6 +67,9 @@ void di_host_rhad_est(const int64_t* m, const int64_t* d, const double* sc, int6
 void di_host_sigmoid_est(const int64_t* num, const int64_t* den, int64_t n, int64_t* out) {
   for (int64_t i = 0; i < n; ++i) out[i] = sigmoid_est((uint32_t)num[i], (uint32_t)den[i]);
 }
+void di_host_sigmoid_est24(const int64_t* num, const int64_t* den, int64_t n, int64_t* out) {
+  for (int64_t i = 0; i < n; ++i) out[i] = sigmoid_est24((uint32_t)num[i], (uint32_t)den[i]);
+}
 // Mismatches of dexp_est(n) and dexp_est_sp(t - n) against the integer DI-Exp
 // for every n in [n_lo, n_hi) at one tpos.
 int64_t di_host_dexp_est_mismatches(int64_t tpos, int64_t n_lo, int64_t n_hi) {

@@ -763,6 +763,7 @@ __global__ void k_op_scalar(int op, const int64_t* a, const int64_t* b, const in
       case 2: norm_scale(a[i], b[i], &x, &y); o1[i] = x; o2[i] = y; break;
       case 3: fit_dyadic_ratio(a[i], b[i], &x, &y); o1[i] = x; o2[i] = y; break;
       case 5: fit_dyadic_ratio_127(a[i], &x, &y); o1[i] = x; o2[i] = y; break;
+      case 7: o1[i] = sigmoid_est24((uint32_t)a[i], (uint32_t)b[i]); break;
       default: o1[i] = scaled_round_div(a[i], b[i], c[i]); break;
     }
   }
@@ -1082,7 +1083,7 @@ int detllm_op_rope(const int64_t* x, const int64_t* pos, const int16_t* cos_t,
 int detllm_op_scalar(int op, const int64_t* a, const int64_t* b, const int64_t* c, int64_t n,
                      int64_t* o1, int64_t* o2, hipStream_t s) {
   if (n <= 0) return DI_OK;
-  if (op < 0 || op > 6) return DI_EINVAL;
+  if (op < 0 || op > 7) return DI_EINVAL;
   if (op == 6)
     hipLaunchKernelGGL(k_op_isqrt_wave, dim3(grid_for(n)), dim3(256), 0, s, a, n, o1);
   else

@@ -241,7 +241,9 @@ int detllm_op_rope(const int64_t* x, const int64_t* pos, const int16_t* cos_t,
  * (dyadic.py:75-90), 3 fit_dyadic_ratio (dyadic.py:52-72), 4
  * scaled_round_div (dyadic.py:45-49); and the device forms the fused kernels
  * use for the same functions: 5 fit_dyadic_ratio(a, 127) (constant-divisor
- * path), 6 isqrt by the wave-parallel search. */
+ * path), 6 isqrt by the wave-parallel search, 7 the SwiGLU sigmoid division
+ * round_half_away_div(a << 7, b) (ops/di_swiglu.py:52-55) in the fused
+ * kernels' single-precision form, for 0 <= a <= b < 2^24. */
 int detllm_op_scalar(int op, const int64_t* a, const int64_t* b, const int64_t* c, int64_t n,
                      int64_t* o1, int64_t* o2, hipStream_t s);
 

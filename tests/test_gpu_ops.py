@@ -93,6 +93,29 @@ def test_device_fast_paths_vs_closed_forms(D):
     eq(m5[:n0], D["fit127_m"]); eq(e5[:n0], D["fit127_e"])
 
 
+def test_sigmoid_division_single_precision_on_device():
+    """The fused SwiGLU's sigmoid division in its device form (v_rcp_f32
+    reciprocal, one remainder step) == round_half_away_div(num << 7, den)
+    (ops/di_swiglu.py:52-55) for 0 <= num <= den < 2^24: every num for
+    den < 300, the top of the range and random pairs of every bit length."""
+    from idempotent_llm_amd._lib import call
+    import random
+    rnd = random.Random(11)
+    num, den = [], []
+    for d in list(range(1, 300)) + [(1 << 24) - 1, (1 << 24) - 2, (1 << 23) + 1, 1 << 23]:
+        for n in (range(0, d + 1) if d < 300 else [0, 1, d // 2, d // 2 + 1, d - 1, d]):
+            num.append(n)
+            den.append(d)
+    for _ in range(1000000):
+        d = rnd.randrange(1, 1 << rnd.randrange(1, 25))
+        num.append(rnd.choice([0, d, d - 1, d // 2, rnd.randrange(0, d + 1)]))
+        den.append(d)
+    a, b = np.array(num, I64), np.array(den, I64)
+    out = torch.empty(a.size, dtype=torch.int64, device="cuda")
+    call("detllm_op_scalar", 7, g(a), g(b), None, a.size, out, None)
+    eq(out, (a * 128 + b // 2) // b)
+
+
 def test_dyadic_scalars(D):
     from idempotent_llm_amd import dyadic as dd
     eq(dd.scaled_round_div(g(D["srd_num"]), g(D["srd_den"]), g(D["srd_e"])), D["srd_out"])

@@ -339,6 +339,32 @@ def test_sigmoid_est_matches_restoring_division(lib):
     assert got.tolist() == want
 
 
+def _sigmoid24_cases(seed):
+    """(num, den) pairs for the single-precision sigmoid division: every num
+    for den < 300, the top of the range and random pairs over every bit
+    length up to 24, with num at 0, den, den - 1, den / 2 and random."""
+    rnd = random.Random(seed)
+    num, den = [], []
+    for d in list(range(1, 300)) + [(1 << 24) - 1, (1 << 24) - 2, (1 << 23) + 1, 1 << 23]:
+        for n in (range(0, d + 1) if d < 300 else [0, 1, d // 2, d // 2 + 1, d - 1, d]):
+            num.append(n)
+            den.append(d)
+    for _ in range(300000):
+        d = rnd.randrange(1, 1 << rnd.randrange(1, 25))
+        num.append(rnd.choice([0, d, d - 1, d // 2, rnd.randrange(0, d + 1)]))
+        den.append(d)
+    return np.array(num, I64), np.array(den, I64)
+
+
+def test_sigmoid_est24_matches_restoring_division(lib):
+    """sigmoid_est24 (single-precision reciprocal plus one remainder step) ==
+    round_half_away_div(num << 7, den) for num <= den < 2^24."""
+    num, den = _sigmoid24_cases(7)
+    got = _call2(lib, "di_host_sigmoid_est24", num, den)
+    want = [(int(n) * 128 + int(d) // 2) // int(d) for n, d in zip(num, den)]
+    assert got.tolist() == want
+
+
 @pytest.mark.parametrize("tpos", [1, 2, 3, 7, 100, 4095, 4096, 46341, 65537, 360626,
                                   (1 << 22) + 1, (1 << 23) - 1])
 def test_dexp_est_exhaustive(lib, tpos):
