@@ -264,7 +264,7 @@ def test_int_gemm_extremes_and_batched():
 
 
 def test_config0_gemm_requant():
-    """[64,1024] x [1024,3072] then requant_i8_static(P,1,0,m,20,1,0)
+    """Config c0: [64,1024] x [1024,3072] then requant_i8_static(P,1,0,m,20,1,0)
     and the rowcol variant, bit-identical to the CPU path."""
     from idempotent_llm_amd import artifact as art
     from idempotent_llm_amd import dyadic as dd
