@@ -228,7 +228,11 @@ def test_rope(O):
                                    (2048, 1024, 4096), (2048, 3072, 1024), (2048, 1024, 6144),
                                    (1000, 2048, 1000), (129, 64, 130), (300, 192, 64),
                                    (3000, 512, 9000), (2100, 1024, 4096), (1900, 256, 6144),
-                                   (9000, 256, 1100)])
+                                   (9000, 256, 1100),
+                                   # LM-head streaming path (M <= 16, N >= 32768) and its edges
+                                   (1, 1024, 151936), (8, 1024, 40000), (16, 1040, 32768),
+                                   (13, 4096, 33000), (5, 2048, 50001), (17, 1024, 40000),
+                                   (16, 1024, 32767)])
 def test_int_gemm_exact(M, K, N):
     from idempotent_llm_amd.backends import int_gemm
     rnd = np.random.default_rng(M * 7 + K + N)
