@@ -60,15 +60,16 @@ def decode_bench(model, B: int, steps: int, warmup: int):
     lens = torch.full((B,), PROMPT_LEN, dtype=torch.int64, device="cuda")
     logits, _, _, cache = model.forward(ids, pos)
     gd = GraphedDecode(model, cache, lens)
-    cur = model.greedy_pick(logits[:, -1])
-    for _ in range(warmup):
-        cur = model.greedy_pick(gd.step(cur))
+    # the greedy pick runs inside the captured step (GraphedDecode.step_greedy:
+    # the same tokens and logits as greedy_pick(step(cur)))
+    gd.step_greedy(model.greedy_pick(logits[:, -1]))
+    for _ in range(warmup - 1):
+        gd.step_greedy()
     torch.cuda.synchronize()
     toks = torch.empty(B, steps, dtype=torch.int64, device="cuda")
     t0 = time.perf_counter()
     for i in range(steps):
-        cur = model.greedy_pick(gd.step(cur))
-        toks[:, i] = cur
+        toks[:, i] = gd.step_greedy()
     torch.cuda.synchronize()
     dt = time.perf_counter() - t0
     return B * steps / dt, 1e3 * dt / steps, toks.cpu()
@@ -206,13 +207,13 @@ def c4_decode_bench(model, steps: int = 128, warmup: int = 10):
     torch.cuda.synchronize()
     t_pre = time.perf_counter() - t0
     gd = GraphedDecode(model, cache, vlens)
-    cur = model.greedy_pick(logits)
-    for _ in range(warmup):
-        cur = model.greedy_pick(gd.step(cur))
+    gd.step_greedy(model.greedy_pick(logits))
+    for _ in range(warmup - 1):
+        gd.step_greedy()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(steps):
-        cur = model.greedy_pick(gd.step(cur))
+        gd.step_greedy()
     torch.cuda.synchronize()
     dt = time.perf_counter() - t0
     return {"batch": B, "prompt_tokens": int(lens.sum()), "padded_len": T,

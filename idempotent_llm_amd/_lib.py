@@ -38,6 +38,7 @@ SIGNATURES = {
     "detllm_attn_decode": [P, P, P, P, P, L, I, I, I, I, L, P, P, P, S],
     "detllm_qkv_attn_decode": [P, I, L, I, I, I, P, P, P, P, L, P, L, P, L, P, L, P, L, P, L,
                                P, P, P, P, P, P, P, P, L, P, P, L, P, L, P, L, I, P, P, P, S],
+    "detllm_decode_prologue": [P, L, I, L, P, P, P, P, L, S],
     "detllm_op_quant_i8_pertoken": [P, P, P, I, I, P, P, P, S],
     "detllm_op_requant_i32_common": [P, P, P, I, L, I, I, I, P, P, S],
     "detllm_op_requant_i8_rowcol": [P, P, P, P, L, I, I, P, P, P, S],

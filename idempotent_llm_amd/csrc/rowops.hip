@@ -515,6 +515,24 @@ __global__ __launch_bounds__(RT) void k_qkv_epilogue_rows(QKVArgs a, int R, int 
   qkv_rows4(a, R, grp * 4, slotw);
 }
 
+// Bookkeeping of one graphed decode step before its replay (graphed.py:112-131
+// semantics): slot `slot` becomes valid in every row, the step's K/V write
+// slot and scanned-slot count go to the device scalars the captured kernels
+// read, and each row's position is its prompt length plus the steps taken.
+__global__ __launch_bounds__(256) void k_decode_prologue(uint8_t* valid, i64 stride, int B, i64 slot,
+                                                         int64_t* len_idx, int64_t* nslots,
+                                                         int64_t* pos, const int64_t* pos0,
+                                                         i64 step) {
+  for (int b = threadIdx.x; b < B; b += blockDim.x) {
+    valid[(i64)b * stride + slot] = 1;
+    pos[b] = pos0[b] + step;
+  }
+  if (threadIdx.x == 0) {
+    len_idx[0] = slot;
+    nslots[0] = slot + 1;
+  }
+}
+
 // =====================================================================
 // Op-level row kernels (one reference function each)
 // =====================================================================
@@ -930,6 +948,22 @@ int detllm_merge_rowcol(const int64_t* attn, int nsplit, int64_t split_stride, i
   a.C = C; a.attn = attn; a.nsplit = nsplit; a.split_stride = split_stride; a.os_m = os_m;
   a.os_k = os_k; a.col_m = col_m; a.col_k = col_k; a.a8 = a8; a.am = am; a.ak = ak;
   DI_ROWS_DISPATCH(R, C, k_merge_rowcol, dim3(R), s, a);
+  DI_LAUNCH_CHECK();
+  return DI_OK;
+}
+
+// One kernel for the per-step bookkeeping of a graphed decode step (a few
+// bytes per row): valid[b][slot] = 1, *len_idx = slot, *nslots = slot + 1,
+// pos[b] = pos0[b] + step.
+int detllm_decode_prologue(uint8_t* valid, int64_t valid_stride, int B, int64_t slot,
+                           int64_t* len_idx, int64_t* nslots, int64_t* pos, const int64_t* pos0,
+                           int64_t step, hipStream_t s) {
+  if (B <= 0) return DI_OK;
+  if (!valid || !len_idx || !nslots || !pos || !pos0 || slot < 0 || slot >= valid_stride ||
+      step < 0)
+    return DI_EINVAL;
+  hipLaunchKernelGGL(k_decode_prologue, dim3(1), dim3(256), 0, s, valid, valid_stride, B, slot,
+                     len_idx, nslots, pos, pos0, step);
   DI_LAUNCH_CHECK();
   return DI_OK;
 }

@@ -18,7 +18,8 @@ from __future__ import annotations
 
 import torch
 
-from .model import IntQwen3, KVCache
+from ._lib import call
+from .model import GREEDY_CHUNK, IntQwen3, KVCache
 
 I64 = torch.int64
 
@@ -39,18 +40,43 @@ class GraphedDecode:
         dev = model.device
         self.B = cache.valid_buf.shape[0]
         self.length = cache.length
+        self.steps = 0
         self.ids_buf = torch.zeros(self.B, 1, dtype=I64, device=dev)
-        self.pos_buf = lens.to(dev).view(self.B, 1).clone().to(I64)
+        self.pos0 = lens.to(dev).to(I64).contiguous().view(self.B).clone()
+        self.pos_buf = self.pos0.view(self.B, 1).clone()
         cache.len_idx = torch.zeros(1, dtype=I64, device=dev)
         cache.nslots = torch.zeros(1, dtype=I64, device=dev)
-        self.graph = None
+        nch = -(-model.vocab // GREEDY_CHUNK)
+        self._pick_scratch = (torch.empty(self.B, nch, dtype=I64, device=dev),
+                              torch.empty(self.B, nch, dtype=I64, device=dev))
+        self.graph = None        # forward only (step)
+        self.graph_pick = None   # forward + greedy pick into ids_buf (step_greedy)
         self.out = None
+        self.out_pick = None
         self._grow_to(_next_bucket(self.length + 1))
 
     def _grow_to(self, cap: int):
         self.cache.resize(cap)
         self.cache.static_cap = cap
         self.graph = None   # a captured graph references the old buffers
+        self.graph_pick = None
+
+    def _prologue(self):
+        """Validity flag, write slot, scanned-slot count and positions of this
+        step, one kernel (graphed.py:112-131 does them as separate ops)."""
+        c = self.cache
+        call("detllm_decode_prologue", c.valid_buf.view(torch.uint8), c.valid_buf.shape[1],
+             self.B, self.length, c.len_idx, c.nslots, self.pos_buf, self.pos0, self.steps)
+
+    def _advance(self):
+        self.length += 1
+        self.steps += 1
+        self.cache.length = self.length
+
+    def _pick_into_ids(self, logits):
+        m = self.model
+        call("detllm_greedy_pick", logits, m.head_m, self.B, m.vocab, GREEDY_CHUNK,
+             self._pick_scratch[0], self._pick_scratch[1], self.ids_buf.view(self.B))
 
     def _run(self):
         logits, _, _, _ = self.model.forward(self.ids_buf, self.pos_buf, self.cache)
@@ -67,6 +93,18 @@ class GraphedDecode:
             self.out = self._run()
         self.graph = g
 
+    def _capture_pick(self):
+        # warm-up as in _capture (the forward only: the pick would overwrite
+        # this step's input ids), then one graph of the forward and the pick
+        for _ in range(3):
+            self._run()
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            self.out_pick = self._run()
+            self._pick_into_ids(self.out_pick[:, 0])
+        self.graph_pick = g
+
     @torch.no_grad()
     def step(self, cur_ids: torch.Tensor) -> torch.Tensor:
         """cur_ids int64 [B] (device). Returns int32 logits [B, vocab]; the
@@ -74,14 +112,30 @@ class GraphedDecode:
         c = self.cache
         if self.length + 1 > c.static_cap:
             self._grow_to(_next_bucket(self.length + 1))
-        c.valid_buf[:, self.length] = True
-        c.len_idx.fill_(self.length)
-        c.nslots.fill_(self.length + 1)
+        self._prologue()
         self.ids_buf.copy_(cur_ids.view(self.B, 1))
         if self.graph is None:
             self._capture()
         self.graph.replay()
-        self.length += 1
-        c.length = self.length
-        self.pos_buf += 1
+        self._advance()
         return self.out[:, 0]
+
+    @torch.no_grad()
+    def step_greedy(self, cur_ids: torch.Tensor | None = None) -> torch.Tensor:
+        """One greedy decode step with the pick (IntQwen3.greedy_pick) inside
+        the captured graph: it reads this step's ids from the buffer the
+        previous pick wrote (cur_ids, int64 [B], seeds it on the first call).
+        Returns the picked ids, int64 [B] (the next step's input buffer —
+        clone to keep); the step's logits are in ``self.out_pick[:, 0]``.
+        Same tokens and logits as ``greedy_pick(step(cur_ids))``."""
+        c = self.cache
+        if self.length + 1 > c.static_cap:
+            self._grow_to(_next_bucket(self.length + 1))
+        self._prologue()
+        if cur_ids is not None:
+            self.ids_buf.copy_(cur_ids.view(self.B, 1))
+        if self.graph_pick is None:
+            self._capture_pick()
+        self.graph_pick.replay()
+        self._advance()
+        return self.ids_buf.view(self.B)

@@ -161,6 +161,16 @@ int detllm_attn_decode(const int8_t* q8, const int64_t* tpos, const int8_t* kcac
                        int S, int n_q, int n_kv, int64_t cap, const int64_t* s_dev,
                        int32_t* scratch, int64_t* out, hipStream_t s);
 
+/* Per-step bookkeeping of the graph-captured decode (src/detllm/graphed.py:
+ * 112-131: the validity flag of the step's slot, the device scalars holding
+ * the write slot and the scanned-slot count, the positions), one launch
+ * before each replay:
+ * valid[b * valid_stride + slot] = 1, *len_idx = slot, *nslots = slot + 1,
+ * pos[b] = pos0[b] + step for b < B. */
+int detllm_decode_prologue(uint8_t* valid, int64_t valid_stride, int B, int64_t slot,
+                           int64_t* len_idx, int64_t* nslots, int64_t* pos, const int64_t* pos0,
+                           int64_t step, hipStream_t s);
+
 /* One decode step's attention block with the Q/K/V epilogue fused in (one
  * query token per row; n_q / n_kv <= 2): detllm_qkv_epilogue with T = 1 —
  * model.py:200-216, :303-358 — followed by detllm_attn_decode — model.py:347-381

@@ -125,3 +125,37 @@ def test_graph_growth_matches_oracle(case):
     te, le = IntQwen3Oracle(d).generate(ids.cpu().numpy(), steps)
     assert tg.cpu().numpy().tolist() == te.tolist()
     assert chain_hashes(lg) == chain_hashes(le)
+
+
+def test_step_greedy_matches_step_then_pick(case):
+    """GraphedDecode.step_greedy (the pick captured in the step's graph, ids
+    fed back on the device) gives the tokens and logits of
+    greedy_pick(step(cur)) at batch 3, across a cache bucket growth for the
+    tiny model (re-capture of both graphs)."""
+    from idempotent_llm_amd.graphed import GraphedDecode
+    rec, m, _ = case
+    ids = _ids(rec)[None].repeat(3, 1)
+    ids[1, -1] = 7
+    ids[2, -2:] = 11
+    B, T = ids.shape
+    steps = 260 - T if rec["dims"]["hidden"] == 256 else 12
+    pos = torch.arange(T, device="cuda").expand(B, T)
+    lens = torch.full((B,), T, dtype=I64, device="cuda")
+    runs = []
+    for mode in ("step", "greedy"):
+        logits, _, _, cache = m.forward(ids, pos)
+        gd = GraphedDecode(m, cache, lens)
+        cur = m.greedy_pick(logits[:, -1])
+        toks, lgs = [], []
+        for i in range(steps):
+            if mode == "step":
+                lg = gd.step(cur)
+                cur = m.greedy_pick(lg)
+            else:
+                cur = gd.step_greedy(cur if i == 0 else None)
+                lg = gd.out_pick[:, 0]
+            toks.append(cur.clone())
+            lgs.append(lg.clone())
+        runs.append((torch.stack(toks), torch.stack(lgs)))
+    assert torch.equal(runs[0][0], runs[1][0])
+    assert torch.equal(runs[0][1], runs[1][1])
