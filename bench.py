@@ -136,7 +136,7 @@ def decode_gemv_jobs(model, B: int):
 
 
 def _traffic():
-    """HBM bytes per k_gemv_nt launch measured by rocprofv3 FETCH_SIZE and
+    """HBM bytes per skinny-GEMM launch measured by rocprofv3 FETCH_SIZE and
     WRITE_SIZE passes over `bench.py --kernel-probe` (profiles/), or None."""
     path = os.path.join(ROOT, "profiles", "gemv_traffic.json")
     if not os.path.exists(path):
@@ -161,7 +161,8 @@ def gemv_roofline(model, B: int):
     achieved = per_launch / (us * 1e-6) / 1e9
     return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
             "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": _traffic(),
-            "kernel": "k_gemv_nt<1,4,2>", "batch": B, "launches_per_step": len(jobs),
+            "kernel": "k_gemv_nt<1,4,2> (LM head: k_gemv_stream)", "batch": B,
+            "launches_per_step": len(jobs),
             "bytes_per_launch": int(per_launch), "avg_launch_us": round(us, 3)}
 
 
