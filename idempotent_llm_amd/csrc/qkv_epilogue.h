@@ -108,7 +108,10 @@ __device__ __forceinline__ void qkv_head(const QKVArgs& a, int r, int slotw, int
   const i64 vqm = a.vq_m[kvh], vqk = a.vq_k[kvh];
   const i64 ksm = a.ks_m[kvh], ksk = a.ks_k[kvh];
   i64 p0, p1;
-  {
+  if (a.nsplit == 1) {  // no K split: one load per channel
+    p0 = a.P[off + c0];
+    p1 = a.P[off + c1];
+  } else {
     uint32_t s0 = 0, s1 = 0;
     for (int k0 = 0; k0 < a.nsplit; k0 += 4) {
       int32_t t0[4], t1[4];

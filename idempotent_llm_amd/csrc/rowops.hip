@@ -213,6 +213,21 @@ template <int NR, int VPT>
 __device__ __forceinline__ void load_rows_i32_sum(i64 (&v)[NR][VPT], const int32_t* P,
                                                   int nsplit, i64 stride, const i64 (&off)[NR],
                                                   int C) {
+  if (nsplit == 1) {  // no K split (block-uniform): one load per element
+#pragma unroll
+    for (int q = 0; q < NR; ++q)
+#pragma unroll
+      for (int j = 0; j < VPT; ++j) {
+        const int c = threadIdx.x + j * (int)blockDim.x;
+        v[q][j] = P[off[q] + (c < C ? c : C - 1)];
+      }
+#pragma unroll
+    for (int q = 0; q < NR; ++q)
+#pragma unroll
+      for (int j = 0; j < VPT; ++j)
+        if (threadIdx.x + j * (int)blockDim.x >= C) v[q][j] = 0;
+    return;
+  }
   constexpr int KU = NR * VPT > 8 ? 2 : 4;  // partials per batch of loads
   uint32_t s[NR][VPT];
 #pragma unroll
@@ -374,32 +389,44 @@ struct SwigluArgs {
 template <int VPT>
 __device__ __forceinline__ void swiglu_quant_row(const SwigluArgs& a, int r, BlockRed& red) {
   const int I = a.I;
+  // Many rows (prefill, more than 4 columns per thread): the down-smoothing
+  // scales load after the requantisation, when the gate/up scales are dead,
+  // and g, u live as int32 — fewer registers, more rows resident per CU (other
+  // rows hide the extra load). Decode rows load everything up front.
+  constexpr bool kLate = VPT > 4;
   i64 gm[VPT], um[VPT], dsm[VPT];
   prefetch_cols(gm, a.gate_m, I);
   prefetch_cols(um, a.up_m, I);
-  prefetch_cols(dsm, a.ds_m, I);
+  if (!kLate) prefetch_cols(dsm, a.ds_m, I);
   const i64 xm = a.xm[r], xk = a.xk[r];
   i64 gu[2][VPT];
   const i64 offs[2] = {(i64)r * 2 * I, (i64)r * 2 * I + I};
   load_rows_i32_sum<2, VPT>(gu, a.P, a.nsplit, a.split_stride, offs, I);
   i64 gk, uk;
   requant_common_row2(gu[0], gm, a.gate_k, gu[1], um, a.up_k, xk, 14, red, &gk, &uk);
+  // requant_i32_common(14) leaves |g|, |u| <= 2^14 (the shift brings the
+  // row's largest magnitude to at most 2^14)
+  int32_t g32[VPT], u32[VPT];
+#pragma unroll
+  for (int j = 0; j < VPT; ++j) {
+    g32[j] = (int32_t)gu[0][j];
+    u32[j] = (int32_t)gu[1][j];
+  }
+  if (kLate) prefetch_cols(dsm, a.ds_m, I);
   const i64 tp = di_exp_tpos_fast(xm, gk);
+  i64 y[VPT];
   if (tp < ((i64)1 << 23)) {
-    // requant_i32_common(14) leaves |g|, |u| <= 2^14 (the shift brings the
-    // row's largest magnitude to at most 2^14)
     const ExpEst Ee = make_expest(tp);
 #pragma unroll
-    for (int j = 0; j < VPT; ++j)
-      gu[0][j] = wmul(swiglu_elem_est((int32_t)gu[0][j], (int32_t)gu[1][j], Ee), dsm[j]);
+    for (int j = 0; j < VPT; ++j) y[j] = wmul(swiglu_elem_est(g32[j], u32[j], Ee), dsm[j]);
   } else {
     const ExpR E = make_exp(tp);
 #pragma unroll
-    for (int j = 0; j < VPT; ++j) gu[0][j] = wmul(swiglu_elem_e(gu[0][j], gu[1][j], E), dsm[j]);
+    for (int j = 0; j < VPT; ++j) y[j] = wmul(swiglu_elem_e(g32[j], u32[j], E), dsm[j]);
   }
   const i64 ym = wmul(xm, xm);
   const i64 yk = wadd(wadd(wadd(gk, uk), 7), a.ds_k);
-  quant_row(gu[0], ym, yk, I, red, a.y8 + (i64)r * I, a.ym + r, a.yk + r);
+  quant_row(y, ym, yk, I, red, a.y8 + (i64)r * I, a.ym + r, a.yk + r);
 }
 
 template <int VPT, int NT = RT_WIDE>
@@ -432,7 +459,14 @@ __device__ __forceinline__ void merge_rowcol_row(const MergeArgs& a, int r, Bloc
   prefetch_cols(cm, a.col_m, C);
 #pragma unroll
   for (int j = 0; j < VPT; ++j) v[j] = 0;
-  for (int k0 = 0; k0 < a.nsplit; k0 += 2) {
+  if (a.nsplit == 1) {  // one load per element (block-uniform)
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) {
+      const int c = threadIdx.x + j * (int)blockDim.x;
+      v[j] = a.attn[off + (c < C ? c : C - 1)];
+    }
+  }
+  for (int k0 = 0; a.nsplit > 1 && k0 < a.nsplit; k0 += 2) {
     i64 t[2][VPT];
 #pragma unroll
     for (int kk = 0; kk < 2; ++kk) {
