@@ -429,8 +429,13 @@ __device__ __forceinline__ void swiglu_quant_row(const SwigluArgs& a, int r, Blo
   quant_row(y, ym, yk, I, red, a.y8 + (i64)r * I, a.ym + r, a.yk + r);
 }
 
+// Prefill (256-thread blocks, 8-12 columns per thread): at least three blocks
+// per CU (168 VGPRs; 12 columns spill a few registers) beat two unspilled
+// blocks by ~3 % on a 2048-token prefill (measured; four blocks spill more and
+// lose).
 template <int VPT, int NT = RT_WIDE>
-__global__ __launch_bounds__(NT) void k_swiglu_quant(SwigluArgs a) {
+__global__ __launch_bounds__(NT, (NT == 256 && VPT >= 8 && VPT <= 12) ? 3 : 1) void k_swiglu_quant(
+    SwigluArgs a) {
   __shared__ i64 red_buf[32];
   BlockRed red{red_buf, 0};
   swiglu_quant_row<VPT>(a, blockIdx.x, red);
