@@ -33,6 +33,7 @@ struct QKVArgs {
   i64 qs_k;
   const int64_t* kq_m;  // [n_kv * 128]
   const int64_t* kq_k;
+  const int64_t* kq_est;  // optional [n_kv * 128][4] (kq_channel_est), else computed
   const int64_t* ks_m;  // [n_kv]
   const int64_t* ks_k;
   const int64_t* vq_m;
@@ -49,6 +50,26 @@ struct QKVArgs {
   const int64_t* slot_base_dev;  // optional device scalar (graph replay)
   i64 slot_base;
 };
+
+// The static K requantisation's divisor of one channel (model.py:326-329,
+// requant_i8_static with row scale (1, rowk)): den = kq_m << max(rowk - kq_k,
+// 0) (1 if not positive), the numerator's up-shift max(kq_k - rowk, 0), and
+// DivEst(den, 1) for rhad_est_i8. Every input is a layer constant, so the
+// estimate can be computed once per channel (kq_est) instead of per element.
+struct KqChan {
+  i64 den, up;
+  DivEst D;
+};
+
+__device__ __forceinline__ KqChan kq_channel(i64 km, i64 kk, i64 rowk) {
+  const i64 shift = wsub(rowk, kk);
+  KqChan q;
+  q.up = imax(wneg(shift), 0);
+  q.den = shl(km, imax(shift, 0));
+  if (q.den <= 0) q.den = 1;
+  q.D = make_divest(q.den < ((i64)1 << 49) ? q.den : 1, 1.0);
+  return q;
+}
 
 // ilog2(max(max |x|, 1)) over the wave's 128 channels (two per lane)
 __device__ __forceinline__ i64 wave_ilog2_absmax(i64 a, i64 b) {
@@ -409,15 +430,20 @@ __device__ __forceinline__ void qkv_rows4(const QKVArgs& a, int R, int r0, int s
     uint32_t w[2] = {0, 0};
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      const i64 km = a.kq_m[kvh * 128 + c[i]], kk = a.kq_k[kvh * 128 + c[i]];
-      const i64 shift = wsub(rowk, kk);
-      const i64 up = imax(wneg(shift), 0), down = imax(shift, 0);
-      i64 den = shl(km, down);
-      if (den <= 0) den = 1;
-      const i64 n = shl(rv[i], up);
+      KqChan q;
+      if (a.kq_est) {
+        const int64_t* e = a.kq_est + (i64)(kvh * 128 + c[i]) * 4;
+        q.den = e[0];
+        q.up = e[1];
+        q.D.r = __longlong_as_double(e[2]);
+        q.D.k = __longlong_as_double(e[3]);
+      } else {
+        q = kq_channel(a.kq_m[kvh * 128 + c[i]], a.kq_k[kvh * 128 + c[i]], rowk);
+      }
+      const i64 n = shl(rv[i], q.up);
       const i64 lim = (i64)1 << 49;  // 2 |n| + den < 2^51 for rhad_est_i8
-      const int o = (den < lim && n > -lim && n < lim) ? rhad_est_i8(n, make_divest(den, 1.0))
-                                                       : (int)clamp_i8(rhad(n, den));
+      const int o = (q.den < lim && n > -lim && n < lim) ? rhad_est_i8(n, q.D)
+                                                         : (int)clamp_i8(rhad(n, q.den));
       w[i >> 2] |= (uint32_t)(uint8_t)(int8_t)o << (8 * (i & 3));
     }
     if (sok) {

@@ -572,6 +572,18 @@ __global__ __launch_bounds__(256) void k_decode_prologue(uint8_t* valid, i64 str
   }
 }
 
+// kq_channel of every channel: est[i] = {den, up, bits of D.r, bits of D.k}
+__global__ __launch_bounds__(256) void k_kq_est(const int64_t* kq_m, const int64_t* kq_k, i64 n,
+                                                i64 rowk, int64_t* est) {
+  const i64 i = blockIdx.x * (i64)blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const KqChan q = kq_channel(kq_m[i], kq_k[i], rowk);
+  est[i * 4 + 0] = q.den;
+  est[i * 4 + 1] = q.up;
+  est[i * 4 + 2] = __double_as_longlong(q.D.r);
+  est[i * 4 + 3] = __double_as_longlong(q.D.k);
+}
+
 // =====================================================================
 // Op-level row kernels (one reference function each)
 // =====================================================================
@@ -1007,6 +1019,19 @@ int detllm_decode_prologue(uint8_t* valid, int64_t valid_stride, int B, int64_t 
   return DI_OK;
 }
 
+// Per-channel divisor estimates of the static K requantisation for one layer
+// (model-load time): est [n][4] = {den, up, bits of 1/den, bits of
+// (floor(den/2) + 1/2) / den} from kq_m, kq_k [n] and rowk = 20 + k_norm_k.
+int detllm_kq_est(const int64_t* kq_m, const int64_t* kq_k, int64_t n, int64_t rowk,
+                  int64_t* est, hipStream_t s) {
+  if (n <= 0) return DI_OK;
+  if (!kq_m || !kq_k || !est) return DI_EINVAL;
+  hipLaunchKernelGGL(k_kq_est, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, kq_m, kq_k, n,
+                     rowk, est);
+  DI_LAUNCH_CHECK();
+  return DI_OK;
+}
+
 int detllm_qkv_epilogue(const int32_t* P, int nsplit, int64_t split_stride, int B, int T,
                         int n_q, int n_kv, const int64_t* xm, const int64_t* xk,
                         const int64_t* positions, const int64_t* q_m, int64_t q_k,
@@ -1018,7 +1043,7 @@ int detllm_qkv_epilogue(const int32_t* P, int nsplit, int64_t split_stride, int 
                         const int16_t* cos_t, const int16_t* sin_t, int64_t max_pos,
                         int8_t* q8, int64_t* tpos, int64_t* dbg, int8_t* kcache,
                         int8_t* vcache, int64_t cap, const int64_t* slot_base_dev,
-                        int64_t slot_base, hipStream_t s) {
+                        int64_t slot_base, const int64_t* kq_est, hipStream_t s) {
   if (B <= 0 || T <= 0) return DI_OK;
   if (n_q <= 0 || n_kv <= 0 || n_q % n_kv != 0 || nsplit < 1 || cap <= 0 || max_pos <= 0)
     return DI_EINVAL;
@@ -1031,7 +1056,7 @@ int detllm_qkv_epilogue(const int32_t* P, int nsplit, int64_t split_stride, int 
   a.kq_k = kq_k; a.ks_m = ks_m; a.ks_k = ks_k; a.vq_m = vq_m; a.vq_k = vq_k; a.cos_t = cos_t;
   a.sin_t = sin_t; a.max_pos = max_pos; a.q8 = q8; a.tpos = tpos; a.dbg = dbg;
   a.kcache = kcache; a.vcache = vcache; a.cap = cap; a.slot_base_dev = slot_base_dev;
-  a.slot_base = slot_base;
+  a.slot_base = slot_base; a.kq_est = kq_est;
   const int heads = n_q + 2 * n_kv;
   const int R = B * T;
   // the rows layout reads P 16 bytes at a time

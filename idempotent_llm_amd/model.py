@@ -78,6 +78,9 @@ class LayerWeights:
     pf_attn: torch.Tensor | None = None   # Q/K/V epilogue + attention-output merge
     pf_o: torch.Tensor | None = None      # residual after o
     pf_mlp: torch.Tensor | None = None    # SwiGLU
+    # per-channel divisors of the static K requantisation, [n_kv * 128, 4]
+    # int64 (detllm_kq_est): layer constants computed once at load
+    kq_est: torch.Tensor | None = None
 
 
 def _pack(L: LayerWeights, names) -> torch.Tensor:
@@ -224,6 +227,8 @@ class IntQwen3:
                                   "attn_out_col_m"])
             L.pf_o = _pack(L, ["o_m", "ms_m"])
             L.pf_mlp = _pack(L, ["gate_m", "up_m", "ds_m"])
+            L.kq_est = torch.empty(L.kq_m.numel(), 4, dtype=I64, device=dev)
+            call("detllm_kq_est", L.kq_m, L.kq_k, L.kq_m.numel(), 20 + L.k_norm_k, L.kq_est)
         self._greedy_scratch = {}
         self._plans: dict = {}
 
@@ -353,7 +358,7 @@ class IntQwen3:
              L.k_norm_m, L.k_norm_k, L.qs_m, L.qs_k, L.kq_m, L.kq_k, L.ks_m, L.ks_k,
              L.vq_m, L.vq_k, self.rope_cos, self.rope_sin, self.max_pos, q8, tpos, None,
              cache.k8[li], cache.v8[li], cache.cap, cache.len_idx if static else None,
-             0 if static else S_past)
+             0 if static else S_past, L.kq_est)
         valid = cache.valid_buf.view(torch.uint8)
         if T == 1:
             call("detllm_attn_decode", q8, tpos, cache.k8[li], cache.v8[li], valid, cache.cap,

@@ -136,7 +136,16 @@ int detllm_qkv_epilogue(const int32_t* P, int nsplit, int64_t split_stride, int 
                         const int16_t* cos_t, const int16_t* sin_t, int64_t max_pos,
                         int8_t* q8, int64_t* tpos, int64_t* dbg, int8_t* kcache,
                         int8_t* vcache, int64_t cap, const int64_t* slot_base_dev,
-                        int64_t slot_base, hipStream_t s);
+                        int64_t slot_base, const int64_t* kq_est, hipStream_t s);
+
+/* The static K requantisation's per-channel divisors for one layer
+ * (requant_i8_static of model.py:326-329 with row scale (1, rowk), rowk =
+ * 20 + k_norm_k), computed once at model load: est [n][4] = {den = kq_m <<
+ * max(rowk - kq_k, 0) (1 if not positive), up = max(kq_k - rowk, 0), the bits
+ * of fl(1/den) and of fl((floor(den/2) + 1/2) / den)}. detllm_qkv_epilogue
+ * reads them through kq_est (nullable: then it derives them per element). */
+int detllm_kq_est(const int64_t* kq_m, const int64_t* kq_k, int64_t n, int64_t rowk,
+                  int64_t* est, hipStream_t s);
 
 /* ------------------------------------------------------------ attention -- */
 

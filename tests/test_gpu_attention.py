@@ -71,7 +71,7 @@ def _run(dims, B, cap, S, slot, device_bounds, seed):
     tpos = torch.empty(B, nq, 1, dtype=I64, device="cuda")
     out_a = torch.empty(B, nq * hd, dtype=I64, device="cuda")
     call("detllm_qkv_epilogue", P, ns, B * P.shape[2], B, 1, nq, nkv, xm, xk, pos, *common,
-         q8, tpos, None, ka, va, cap, slot_dev, slot)
+         q8, tpos, None, ka, va, cap, slot_dev, slot, None)
     call("detllm_attn_decode", q8, tpos, ka, va, vbytes, cap, B, S_host, nq, nkv, cap, s_dev,
          scratch, out_a)
     # fused launch
@@ -234,3 +234,41 @@ def test_decode_attention_vs_oracle(name):
     got = out.cpu().numpy()
     bad = np.argwhere(got != want)
     assert bad.size == 0, f"{len(bad)} mismatches, first at {bad[0].tolist()}"
+
+
+@pytest.mark.parametrize("T", [100, 257])
+def test_prefill_epilogue_kq_estimates(T):
+    """The prefill Q/K/V epilogue (rows layout, R > 64) with the K channels'
+    divisor estimates precomputed at load (detllm_kq_est) writes the same q8,
+    DI-Exp constants and K/V cache bytes as deriving them per element."""
+    from idempotent_llm_amd._lib import call
+    dims = art.MID
+    prm = _layer_params(dims, 3)
+    nq, nkv, hd = dims["n_q_heads"], dims["n_kv_heads"], 128
+    rnd = torch.Generator().manual_seed(T)
+    B, cap = 1, 512
+    P = torch.randint(-(1 << 19), 1 << 19, (1, B * T, (nq + 2 * nkv) * hd), generator=rnd,
+                      dtype=torch.int32).cuda()
+    xm = torch.randint(1 << 15, 1 << 16, (B * T,), generator=rnd, dtype=I64).cuda()
+    xk = torch.randint(22, 30, (B * T,), generator=rnd, dtype=I64).cuda()
+    pos = torch.arange(T, dtype=I64).cuda()
+    common = (prm["q_m"], prm["q_k"], prm["k_m"], prm["k_k"], prm["v_m"], prm["v_k"],
+              prm["q_norm_m"], prm["q_norm_k"], prm["k_norm_m"], prm["k_norm_k"], prm["qs_m"],
+              prm["qs_k"], prm["kq_m"], prm["kq_k"], prm["ks_m"], prm["ks_k"], prm["vq_m"],
+              prm["vq_k"], prm["cos"], prm["sin"], prm["cos"].shape[0])
+    est = torch.empty(prm["kq_m"].numel(), 4, dtype=I64, device="cuda")
+    call("detllm_kq_est", prm["kq_m"], prm["kq_k"], prm["kq_m"].numel(),
+         20 + prm["k_norm_k"], est)
+    outs = []
+    for e in (None, est):
+        q8 = torch.empty(B, nq, T, hd, dtype=torch.int8, device="cuda")
+        tpos = torch.empty(B, nq, T, dtype=I64, device="cuda")
+        kc = torch.zeros(B, nkv, cap, hd, dtype=torch.int8, device="cuda")
+        vc = torch.zeros(B, nkv, hd, cap, dtype=torch.int8, device="cuda")
+        call("detllm_qkv_epilogue", P, 1, B * T * P.shape[2], B, T, nq, nkv, xm, xk, pos,
+             *common, q8, tpos, None, kc, vc, cap, None, 0, e)
+        outs.append((q8, tpos, kc, vc))
+    torch.cuda.synchronize()
+    for a, b in zip(*outs):
+        assert torch.equal(a, b)
+    assert outs[0][2].abs().sum().item() > 0
