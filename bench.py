@@ -66,13 +66,13 @@ def decode_bench(model, B: int, steps: int, warmup: int):
     for _ in range(warmup - 1):
         gd.step_greedy()
     torch.cuda.synchronize()
-    toks = torch.empty(B, steps, dtype=torch.int64, device="cuda")
+    toks = torch.empty(steps, B, dtype=torch.int64, device="cuda")  # rows: contiguous copies
     t0 = time.perf_counter()
     for i in range(steps):
-        toks[:, i] = gd.step_greedy()
+        toks[i] = gd.step_greedy()
     torch.cuda.synchronize()
     dt = time.perf_counter() - t0
-    return B * steps / dt, 1e3 * dt / steps, toks.cpu()
+    return B * steps / dt, 1e3 * dt / steps, toks.t().cpu()
 
 
 def prefill_bench(model, T: int):

@@ -280,20 +280,21 @@ class IntQwen3:
         ids = ids.to(device=dev, dtype=I64)
         positions = positions.to(device=dev, dtype=I64)
         B, T = ids.shape
-        if chunk_valid is None:
-            chunk_valid = torch.ones(B, T, dtype=torch.bool, device=dev)
-        chunk_valid = chunk_valid.to(dev)
         if cache is None:
             cache = KVCache()
         static = cache.static_cap > 0
         S_past = cache.length
         if static:
+            # the step's slot flag is set before the replay (graphed.py)
             assert T == 1, "graphed (static-capacity) mode decodes one token per row"
             S = cache.static_cap
         else:
             S = S_past + T
             cache.reserve(self, B, S)
-            cache.valid_buf[:, S_past:S] = chunk_valid
+            if chunk_valid is None:
+                cache.valid_buf[:, S_past:S] = True
+            else:
+                cache.valid_buf[:, S_past:S] = chunk_valid.to(dev)
         H, R = self.hidden, B * T
         h = torch.empty(R, H, dtype=torch.int32, device=dev)
         k_res = torch.empty(R, dtype=I64, device=dev)
