@@ -202,6 +202,9 @@ def c4_decode_bench(model, steps: int = 128, warmup: int = 10):
     valid = torch.from_numpy(valid).cuda()
     pos = torch.arange(T, device="cuda").expand(B, T)
     vlens = valid.sum(dim=1)
+    # one untimed prefill first (as prefill_bench does): the first one also
+    # pays the allocator's growth for the batch-32 caches and activations
+    model._forward(ids, pos, None, valid, (vlens - 1).clamp(min=0))
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     logits, _, _, cache = model._forward(ids, pos, None, valid, (vlens - 1).clamp(min=0))
