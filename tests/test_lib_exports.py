@@ -112,3 +112,17 @@ def test_model_requires_gpu_loudly(tmp_path):
         IntQwen3(d, backend="rocm")
     with pytest.raises(ValueError):
         IntQwen3(d, backend="cpu")
+
+
+def test_missing_library_fails_loudly(monkeypatch, tmp_path):
+    # No CPU fallback: with the shared library absent, loading it and every
+    # call through the C-ABI raise LibraryMissing instead of computing.
+    from idempotent_llm_amd import _lib
+    monkeypatch.setattr(_lib, "_lib", None)
+    monkeypatch.setattr(_lib, "LIB_PATH", str(tmp_path / "libdetllm_hip.so"))
+    with pytest.raises(_lib.LibraryMissing, match="no CPU fallback"):
+        _lib.load()
+    with pytest.raises(_lib.LibraryMissing):
+        _lib.gemv_plan(8, 1024, 1024)
+    with pytest.raises(_lib.LibraryMissing):
+        _lib.call("detllm_igemv_plan", 8, 1024, 1024)
