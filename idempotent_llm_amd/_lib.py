@@ -27,18 +27,19 @@ SIGNATURES = {
     "detllm_igemv_plan": [I, I, I, P],
     "detllm_transpose_i8": [P, P, I, I, I, L, L, S],
     "detllm_greedy_pick": [P, P, I, I, I, P, P, P, S],
-    "detllm_embed_normq": [P, I, I, L, P, P, P, P, P, P, L, P, P, P, S],
+    "detllm_logits_digest": [P, I, I, P, S],
+    "detllm_embed_normq": [P, I, I, L, P, P, P, P, P, P, L, P, P, P, P, S],
     "detllm_residual_normq": [P, I, L, I, I, P, P, P, L, I, P, P, P, L, P, P, P, S],
     "detllm_norm_quant": [P, I, I, P, L, P, P, P, S],
     "detllm_swiglu_quant": [P, I, L, I, I, P, P, P, L, P, L, P, L, P, P, P, S],
     "detllm_merge_rowcol": [P, I, L, I, I, P, L, P, L, P, P, P, S],
     "detllm_qkv_epilogue": [P, I, L, I, I, I, I, P, P, P, P, L, P, L, P, L, P, L, P, L, P, L,
-                            P, P, P, P, P, P, P, P, L, P, P, P, P, P, L, P, L, P, S],
+                            P, P, P, P, P, P, P, P, L, P, P, P, P, P, L, P, L, P, P, S],
     "detllm_kq_est": [P, P, L, L, P, S],
     "detllm_attn_prefill": [P, P, P, P, P, L, I, I, I, I, I, L, P, S],
-    "detllm_attn_decode": [P, P, P, P, P, L, I, I, I, I, L, P, P, P, S],
+    "detllm_attn_decode": [P, P, P, P, P, L, I, I, I, I, L, P, P, P, P, S],
     "detllm_qkv_attn_decode": [P, I, L, I, I, I, P, P, P, P, L, P, L, P, L, P, L, P, L, P, L,
-                               P, P, P, P, P, P, P, P, L, P, P, L, P, L, P, L, I, P, P, P, S],
+                               P, P, P, P, P, P, P, P, L, P, P, L, P, L, P, L, I, P, P, P, P, S],
     "detllm_decode_prologue": [P, L, I, L, P, P, P, P, L, S],
     "detllm_op_quant_i8_pertoken": [P, P, P, I, I, P, P, P, S],
     "detllm_op_requant_i32_common": [P, P, P, I, L, I, I, I, P, P, S],
@@ -49,7 +50,7 @@ SIGNATURES = {
     "detllm_op_softmax": [P, P, P, P, I, L, I, I, I, P, S],
     "detllm_op_di_exp": [P, P, P, I, I, P, P, S],
     "detllm_op_swiglu": [P, P, P, P, P, P, I, I, P, P, P, S],
-    "detllm_op_rope": [P, P, P, P, L, L, P, S],
+    "detllm_op_rope": [P, P, P, P, L, L, P, P, S],
     "detllm_op_scalar": [I, P, P, P, L, P, P, S],
 }
 
@@ -108,6 +109,27 @@ def gemv_plan(M: int, N: int, K: int) -> int:
     if rc != 0:
         raise RuntimeError(f"detllm_igemv_plan failed (code {rc})")
     return out.value
+
+
+# bits of the device error word (include/detllm_hip.h)
+ERR_TOKEN, ERR_POSITION, ERR_SLOTS = 1, 2, 4
+
+
+def raise_for_error_word(word: int, vocab=None, max_pos=None) -> None:
+    """Raise what the reference raises for the indices a kernel flagged:
+    IndexError for a token id or position outside the table (embed_e8[ids],
+    cos_t[positions] in src/detllm/model.py, ops/rope.py:48-49)."""
+    word = int(word)
+    if not word:
+        return
+    msgs = []
+    if word & ERR_TOKEN:
+        msgs.append(f"token id out of range for the embedding table (size {vocab})")
+    if word & ERR_POSITION:
+        msgs.append(f"position out of range for the RoPE tables (size {max_pos})")
+    if word & ERR_SLOTS:
+        msgs.append("device slot count exceeded the slots the attention launch was sized for")
+    raise IndexError("; ".join(msgs))
 
 
 def call(name: str, *args, stream=None) -> None:

@@ -18,6 +18,7 @@ from __future__ import annotations
 
 import torch
 
+from . import torch_ops  # noqa: F401  (registers the detllm_rocm:: operators)
 from ._lib import call
 
 BACKENDS = ("reference", "cuda", "rocm")
@@ -81,13 +82,23 @@ def gemm_nt(a: torch.Tensor, bt: torch.Tensor, out: torch.Tensor | None = None,
 
 def int_gemm(a: torch.Tensor, b: torch.Tensor, backend: str = "rocm") -> torch.Tensor:
     """Exact integer GEMM: a [*, M, K] int8 x b [*, K, N] int8 -> int32
-    (backends.py:88-135). Batched dims must match; a 2-D b is shared."""
+    (backends.py:88-135). Batched dims must match; a 2-D b is shared. Runs
+    as the custom operator detllm_rocm::int_gemm, so torch.compile and
+    graph capture see one opaque node (as int_prims.py:96-136 does for the
+    reference's kernels)."""
     assert a.dtype == torch.int8 and b.dtype == torch.int8, (a.dtype, b.dtype)
     assert a.shape[-1] == b.shape[-2]
     _require_rocm(backend)
+    if b.dim() != 2 or a.dim() == 2:
+        assert a.shape[:-2] == b.shape[:-2], (a.shape, b.shape)
+    return torch.ops.detllm_rocm.int_gemm(a, b)
+
+
+def _int_gemm_impl(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
+    """The kernel behind detllm_rocm::int_gemm (operands checked by int_gemm)."""
     if b.dim() == 2 and a.dim() > 2:
         lead = a.shape[:-1]
-        out = int_gemm(a.reshape(-1, a.shape[-1]), b, backend)
+        out = _int_gemm_impl(a.reshape(-1, a.shape[-1]), b)
         return out.reshape(*lead, b.shape[-1])
     M, K, N = a.shape[-2], a.shape[-1], b.shape[-1]
     if M == 0 or N == 0:
@@ -97,7 +108,6 @@ def int_gemm(a: torch.Tensor, b: torch.Tensor, backend: str = "rocm") -> torch.T
     ap = _pad_k(a, Kp)
     if a.dim() == 2:
         return gemm_nt(ap, bt)[0]
-    assert a.shape[:-2] == b.shape[:-2], (a.shape, b.shape)
     A = ap.reshape(-1, M, Kp)
     Bt = bt.reshape(-1, N, Kp)
     batch = A.shape[0]
@@ -107,10 +117,11 @@ def int_gemm(a: torch.Tensor, b: torch.Tensor, backend: str = "rocm") -> torch.T
 
 
 def int_gemm_u8i8(p_u8: torch.Tensor, b: torch.Tensor, backend: str = "rocm") -> torch.Tensor:
-    """backends.py:138-149: (p-64)@b + 64*colsum(b) for p in [0, 128]."""
+    """backends.py:138-149: (p-64)@b + 64*colsum(b) for p in [0, 128].
+    int64, as in the reference, where the int32 column sum promotes."""
     shifted = (p_u8 - 64).to(torch.int8)
     core = int_gemm(shifted, b, backend)
-    corr = b.to(torch.int32).sum(dim=-2, keepdim=True, dtype=torch.int32) * 64
+    corr = b.to(torch.int64).sum(dim=-2, keepdim=True) * 64
     return core + corr
 
 

@@ -454,6 +454,7 @@ struct DecodeArgs {
   const int64_t* s_dev;  // optional device bound on the scanned slots
   int S, n_q, n_kv;
   i64 cap, valid_stride;
+  int32_t* err;          // optional device error word (DI_ERR_SLOTS)
 };
 
 constexpr int MAXG = 8;
@@ -513,6 +514,9 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, int kvh, int b,
   int S = a.S;
   if (a.s_dev) {
     const i64 sd = a.s_dev[0];
+    // more slots than the launch was sized for: the reference would scan
+    // them, so the result would differ; report instead of truncating
+    if (sd > (i64)S && a.err && threadIdx.x == 0 && kvh == 0) atomicOr(a.err, DI_ERR_SLOTS);
     S = (int)imax(0, imin((i64)S, sd));
   }
   const int Spad = (a.S + 15) & ~15;
@@ -803,7 +807,7 @@ int detllm_attn_prefill(const int8_t* q8, const int64_t* tpos, const int8_t* kc,
 int detllm_attn_decode(const int8_t* q8, const int64_t* tpos, const int8_t* kc, const int8_t* vc,
                        const uint8_t* valid, int64_t valid_stride, int B, int S, int n_q, int n_kv,
                        int64_t cap, const int64_t* s_dev, int32_t* scratch, int64_t* out,
-                       hipStream_t s) {
+                       int32_t* err, hipStream_t s) {
   if (B <= 0) return DI_OK;
   if (n_q <= 0 || n_kv <= 0 || n_q % n_kv || S < 0 || S > cap || cap % 16 != 0 ||
       valid_stride < S)
@@ -820,7 +824,8 @@ int detllm_attn_decode(const int8_t* q8, const int64_t* tpos, const int8_t* kc, 
   } else if (!scratch) {
     return DI_ERANGE;
   }
-  DecodeArgs a{q8, tpos, kc, vc, valid, out, scratch, s_dev, S, n_q, n_kv, cap, valid_stride};
+  DecodeArgs a{q8, tpos, kc, vc, valid, out, scratch, s_dev, S, n_q, n_kv, cap, valid_stride,
+               err};
   const dim3 grid(n_kv, B);
   switch (G) {
     case 1: hipLaunchKernelGGL(k_attn_decode<1>, grid, dim3(256), dyn, s, a); break;
@@ -847,12 +852,13 @@ int detllm_qkv_attn_decode(const int32_t* P, int nsplit, int64_t split_stride, i
                            int8_t* kcache, int8_t* vcache, int64_t cap,
                            const int64_t* slot_base_dev, int64_t slot_base,
                            const uint8_t* valid, int64_t valid_stride, int S,
-                           const int64_t* s_dev, int32_t* scratch, int64_t* out,
+                           const int64_t* s_dev, int32_t* scratch, int64_t* out, int32_t* err,
                            hipStream_t s) {
   if (B <= 0) return DI_OK;
   if (n_q <= 0 || n_kv <= 0 || n_q % n_kv || nsplit < 1 || S < 1 || S > cap || cap % 16 != 0 ||
       valid_stride < S || max_pos <= 0 || !P || !out)
     return DI_EINVAL;
+  if (S > DEC_MAX_S) return DI_ERANGE;  // int32 MFMA accumulators of P.V
   if (!slot_base_dev && (slot_base < 0 || slot_base + 1 > cap)) return DI_ERANGE;
   const int G = n_q / n_kv;
   if (G > 2) return DI_ENOSYS;  // one wave per head slot of the block
@@ -874,9 +880,9 @@ int detllm_qkv_attn_decode(const int32_t* P, int nsplit, int64_t split_stride, i
   qa.ks_m = ks_m; qa.ks_k = ks_k; qa.vq_m = vq_m; qa.vq_k = vq_k; qa.cos_t = cos_t;
   qa.sin_t = sin_t; qa.max_pos = max_pos; qa.q8 = nullptr; qa.tpos = nullptr; qa.dbg = nullptr;
   qa.kcache = kcache; qa.vcache = vcache; qa.cap = cap; qa.slot_base_dev = slot_base_dev;
-  qa.slot_base = slot_base;
+  qa.slot_base = slot_base; qa.err = err;
   DecodeArgs a{nullptr, nullptr, kcache, vcache, valid, out, scratch, s_dev, S, n_q, n_kv, cap,
-               valid_stride};
+               valid_stride, err};
   const dim3 grid(n_kv, B);
   if (G == 1)
     hipLaunchKernelGGL(k_qkv_attn_decode<1>, grid, dim3(256), dyn, s, a, qa);

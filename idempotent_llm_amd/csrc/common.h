@@ -22,7 +22,27 @@
     if (e_ != hipSuccess) return (int)e_;          \
   } while (0)
 
+// Bits of the device error word (an int32 the caller passes as `err`):
+// an index the reference would reject with IndexError.
+#define DI_ERR_TOKEN 1     // token id outside [-vocab, vocab)
+#define DI_ERR_POSITION 2  // position outside [-max_pos, max_pos)
+#define DI_ERR_SLOTS 4     // device slot count beyond the launch's slot bound
+
 namespace di {
+
+// torch's advanced-indexing rule for a table of n rows (the reference's
+// embed_e8[ids] and cos_t[positions]): -n <= x < 0 reads row x + n, any other
+// x outside [0, n) raises IndexError. Here such an x reads row 0 (memory
+// safety) and ORs `bit` into *err when err is non-null; the host raises from
+// the word at its next check.
+__device__ __forceinline__ i64 torch_index(i64 x, i64 n, int32_t* err, int bit) {
+  if (x < 0) x += n;
+  if (x < 0 || x >= n) {
+    if (err) atomicOr(err, bit);
+    return 0;
+  }
+  return x;
+}
 
 __device__ __forceinline__ i64 shfl_xor64(i64 v, int mask) {
   int lo = (int)(v & 0xffffffff);

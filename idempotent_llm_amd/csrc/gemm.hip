@@ -401,6 +401,27 @@ __global__ __launch_bounds__(256) void k_argmax_final(const int64_t* pv, const i
   if (threadIdx.x == 0) out[r] = b.i;
 }
 
+// 64-bit digest of a logits row: the wrapping sum over i of the splitmix64
+// finaliser of (i << 32) | (uint32) x_i. Addition modulo 2^64 is associative
+// and commutative, so the block's reduction order cannot change the value.
+__device__ __forceinline__ u64 mix64(u64 z) {
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+  return z ^ (z >> 31);
+}
+
+__global__ __launch_bounds__(1024) void k_logits_digest(const int32_t* __restrict__ rows, int V,
+                                                        int64_t* out) {
+  __shared__ i64 red_buf[32];
+  BlockRed red{red_buf, 0};
+  const int32_t* row = rows + (i64)blockIdx.x * V;
+  i64 acc = 0;
+  for (int i = threadIdx.x; i < V; i += blockDim.x)
+    acc = wadd(acc, (i64)mix64(((u64)(uint32_t)i << 32) | (u64)(uint32_t)row[i]));
+  acc = red.sum(acc);
+  if (threadIdx.x == 0) out[blockIdx.x] = acc;
+}
+
 // Recommended K split of the skinny GEMM for an [M, K] x [N, K]^T product:
 // enough (block, K-range) pairs to spread the weight stream over the CUs,
 // at most 8 partials. The caller sizes the partial buffer with it.
@@ -552,6 +573,15 @@ int detllm_greedy_pick(const int32_t* logits, const int64_t* head_m, int R, int 
                      pv, pi);
   DI_LAUNCH_CHECK();
   hipLaunchKernelGGL(k_argmax_final, dim3(R), dim3(256), 0, s, pv, pi, nch, out);
+  DI_LAUNCH_CHECK();
+  return DI_OK;
+}
+
+// One 64-bit digest per int32 row [R][V] (k_logits_digest).
+int detllm_logits_digest(const int32_t* rows, int R, int V, int64_t* out, hipStream_t s) {
+  if (R <= 0) return DI_OK;
+  if (V <= 0 || !rows || !out || R > 0x7fffffff) return DI_EINVAL;
+  hipLaunchKernelGGL(k_logits_digest, dim3(R), dim3(1024), 0, s, rows, V, out);
   DI_LAUNCH_CHECK();
   return DI_OK;
 }

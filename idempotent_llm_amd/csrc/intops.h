@@ -22,6 +22,14 @@
 #include <math.h>
 #include <stdint.h>
 
+// The exact-integer estimates below rely on IEEE-correct rounding of every
+// fp64/fp32 operation as written: no reassociation, no reciprocal
+// substitution, no contraction of a separate multiply and add into an fma.
+#if defined(__FAST_MATH__) || defined(__FINITE_MATH_ONLY__) && __FINITE_MATH_ONLY__
+#error "intops.h must not be built with -ffast-math or -ffinite-math-only"
+#endif
+#pragma clang fp contract(off)
+
 #if defined(__HIPCC__) || defined(__HIP__)
 #include <hip/hip_runtime.h>
 #define DI_HD __host__ __device__ __forceinline__

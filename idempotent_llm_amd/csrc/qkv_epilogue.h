@@ -49,6 +49,7 @@ struct QKVArgs {
   i64 cap;
   const int64_t* slot_base_dev;  // optional device scalar (graph replay)
   i64 slot_base;
+  int32_t* err;  // optional device error word (DI_ERR_POSITION)
 };
 
 // The static K requantisation's divisor of one channel (model.py:326-329,
@@ -152,7 +153,8 @@ __device__ __forceinline__ void qkv_head(const QKVArgs& a, int r, int slotw, int
     p0 = (int32_t)s0;
     p1 = (int32_t)s1;
   }
-  const i64 pos = pos_raw < 0 ? 0 : (pos_raw >= a.max_pos ? a.max_pos - 1 : pos_raw);
+  const i64 pos = torch_index(pos_raw, a.max_pos, is_v || lane ? nullptr : a.err,
+                              DI_ERR_POSITION);
   const i64 cs0 = a.cos_t[pos * 128 + c0], cs1 = a.cos_t[pos * 128 + c1];
   const i64 sn0 = a.sin_t[pos * 128 + c0], sn1 = a.sin_t[pos * 128 + c1];
   const i64 slot = base + t;
@@ -370,7 +372,8 @@ __device__ __forceinline__ void qkv_rows4(const QKVArgs& a, int R, int r0, int s
   }
   const int64_t* gam = is_q ? a.q_norm_m : a.k_norm_m;
   i64 gm[8], cs[8], sn[8];
-  const i64 pos = pos_raw < 0 ? 0 : (pos_raw >= a.max_pos ? a.max_pos - 1 : pos_raw);
+  const i64 pos = torch_index(pos_raw, a.max_pos, (j == 0 && rok) ? a.err : nullptr,
+                              DI_ERR_POSITION);
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     gm[i] = gam[c[i]];

@@ -290,6 +290,7 @@ struct ResNormArgs {
   int8_t* x8;  // null: no norm-quant
   int64_t* xm;
   int64_t* xk;
+  int32_t* err;  // optional device error word (DI_ERR_TOKEN)
 };
 
 template <int VPT>
@@ -311,8 +312,7 @@ __device__ __forceinline__ void residual_normq_row(const ResNormArgs& a, int r, 
       if (threadIdx.x + j * (int)blockDim.x >= C) h[j] = 0;
     kr = 0;
   } else if (a.mode == 0) {
-    i64 id = a.ids[r];
-    id = id < 0 ? 0 : (id >= a.vocab ? a.vocab - 1 : id);  // memory safety only
+    const i64 id = torch_index(a.ids[r], a.vocab, threadIdx.x ? nullptr : a.err, DI_ERR_TOKEN);
     const i64 dm = a.em[id], ek = a.ek[id];
 #pragma unroll
     for (int j = 0; j < VPT; ++j) {
@@ -788,13 +788,13 @@ __global__ void k_op_swiglu(const int64_t* gate, const int64_t* gm, const int64_
 }
 
 __global__ void k_op_rope(const int64_t* x, const int64_t* pos, const int16_t* cos_t,
-                          const int16_t* sin_t, i64 max_pos, i64 rows, int64_t* y) {
+                          const int16_t* sin_t, i64 max_pos, i64 rows, int64_t* y,
+                          int32_t* err) {
   // ops/rope.py:38-55 on rows of 128 channels
   const i64 r = blockIdx.x * 4 + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   if (r >= rows) return;
-  i64 p = pos[r];
-  p = p < 0 ? 0 : (p >= max_pos ? max_pos - 1 : p);
+  const i64 p = torch_index(pos[r], max_pos, lane ? nullptr : err, DI_ERR_POSITION);
   const i64 x0 = x[r * 128 + lane], x1 = x[r * 128 + lane + 64];
   y[r * 128 + lane] = rshift_round(
       wadd(wmul(x0, (i64)cos_t[p * 128 + lane]), wmul(wneg(x1), (i64)sin_t[p * 128 + lane])), 14);
@@ -833,6 +833,22 @@ __global__ void k_op_scalar(int op, const int64_t* a, const int64_t* b, const in
       case 3: fit_dyadic_ratio(a[i], b[i], &x, &y); o1[i] = x; o2[i] = y; break;
       case 5: fit_dyadic_ratio_127(a[i], &x, &y); o1[i] = x; o2[i] = y; break;
       case 7: o1[i] = sigmoid_est24((uint32_t)a[i], (uint32_t)b[i]); break;
+      // the fp64-estimate forms of the fused kernels, element by element:
+      // a = operand, b = divisor or tpos, c = scale s (8, 9, 11) or k (14)
+      case 8: o1[i] = rhad_est((double)a[i], make_divest(b[i], (double)c[i])); break;
+      case 9: o1[i] = rhad_est_signed(a[i], make_divest(b[i], (double)c[i])); break;
+      case 10: o1[i] = rhad_est_i8(a[i], make_divest(b[i], 1.0)); break;
+      case 11:
+        o1[i] = rhad_est_corr_signed(a[i], (int)c[i], b[i], make_divest(b[i], (double)c[i]));
+        break;
+      case 12: o1[i] = dexp_est((uint32_t)a[i], make_expest(b[i])); break;
+      case 13: {
+        const ExpEst E = make_expest(b[i]);
+        o1[i] = dexp_est_sp((int32_t)a[i], E, dexp_sp_const(E));
+        break;
+      }
+      case 14: o1[i] = di_exp_tpos_fast(a[i], b[i]); break;
+      case 15: o1[i] = isqrt_est(a[i]); break;
       default: o1[i] = scaled_round_div(a[i], b[i], c[i]); break;
     }
   }
@@ -936,12 +952,13 @@ extern "C" {
 int detllm_embed_normq(const int64_t* ids, int R, int C, int64_t vocab, const int8_t* e8,
                        const int64_t* em, const int64_t* ek, int32_t* h, int64_t* k_res,
                        const int64_t* sm_m, int64_t sm_k, int8_t* x8, int64_t* xm, int64_t* xk,
-                       hipStream_t s) {
+                       int32_t* err, hipStream_t s) {
   if (R <= 0) return DI_OK;
   if (C <= 0 || vocab <= 0 || !ids || !e8 || !em || !ek || !h || !k_res) return DI_EINVAL;
   ResNormArgs a{};
   a.C = C; a.mode = 0; a.vocab = vocab; a.ids = ids; a.e8 = e8; a.em = em; a.ek = ek;
   a.h = h; a.k_res = k_res; a.sm_m = sm_m; a.sm_k = sm_k; a.x8 = x8; a.xm = xm; a.xk = xk;
+  a.err = err;
   DI_ROWS_DISPATCH(R, C, k_residual_normq, dim3(R), s, a);
   DI_LAUNCH_CHECK();
   return DI_OK;
@@ -1043,7 +1060,7 @@ int detllm_qkv_epilogue(const int32_t* P, int nsplit, int64_t split_stride, int 
                         const int16_t* cos_t, const int16_t* sin_t, int64_t max_pos,
                         int8_t* q8, int64_t* tpos, int64_t* dbg, int8_t* kcache,
                         int8_t* vcache, int64_t cap, const int64_t* slot_base_dev,
-                        int64_t slot_base, const int64_t* kq_est, hipStream_t s) {
+                        int64_t slot_base, const int64_t* kq_est, int32_t* err, hipStream_t s) {
   if (B <= 0 || T <= 0) return DI_OK;
   if (n_q <= 0 || n_kv <= 0 || n_q % n_kv != 0 || nsplit < 1 || cap <= 0 || max_pos <= 0)
     return DI_EINVAL;
@@ -1056,7 +1073,7 @@ int detllm_qkv_epilogue(const int32_t* P, int nsplit, int64_t split_stride, int 
   a.kq_k = kq_k; a.ks_m = ks_m; a.ks_k = ks_k; a.vq_m = vq_m; a.vq_k = vq_k; a.cos_t = cos_t;
   a.sin_t = sin_t; a.max_pos = max_pos; a.q8 = q8; a.tpos = tpos; a.dbg = dbg;
   a.kcache = kcache; a.vcache = vcache; a.cap = cap; a.slot_base_dev = slot_base_dev;
-  a.slot_base = slot_base; a.kq_est = kq_est;
+  a.slot_base = slot_base; a.kq_est = kq_est; a.err = err;
   const int heads = n_q + 2 * n_kv;
   const int R = B * T;
   // the rows layout reads P 16 bytes at a time
@@ -1169,11 +1186,11 @@ int detllm_op_swiglu(const int64_t* gate, const int64_t* gm, const int64_t* gk,
 
 int detllm_op_rope(const int64_t* x, const int64_t* pos, const int16_t* cos_t,
                    const int16_t* sin_t, int64_t max_pos, int64_t rows, int64_t* y,
-                   hipStream_t s) {
+                   int32_t* err, hipStream_t s) {
   if (rows <= 0) return DI_OK;
   if (max_pos <= 0) return DI_EINVAL;
   hipLaunchKernelGGL(k_op_rope, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, s, x, pos, cos_t,
-                     sin_t, max_pos, rows, y);
+                     sin_t, max_pos, rows, y, err);
   DI_LAUNCH_CHECK();
   return DI_OK;
 }
@@ -1181,7 +1198,7 @@ int detllm_op_rope(const int64_t* x, const int64_t* pos, const int16_t* cos_t,
 int detllm_op_scalar(int op, const int64_t* a, const int64_t* b, const int64_t* c, int64_t n,
                      int64_t* o1, int64_t* o2, hipStream_t s) {
   if (n <= 0) return DI_OK;
-  if (op < 0 || op > 7) return DI_EINVAL;
+  if (op < 0 || op > 15) return DI_EINVAL;
   if (op == 6)
     hipLaunchKernelGGL(k_op_isqrt_wave, dim3(grid_for(n)), dim3(256), 0, s, a, n, o1);
   else

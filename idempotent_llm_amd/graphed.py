@@ -12,6 +12,15 @@ construction:
   * bucket overflow reallocates the cache (filled slots copied verbatim) and
     the next step recaptures.
 The graph contains kernel launches only (no memset nodes, no host reads).
+
+``mode`` and ``layer_compile`` are the reference's arguments
+(graphed.py:44-45). mode="capture" (default) replays the whole-step graph;
+mode="layers" runs the same static-capacity step as eager launches of the
+fused layer kernels (where the reference hands per-layer graphs to
+inductor). ``layer_compile`` is accepted for the same signature: the
+reference compiles its generic layer with inductor, and here every layer is
+already a fixed sequence of hand-fused kernels, so there is nothing to
+compile. Both modes give the same bits.
 """
 
 from __future__ import annotations
@@ -19,7 +28,7 @@ from __future__ import annotations
 import torch
 
 from ._lib import call
-from .model import GREEDY_CHUNK, IntQwen3, KVCache
+from .model import DEC_MAX_SLOTS, GREEDY_CHUNK, IntQwen3, KVCache
 
 I64 = torch.int64
 
@@ -32,9 +41,17 @@ def _next_bucket(n: int) -> int:
 
 
 class GraphedDecode:
-    def __init__(self, model: IntQwen3, cache: KVCache, lens: torch.Tensor):
+    def __init__(self, model: IntQwen3, cache: KVCache, lens: torch.Tensor,
+                 mode: str = "capture", layer_compile: bool = True):
         """cache: as returned by a prefill ``forward``; lens: int64 [B] true
-        prompt lengths (the next token's position per row)."""
+        prompt lengths (the next token's position per row); mode "capture"
+        (whole-step graph) or "layers" (eager static-capacity step)."""
+        if getattr(model, "backend", None) != "rocm":
+            raise ValueError("GraphedDecode drives the rocm backend's IntQwen3")
+        if mode not in ("capture", "layers"):
+            raise ValueError(f"unknown mode {mode!r}; expected 'capture' or 'layers'")
+        self.mode = mode
+        self.layer_compile = bool(layer_compile)
         self.model = model
         self.cache = cache
         dev = model.device
@@ -56,6 +73,9 @@ class GraphedDecode:
         self._grow_to(_next_bucket(self.length + 1))
 
     def _grow_to(self, cap: int):
+        if self.length + 1 > DEC_MAX_SLOTS:
+            raise IndexError(f"decode past {DEC_MAX_SLOTS} cache slots is not supported "
+                             "(int32 accumulators of the decode attention)")
         self.cache.resize(cap)
         self.cache.static_cap = cap
         self.graph = None   # a captured graph references the old buffers
@@ -114,9 +134,12 @@ class GraphedDecode:
             self._grow_to(_next_bucket(self.length + 1))
         self._prologue()
         self.ids_buf.copy_(cur_ids.view(self.B, 1))
-        if self.graph is None:
-            self._capture()
-        self.graph.replay()
+        if self.mode == "layers":
+            self.out = self._run()
+        else:
+            if self.graph is None:
+                self._capture()
+            self.graph.replay()
         self._advance()
         return self.out[:, 0]
 
@@ -134,8 +157,12 @@ class GraphedDecode:
         self._prologue()
         if cur_ids is not None:
             self.ids_buf.copy_(cur_ids.view(self.B, 1))
-        if self.graph_pick is None:
-            self._capture_pick()
-        self.graph_pick.replay()
+        if self.mode == "layers":
+            self.out_pick = self._run()
+            self._pick_into_ids(self.out_pick[:, 0])
+        else:
+            if self.graph_pick is None:
+                self._capture_pick()
+            self.graph_pick.replay()
         self._advance()
         return self.ids_buf.view(self.B)

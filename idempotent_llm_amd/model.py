@@ -36,14 +36,19 @@ from dataclasses import dataclass
 
 import torch
 
-from ._lib import call, gemv_plan
-from .backends import canonical_backend, gemm_nt
+from . import dyadic as dy
+from . import ops
+from ._lib import call, gemv_plan, raise_for_error_word
+from .backends import canonical_backend, gemm_nt, int_gemm, int_gemm_u16i8
 from .guard import NoFloatMode
 
 I64 = torch.int64
 P_OUT_BITS = 15
 OUT_FRAC_BITS = 20
 GREEDY_CHUNK = 2048
+# slots the decode attention scans at most (int32 MFMA accumulators of P.V:
+# 128 * 128 * S < 2^31)
+DEC_MAX_SLOTS = 131071
 
 
 @dataclass
@@ -231,6 +236,30 @@ class IntQwen3:
             call("detllm_kq_est", L.kq_m, L.kq_k, L.kq_m.numel(), 20 + L.k_norm_k, L.kq_est)
         self._greedy_scratch = {}
         self._plans: dict = {}
+        # device error word of the index checks the reference does on the
+        # host (IndexError from embed_e8[ids] / cos_t[positions]); the
+        # kernels OR bits into it, raise_if_device_error() reads it
+        self._err = torch.zeros(1, dtype=torch.int32, device=dev)
+
+    def raise_if_device_error(self):
+        """Synchronise on the error word and raise IndexError (as the
+        reference's embed_e8[ids] / cos_t[positions] do) when a kernel saw a
+        token id or position outside its table since the last check."""
+        word = int(self._err.item())
+        if word:
+            self._err.zero_()
+            raise_for_error_word(word, vocab=self.vocab, max_pos=self.max_pos)
+
+    def _check_host_indices(self, ids: torch.Tensor, positions: torch.Tensor):
+        """Host tensors are checked before the copy, so a bad index raises
+        where the reference's indexing raises."""
+        for t, n, what in ((ids, self.vocab, "token id"), (positions, self.max_pos, "position")):
+            if t.device.type == "cpu" and t.numel():
+                lo, hi = int(t.min()), int(t.max())
+                if lo < -n or hi >= n:
+                    bad = lo if lo < -n else hi
+                    raise IndexError(f"{what} {bad} is out of bounds for dimension 0 "
+                                     f"with size {n}")
 
     # reference-layout view of the LM head (model.py:136)
     @property
@@ -277,6 +306,7 @@ class IntQwen3:
 
     def _forward(self, ids, positions, cache, chunk_valid, head_rows=None):
         dev = self.device
+        self._check_host_indices(ids, positions)
         ids = ids.to(device=dev, dtype=I64)
         positions = positions.to(device=dev, dtype=I64)
         B, T = ids.shape
@@ -287,7 +317,7 @@ class IntQwen3:
         if static:
             # the step's slot flag is set before the replay (graphed.py)
             assert T == 1, "graphed (static-capacity) mode decodes one token per row"
-            S = cache.static_cap
+            S = min(cache.static_cap, DEC_MAX_SLOTS)
         else:
             S = S_past + T
             cache.reserve(self, B, S)
@@ -303,7 +333,7 @@ class IntQwen3:
         xk = torch.empty(R, dtype=I64, device=dev)
         L0 = self.layers[0]
         call("detllm_embed_normq", ids.contiguous().view(-1), R, H, self.vocab, self.embed_e8,
-             self.embed_m, self.embed_k, h, k_res, L0.as_m, L0.as_k, x8, xm, xk)
+             self.embed_m, self.embed_k, h, k_res, L0.as_m, L0.as_k, x8, xm, xk, self._err)
         pos = positions.contiguous().view(-1)
         for li, L in enumerate(self.layers):
             nxt = self.layers[li + 1] if li + 1 < self.n_layers else None
@@ -311,12 +341,57 @@ class IntQwen3:
         if not static:
             cache.length = S
         if head_rows is not None:
-            xh = x8.view(B, T, H)[torch.arange(B, device=dev), head_rows].contiguous()
-            logits = self._gemm(xh, self.head_w, (self.head_m,), split=False)[0][0]
+            sel = (torch.arange(B, device=dev), head_rows)
+            logits = self._lm_head(x8.view(B, T, H)[sel].contiguous(), xm.view(B, T)[sel],
+                                   xk.view(B, T)[sel])
             return logits, xm.view(B, T, 1), xk.view(B, T, 1), cache
-        logits = self._gemm(x8, self.head_w, (self.head_m,), split=False)[0][0].view(
-            B, T, self.vocab)
+        logits = self._lm_head(x8.view(B, T, H), xm.view(B, T, 1), xk.view(B, T, 1))
         return logits, xm.view(B, T, 1), xk.view(B, T, 1), cache
+
+    # -- seams (model.py:430-432, :469-478): override points for diagnostics --------
+    def _lm_head(self, x8: torch.Tensor, xm: torch.Tensor, xk: torch.Tensor) -> torch.Tensor:
+        """Seam: the LM head GEMM, x8 [..., H] int8 -> int32 [..., vocab]
+        (xm/xk unused on the integer path, model.py:430-432)."""
+        lead = x8.shape[:-1]
+        x2 = x8.reshape(-1, self.hidden).contiguous()
+        logits = self._gemm(x2, self.head_w, (self.head_m,), split=False)[0][0]
+        return logits.view(*lead, self.vocab)
+
+    def _attn_scores(self, q8, qm, qk, K8r, L, group, aux=None):
+        """Seam (model.py:469-474): int8 Q.K^T with the per-row dyadic score
+        scale. Called by prefill only when a subclass overrides a seam; the
+        default prefill runs the fused attention kernel, same bits."""
+        scores = int_gemm(q8, K8r.transpose(-1, -2).contiguous(), self.backend)
+        ks_m = L.ks_m.repeat_interleave(group).view(1, self.n_q, 1, 1)
+        ks_k = L.ks_k.repeat_interleave(group).view(1, self.n_q, 1, 1)
+        return (scores,) + dy.norm_scale(qm * ks_m, qk + ks_k)
+
+    def _attn_context(self, probs, V8r, L, aux=None):
+        """Seam (model.py:476-478): 15-bit probabilities x int8 V, exact
+        hi/lo split (backends.py:152-164)."""
+        return int_gemm_u16i8(probs, V8r, self.backend)
+
+    def _seams_overridden(self) -> bool:
+        cls = type(self)
+        return (cls._attn_scores is not IntQwen3._attn_scores
+                or cls._attn_context is not IntQwen3._attn_context)
+
+    def _qk_head_pipeline(self, P, row_m, row_k, w_m, w_k, gamma_m, gamma_k, n_heads,
+                          positions):
+        """model.py:200-216 on the op kernels: per-(token, head)
+        requant_i32_common(16), di_rmsnorm_gamma, permute, RoPE. P [B, T,
+        n_heads * hd] int32 -> (int64 [B, n_heads, T, hd], k). The fused
+        epilogue computes the same integers; this form feeds the seams'
+        diagnostics."""
+        B, T, _ = P.shape
+        Ph = P.view(B, T, n_heads, self.hd)
+        cm = w_m.view(n_heads, self.hd)
+        y, _, _ = dy.requant_i32_common(Ph, row_m.unsqueeze(-1), row_k.unsqueeze(-1), cm, w_k,
+                                        target_bits=16)
+        yn, k_out = ops.di_rmsnorm_gamma(y, gamma_m, gamma_k)
+        yn = yn.permute(0, 2, 1, 3)
+        pos = positions.view(B, 1, T).expand(B, n_heads, T)
+        return ops.apply_int_rope(yn, self.rope_cos, self.rope_sin, pos), k_out
 
     def _layer(self, L: LayerWeights, nxt, B, T, h, k_res, x8, xm, xk, pos, cache: KVCache,
                S_past, S, static):
@@ -335,7 +410,9 @@ class IntQwen3:
                  L.vq_m, L.vq_k, self.rope_cos, self.rope_sin, self.max_pos,
                  cache.k8[li], cache.v8[li], cache.cap, cache.len_idx if static else None,
                  0 if static else S_past, valid, cache.cap, S,
-                 cache.nslots if static else None, scratch, attn)
+                 cache.nslots if static else None, scratch, attn, self._err)
+        elif T > 1 and self._seams_overridden():
+            self._attention_seams(L, B, T, P, ns, st, xm, xk, pos, cache, S_past, S, attn)
         else:
             self._attention(L, B, T, P, ns, st, xm, xk, pos, cache, S_past, S, static, attn)
         self._after_attention(L, nxt, B, T, attn, h, k_res, x8, xm, xk)
@@ -359,15 +436,67 @@ class IntQwen3:
              L.k_norm_m, L.k_norm_k, L.qs_m, L.qs_k, L.kq_m, L.kq_k, L.ks_m, L.ks_k,
              L.vq_m, L.vq_k, self.rope_cos, self.rope_sin, self.max_pos, q8, tpos, None,
              cache.k8[li], cache.v8[li], cache.cap, cache.len_idx if static else None,
-             0 if static else S_past, L.kq_est)
+             0 if static else S_past, L.kq_est, self._err)
         valid = cache.valid_buf.view(torch.uint8)
         if T == 1:
             call("detllm_attn_decode", q8, tpos, cache.k8[li], cache.v8[li], valid, cache.cap,
                  B, S, nq, nkv, cache.cap, cache.nslots if static else None,
-                 self._decode_scratch(B, S), attn)
+                 self._decode_scratch(B, S), attn, self._err)
         else:
             call("detllm_attn_prefill", q8, tpos, cache.k8[li], cache.v8[li], valid, cache.cap,
                  B, T, S_past, nq, nkv, cache.cap, attn)
+
+    def _attention_seams(self, L, B, T, P, ns, st, xm, xk, pos, cache, S_past, S, attn):
+        """Prefill attention through the overridable seams, as the
+        reference's prefill branch runs it (model.py:382-402): K/V are
+        requantised into the cache by the fused epilogue (which also yields
+        q8 and its scale (qm, qk)); the scores come from _attn_scores, the
+        probabilities from di_softmax, the context from _attn_context, query
+        chunk by query chunk under the reference's memory budget. aux carries
+        the reference's diagnostics (model.py:385-386)."""
+        dev = self.device
+        nq, nkv, hd, li = self.n_q, self.n_kv, self.hd, L.idx
+        group = nq // nkv
+        q8 = torch.empty(B, nq, T, hd, dtype=torch.int8, device=dev)
+        tpos = torch.empty(B, nq, T, dtype=I64, device=dev)
+        dbg = torch.empty(B, nq, T, 4, dtype=I64, device=dev)
+        call("detllm_qkv_epilogue", P, ns, st, B, T, nq, nkv, xm, xk, pos,
+             L.q_m, L.q_k, L.k_m, L.k_k, L.v_m, L.v_k, L.q_norm_m, L.q_norm_k,
+             L.k_norm_m, L.k_norm_k, L.qs_m, L.qs_k, L.kq_m, L.kq_k, L.ks_m, L.ks_k,
+             L.vq_m, L.vq_k, self.rope_cos, self.rope_sin, self.max_pos, q8, tpos, dbg,
+             cache.k8[li], cache.v8[li], cache.cap, None, S_past, L.kq_est, self._err)
+        qm, qk = dbg[..., 0:1], dbg[..., 1:2]
+        Pfull = P.view(ns, B, T, -1).sum(dim=0, dtype=torch.int32) if ns > 1 else \
+            P.view(B, T, -1)
+        nqc, nkc = nq * hd, nkv * hd
+        Pq, Pk, Pv = Pfull[..., :nqc], Pfull[..., nqc:nqc + nkc], Pfull[..., nqc + nkc:]
+        xm3, xk3 = xm.view(B, T, 1), xk.view(B, T, 1)
+        positions = pos.view(B, T)
+        q, qkk = self._qk_head_pipeline(Pq.contiguous(), xm3, xk3, L.q_m, L.q_k, L.q_norm_m,
+                                        L.q_norm_k, nq, positions)
+        kk, kkk = self._qk_head_pipeline(Pk.contiguous(), xm3, xk3, L.k_m, L.k_k, L.k_norm_m,
+                                         L.k_norm_k, nkv, positions)
+        aux = {"li": li, "q": q, "qkk": qkk, "kk": kk, "kkk": kkk, "Pv": Pv.contiguous(),
+               "xm": xm3, "xk": xk3, "L": L}
+        K8 = cache.k8[li][:, :, :S]
+        V8 = cache.v8[li][..., :S].transpose(-1, -2)
+        K8r = K8.repeat_interleave(group, dim=1).contiguous()
+        V8r = V8.repeat_interleave(group, dim=1).contiguous()
+        slot = torch.arange(S, device=dev)
+        causal = slot[None, :] <= (S_past + torch.arange(T, device=dev))[:, None]
+        mask = cache.valid_buf[:, None, None, :S] & causal[None, None]
+        budget = max(1, (1 << 27) // max(1, B * nq * S))
+        CH = T if T <= budget else max(128, budget)
+        parts = []
+        for qlo in range(0, T, CH):
+            qhi = min(qlo + CH, T)
+            scores, sm, sk = self._attn_scores(q8[:, :, qlo:qhi], qm[:, :, qlo:qhi],
+                                               qk[:, :, qlo:qhi], K8r, L, group, aux)
+            probs = ops.di_softmax(scores, sm, sk,
+                                   mask[:, :, qlo:qhi].expand(B, nq, qhi - qlo, S))
+            parts.append(self._attn_context(probs, V8r, L, aux))
+        a = torch.cat(parts, dim=2) if len(parts) > 1 else parts[0]
+        attn.copy_(a.permute(0, 2, 1, 3).reshape(B * T, nq * hd))
 
     def _after_attention(self, L, nxt, B, T, attn, h, k_res, x8, xm, xk):
         dev = self.device
@@ -416,8 +545,15 @@ class IntQwen3:
         """Greedy generation; ids int64 [B, T0] right-padded (pads False in
         chunk_valid). Returns (tokens [B, max_new], step_logits list of [B, V])."""
         dev = self.device
-        ids = ids.to(dev)
         B, T0 = ids.shape
+        # the last decode step runs at position <= T0 + max_new - 2; the
+        # reference's cos_t[positions] raises IndexError there, so refuse up
+        # front rather than after max_pos steps
+        if T0 + max_new - 1 > self.max_pos:
+            raise IndexError(f"prompt of {T0} tokens + {max_new} new tokens reaches position "
+                             f"{T0 + max_new - 2}, outside the RoPE tables (size {self.max_pos})")
+        self._check_host_indices(ids, torch.zeros(1, dtype=I64))
+        ids = ids.to(dev)
         if chunk_valid is None:
             chunk_valid = torch.ones(B, T0, dtype=torch.bool, device=dev)
         chunk_valid = chunk_valid.to(dev)
@@ -440,6 +576,7 @@ class IntQwen3:
                 step_logits.append(lg)
                 cur = self.greedy_pick(lg)
                 out.append(cur)
+            self.raise_if_device_error()
             return torch.stack(out, dim=1), step_logits
         ones = torch.ones(B, 1, dtype=torch.bool, device=dev)
         for step in range(1, max_new):
@@ -448,4 +585,5 @@ class IntQwen3:
             step_logits.append(lg[:, 0])
             cur = self.greedy_pick(lg[:, 0])
             out.append(cur)
+        self.raise_if_device_error()
         return torch.stack(out, dim=1), step_logits

@@ -6,7 +6,7 @@ from __future__ import annotations
 
 import torch
 
-from ._lib import call
+from ._lib import call, raise_for_error_word
 from .dyadic import _dev, _rows
 
 I64 = torch.int64
@@ -90,8 +90,11 @@ def apply_int_rope(x: torch.Tensor, cos_t: torch.Tensor, sin_t: torch.Tensor,
     rows = x2.shape[0]
     pos = positions.to(device=x.device, dtype=I64).broadcast_to(x.shape[:-1]).contiguous()
     y = torch.empty(x.shape, dtype=I64, device=x.device)
+    err = torch.zeros(1, dtype=torch.int32, device=x.device)
     call("detllm_op_rope", x2, pos, cos_t.contiguous(), sin_t.contiguous(), cos_t.shape[0],
-         rows, y)
+         rows, y, err)
+    if not torch.cuda.is_current_stream_capturing():
+        raise_for_error_word(err.item(), max_pos=cos_t.shape[0])   # as cos_t[positions] raises
     return y
 
 

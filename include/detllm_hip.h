@@ -10,10 +10,21 @@
  *   - work is enqueued on the given hipStream_t;
  *   - return 0 on success, > 0 = hipError_t of a failed launch,
  *     < 0 = argument error (-22 EINVAL, -34 ERANGE, -38 ENOSYS).
- *   - all arithmetic is integer and bit-identical to the reference CPU
+ *   - every result is an integer bit-identical to the reference CPU
  *     ("reference") backend: int64 wraps, torch shift clamping, floor
  *     division, round_half_away_div / rshift_round rounding
- *     (src/detllm/intmath.py:7-17).
+ *     (src/detllm/intmath.py:7-17). Inputs, outputs and stored state are
+ *     integers; inside some kernels a quotient is obtained as the truncation
+ *     of a biased fp64 (or fp32) estimate that provably equals the exact
+ *     integer under operand bounds each kernel checks, else the integer
+ *     routine runs (csrc/intops.h states each bound; the library refuses to
+ *     build under -ffast-math);
+ *   - err (where present, nullable) is a device int32 word: an index the
+ *     reference would reject with IndexError sets bit 1 (token id outside
+ *     [-vocab, vocab)), bit 2 (position outside [-max_pos, max_pos)), and a
+ *     device slot count above a launch's slot bound bit 4; the kernel then
+ *     reads row 0 / scans the bounded slots, and the host raises from the
+ *     word at its next check (negative indices wrap as in torch).
  *
  * Reference interfaces each entry replaces are cited as file:line in
  * rishabh135/idempotent_llm. The reference has no FFI: its boundary is the
@@ -73,18 +84,24 @@ int detllm_transpose_i8(const int8_t* src, int8_t* dst, int R, int C, int batch,
 int detllm_greedy_pick(const int32_t* logits, const int64_t* head_m, int R, int V, int chunk,
                        int64_t* pv, int64_t* pi, int64_t* out, hipStream_t s);
 
+/* Compact digest of logits rows for the determinism harness (scripts/demo.py:
+ * 58-75 hashes whole rows on the host; this 64-bit digest lets rows be
+ * compared on the device): out[r] = sum over v of splitmix64_mix((v << 32) |
+ * (uint32) logits[r][v]) modulo 2^64, as int64. */
+int detllm_logits_digest(const int32_t* logits, int R, int V, int64_t* out, hipStream_t s);
+
 /* ------------------------------------------------- fused layer kernels -- */
 
 /* Embedding lookup + residual_from_delta + _norm_quant —
  * model.py:246-249 (dyadic.py:187-190, :174-184) fused with model.py:187-198
  * for the first layer's attention input (sm_m = as_m of layer 0; null skips
  * the smoothing multiply; x8 null skips the norm-quant). h [R][C] int32,
- * k_res/xm/xk [R] int64, x8 [R][C] int8. Ids outside [0, vocab) are clamped
- * (the reference raises IndexError; a device kernel cannot). */
+ * k_res/xm/xk [R] int64, x8 [R][C] int8. Ids index as embed_e8[ids] does
+ * (negative ids wrap); an id outside [-vocab, vocab) sets bit 1 of *err. */
 int detllm_embed_normq(const int64_t* ids, int R, int C, int64_t vocab, const int8_t* e8,
                        const int64_t* em, const int64_t* ek, int32_t* h, int64_t* k_res,
                        const int64_t* sm_m, int64_t sm_k, int8_t* x8, int64_t* xm, int64_t* xk,
-                       hipStream_t s);
+                       int32_t* err, hipStream_t s);
 
 /* requant_i32_common(P, row_m, row_k, col_m, col_k, tb) + residual_add +
  * _norm_quant(sm_m, sm_k) — model.py:410-415 / :424-427, :303, :284
@@ -124,7 +141,9 @@ int detllm_merge_rowcol(const int64_t* attn, int nsplit, int64_t split_stride, i
  * Outputs: q8 [B][n_q][T][128], tpos [B][n_q][T]; optional dbg
  * [B][n_q][T][4] = (qm, qk, sm, sk); K into kcache [B][n_kv][cap][128] and
  * V into vcache [B][n_kv][128][cap] (transposed) at slot base + t, where base
- * is *slot_base_dev when non-null (graph replay) else slot_base. */
+ * is *slot_base_dev when non-null (graph replay) else slot_base. Positions
+ * index the RoPE tables as cos_t[positions] does; one outside
+ * [-max_pos, max_pos) sets bit 2 of *err. */
 int detllm_qkv_epilogue(const int32_t* P, int nsplit, int64_t split_stride, int B, int T,
                         int n_q, int n_kv, const int64_t* xm, const int64_t* xk,
                         const int64_t* positions, const int64_t* q_m, int64_t q_k,
@@ -136,7 +155,7 @@ int detllm_qkv_epilogue(const int32_t* P, int nsplit, int64_t split_stride, int 
                         const int16_t* cos_t, const int16_t* sin_t, int64_t max_pos,
                         int8_t* q8, int64_t* tpos, int64_t* dbg, int8_t* kcache,
                         int8_t* vcache, int64_t cap, const int64_t* slot_base_dev,
-                        int64_t slot_base, const int64_t* kq_est, hipStream_t s);
+                        int64_t slot_base, const int64_t* kq_est, int32_t* err, hipStream_t s);
 
 /* The static K requantisation's per-channel divisors for one layer
  * (requant_i8_static of model.py:326-329 with row scale (1, rowk), rowk =
@@ -164,11 +183,11 @@ int detllm_attn_prefill(const int8_t* q8, const int64_t* tpos, const int8_t* kca
  * Triton kernel ops/fused_attn.py:47-142 it replaces. Scans S <= 131071 slots
  * (further bounded by *s_dev when non-null); scratch [B][n_q][ceil16(S)]
  * int32 is required only when n_q/n_kv * ceil16(S) * 4 > 48 KiB.
- * out [B][n_q*128]. */
+ * out [B][n_q*128]. *s_dev above S sets bit 4 of *err. */
 int detllm_attn_decode(const int8_t* q8, const int64_t* tpos, const int8_t* kcache,
                        const int8_t* vcache, const uint8_t* valid, int64_t valid_stride, int B,
                        int S, int n_q, int n_kv, int64_t cap, const int64_t* s_dev,
-                       int32_t* scratch, int64_t* out, hipStream_t s);
+                       int32_t* scratch, int64_t* out, int32_t* err, hipStream_t s);
 
 /* Per-step bookkeeping of the graph-captured decode (src/detllm/graphed.py:
  * 112-131: the validity flag of the step's slot, the device scalars holding
@@ -185,8 +204,8 @@ int detllm_decode_prologue(uint8_t* valid, int64_t valid_stride, int B, int64_t 
  * model.py:200-216, :303-358 — followed by detllm_attn_decode — model.py:347-381
  * and ops/fused_attn.py:47-142 — in one launch. Arguments as in those two
  * entry points (P [nsplit][B][(n_q + 2 n_kv) * 128]; the step's slot is
- * *slot_base_dev or slot_base; S slots are scanned, bounded by *s_dev when
- * non-null). out [B][n_q * 128] int64. */
+ * *slot_base_dev or slot_base; S <= 131071 slots are scanned, bounded by
+ * *s_dev when non-null). out [B][n_q * 128] int64. err as in both. */
 int detllm_qkv_attn_decode(const int32_t* P, int nsplit, int64_t split_stride, int B, int n_q,
                            int n_kv, const int64_t* xm, const int64_t* xk,
                            const int64_t* positions, const int64_t* q_m, int64_t q_k,
@@ -199,7 +218,7 @@ int detllm_qkv_attn_decode(const int32_t* P, int nsplit, int64_t split_stride, i
                            int8_t* kcache, int8_t* vcache, int64_t cap,
                            const int64_t* slot_base_dev, int64_t slot_base,
                            const uint8_t* valid, int64_t valid_stride, int S,
-                           const int64_t* s_dev, int32_t* scratch, int64_t* out,
+                           const int64_t* s_dev, int32_t* scratch, int64_t* out, int32_t* err,
                            hipStream_t s);
 
 /* ------------------------------------------- operator-level entry points -- */
@@ -250,10 +269,11 @@ int detllm_op_swiglu(const int64_t* gate, const int64_t* gm, const int64_t* gk,
                      const int64_t* up, const int64_t* um, const int64_t* uk, int R, int C,
                      int64_t* y, int64_t* ym, int64_t* yk, hipStream_t s);
 
-/* ops.apply_int_rope — src/detllm/ops/rope.py:38-55 (head_dim 128) */
+/* ops.apply_int_rope — src/detllm/ops/rope.py:38-55 (head_dim 128); a
+ * position outside [-max_pos, max_pos) sets bit 2 of *err */
 int detllm_op_rope(const int64_t* x, const int64_t* pos, const int16_t* cos_t,
                    const int16_t* sin_t, int64_t max_pos, int64_t rows, int64_t* y,
-                   hipStream_t s);
+                   int32_t* err, hipStream_t s);
 
 /* Elementwise primitives: op 0 isqrt (intmath.py:180-202, int_prims.py:31-44),
  * 1 ilog2_floor (intmath.py:164-177, int_prims.py:47-55), 2 norm_scale
@@ -262,7 +282,14 @@ int detllm_op_rope(const int64_t* x, const int64_t* pos, const int16_t* cos_t,
  * use for the same functions: 5 fit_dyadic_ratio(a, 127) (constant-divisor
  * path), 6 isqrt by the wave-parallel search, 7 the SwiGLU sigmoid division
  * round_half_away_div(a << 7, b) (ops/di_swiglu.py:52-55) in the fused
- * kernels' single-precision form, for 0 <= a <= b < 2^24. */
+ * kernels' single-precision form, for 0 <= a <= b < 2^24; and the fp64
+ * estimate forms, each valid under the bound intops.h states for it:
+ * 8 rhad(a c, b) for a >= 0 (rhad_est), 9 its signed form (rhad_est_signed),
+ * 10 clamp_i8(rhad(a, b)) (rhad_est_i8), 11 sign(a) rhad(|a| c, b) with the
+ * remainder step (rhad_est_corr_signed), 12 DI-Exp of -a with tpos b
+ * (dexp_est, ops/di_exp.py:27-37), 13 the same from a = t - n with t = b
+ * (dexp_est_sp), 14 the DI-Exp constant of (m, k) = (a, b) (di_exp_tpos_fast,
+ * model.py:355-358), 15 isqrt(a) (isqrt_est). */
 int detllm_op_scalar(int op, const int64_t* a, const int64_t* b, const int64_t* c, int64_t n,
                      int64_t* o1, int64_t* o2, hipStream_t s);
 

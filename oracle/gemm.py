@@ -5,7 +5,7 @@ int8 x int8 -> int32 product-sum. The oracle evaluates it with a float64
 BLAS matmul, which is exact here: every partial sum is an integer of
 magnitude <= K * 128 * 128 < 2^53 (asserted), so any summation order gives
 the same integer. Pinned: naive-loop brute force (the reference's
-tests/test_ops.py:52-61 restated) in tests/test_oracle_gemm.py.
+tests/test_ops.py:52-61 restated) in tests/test_oracle_model.py.
 
 ``int_gemm_u8i8`` / ``int_gemm_u16i8`` follow backends.py:138-164; both are
 exact identities, pinned against the plain int64 product (test_ops.py:63-78).
@@ -54,11 +54,13 @@ def int_gemm(a: np.ndarray, b: np.ndarray) -> np.ndarray:
 
 
 def int_gemm_u8i8(p_u8: np.ndarray, b: np.ndarray) -> np.ndarray:
-    """backends.py:138-149 — (p-64)@b + 64*colsum(b) for p in [0, 128]."""
+    """backends.py:138-149 — (p-64)@b + 64*colsum(b) for p in [0, 128];
+    int64, as the reference's int32 column sum promotes (torch sum of int32
+    gives int64)."""
     shifted = (p_u8.astype(I64) - 64).astype(np.int8)
     core = int_gemm(shifted, b)
-    corr = b.astype(I32).sum(axis=-2, keepdims=True, dtype=I32) * 64
-    return (core + corr).astype(I32)
+    corr = b.astype(I64).sum(axis=-2, keepdims=True) * 64
+    return core.astype(I64) + corr
 
 
 def int_gemm_u16i8(p_u16: np.ndarray, b: np.ndarray) -> np.ndarray:

@@ -71,14 +71,14 @@ def _run(dims, B, cap, S, slot, device_bounds, seed):
     tpos = torch.empty(B, nq, 1, dtype=I64, device="cuda")
     out_a = torch.empty(B, nq * hd, dtype=I64, device="cuda")
     call("detllm_qkv_epilogue", P, ns, B * P.shape[2], B, 1, nq, nkv, xm, xk, pos, *common,
-         q8, tpos, None, ka, va, cap, slot_dev, slot, None)
+         q8, tpos, None, ka, va, cap, slot_dev, slot, None, None)
     call("detllm_attn_decode", q8, tpos, ka, va, vbytes, cap, B, S_host, nq, nkv, cap, s_dev,
-         scratch, out_a)
+         scratch, out_a, None)
     # fused launch
     kb, vb = k0.clone(), v0.clone()
     out_b = torch.empty(B, nq * hd, dtype=I64, device="cuda")
     call("detllm_qkv_attn_decode", P, ns, B * P.shape[2], B, nq, nkv, xm, xk, pos, *common,
-         kb, vb, cap, slot_dev, slot, vbytes, cap, S_host, s_dev, scratch, out_b)
+         kb, vb, cap, slot_dev, slot, vbytes, cap, S_host, s_dev, scratch, out_b, None)
     torch.cuda.synchronize()
     assert torch.equal(ka, kb)
     assert torch.equal(va, vb)
@@ -230,7 +230,7 @@ def test_decode_attention_vs_oracle(name):
                if G * Spad * 4 > 48 * 1024 else None)
     out = torch.full((B, n_q * 128), -7, dtype=I64, device="cuda")
     call("detllm_attn_decode", d(q8[:, :, 0]), d(tpos[:, :, 0, 0]), d(kc), d(vc),
-         d(valid.astype(np.uint8)), cap, B, S, n_q, n_kv, cap, None, scratch, out)
+         d(valid.astype(np.uint8)), cap, B, S, n_q, n_kv, cap, None, scratch, out, None)
     got = out.cpu().numpy()
     bad = np.argwhere(got != want)
     assert bad.size == 0, f"{len(bad)} mismatches, first at {bad[0].tolist()}"
@@ -266,7 +266,7 @@ def test_prefill_epilogue_kq_estimates(T):
         kc = torch.zeros(B, nkv, cap, hd, dtype=torch.int8, device="cuda")
         vc = torch.zeros(B, nkv, hd, cap, dtype=torch.int8, device="cuda")
         call("detllm_qkv_epilogue", P, 1, B * T * P.shape[2], B, T, nq, nkv, xm, xk, pos,
-             *common, q8, tpos, None, kc, vc, cap, None, 0, e)
+             *common, q8, tpos, None, kc, vc, cap, None, 0, e, None)
         outs.append((q8, tpos, kc, vc))
     torch.cuda.synchronize()
     for a, b in zip(*outs):

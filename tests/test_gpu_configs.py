@@ -203,18 +203,39 @@ def full_model(tmp_path_factory):
     return d, IntQwen3(d, backend="rocm")
 
 
-def test_c3_full_model_b1_vs_oracle(full_model):
-    """64-token prompt (seed 30), prefill + 5 greedy decode steps of the full
-    28-layer model: tokens and demo chain hashes equal the CPU oracle's."""
-    from idempotent_llm_amd.hashchain import chain_hashes
-    from oracle.model import IntQwen3Oracle
+def _c3_fixture():
+    import json
+    import os
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "c3_chains.json")
+    with open(path) as f:
+        return json.load(f)
+
+
+@pytest.mark.parametrize("config", ["b1", "b8", "split"])
+def test_c3_every_step_vs_oracle_fixture(full_model, config):
+    """Config c3 as configured: 64-token prompt (seed 30), 512 greedy steps
+    (prefill + 511 graphed decodes) at batch 1, batch 8 (every row) and split
+    prefill, run by the determinism harness (scripts/demo.py:101-164). The
+    tokens and the demo chain hashes of every step of every row equal the
+    CPU oracle's (tests/golden/c3_chains.json, make_c3_fixture.py)."""
+    from idempotent_llm_amd.demo import run_int8
     d, m = full_model
-    print("[c3 full model vs oracle]", flush=True)
-    ids = art.prompt_ids(30, 64, art.QWEN3_0_6B["vocab"])
-    toks, lg = m.generate(torch.from_numpy(ids)[None].cuda(), 6, use_graph=True)
-    o_toks, o_lg = IntQwen3Oracle(d).generate(ids[None], 6)
-    assert toks.cpu().numpy().tolist() == o_toks.tolist()
-    assert chain_hashes(lg) == chain_hashes(o_lg)
+    fx = _c3_fixture()
+    assert art.artifact_digest(d) == fx["artifact_sha256"], "artifact generator drifted"
+    V = art.QWEN3_0_6B["vocab"]
+    prompt = art.prompt_ids(fx["prompt_seed"], fx["prompt_len"], V)
+    co = art.co_prompts(fx["co_prompt_seed"], 7, V)
+    steps = fx["steps"]
+    print(f"[c3 {config}: {steps} steps vs oracle fixture]", flush=True)
+    tcs, lcs = run_int8(m, f"int8-rocm-{config}", steps, prompt, co, all_rows=True)
+    want = fx[config] if config == "b8" else [fx[config]]
+    assert len(tcs) == len(want)
+    for r, (tc, lc, w) in enumerate(zip(tcs, lcs, want)):
+        first_bad = next((i for i, (a, b) in enumerate(zip(lc.steps, w["logit_chain"]))
+                          if a != b), None)
+        assert first_bad is None, f"row {r}: logits diverge from the oracle at step {first_bad}"
+        assert tc.steps == w["token_chain"], f"row {r}: tokens"
+        assert len(lc.steps) == steps
 
 
 def test_c3_batch8_row0_equals_batch1_512_steps(full_model):

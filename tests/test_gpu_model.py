@@ -159,3 +159,174 @@ def test_step_greedy_matches_step_then_pick(case):
         runs.append((torch.stack(toks), torch.stack(lgs)))
     assert torch.equal(runs[0][0], runs[1][0])
     assert torch.equal(runs[0][1], runs[1][1])
+
+
+@pytest.mark.parametrize("chunk", [2048, 64, 1, 5000])
+def test_greedy_pick_real_ties_on_device(chunk):
+    """detllm_greedy_pick (the pick of IntQwen3.greedy_pick and of the graphed
+    step) on rows with real ties inside and across arg-max chunks, with the
+    chunk size varied so the cross-chunk combine sees 1 to 5000 partials:
+    the lowest id among the maxima, as brute force in Python integers."""
+    if not torch.cuda.is_available():
+        pytest.skip("needs a GPU")
+    from idempotent_llm_amd._lib import call
+    from tiecases import EXPECTED, brute_pick, tie_cases
+    print(f"[greedy ties chunk={chunk}]", flush=True)
+    rows, hm = tie_cases()
+    assert brute_pick(rows, hm) == EXPECTED
+    R, V = rows.shape
+    nch = -(-V // chunk)
+    pv = torch.empty(R, nch, dtype=I64, device="cuda")
+    pi = torch.empty(R, nch, dtype=I64, device="cuda")
+    out = torch.full((R,), -1, dtype=I64, device="cuda")
+    call("detllm_greedy_pick", torch.from_numpy(rows).cuda(), torch.from_numpy(hm).cuda(),
+         R, V, chunk, pv, pi, out)
+    assert out.tolist() == EXPECTED
+
+
+# ---------------------------------------------------------------- index errors
+
+def test_out_of_range_indices_raise_like_the_reference(case):
+    """embed_e8[ids] and cos_t[positions] raise IndexError in the reference
+    (model.py:244-246, ops/rope.py:48-49); negative indices wrap as torch's
+    indexing does."""
+    rec, m, _ = case
+    V, P = rec["dims"]["vocab"], rec["dims"]["max_pos"]
+    ids = _ids(rec)[None]
+    T = ids.shape[1]
+    pos = torch.arange(T, device="cuda")[None]
+    # host tensors: checked before the launch
+    with pytest.raises(IndexError):
+        m.forward(torch.tensor([[V]]), torch.tensor([[0]]))
+    with pytest.raises(IndexError):
+        m.forward(torch.tensor([[1]]), torch.tensor([[P]]))
+    with pytest.raises(IndexError):
+        m.generate(ids, P)                 # runs past the RoPE table
+    # device tensors: flagged by the kernels, raised at the next check
+    bad = ids.clone()
+    bad[0, 3] = V + 5
+    m.forward(bad, pos)
+    with pytest.raises(IndexError, match="token id"):
+        m.raise_if_device_error()
+    m.forward(ids, pos + P)
+    with pytest.raises(IndexError, match="position"):
+        m.raise_if_device_error()
+    m.raise_if_device_error()              # the word was cleared
+    # negative ids and positions wrap (torch semantics)
+    wrapped = ids.clone()
+    wrapped[0, 2] = ids[0, 2] - V
+    a, _, _, _ = m.forward(ids, pos)
+    b, _, _, _ = m.forward(wrapped, pos)
+    m.raise_if_device_error()
+    assert torch.equal(a, b)
+
+
+# ---------------------------------------------------------------- seams
+
+def test_seams_are_honoured(case):
+    """_attn_scores / _attn_context / _lm_head (model.py:430-432, :469-478)
+    are override points: a subclass that calls the defaults gets the fused
+    path's bits through the unfused seam path, and an override that changes
+    the result changes the logits."""
+    from idempotent_llm_amd.model import IntQwen3
+    rec, m, d = case
+    calls = []
+
+    class Spy(IntQwen3):
+        def _attn_scores(self, q8, qm, qk, K8r, L, group, aux=None):
+            calls.append(("scores", aux["li"], tuple(q8.shape)))
+            assert aux["q"].dtype == torch.int64 and aux["kk"].dtype == torch.int64
+            return super()._attn_scores(q8, qm, qk, K8r, L, group, aux)
+
+        def _attn_context(self, probs, V8r, L, aux=None):
+            calls.append(("context", aux["li"]))
+            return super()._attn_context(probs, V8r, L, aux)
+
+    spy = Spy(d, backend="rocm")
+    ids = _ids(rec)[None]
+    pos = torch.arange(ids.shape[1], device="cuda")[None]
+    want, _, _, _ = m.forward(ids, pos)
+    got, _, _, _ = spy.forward(ids, pos)
+    assert torch.equal(got, want)
+    n_layers = rec["dims"]["n_layers"]
+    assert [c[1] for c in calls if c[0] == "scores"] == list(range(n_layers))
+    assert chain_hashes(got[0]) == rec["prefill_chain"]
+
+    class ZeroHead(IntQwen3):
+        def _lm_head(self, x8, xm, xk):
+            return torch.zeros(*x8.shape[:-1], self.vocab, dtype=torch.int32, device=x8.device)
+
+    z, _, _, _ = ZeroHead(d, backend="rocm").forward(ids, pos)
+    assert int(z.abs().max()) == 0
+
+
+def test_qk_head_pipeline_matches_fused_q8(case):
+    """The op-kernel _qk_head_pipeline (model.py:200-216) feeding the seams'
+    diagnostics gives, after QK smoothing and quant_i8_pertoken
+    (model.py:317-323), the q8 the fused epilogue produced."""
+    from idempotent_llm_amd import dyadic as dy
+    from idempotent_llm_amd.model import IntQwen3
+    rec, m, d = case
+    seen = {}
+
+    class Grab(IntQwen3):
+        def _attn_scores(self, q8, qm, qk, K8r, L, group, aux=None):
+            if aux["li"] == 0:
+                seen.update(q8=q8.clone(), qm=qm.clone(), qk=qk.clone(), q=aux["q"],
+                            qkk=aux["qkk"], L=L, group=group)
+            return super()._attn_scores(q8, qm, qk, K8r, L, group, aux)
+
+    g = Grab(d, backend="rocm")
+    ids = _ids(rec)[None]
+    g.forward(ids, torch.arange(ids.shape[1], device="cuda")[None])
+    L, grp = seen["L"], seen["group"]
+    qs = L.qs_m.view(g.n_kv, g.hd).repeat_interleave(grp, dim=0)
+    q = seen["q"] * qs[None, :, None, :]
+    one = torch.ones(*q.shape[:-1], 1, dtype=I64, device="cuda")
+    q8, qm, qk = dy.quant_i8_pertoken(q, one, one * 0 + seen["qkk"] + L.qs_k)
+    assert torch.equal(q8, seen["q8"])
+    assert torch.equal(qm, seen["qm"]) and torch.equal(qk, seen["qk"])
+
+
+def test_graphed_modes_and_signature(case):
+    """GraphedDecode(model, cache, lens, mode, layer_compile) (graphed.py:44-45):
+    mode "capture" and "layers" give the same tokens and logits."""
+    from idempotent_llm_amd.graphed import GraphedDecode
+    rec, m, _ = case
+    ids = _ids(rec)[None]
+    T = ids.shape[1]
+    pos = torch.arange(T, device="cuda")[None]
+    lens = torch.full((1,), T, dtype=I64, device="cuda")
+    runs = []
+    for mode in ("capture", "layers"):
+        lg, _, _, cache = m.forward(ids, pos)
+        gd = GraphedDecode(m, cache, lens, mode=mode, layer_compile=True)
+        cur = m.greedy_pick(lg[:, -1])
+        out = []
+        for _ in range(6):
+            lg1 = gd.step(cur).clone()
+            cur = m.greedy_pick(lg1)
+            out.append(lg1)
+        runs.append(torch.stack(out))
+    assert torch.equal(runs[0], runs[1])
+    with pytest.raises(ValueError):
+        GraphedDecode(m, m.forward(ids, pos)[3], lens, mode="bogus")
+
+
+def test_logits_digest_matches_host_formula(case):
+    """detllm_logits_digest against the same sum computed in Python."""
+    from idempotent_llm_amd.demo import logits_digest
+    rec, m, _ = case
+    rows = torch.tensor(np.stack([rec["prefill_last_row"], [0] * len(rec["prefill_last_row"])]),
+                        dtype=torch.int32, device="cuda")
+    got = logits_digest(rows).cpu().tolist()
+    M = (1 << 64) - 1
+
+    def mix(z):
+        z = ((z ^ (z >> 30)) * 0xBF58476D1CE4E5B9) & M
+        z = ((z ^ (z >> 27)) * 0x94D049BB133111EB) & M
+        return z ^ (z >> 31)
+
+    for r, g in zip(rows.cpu().numpy(), got):
+        want = sum(mix((i << 32) | (int(x) & 0xFFFFFFFF)) for i, x in enumerate(r)) & M
+        assert g & M == want

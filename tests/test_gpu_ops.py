@@ -261,10 +261,14 @@ def test_int_gemm_extremes_and_batched():
     eq(int_gemm(g(a), g(b), "rocm"), np.full((300, 200), 1024 * 128 * 128))
     p = rnd.integers(0, 129, (9, 21)).astype(np.int32)
     v = rnd.integers(-128, 128, (21, 6)).astype(np.int8)
-    eq(int_gemm_u8i8(g(p), g(v), "rocm"), p.astype(I64) @ v.astype(I64))
+    got = int_gemm_u8i8(g(p), g(v), "rocm")
+    assert got.dtype == torch.int64   # the reference's int32 colsum promotes
+    eq(got, p.astype(I64) @ v.astype(I64))
     p = rnd.integers(0, (1 << 14) + 1, (9, 300)).astype(np.int32)
     v = rnd.integers(-128, 128, (300, 6)).astype(np.int8)
-    eq(int_gemm_u16i8(g(p), g(v), "rocm"), ogemm.int_gemm_u16i8(p, v))
+    got = int_gemm_u16i8(g(p), g(v), "rocm")
+    assert got.dtype == torch.int64
+    eq(got, ogemm.int_gemm_u16i8(p, v))
 
 
 def test_config0_gemm_requant():

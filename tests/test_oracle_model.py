@@ -51,7 +51,9 @@ def test_u8_and_u16_tricks_exact():
     rng = np.random.default_rng(7)
     p = rng.integers(0, 129, (9, 21)).astype(np.int32)
     v = rng.integers(-128, 128, (21, 6)).astype(np.int8)
-    assert np.array_equal(gemm.int_gemm_u8i8(p, v), p.astype(I64) @ v.astype(I64))
+    got = gemm.int_gemm_u8i8(p, v)
+    assert got.dtype == I64   # backends.py:148-149: the int32 colsum promotes
+    assert np.array_equal(got, p.astype(I64) @ v.astype(I64))
     p = rng.integers(0, (1 << 14) + 1, (9, 300)).astype(np.int32)
     v = rng.integers(-128, 128, (300, 6)).astype(np.int8)
     got = gemm.int_gemm_u16i8(p, v)
@@ -124,3 +126,50 @@ def test_greedy_pick_ties(case):
     rec, m = case
     rows = np.array(rec["tie_rows"], dtype=np.int32)
     assert m.greedy_pick(rows).tolist() == rec["tie_picks"]
+
+
+def _ns_pick(head_m):
+    """The oracle's greedy_pick bound to a given head_m (model.py:482-490)."""
+    from types import SimpleNamespace
+    return lambda rows: IntQwen3Oracle.greedy_pick(
+        SimpleNamespace(head_m=head_m, vocab=head_m.shape[0]), rows)
+
+
+def test_greedy_pick_real_ties_vs_brute_force():
+    """Rows with real ties (inside a 2048-id chunk, across chunk boundaries,
+    many-way, all-zero, int32 extremes): the oracle's pick equals the lowest
+    id among the maxima computed in Python integers."""
+    from tiecases import EXPECTED, brute_pick, tie_cases
+    rows, hm = tie_cases()
+    prods = rows.astype(object) * hm.astype(object)
+    n_max = [(p == p.max()).sum() for p in prods]
+    assert sum(n > 1 for n in n_max) == len(EXPECTED) - 1   # every row but one ties
+    assert brute_pick(rows, hm) == EXPECTED
+    assert _ns_pick(hm)(rows).tolist() == EXPECTED
+
+
+def test_tie_rows_reject_a_flipped_tie_rule():
+    """A planted mistake in the oracle (highest id among the maxima, or the
+    first maximum of the last 2048-id chunk) fails on these rows."""
+    from tiecases import EXPECTED, tie_cases
+    rows, hm = tie_cases()
+    scaled = rows.astype(I64) * hm
+
+    def highest(s):
+        mx = s.max(axis=-1, keepdims=True)
+        return np.where(s == mx, np.arange(s.shape[1]), -1).max(axis=-1).tolist()
+
+    def chunk_last_wins(s, chunk=2048):
+        out = []
+        for row in s:
+            best_v, best_i = None, None
+            for c0 in range(0, row.shape[0], chunk):
+                seg = row[c0:c0 + chunk]
+                i = int(np.argmax(seg)) + c0
+                if best_v is None or row[i] >= best_v:   # ">=": later chunk wins ties
+                    best_v, best_i = row[i], i
+            out.append(best_i)
+        return out
+
+    assert highest(scaled) != EXPECTED
+    assert chunk_last_wins(scaled) != EXPECTED
