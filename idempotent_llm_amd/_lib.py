@@ -27,6 +27,7 @@ SIGNATURES = {
     "detllm_igemv_plan": [I, I, I, P],
     "detllm_transpose_i8": [P, P, I, I, I, L, L, S],
     "detllm_greedy_pick": [P, P, I, I, I, P, P, P, S],
+    "detllm_greedy_pick_noalloc": [P, P, I, I, P, S],
     "detllm_logits_digest": [P, I, I, P, S],
     "detllm_embed_normq": [P, I, I, L, P, P, P, P, P, P, L, P, P, P, P, S],
     "detllm_residual_normq": [P, I, L, I, I, P, P, P, L, I, P, P, P, L, P, P, P, S],

@@ -30,6 +30,8 @@
 //   k_argmax_*  — greedy_pick (model.py:482-490): argmax of logits * head_m
 //                 in int64 with the lowest-id tie-break.
 
+#include <mutex>
+
 #include "common.h"
 #include "gemv.h"
 
@@ -480,6 +482,35 @@ int igemv(const int8_t* A, const int8_t* B, int32_t* C, int M, int N, int K, int
 
 }  // namespace
 
+// Scratch of the allocation-free greedy pick: the per-chunk partial maxima
+// (values, then ids) of k_argmax_partial, NOALLOC_PARTIALS int64 each. A
+// file-scope device array: each GPU holds its own copy for the life of the
+// process. Host code reaches it only through the address hipGetSymbolAddress
+// returns for the current device (the array's name is not a device address
+// on the host).
+constexpr int NOALLOC_PARTIALS = 32768;
+static __device__ __align__(256) int64_t scratch[2 * NOALLOC_PARTIALS];
+
+namespace {
+constexpr int MAX_DEVICES = 64;
+std::mutex g_scratch_mu;
+int64_t* g_scratch_ptr[MAX_DEVICES] = {};
+
+// Address of this device's scratch, resolved once per device (with that
+// device current); nullptr when the lookup fails.
+int64_t* device_scratch() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAX_DEVICES) return nullptr;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* ptr = nullptr;
+    if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess || !ptr) return nullptr;
+    g_scratch_ptr[dev] = (int64_t*)ptr;
+  }
+  return g_scratch_ptr[dev];
+}
+}  // namespace
+
 extern "C" {
 
 // C[b] = A[b] . B[b]^T; A [batch][M][K], B [batch][N][K], C [batch][M][N]
@@ -569,6 +600,30 @@ int detllm_greedy_pick(const int32_t* logits, const int64_t* head_m, int R, int 
   if (R <= 0) return DI_OK;
   if (V <= 0 || chunk <= 0 || !logits || !head_m || !pv || !pi || !out) return DI_EINVAL;
   const int nch = (V + chunk - 1) / chunk;
+  hipLaunchKernelGGL(k_argmax_partial, dim3(nch, R), dim3(256), 0, s, logits, head_m, V, chunk,
+                     pv, pi);
+  DI_LAUNCH_CHECK();
+  hipLaunchKernelGGL(k_argmax_final, dim3(R), dim3(256), 0, s, pv, pi, nch, out);
+  DI_LAUNCH_CHECK();
+  return DI_OK;
+}
+
+// detllm_greedy_pick without caller scratch and without any allocation: the
+// partials live in the library's per-device `scratch` array (chunk 2048, so
+// R * ceil(V / 2048) <= NOALLOC_PARTIALS). Every partial slot a call reads
+// is written earlier in the same call, so nothing needs clearing; calls that
+// overlap on one GPU (different streams) share the array and race.
+int detllm_greedy_pick_noalloc(const int32_t* logits, const int64_t* head_m, int R, int V,
+                               int64_t* out, hipStream_t s) {
+  if (R <= 0) return DI_OK;
+  if (V <= 0 || !logits || !head_m || !out) return DI_EINVAL;
+  constexpr int chunk = 2048;
+  const int nch = (V + chunk - 1) / chunk;
+  if ((int64_t)R * nch > NOALLOC_PARTIALS) return DI_ERANGE;
+  int64_t* ptr = device_scratch();
+  if (!ptr) return (int)hipErrorInvalidSymbol;
+  int64_t* pv = ptr;
+  int64_t* pi = ptr + NOALLOC_PARTIALS;
   hipLaunchKernelGGL(k_argmax_partial, dim3(nch, R), dim3(256), 0, s, logits, head_m, V, chunk,
                      pv, pi);
   DI_LAUNCH_CHECK();

@@ -84,6 +84,18 @@ int detllm_transpose_i8(const int8_t* src, int8_t* dst, int R, int C, int batch,
 int detllm_greedy_pick(const int32_t* logits, const int64_t* head_m, int R, int V, int chunk,
                        int64_t* pv, int64_t* pi, int64_t* out, hipStream_t s);
 
+/* No counterpart in the reference: detllm_greedy_pick for callers that
+ * cannot allocate (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc). Same result as detllm_greedy_pick with
+ * chunk 2048; the partials live in the library's own per-device scratch
+ * array (2 x 32768 int64 = 512 KiB per GPU, held until the process ends), so
+ * R * ceil(V / 2048) <= 32768 or the call returns -34 (ERANGE). The first
+ * call on a device resolves that device's array address (do it outside
+ * capture). Calls that overlap on one GPU share the array and race; the
+ * caller orders them (one stream, or events). Allocates nothing. */
+int detllm_greedy_pick_noalloc(const int32_t* logits, const int64_t* head_m, int R, int V,
+                               int64_t* out, hipStream_t s);
+
 /* Compact digest of logits rows for the determinism harness (scripts/demo.py:
  * 58-75 hashes whole rows on the host; this 64-bit digest lets rows be
  * compared on the device): out[r] = sum over v of splitmix64_mix((v << 32) |
