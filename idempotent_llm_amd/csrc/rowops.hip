@@ -818,6 +818,40 @@ __global__ void k_op_static(const int64_t* P, const int64_t* row_m, const int64_
   }
 }
 
+// requant_i8_static of a GEMM's int32 output with per-row (row_m, row_k)
+// (null: (1, 0)), per-column col_m, scalar col_k and a scalar static target
+// (s_m, s_k) — dyadic.py:142-163; config c0's canonical epilogue is
+// (P, 1, 0, m, 20, 1, 0). P: nsplit int32 partials, summed in a fixed order.
+// One thread per 4 consecutive columns of a row.
+__global__ __launch_bounds__(256) void k_static_cols(const int32_t* __restrict__ P, int nsplit,
+                                                     i64 split_stride, int R, int C,
+                                                     const int64_t* row_m, const int64_t* row_k,
+                                                     const int64_t* __restrict__ col_m, i64 col_k,
+                                                     i64 s_m, i64 s_k, int8_t* __restrict__ y8) {
+  const int cq = (C + 3) / 4;
+  const i64 t = (i64)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= (i64)R * cq) return;
+  const int r = (int)(t / cq), c0 = (int)(t - (i64)r * cq) * 4;
+  const i64 rm = row_m ? row_m[r] : 1, rk = row_k ? row_k[r] : 0;
+  const i64 shift = wsub(wadd(rk, col_k), s_k);
+  const i64 up = imax(wneg(shift), 0), down = imax(shift, 0);
+  i64 den = shl(s_m, down);
+  if (den <= 0) den = 1;
+  const bool fast_den = den < ((i64)1 << 49);
+  const DivEst D = make_divest(fast_den ? den : 1, 1.0);
+  const i64 off = (i64)r * C + c0;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    if (c0 + j >= C) break;
+    uint32_t acc = 0;
+    for (int k = 0; k < nsplit; ++k) acc += (uint32_t)P[(i64)k * split_stride + off + j];
+    const i64 n = shl(wmul(wmul((i64)(int32_t)acc, col_m[c0 + j]), rm), up);
+    const i64 lim = (i64)1 << 49;  // 2 |n| + den < 2^51 for rhad_est_i8
+    y8[off + j] = (int8_t)((fast_den && n > -lim && n < lim) ? rhad_est_i8(n, D)
+                                                             : clamp_i8(rhad(n, den)));
+  }
+}
+
 // op: 0 isqrt, 1 ilog2, 2 norm_scale, 3 fit_dyadic_ratio, 4 scaled_round_div,
 // 5 fit_dyadic_ratio(a, 127) through the constant-127 path the kernels use
 // (6, the wave-parallel isqrt, runs in k_op_isqrt_wave)
@@ -1128,6 +1162,21 @@ int detllm_op_requant_i8_static(const int64_t* P, const int64_t* row_m, const in
   if (n <= 0) return DI_OK;
   hipLaunchKernelGGL(k_op_static, dim3(grid_for(n)), dim3(256), 0, s, P, row_m, row_k, col_m,
                      col_k, s_m, s_k, n, y8);
+  DI_LAUNCH_CHECK();
+  return DI_OK;
+}
+
+int detllm_requant_static_cols(const int32_t* P, int nsplit, int64_t split_stride, int R, int C,
+                               const int64_t* row_m, const int64_t* row_k, const int64_t* col_m,
+                               int64_t col_k, int64_t s_m, int64_t s_k, int8_t* y8,
+                               hipStream_t s) {
+  if (R <= 0 || C <= 0) return DI_OK;
+  if (nsplit < 1 || !P || !col_m || !y8) return DI_EINVAL;
+  const i64 threads = (i64)R * ((C + 3) / 4);
+  if ((threads + 255) / 256 > 0x7fffffff) return DI_ERANGE;
+  hipLaunchKernelGGL(k_static_cols, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s, P,
+                     nsplit, (i64)split_stride, R, C, row_m, row_k, col_m, (i64)col_k, (i64)s_m,
+                     (i64)s_k, y8);
   DI_LAUNCH_CHECK();
   return DI_OK;
 }

@@ -178,6 +178,16 @@ int detllm_qkv_epilogue(const int32_t* P, int nsplit, int64_t split_stride, int 
 int detllm_kq_est(const int64_t* kq_m, const int64_t* kq_k, int64_t n, int64_t rowk,
                   int64_t* est, hipStream_t s);
 
+/* requant_i8_static of a GEMM output — src/detllm/dyadic.py:142-163 with
+ * per-row (row_m, row_k) (null: (1, 0)), per-column col_m [C], scalar col_k
+ * and a scalar static target (s_m, s_k): y8 = clamp_i8(rhad(P col_m row_m
+ * << up, s_m << down)), shift = row_k + col_k - s_k. P: nsplit int32
+ * partials [nsplit][R][C]. Config c0's epilogue is (P, 1, 0, m, 20, 1, 0). */
+int detllm_requant_static_cols(const int32_t* P, int nsplit, int64_t split_stride, int R, int C,
+                               const int64_t* row_m, const int64_t* row_k, const int64_t* col_m,
+                               int64_t col_k, int64_t s_m, int64_t s_k, int8_t* y8,
+                               hipStream_t s);
+
 /* ------------------------------------------------------------ attention -- */
 
 /* Prefill/chunk attention — model.py:382-402 (_attn_scores :469-474,

@@ -287,6 +287,37 @@ def test_config0_gemm_requant():
     y8, mo, ko = dd.requant_i8_rowcol(P, 1, 0, g(m), 20)
     wy, wm, wk = ody.requant_i8_rowcol(Pw, np.ones((64, 1), I64), np.zeros((64, 1), I64), m, 20)
     eq(y8, wy); eq(mo, wm); eq(ko, wk)
+    # the bench's c0 path: skinny GEMM partials, then the fused static epilogue
+    from idempotent_llm_amd._lib import call, gemv_plan
+    from idempotent_llm_amd.backends import gemm_nt
+    ks = gemv_plan(64, 3072, 1024)
+    Pp = gemm_nt(g(A), g(W.T.copy()), ksplit=ks)
+    y8s = torch.empty(64, 3072, dtype=torch.int8, device="cuda")
+    call("detllm_requant_static_cols", Pp, ks, 64 * 3072, 64, 3072, None, None, g(m), 20, 1, 0,
+         y8s)
+    eq(y8s, ody.requant_i8_static(Pw, 1, 0, m, 20, 1, 0))
+
+
+@pytest.mark.parametrize("seed", [0, 1])
+def test_requant_static_cols_general(seed):
+    """detllm_requant_static_cols with per-row scales, up- and down-shifts
+    and numerators past the estimate's bound (the exact integer path),
+    against dyadic.py:142-163 restated in the oracle."""
+    from idempotent_llm_amd._lib import call
+    rnd = np.random.default_rng(40 + seed)
+    R, C, ks = 7, 301, 3
+    parts = rnd.integers(-(1 << 29), 1 << 29, (ks, R, C)).astype(np.int32)
+    Pw = parts.astype(I64).sum(axis=0)
+    Pw = ((Pw + (1 << 31)) % (1 << 32) - (1 << 31)).astype(np.int32)   # int32 wrap of the sum
+    row_m = rnd.integers(1, 1 << 16, (R, 1)).astype(I64)
+    row_k = rnd.integers(0, 30, (R, 1)).astype(I64)
+    col_m = rnd.integers(1 << 14, 1 << 16, (C,)).astype(I64)
+    for col_k, s_m, s_k in ((20, 1, 0), (5, 40000, 60), (24, (1 << 20) + 7, 3)):
+        want = ody.requant_i8_static(Pw, row_m, row_k, col_m, col_k, s_m, s_k)
+        y8 = torch.empty(R, C, dtype=torch.int8, device="cuda")
+        call("detllm_requant_static_cols", g(parts), ks, R * C, R, C, g(row_m[:, 0]),
+             g(row_k[:, 0]), g(col_m), col_k, s_m, s_k, y8)
+        eq(y8, want)
 
 
 def test_di_matmul_composition():
