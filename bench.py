@@ -450,14 +450,16 @@ def c2_bench():
     from idempotent_llm_amd._lib import call
     T = 2048
     dev = "cuda"
+    from idempotent_llm_amd.kvcache import pages_from_contiguous
     q8 = torch.randint(-127, 128, (1, 16, T, 128), dtype=torch.int8, device=dev)
     tpos = torch.full((1, 16, T), 1 << 12, dtype=torch.int64, device=dev)
     kc = torch.randint(-127, 128, (1, 8, T, 128), dtype=torch.int8, device=dev)
     vc = torch.randint(-127, 128, (1, 8, 128, T), dtype=torch.int8, device=dev)
+    kp, vp, table = pages_from_contiguous(kc, vc)
     valid = torch.ones(1, T, dtype=torch.uint8, device=dev)
     out = torch.empty(1, T, 16 * 128, dtype=torch.int64, device=dev)
-    us2 = _graph_time_us(lambda: call("detllm_attn_prefill", q8, tpos, kc, vc, valid, T, 1, T,
-                                      0, 16, 8, T, out), 10, 1)
+    us2 = _graph_time_us(lambda: call("detllm_attn_prefill", q8, tpos, kp, vp, table,
+                                      table.shape[1], valid, T, 1, T, 0, 16, 8, out), 10, 1)
     ops2 = 2.0 * 2 * 16 * (T * (T + 1) // 2) * 128
     return {"us": round(us2, 2), "tops": round(ops2 / (us2 * 1e-6) / 1e12, 1),
             "frac_mfma_peak": round(ops2 / (us2 * 1e-6) / 1e12 / I8_PEAK_TOPS, 4),

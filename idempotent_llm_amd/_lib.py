@@ -35,13 +35,13 @@ SIGNATURES = {
     "detllm_swiglu_quant": [P, I, L, I, I, P, P, P, L, P, L, P, L, P, P, P, S],
     "detllm_merge_rowcol": [P, I, L, I, I, P, L, P, L, P, P, P, S],
     "detllm_qkv_epilogue": [P, I, L, I, I, I, I, P, P, P, P, L, P, L, P, L, P, L, P, L, P, L,
-                            P, P, P, P, P, P, P, P, L, P, P, P, P, P, L, P, L, P, P, S],
+                            P, P, P, P, P, P, P, P, L, P, P, P, P, P, P, I, P, L, P, P, S],
     "detllm_kq_est": [P, P, L, L, P, S],
     "detllm_requant_static_cols": [P, I, L, I, I, P, P, P, L, L, L, P, S],
-    "detllm_attn_prefill": [P, P, P, P, P, L, I, I, I, I, I, L, P, S],
-    "detllm_attn_decode": [P, P, P, P, P, L, I, I, I, I, L, P, P, P, P, S],
+    "detllm_attn_prefill": [P, P, P, P, P, I, P, L, I, I, I, I, I, P, S],
+    "detllm_attn_decode": [P, P, P, P, P, I, P, L, I, I, I, I, P, P, P, P, S],
     "detllm_qkv_attn_decode": [P, I, L, I, I, I, P, P, P, P, L, P, L, P, L, P, L, P, L, P, L,
-                               P, P, P, P, P, P, P, P, L, P, P, L, P, L, P, L, I, P, P, P, P, S],
+                               P, P, P, P, P, P, P, P, L, P, P, P, I, P, L, P, L, I, P, P, P, P, S],
     "detllm_decode_prologue": [P, L, I, L, P, P, P, P, L, S],
     "detllm_op_quant_i8_pertoken": [P, P, P, I, I, P, P, P, S],
     "detllm_op_requant_i32_common": [P, P, P, I, L, I, I, I, P, P, S],

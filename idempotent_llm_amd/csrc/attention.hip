@@ -9,10 +9,12 @@
 // query at absolute slot S_past + t iff s <= S_past + t and valid[b][s]
 // (model.py:259-266).
 //
-// Cache layout in HBM: K [B][n_kv][cap][128] (row per slot) and V stored
-// transposed, V^T [B][n_kv][128][cap], so that both the MFMA B-fragments of
-// P.V (16 consecutive slots per lane) and the decode reduction over slots
-// read slot-contiguous bytes. cap % 16 == 0.
+// Cache layout in HBM: paged (common.h KVPages). A row's slots map through
+// its page table to pages of DI_PAGE = 128 slots; a page holds K rows
+// [n_kv][128 slots][128] and V transposed [n_kv][128 channels][128 slots], so
+// both the MFMA B-fragments of P.V (16 consecutive slots per lane) and the
+// decode reduction over slots read slot-contiguous bytes. A prefill key tile
+// is exactly one page.
 //
 // Prefill (k_attn_prefill): block = 64 queries of one head, 4 waves of 16.
 // Scores are computed transposed, S^T = K . Q^T, with v_mfma_i32_16x16x64_i8:
@@ -46,12 +48,11 @@ __device__ __forceinline__ v4i mfma16(v4i a, v4i b, v4i c) {
 struct PrefillArgs {
   const int8_t* q8;      // [B][n_q][T][128]
   const int64_t* tpos;   // [B][n_q][T]
-  const int8_t* kc;      // [B][n_kv][cap][128]
-  const int8_t* vc;      // [B][n_kv][128][cap]
+  KVPages kv;
   const uint8_t* valid;  // [B][valid_stride]
   int64_t* out;          // [B][T][n_q * 128]
   int T, S, S_past, n_q, n_kv, B;
-  i64 cap, valid_stride;
+  i64 valid_stride;
 };
 
 constexpr int PF_KBYTES = 128 * 128;      // K tile: 128 slot rows of 128 B
@@ -96,9 +97,11 @@ __device__ __forceinline__ void pf_pack(const uint32_t (&p)[4], int& whi, int& w
 
 __global__ __launch_bounds__(256, 2) void k_attn_prefill(PrefillArgs a) {
   __shared__ __attribute__((aligned(1024))) int8_t ring[PF_RING];
-  extern __shared__ __attribute__((aligned(16))) int8_t dyn[];  // PF_CSUM + 8 per 64 slots
+  // PF_CSUM + 8 per 64 slots (tile masks) + 4 per page (page ids)
+  extern __shared__ __attribute__((aligned(16))) int8_t dyn[];
   int32_t* const csum_lds = (int32_t*)dyn;
   u64* const vmask = (u64*)(dyn + PF_CSUM);  // per 64-slot key tile
+  int32_t* const pages = (int32_t*)(dyn + PF_CSUM + 8 * ((a.S + 63) / 64));
   // Causal work per query tile grows with its index. Pair pi = (b, h, k)
   // (k fastest) stands for the heavy tile nqt - 1 - k and its light partner
   // k. Blocks are dispatched round-robin over the 8 XCDs (XCD = blockIdx % 8);
@@ -140,9 +143,9 @@ __global__ __launch_bounds__(256, 2) void k_attn_prefill(PrefillArgs a) {
   const int wlim = a.S_past + qt * 64 + wave * 16;  // the smallest limit in the wave
   const int kend = min(a.S, a.S_past + qt * 64 + 64);
   const int ntiles = (kend + 63) / 64;
-  const int8_t* kbase = a.kc + ((i64)b * a.n_kv + kvh) * a.cap * 128;
-  const int8_t* vbase = a.vc + ((i64)b * a.n_kv + kvh) * 128 * a.cap;
   const uint8_t* vrow = a.valid + (i64)b * a.valid_stride;
+  const int ntiles2 = (ntiles + 1) / 2;  // 128-slot tiles = pages
+  for (int i = tid; i < ntiles2; i += 256) pages[i] = a.kv.page(b, (i64)i * DI_PAGE);
 
   // validity bitmask of every key tile (bit s - 64 i of tile i: slot s < S
   // and valid), made once and read by all three passes for the tiles that
@@ -174,32 +177,35 @@ __global__ __launch_bounds__(256, 2) void k_attn_prefill(PrefillArgs a) {
   // halves (the 64-slot tiles `it` of the masks) between one barrier and the
   // next. K: instruction j of wave w covers tile rows 8(4w + j) .. +7, lane l
   // row 8(4w + j) + l/8 at physical chunk l % 8; V^T likewise with dims for
-  // rows. Buffer loads bounded by the (b, kv head) slice of each cache: slots
-  // past the cache read as 0 (K) or as the next V^T row / 0 (V); such slots
-  // are never visible (p = 0: their hi byte -64 and the +64 column-sum term
-  // cancel).
-  const int ntiles2 = (ntiles + 1) / 2;
-  const __amdgpu_buffer_rsrc_t krs =
-      __builtin_amdgcn_make_buffer_rsrc((void*)kbase, (short)0, (int)(a.cap * 128), 0x00020000);
-  const __amdgpu_buffer_rsrc_t vrs =
-      __builtin_amdgcn_make_buffer_rsrc((void*)vbase, (short)0, (int)(a.cap * 128), 0x00020000);
+  // rows. A tile is one page; the buffer resources span that page's
+  // (kv head) part, 16 KB of K and of V^T. A page that is not mapped gets a
+  // zero-length resource, so its loads read 0. Slots past the scanned range
+  // in a mapped page read whatever the page holds; such slots are never
+  // visible (p = 0: their hi byte -64 and the +64 column-sum term cancel).
   int koffl[4], voffl[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int row = (wave * 4 + j) * 8 + (lane >> 3);
     koffl[j] = row * 128 + ((lane & 7) ^ pf_kswz(row)) * 16;
-    voffl[j] = row * (int)a.cap + ((lane & 7) ^ pf_vswz(row)) * 16;
+    voffl[j] = row * DI_PAGE + ((lane & 7) ^ pf_vswz(row)) * 16;
   }
   auto issue = [&](int tile, int8_t* st, bool with_v) {
+    const int pg = __builtin_amdgcn_readfirstlane(pages[tile]);
+    const int pgc = pg < 0 ? 0 : pg;
+    const int nrec = pg < 0 ? 0 : DI_PAGE * 128;
+    const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)a.kv.krow(pgc, kvh, 0), (short)0, nrec, 0x00020000);
 #pragma unroll
     for (int j = 0; j < 4; ++j)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(krs, (lds_ptr_t)(st + (wave * 4 + j) * 1024), 16,
-                                               koffl[j], tile * 128 * 128, 0, 0);
+                                               koffl[j], 0, 0, 0);
     if (with_v) {
+      const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc(
+          (void*)a.kv.vchan(pgc, kvh, 0), (short)0, nrec, 0x00020000);
 #pragma unroll
       for (int j = 0; j < 4; ++j)
         __builtin_amdgcn_raw_ptr_buffer_load_lds(
-            vrs, (lds_ptr_t)(st + PF_KBYTES + (wave * 4 + j) * 1024), 16, voffl[j], tile * 128, 0, 0);
+            vrs, (lds_ptr_t)(st + PF_KBYTES + (wave * 4 + j) * 1024), 16, voffl[j], 0, 0, 0);
     }
   };
   // one pass over the key tiles; body(it2, stage) runs with tile it2 in LDS.
@@ -446,16 +452,17 @@ __global__ __launch_bounds__(256, 2) void k_attn_prefill(PrefillArgs a) {
 struct DecodeArgs {
   const int8_t* q8;      // [B][n_q][128]
   const int64_t* tpos;   // [B][n_q]
-  const int8_t* kc;      // [B][n_kv][cap][128]
-  const int8_t* vc;      // [B][n_kv][128][cap]
+  KVPages kv;
   const uint8_t* valid;  // [B][valid_stride]
   int64_t* out;          // [B][n_q * 128]
   int32_t* scratch;      // [B][n_q][S] when scores do not fit in LDS, else null
   const int64_t* s_dev;  // optional device bound on the scanned slots
   int S, n_q, n_kv;
-  i64 cap, valid_stride;
+  i64 valid_stride;
   int32_t* err;          // optional device error word (DI_ERR_SLOTS)
 };
+
+constexpr int DEC_MAX_PAGES = 1024;  // ceil(131071 / DI_PAGE)
 
 constexpr int MAXG = 8;
 constexpr i64 DECODE_LDS_BYTES = 48 * 1024;
@@ -502,10 +509,13 @@ struct KPre {
   i64 new_slot;         // -1: none
 };
 
+// pg_lds: the row's page ids for slots [0, S) (filled by the caller, before
+// a barrier). Slots whose page is not mapped are masked and read page 0.
 template <int G>
 __device__ __forceinline__ void decode_body(const DecodeArgs& a, int kvh, int b,
                                             const int8_t* qsrc, const int64_t* tsrc,
-                                            int32_t* sh_scores, const KPre* pre = nullptr) {
+                                            int32_t* sh_scores, const int32_t* pg_lds,
+                                            const KPre* pre = nullptr) {
   static_assert(G <= 8, "query heads per kv head");
   __shared__ i64 red_buf[32];
   BlockRed red{red_buf, 0};
@@ -521,18 +531,20 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, int kvh, int b,
   }
   const int Spad = (a.S + 15) & ~15;
   int32_t* sc = a.scratch ? a.scratch + ((i64)b * a.n_q + kvh * G) * Spad : sh_scores;
-  const int8_t* kbase = a.kc + ((i64)b * a.n_kv + kvh) * a.cap * 128;
-  const int8_t* vbase = a.vc + ((i64)b * a.n_kv + kvh) * 128 * a.cap;
   const uint8_t* vrow = a.valid + (i64)b * a.valid_stride;
   const int nstep = (S + 63) / 64;  // 64-slot steps of P.V
+  auto pg_of = [&](int s) -> int {  // page of slot s < S, page 0 when not mapped
+    const int pg = pg_lds[s >> 7];
+    return pg < 0 ? 0 : pg;
+  };
 
   // V fragments of the first VPRE steps, loaded now to overlap the scores
-  const int8_t* vch[2];
-#pragma unroll
-  for (int nb = 0; nb < 2; ++nb) vch[nb] = vbase + (i64)(wave * 32 + nb * 16 + l16) * a.cap;
+  // (a 64-slot step lies in one page)
   auto vfrag = [&](int st, int nb) -> v4i {
     const int s0 = st * 64 + grp * 16;
-    return s0 < S ? *(const v4i*)(vch[nb] + s0) : v4i{0, 0, 0, 0};
+    if (s0 >= S) return v4i{0, 0, 0, 0};
+    const int8_t* vch = a.kv.vchan(pg_of(s0), kvh, wave * 32 + nb * 16 + l16);
+    return *(const v4i*)(vch + (s0 & (DI_PAGE - 1)));
   };
   v4i vpre[VPRE][2];
 #pragma unroll
@@ -565,7 +577,7 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, int kvh, int b,
       for (int u = 0; u < 4; ++u) {
         kb[u][0] = pre->kb[u][0];
         kb[u][1] = pre->kb[u][1];
-        vf[u] = pre->vf[u];
+        vf[u] = pre->vf[u];  // 0 for slots of pages that are not mapped
         if ((blk0 + u * 4) * 16 + l16 == pre->new_slot) {
           kb[u][0] = *(const v4i*)(pre->k_new + grp * 16);
           kb[u][1] = *(const v4i*)(pre->k_new + 64 + grp * 16);
@@ -576,9 +588,10 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, int kvh, int b,
       for (int u = 0; u < 4; ++u) {
         const int s = (blk0 + u * 4) * 16 + l16;
         const int sc_ = s < S ? s : 0;
-        kb[u][0] = *(const v4i*)(kbase + (i64)sc_ * 128 + grp * 16);
-        kb[u][1] = *(const v4i*)(kbase + (i64)sc_ * 128 + 64 + grp * 16);
-        vf[u] = vrow[sc_];
+        const int8_t* kr = a.kv.krow(pg_of(sc_), kvh, sc_ & (DI_PAGE - 1));
+        kb[u][0] = *(const v4i*)(kr + grp * 16);
+        kb[u][1] = *(const v4i*)(kr + 64 + grp * 16);
+        vf[u] = pg_lds[sc_ >> 7] >= 0 ? vrow[sc_] : 0;
       }
     }
 #pragma unroll
@@ -731,9 +744,13 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, int kvh, int b,
 template <int G>
 __global__ __launch_bounds__(256) void k_attn_decode(DecodeArgs a) {
   extern __shared__ __attribute__((aligned(16))) int32_t sh_scores[];
+  __shared__ int32_t pg_lds[DEC_MAX_PAGES];
   const int kvh = blockIdx.x, b = blockIdx.y;
   const i64 q0 = (i64)b * a.n_q + kvh * G;
-  decode_body<G>(a, kvh, b, a.q8 + q0 * 128, a.tpos + q0, sh_scores);
+  const int npages = (a.S + DI_PAGE - 1) / DI_PAGE;
+  for (int i = threadIdx.x; i < npages; i += 256) pg_lds[i] = a.kv.page(b, (i64)i * DI_PAGE);
+  __syncthreads();
+  decode_body<G>(a, kvh, b, a.q8 + q0 * 128, a.tpos + q0, sh_scores, pg_lds);
 }
 
 // Decode step with the Q/K/V epilogue fused in (G <= 2): waves 0..G-1 finish
@@ -752,65 +769,94 @@ __global__ __launch_bounds__(256) void k_qkv_attn_decode(DecodeArgs a, QKVArgs q
   else if (w == G) slotw = qa.n_q + kvh;
   else if (w == G + 1) slotw = qa.n_q + qa.n_kv + kvh;
   __shared__ __attribute__((aligned(16))) int8_t k_new[128];
+  __shared__ int32_t pg_lds[DEC_MAX_PAGES];
+  // the row's page ids (stored to LDS after the epilogue) and the page ids of
+  // the first two pages, which the prefetch below addresses
+  const int npages = (a.S + DI_PAGE - 1) / DI_PAGE;
+  int pgv[DEC_MAX_PAGES / 256];
+#pragma unroll
+  for (int q = 0; q < DEC_MAX_PAGES / 256; ++q) {
+    const int i = (int)threadIdx.x + 256 * q;
+    pgv[q] = i < npages ? a.kv.page(b, (i64)i * DI_PAGE) : -1;
+  }
+  const int pg0 = a.kv.page(b, 0), pg1 = a.kv.page(b, DI_PAGE);
   // prefetch this wave's first K blocks of the scores pass (slots below the
-  // host bound a.S <= cap; the pass masks slots at or past the scanned count)
+  // host bound a.S <= capacity; the pass masks slots at or past the scanned
+  // count and slots of pages that are not mapped)
   KPre pre;
   {
     const int lane = threadIdx.x & 63, l16 = lane & 15, grp = lane >> 4;
-    const int8_t* kbase = a.kc + ((i64)b * a.n_kv + kvh) * a.cap * 128;
     const uint8_t* vrow = a.valid + (i64)b * a.valid_stride;
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
-      const int s = (w + u * 4) * 16 + l16;
+      const int s = (w + u * 4) * 16 + l16;  // < 256: pages 0 and 1
       const int sc_ = s < a.S ? s : 0;
-      pre.kb[u][0] = *(const v4i*)(kbase + (i64)sc_ * 128 + grp * 16);
-      pre.kb[u][1] = *(const v4i*)(kbase + (i64)sc_ * 128 + 64 + grp * 16);
-      pre.vf[u] = vrow[sc_];
+      const int pg = (sc_ >> 7) ? pg1 : pg0;
+      const int8_t* kr = a.kv.krow(pg < 0 ? 0 : pg, kvh, sc_ & (DI_PAGE - 1));
+      pre.kb[u][0] = *(const v4i*)(kr + grp * 16);
+      pre.kb[u][1] = *(const v4i*)(kr + 64 + grp * 16);
+      pre.vf[u] = pg >= 0 ? vrow[sc_] : 0;
     }
     const i64 base = qa.slot_base_dev ? qa.slot_base_dev[0] : qa.slot_base;
-    pre.new_slot = (base >= 0 && base < qa.cap) ? base : -1;  // T = 1: slot = base
+    // T = 1: the step's slot is base; -1 when it has no mapped page
+    pre.new_slot = qa.kv.page(b, base) >= 0 ? base : -1;
     pre.k_new = k_new;
   }
   if (slotw >= 0)
     qkv_head(qa, b, slotw, w < G ? q_lds[w] : nullptr, w < G ? &t_lds[w] : nullptr,
              w == G ? k_new : nullptr);
+#pragma unroll
+  for (int q = 0; q < DEC_MAX_PAGES / 256; ++q) {
+    const int i = (int)threadIdx.x + 256 * q;
+    if (i < npages) pg_lds[i] = pgv[q];
+  }
   __syncthreads();
-  decode_body<G>(a, kvh, b, &q_lds[0][0], t_lds, sh_scores, &pre);
+  decode_body<G>(a, kvh, b, &q_lds[0][0], t_lds, sh_scores, pg_lds, &pre);
 }
 
 }  // namespace
 
 extern "C" {
 
-int detllm_attn_prefill(const int8_t* q8, const int64_t* tpos, const int8_t* kc, const int8_t* vc,
+// The paged cache arguments of every entry below: kpool / vpool the layer's
+// page pools (common.h KVPages), table [B][width] int32 page ids (-1: not
+// mapped); a row holds width * 128 slots.
+static bool kv_ok(const int8_t* kpool, const int8_t* vpool, const int32_t* table, int width) {
+  return kpool && vpool && table && width > 0 && width <= (1 << 24);
+}
+
+int detllm_attn_prefill(const int8_t* q8, const int64_t* tpos, const int8_t* kpool,
+                        const int8_t* vpool, const int32_t* table, int width,
                         const uint8_t* valid, int64_t valid_stride, int B, int T, int S_past,
-                        int n_q, int n_kv, int64_t cap, int64_t* out, hipStream_t s) {
+                        int n_q, int n_kv, int64_t* out, hipStream_t s) {
   if (B <= 0 || T <= 0) return DI_OK;
   const i64 S = (i64)S_past + T;
-  if (n_q <= 0 || n_kv <= 0 || n_q % n_kv || S_past < 0 || S > cap || cap % 16 != 0 ||
-      valid_stride < S)
+  if (n_q <= 0 || n_kv <= 0 || n_q % n_kv || S_past < 0 || !kv_ok(kpool, vpool, table, width) ||
+      S > (i64)width * DI_PAGE || valid_stride < S || !q8 || !tpos || !valid || !out)
     return DI_EINVAL;
   if (S > 131071) return DI_ERANGE;  // int32 MFMA accumulators of P.V
-  if (cap > ((i64)1 << 24)) return DI_ERANGE;  // 32-bit buffer offsets of a cache slice
-  PrefillArgs a{q8, tpos, kc, vc, valid, out, T, (int)S, S_past, n_q, n_kv, B, cap, valid_stride};
+  PrefillArgs a{q8, tpos, KVPages{(int8_t*)kpool, (int8_t*)vpool, table, width, n_kv}, valid, out,
+                T, (int)S, S_past, n_q, n_kv, B, valid_stride};
   const i64 pairs = (i64)(((T + 63) / 64 + 1) / 2) * n_q * B;
   if (2 * pairs > 0x7fffffff) return DI_ERANGE;
-  const size_t lds = PF_CSUM + 8 * (size_t)((S + 63) / 64);  // column sums, tile masks
+  // column sums, tile masks, page ids
+  const size_t lds = PF_CSUM + 8 * (size_t)((S + 63) / 64) + 4 * (size_t)((S + 127) / 128);
   hipLaunchKernelGGL(k_attn_prefill, dim3((unsigned)(2 * pairs)), dim3(256), lds, s, a);
   DI_LAUNCH_CHECK();
   return DI_OK;
 }
 
-// Decode (one query per batch row). S: slots to scan (<= cap); s_dev:
-// optional device scalar that further bounds it (graph replay). scratch may
-// be null when n_q/n_kv * ceil16(S) * 4 bytes fit in 48 KiB of LDS.
-int detllm_attn_decode(const int8_t* q8, const int64_t* tpos, const int8_t* kc, const int8_t* vc,
+// Decode (one query per batch row). S: slots to scan (<= width * 128);
+// s_dev: optional device scalar that further bounds it (graph replay).
+// scratch may be null when n_q/n_kv * ceil16(S) * 4 bytes fit in 48 KiB of LDS.
+int detllm_attn_decode(const int8_t* q8, const int64_t* tpos, const int8_t* kpool,
+                       const int8_t* vpool, const int32_t* table, int width,
                        const uint8_t* valid, int64_t valid_stride, int B, int S, int n_q, int n_kv,
-                       int64_t cap, const int64_t* s_dev, int32_t* scratch, int64_t* out,
-                       int32_t* err, hipStream_t s) {
+                       const int64_t* s_dev, int32_t* scratch, int64_t* out, int32_t* err,
+                       hipStream_t s) {
   if (B <= 0) return DI_OK;
-  if (n_q <= 0 || n_kv <= 0 || n_q % n_kv || S < 0 || S > cap || cap % 16 != 0 ||
-      valid_stride < S)
+  if (n_q <= 0 || n_kv <= 0 || n_q % n_kv || S < 0 || !kv_ok(kpool, vpool, table, width) ||
+      S > (i64)width * DI_PAGE || valid_stride < S || !q8 || !tpos || !valid || !out)
     return DI_EINVAL;
   const int G = n_q / n_kv;
   if (G > MAXG) return DI_ENOSYS;
@@ -824,8 +870,8 @@ int detllm_attn_decode(const int8_t* q8, const int64_t* tpos, const int8_t* kc, 
   } else if (!scratch) {
     return DI_ERANGE;
   }
-  DecodeArgs a{q8, tpos, kc, vc, valid, out, scratch, s_dev, S, n_q, n_kv, cap, valid_stride,
-               err};
+  DecodeArgs a{q8, tpos, KVPages{(int8_t*)kpool, (int8_t*)vpool, table, width, n_kv}, valid, out,
+               scratch, s_dev, S, n_q, n_kv, valid_stride, err};
   const dim3 grid(n_kv, B);
   switch (G) {
     case 1: hipLaunchKernelGGL(k_attn_decode<1>, grid, dim3(256), dyn, s, a); break;
@@ -849,17 +895,18 @@ int detllm_qkv_attn_decode(const int32_t* P, int nsplit, int64_t split_stride, i
                            const int64_t* kq_m, const int64_t* kq_k, const int64_t* ks_m,
                            const int64_t* ks_k, const int64_t* vq_m, const int64_t* vq_k,
                            const int16_t* cos_t, const int16_t* sin_t, int64_t max_pos,
-                           int8_t* kcache, int8_t* vcache, int64_t cap,
+                           int8_t* kpool, int8_t* vpool, const int32_t* table, int width,
                            const int64_t* slot_base_dev, int64_t slot_base,
                            const uint8_t* valid, int64_t valid_stride, int S,
                            const int64_t* s_dev, int32_t* scratch, int64_t* out, int32_t* err,
                            hipStream_t s) {
   if (B <= 0) return DI_OK;
-  if (n_q <= 0 || n_kv <= 0 || n_q % n_kv || nsplit < 1 || S < 1 || S > cap || cap % 16 != 0 ||
-      valid_stride < S || max_pos <= 0 || !P || !out)
+  if (n_q <= 0 || n_kv <= 0 || n_q % n_kv || nsplit < 1 || S < 1 ||
+      !kv_ok(kpool, vpool, table, width) || S > (i64)width * DI_PAGE || valid_stride < S ||
+      max_pos <= 0 || !P || !out || !valid)
     return DI_EINVAL;
   if (S > DEC_MAX_S) return DI_ERANGE;  // int32 MFMA accumulators of P.V
-  if (!slot_base_dev && (slot_base < 0 || slot_base + 1 > cap)) return DI_ERANGE;
+  if (!slot_base_dev && (slot_base < 0 || slot_base + 1 > (i64)width * DI_PAGE)) return DI_ERANGE;
   const int G = n_q / n_kv;
   if (G > 2) return DI_ENOSYS;  // one wave per head slot of the block
   const i64 Spad = ((i64)S + 15) & ~15;
@@ -871,6 +918,7 @@ int detllm_qkv_attn_decode(const int32_t* P, int nsplit, int64_t split_stride, i
   } else if (!scratch) {
     return DI_ERANGE;
   }
+  const KVPages kv{kpool, vpool, table, width, n_kv};
   QKVArgs qa{};
   qa.T = 1; qa.n_q = n_q; qa.n_kv = n_kv; qa.P = P; qa.nsplit = nsplit;
   qa.split_stride = split_stride; qa.xm = xm; qa.xk = xk; qa.positions = positions;
@@ -879,10 +927,8 @@ int detllm_qkv_attn_decode(const int32_t* P, int nsplit, int64_t split_stride, i
   qa.k_norm_k = k_norm_k; qa.qs_m = qs_m; qa.qs_k = qs_k; qa.kq_m = kq_m; qa.kq_k = kq_k;
   qa.ks_m = ks_m; qa.ks_k = ks_k; qa.vq_m = vq_m; qa.vq_k = vq_k; qa.cos_t = cos_t;
   qa.sin_t = sin_t; qa.max_pos = max_pos; qa.q8 = nullptr; qa.tpos = nullptr; qa.dbg = nullptr;
-  qa.kcache = kcache; qa.vcache = vcache; qa.cap = cap; qa.slot_base_dev = slot_base_dev;
-  qa.slot_base = slot_base; qa.err = err;
-  DecodeArgs a{nullptr, nullptr, kcache, vcache, valid, out, scratch, s_dev, S, n_q, n_kv, cap,
-               valid_stride, err};
+  qa.kv = kv; qa.slot_base_dev = slot_base_dev; qa.slot_base = slot_base; qa.err = err;
+  DecodeArgs a{nullptr, nullptr, kv, valid, out, scratch, s_dev, S, n_q, n_kv, valid_stride, err};
   const dim3 grid(n_kv, B);
   if (G == 1)
     hipLaunchKernelGGL(k_qkv_attn_decode<1>, grid, dim3(256), dyn, s, a, qa);

@@ -28,7 +28,38 @@
 #define DI_ERR_POSITION 2  // position outside [-max_pos, max_pos)
 #define DI_ERR_SLOTS 4     // device slot count beyond the launch's slot bound
 
+// Slots per page of the paged KV cache.
+#define DI_PAGE 128
+
 namespace di {
+
+// The paged int8 KV cache of one layer. A row's slot s lives in page
+// table[b][s / DI_PAGE] (-1: not mapped) at offset s % DI_PAGE; pages hold
+// every kv head:
+//   K page [n_kv][DI_PAGE][128]   (a slot's K row: 128 contiguous bytes)
+//   V page [n_kv][128][DI_PAGE]   (V transposed: a channel's slots contiguous)
+// so both attention passes read slot-contiguous bytes, as the contiguous
+// layout did, and a page is the unit a growing cache hands out.
+struct KVPages {
+  int8_t* k;
+  int8_t* v;
+  const int32_t* table;  // [B][width]
+  int width;             // pages per row
+  int n_kv;
+
+  __device__ __forceinline__ i64 cap() const { return (i64)width * DI_PAGE; }
+  // page of row b's slot s (-1 when s is outside the table or not mapped)
+  __device__ __forceinline__ int page(int b, i64 s) const {
+    return (s >= 0 && s < cap()) ? table[(i64)b * width + (s >> 7)] : -1;
+  }
+  __device__ __forceinline__ int8_t* krow(int pg, int h, int off) const {
+    return k + (((i64)pg * n_kv + h) * DI_PAGE + off) * 128;
+  }
+  __device__ __forceinline__ int8_t* vchan(int pg, int h, int d) const {
+    return v + (((i64)pg * n_kv + h) * 128 + d) * DI_PAGE;
+  }
+};
+static_assert(DI_PAGE == 128, "page lookups shift by 7");
 
 // torch's advanced-indexing rule for a table of n rows (the reference's
 // embed_e8[ids] and cos_t[positions]): -n <= x < 0 reads row x + n, any other

@@ -44,9 +44,7 @@ struct QKVArgs {
   int8_t* q8;      // [B][n_q][T][128]
   int64_t* tpos;   // [B][n_q][T]
   int64_t* dbg;    // optional [B][n_q][T][4]: qm, qk, sm, sk
-  int8_t* kcache;  // [B][n_kv][cap][128]
-  int8_t* vcache;  // [B][n_kv][128][cap]  (V stored transposed)
-  i64 cap;
+  KVPages kv;      // the layer's paged cache: K and V of slot base + t are written
   const int64_t* slot_base_dev;  // optional device scalar (graph replay)
   i64 slot_base;
   int32_t* err;  // optional device error word (DI_ERR_POSITION)
@@ -167,7 +165,7 @@ __device__ __forceinline__ void qkv_head(const QKVArgs& a, int r, int slotw, int
     if (den <= 0) den = 1;  // static scales are positive mantissas in artifacts
     const i64 n0 = shl(wmul(wmul(p0, wm0), xm), up);
     const i64 n1 = shl(wmul(wmul(p1, wm1), xm), up);
-    int8_t* vrow = a.vcache + ((i64)b * a.n_kv + h) * 128 * a.cap;
+    const int pg = a.kv.page(b, slot);
     int8_t o0, o1;
     const i64 lim = (i64)1 << 49;  // 2 |n| + den < 2^51 for rhad_est_i8
     if (den < lim && n0 > -lim && n0 < lim && n1 > -lim && n1 < lim) {
@@ -179,9 +177,9 @@ __device__ __forceinline__ void qkv_head(const QKVArgs& a, int r, int slotw, int
       o0 = (int8_t)clamp_i8(rhad_r(n0, R));
       o1 = (int8_t)clamp_i8(rhad_r(n1, R));
     }
-    if (slot >= 0 && slot < a.cap) {
-      vrow[(i64)c0 * a.cap + slot] = o0;
-      vrow[(i64)c1 * a.cap + slot] = o1;
+    if (pg >= 0) {
+      a.kv.vchan(pg, h, c0)[slot & (DI_PAGE - 1)] = o0;
+      a.kv.vchan(pg, h, c1)[slot & (DI_PAGE - 1)] = o1;
     }
     return;
   }
@@ -203,7 +201,7 @@ __device__ __forceinline__ void qkv_head(const QKVArgs& a, int r, int slotw, int
   if (!is_q) {
     // K: requant_i8_static(kk, 1, k_rowk, 1, 0, kq_m, kq_k)   (model.py:326-329)
     const i64 rowk = 20 + a.k_norm_k;
-    int8_t* krow = a.kcache + (((i64)b * a.n_kv + h) * a.cap + slot) * 128;
+    const int pg = a.kv.page(b, slot);
     const i64 rv[2] = {r0, r1}, km[2] = {kqm0, kqm1}, kk[2] = {kqk0, kqk1};
     i64 outv[2];
 #pragma unroll
@@ -219,7 +217,8 @@ __device__ __forceinline__ void qkv_head(const QKVArgs& a, int r, int slotw, int
       else
         outv[q] = clamp_i8(rhad(n, den));
     }
-    if (slot >= 0 && slot < a.cap) {
+    if (pg >= 0) {
+      int8_t* krow = a.kv.krow(pg, h, (int)(slot & (DI_PAGE - 1)));
       krow[c0] = (int8_t)outv[0];
       krow[c1] = (int8_t)outv[1];
     }
@@ -337,7 +336,8 @@ __device__ __forceinline__ void qkv_rows4(const QKVArgs& a, int R, int r0, int s
     for (int i = 0; i < 8; ++i) p[i] = (int32_t)s[i];
   }
   const i64 slot = base + t;
-  const bool sok = rok && slot >= 0 && slot < a.cap;
+  const int pg = rok ? a.kv.page(b, slot) : -1;
+  const bool sok = pg >= 0;
 
   if (is_v) {
     // V head: requant_i8_static(Pv, xm, xk, v_m, v_k, vq_m[h], vq_k[h])
@@ -364,9 +364,8 @@ __device__ __forceinline__ void qkv_rows4(const QKVArgs& a, int R, int r0, int s
       for (int i = 0; i < 8; ++i) o[i] = (int8_t)clamp_i8(rhad_r(n[i], Rr));
     }
     if (sok) {
-      int8_t* vrow = a.vcache + ((i64)b * a.n_kv + h) * 128 * a.cap + slot;
 #pragma unroll
-      for (int i = 0; i < 8; ++i) vrow[(i64)c[i] * a.cap] = o[i];
+      for (int i = 0; i < 8; ++i) a.kv.vchan(pg, kvh, c[i])[slot & (DI_PAGE - 1)] = o[i];
     }
     return;
   }
@@ -450,7 +449,7 @@ __device__ __forceinline__ void qkv_rows4(const QKVArgs& a, int R, int r0, int s
       w[i >> 2] |= (uint32_t)(uint8_t)(int8_t)o << (8 * (i & 3));
     }
     if (sok) {
-      int8_t* krow = a.kcache + (((i64)b * a.n_kv + h) * a.cap + slot) * 128;
+      int8_t* krow = a.kv.krow(pg, h, (int)(slot & (DI_PAGE - 1)));
       *(uint32_t*)(krow + 4 * j) = w[0];
       *(uint32_t*)(krow + 64 + 4 * j) = w[1];
     }

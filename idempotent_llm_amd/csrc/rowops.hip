@@ -1092,13 +1092,15 @@ int detllm_qkv_epilogue(const int32_t* P, int nsplit, int64_t split_stride, int 
                         const int64_t* kq_m, const int64_t* kq_k, const int64_t* ks_m,
                         const int64_t* ks_k, const int64_t* vq_m, const int64_t* vq_k,
                         const int16_t* cos_t, const int16_t* sin_t, int64_t max_pos,
-                        int8_t* q8, int64_t* tpos, int64_t* dbg, int8_t* kcache,
-                        int8_t* vcache, int64_t cap, const int64_t* slot_base_dev,
-                        int64_t slot_base, const int64_t* kq_est, int32_t* err, hipStream_t s) {
+                        int8_t* q8, int64_t* tpos, int64_t* dbg, int8_t* kpool,
+                        int8_t* vpool, const int32_t* table, int width,
+                        const int64_t* slot_base_dev, int64_t slot_base, const int64_t* kq_est,
+                        int32_t* err, hipStream_t s) {
   if (B <= 0 || T <= 0) return DI_OK;
-  if (n_q <= 0 || n_kv <= 0 || n_q % n_kv != 0 || nsplit < 1 || cap <= 0 || max_pos <= 0)
+  if (n_q <= 0 || n_kv <= 0 || n_q % n_kv != 0 || nsplit < 1 || max_pos <= 0 || !kpool ||
+      !vpool || !table || width <= 0 || width > (1 << 24))
     return DI_EINVAL;
-  if (!slot_base_dev && (slot_base < 0 || slot_base + T > cap)) return DI_ERANGE;
+  if (!slot_base_dev && (slot_base < 0 || slot_base + T > (i64)width * DI_PAGE)) return DI_ERANGE;
   QKVArgs a{};
   a.T = T; a.n_q = n_q; a.n_kv = n_kv; a.P = P; a.nsplit = nsplit; a.split_stride = split_stride;
   a.xm = xm; a.xk = xk; a.positions = positions; a.q_m = q_m; a.k_m = k_m; a.v_m = v_m;
@@ -1106,7 +1108,7 @@ int detllm_qkv_epilogue(const int32_t* P, int nsplit, int64_t split_stride, int 
   a.q_norm_k = q_norm_k; a.k_norm_k = k_norm_k; a.qs_m = qs_m; a.qs_k = qs_k; a.kq_m = kq_m;
   a.kq_k = kq_k; a.ks_m = ks_m; a.ks_k = ks_k; a.vq_m = vq_m; a.vq_k = vq_k; a.cos_t = cos_t;
   a.sin_t = sin_t; a.max_pos = max_pos; a.q8 = q8; a.tpos = tpos; a.dbg = dbg;
-  a.kcache = kcache; a.vcache = vcache; a.cap = cap; a.slot_base_dev = slot_base_dev;
+  a.kv = KVPages{kpool, vpool, table, width, n_kv}; a.slot_base_dev = slot_base_dev;
   a.slot_base = slot_base; a.kq_est = kq_est; a.err = err;
   const int heads = n_q + 2 * n_kv;
   const int R = B * T;

@@ -4,13 +4,16 @@ The whole decode step — 28 layers of fused HIP kernels plus the LM head — is
 recorded once into a HIP graph (torch.cuda.CUDAGraph, which is hipGraph on
 ROCm) and replayed per token. Static-shape decode stays bit-exact by
 construction:
-  * the cache has a fixed bucketed capacity (256 * 2^n); attention scans the
-    filled slots (a device-side slot count bounds the scan) and the validity
-    mask excludes everything else, exactly as a length-wide computation;
+  * the cache's page tables cover a fixed bucketed capacity (256 * 2^n
+    slots); attention scans the filled slots (a device-side slot count bounds
+    the scan) and the validity mask excludes everything else, exactly as a
+    length-wide computation;
   * the K/V write slot is a device scalar (``len_idx``), so every replay
     writes the same bytes to the same slot as the eager path;
-  * bucket overflow reallocates the cache (filled slots copied verbatim) and
-    the next step recaptures.
+  * pages are mapped into the tables as the steps reach them, in place, so
+    the captured graph keeps running; bucket overflow widens the tables (no
+    K/V bytes move) and the next step recaptures, as does a page pool that
+    had to be reallocated.
 The graph contains kernel launches only (no memset nodes, no host reads).
 
 ``mode`` and ``layer_compile`` are the reference's arguments
@@ -77,9 +80,18 @@ class GraphedDecode:
             raise IndexError(f"decode past {DEC_MAX_SLOTS} cache slots is not supported "
                              "(int32 accumulators of the decode attention)")
         self.cache.resize(cap)
-        self.cache.static_cap = cap
-        self.graph = None   # a captured graph references the old buffers
+        self.cache.static_cap = self.cache.cap   # a planned cache may already be wider
+        self.graph = None   # a captured graph references the old tables
         self.graph_pick = None
+
+    def _map_next(self):
+        """Pages for this step's slot (a no-op within a mapped page); a pool
+        reallocation invalidates the captured graphs."""
+        gen = self.cache.pool_generation
+        self.cache.map_slots(self.length + 1)
+        if self.cache.pool_generation != gen:
+            self.graph = None
+            self.graph_pick = None
 
     def _prologue(self):
         """Validity flag, write slot, scanned-slot count and positions of this
@@ -132,6 +144,7 @@ class GraphedDecode:
         c = self.cache
         if self.length + 1 > c.static_cap:
             self._grow_to(_next_bucket(self.length + 1))
+        self._map_next()
         self._prologue()
         self.ids_buf.copy_(cur_ids.view(self.B, 1))
         if self.mode == "layers":
@@ -154,6 +167,7 @@ class GraphedDecode:
         c = self.cache
         if self.length + 1 > c.static_cap:
             self._grow_to(_next_bucket(self.length + 1))
+        self._map_next()
         self._prologue()
         if cur_ids is not None:
             self.ids_buf.copy_(cur_ids.view(self.B, 1))

@@ -24,8 +24,8 @@ One layer is 9 launches, each fusing everything between two GEMMs
 Memory layout in HBM (all integer; built once at load by integer
 permutation of the artifact's tensors): weights as [out, in] int8 with
 q|k|v and gate|up concatenated along out; per-channel mantissas int64; the
-KV cache as K [B, n_kv, cap, 128] and V^T [B, n_kv, 128, cap] int8 per layer
-plus a [B, cap] validity mask; cap is a multiple of 256.
+KV cache paged (kvcache.py: per-layer page pools of 128 slots, a page table
+per row) plus a [B, slots] validity mask.
 """
 
 from __future__ import annotations
@@ -41,6 +41,7 @@ from . import ops
 from ._lib import call, gemv_plan, raise_for_error_word
 from .backends import canonical_backend, gemm_nt, int_gemm, int_gemm_u16i8
 from .guard import NoFloatMode
+from .kvcache import PAGE, KVCache  # noqa: F401  (KVCache is part of this module's API)
 
 I64 = torch.int64
 P_OUT_BITS = 15
@@ -98,67 +99,6 @@ def _pack(L: LayerWeights, names) -> torch.Tensor:
         setattr(L, n, buf[off:off + t.numel()].view(t.shape))
         off += t.numel()
     return buf
-
-
-class KVCache:
-    """int8 K/V cache (model.py:67-102 semantics): ``length`` filled slots,
-    contents of filled slots never move, buffers grow geometrically (or to a
-    bucketed static capacity for graphed decode, graphed.py:36-93)."""
-
-    def __init__(self):
-        self.k8: list = []        # per layer [B, n_kv, cap, hd]
-        self.v8: list = []        # per layer V^T [B, n_kv, hd, cap]
-        self.valid_buf = None     # [B, cap] bool
-        self.length = 0
-        self.cap = 0
-        self.static_cap = 0
-        self.len_idx = None       # [1] int64 device: slot written by a graphed step
-        self.nslots = None        # [1] int64 device: slots visible to a graphed step
-
-    @property
-    def valid(self):
-        return None if self.valid_buf is None else self.valid_buf[:, :self.length]
-
-    def seq_len(self) -> int:
-        return self.length
-
-    # Slots at or past the filled length are never read as data: scores of
-    # such slots are masked, and their V bytes enter P.V only with p = 0 (the
-    # hi/lo split's colsum term cancels them exactly), so the buffers are not
-    # zero-filled.
-    def _alloc(self, B, n_layers, n_kv, hd, cap, device):
-        self.k8 = [torch.empty(B, n_kv, cap, hd, dtype=torch.int8, device=device)
-                   for _ in range(n_layers)]
-        self.v8 = [torch.empty(B, n_kv, hd, cap, dtype=torch.int8, device=device)
-                   for _ in range(n_layers)]
-        self.valid_buf = torch.zeros(B, cap, dtype=torch.bool, device=device)
-        self.cap = cap
-
-    def reserve(self, model: "IntQwen3", B: int, need: int):
-        if not self.k8:
-            cap = max(256, (need + 255) // 256 * 256)
-            self._alloc(B, model.n_layers, model.n_kv, model.hd, cap, model.device)
-        elif need > self.cap:
-            self.resize(max((need + 255) // 256 * 256, 2 * self.cap))
-
-    def resize(self, cap: int):
-        """Reallocate at capacity ``cap`` (multiple of 16), copying the filled
-        prefix verbatim (model.py:93-102, graphed.py:76-93)."""
-        assert cap % 16 == 0
-        L = self.length
-        for li in range(len(self.k8)):
-            B, n_kv, _, hd = self.k8[li].shape
-            nk = self.k8[li].new_empty(B, n_kv, cap, hd)
-            nk[:, :, :L] = self.k8[li][:, :, :L]
-            nv = self.v8[li].new_empty(B, n_kv, hd, cap)
-            nv[..., :L] = self.v8[li][..., :L]
-            self.k8[li], self.v8[li] = nk, nv
-        valid = torch.zeros(self.valid_buf.shape[0], cap, dtype=torch.bool,
-                            device=self.valid_buf.device)
-        n = min(cap, self.valid_buf.shape[1])
-        valid[:, :n] = self.valid_buf[:, :n]
-        self.valid_buf = valid
-        self.cap = cap
 
 
 class IntQwen3:
@@ -408,7 +348,7 @@ class IntQwen3:
                  L.q_m, L.q_k, L.k_m, L.k_k, L.v_m, L.v_k, L.q_norm_m, L.q_norm_k,
                  L.k_norm_m, L.k_norm_k, L.qs_m, L.qs_k, L.kq_m, L.kq_k, L.ks_m, L.ks_k,
                  L.vq_m, L.vq_k, self.rope_cos, self.rope_sin, self.max_pos,
-                 cache.k8[li], cache.v8[li], cache.cap, cache.len_idx if static else None,
+                 *cache.layer_args(li), cache.len_idx if static else None,
                  0 if static else S_past, valid, cache.cap, S,
                  cache.nslots if static else None, scratch, attn, self._err)
         elif T > 1 and self._seams_overridden():
@@ -435,16 +375,16 @@ class IntQwen3:
              L.q_m, L.q_k, L.k_m, L.k_k, L.v_m, L.v_k, L.q_norm_m, L.q_norm_k,
              L.k_norm_m, L.k_norm_k, L.qs_m, L.qs_k, L.kq_m, L.kq_k, L.ks_m, L.ks_k,
              L.vq_m, L.vq_k, self.rope_cos, self.rope_sin, self.max_pos, q8, tpos, None,
-             cache.k8[li], cache.v8[li], cache.cap, cache.len_idx if static else None,
+             *cache.layer_args(li), cache.len_idx if static else None,
              0 if static else S_past, L.kq_est, self._err)
         valid = cache.valid_buf.view(torch.uint8)
         if T == 1:
-            call("detllm_attn_decode", q8, tpos, cache.k8[li], cache.v8[li], valid, cache.cap,
-                 B, S, nq, nkv, cache.cap, cache.nslots if static else None,
+            call("detllm_attn_decode", q8, tpos, *cache.layer_args(li), valid, cache.cap,
+                 B, S, nq, nkv, cache.nslots if static else None,
                  self._decode_scratch(B, S), attn, self._err)
         else:
-            call("detllm_attn_prefill", q8, tpos, cache.k8[li], cache.v8[li], valid, cache.cap,
-                 B, T, S_past, nq, nkv, cache.cap, attn)
+            call("detllm_attn_prefill", q8, tpos, *cache.layer_args(li), valid, cache.cap,
+                 B, T, S_past, nq, nkv, attn)
 
     def _attention_seams(self, L, B, T, P, ns, st, xm, xk, pos, cache, S_past, S, attn):
         """Prefill attention through the overridable seams, as the
@@ -464,7 +404,7 @@ class IntQwen3:
              L.q_m, L.q_k, L.k_m, L.k_k, L.v_m, L.v_k, L.q_norm_m, L.q_norm_k,
              L.k_norm_m, L.k_norm_k, L.qs_m, L.qs_k, L.kq_m, L.kq_k, L.ks_m, L.ks_k,
              L.vq_m, L.vq_k, self.rope_cos, self.rope_sin, self.max_pos, q8, tpos, dbg,
-             cache.k8[li], cache.v8[li], cache.cap, None, S_past, L.kq_est, self._err)
+             *cache.layer_args(li), None, S_past, L.kq_est, self._err)
         qm, qk = dbg[..., 0:1], dbg[..., 1:2]
         Pfull = P.view(ns, B, T, -1).sum(dim=0, dtype=torch.int32) if ns > 1 else \
             P.view(B, T, -1)
@@ -478,8 +418,8 @@ class IntQwen3:
                                          L.k_norm_k, nkv, positions)
         aux = {"li": li, "q": q, "qkk": qkk, "kk": kk, "kkk": kkk, "Pv": Pv.contiguous(),
                "xm": xm3, "xk": xk3, "L": L}
-        K8 = cache.k8[li][:, :, :S]
-        V8 = cache.v8[li][..., :S].transpose(-1, -2)
+        K8 = cache._gather(li, "k", S)
+        V8 = cache._gather(li, "v", S)
         K8r = K8.repeat_interleave(group, dim=1).contiguous()
         V8r = V8.repeat_interleave(group, dim=1).contiguous()
         slot = torch.arange(S, device=dev)
@@ -560,11 +500,14 @@ class IntQwen3:
         positions = torch.arange(T0, device=dev).expand(B, T0)
         lens = chunk_valid.sum(dim=1)
         last = (lens - 1).clamp(min=0)
+        # the cache is sized for the whole generation up front: decoding then
+        # only maps pages (no reallocation, no copy, one graph capture)
+        cache = KVCache().plan(self, B, T0 + max_new)
         if guard:
             with NoFloatMode():
-                first, _, _, cache = self._forward(ids, positions, None, chunk_valid, last)
+                first, _, _, cache = self._forward(ids, positions, cache, chunk_valid, last)
         else:
-            first, _, _, cache = self._forward(ids, positions, None, chunk_valid, last)
+            first, _, _, cache = self._forward(ids, positions, cache, chunk_valid, last)
         step_logits = [first]
         cur = self.greedy_pick(first)
         out = [cur]

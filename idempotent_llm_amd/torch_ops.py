@@ -11,8 +11,10 @@ returns integer tensors of the right shape, so ``NoFloatMode`` holds during
 tracing too. The ops are registered for CUDA (HIP) tensors only: there is no
 CPU kernel behind them.
 
-Cache tensors use this backend's layout (K [B, n_kv, cap, 128], V stored
-transposed as V^T [B, n_kv, 128, cap], a [B, cap] bool validity mask).
+Cache tensors use this backend's paged layout (kvcache.py: per-layer K pool
+[n_pages, n_kv, 128, 128], V pool [n_pages, n_kv, 128, 128] holding V
+transposed per page, a [B, width] int32 page table, a [B, width * 128] bool
+validity mask).
 """
 
 from __future__ import annotations
@@ -193,13 +195,14 @@ def _(attn, os_m, os_k, col_m, col_k):
 
 # ------------------------------------------------------------- attention
 
-@_op("qkv_epilogue", mutates=("kcache", "vcache", "err"))
+@_op("qkv_epilogue", mutates=("kpool", "vpool", "err"))
 def qkv_epilogue(P: Tensor, B: int, T: int, n_q: int, n_kv: int, xm: Tensor, xk: Tensor,
                  positions: Tensor, q_m: Tensor, q_k: int, k_m: Tensor, k_k: int, v_m: Tensor,
                  v_k: int, q_norm_m: Tensor, q_norm_k: int, k_norm_m: Tensor, k_norm_k: int,
                  qs_m: Tensor, qs_k: int, kq_m: Tensor, kq_k: Tensor, ks_m: Tensor, ks_k: Tensor,
-                 vq_m: Tensor, vq_k: Tensor, cos_t: Tensor, sin_t: Tensor, kcache: Tensor,
-                 vcache: Tensor, slot_base: int, err: Tensor) -> tuple[Tensor, Tensor]:
+                 vq_m: Tensor, vq_k: Tensor, cos_t: Tensor, sin_t: Tensor, kpool: Tensor,
+                 vpool: Tensor, table: Tensor, slot_base: int,
+                 err: Tensor) -> tuple[Tensor, Tensor]:
     """_qk_head_pipeline + QK smoothing + Q quant + K/V static requant into
     the cache + score scale / DI-Exp constant (model.py:200-216, :303-358).
     P int32 [nsplit, B*T, (n_q + 2 n_kv) * 128]; returns (q8 [B, n_q, T, 128],
@@ -210,8 +213,8 @@ def qkv_epilogue(P: Tensor, B: int, T: int, n_q: int, n_kv: int, xm: Tensor, xk:
     call("detllm_qkv_epilogue", P.contiguous(), ns, R * P.shape[2], B, T, n_q, n_kv, xm, xk,
          positions.contiguous().view(-1), q_m, q_k, k_m, k_k, v_m, v_k, q_norm_m, q_norm_k,
          k_norm_m, k_norm_k, qs_m, qs_k, kq_m, kq_k, ks_m, ks_k, vq_m, vq_k, cos_t, sin_t,
-         cos_t.shape[0], q8, tpos, None, kcache, vcache, kcache.shape[2], None, slot_base, None,
-         err)
+         cos_t.shape[0], q8, tpos, None, kpool, vpool, table, table.shape[1], None, slot_base,
+         None, err)
     return q8, tpos
 
 
@@ -221,44 +224,45 @@ def _(P, B, T, n_q, n_kv, *rest):
 
 
 @_op("attn_prefill")
-def attn_prefill(q8: Tensor, tpos: Tensor, kcache: Tensor, vcache: Tensor, valid: Tensor,
-                 S_past: int) -> Tensor:
+def attn_prefill(q8: Tensor, tpos: Tensor, kpool: Tensor, vpool: Tensor, table: Tensor,
+                 valid: Tensor, S_past: int) -> Tensor:
     """Prefill attention (model.py:382-402): q8 [B, n_q, T, 128] over the
     cache's first S_past + T slots (causal by slot, valid-masked) -> exact
     int64 context [B, T, n_q * 128]."""
     B, n_q, T, _ = q8.shape
-    n_kv, cap = kcache.shape[1], kcache.shape[2]
+    n_kv = kpool.shape[1]
     out = torch.empty(B, T, n_q * 128, dtype=I64, device=q8.device)
-    call("detllm_attn_prefill", q8.contiguous(), tpos.contiguous(), kcache, vcache,
-         valid.view(torch.uint8), valid.shape[1], B, T, S_past, n_q, n_kv, cap, out)
+    call("detllm_attn_prefill", q8.contiguous(), tpos.contiguous(), kpool, vpool, table,
+         table.shape[1], valid.view(torch.uint8), valid.shape[1], B, T, S_past, n_q, n_kv, out)
     return out
 
 
 @attn_prefill.register_fake
-def _(q8, tpos, kcache, vcache, valid, S_past):
+def _(q8, tpos, kpool, vpool, table, valid, S_past):
     B, n_q, T, _ = q8.shape
     return q8.new_empty(B, T, n_q * 128, dtype=I64)
 
 
 @_op("attn_decode", mutates=("err",))
-def attn_decode(q8: Tensor, tpos: Tensor, kcache: Tensor, vcache: Tensor, valid: Tensor, S: int,
-                err: Tensor) -> Tensor:
+def attn_decode(q8: Tensor, tpos: Tensor, kpool: Tensor, vpool: Tensor, table: Tensor,
+                valid: Tensor, S: int, err: Tensor) -> Tensor:
     """Decode attention (model.py:347-381, ops/fused_attn.py:47-142): one
     query per row, q8 [B, n_q, 128], over S slots -> int64 [B, n_q * 128]."""
     B, n_q = q8.shape[0], q8.shape[1]
-    n_kv, cap = kcache.shape[1], kcache.shape[2]
+    n_kv = kpool.shape[1]
     G = n_q // n_kv
     Spad = (S + 15) // 16 * 16
     scratch = (torch.empty(B, n_q, Spad, dtype=torch.int32, device=q8.device)
                if G * Spad * 4 > 48 * 1024 else None)
     out = torch.empty(B, n_q * 128, dtype=I64, device=q8.device)
-    call("detllm_attn_decode", q8.contiguous(), tpos.contiguous(), kcache, vcache,
-         valid.view(torch.uint8), valid.shape[1], B, S, n_q, n_kv, cap, None, scratch, out, err)
+    call("detllm_attn_decode", q8.contiguous(), tpos.contiguous(), kpool, vpool, table,
+         table.shape[1], valid.view(torch.uint8), valid.shape[1], B, S, n_q, n_kv, None, scratch,
+         out, err)
     return out
 
 
 @attn_decode.register_fake
-def _(q8, tpos, kcache, vcache, valid, S, err):
+def _(q8, tpos, kpool, vpool, table, valid, S, err):
     return q8.new_empty(q8.shape[0], q8.shape[1] * 128, dtype=I64)
 
 

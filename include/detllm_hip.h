@@ -146,14 +146,24 @@ int detllm_merge_rowcol(const int64_t* attn, int nsplit, int64_t split_stride, i
                         const int64_t* os_m, int64_t os_k, const int64_t* col_m, int64_t col_k,
                         int8_t* a8, int64_t* am, int64_t* ak, hipStream_t s);
 
-/* Q/K/V epilogue per (token, head) — model.py:200-216 (_qk_head_pipeline),
+/* The KV cache is paged. Per layer, a K pool [n_pages][n_kv][128][128] (a
+ * page's K rows: n_kv heads x 128 slots x 128 channels) and a V pool
+ * [n_pages][n_kv][128][128] (V transposed: channels x slots); table
+ * [B][width] int32 gives row b's page for slots [128 j, 128 j + 128)
+ * (-1: not mapped; such slots are never written and never read as data).
+ * A row holds width * 128 slots. The reference keeps one contiguous
+ * [B, n_kv, CAP, hd] buffer per layer (model.py:67-102): same contents, only
+ * the addressing differs, so pages allocated as a cache grows never move
+ * earlier slots.
+ *
+ * Q/K/V epilogue per (token, head) — model.py:200-216 (_qk_head_pipeline),
  * :303-340 (QK smoothing, Q quant_i8_pertoken, K/V requant_i8_static, cache
  * write) and :351-358 (score scale norm_scale + DI-Exp constant tpos).
  * P: [nsplit][B*T][(n_q + 2 n_kv) * 128] int32 (q | k | v columns).
  * Outputs: q8 [B][n_q][T][128], tpos [B][n_q][T]; optional dbg
- * [B][n_q][T][4] = (qm, qk, sm, sk); K into kcache [B][n_kv][cap][128] and
- * V into vcache [B][n_kv][128][cap] (transposed) at slot base + t, where base
- * is *slot_base_dev when non-null (graph replay) else slot_base. Positions
+ * [B][n_q][T][4] = (qm, qk, sm, sk); K and V into the paged cache at slot
+ * base + t, where base is *slot_base_dev when non-null (graph replay) else
+ * slot_base. Positions
  * index the RoPE tables as cos_t[positions] does; one outside
  * [-max_pos, max_pos) sets bit 2 of *err. */
 int detllm_qkv_epilogue(const int32_t* P, int nsplit, int64_t split_stride, int B, int T,
@@ -165,9 +175,10 @@ int detllm_qkv_epilogue(const int32_t* P, int nsplit, int64_t split_stride, int 
                         const int64_t* kq_m, const int64_t* kq_k, const int64_t* ks_m,
                         const int64_t* ks_k, const int64_t* vq_m, const int64_t* vq_k,
                         const int16_t* cos_t, const int16_t* sin_t, int64_t max_pos,
-                        int8_t* q8, int64_t* tpos, int64_t* dbg, int8_t* kcache,
-                        int8_t* vcache, int64_t cap, const int64_t* slot_base_dev,
-                        int64_t slot_base, const int64_t* kq_est, int32_t* err, hipStream_t s);
+                        int8_t* q8, int64_t* tpos, int64_t* dbg, int8_t* kpool,
+                        int8_t* vpool, const int32_t* table, int width,
+                        const int64_t* slot_base_dev, int64_t slot_base, const int64_t* kq_est,
+                        int32_t* err, hipStream_t s);
 
 /* The static K requantisation's per-channel divisors for one layer
  * (requant_i8_static of model.py:326-329 with row scale (1, rowk), rowk =
@@ -194,22 +205,23 @@ int detllm_requant_static_cols(const int32_t* P, int nsplit, int64_t split_strid
  * di_softmax ops/di_softmax.py:33-61, _attn_context :476-478 with
  * int_gemm_u16i8 backends.py:152-164). Queries t in [0, T) sit at slots
  * S_past + t; slot s is visible iff s <= S_past + t and valid[b][s].
- * out [B][T][n_q*128] int64 = exact sum_s p_s v_s. cap % 16 == 0,
- * cap <= 2^24, S_past + T <= min(cap, 131071). */
-int detllm_attn_prefill(const int8_t* q8, const int64_t* tpos, const int8_t* kcache,
-                        const int8_t* vcache, const uint8_t* valid, int64_t valid_stride, int B,
-                        int T, int S_past, int n_q, int n_kv, int64_t cap, int64_t* out,
-                        hipStream_t s);
+ * out [B][T][n_q*128] int64 = exact sum_s p_s v_s over the paged cache;
+ * S_past + T <= min(width * 128, 131071). */
+int detllm_attn_prefill(const int8_t* q8, const int64_t* tpos, const int8_t* kpool,
+                        const int8_t* vpool, const int32_t* table, int width,
+                        const uint8_t* valid, int64_t valid_stride, int B, int T, int S_past,
+                        int n_q, int n_kv, int64_t* out, hipStream_t s);
 
 /* Decode attention (one query per row) — model.py:347-381 and the fused
  * Triton kernel ops/fused_attn.py:47-142 it replaces. Scans S <= 131071 slots
  * (further bounded by *s_dev when non-null); scratch [B][n_q][ceil16(S)]
  * int32 is required only when n_q/n_kv * ceil16(S) * 4 > 48 KiB.
  * out [B][n_q*128]. *s_dev above S sets bit 4 of *err. */
-int detllm_attn_decode(const int8_t* q8, const int64_t* tpos, const int8_t* kcache,
-                       const int8_t* vcache, const uint8_t* valid, int64_t valid_stride, int B,
-                       int S, int n_q, int n_kv, int64_t cap, const int64_t* s_dev,
-                       int32_t* scratch, int64_t* out, int32_t* err, hipStream_t s);
+int detllm_attn_decode(const int8_t* q8, const int64_t* tpos, const int8_t* kpool,
+                       const int8_t* vpool, const int32_t* table, int width,
+                       const uint8_t* valid, int64_t valid_stride, int B, int S, int n_q, int n_kv,
+                       const int64_t* s_dev, int32_t* scratch, int64_t* out, int32_t* err,
+                       hipStream_t s);
 
 /* Per-step bookkeeping of the graph-captured decode (src/detllm/graphed.py:
  * 112-131: the validity flag of the step's slot, the device scalars holding
@@ -237,7 +249,7 @@ int detllm_qkv_attn_decode(const int32_t* P, int nsplit, int64_t split_stride, i
                            const int64_t* kq_m, const int64_t* kq_k, const int64_t* ks_m,
                            const int64_t* ks_k, const int64_t* vq_m, const int64_t* vq_k,
                            const int16_t* cos_t, const int16_t* sin_t, int64_t max_pos,
-                           int8_t* kcache, int8_t* vcache, int64_t cap,
+                           int8_t* kpool, int8_t* vpool, const int32_t* table, int width,
                            const int64_t* slot_base_dev, int64_t slot_base,
                            const uint8_t* valid, int64_t valid_stride, int S,
                            const int64_t* s_dev, int32_t* scratch, int64_t* out, int32_t* err,

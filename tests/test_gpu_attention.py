@@ -11,6 +11,7 @@ import pytest
 import torch
 
 from idempotent_llm_amd import artifact as art
+from pagedcache import paged
 
 pytestmark = pytest.mark.gpu
 I64 = torch.int64
@@ -53,7 +54,9 @@ def _run(dims, B, cap, S, slot, device_bounds, seed):
     v0 = torch.randint(-128, 128, (B, nkv, hd, cap), generator=rnd, dtype=torch.int8).cuda()
     valid = (torch.rand(B, cap, generator=rnd) < 0.8).cuda()
     valid[:, slot] = True
+    k0, v0, table, width, valid = paged(k0, v0, valid, seed=seed)
     vbytes = valid.view(torch.uint8)
+    cap = width * 128
     G = nq // nkv
     Spad = (S + 15) // 16 * 16
     scratch = (torch.empty(B, nq, Spad, dtype=torch.int32, device="cuda")
@@ -71,14 +74,14 @@ def _run(dims, B, cap, S, slot, device_bounds, seed):
     tpos = torch.empty(B, nq, 1, dtype=I64, device="cuda")
     out_a = torch.empty(B, nq * hd, dtype=I64, device="cuda")
     call("detllm_qkv_epilogue", P, ns, B * P.shape[2], B, 1, nq, nkv, xm, xk, pos, *common,
-         q8, tpos, None, ka, va, cap, slot_dev, slot, None, None)
-    call("detllm_attn_decode", q8, tpos, ka, va, vbytes, cap, B, S_host, nq, nkv, cap, s_dev,
-         scratch, out_a, None)
+         q8, tpos, None, ka, va, table, width, slot_dev, slot, None, None)
+    call("detllm_attn_decode", q8, tpos, ka, va, table, width, vbytes, cap, B, S_host, nq, nkv,
+         s_dev, scratch, out_a, None)
     # fused launch
     kb, vb = k0.clone(), v0.clone()
     out_b = torch.empty(B, nq * hd, dtype=I64, device="cuda")
     call("detllm_qkv_attn_decode", P, ns, B * P.shape[2], B, nq, nkv, xm, xk, pos, *common,
-         kb, vb, cap, slot_dev, slot, vbytes, cap, S_host, s_dev, scratch, out_b, None)
+         kb, vb, table, width, slot_dev, slot, vbytes, cap, S_host, s_dev, scratch, out_b, None)
     torch.cuda.synchronize()
     assert torch.equal(ka, kb)
     assert torch.equal(va, vb)
@@ -188,8 +191,9 @@ def test_prefill_attention_vs_oracle(name):
     want = _prefill_oracle(q8, kc, vc, valid, sm, sk, S_past)
     d = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
     out = torch.full((B, T, n_q * 128), -7, dtype=I64, device="cuda")
-    call("detllm_attn_prefill", d(q8), d(tpos[..., 0]), d(kc), d(vc), d(valid.astype(np.uint8)),
-         cap, B, T, S_past, n_q, n_kv, cap, out)
+    kp, vp, table, width, vmask = paged(kc, vc, valid, seed=seed)
+    call("detllm_attn_prefill", d(q8), d(tpos[..., 0]), kp, vp, table, width,
+         vmask.view(torch.uint8), width * 128, B, T, S_past, n_q, n_kv, out)
     got = out.cpu().numpy()
     bad = np.argwhere(got != want)
     assert bad.size == 0, f"{len(bad)} mismatches, first at {bad[0].tolist()}"
@@ -229,8 +233,9 @@ def test_decode_attention_vs_oracle(name):
     scratch = (torch.empty(B, n_q, Spad, dtype=torch.int32, device="cuda")
                if G * Spad * 4 > 48 * 1024 else None)
     out = torch.full((B, n_q * 128), -7, dtype=I64, device="cuda")
-    call("detllm_attn_decode", d(q8[:, :, 0]), d(tpos[:, :, 0, 0]), d(kc), d(vc),
-         d(valid.astype(np.uint8)), cap, B, S, n_q, n_kv, cap, None, scratch, out, None)
+    kp, vp, table, width, vmask = paged(kc, vc, valid, seed=seed)
+    call("detllm_attn_decode", d(q8[:, :, 0]), d(tpos[:, :, 0, 0]), kp, vp, table, width,
+         vmask.view(torch.uint8), width * 128, B, S, n_q, n_kv, None, scratch, out, None)
     got = out.cpu().numpy()
     bad = np.argwhere(got != want)
     assert bad.size == 0, f"{len(bad)} mismatches, first at {bad[0].tolist()}"
@@ -263,10 +268,10 @@ def test_prefill_epilogue_kq_estimates(T):
     for e in (None, est):
         q8 = torch.empty(B, nq, T, hd, dtype=torch.int8, device="cuda")
         tpos = torch.empty(B, nq, T, dtype=I64, device="cuda")
-        kc = torch.zeros(B, nkv, cap, hd, dtype=torch.int8, device="cuda")
-        vc = torch.zeros(B, nkv, hd, cap, dtype=torch.int8, device="cuda")
+        kc, vc, table, width = paged(torch.zeros(B, nkv, cap, hd, dtype=torch.int8),
+                                     torch.zeros(B, nkv, hd, cap, dtype=torch.int8), seed=T)
         call("detllm_qkv_epilogue", P, 1, B * T * P.shape[2], B, T, nq, nkv, xm, xk, pos,
-             *common, q8, tpos, None, kc, vc, cap, None, 0, e, None)
+             *common, q8, tpos, None, kc, vc, table, width, None, 0, e, None)
         outs.append((q8, tpos, kc, vc))
     torch.cuda.synchronize()
     for a, b in zip(*outs):

@@ -134,13 +134,15 @@ def _c2_gpu(T, chunk=None):
     k8 = dd.requant_i8_static(dops.apply_int_rope(g(k), g(cos_t), g(sin_t), pos), 1, 0, 1, 0, 1, 0)
     sm, sk = dd.norm_scale(qm * 46341, qk + 19)
     _, tpos = dops.di_exp(torch.zeros_like(sm), sm, sk)
+    from pagedcache import paged
     cap = (T + 255) // 256 * 256
     kc = torch.zeros(1, 8, cap, 128, dtype=torch.int8, device="cuda")
     vc = torch.zeros(1, 8, 128, cap, dtype=torch.int8, device="cuda")
     kc[:, :, :T] = k8
     vc[..., :T] = g(v).transpose(2, 3)
-    valid = torch.zeros(1, cap, dtype=torch.uint8, device="cuda")
-    valid[:, :T] = 1
+    valid = torch.zeros(1, cap, dtype=torch.bool, device="cuda")
+    valid[:, :T] = True
+    kp, vp, table, width, valid = paged(kc, vc, valid, seed=T)
     out = torch.empty(1, T, 16 * 128, dtype=I64, device="cuda")
     step = chunk or T
     for t0 in range(0, T, step):
@@ -148,7 +150,8 @@ def _c2_gpu(T, chunk=None):
         q8c = q8[:, :, t0:t1].contiguous()
         tc = tpos[:, :, t0:t1, 0].contiguous()
         oc = torch.empty(1, t1 - t0, 16 * 128, dtype=I64, device="cuda")
-        call("detllm_attn_prefill", q8c, tc, kc, vc, valid, cap, 1, t1 - t0, t0, 16, 8, cap, oc)
+        call("detllm_attn_prefill", q8c, tc, kp, vp, table, width, valid.view(torch.uint8),
+             width * 128, 1, t1 - t0, t0, 16, 8, oc)
         out[:, t0:t1] = oc
     res = dd.requant_i8_rowcol(out[0], 1, 0, torch.ones(2048, dtype=I64, device="cuda"), 14)
     return (q8, k8, sm, sk), out, res
@@ -302,13 +305,13 @@ def test_c4_batch32_to_4096_slots(full_model):
 
 
 def test_c4_split_prefill_batch32(full_model):
-    """Split prefill of a ragged batch of 32 (lengths halved to keep the
-    token-by-token part short): the first half of the padded length at once,
-    then token by token (padding slots stay invalid); the logits of every
-    valid position equal the one-shot prefill's (tests/test_determinism.py:96-113,
-    for a batch)."""
+    """Split prefill of config c4's ragged batch of 32 (seeded lengths in
+    [16, 1024]): the first half of the padded length at once, then token by
+    token (padding slots stay invalid); the logits of every valid position
+    equal the one-shot prefill's (tests/test_determinism.py:96-113, for a
+    batch)."""
     _, m = full_model
-    lens = art.uniform_int(4, "c4.lens", (32,), 16, 1025) // 2
+    lens = art.uniform_int(4, "c4.lens", (32,), 16, 1025)
     prompts = [art.uniform_int(4, f"c4.prompt.{i}", (int(n),), 100, 50000)
                for i, n in enumerate(lens)]
     ids, valid = art.right_pad(prompts)
