@@ -32,6 +32,9 @@ SIGNATURES = {
     "detllm_embed_normq": [P, I, I, L, P, P, P, P, P, P, L, P, P, P, P, S],
     "detllm_residual_normq": [P, I, L, I, I, P, P, P, L, I, P, P, P, L, P, P, P, S],
     "detllm_norm_quant": [P, I, I, P, L, P, P, P, S],
+    "detllm_igemv_resnormq": [P, P, I, I, I, I, L, P, I, L, P, P, P, L, I, P, P, P, P, P, L, P,
+                              P, P, L, P, L, S],
+    "detllm_igemv_merge": [P, P, I, I, I, I, L, P, I, L, P, L, P, L, P, P, P, L, P, L, S],
     "detllm_swiglu_quant": [P, I, L, I, I, P, P, P, L, P, L, P, L, P, P, P, S],
     "detllm_merge_rowcol": [P, I, L, I, I, P, L, P, L, P, P, P, S],
     "detllm_qkv_epilogue": [P, I, L, I, I, I, I, P, P, P, P, L, P, L, P, L, P, L, P, L, P, L,
@@ -111,6 +114,20 @@ def gemv_plan(M: int, N: int, K: int) -> int:
     if rc != 0:
         raise RuntimeError(f"detllm_igemv_plan failed (code {rc})")
     return out.value
+
+
+def pro_fits(K: int, ksplit: int) -> bool:
+    """True when the fused decode GEMVs (detllm_igemv_resnormq /
+    detllm_igemv_merge) cover a K split of ``ksplit``: each split a whole
+    number of 512-byte chunks, at most two (the check those entry points make
+    before returning -38)."""
+    if K <= 0 or K % 16 or ksplit < 1:
+        return False
+    kchunk = -(-K // ksplit)
+    kchunk = -(-kchunk // 64) * 64
+    if -(-K // kchunk) != ksplit or kchunk % 512:
+        return False
+    return kchunk // 512 <= 2
 
 
 # bits of the device error word (include/detllm_hip.h)

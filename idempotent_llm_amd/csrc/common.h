@@ -178,6 +178,10 @@ struct BlockRed {
   i64* buf;  // __shared__ i64[32]
   int k;
 
+  // the row's threads: the whole block
+  __device__ __forceinline__ int tid() const { return (int)threadIdx.x; }
+  __device__ __forceinline__ int nt() const { return (int)blockDim.x; }
+
   template <bool MAX>
   __device__ __forceinline__ i64 reduce(i64 v) {
     v = wave_part<MAX>(v);
@@ -260,6 +264,23 @@ struct BlockRed {
       v = wadd(v, dpp64<0x143, 0xC>(v, 0));
     }
     return v;
+  }
+};
+
+// Reductions over one wave's 64 lanes (DPP, no LDS, no barrier): a row
+// handled by a single wave, several rows per block side by side. Same
+// integers as BlockRed (max and wrapping sum are order-independent).
+struct WaveRed {
+  __device__ __forceinline__ int tid() const { return (int)(threadIdx.x & 63); }
+  __device__ __forceinline__ int nt() const { return 64; }
+  __device__ __forceinline__ i64 max(i64 v) { return wave_max(v); }
+  __device__ __forceinline__ i64 sum(i64 v) { return wave_sum(v); }
+  __device__ __forceinline__ uint32_t max_u32(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_readlane((int)BlockRed::wave_max_u32(v), 63);
+  }
+  __device__ __forceinline__ void max2_u32(uint32_t& a, uint32_t& b) {
+    a = max_u32(a);
+    b = max_u32(b);
   }
 };
 

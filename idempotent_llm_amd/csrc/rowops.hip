@@ -23,6 +23,7 @@
 // back the op API used by the parity tests.
 
 #include "common.h"
+#include "gemv.h"
 #include "qkv_epilogue.h"
 
 using namespace di;
@@ -35,8 +36,8 @@ constexpr int RT = DI_ROW_THREADS;
 // serial per-row chain that bounds them at decode.
 constexpr int RT_WIDE = 1024;
 
-template <int VPT>
-__device__ __forceinline__ i64 row_absmax(const i64 (&v)[VPT], BlockRed& red) {
+template <int VPT, class Red>
+__device__ __forceinline__ i64 row_absmax(const i64 (&v)[VPT], Red& red) {
   i64 g = 0;
 #pragma unroll
   for (int j = 0; j < VPT; ++j) g = imax(g, wabs(v[j]));
@@ -44,8 +45,8 @@ __device__ __forceinline__ i64 row_absmax(const i64 (&v)[VPT], BlockRed& red) {
 }
 
 // ilog2(max(max_j |v_j|, 1)) over the row, from a 32-bit bit-length maximum
-template <int VPT>
-__device__ __forceinline__ i64 row_ilog2_absmax(const i64 (&v)[VPT], BlockRed& red) {
+template <int VPT, class Red>
+__device__ __forceinline__ i64 row_ilog2_absmax(const i64 (&v)[VPT], Red& red) {
   uint32_t L = 0;
 #pragma unroll
   for (int j = 0; j < VPT; ++j) L = ::max(L, bitlen_abs(v[j]));
@@ -55,8 +56,8 @@ __device__ __forceinline__ i64 row_ilog2_absmax(const i64 (&v)[VPT], BlockRed& r
 // ops/di_rmsnorm.py:33-52: v (<= C valid columns, 0 elsewhere) -> y (int32
 // values). lg: ilog2(max(max |v|, 1)) when the caller already knows it, else
 // -1 (one more block reduction).
-template <int VPT>
-__device__ __forceinline__ void rmsnorm_row(i64 (&v)[VPT], int C, BlockRed& red, i64 lg = -1) {
+template <int VPT, class Red>
+__device__ __forceinline__ void rmsnorm_row(i64 (&v)[VPT], int C, Red& red, i64 lg = -1) {
   const i64 sh = 25 - (lg >= 0 ? lg : row_ilog2_absmax(v, red));
   const i64 up = imax(sh, 0), down = imax(-sh, 0);
   i64 ss = 0;
@@ -85,9 +86,9 @@ __device__ __forceinline__ void rmsnorm_row(i64 (&v)[VPT], int C, BlockRed& red,
 // dyadic.py:93-105. The quotients rhad(127 x, a) with |x| <= a come from the
 // fp64 estimate (intops.h rhad_est) when a < 2^43 (then 2 * 127 |x| + a <
 // 2^51 and no 127 x wraps), else from the 64-bit reciprocal.
-template <int VPT>
+template <int VPT, class Red>
 __device__ __forceinline__ void quant_row(const i64 (&v)[VPT], i64 m_in, i64 k_in, int C,
-                                          BlockRed& red, int8_t* out, i64* m_out, i64* k_out) {
+                                          Red& red, int8_t* out, i64* m_out, i64* k_out) {
   i64 m, k;
   norm_scale(m_in, k_in, &m, &k);
   const i64 a = imax(row_absmax(v, red), 1);
@@ -95,18 +96,18 @@ __device__ __forceinline__ void quant_row(const i64 (&v)[VPT], i64 m_in, i64 k_i
     const DivEst D = make_divest(a, 127.0);
 #pragma unroll
     for (int j = 0; j < VPT; ++j) {
-      const int c = threadIdx.x + j * (int)blockDim.x;
+      const int c = red.tid() + j * red.nt();
       if (c < C) out[c] = (int8_t)rhad_est_signed(v[j], D);
     }
   } else {
     const Recip R = make_recip(a);
 #pragma unroll
     for (int j = 0; j < VPT; ++j) {
-      const int c = threadIdx.x + j * (int)blockDim.x;
+      const int c = red.tid() + j * red.nt();
       if (c < C) out[c] = (int8_t)clamp_i8(rhad_r(wmul(v[j], 127), R));
     }
   }
-  if (threadIdx.x == 0) {
+  if (red.tid() == 0 && m_out) {
     i64 mo, e;
     fit_dyadic_ratio_127(wmul(a, m), &mo, &e);
     *m_out = mo;
@@ -116,9 +117,9 @@ __device__ __forceinline__ void quant_row(const i64 (&v)[VPT], i64 m_in, i64 k_i
 
 // dyadic.py:108-120: v holds P on entry, y (int32 values) on exit; cm holds
 // col_m of this thread's columns (0 past C); returns k_out
-template <int VPT>
+template <int VPT, class Red>
 __device__ __forceinline__ i64 requant_common_row(i64 (&v)[VPT], const i64 (&cm)[VPT], i64 row_k,
-                                                  i64 col_k, int tb, BlockRed& red) {
+                                                  i64 col_k, int tb, Red& red) {
 #pragma unroll
   for (int j = 0; j < VPT; ++j) v[j] = wmul(v[j], cm[j]);
   const i64 sh = imax(row_ilog2_absmax(v, red) - (tb - 1), 0);
@@ -129,11 +130,11 @@ __device__ __forceinline__ i64 requant_common_row(i64 (&v)[VPT], const i64 (&cm)
 
 // requant_common_row on two rows at once (gate and up of the same token):
 // both bit-length maxima share one barrier. Returns the two k_out.
-template <int VPT>
+template <int VPT, class Red>
 __device__ __forceinline__ void requant_common_row2(i64 (&v0)[VPT], const i64 (&cm0)[VPT],
                                                     i64 col_k0, i64 (&v1)[VPT],
                                                     const i64 (&cm1)[VPT], i64 col_k1, i64 row_k,
-                                                    int tb, BlockRed& red, i64* k0, i64* k1) {
+                                                    int tb, Red& red, i64* k0, i64* k1) {
   uint32_t L0 = 0, L1 = 0;
 #pragma unroll
   for (int j = 0; j < VPT; ++j) {
@@ -159,8 +160,8 @@ __device__ __forceinline__ void requant_common_row2(i64 (&v0)[VPT], const i64 (&
 // down-shift it does: an exact up-shift by u adds u to every bit length (and
 // no shift leaves them), while rounding a down-shift may carry into the next
 // bit.
-template <int VPT>
-__device__ __forceinline__ i64 residual_renorm_row(i64 (&h)[VPT], i64 k_res, BlockRed& red,
+template <int VPT, class Red>
+__device__ __forceinline__ i64 residual_renorm_row(i64 (&h)[VPT], i64 k_res, Red& red,
                                                    i64* lg_out) {
   uint32_t L = 0;
 #pragma unroll
@@ -177,9 +178,9 @@ __device__ __forceinline__ i64 residual_renorm_row(i64 (&h)[VPT], i64 k_res, Blo
 }
 
 // dyadic.py:193-206
-template <int VPT>
+template <int VPT, class Red>
 __device__ __forceinline__ i64 residual_add_row(i64 (&h)[VPT], i64 k_res, const i64 (&d)[VPT],
-                                                i64 dm, i64 dk, BlockRed& red, i64* lg_out) {
+                                                i64 dm, i64 dk, Red& red, i64* lg_out) {
   const i64 rel = wsub(dk, k_res);
   const i64 down = imax(rel, 0), up = imax(wneg(rel), 0);
 #pragma unroll
@@ -195,37 +196,38 @@ __device__ __forceinline__ i64 residual_add_row(i64 (&h)[VPT], i64 k_res, const 
 
 // x[c] for the columns c = threadIdx.x + j * blockDim.x this thread owns (0 past C or
 // when x is null).
-template <int VPT>
-__device__ __forceinline__ void prefetch_cols(i64 (&v)[VPT], const int64_t* x, int C) {
+template <int VPT, class Red>
+__device__ __forceinline__ void prefetch_cols(i64 (&v)[VPT], const int64_t* x, int C,
+                                              const Red& red) {
 #pragma unroll
   for (int j = 0; j < VPT; ++j) {
-    const int c = threadIdx.x + j * (int)blockDim.x;
+    const int c = red.tid() + j * red.nt();
     v[j] = x ? x[c < C ? c : C - 1] : 0;
   }
 #pragma unroll
   for (int j = 0; j < VPT; ++j)
-    if (threadIdx.x + j * (int)blockDim.x >= C) v[j] = 0;
+    if (red.tid() + j * red.nt() >= C) v[j] = 0;
 }
 
 // Sum of nsplit int32 partials P[k * stride + off + c] (the K-split of the
 // skinny GEMM) in a fixed order, for NR rows at offsets off[0..NR).
-template <int NR, int VPT>
+template <int NR, int VPT, class Red>
 __device__ __forceinline__ void load_rows_i32_sum(i64 (&v)[NR][VPT], const int32_t* P,
                                                   int nsplit, i64 stride, const i64 (&off)[NR],
-                                                  int C) {
+                                                  int C, const Red& red) {
   if (nsplit == 1) {  // no K split (block-uniform): one load per element
 #pragma unroll
     for (int q = 0; q < NR; ++q)
 #pragma unroll
       for (int j = 0; j < VPT; ++j) {
-        const int c = threadIdx.x + j * (int)blockDim.x;
+        const int c = red.tid() + j * red.nt();
         v[q][j] = P[off[q] + (c < C ? c : C - 1)];
       }
 #pragma unroll
     for (int q = 0; q < NR; ++q)
 #pragma unroll
       for (int j = 0; j < VPT; ++j)
-        if (threadIdx.x + j * (int)blockDim.x >= C) v[q][j] = 0;
+        if (red.tid() + j * red.nt() >= C) v[q][j] = 0;
     return;
   }
   constexpr int KU = NR * VPT > 8 ? 2 : 4;  // partials per batch of loads
@@ -243,7 +245,7 @@ __device__ __forceinline__ void load_rows_i32_sum(i64 (&v)[NR][VPT], const int32
       for (int q = 0; q < NR; ++q)
 #pragma unroll
         for (int j = 0; j < VPT; ++j) {
-          const int c = threadIdx.x + j * (int)blockDim.x;
+          const int c = red.tid() + j * red.nt();
           t[kk][q][j] = P[(i64)k * stride + off[q] + (c < C ? c : C - 1)];
         }
     }
@@ -259,7 +261,7 @@ __device__ __forceinline__ void load_rows_i32_sum(i64 (&v)[NR][VPT], const int32
   for (int q = 0; q < NR; ++q)
 #pragma unroll
     for (int j = 0; j < VPT; ++j)
-      v[q][j] = threadIdx.x + j * (int)blockDim.x < C ? (i64)(int32_t)s[q][j] : 0;
+      v[q][j] = red.tid() + j * red.nt() < C ? (i64)(int32_t)s[q][j] : 0;
 }
 
 // =====================================================================
@@ -283,72 +285,77 @@ struct ResNormArgs {
   const int64_t* col_m;
   i64 col_k;
   int tb;
-  int32_t* h;
+  const int32_t* h_in;     // residual read (mode 1, 2); h when null
+  const int64_t* k_res_in; // its k (mode 1); k_res when null
+  int32_t* h;              // residual written (modes 0, 1); null: not stored
   int64_t* k_res;
   const int64_t* sm_m;  // null: no smoothing multiply
   i64 sm_k;
   int8_t* x8;  // null: no norm-quant
-  int64_t* xm;
+  i64 x8_stride;  // row stride of x8 (0: C)
+  int64_t* xm;    // null: (m, k) of x8 not stored
   int64_t* xk;
   int32_t* err;  // optional device error word (DI_ERR_TOKEN)
 };
 
-template <int VPT>
-__device__ __forceinline__ void residual_normq_row(const ResNormArgs& a, int r, BlockRed& red) {
+template <int VPT, class Red>
+__device__ __forceinline__ void residual_normq_row(const ResNormArgs& a, int r, Red& red) {
   const int C = a.C;
   const i64 off = (i64)r * C;
   i64 h[VPT], d[VPT], smv[VPT];
   i64 kr, lg = -1;
-  prefetch_cols(smv, a.sm_m, C);
+  const int32_t* h_in = a.h_in ? a.h_in : a.h;
+  prefetch_cols(smv, a.sm_m, C, red);
   if (a.mode == 2) {
     // _norm_quant of a given residual row: h is read, not written
 #pragma unroll
     for (int j = 0; j < VPT; ++j) {
-      const int c = threadIdx.x + j * (int)blockDim.x;
-      h[j] = a.h[off + (c < C ? c : C - 1)];
+      const int c = red.tid() + j * red.nt();
+      h[j] = h_in[off + (c < C ? c : C - 1)];
     }
 #pragma unroll
     for (int j = 0; j < VPT; ++j)
-      if (threadIdx.x + j * (int)blockDim.x >= C) h[j] = 0;
+      if (red.tid() + j * red.nt() >= C) h[j] = 0;
     kr = 0;
   } else if (a.mode == 0) {
-    const i64 id = torch_index(a.ids[r], a.vocab, threadIdx.x ? nullptr : a.err, DI_ERR_TOKEN);
+    const i64 id = torch_index(a.ids[r], a.vocab, red.tid() ? nullptr : a.err, DI_ERR_TOKEN);
     const i64 dm = a.em[id], ek = a.ek[id];
 #pragma unroll
     for (int j = 0; j < VPT; ++j) {
-      const int c = threadIdx.x + j * (int)blockDim.x;
+      const int c = red.tid() + j * red.nt();
       h[j] = a.e8[id * C + (c < C ? c : C - 1)];
     }
 #pragma unroll
-    for (int j = 0; j < VPT; ++j) h[j] = threadIdx.x + j * (int)blockDim.x < C ? wmul(h[j], dm) : 0;
+    for (int j = 0; j < VPT; ++j) h[j] = red.tid() + j * red.nt() < C ? wmul(h[j], dm) : 0;
     kr = residual_renorm_row(h, ek, red, &lg);
   } else {
     i64 cm[VPT];
-    prefetch_cols(cm, a.col_m, C);
+    prefetch_cols(cm, a.col_m, C, red);
 #pragma unroll
     for (int j = 0; j < VPT; ++j) {
-      const int c = threadIdx.x + j * (int)blockDim.x;
-      h[j] = a.h[off + (c < C ? c : C - 1)];
+      const int c = red.tid() + j * red.nt();
+      h[j] = h_in[off + (c < C ? c : C - 1)];
     }
-    const i64 row_k = a.row_k[r], row_m = a.row_m[r], k_res = a.k_res[r];
+    const i64 row_k = a.row_k[r], row_m = a.row_m[r];
+    const i64 k_res = (a.k_res_in ? a.k_res_in : a.k_res)[r];
     i64 dd[1][VPT];
     const i64 offs[1] = {off};
-    load_rows_i32_sum<1, VPT>(dd, a.P, a.nsplit, a.split_stride, offs, C);
+    load_rows_i32_sum<1, VPT>(dd, a.P, a.nsplit, a.split_stride, offs, C, red);
 #pragma unroll
     for (int j = 0; j < VPT; ++j) {
       d[j] = dd[0][j];
-      if (threadIdx.x + j * (int)blockDim.x >= C) h[j] = 0;
+      if (red.tid() + j * red.nt() >= C) h[j] = 0;
     }
     const i64 dk = requant_common_row(d, cm, row_k, a.col_k, a.tb, red);
     kr = residual_add_row(h, k_res, d, row_m, dk, red, &lg);
   }
-  if (a.mode != 2) {
+  if (a.mode != 2 && a.h) {
 #pragma unroll
     for (int j = 0; j < VPT; ++j) {
-      const int c = threadIdx.x + j * (int)blockDim.x;
+      const int c = red.tid() + j * red.nt();
       if (c < C) a.h[off + c] = (int32_t)h[j];
     }
-    if (threadIdx.x == 0) a.k_res[r] = kr;
+    if (red.tid() == 0) a.k_res[r] = kr;
   }
   if (a.x8 == nullptr) return;
   rmsnorm_row(h, C, red, lg);
@@ -358,7 +365,8 @@ __device__ __forceinline__ void residual_normq_row(const ResNormArgs& a, int r, 
     for (int j = 0; j < VPT; ++j) h[j] = wmul(h[j], smv[j]);
     kq += a.sm_k;
   }
-  quant_row(h, 1, kq, C, red, a.x8 + off, a.xm + r, a.xk + r);
+  quant_row(h, 1, kq, C, red, a.x8 + (i64)r * (a.x8_stride ? a.x8_stride : C),
+            a.xm ? a.xm + r : nullptr, a.xk ? a.xk + r : nullptr);
 }
 
 template <int VPT, int NT = RT_WIDE>
@@ -386,8 +394,8 @@ struct SwigluArgs {
   int64_t* yk;
 };
 
-template <int VPT>
-__device__ __forceinline__ void swiglu_quant_row(const SwigluArgs& a, int r, BlockRed& red) {
+template <int VPT, class Red>
+__device__ __forceinline__ void swiglu_quant_row(const SwigluArgs& a, int r, Red& red) {
   const int I = a.I;
   // Many rows (prefill, more than 4 columns per thread): the down-smoothing
   // scales load after the requantisation, when the gate/up scales are dead,
@@ -395,13 +403,13 @@ __device__ __forceinline__ void swiglu_quant_row(const SwigluArgs& a, int r, Blo
   // rows hide the extra load). Decode rows load everything up front.
   constexpr bool kLate = VPT > 4;
   i64 gm[VPT], um[VPT], dsm[VPT];
-  prefetch_cols(gm, a.gate_m, I);
-  prefetch_cols(um, a.up_m, I);
-  if (!kLate) prefetch_cols(dsm, a.ds_m, I);
+  prefetch_cols(gm, a.gate_m, I, red);
+  prefetch_cols(um, a.up_m, I, red);
+  if (!kLate) prefetch_cols(dsm, a.ds_m, I, red);
   const i64 xm = a.xm[r], xk = a.xk[r];
   i64 gu[2][VPT];
   const i64 offs[2] = {(i64)r * 2 * I, (i64)r * 2 * I + I};
-  load_rows_i32_sum<2, VPT>(gu, a.P, a.nsplit, a.split_stride, offs, I);
+  load_rows_i32_sum<2, VPT>(gu, a.P, a.nsplit, a.split_stride, offs, I, red);
   i64 gk, uk;
   requant_common_row2(gu[0], gm, a.gate_k, gu[1], um, a.up_k, xk, 14, red, &gk, &uk);
   // requant_i32_common(14) leaves |g|, |u| <= 2^14 (the shift brings the
@@ -412,7 +420,7 @@ __device__ __forceinline__ void swiglu_quant_row(const SwigluArgs& a, int r, Blo
     g32[j] = (int32_t)gu[0][j];
     u32[j] = (int32_t)gu[1][j];
   }
-  if (kLate) prefetch_cols(dsm, a.ds_m, I);
+  if (kLate) prefetch_cols(dsm, a.ds_m, I, red);
   const i64 tp = di_exp_tpos_fast(xm, gk);
   i64 y[VPT];
   if (tp < ((i64)1 << 23)) {
@@ -451,45 +459,56 @@ struct MergeArgs {
   const int64_t* col_m;
   i64 col_k;
   int8_t* a8;
-  int64_t* am;
+  i64 a8_stride;  // row stride of a8 (0: C)
+  int64_t* am;    // null: (m, k) of a8 not stored
   int64_t* ak;
 };
 
-template <int VPT>
-__device__ __forceinline__ void merge_rowcol_row(const MergeArgs& a, int r, BlockRed& red) {
+template <int VPT, class Red>
+__device__ __forceinline__ void merge_rowcol_row(const MergeArgs& a, int r, Red& red) {
   const int C = a.C;
   const i64 off = (i64)r * C;
-  i64 v[VPT], om[VPT], cm[VPT];
-  prefetch_cols(om, a.os_m, C);
-  prefetch_cols(cm, a.col_m, C);
+  int8_t* const a8 = a.a8 + (i64)r * (a.a8_stride ? a.a8_stride : C);
+  i64 v[VPT], om[VPT];
+  // per-column factor os_m * col_m (col_m null: os_m already holds the
+  // product; int64 multiplication wraps modulo 2^64, so the order of the
+  // two factors does not change a bit)
+  prefetch_cols(om, a.os_m, C, red);
+  if (a.col_m) {
+    i64 cm[VPT];
+    prefetch_cols(cm, a.col_m, C, red);
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) om[j] = wmul(om[j], cm[j]);
+  }
 #pragma unroll
   for (int j = 0; j < VPT; ++j) v[j] = 0;
   if (a.nsplit == 1) {  // one load per element (block-uniform)
 #pragma unroll
     for (int j = 0; j < VPT; ++j) {
-      const int c = threadIdx.x + j * (int)blockDim.x;
+      const int c = red.tid() + j * red.nt();
       v[j] = a.attn[off + (c < C ? c : C - 1)];
     }
   }
-  for (int k0 = 0; a.nsplit > 1 && k0 < a.nsplit; k0 += 2) {
-    i64 t[2][VPT];
+  constexpr int KB = VPT > 16 ? 1 : 2;  // partials per batch of loads (registers)
+  for (int k0 = 0; a.nsplit > 1 && k0 < a.nsplit; k0 += KB) {
+    i64 t[KB][VPT];
 #pragma unroll
-    for (int kk = 0; kk < 2; ++kk) {
+    for (int kk = 0; kk < KB; ++kk) {
       const int k = k0 + kk < a.nsplit ? k0 + kk : a.nsplit - 1;
 #pragma unroll
       for (int j = 0; j < VPT; ++j) {
-        const int c = threadIdx.x + j * (int)blockDim.x;
+        const int c = red.tid() + j * red.nt();
         t[kk][j] = a.attn[(i64)k * a.split_stride + off + (c < C ? c : C - 1)];
       }
     }
 #pragma unroll
-    for (int kk = 0; kk < 2; ++kk)
+    for (int kk = 0; kk < KB; ++kk)
       if (k0 + kk < a.nsplit)
 #pragma unroll
         for (int j = 0; j < VPT; ++j) v[j] = wadd(v[j], t[kk][j]);
   }
 #pragma unroll
-  for (int j = 0; j < VPT; ++j) v[j] = wmul(wmul(v[j], om[j]), cm[j]);  // 0 past C
+  for (int j = 0; j < VPT; ++j) v[j] = wmul(v[j], om[j]);  // 0 past C
   const i64 sh = imax(row_ilog2_absmax(v, red) - 45, 0);
 #pragma unroll
   for (int j = 0; j < VPT; ++j) v[j] = rshift_round(v[j], sh);
@@ -502,25 +521,25 @@ __device__ __forceinline__ void merge_rowcol_row(const MergeArgs& a, int r, Bloc
     if (a2 < ((i64)1 << 43)) {
 #pragma unroll
       for (int j = 0; j < VPT; ++j) {
-        const int c = threadIdx.x + j * (int)blockDim.x;
-        if (c < C) a.a8[off + c] = (int8_t)rhad_est_signed(v[j], D);
+        const int c = red.tid() + j * red.nt();
+        if (c < C) a8[c] = (int8_t)rhad_est_signed(v[j], D);
       }
     } else {
 #pragma unroll
       for (int j = 0; j < VPT; ++j) {
-        const int c = threadIdx.x + j * (int)blockDim.x;
-        if (c < C) a.a8[off + c] = (int8_t)rhad_est_corr_signed(v[j], 127, a2, D);
+        const int c = red.tid() + j * red.nt();
+        if (c < C) a8[c] = (int8_t)rhad_est_corr_signed(v[j], 127, a2, D);
       }
     }
   } else {
     const Recip R = make_recip(a2);
 #pragma unroll
     for (int j = 0; j < VPT; ++j) {
-      const int c = threadIdx.x + j * (int)blockDim.x;
-      if (c < C) a.a8[off + c] = (int8_t)clamp_i8(rhad_r(wmul(v[j], 127), R));
+      const int c = red.tid() + j * red.nt();
+      if (c < C) a8[c] = (int8_t)clamp_i8(rhad_r(wmul(v[j], 127), R));
     }
   }
-  if (threadIdx.x == 0) {
+  if (red.tid() == 0 && a.am) {
     i64 mo, e;
     fit_dyadic_ratio_127(a2, &mo, &e);
     a.am[r] = mo;
@@ -620,7 +639,7 @@ __global__ __launch_bounds__(RT) void k_op_requant_common(const int64_t* P, cons
   i64 v[VPT];
   load_row64(v, P, (i64)r * C, C);
   i64 cm[VPT];
-  prefetch_cols(cm, col_m + (i64)(r % G) * C, C);
+  prefetch_cols(cm, col_m + (i64)(r % G) * C, C, red);
   const i64 k = requant_common_row(v, cm, row_k[r], col_k, tb, red);
 #pragma unroll
   for (int j = 0; j < VPT; ++j) {
@@ -935,6 +954,166 @@ inline int grid_for(i64 n) {
   return (int)(g < 65536 ? (g < 1 ? 1 : g) : 65536);
 }
 
+// =====================================================================
+// Decode GEMV with its operand's row kernel fused in
+// =====================================================================
+//
+// At decode (R <= 8 rows) a skinny GEMM waits for the row kernel that makes
+// its int8 operand, and each of those launches is latency-bound: the row
+// kernel by its chain of block reductions and divisions, the GEMM by the
+// first loads of its weights. k_gemv_pro runs both in one launch: every block
+// first issues the loads of its weight slice (registers), then computes the
+// operand rows itself into LDS (the producing row kernel's body, the same
+// integers: one wave per row, wave-wide reductions; one row uses the whole
+// block), so the weight latency hides behind the row chain and the operand
+// never goes through global memory. Every block recomputes the same rows;
+// block (0, 0) alone stores the rows' other outputs (residual, row scales).
+//
+// Block: 512 threads, NB 16-column groups x one K split of the product; wave
+// w covers K [kbeg + 64 NI w, + 64 NI) with NI MFMA steps (kchunk = 512 NI)
+// for each group. The 8 waves' int32 accumulators are summed through LDS
+// (exact).
+
+constexpr int PRO_THREADS = 512;
+constexpr int PRO_ROWS = 8;
+constexpr int PRO_WAVES = PRO_THREADS / 64;
+
+struct ProGemv {
+  const int8_t* B;  // [N][K] weights
+  int32_t* C;       // [ksplit][R][N] int32 partials, split_stride elements apart
+  int R, N, K, kchunk;
+  i64 split_stride;
+};
+
+template <int CMAX, int NB>
+struct ProLds {
+  int8_t a[16][CMAX + 16];  // operand rows (rows >= R unused), padded against bank conflicts
+  int32_t red[PRO_WAVES - 1][NB][4][64];
+  i64 red_buf[32];
+};
+
+// PRO 1: residual_normq (ResNormArgs, mode 1, C = K <= CMAX); 2: merge_rowcol
+// (MergeArgs, C = K <= CMAX). ONE: a single row, computed by the whole block
+// (else one wave per row); separate instantiations keep the one-row kernel
+// free of the wave path's registers.
+template <int PRO, int CMAX, int NI, int NB, bool ONE>
+__global__ __launch_bounds__(PRO_THREADS) void k_gemv_pro(ProGemv g, ResNormArgs ra, MergeArgs ma,
+                                                         Prefetch pf) {
+  __shared__ __attribute__((aligned(16))) ProLds<CMAX, NB> L;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int bx = blockIdx.x, by = blockIdx.y;
+  const int kbeg = by * g.kchunk;
+  // 1. this wave's weight fragments, loaded before anything else
+  v4i b[NB][NI];
+#pragma unroll
+  for (int n = 0; n < NB; ++n) {
+    const int col = (bx * NB + n) * 16 + (lane & 15);
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+      const int k = kbeg + (wave * NI + i) * 64 + (lane >> 4) * 16;
+      b[n][i] = (col < g.N && k < g.K) ? *(const v4i*)(g.B + (i64)col * g.K + k) : zero4();
+    }
+  }
+  if (by == 0) prefetch_lines(pf, (i64)bx * PRO_THREADS + tid);
+  // 2. the operand rows into LDS
+  const bool lead = bx == 0 && by == 0;  // the block that stores the row outputs
+  if (PRO == 1) {
+    ResNormArgs a = ra;
+    a.x8 = &L.a[0][0];
+    a.x8_stride = CMAX + 16;
+    if (!lead) {
+      a.h = nullptr;
+      a.k_res = nullptr;
+      a.xm = nullptr;
+      a.xk = nullptr;
+    }
+    if (ONE) {
+      BlockRed red{L.red_buf, 0};
+      residual_normq_row<CMAX / PRO_THREADS>(a, 0, red);
+    } else if (wave < g.R) {
+      WaveRed red;
+      residual_normq_row<CMAX / 64>(a, wave, red);
+    }
+  } else {
+    MergeArgs a = ma;
+    a.a8 = &L.a[0][0];
+    a.a8_stride = CMAX + 16;
+    if (!lead) {
+      a.am = nullptr;
+      a.ak = nullptr;
+    }
+    if (ONE) {
+      BlockRed red{L.red_buf, 0};
+      merge_rowcol_row<CMAX / PRO_THREADS>(a, 0, red);
+    } else if (wave < g.R) {
+      WaveRed red;
+      merge_rowcol_row<CMAX / 64>(a, wave, red);
+    }
+  }
+  __syncthreads();
+  // 3. MFMAs: A rows from LDS (row lane % 16), B from registers
+  v4i acc[NB];
+#pragma unroll
+  for (int n = 0; n < NB; ++n) acc[n] = zero4();
+#pragma unroll
+  for (int i = 0; i < NI; ++i) {
+    const int k = kbeg + (wave * NI + i) * 64 + (lane >> 4) * 16;
+    const v4i a = k < g.K ? *(const v4i*)(&L.a[lane & 15][k]) : zero4();
+#pragma unroll
+    for (int n = 0; n < NB; ++n) acc[n] = mfma16(a, b[n][i], acc[n]);
+  }
+  if (wave > 0) {
+#pragma unroll
+    for (int n = 0; n < NB; ++n)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) L.red[wave - 1][n][r][lane] = acc[n][r];
+  }
+  __syncthreads();
+  if (wave > 0) return;
+#pragma unroll
+  for (int n = 0; n < NB; ++n) {
+    const int col = (bx * NB + n) * 16 + (lane & 15);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      int32_t s = acc[n][r];
+#pragma unroll
+      for (int w = 0; w < PRO_WAVES - 1; ++w) s += L.red[w][n][r][lane];
+      const int row = (lane >> 4) * 4 + r;
+      if (row < g.R && col < g.N) g.C[by * g.split_stride + (i64)row * g.N + col] = s;
+    }
+  }
+}
+
+// One launch of k_gemv_pro.
+template <int PRO, int CMAX, bool ONE>
+void launch_pro1(const ProGemv& g, int ni, int nb, dim3 grid, const ResNormArgs& ra,
+                 const MergeArgs& ma, const Prefetch& pf, hipStream_t s) {
+  const dim3 block(PRO_THREADS);
+#define DI_PRO_LAUNCH(NI_, NB_) \
+  hipLaunchKernelGGL((k_gemv_pro<PRO, CMAX, NI_, NB_, ONE>), grid, block, 0, s, g, ra, ma, pf)
+  if (nb == 1) {
+    if (ni == 1) DI_PRO_LAUNCH(1, 1);
+    else DI_PRO_LAUNCH(2, 1);
+  } else {
+    if (ni == 1) DI_PRO_LAUNCH(1, 2);
+    else DI_PRO_LAUNCH(2, 2);
+  }
+#undef DI_PRO_LAUNCH
+}
+
+template <int PRO, int CMAX>
+void launch_pro(const ProGemv& g, int ni, int ksplit, const ResNormArgs& ra, const MergeArgs& ma,
+                const Prefetch& pf, hipStream_t s) {
+  // NB = 2 when one column group per block would need more blocks than the
+  // chip has CUs (measured at one row, c3 b1: 1.635 ms per step against
+  // 1.670 with one group per block and 1.677 with up to four)
+  const int groups = (g.N + 15) / 16;
+  const int nb = (long)groups * ksplit > 256 ? 2 : 1;
+  const dim3 grid((groups + nb - 1) / nb, ksplit);
+  if (g.R == 1) launch_pro1<PRO, CMAX, true>(g, ni, nb, grid, ra, ma, pf, s);
+  else launch_pro1<PRO, CMAX, false>(g, ni, nb, grid, ra, ma, pf, s);
+}
+
 }  // namespace
 
 #define DI_VPT_DISPATCH(vpt, KERNEL, GRID, STREAM, ...)                                  \
@@ -1009,6 +1188,82 @@ int detllm_residual_normq(const int32_t* P, int nsplit, int64_t split_stride, in
   a.row_m = row_m; a.row_k = row_k; a.col_m = col_m; a.col_k = col_k; a.tb = tb;
   a.h = h; a.k_res = k_res; a.sm_m = sm_m; a.sm_k = sm_k; a.x8 = x8; a.xm = xm; a.xk = xk;
   DI_ROWS_DISPATCH(R, C, k_residual_normq, dim3(R), s, a);
+  DI_LAUNCH_CHECK();
+  return DI_OK;
+}
+
+// Prefetch ranges of the fused GEMVs (n a multiple of 4, 0 = unused)
+static bool pro_prefetch(const void* pf0, int64_t n0, const void* pf1, int64_t n1, Prefetch* pf) {
+  *pf = Prefetch{};
+  const void* ps[2] = {pf0, pf1};
+  const int64_t ns[2] = {n0, n1};
+  for (int i = 0; i < 2; ++i) {
+    if (ns[i] < 0 || (ns[i] > 0 && (!ps[i] || (ns[i] & 3) != 0 || ((uintptr_t)ps[i] & 3) != 0)))
+      return false;
+    pf->p[i] = (const int8_t*)ps[i];
+    pf->n[i] = ps[i] ? ns[i] : 0;
+  }
+  return true;
+}
+
+// The product's K split (detllm_igemv_plan) and the MFMA steps per wave it
+// gives, or 0 when the fused kernel does not cover the shape.
+static int pro_steps(int K, int ksplit, int* kchunk) {
+  if (K <= 0 || K % 16 != 0 || ksplit < 1) return 0;
+  *kchunk = gemv_kchunk(K, ksplit);
+  if ((K + *kchunk - 1) / *kchunk != ksplit || *kchunk % (PRO_THREADS) != 0) return 0;
+  const int ni = *kchunk / PRO_THREADS;
+  return ni <= 2 ? ni : 0;
+}
+
+int detllm_igemv_resnormq(const int8_t* W, int32_t* C, int R, int N, int K, int ksplit,
+                          int64_t split_stride, const int32_t* P, int nsplit,
+                          int64_t p_split_stride, const int64_t* row_m, const int64_t* row_k,
+                          const int64_t* col_m, int64_t col_k, int tb, const int32_t* h_in,
+                          const int64_t* k_res_in, int32_t* h_out, int64_t* k_res_out,
+                          const int64_t* sm_m, int64_t sm_k, int64_t* xm, int64_t* xk,
+                          const void* pf0, int64_t n0, const void* pf1, int64_t n1,
+                          hipStream_t s) {
+  if (R <= 0 || N <= 0) return DI_OK;
+  if (R > PRO_ROWS || K > 1024 || !W || !C || !P || nsplit < 1 || !row_m || !row_k || !col_m ||
+      !h_in || !k_res_in || !h_out || !k_res_out || !xm || !xk || (void*)h_in == (void*)h_out ||
+      (void*)k_res_in == (void*)k_res_out || (ksplit > 1 && split_stride < (int64_t)R * N))
+    return DI_EINVAL;
+  int kchunk = 0;
+  const int ni = pro_steps(K, ksplit, &kchunk);
+  if (ni == 0) return DI_ENOSYS;
+  Prefetch pf;
+  if (!pro_prefetch(pf0, n0, pf1, n1, &pf)) return DI_EINVAL;
+  ResNormArgs a{};
+  a.C = K; a.mode = 1; a.P = P; a.nsplit = nsplit; a.split_stride = p_split_stride;
+  a.row_m = row_m; a.row_k = row_k; a.col_m = col_m; a.col_k = col_k; a.tb = tb;
+  a.h_in = h_in; a.k_res_in = k_res_in; a.h = h_out; a.k_res = k_res_out; a.sm_m = sm_m;
+  a.sm_k = sm_k; a.xm = xm; a.xk = xk;
+  const ProGemv g{W, C, R, N, K, kchunk, (i64)split_stride};
+  launch_pro<1, 1024>(g, ni, ksplit, a, MergeArgs{}, pf, s);
+  DI_LAUNCH_CHECK();
+  return DI_OK;
+}
+
+int detllm_igemv_merge(const int8_t* W, int32_t* C, int R, int N, int K, int ksplit,
+                       int64_t split_stride, const int64_t* attn, int nsplit,
+                       int64_t a_split_stride, const int64_t* os_m, int64_t os_k,
+                       const int64_t* col_m, int64_t col_k, int64_t* am, int64_t* ak,
+                       const void* pf0, int64_t n0, const void* pf1, int64_t n1, hipStream_t s) {
+  if (R <= 0 || N <= 0) return DI_OK;
+  if (R > PRO_ROWS || K > 2048 || !W || !C || !attn || nsplit < 1 || !os_m || !am || !ak ||
+      (ksplit > 1 && split_stride < (int64_t)R * N))
+    return DI_EINVAL;
+  int kchunk = 0;
+  const int ni = pro_steps(K, ksplit, &kchunk);
+  if (ni == 0) return DI_ENOSYS;
+  Prefetch pf;
+  if (!pro_prefetch(pf0, n0, pf1, n1, &pf)) return DI_EINVAL;
+  MergeArgs m{};
+  m.C = K; m.attn = attn; m.nsplit = nsplit; m.split_stride = a_split_stride; m.os_m = os_m;
+  m.os_k = os_k; m.col_m = col_m; m.col_k = col_k; m.am = am; m.ak = ak;
+  const ProGemv g{W, C, R, N, K, kchunk, (i64)split_stride};
+  launch_pro<2, 2048>(g, ni, ksplit, ResNormArgs{}, m, pf, s);
   DI_LAUNCH_CHECK();
   return DI_OK;
 }

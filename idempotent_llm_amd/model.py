@@ -38,7 +38,7 @@ import torch
 
 from . import dyadic as dy
 from . import ops
-from ._lib import call, gemv_plan, raise_for_error_word
+from ._lib import call, gemv_plan, pro_fits, raise_for_error_word
 from .backends import canonical_backend, gemm_nt, int_gemm, int_gemm_u16i8
 from .guard import NoFloatMode
 from .kvcache import PAGE, KVCache  # noqa: F401  (KVCache is part of this module's API)
@@ -79,6 +79,7 @@ class LayerWeights:
     vq_m: torch.Tensor; vq_k: torch.Tensor
     attn_out_col_m: torch.Tensor
     attn_out_col_k: int
+    osc_m: torch.Tensor | None = None     # os_m * attn_out_col_m (fused o-GEMM)
     # the per-column scale vectors each row kernel reads, packed contiguously
     # so the skinny GEMM before it can prefetch them as one range
     pf_attn: torch.Tensor | None = None   # Q/K/V epilogue + attention-output merge
@@ -167,15 +168,27 @@ class IntQwen3:
                 attn_out_col_m=col_m.to(dev), attn_out_col_k=vk_shared + (P_OUT_BITS - 1)))
         del tensors
         for L in self.layers:
+            # the attention-output merge's per-column factor os_m * col_m
+            # (int64, wrapping as the kernel's own product does) for the
+            # fused o-GEMM
+            L.osc_m = L.os_m * L.attn_out_col_m
             L.pf_attn = _pack(L, ["q_m", "k_m", "v_m", "q_norm_m", "k_norm_m", "qs_m", "kq_m",
                                   "kq_k", "ks_m", "ks_k", "vq_m", "vq_k", "os_m",
-                                  "attn_out_col_m"])
+                                  "attn_out_col_m", "osc_m"])
             L.pf_o = _pack(L, ["o_m", "ms_m"])
             L.pf_mlp = _pack(L, ["gate_m", "up_m", "ds_m"])
             L.kq_est = torch.empty(L.kq_m.numel(), 4, dtype=I64, device=dev)
             call("detllm_kq_est", L.kq_m, L.kq_k, L.kq_m.numel(), 20 + L.k_norm_k, L.kq_est)
         self._greedy_scratch = {}
         self._plans: dict = {}
+        # decode rows run the fused-operand GEMVs where their shapes allow
+        L0 = self.layers[0]
+        nqkv, nqh = L0.wqkv.shape[0], self.n_q * self.hd
+        self._fused_decode = (
+            self.hidden <= 1024 and nqh <= 2048
+            and pro_fits(self.hidden, self._ksplit(nqkv, self.hidden))
+            and pro_fits(nqh, self._ksplit(self.hidden, nqh))
+            and pro_fits(self.hidden, self._ksplit(2 * self.inter, self.hidden)))
         # device error word of the index checks the reference does on the
         # host (IndexError from embed_e8[ids] / cos_t[positions]); the
         # kernels OR bits into it, raise_if_device_error() reads it
@@ -266,8 +279,15 @@ class IntQwen3:
             else:
                 cache.valid_buf[:, S_past:S] = chunk_valid.to(dev)
         H, R = self.hidden, B * T
-        h = torch.empty(R, H, dtype=torch.int32, device=dev)
-        k_res = torch.empty(R, dtype=I64, device=dev)
+        # one decode row: the GEMVs run their operand's row kernel themselves
+        # (at 2+ rows the fused prologue gives each row one wave, whose
+        # 64-bit chain over 16+ columns per lane outlasts the separate
+        # launches: c3 b8 2.35 vs 1.94 ms per step, b1 1.64 vs 1.80)
+        fused = T == 1 and R == 1 and self._fused_decode
+        # the fused decode stack double-buffers the residual (h = buffer 0)
+        hb = torch.empty(2 if fused else 1, R, H, dtype=torch.int32, device=dev)
+        kb = torch.empty(2 if fused else 1, R, dtype=I64, device=dev)
+        h, k_res = hb[0], kb[0]
         x8 = torch.empty(R, H, dtype=torch.int8, device=dev)
         xm = torch.empty(R, dtype=I64, device=dev)
         xk = torch.empty(R, dtype=I64, device=dev)
@@ -275,9 +295,12 @@ class IntQwen3:
         call("detllm_embed_normq", ids.contiguous().view(-1), R, H, self.vocab, self.embed_e8,
              self.embed_m, self.embed_k, h, k_res, L0.as_m, L0.as_k, x8, xm, xk, self._err)
         pos = positions.contiguous().view(-1)
-        for li, L in enumerate(self.layers):
-            nxt = self.layers[li + 1] if li + 1 < self.n_layers else None
-            self._layer(L, nxt, B, T, h, k_res, x8, xm, xk, pos, cache, S_past, S, static)
+        if fused:
+            self._layers_fused(B, hb, kb, x8, xm, xk, pos, cache, S_past, S, static)
+        else:
+            for li, L in enumerate(self.layers):
+                nxt = self.layers[li + 1] if li + 1 < self.n_layers else None
+                self._layer(L, nxt, B, T, h, k_res, x8, xm, xk, pos, cache, S_past, S, static)
         if not static:
             cache.length = S
         if head_rows is not None:
@@ -335,10 +358,17 @@ class IntQwen3:
 
     def _layer(self, L: LayerWeights, nxt, B, T, h, k_res, x8, xm, xk, pos, cache: KVCache,
                S_past, S, static):
-        dev = self.device
-        R, H, nq, nkv, hd, I_ = B * T, self.hidden, self.n_q, self.n_kv, self.hd, self.inter
-        li = L.idx
         P, ns, st = self._gemm(x8, L.wqkv, (L.pf_attn,))
+        attn = self._attend(L, B, T, P, ns, st, xm, xk, pos, cache, S_past, S, static)
+        self._after_attention(L, nxt, B, T, attn, h, k_res, x8, xm, xk)
+
+    def _attend(self, L: LayerWeights, B, T, P, ns, st, xm, xk, pos, cache: KVCache, S_past, S,
+                static) -> torch.Tensor:
+        """Q/K/V epilogue (cache write) and attention of one layer from the
+        QKV partials P: int64 context [B * T, n_q * hd]."""
+        dev = self.device
+        R, nq, nkv, hd = B * T, self.n_q, self.n_kv, self.hd
+        li = L.idx
         attn = torch.empty(R, nq * hd, dtype=I64, device=dev)
         valid = cache.valid_buf.view(torch.uint8)
         if T == 1 and nq // nkv <= 2:
@@ -355,7 +385,57 @@ class IntQwen3:
             self._attention_seams(L, B, T, P, ns, st, xm, xk, pos, cache, S_past, S, attn)
         else:
             self._attention(L, B, T, P, ns, st, xm, xk, pos, cache, S_past, S, static, attn)
-        self._after_attention(L, nxt, B, T, attn, h, k_res, x8, xm, xk)
+        return attn
+
+    def _partials(self, R: int, N: int, K: int):
+        ks = self._ksplit(N, K, R)
+        return torch.empty(ks, R, N, dtype=torch.int32, device=self.device), ks, R * N
+
+    def _layers_fused(self, B, hb, kb, x8, xm, xk, pos, cache, S_past, S, static):
+        """The decoder stack for a decode row (T == 1, B == 1) with each
+        skinny GEMM's operand row kernel fused into it (detllm_igemv_merge,
+        detllm_igemv_resnormq): per layer QKV-GEMM(+residual_normq of the
+        previous layer's down product) -> attention -> o-GEMM(+merge) ->
+        gate|up-GEMM(+residual_normq of the o product) -> SwiGLU -> down-GEMM;
+        the same integers as _layer's sequence. The residual alternates
+        between two buffers (a fused launch reads one while its lead block
+        writes the other): hb [2, B, H], kb [2, B] with the embedding's
+        residual in buffer 0."""
+        dev = self.device
+        R, H, nq, hd, I_ = B, self.hidden, self.n_q, self.hd, self.inter
+        cur = 0
+        am = torch.empty(R, dtype=I64, device=dev)
+        ak = torch.empty(R, dtype=I64, device=dev)
+        y8 = torch.empty(R, I_, dtype=torch.int8, device=dev)
+        ym = torch.empty(R, dtype=I64, device=dev)
+        yk = torch.empty(R, dtype=I64, device=dev)
+        L0 = self.layers[0]
+        P, ns, st = self._gemm(x8, L0.wqkv, (L0.pf_attn,))
+        for li, L in enumerate(self.layers):
+            nxt = self.layers[li + 1] if li + 1 < self.n_layers else None
+            attn = self._attend(L, B, 1, P, ns, st, xm, xk, pos, cache, S_past, S, static)
+            Po, nso, sto = self._partials(R, H, nq * hd)
+            call("detllm_igemv_merge", L.wo, Po, R, H, nq * hd, nso, sto, attn, 1, 0, L.osc_m,
+                 L.os_k, None, L.attn_out_col_k, am, ak, L.pf_o, L.pf_o.numel() * 8, None, 0)
+            Pg, nsg, stg = self._partials(R, 2 * I_, H)
+            call("detllm_igemv_resnormq", L.wgu, Pg, R, 2 * I_, H, nsg, stg, Po, nso, sto, am, ak,
+                 L.o_m, L.o_k, 20, hb[cur], kb[cur], hb[1 - cur], kb[1 - cur], L.ms_m, L.ms_k,
+                 xm, xk, L.pf_mlp, L.pf_mlp.numel() * 8, None, 0)
+            cur = 1 - cur
+            call("detllm_swiglu_quant", Pg, nsg, stg, R, I_, xm, xk, L.gate_m, L.gate_k, L.up_m,
+                 L.up_k, L.ds_m, L.ds_k, y8, ym, yk)
+            Pd, nsd, std = self._gemm(y8, L.wd, (L.down_m,) if nxt is None else
+                                      (L.down_m, nxt.as_m))
+            if nxt is None:
+                call("detllm_residual_normq", Pd, nsd, std, R, H, ym, yk, L.down_m, L.down_k, 20,
+                     hb[cur], kb[cur], None, 0, x8, xm, xk)
+                break
+            N = nxt.wqkv.shape[0]
+            P, ns, st = self._partials(R, N, H)
+            call("detllm_igemv_resnormq", nxt.wqkv, P, R, N, H, ns, st, Pd, nsd, std, ym, yk,
+                 L.down_m, L.down_k, 20, hb[cur], kb[cur], hb[1 - cur], kb[1 - cur], nxt.as_m,
+                 nxt.as_k, xm, xk, nxt.pf_attn, nxt.pf_attn.numel() * 8, None, 0)
+            cur = 1 - cur
 
     def _decode_scratch(self, B, S):
         """Global score scratch of the decode attention when the scores of a

@@ -125,6 +125,38 @@ int detllm_residual_normq(const int32_t* P, int nsplit, int64_t split_stride, in
                           const int64_t* sm_m, int64_t sm_k, int8_t* x8, int64_t* xm,
                           int64_t* xk, hipStream_t s);
 
+/* Decode skinny GEMMs with the row kernel that makes their int8 operand
+ * fused in (R <= 8 rows). Results equal the two launches they replace: the
+ * row kernel below, then detllm_igemv_nt into C [ksplit][R][N] with the K
+ * split of detllm_igemv_plan. Every block recomputes the operand rows (in
+ * LDS, while its weight loads are in flight); one block stores the rows'
+ * other outputs. Shapes outside the fused kernel's range return -38 (ENOSYS)
+ * and the caller runs the two launches.
+ *
+ * detllm_igemv_resnormq: operand = detllm_residual_normq of (P, row_m, row_k,
+ * col_m, col_k, tb) on the residual h_in / k_res_in — model.py:410-415,
+ * :424-427, :187-198 — which it writes to h_out / k_res_out (h_out must not
+ * alias h_in: other blocks still read it) and whose (m, k) go to xm / xk;
+ * K <= 1024. W [N][K] the next product's weights. */
+int detllm_igemv_resnormq(const int8_t* W, int32_t* C, int R, int N, int K, int ksplit,
+                          int64_t split_stride, const int32_t* P, int nsplit,
+                          int64_t p_split_stride, const int64_t* row_m, const int64_t* row_k,
+                          const int64_t* col_m, int64_t col_k, int tb, const int32_t* h_in,
+                          const int64_t* k_res_in, int32_t* h_out, int64_t* k_res_out,
+                          const int64_t* sm_m, int64_t sm_k, int64_t* xm, int64_t* xk,
+                          const void* pf0, int64_t n0, const void* pf1, int64_t n1,
+                          hipStream_t s);
+
+/* detllm_igemv_merge: operand = the attention-output merge
+ * requant_i8_rowcol(attn * os_m, 1, os_k, col_m, col_k) — model.py:404-409 —
+ * of int64 attn [nsplit][R][K], K <= 2048; col_m may be null when os_m holds
+ * the per-column product os_m * col_m. (m, k) to am / ak. */
+int detllm_igemv_merge(const int8_t* W, int32_t* C, int R, int N, int K, int ksplit,
+                       int64_t split_stride, const int64_t* attn, int nsplit,
+                       int64_t a_split_stride, const int64_t* os_m, int64_t os_k,
+                       const int64_t* col_m, int64_t col_k, int64_t* am, int64_t* ak,
+                       const void* pf0, int64_t n0, const void* pf1, int64_t n1, hipStream_t s);
+
 /* IntQwen3._norm_quant — model.py:187-198: di_rmsnorm(h) (ops/di_rmsnorm.py:33-52),
  * optional smoothing multiply by sm_m (null: none) with k 20 + sm_k, then
  * quant_i8_pertoken (dyadic.py:93-105). h [R][C] int32 is only read. */
