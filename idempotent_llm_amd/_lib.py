@@ -25,6 +25,7 @@ SIGNATURES = {
     "detllm_igemv_nt": [P, P, P, I, I, I, I, L, S],
     "detllm_igemv_nt_pf": [P, P, P, I, I, I, I, L, P, L, P, L, P, L, P, L, S],
     "detllm_igemv_plan": [I, I, I, P],
+    "detllm_attn_split_plan": [I, I, I, I, P, P],
     "detllm_transpose_i8": [P, P, I, I, I, L, L, S],
     "detllm_greedy_pick": [P, P, I, I, I, P, P, P, S],
     "detllm_greedy_pick_noalloc": [P, P, I, I, P, S],
@@ -32,6 +33,7 @@ SIGNATURES = {
     "detllm_embed_normq": [P, I, I, L, P, P, P, P, P, P, L, P, P, P, P, S],
     "detllm_residual_normq": [P, I, L, I, I, P, P, P, L, I, P, P, P, L, P, P, P, S],
     "detllm_norm_quant": [P, I, I, P, L, P, P, P, S],
+    "detllm_attn_decode_split": [P, P, P, P, P, I, P, L, I, I, I, I, P, I, P, P, P, P, S],
     "detllm_igemv_resnormq": [P, P, I, I, I, I, L, P, I, L, P, P, P, L, I, P, P, P, P, P, L, P,
                               P, P, L, P, L, S],
     "detllm_igemv_merge": [P, P, I, I, I, I, L, P, I, L, P, L, P, L, P, P, P, L, P, L, S],
@@ -60,7 +62,7 @@ SIGNATURES = {
 }
 
 # host-only entry points (no device work, so no stream argument)
-HOST_ONLY = frozenset({"detllm_igemv_plan"})
+HOST_ONLY = frozenset({"detllm_igemv_plan", "detllm_attn_split_plan"})
 
 _CT = {P: ctypes.c_void_p, I: ctypes.c_int, L: ctypes.c_int64, S: ctypes.c_void_p}
 
@@ -114,6 +116,17 @@ def gemv_plan(M: int, N: int, K: int) -> int:
     if rc != 0:
         raise RuntimeError(f"detllm_igemv_plan failed (code {rc})")
     return out.value
+
+
+def attn_split_plan(B: int, S: int, n_q: int, n_kv: int):
+    """(chunk, nsplit) of the split-S decode attention at this shape."""
+    lib = load()
+    ch, ns = ctypes.c_int(0), ctypes.c_int(0)
+    rc = lib.detllm_attn_split_plan(int(B), int(S), int(n_q), int(n_kv), ctypes.byref(ch),
+                                    ctypes.byref(ns))
+    if rc != 0:
+        raise RuntimeError(f"detllm_attn_split_plan failed (code {rc})")
+    return ch.value, ns.value
 
 
 def pro_fits(K: int, ksplit: int) -> bool:

@@ -499,6 +499,49 @@ __device__ __forceinline__ int32_t row16_max(int32_t v) {
 // Slots past S read zero V fragments (16-slot chunks starting at or past S),
 // so their A values do not matter; the p of slots S .. ceil16(S) are 0.
 // |accumulators| <= 128 * 128 * S < 2^31 for S <= 131071.
+// p in [0, 2^14] packed as (hi - 64) | lo << 8 (p = 128 hi + lo; p = 0 packs
+// as hi - 64 = -64, lo = 0)
+__device__ __forceinline__ int32_t pack_p(i64 p) {
+  const int hi = (int)(p >> 7), lo = (int)(p & 127);
+  return (int32_t)((uint32_t)(uint8_t)(int8_t)(hi - 64) | ((uint32_t)lo << 8));
+}
+
+// MFMA A fragments of 16 packed p words (16 consecutive slots of one head):
+// bytes 0 of the words -> hi - 64 fragment, bytes 1 -> lo
+__device__ __forceinline__ void p_frags(const int32_t* pp, v4i& ahi, v4i& alo) {
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const v4i w = *(const v4i*)(pp + 4 * q);
+    const uint32_t h01 = __builtin_amdgcn_perm((uint32_t)w[1], (uint32_t)w[0], 0x0c0c0400u);
+    const uint32_t h23 = __builtin_amdgcn_perm((uint32_t)w[3], (uint32_t)w[2], 0x04000c0cu);
+    const uint32_t l01 = __builtin_amdgcn_perm((uint32_t)w[1], (uint32_t)w[0], 0x0c0c0501u);
+    const uint32_t l23 = __builtin_amdgcn_perm((uint32_t)w[3], (uint32_t)w[2], 0x05010c0cu);
+    ahi[q] = (int)(h01 | h23);
+    alo[q] = (int)(l01 | l23);
+  }
+}
+
+// sum_s p_s v_s of the wave's channels from the hi/lo accumulators: lane
+// (grp, l16), element r holds head 4 grp + r, channel 32 wave + 16 nb + l16;
+// the colsum of that channel sits in row G (lane 16 (G / 4) + l16, element
+// G % 4). out_heads: the block's first head row of [.][128] int64.
+template <int G>
+__device__ __forceinline__ void store_pv(const v4i (&chi)[2], const v4i (&clo)[2],
+                                         int64_t* out_heads) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, l16 = lane & 15, grp = lane >> 4;
+#pragma unroll
+  for (int nb = 0; nb < 2; ++nb) {
+    const int cs_src = (G / 4) * 16 + l16;
+    const int32_t cs = __shfl(chi[nb][G % 4], cs_src, 64);
+    const int d = wave * 32 + nb * 16 + l16;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int hh = grp * 4 + r;
+      if (hh < G) out_heads[hh * 128 + d] = ((i64)chi[nb][r] + 64 * (i64)cs) * 128 + (i64)clo[nb][r];
+    }
+  }
+}
+
 // K rows and validity flags of a wave's first 16-slot blocks, loaded before
 // the fused kernel's Q/K/V epilogue so that their latency hides behind it;
 // the slot the epilogue writes is taken from LDS instead.
@@ -650,10 +693,7 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, int kvh, int b,
   const int nchunk = (S + 15) / 16;
 #pragma unroll
   for (int hh = 0; hh < G; ++hh) {
-    auto put = [&](int s, i64 p) {
-      const int hi = (int)(p >> 7), lo = (int)(p & 127);
-      sc[hh * Spad + s] = (int32_t)((uint32_t)(uint8_t)(int8_t)(hi - 64) | ((uint32_t)lo << 8));
-    };
+    auto put = [&](int s, i64 p) { sc[hh * Spad + s] = pack_p(p); };
     if (tph[hh] < ((i64)1 << 23) && den[hh] < ((i64)1 << 34)) {
       // exps below 2^23, den < 2^34: p = rhad(ex 2^14, den) from rhad_est
       const ExpEst Ee = make_expest(tph[hh]);
@@ -689,18 +729,7 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, int kvh, int b,
     v4i ahi = v4i{0, 0, 0, 0}, alo = v4i{0, 0, 0, 0};
     const int s0 = st * 64 + grp * 16;
     if (l16 < G && s0 < S) {
-      const int32_t* pp = sc + l16 * Spad + s0;  // 16 packed p of head l16
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const v4i w = *(const v4i*)(pp + 4 * q);
-        // bytes 0 of the four words -> hi - 64 fragment, bytes 1 -> lo
-        const uint32_t h01 = __builtin_amdgcn_perm((uint32_t)w[1], (uint32_t)w[0], 0x0c0c0400u);
-        const uint32_t h23 = __builtin_amdgcn_perm((uint32_t)w[3], (uint32_t)w[2], 0x04000c0cu);
-        const uint32_t l01 = __builtin_amdgcn_perm((uint32_t)w[1], (uint32_t)w[0], 0x0c0c0501u);
-        const uint32_t l23 = __builtin_amdgcn_perm((uint32_t)w[3], (uint32_t)w[2], 0x05010c0cu);
-        ahi[q] = (int)(h01 | h23);
-        alo[q] = (int)(l01 | l23);
-      }
+      p_frags(sc + l16 * Spad + s0, ahi, alo);  // 16 packed p of head l16
     } else if (l16 == G) {
       ahi = v4i{0x01010101, 0x01010101, 0x01010101, 0x01010101};  // colsum row
     }
@@ -723,22 +752,7 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, int kvh, int b,
     for (int i = 0; i < 4; ++i)
       if (st0 + i < nstep) pv_step(st0 + i, vb[i]);
   }
-  // lane (grp, l16), element r: head 4 grp + r, channel 32 wave + 16 nb + l16;
-  // the colsum of that channel sits in row G: lane 16 (G / 4) + l16, element G % 4
-#pragma unroll
-  for (int nb = 0; nb < 2; ++nb) {
-    const int cs_src = (G / 4) * 16 + l16;
-    const int32_t cs = __shfl(chi[nb][G % 4], cs_src, 64);
-    const int d = wave * 32 + nb * 16 + l16;
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int hh = grp * 4 + r;
-      if (hh < G) {
-        const i64 v = ((i64)chi[nb][r] + 64 * (i64)cs) * 128 + (i64)clo[nb][r];
-        a.out[(i64)b * a.n_q * 128 + (kvh * G + hh) * 128 + d] = v;
-      }
-    }
-  }
+  store_pv<G>(chi, clo, a.out + (i64)b * a.n_q * 128 + kvh * G * 128);
 }
 
 template <int G>
@@ -812,6 +826,246 @@ __global__ __launch_bounds__(256) void k_qkv_attn_decode(DecodeArgs a, QKVArgs q
   }
   __syncthreads();
   decode_body<G>(a, kvh, b, &q_lds[0][0], t_lds, sh_scores, pg_lds, &pre);
+}
+
+// ---------------------------------------------------------------------------
+// Split-S decode attention: the slots of a (row, kv head) are cut into chunks
+// of `chunk` slots (a multiple of the page), one block per chunk, in two
+// launches:
+//   k_attn_split_scores: the chunk's scores (int32, to a global scratch) and
+//     its per-head maximum over visible slots;
+//   k_attn_split_pv: the row maximum (the maximum of the chunk maxima — the
+//     TRUE row max, DI-Exp being not multiplicative), the denominator over
+//     ALL the row's slots (every block sums the same integers, so every block
+//     holds the same den), then p of the chunk's slots and their P.V into the
+//     chunk's own int64 partial context.
+// The context is the sum of the partials (exact integer addition, in any
+// order); the attention-output merge sums them. Same integers as
+// k_attn_decode for every chunking.
+
+constexpr int SPLIT_MAX_CHUNK = 4096;                  // slots per chunk
+constexpr int SPLIT_MAX_PAGES = SPLIT_MAX_CHUNK / DI_PAGE;
+
+struct SplitArgs {
+  DecodeArgs d;     // scratch: scores [B][n_q][spad]; out: partials [ns][B][n_q * 128]
+  int32_t* cmax;    // [B][n_q][ns] chunk maxima (SCORE_MASKED: no visible slot)
+  int chunk, ns;
+  i64 spad;         // row stride of the scores (>= S)
+  i64 out_stride;   // elements between partials (B * n_q * 128)
+};
+
+// Slots a decode block scans: S, bounded by the device count when given (the
+// count beyond S is reported by one block, as k_attn_decode does).
+__device__ __forceinline__ int scanned_slots(const DecodeArgs& a, bool report) {
+  int S = a.S;
+  if (a.s_dev) {
+    const i64 sd = a.s_dev[0];
+    if (sd > (i64)S && report && a.err && threadIdx.x == 0) atomicOr(a.err, DI_ERR_SLOTS);
+    S = (int)imax(0, imin((i64)S, sd));
+  }
+  return S;
+}
+
+template <int G>
+__global__ __launch_bounds__(256) void k_attn_split_scores(SplitArgs sa) {
+  const DecodeArgs& a = sa.d;
+  __shared__ i64 red_buf[32];
+  __shared__ int32_t pg_lds[SPLIT_MAX_PAGES];
+  BlockRed red{red_buf, 0};
+  const int kvh = blockIdx.x, b = blockIdx.y, c = blockIdx.z;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, l16 = lane & 15, grp = lane >> 4;
+  const int S = scanned_slots(a, kvh == 0 && c == 0);
+  const int lo = c * sa.chunk, hi = ::min(lo + sa.chunk, S);
+  const i64 q0 = (i64)b * a.n_q + kvh * G;
+  int32_t* cm = sa.cmax + q0 * sa.ns + c;  // head hh at cm[hh * ns]
+  if (lo >= hi) {  // block-uniform: a chunk past the scanned slots
+    if (tid < G) cm[tid * sa.ns] = SCORE_MASKED;
+    return;
+  }
+  const int npg = (hi - lo + DI_PAGE - 1) / DI_PAGE;
+  if (tid < npg) pg_lds[tid] = a.kv.page(b, (i64)lo + (i64)tid * DI_PAGE);
+  v4i qa0 = v4i{0, 0, 0, 0}, qa1 = v4i{0, 0, 0, 0};
+  if (l16 < G) {
+    const int8_t* qsrc = a.q8 + q0 * 128;
+    qa0 = *(const v4i*)(qsrc + l16 * 128 + grp * 16);
+    qa1 = *(const v4i*)(qsrc + l16 * 128 + 64 + grp * 16);
+  }
+  __syncthreads();
+  int32_t* sc = a.scratch + q0 * sa.spad;
+  const uint8_t* vrow = a.valid + (i64)b * a.valid_stride;
+  int32_t mx[4] = {SCORE_MASKED, SCORE_MASKED, SCORE_MASKED, SCORE_MASKED};
+  const int blo = lo / 16, bhi = (hi + 15) / 16;
+  for (int blk0 = blo + wave; blk0 < bhi; blk0 += 16) {
+    v4i kb[4][2];
+    int vf[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int s = (blk0 + u * 4) * 16 + l16;
+      const int sc_ = s < hi ? s : lo;
+      const int pg = pg_lds[(sc_ - lo) / DI_PAGE];
+      const int8_t* kr = a.kv.krow(pg < 0 ? 0 : pg, kvh, sc_ & (DI_PAGE - 1));
+      kb[u][0] = *(const v4i*)(kr + grp * 16);
+      kb[u][1] = *(const v4i*)(kr + 64 + grp * 16);
+      vf[u] = pg >= 0 ? vrow[sc_] : 0;
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int blk = blk0 + u * 4;
+      if (blk < bhi) {  // wave-uniform
+        v4i cc = mfma16(qa0, kb[u][0], v4i{0, 0, 0, 0});
+        cc = mfma16(qa1, kb[u][1], cc);
+        const int s = blk * 16 + l16;
+        const bool vis = s < hi && vf[u] != 0;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int hh = grp * 4 + r;
+          if (hh < G) {
+            if (s < hi) sc[hh * sa.spad + s] = vis ? cc[r] : SCORE_MASKED;
+            if (vis) mx[r] = ::max(mx[r], cc[r]);
+          }
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < 4; ++r) mx[r] = row16_max(mx[r]);
+#pragma unroll
+  for (int hh = 0; hh < G; ++hh) {
+    const int32_t mine = grp == hh / 4 ? mx[hh % 4] : SCORE_MASKED;
+    const i64 m = red.max((i64)mine);
+    if (tid == 0) cm[hh * sa.ns] = (int32_t)m;
+  }
+}
+
+template <int G>
+__global__ __launch_bounds__(256) void k_attn_split_pv(SplitArgs sa) {
+  const DecodeArgs& a = sa.d;
+  extern __shared__ __attribute__((aligned(16))) int32_t p_lds[];  // [G][chunk] packed p
+  __shared__ i64 red_buf[32];
+  __shared__ int32_t pg_lds[SPLIT_MAX_PAGES];
+  BlockRed red{red_buf, 0};
+  const int kvh = blockIdx.x, b = blockIdx.y, c = blockIdx.z;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, l16 = lane & 15, grp = lane >> 4;
+  const int S = scanned_slots(a, false);
+  const int lo = c * sa.chunk, hi = ::min(lo + sa.chunk, S);
+  const i64 q0 = (i64)b * a.n_q + kvh * G;
+  int64_t* outp = a.out + c * sa.out_stride + q0 * 128;
+  if (lo >= hi) {  // block-uniform: this chunk contributes nothing
+    for (int i = tid; i < G * 128; i += 256) outp[i] = 0;
+    return;
+  }
+  const int npg = (hi - lo + DI_PAGE - 1) / DI_PAGE;
+  if (tid < npg) pg_lds[tid] = a.kv.page(b, (i64)lo + (i64)tid * DI_PAGE);
+  i64 tph[G], hmax[G];
+#pragma unroll
+  for (int hh = 0; hh < G; ++hh) {
+    tph[hh] = a.tpos[q0 + hh];
+    i64 m = SCORE_MASKED;
+    const int32_t* cmh = sa.cmax + (q0 + hh) * sa.ns;
+    for (int k = 0; k < sa.ns; ++k) m = imax(m, (i64)cmh[k]);
+    hmax[hh] = m == (i64)SCORE_MASKED ? 0 : m;  // no visible slot: max := 0, every p = 0
+  }
+  __syncthreads();
+  // V fragments of the chunk's first VPRE 64-slot steps (a step lies in one
+  // page), loaded before the denominator pass
+  auto vfrag = [&](int st, int nb) -> v4i {
+    const int s0 = st * 64 + grp * 16;
+    if (s0 >= hi) return v4i{0, 0, 0, 0};
+    const int pg = pg_lds[(s0 - lo) / DI_PAGE];
+    const int8_t* vch = a.kv.vchan(pg < 0 ? 0 : pg, kvh, wave * 32 + nb * 16 + l16);
+    return *(const v4i*)(vch + (s0 & (DI_PAGE - 1)));
+  };
+  const int st_lo = lo / 64, st_hi = (hi + 63) / 64;
+  v4i vpre[VPRE][2];
+#pragma unroll
+  for (int i = 0; i < VPRE; ++i)
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb) vpre[i][nb] = st_lo + i < st_hi ? vfrag(st_lo + i, nb) : v4i{0, 0, 0, 0};
+  const int32_t* sc = a.scratch + q0 * sa.spad;
+  // denominators over every scanned slot of the row
+  i64 den[G];
+#pragma unroll
+  for (int hh = 0; hh < G; ++hh) {
+    i64 acc = 0;
+    if (tph[hh] < ((i64)1 << 23)) {
+      const ExpEst Ee = make_expest(tph[hh]);
+      for (int s = tid; s < S; s += 256) {
+        const int32_t x = sc[hh * sa.spad + s];
+        if (x != SCORE_MASKED) acc += dexp_est((uint32_t)(hmax[hh] - x), Ee);
+      }
+    } else {
+      const ExpR E = make_exp(tph[hh]);
+      for (int s = tid; s < S; s += 256) {
+        const int32_t x = sc[hh * sa.spad + s];
+        if (x != SCORE_MASKED) acc = wadd(acc, di_exp_neg((u64)wsub(hmax[hh], (i64)x), E));
+      }
+    }
+    den[hh] = imax(red.sum(acc), 1);
+  }
+  // p of the chunk's slots, packed into LDS (0 for masked slots and the
+  // padding to the next multiple of 16)
+  const int n16 = (hi - lo + 15) / 16 * 16;
+#pragma unroll
+  for (int hh = 0; hh < G; ++hh) {
+    int32_t* ph = p_lds + hh * sa.chunk;
+    if (tph[hh] < ((i64)1 << 23) && den[hh] < ((i64)1 << 34)) {
+      const ExpEst Ee = make_expest(tph[hh]);
+      const DivEst D = make_divest(den[hh], 16384.0);
+      for (int i = tid; i < n16; i += 256) {
+        i64 p = 0;
+        if (lo + i < hi) {
+          const int32_t x = sc[hh * sa.spad + lo + i];
+          if (x != SCORE_MASKED) p = rhad_est((double)dexp_est((uint32_t)(hmax[hh] - x), Ee), D);
+        }
+        ph[i] = pack_p(p);
+      }
+    } else {
+      const ExpR E = make_exp(tph[hh]);
+      const Recip Rd = make_recip(den[hh]);
+      for (int i = tid; i < n16; i += 256) {
+        i64 p = 0;
+        if (lo + i < hi) {
+          const int32_t x = sc[hh * sa.spad + lo + i];
+          if (x != SCORE_MASKED) {
+            const i64 ex = di_exp_neg((u64)wsub(hmax[hh], (i64)x), E);
+            p = to_i32(rhad_r(shl(ex, 14), Rd));
+          }
+        }
+        ph[i] = pack_p(p);
+      }
+    }
+  }
+  __syncthreads();
+  // P.V of the chunk
+  v4i chi[2] = {v4i{0, 0, 0, 0}, v4i{0, 0, 0, 0}}, clo[2] = {v4i{0, 0, 0, 0}, v4i{0, 0, 0, 0}};
+  auto pv_step = [&](int st, const v4i (&vb)[2]) {
+    v4i ahi = v4i{0, 0, 0, 0}, alo = v4i{0, 0, 0, 0};
+    const int s0 = st * 64 + grp * 16;
+    if (l16 < G && s0 < hi) {
+      p_frags(p_lds + l16 * sa.chunk + (s0 - lo), ahi, alo);
+    } else if (l16 == G) {
+      ahi = v4i{0x01010101, 0x01010101, 0x01010101, 0x01010101};  // colsum row
+    }
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb) {
+      chi[nb] = mfma16(ahi, vb[nb], chi[nb]);
+      clo[nb] = mfma16(alo, vb[nb], clo[nb]);
+    }
+  };
+#pragma unroll
+  for (int i = 0; i < VPRE; ++i)
+    if (st_lo + i < st_hi) pv_step(st_lo + i, vpre[i]);
+  for (int st0 = st_lo + VPRE; st0 < st_hi; st0 += 4) {
+    v4i vb[4][2];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int nb = 0; nb < 2; ++nb) vb[i][nb] = st0 + i < st_hi ? vfrag(st0 + i, nb) : v4i{0, 0, 0, 0};
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      if (st0 + i < st_hi) pv_step(st0 + i, vb[i]);
+  }
+  store_pv<G>(chi, clo, outp);
 }
 
 }  // namespace
@@ -934,6 +1188,72 @@ int detllm_qkv_attn_decode(const int32_t* P, int nsplit, int64_t split_stride, i
     hipLaunchKernelGGL(k_qkv_attn_decode<1>, grid, dim3(256), dyn, s, a, qa);
   else
     hipLaunchKernelGGL(k_qkv_attn_decode<2>, grid, dim3(256), dyn, s, a, qa);
+  DI_LAUNCH_CHECK();
+  return DI_OK;
+}
+
+// Chunking of the split-S decode attention: enough chunks that the launch has
+// about 1024 blocks (four per CU; c4, 32 rows x 8 kv heads at 4096 slots:
+// 3.88 ms per step at 1024-slot chunks against 4.41 at 512, 4.20 at 2048 —
+// every block sums the whole row's denominator, so more chunks cost more),
+// chunks of at least 256 slots, a multiple of the page, within the LDS of
+// the packed p (G * chunk * 4 bytes <= 48 KiB) and SPLIT_MAX_CHUNK.
+int detllm_attn_split_plan(int B, int S, int n_q, int n_kv, int* chunk, int* nsplit) {
+  if (!chunk || !nsplit || B <= 0 || S <= 0 || n_q <= 0 || n_kv <= 0 || n_q % n_kv) return DI_EINVAL;
+  const int G = n_q / n_kv;
+  if (G > MAXG) return DI_ENOSYS;
+  const i64 blocks = (i64)B * n_kv;
+  const i64 want = blocks >= 1024 ? 1 : (1024 + blocks - 1) / blocks;
+  i64 ch = ((i64)S + want - 1) / want;
+  ch = (ch + DI_PAGE - 1) / DI_PAGE * DI_PAGE;
+  i64 cmax = DECODE_LDS_BYTES / (4 * G) / DI_PAGE * DI_PAGE;
+  if (cmax > SPLIT_MAX_CHUNK) cmax = SPLIT_MAX_CHUNK;
+  ch = imax(imin(ch, cmax), (i64)2 * DI_PAGE);
+  *chunk = (int)ch;
+  *nsplit = (int)(((i64)S + ch - 1) / ch);
+  return DI_OK;
+}
+
+// Split-S decode attention (one query token per row; q8, tpos as written by
+// detllm_qkv_epilogue with T = 1). scores: int32 [B][n_q][nsplit * chunk];
+// cmax: int32 [B][n_q][nsplit]; out: int64 partial contexts
+// [nsplit][B][n_q * 128] whose sum is detllm_attn_decode's out.
+int detllm_attn_decode_split(const int8_t* q8, const int64_t* tpos, const int8_t* kpool,
+                             const int8_t* vpool, const int32_t* table, int width,
+                             const uint8_t* valid, int64_t valid_stride, int B, int S, int n_q,
+                             int n_kv, const int64_t* s_dev, int chunk, int32_t* scores,
+                             int32_t* cmax, int64_t* out, int32_t* err, hipStream_t s) {
+  if (B <= 0) return DI_OK;
+  if (n_q <= 0 || n_kv <= 0 || n_q % n_kv || S < 1 || !kv_ok(kpool, vpool, table, width) ||
+      S > (i64)width * DI_PAGE || valid_stride < S || !q8 || !tpos || !valid || !out || !scores ||
+      !cmax || chunk < DI_PAGE || chunk % DI_PAGE || chunk > SPLIT_MAX_CHUNK)
+    return DI_EINVAL;
+  const int G = n_q / n_kv;
+  if (G > MAXG) return DI_ENOSYS;
+  if (S > DEC_MAX_S) return DI_ERANGE;  // int32 MFMA accumulators of P.V
+  const i64 dyn = (i64)G * chunk * 4;
+  if (dyn > DECODE_LDS_BYTES) return DI_ERANGE;
+  const int ns = (S + chunk - 1) / chunk;
+  SplitArgs sa{};
+  sa.d = DecodeArgs{q8, tpos, KVPages{(int8_t*)kpool, (int8_t*)vpool, table, width, n_kv}, valid,
+                    out, scores, s_dev, S, n_q, n_kv, valid_stride, err};
+  sa.cmax = cmax;
+  sa.chunk = chunk;
+  sa.ns = ns;
+  sa.spad = (i64)ns * chunk;
+  sa.out_stride = (i64)B * n_q * 128;
+  const dim3 grid(n_kv, B, ns);
+#define DI_SPLIT_LAUNCH(G_)                                                                   \
+  hipLaunchKernelGGL(k_attn_split_scores<G_>, grid, dim3(256), 0, s, sa);                     \
+  hipLaunchKernelGGL(k_attn_split_pv<G_>, grid, dim3(256), (size_t)dyn, s, sa)
+  switch (G) {
+    case 1: DI_SPLIT_LAUNCH(1); break;
+    case 2: DI_SPLIT_LAUNCH(2); break;
+    case 4: DI_SPLIT_LAUNCH(4); break;
+    case 8: DI_SPLIT_LAUNCH(8); break;
+    default: return DI_ENOSYS;
+  }
+#undef DI_SPLIT_LAUNCH
   DI_LAUNCH_CHECK();
   return DI_OK;
 }

@@ -38,7 +38,7 @@ import torch
 
 from . import dyadic as dy
 from . import ops
-from ._lib import call, gemv_plan, pro_fits, raise_for_error_word
+from ._lib import attn_split_plan, call, gemv_plan, pro_fits, raise_for_error_word
 from .backends import canonical_backend, gemm_nt, int_gemm, int_gemm_u16i8
 from .guard import NoFloatMode
 from .kvcache import PAGE, KVCache  # noqa: F401  (KVCache is part of this module's API)
@@ -50,6 +50,8 @@ GREEDY_CHUNK = 2048
 # slots the decode attention scans at most (int32 MFMA accumulators of P.V:
 # 128 * 128 * S < 2^31)
 DEC_MAX_SLOTS = 131071
+# decode rows scanning at least this many slots use the split-S attention
+SPLIT_MIN_SLOTS = 2048
 
 
 @dataclass
@@ -181,6 +183,7 @@ class IntQwen3:
             call("detllm_kq_est", L.kq_m, L.kq_k, L.kq_m.numel(), 20 + L.k_norm_k, L.kq_est)
         self._greedy_scratch = {}
         self._plans: dict = {}
+        self._split_plans: dict = {}
         # decode rows run the fused-operand GEMVs where their shapes allow
         L0 = self.layers[0]
         nqkv, nqh = L0.wqkv.shape[0], self.n_q * self.hd
@@ -362,15 +365,48 @@ class IntQwen3:
         attn = self._attend(L, B, T, P, ns, st, xm, xk, pos, cache, S_past, S, static)
         self._after_attention(L, nxt, B, T, attn, h, k_res, x8, xm, xk)
 
+    def _split_plan(self, B: int, S: int):
+        """(chunk, nsplit) of the split-S decode attention, or None when the
+        one-block-per-(row, kv head) kernel is used (fewer slots than
+        SPLIT_MIN_SLOTS, or one chunk)."""
+        if S < SPLIT_MIN_SLOTS:
+            return None
+        key = (B, S)
+        plan = self._split_plans.get(key)
+        if plan is None:
+            plan = attn_split_plan(B, S, self.n_q, self.n_kv)
+            self._split_plans[key] = plan
+        return plan if plan[1] > 1 else None
+
     def _attend(self, L: LayerWeights, B, T, P, ns, st, xm, xk, pos, cache: KVCache, S_past, S,
-                static) -> torch.Tensor:
+                static):
         """Q/K/V epilogue (cache write) and attention of one layer from the
-        QKV partials P: int64 context [B * T, n_q * hd]."""
+        QKV partials P. Returns (attn, nsplit, split_stride): int64 context
+        partials [nsplit][B * T][n_q * hd] whose sum is the context."""
         dev = self.device
         R, nq, nkv, hd = B * T, self.n_q, self.n_kv, self.hd
         li = L.idx
-        attn = torch.empty(R, nq * hd, dtype=I64, device=dev)
         valid = cache.valid_buf.view(torch.uint8)
+        plan = self._split_plan(B, S) if T == 1 else None
+        if plan is not None:
+            # long rows: Q/K/V epilogue, then the split-S attention
+            chunk, nsp = plan
+            q8 = torch.empty(B, nq, 1, hd, dtype=torch.int8, device=dev)
+            tpos = torch.empty(B, nq, 1, dtype=I64, device=dev)
+            call("detllm_qkv_epilogue", P, ns, st, B, 1, nq, nkv, xm, xk, pos,
+                 L.q_m, L.q_k, L.k_m, L.k_k, L.v_m, L.v_k, L.q_norm_m, L.q_norm_k,
+                 L.k_norm_m, L.k_norm_k, L.qs_m, L.qs_k, L.kq_m, L.kq_k, L.ks_m, L.ks_k,
+                 L.vq_m, L.vq_k, self.rope_cos, self.rope_sin, self.max_pos, q8, tpos, None,
+                 *cache.layer_args(li), cache.len_idx if static else None,
+                 0 if static else S_past, L.kq_est, self._err)
+            scores = torch.empty(B, nq, nsp * chunk, dtype=torch.int32, device=dev)
+            cmax = torch.empty(B, nq, nsp, dtype=torch.int32, device=dev)
+            attn = torch.empty(nsp, R, nq * hd, dtype=I64, device=dev)
+            call("detllm_attn_decode_split", q8, tpos, *cache.layer_args(li), valid, cache.cap,
+                 B, S, nq, nkv, cache.nslots if static else None, chunk, scores, cmax, attn,
+                 self._err)
+            return attn, nsp, R * nq * hd
+        attn = torch.empty(R, nq * hd, dtype=I64, device=dev)
         if T == 1 and nq // nkv <= 2:
             # decode: Q/K/V epilogue and attention in one launch
             scratch = self._decode_scratch(B, S)
@@ -385,7 +421,7 @@ class IntQwen3:
             self._attention_seams(L, B, T, P, ns, st, xm, xk, pos, cache, S_past, S, attn)
         else:
             self._attention(L, B, T, P, ns, st, xm, xk, pos, cache, S_past, S, static, attn)
-        return attn
+        return attn, 1, 0
 
     def _partials(self, R: int, N: int, K: int):
         ks = self._ksplit(N, K, R)
@@ -415,7 +451,7 @@ class IntQwen3:
             nxt = self.layers[li + 1] if li + 1 < self.n_layers else None
             attn = self._attend(L, B, 1, P, ns, st, xm, xk, pos, cache, S_past, S, static)
             Po, nso, sto = self._partials(R, H, nq * hd)
-            call("detllm_igemv_merge", L.wo, Po, R, H, nq * hd, nso, sto, attn, 1, 0, L.osc_m,
+            call("detllm_igemv_merge", L.wo, Po, R, H, nq * hd, nso, sto, *attn, L.osc_m,
                  L.os_k, None, L.attn_out_col_k, am, ak, L.pf_o, L.pf_o.numel() * 8, None, 0)
             Pg, nsg, stg = self._partials(R, 2 * I_, H)
             call("detllm_igemv_resnormq", L.wgu, Pg, R, 2 * I_, H, nsg, stg, Po, nso, sto, am, ak,
@@ -519,12 +555,13 @@ class IntQwen3:
         attn.copy_(a.permute(0, 2, 1, 3).reshape(B * T, nq * hd))
 
     def _after_attention(self, L, nxt, B, T, attn, h, k_res, x8, xm, xk):
+        """attn: (context partials, nsplit, split_stride) as _attend returns."""
         dev = self.device
         R, H, nq, hd, I_ = B * T, self.hidden, self.n_q, self.hd, self.inter
         a8 = torch.empty(R, nq * hd, dtype=torch.int8, device=dev)
         am = torch.empty(R, dtype=I64, device=dev)
         ak = torch.empty(R, dtype=I64, device=dev)
-        call("detllm_merge_rowcol", attn, 1, 0, R, nq * hd, L.os_m, L.os_k, L.attn_out_col_m,
+        call("detllm_merge_rowcol", *attn, R, nq * hd, L.os_m, L.os_k, L.attn_out_col_m,
              L.attn_out_col_k, a8, am, ak)
         P, ns, st = self._gemm(a8, L.wo, (L.pf_o,))
         call("detllm_residual_normq", P, ns, st, R, H, am, ak, L.o_m, L.o_k, 20, h, k_res,

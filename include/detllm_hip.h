@@ -255,6 +255,27 @@ int detllm_attn_decode(const int8_t* q8, const int64_t* tpos, const int8_t* kpoo
                        const int64_t* s_dev, int32_t* scratch, int64_t* out, int32_t* err,
                        hipStream_t s);
 
+/* Split-S decode attention — the same integers as detllm_attn_decode, with
+ * each row's slots cut into chunks of `chunk` slots, one block per (row, kv
+ * head, chunk) (the reference scans a row in one Triton program,
+ * ops/fused_attn.py:47-142). Two launches: scores of each chunk to
+ * scores [B][n_q][nsplit * chunk] int32 with per-chunk maxima to
+ * cmax [B][n_q][nsplit] int32; then, from the true row maximum and the
+ * denominator over all the row's slots, each chunk's partial context to
+ * out [nsplit][B][n_q * 128] int64. The context is the sum of the nsplit
+ * partials (detllm_merge_rowcol sums them). nsplit = ceil(S / chunk); chunk a
+ * multiple of 128, at most 4096, with n_q/n_kv * chunk * 4 <= 48 KiB.
+ * Other arguments and err as in detllm_attn_decode. */
+int detllm_attn_decode_split(const int8_t* q8, const int64_t* tpos, const int8_t* kpool,
+                             const int8_t* vpool, const int32_t* table, int width,
+                             const uint8_t* valid, int64_t valid_stride, int B, int S, int n_q,
+                             int n_kv, const int64_t* s_dev, int chunk, int32_t* scores,
+                             int32_t* cmax, int64_t* out, int32_t* err, hipStream_t s);
+
+/* The chunking detllm_attn_decode_split is tuned for at (B, S, n_q, n_kv):
+ * about 1024 blocks, chunks of 256 slots or more. Writes *chunk, *nsplit. */
+int detllm_attn_split_plan(int B, int S, int n_q, int n_kv, int* chunk, int* nsplit);
+
 /* Per-step bookkeeping of the graph-captured decode (src/detllm/graphed.py:
  * 112-131: the validity flag of the step's slot, the device scalars holding
  * the write slot and the scanned-slot count, the positions), one launch

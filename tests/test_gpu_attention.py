@@ -241,6 +241,117 @@ def test_decode_attention_vs_oracle(name):
     assert bad.size == 0, f"{len(bad)} mismatches, first at {bad[0].tolist()}"
 
 
+# ------------------------------------------------------ split-S decode kernel
+
+def _split(q8, tpos, kp, vp, table, width, vmask, B, S, n_q, n_kv, chunk, s_dev=None):
+    """detllm_attn_decode_split -> its nsplit partial contexts (scratch and
+    chunk maxima pre-filled with junk: every entry read must be written)."""
+    from idempotent_llm_amd._lib import call
+    ns = -(-S // chunk)
+    scores = torch.full((B, n_q, ns * chunk), 0x7F7F7F7F, dtype=torch.int32, device="cuda")
+    cmax = torch.full((B, n_q, ns), 0x7F7F7F7F, dtype=torch.int32, device="cuda")
+    out = torch.full((ns, B, n_q * 128), -7, dtype=I64, device="cuda")
+    call("detllm_attn_decode_split", q8, tpos, kp, vp, table, width, vmask.view(torch.uint8),
+         width * 128, B, S, n_q, n_kv, s_dev, chunk, scores, cmax, out, None)
+    return out
+
+
+SPLIT_CASES = dict(DECODE_CASES)
+# two rows of 4096 slots with ragged masks, one of them dead for its first
+# 1000 slots (whole chunks with no visible slot)
+SPLIT_CASES["long_ragged"] = (2, 4, 2, 4096, 4096, 15, 29, 34, dict(dead_prefix=1000))
+
+
+@pytest.mark.parametrize("name", list(SPLIT_CASES))
+@pytest.mark.parametrize("chunk", [256, "plan"])
+def test_split_decode_vs_oracle(name, chunk):
+    """detllm_attn_decode_split: the sum of the chunk partials against the
+    oracle composition (the same cases as the one-block decode kernel, plus
+    4096-slot ragged rows), at 256-slot chunks and at the planned chunking."""
+    from idempotent_llm_amd._lib import attn_split_plan
+    B, n_q, n_kv, S, cap, seed, lo, hi, extra = SPLIT_CASES[name]
+    if chunk == "plan":
+        chunk = attn_split_plan(B, S, n_q, n_kv)[0]
+    print(f"[split decode {name}: B={B} n_q={n_q} n_kv={n_kv} S={S} chunk={chunk}]", flush=True)
+    q8, kc, vc, valid, sm, sk, tpos = _prefill_case(B, n_q, n_kv, 1, S - 1, cap, seed, lo, hi,
+                                                    **extra)
+    want = _prefill_oracle(q8, kc, vc, valid, sm, sk, S - 1)[:, 0]
+    d = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
+    kp, vp, table, width, vmask = paged(kc, vc, valid, seed=seed)
+    out = _split(d(q8[:, :, 0]), d(tpos[:, :, 0, 0]), kp, vp, table, width, vmask, B, S, n_q,
+                 n_kv, chunk)
+    got = out.sum(0).cpu().numpy()
+    bad = np.argwhere(got != want)
+    assert bad.size == 0, f"{len(bad)} mismatches, first at {bad[0].tolist()}"
+
+
+@pytest.mark.parametrize("B,n_q,n_kv,S,s_dev", [
+    (8, 16, 8, 4096, None),     # the c4 / long-context shape, planned and forced chunkings
+    (8, 16, 8, 4096, 1000),     # device-bounded scan: chunks past 1000 slots contribute 0
+    (1, 8, 1, 3000, None),      # G = 8 (chunks within 48 KiB of packed p)
+    (3, 4, 4, 700, 700),        # G = 1, ragged last chunk
+])
+def test_split_decode_equals_one_block_kernel(B, n_q, n_kv, S, s_dev):
+    """Random caches, queries and DI-Exp constants: the split partials sum to
+    detllm_attn_decode's output for every chunking tried."""
+    from idempotent_llm_amd._lib import attn_split_plan, call
+    print(f"[split vs one-block decode B={B} n_q={n_q} n_kv={n_kv} S={S} s_dev={s_dev}]",
+          flush=True)
+    g = torch.Generator().manual_seed(S + B)
+    cap = -(-S // 128) * 128
+    q8 = torch.randint(-128, 128, (B, n_q, 128), generator=g, dtype=torch.int8).cuda()
+    tpos = torch.randint(1, 1 << 22, (B, n_q), generator=g, dtype=I64).cuda()
+    tpos[0, 0] = 1 << 40                      # the integer DI-Exp branch
+    kc = torch.randint(-128, 128, (B, n_kv, cap, 128), generator=g, dtype=torch.int8)
+    vc = torch.randint(-128, 128, (B, n_kv, 128, cap), generator=g, dtype=torch.int8)
+    valid = torch.rand(B, cap, generator=g) < 0.7
+    kp, vp, table, width, vmask = paged(kc, vc, valid, seed=B)
+    sd = None if s_dev is None else torch.tensor([s_dev], dtype=I64, device="cuda")
+    G = n_q // n_kv
+    Spad = (S + 15) // 16 * 16
+    scratch = (torch.empty(B, n_q, Spad, dtype=torch.int32, device="cuda")
+               if G * Spad * 4 > 48 * 1024 else None)
+    want = torch.empty(B, n_q * 128, dtype=I64, device="cuda")
+    call("detllm_attn_decode", q8, tpos, kp, vp, table, width, vmask.view(torch.uint8),
+         width * 128, B, S, n_q, n_kv, sd, scratch, want, None)
+    chunks = {attn_split_plan(B, S, n_q, n_kv)[0], 256, 384}
+    if G * 4096 * 4 <= 48 * 1024:
+        chunks.add(4096)
+    for ch in sorted(chunks):
+        out = _split(q8, tpos, kp, vp, table, width, vmask, B, S, n_q, n_kv, ch, sd)
+        assert torch.equal(out.sum(0), want), ch
+        if s_dev is not None:
+            first_empty = -(-s_dev // ch)
+            assert (out[first_empty:] == 0).all()
+    assert want.abs().sum().item() > 0
+
+
+def test_split_decode_argument_errors():
+    from idempotent_llm_amd._lib import call
+    print("[split decode argument errors]", flush=True)
+    B, n_q, n_kv, S = 1, 8, 1, 512
+    q8 = torch.zeros(B, n_q, 128, dtype=torch.int8, device="cuda")
+    tpos = torch.ones(B, n_q, dtype=I64, device="cuda")
+    kc = torch.zeros(B, n_kv, S, 128, dtype=torch.int8)
+    vc = torch.zeros(B, n_kv, 128, S, dtype=torch.int8)
+    kp, vp, table, width, vmask = paged(kc, vc, torch.ones(B, S, dtype=torch.bool))
+    sc = torch.empty(B, n_q, 4096, dtype=torch.int32, device="cuda")
+    cm = torch.empty(B, n_q, 16, dtype=torch.int32, device="cuda")
+    out = torch.empty(16, B, n_q * 128, dtype=I64, device="cuda")
+
+    def run(chunk):
+        call("detllm_attn_decode_split", q8, tpos, kp, vp, table, width,
+             vmask.view(torch.uint8), width * 128, B, S, n_q, n_kv, None, chunk, sc, cm, out,
+             None)
+
+    with pytest.raises(RuntimeError, match="code -22"):
+        run(200)          # not a multiple of the page
+    with pytest.raises(RuntimeError, match="code -34"):
+        run(2048)         # 8 heads x 2048 slots x 4 bytes of packed p > 48 KiB
+    run(256)
+    torch.cuda.synchronize()
+
+
 @pytest.mark.parametrize("T", [100, 257])
 def test_prefill_epilogue_kq_estimates(T):
     """The prefill Q/K/V epilogue (rows layout, R > 64) with the K channels'

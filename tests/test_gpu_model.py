@@ -127,6 +127,36 @@ def test_graph_growth_matches_oracle(case):
     assert chain_hashes(lg) == chain_hashes(le)
 
 
+def test_split_attention_decode_matches_oracle(case, monkeypatch):
+    """Decode through the split-S attention (threshold lowered so that rows
+    past 256 slots split into 256-slot chunks; the merge sums the partials):
+    eager and graphed generation equal the oracle for 250 steps, and a batch
+    of 3 gives the same logits split and unsplit."""
+    rec, m, d = case
+    if rec["dims"]["hidden"] != 256:
+        pytest.skip("tiny model only (oracle speed)")
+    import idempotent_llm_amd.model as mdl
+    from oracle.model import IntQwen3Oracle
+    steps = 250
+    ids = _ids(rec)[None]
+    te, le = IntQwen3Oracle(d).generate(ids.cpu().numpy(), steps)
+    monkeypatch.setattr(mdl, "SPLIT_MIN_SLOTS", 0)
+    assert m._split_plan(1, 512) is not None
+    for use_graph in (False, True):
+        tg, lg = m.generate(ids, steps, use_graph=use_graph)
+        assert tg.cpu().numpy().tolist() == te.tolist(), use_graph
+        assert chain_hashes(lg) == chain_hashes(le), use_graph
+    ids3 = ids.repeat(3, 1)
+    ids3[1, -1] = 7
+    runs = []
+    for thr in (0, 1 << 30):
+        monkeypatch.setattr(mdl, "SPLIT_MIN_SLOTS", thr)
+        runs.append(m.generate(ids3, 40 + 256 - ids.shape[1], use_graph=True))
+    assert torch.equal(runs[0][0], runs[1][0])
+    for a, b in zip(runs[0][1], runs[1][1]):
+        assert torch.equal(a, b)
+
+
 def test_step_greedy_matches_step_then_pick(case):
     """GraphedDecode.step_greedy (the pick captured in the step's graph, ids
     fed back on the device) gives the tokens and logits of
