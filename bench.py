@@ -262,6 +262,52 @@ def gemv_rooflines(model, B: int):
     return res["k_gemv_nt"], res["k_gemv_stream"]
 
 
+def split_attention_case(model, B: int = 32, S: int = 4096, seed: int = 4):
+    """The split-S decode attention at config c4's decode shape (B rows
+    scanning S slots, the model's head counts) on a random paged cache with
+    every slot valid. Returns (launch fn, algorithmic bytes per call, plan):
+    the bytes are the K and V bytes scanned, the queries, DI-Exp constants and
+    the int64 partial contexts written."""
+    import torch
+    from idempotent_llm_amd._lib import attn_split_plan, call
+    from idempotent_llm_amd.kvcache import pages_from_contiguous
+    nq, nkv, hd = model.n_q, model.n_kv, model.hd
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    kc = torch.randint(-128, 128, (B, nkv, S, hd), device="cuda", dtype=torch.int8, generator=g)
+    vc = torch.randint(-128, 128, (B, nkv, hd, S), device="cuda", dtype=torch.int8, generator=g)
+    kp, vp, table = pages_from_contiguous(kc, vc, seed=seed)
+    del kc, vc
+    valid = torch.ones(B, S, dtype=torch.uint8, device="cuda")
+    q8 = torch.randint(-128, 128, (B, nq, hd), device="cuda", dtype=torch.int8, generator=g)
+    tpos = torch.randint(1, 1 << 22, (B, nq), device="cuda", dtype=torch.int64, generator=g)
+    chunk, ns = attn_split_plan(B, S, nq, nkv)
+    scores = torch.empty(B, nq, ns * chunk, dtype=torch.int32, device="cuda")
+    cmax = torch.empty(B, nq, ns, dtype=torch.int32, device="cuda")
+    out = torch.empty(ns, B, nq * hd, dtype=torch.int64, device="cuda")
+
+    def run():
+        call("detllm_attn_decode_split", q8, tpos, kp, vp, table, S // 128, valid, S, B, S, nq,
+             nkv, None, chunk, scores, cmax, out, None)
+
+    nbytes = 2 * B * nkv * S * hd + q8.numel() + 8 * tpos.numel() + 8 * out.numel()
+    return run, nbytes, (chunk, ns)
+
+
+def split_attention_roofline(model):
+    """HBM roofline of the split-S decode attention (its two kernels) at the
+    c4 shape, timed over graph replays of one call."""
+    run, nbytes, (chunk, ns) = split_attention_case(model)
+    us = _graph_time_us(run, 20, 1)
+    achieved = nbytes / (us * 1e-6) / 1e9
+    return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+            "kernel": "k_attn_split_scores + k_attn_split_pv", "batch": 32, "slots": 4096,
+            "chunk": chunk, "nsplit": ns, "bytes_per_call": int(nbytes),
+            "avg_call_us": round(us, 3),
+            "timing": "HIP events around 20 replays of a graph of one split-S attention call "
+                      "(one layer of c4's decode at 4096 slots)"}
+
+
 def kernel_probe(model, B: int, reps: int = 3):
     """Eager launches for counter passes (rocprofv3 --pmc): a plain device copy
     of known size (the calibration of FETCH_SIZE / WRITE_SIZE), the decode
@@ -294,9 +340,24 @@ def kernel_probe(model, B: int, reps: int = 3):
             log("kernel probe: eager decode steps at ~320 slots follow")
         model.forward(cur, torch.full((B, 1), T + i, device="cuda"), cache, one)
     torch.cuda.synchronize()
+    # one-row decode steps (the fused-operand GEMVs)
+    ids1, valid1 = c3_inputs(1, model.vocab)
+    ids1 = torch.from_numpy(ids1).cuda()
+    T1 = ids1.shape[1]
+    _, _, _, cache1 = model.forward(ids1, torch.arange(T1, device="cuda")[None])
+    for i in range(reps):
+        model.forward(cur[:1], torch.full((1, 1), T1 + i, device="cuda"), cache1)
+    torch.cuda.synchronize()
+    del cache, cache1
+    # the split-S attention at the c4 shape
+    run, nbytes, plan = split_attention_case(model)
+    for _ in range(reps):
+        run()
+    torch.cuda.synchronize()
     log(f"kernel probe: copy {n} B x {reps}, {len(jobs) + 1} GEMV launches x {reps} "
         f"({_job_bytes(jobs) / len(jobs):.0f} algorithmic B per k_gemv_nt launch), "
-        f"256 eager decode steps at batch {B}")
+        f"256 eager decode steps at batch {B}, {reps} at batch 1, split-S attention x {reps} "
+        f"(plan {plan}, {nbytes} algorithmic B per call)")
 
 
 # ------------------------------------------------------------ other configs
@@ -622,6 +683,8 @@ def main():
                     help="only time 2048-token prefills of the model, print them, exit")
     ap.add_argument("--roofline-probe", action="store_true",
                     help="only time the decode GEMV graphs of the roofline legs, print, exit")
+    ap.add_argument("--split-probe", action="store_true",
+                    help="only time the split-S decode attention at the c4 shape, print, exit")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}): this build "
@@ -660,6 +723,10 @@ def main():
             r, rs = gemv_rooflines(model, 8)
             print(json.dumps({"roofline": r, "roofline_lm_head": rs}), flush=True)
             return
+        if args.split_probe:
+            print(json.dumps({"roofline_attn_split": split_attention_roofline(model)}),
+                  flush=True)
+            return
         w8 = c3_window(model, 8, args.steps, args.warmup)
         log(f"c3 b8: {w8['tok_s']:.1f} tok/s ({w8['ms_per_step']:.3f} ms/step, slots "
             f"{w8['slots']})")
@@ -690,6 +757,8 @@ def main():
             log(f"c1: {c1} c2: {c2}")
             extras["c4_batch32"] = c4_bench(model)
             log(f"c4: {extras['c4_batch32']}")
+            extras["roofline_attn_split"] = split_attention_roofline(model)
+            log(f"split-S attention roofline: {extras['roofline_attn_split']}")
         del model
         torch.cuda.empty_cache()
         cpu = cpu_cfg = None

@@ -542,19 +542,25 @@ __device__ __forceinline__ void store_pv(const v4i (&chi)[2], const v4i (&clo)[2
   }
 }
 
-// K rows and validity flags of a wave's first 16-slot blocks, loaded before
-// the fused kernel's Q/K/V epilogue so that their latency hides behind it;
-// the slot the epilogue writes is taken from LDS instead.
+// K rows and validity flags of a wave's first KPRE_IT iterations of 16-slot
+// blocks (the first 16 * 16 * KPRE_IT slots of the row), loaded before the
+// fused kernel's Q/K/V epilogue so that their latency hides behind it; the
+// slot the epilogue writes is taken from LDS instead.
+constexpr int KPRE_IT = 2;
+constexpr int KPRE_SLOTS = 256 * KPRE_IT;
 struct KPre {
-  v4i kb[4][2];
-  int vf[4];
+  v4i kb[KPRE_IT][4][2];
+  int vf[KPRE_IT][4];   // 0 for slots of pages that are not mapped
   const int8_t* k_new;  // LDS, 128 bytes
   i64 new_slot;         // -1: none
 };
 
 // pg_lds: the row's page ids for slots [0, S) (filled by the caller, before
-// a barrier). Slots whose page is not mapped are masked and read page 0.
-template <int G>
+// a barrier). Slots whose page is not mapped are masked and read page 0. VP:
+// 64-slot steps of V loaded ahead. SCR: the scores live in the global
+// scratch (a.scratch) instead of LDS (a compile-time choice: LDS-only code
+// never issues flat accesses, which would wait on every outstanding load).
+template <int G, int VP, bool SCR>
 __device__ __forceinline__ void decode_body(const DecodeArgs& a, int kvh, int b,
                                             const int8_t* qsrc, const int64_t* tsrc,
                                             int32_t* sh_scores, const int32_t* pg_lds,
@@ -573,7 +579,7 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, int kvh, int b,
     S = (int)imax(0, imin((i64)S, sd));
   }
   const int Spad = (a.S + 15) & ~15;
-  int32_t* sc = a.scratch ? a.scratch + ((i64)b * a.n_q + kvh * G) * Spad : sh_scores;
+  int32_t* sc = SCR ? a.scratch + ((i64)b * a.n_q + kvh * G) * Spad : sh_scores;
   const uint8_t* vrow = a.valid + (i64)b * a.valid_stride;
   const int nstep = (S + 63) / 64;  // 64-slot steps of P.V
   auto pg_of = [&](int s) -> int {  // page of slot s < S, page 0 when not mapped
@@ -581,19 +587,16 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, int kvh, int b,
     return pg < 0 ? 0 : pg;
   };
 
-  // V fragments of the first VPRE steps, loaded now to overlap the scores
-  // (a 64-slot step lies in one page)
+  // V fragments of 64-slot steps (a step lies in one page). Loads are
+  // unconditional (no branch whose merge would make them complete early): a
+  // 16-slot group at or past S reads slot 0's bytes, and every A row of such
+  // a group, the colsum row included, is zero.
   auto vfrag = [&](int st, int nb) -> v4i {
     const int s0 = st * 64 + grp * 16;
-    if (s0 >= S) return v4i{0, 0, 0, 0};
-    const int8_t* vch = a.kv.vchan(pg_of(s0), kvh, wave * 32 + nb * 16 + l16);
-    return *(const v4i*)(vch + (s0 & (DI_PAGE - 1)));
+    const int sl = s0 < S ? s0 : 0;
+    const int8_t* vch = a.kv.vchan(pg_of(sl), kvh, wave * 32 + nb * 16 + l16);
+    return *(const v4i*)(vch + (sl & (DI_PAGE - 1)));
   };
-  v4i vpre[VPRE][2];
-#pragma unroll
-  for (int i = 0; i < VPRE; ++i)
-#pragma unroll
-    for (int nb = 0; nb < 2; ++nb) vpre[i][nb] = vfrag(i, nb);
 
   // query fragments (row l16 = head) and the heads' DI-Exp constants
   v4i qa0 = v4i{0, 0, 0, 0}, qa1 = v4i{0, 0, 0, 0};
@@ -612,31 +615,8 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, int kvh, int b,
   // Lane (grp, l16) holds C[4 grp + r][slot l16] in element r.
   int32_t mx[4] = {SCORE_MASKED, SCORE_MASKED, SCORE_MASKED, SCORE_MASKED};
   const int nblk = (S + 15) / 16;
-  for (int blk0 = wave; blk0 < nblk; blk0 += 16) {
-    v4i kb[4][2];
-    int vf[4];
-    if (pre && blk0 == wave) {
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        kb[u][0] = pre->kb[u][0];
-        kb[u][1] = pre->kb[u][1];
-        vf[u] = pre->vf[u];  // 0 for slots of pages that are not mapped
-        if ((blk0 + u * 4) * 16 + l16 == pre->new_slot) {
-          kb[u][0] = *(const v4i*)(pre->k_new + grp * 16);
-          kb[u][1] = *(const v4i*)(pre->k_new + 64 + grp * 16);
-        }
-      }
-    } else {
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const int s = (blk0 + u * 4) * 16 + l16;
-        const int sc_ = s < S ? s : 0;
-        const int8_t* kr = a.kv.krow(pg_of(sc_), kvh, sc_ & (DI_PAGE - 1));
-        kb[u][0] = *(const v4i*)(kr + grp * 16);
-        kb[u][1] = *(const v4i*)(kr + 64 + grp * 16);
-        vf[u] = pg_lds[sc_ >> 7] >= 0 ? vrow[sc_] : 0;
-      }
-    }
+  // blocks blk0 + 4u (u < 4) from K fragments kb and validity flags vf
+  auto score4 = [&](int blk0, const v4i (&kb)[4][2], const int (&vf)[4]) {
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
       const int blk = blk0 + u * 4;
@@ -655,19 +635,72 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, int kvh, int b,
         }
       }
     }
+  };
+  int blk0 = wave;
+  if (pre) {
+#pragma unroll
+    for (int it = 0; it < KPRE_IT; ++it) {
+      const int bb = wave + 16 * it;
+      if (bb >= nblk) continue;  // wave-uniform
+      v4i kb[4][2];
+      int vf[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        kb[u][0] = pre->kb[it][u][0];
+        kb[u][1] = pre->kb[it][u][1];
+        if ((bb + u * 4) * 16 + l16 == pre->new_slot) {
+          kb[u][0] = *(const v4i*)(pre->k_new + grp * 16);
+          kb[u][1] = *(const v4i*)(pre->k_new + 64 + grp * 16);
+        }
+        vf[u] = pre->vf[it][u];
+      }
+      score4(bb, kb, vf);
+    }
+    blk0 = wave + 16 * KPRE_IT;
   }
+  for (; blk0 < nblk; blk0 += 16) {
+    v4i kb[4][2];
+    int vraw[4], vf[4];
+    bool ok[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int s = (blk0 + u * 4) * 16 + l16;
+      const int sc_ = s < S ? s : 0;
+      const int8_t* kr = a.kv.krow(pg_of(sc_), kvh, sc_ & (DI_PAGE - 1));
+      kb[u][0] = *(const v4i*)(kr + grp * 16);
+      kb[u][1] = *(const v4i*)(kr + 64 + grp * 16);
+      vraw[u] = vrow[sc_];  // loaded unconditionally, masked at use (no wait per block)
+      ok[u] = pg_lds[sc_ >> 7] >= 0;
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) vf[u] = ok[u] ? vraw[u] : 0;
+    score4(blk0, kb, vf);
+  }
+  // the first VP steps of V, loaded now (the K fragments' registers are
+  // free) to overlap the maxima, denominators and probabilities
+  v4i vpre[VP][2];
+#pragma unroll
+  for (int i = 0; i < VP; ++i)
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb) vpre[i][nb] = vfrag(i, nb);
+  // per-head row maxima, two heads per block reduction (int32 scores biased
+  // to order-preserving unsigned values)
   i64 hmax[G];
 #pragma unroll
   for (int r = 0; r < 4; ++r) mx[r] = row16_max(mx[r]);
 #pragma unroll
-  for (int hh = 0; hh < G; ++hh) {
+  for (int hh = 0; hh < G; hh += 2) {
     // head hh lives in lanes 16 (hh / 4) .. + 15, element hh % 4
-    const int32_t mine = grp == hh / 4 ? mx[hh % 4] : SCORE_MASKED;
-    const i64 m = red.max((i64)mine);
-    hmax[hh] = m == (i64)SCORE_MASKED ? 0 : m;  // no visible slot: max := 0, every p = 0
+    const int32_t m0 = grp == hh / 4 ? mx[hh % 4] : SCORE_MASKED;
+    const int32_t m1 = hh + 1 < G && grp == (hh + 1) / 4 ? mx[(hh + 1) % 4] : SCORE_MASKED;
+    uint32_t u0 = (uint32_t)m0 ^ 0x80000000u, u1 = (uint32_t)m1 ^ 0x80000000u;
+    red.max2_u32(u0, u1);
+    const int32_t r0 = (int32_t)(u0 ^ 0x80000000u), r1 = (int32_t)(u1 ^ 0x80000000u);
+    hmax[hh] = r0 == SCORE_MASKED ? 0 : r0;  // no visible slot: max := 0, every p = 0
+    if (hh + 1 < G) hmax[hh + 1] = r1 == SCORE_MASKED ? 0 : r1;
   }
   __syncthreads();
-  // ---- pass 2: denominators
+  // ---- pass 2: denominators (two heads per block reduction)
   i64 den[G];
 #pragma unroll
   for (int hh = 0; hh < G; ++hh) {
@@ -685,7 +718,14 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, int kvh, int b,
         if (x != SCORE_MASKED) acc = wadd(acc, di_exp_neg((u64)wsub(hmax[hh], (i64)x), E));
       }
     }
-    den[hh] = imax(red.sum(acc), 1);
+    den[hh] = acc;
+  }
+#pragma unroll
+  for (int hh = 0; hh < G; hh += 2) {
+    i64 d1 = hh + 1 < G ? den[hh + 1] : 0;
+    red.sum2(den[hh], d1);
+    den[hh] = imax(den[hh], 1);
+    if (hh + 1 < G) den[hh + 1] = imax(d1, 1);
   }
   // ---- pass 3: p in [0, 2^14] as (hi - 64) | lo << 8 in place of the score
   // (0 for masked slots and the padding up to the next multiple of 16, i.e.
@@ -730,7 +770,7 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, int kvh, int b,
     const int s0 = st * 64 + grp * 16;
     if (l16 < G && s0 < S) {
       p_frags(sc + l16 * Spad + s0, ahi, alo);  // 16 packed p of head l16
-    } else if (l16 == G) {
+    } else if (l16 == G && s0 < S) {
       ahi = v4i{0x01010101, 0x01010101, 0x01010101, 0x01010101};  // colsum row
     }
 #pragma unroll
@@ -740,14 +780,14 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, int kvh, int b,
     }
   };
 #pragma unroll
-  for (int i = 0; i < VPRE; ++i)
+  for (int i = 0; i < VP; ++i)
     if (i < nstep) pv_step(i, vpre[i]);
-  for (int st0 = VPRE; st0 < nstep; st0 += 4) {
+  for (int st0 = VP; st0 < nstep; st0 += 4) {
     v4i vb[4][2];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
-      for (int nb = 0; nb < 2; ++nb) vb[i][nb] = st0 + i < nstep ? vfrag(st0 + i, nb) : v4i{0, 0, 0, 0};
+      for (int nb = 0; nb < 2; ++nb) vb[i][nb] = vfrag(st0 + i, nb);
 #pragma unroll
     for (int i = 0; i < 4; ++i)
       if (st0 + i < nstep) pv_step(st0 + i, vb[i]);
@@ -755,7 +795,7 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, int kvh, int b,
   store_pv<G>(chi, clo, a.out + (i64)b * a.n_q * 128 + kvh * G * 128);
 }
 
-template <int G>
+template <int G, bool SCR>
 __global__ __launch_bounds__(256) void k_attn_decode(DecodeArgs a) {
   extern __shared__ __attribute__((aligned(16))) int32_t sh_scores[];
   __shared__ int32_t pg_lds[DEC_MAX_PAGES];
@@ -763,29 +803,34 @@ __global__ __launch_bounds__(256) void k_attn_decode(DecodeArgs a) {
   const i64 q0 = (i64)b * a.n_q + kvh * G;
   const int npages = (a.S + DI_PAGE - 1) / DI_PAGE;
   for (int i = threadIdx.x; i < npages; i += 256) pg_lds[i] = a.kv.page(b, (i64)i * DI_PAGE);
+  if (npages == 0 && threadIdx.x == 0) pg_lds[0] = -1;  // S = 0: loads read page 0
   __syncthreads();
-  decode_body<G>(a, kvh, b, a.q8 + q0 * 128, a.tpos + q0, sh_scores, pg_lds);
+  decode_body<G, VPRE, SCR>(a, kvh, b, a.q8 + q0 * 128, a.tpos + q0, sh_scores, pg_lds);
 }
 
 // Decode step with the Q/K/V epilogue fused in (G <= 2): waves 0..G-1 finish
 // the block's query heads into LDS, wave G writes the key head and wave G + 1
 // the value head of this step's slot into the cache; after one barrier the
-// block attends over every slot, the new one included.
-template <int G>
+// block attends over every slot, the new one included. NS1: the Q/K/V
+// product has no K split (qa.nsplit == 1). SCR as in decode_body.
+template <int G, bool NS1, bool SCR>
 __global__ __launch_bounds__(256) void k_qkv_attn_decode(DecodeArgs a, QKVArgs qa) {
   static_assert(G + 2 <= 4, "one wave per head slot");
   extern __shared__ __attribute__((aligned(16))) int32_t sh_scores[];
   __shared__ __attribute__((aligned(16))) int8_t q_lds[G][128];
   __shared__ int64_t t_lds[G];
-  const int kvh = blockIdx.x, b = blockIdx.y, w = threadIdx.x >> 6;
+  const int kvh = blockIdx.x, b = blockIdx.y;
+  const int w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));  // wave-uniform
   int slotw = -1;
   if (w < G) slotw = kvh * G + w;
   else if (w == G) slotw = qa.n_q + kvh;
   else if (w == G + 1) slotw = qa.n_q + qa.n_kv + kvh;
   __shared__ __attribute__((aligned(16))) int8_t k_new[128];
   __shared__ int32_t pg_lds[DEC_MAX_PAGES];
-  // the row's page ids (stored to LDS after the epilogue) and the page ids of
-  // the first two pages, which the prefetch below addresses
+  const int lane = threadIdx.x & 63, l16 = lane & 15, grp = lane >> 4;
+  // 1. the loads that depend on nothing, together: the row's page ids
+  // (stored to LDS after the epilogue), the pages of the prefetched slots,
+  // the step's slot, then the epilogue's own loads
   const int npages = (a.S + DI_PAGE - 1) / DI_PAGE;
   int pgv[DEC_MAX_PAGES / 256];
 #pragma unroll
@@ -793,39 +838,62 @@ __global__ __launch_bounds__(256) void k_qkv_attn_decode(DecodeArgs a, QKVArgs q
     const int i = (int)threadIdx.x + 256 * q;
     pgv[q] = i < npages ? a.kv.page(b, (i64)i * DI_PAGE) : -1;
   }
-  const int pg0 = a.kv.page(b, 0), pg1 = a.kv.page(b, DI_PAGE);
-  // prefetch this wave's first K blocks of the scores pass (slots below the
-  // host bound a.S <= capacity; the pass masks slots at or past the scanned
-  // count and slots of pages that are not mapped)
+  constexpr int NPK = KPRE_SLOTS / DI_PAGE;
+  int pgk[NPK];
+#pragma unroll
+  for (int j = 0; j < NPK; ++j) pgk[j] = j * DI_PAGE < a.S ? a.kv.page(b, (i64)j * DI_PAGE) : -1;
+  const i64 base = qa.slot_base_dev ? qa.slot_base_dev[0] : qa.slot_base;
+  // (unconditional: a wave without a head slot loads slot 0's and ignores
+  // them, so no branch merge forces the loads to complete early)
+  const int slotl = slotw >= 0 ? slotw : 0;
+  QKVHeadIn in = qkv_head_load<NS1>(qa, b, slotl);
+  qkv_head_rope_load(qa, slotl, in);  // waits for the position only
+  // 2. the loads that depend on those: this wave's K rows of the scores
+  // pass's first iterations (slots below the host bound a.S <= capacity; the
+  // pass masks slots at or past the scanned count and slots of pages that are
+  // not mapped)
   KPre pre;
+  int vraw[KPRE_IT][4];
+  bool vok[KPRE_IT][4];
   {
-    const int lane = threadIdx.x & 63, l16 = lane & 15, grp = lane >> 4;
     const uint8_t* vrow = a.valid + (i64)b * a.valid_stride;
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int s = (w + u * 4) * 16 + l16;  // < 256: pages 0 and 1
-      const int sc_ = s < a.S ? s : 0;
-      const int pg = (sc_ >> 7) ? pg1 : pg0;
-      const int8_t* kr = a.kv.krow(pg < 0 ? 0 : pg, kvh, sc_ & (DI_PAGE - 1));
-      pre.kb[u][0] = *(const v4i*)(kr + grp * 16);
-      pre.kb[u][1] = *(const v4i*)(kr + 64 + grp * 16);
-      pre.vf[u] = pg >= 0 ? vrow[sc_] : 0;
-    }
-    const i64 base = qa.slot_base_dev ? qa.slot_base_dev[0] : qa.slot_base;
-    // T = 1: the step's slot is base; -1 when it has no mapped page
-    pre.new_slot = qa.kv.page(b, base) >= 0 ? base : -1;
+    for (int it = 0; it < KPRE_IT; ++it)
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int s = (w + 16 * it + u * 4) * 16 + l16;  // < KPRE_SLOTS
+        const int sc_ = s < a.S ? s : 0;
+        const int j = sc_ >> 7;
+        int pg = pgk[0];
+#pragma unroll
+        for (int jj = 1; jj < NPK; ++jj) pg = j == jj ? pgk[jj] : pg;
+        const int8_t* kr = a.kv.krow(pg < 0 ? 0 : pg, kvh, sc_ & (DI_PAGE - 1));
+        pre.kb[it][u][0] = *(const v4i*)(kr + grp * 16);
+        pre.kb[it][u][1] = *(const v4i*)(kr + 64 + grp * 16);
+        vraw[it][u] = vrow[sc_];  // masked after the epilogue: no wait here
+        vok[it][u] = pg >= 0;
+      }
     pre.k_new = k_new;
   }
+  // 3. the epilogue
   if (slotw >= 0)
-    qkv_head(qa, b, slotw, w < G ? q_lds[w] : nullptr, w < G ? &t_lds[w] : nullptr,
-             w == G ? k_new : nullptr);
+    qkv_head_compute(qa, b, slotw, in, w < G ? q_lds[w] : nullptr, w < G ? &t_lds[w] : nullptr,
+                     w == G ? k_new : nullptr);
+  if (slotw >= 0) qkv_head_report(qa, slotw, in);
+#pragma unroll
+  for (int it = 0; it < KPRE_IT; ++it)
+#pragma unroll
+    for (int u = 0; u < 4; ++u) pre.vf[it][u] = vok[it][u] ? vraw[it][u] : 0;
+  // T = 1: the step's slot is base (when its page is not mapped nothing was
+  // written, and the slot is masked: the substituted row is never a score)
+  pre.new_slot = base;
 #pragma unroll
   for (int q = 0; q < DEC_MAX_PAGES / 256; ++q) {
     const int i = (int)threadIdx.x + 256 * q;
     if (i < npages) pg_lds[i] = pgv[q];
   }
   __syncthreads();
-  decode_body<G>(a, kvh, b, &q_lds[0][0], t_lds, sh_scores, pg_lds, &pre);
+  decode_body<G, 2 * VPRE, SCR>(a, kvh, b, &q_lds[0][0], t_lds, sh_scores, pg_lds, &pre);
 }
 
 // ---------------------------------------------------------------------------
@@ -897,7 +965,8 @@ __global__ __launch_bounds__(256) void k_attn_split_scores(SplitArgs sa) {
   const int blo = lo / 16, bhi = (hi + 15) / 16;
   for (int blk0 = blo + wave; blk0 < bhi; blk0 += 16) {
     v4i kb[4][2];
-    int vf[4];
+    int vraw[4], vf[4];
+    bool ok[4];
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
       const int s = (blk0 + u * 4) * 16 + l16;
@@ -906,8 +975,11 @@ __global__ __launch_bounds__(256) void k_attn_split_scores(SplitArgs sa) {
       const int8_t* kr = a.kv.krow(pg < 0 ? 0 : pg, kvh, sc_ & (DI_PAGE - 1));
       kb[u][0] = *(const v4i*)(kr + grp * 16);
       kb[u][1] = *(const v4i*)(kr + 64 + grp * 16);
-      vf[u] = pg >= 0 ? vrow[sc_] : 0;
+      vraw[u] = vrow[sc_];  // masked at use (no wait per block)
+      ok[u] = pg >= 0;
     }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) vf[u] = ok[u] ? vraw[u] : 0;
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
       const int blk = blk0 + u * 4;
@@ -968,19 +1040,19 @@ __global__ __launch_bounds__(256) void k_attn_split_pv(SplitArgs sa) {
   __syncthreads();
   // V fragments of the chunk's first VPRE 64-slot steps (a step lies in one
   // page), loaded before the denominator pass
-  auto vfrag = [&](int st, int nb) -> v4i {
+  auto vfrag = [&](int st, int nb) -> v4i {  // unconditional, as in decode_body
     const int s0 = st * 64 + grp * 16;
-    if (s0 >= hi) return v4i{0, 0, 0, 0};
-    const int pg = pg_lds[(s0 - lo) / DI_PAGE];
+    const int sl = s0 < hi ? s0 : lo;
+    const int pg = pg_lds[(sl - lo) / DI_PAGE];
     const int8_t* vch = a.kv.vchan(pg < 0 ? 0 : pg, kvh, wave * 32 + nb * 16 + l16);
-    return *(const v4i*)(vch + (s0 & (DI_PAGE - 1)));
+    return *(const v4i*)(vch + (sl & (DI_PAGE - 1)));
   };
   const int st_lo = lo / 64, st_hi = (hi + 63) / 64;
   v4i vpre[VPRE][2];
 #pragma unroll
   for (int i = 0; i < VPRE; ++i)
 #pragma unroll
-    for (int nb = 0; nb < 2; ++nb) vpre[i][nb] = st_lo + i < st_hi ? vfrag(st_lo + i, nb) : v4i{0, 0, 0, 0};
+    for (int nb = 0; nb < 2; ++nb) vpre[i][nb] = vfrag(st_lo + i, nb);
   const int32_t* sc = a.scratch + q0 * sa.spad;
   // denominators over every scanned slot of the row
   i64 den[G];
@@ -1043,7 +1115,7 @@ __global__ __launch_bounds__(256) void k_attn_split_pv(SplitArgs sa) {
     const int s0 = st * 64 + grp * 16;
     if (l16 < G && s0 < hi) {
       p_frags(p_lds + l16 * sa.chunk + (s0 - lo), ahi, alo);
-    } else if (l16 == G) {
+    } else if (l16 == G && s0 < hi) {
       ahi = v4i{0x01010101, 0x01010101, 0x01010101, 0x01010101};  // colsum row
     }
 #pragma unroll
@@ -1060,7 +1132,7 @@ __global__ __launch_bounds__(256) void k_attn_split_pv(SplitArgs sa) {
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
-      for (int nb = 0; nb < 2; ++nb) vb[i][nb] = st0 + i < st_hi ? vfrag(st0 + i, nb) : v4i{0, 0, 0, 0};
+      for (int nb = 0; nb < 2; ++nb) vb[i][nb] = vfrag(st0 + i, nb);
 #pragma unroll
     for (int i = 0; i < 4; ++i)
       if (st0 + i < st_hi) pv_step(st0 + i, vb[i]);
@@ -1128,10 +1200,14 @@ int detllm_attn_decode(const int8_t* q8, const int64_t* tpos, const int8_t* kpoo
                scratch, s_dev, S, n_q, n_kv, valid_stride, err};
   const dim3 grid(n_kv, B);
   switch (G) {
-    case 1: hipLaunchKernelGGL(k_attn_decode<1>, grid, dim3(256), dyn, s, a); break;
-    case 2: hipLaunchKernelGGL(k_attn_decode<2>, grid, dim3(256), dyn, s, a); break;
-    case 4: hipLaunchKernelGGL(k_attn_decode<4>, grid, dim3(256), dyn, s, a); break;
-    case 8: hipLaunchKernelGGL(k_attn_decode<8>, grid, dim3(256), dyn, s, a); break;
+#define DI_DEC_LAUNCH(G_)                                                                      \
+  if (scratch) hipLaunchKernelGGL((k_attn_decode<G_, true>), grid, dim3(256), dyn, s, a);    \
+  else hipLaunchKernelGGL((k_attn_decode<G_, false>), grid, dim3(256), dyn, s, a)
+    case 1: DI_DEC_LAUNCH(1); break;
+    case 2: DI_DEC_LAUNCH(2); break;
+    case 4: DI_DEC_LAUNCH(4); break;
+    case 8: DI_DEC_LAUNCH(8); break;
+#undef DI_DEC_LAUNCH
     default: return DI_ENOSYS;
   }
   DI_LAUNCH_CHECK();
@@ -1184,10 +1260,17 @@ int detllm_qkv_attn_decode(const int32_t* P, int nsplit, int64_t split_stride, i
   qa.kv = kv; qa.slot_base_dev = slot_base_dev; qa.slot_base = slot_base; qa.err = err;
   DecodeArgs a{nullptr, nullptr, kv, valid, out, scratch, s_dev, S, n_q, n_kv, valid_stride, err};
   const dim3 grid(n_kv, B);
-  if (G == 1)
-    hipLaunchKernelGGL(k_qkv_attn_decode<1>, grid, dim3(256), dyn, s, a, qa);
-  else
-    hipLaunchKernelGGL(k_qkv_attn_decode<2>, grid, dim3(256), dyn, s, a, qa);
+#define DI_QAD_LAUNCH(G_, NS1_)                                                                 \
+  if (scratch) hipLaunchKernelGGL((k_qkv_attn_decode<G_, NS1_, true>), grid, dim3(256), dyn, s, a, qa); \
+  else hipLaunchKernelGGL((k_qkv_attn_decode<G_, NS1_, false>), grid, dim3(256), dyn, s, a, qa)
+  if (G == 1) {
+    if (nsplit == 1) { DI_QAD_LAUNCH(1, true); }
+    else { DI_QAD_LAUNCH(1, false); }
+  } else {
+    if (nsplit == 1) { DI_QAD_LAUNCH(2, true); }
+    else { DI_QAD_LAUNCH(2, false); }
+  }
+#undef DI_QAD_LAUNCH
   DI_LAUNCH_CHECK();
   return DI_OK;
 }

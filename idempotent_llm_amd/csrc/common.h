@@ -202,6 +202,27 @@ struct BlockRed {
   __device__ __forceinline__ i64 max(i64 v) { return reduce<true>(v); }
   __device__ __forceinline__ i64 sum(i64 v) { return reduce<false>(v); }
 
+  // Block sums of two values (one barrier; blocks of at most 512 threads)
+  __device__ __forceinline__ void sum2(i64& a, i64& b) {
+    a = wave_part<false>(a);
+    b = wave_part<false>(b);
+    i64* slot = buf + (k & 1) * 16;
+    ++k;
+    if ((threadIdx.x & 63) == 63) {
+      slot[threadIdx.x >> 6] = a;
+      slot[8 + (threadIdx.x >> 6)] = b;
+    }
+    __syncthreads();
+    const int nw = blockDim.x >> 6;
+    i64 ra = 0, rb = 0;
+    for (int i = 0; i < nw; ++i) {
+      ra = wadd(ra, slot[i]);
+      rb = wadd(rb, slot[8 + i]);
+    }
+    a = ra;
+    b = rb;
+  }
+
   // Block maxima of one or two 32-bit unsigned values (one barrier). A row
   // shift that depends only on the bit length of max |x| reduces bit lengths
   // (bitlen_abs below) here instead of 64-bit magnitudes.

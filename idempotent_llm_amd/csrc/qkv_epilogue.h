@@ -96,15 +96,23 @@ __device__ __forceinline__ void wave_rmsnorm128(i64& a, i64& b) {
   }
 }
 
-// The whole wave must be active. K and V go to the cache; a query head's
-// int8 row goes to q8_out[0..128) and its DI-Exp constant to *tpos_out
-// (global memory for the standalone kernel, LDS for the fused one).
-__device__ __forceinline__ void qkv_head(const QKVArgs& a, int r, int slotw, int8_t* q8_out,
-                                         int64_t* tpos_out, int8_t* k_lds = nullptr) {
+// The loads of one (token row, head slot) of qkv_head: every global load
+// that does not depend on another, issued together (one memory round trip).
+struct QKVHeadIn {
+  i64 pos_raw, xk, xm, base;
+  i64 wm0, wm1, g0, g1, qs0, qs1, kqm0, kqm1, kqk0, kqk1, vqm, vqk, ksm, ksk;
+  int32_t p0, p1;          // sign-extended where used (no wait at the load)
+  i64 pos;                 // qkv_head_rope_load: the checked position
+  bool pos_bad;            // and whether it was out of range (reported by compute)
+  int16_t cs0, cs1, sn0, sn1;  // and its RoPE table entries (widened where used)
+};
+
+// ONE: the caller guarantees nsplit == 1 (straight-line loads, no branch
+// whose merge would force them to complete early).
+template <bool ONE = false>
+__device__ __forceinline__ QKVHeadIn qkv_head_load(const QKVArgs& a, int r, int slotw) {
   const int lane = threadIdx.x & 63;
   const int n_heads = a.n_q + 2 * a.n_kv;
-
-  const int b = r / a.T, t = r - b * a.T;
   const int NQKV = n_heads * 128;
   const i64 off = (i64)r * NQKV + (i64)slotw * 128;
   const int group = a.n_q / a.n_kv;
@@ -112,25 +120,30 @@ __device__ __forceinline__ void qkv_head(const QKVArgs& a, int r, int slotw, int
   const int h = is_q ? slotw : (is_v ? slotw - a.n_q - a.n_kv : slotw - a.n_q);
   const int kvh = is_q ? h / group : h;
   const int c0 = lane, c1 = lane + 64;
-
-  // ---- every global load up front (one memory round trip, plus the RoPE
-  // table rows that depend on the position)
-  const i64 pos_raw = a.positions[r];
-  const i64 xk = a.xk[r], xm = a.xm[r];
-  const i64 base = a.slot_base_dev ? a.slot_base_dev[0] : a.slot_base;
+  QKVHeadIn in;
+  in.pos_raw = a.positions[r];
+  in.xk = a.xk[r];
+  in.xm = a.xm[r];
+  in.base = a.slot_base_dev ? a.slot_base_dev[0] : a.slot_base;
   const int64_t* wmp = (is_q ? a.q_m : (is_v ? a.v_m : a.k_m)) + (i64)h * 128;
-  const i64 wm0 = wmp[c0], wm1 = wmp[c1];
+  in.wm0 = wmp[c0];
+  in.wm1 = wmp[c1];
   const int64_t* gam = is_q ? a.q_norm_m : a.k_norm_m;
-  const i64 g0 = gam[c0], g1 = gam[c1];
-  const i64 qs0 = a.qs_m[kvh * 128 + c0], qs1 = a.qs_m[kvh * 128 + c1];
-  const i64 kqm0 = a.kq_m[kvh * 128 + c0], kqm1 = a.kq_m[kvh * 128 + c1];
-  const i64 kqk0 = a.kq_k[kvh * 128 + c0], kqk1 = a.kq_k[kvh * 128 + c1];
-  const i64 vqm = a.vq_m[kvh], vqk = a.vq_k[kvh];
-  const i64 ksm = a.ks_m[kvh], ksk = a.ks_k[kvh];
-  i64 p0, p1;
-  if (a.nsplit == 1) {  // no K split: one load per channel
-    p0 = a.P[off + c0];
-    p1 = a.P[off + c1];
+  in.g0 = gam[c0];
+  in.g1 = gam[c1];
+  in.qs0 = a.qs_m[kvh * 128 + c0];
+  in.qs1 = a.qs_m[kvh * 128 + c1];
+  in.kqm0 = a.kq_m[kvh * 128 + c0];
+  in.kqm1 = a.kq_m[kvh * 128 + c1];
+  in.kqk0 = a.kq_k[kvh * 128 + c0];
+  in.kqk1 = a.kq_k[kvh * 128 + c1];
+  in.vqm = a.vq_m[kvh];
+  in.vqk = a.vq_k[kvh];
+  in.ksm = a.ks_m[kvh];
+  in.ksk = a.ks_k[kvh];
+  if (ONE || a.nsplit == 1) {  // no K split: one load per channel
+    in.p0 = a.P[off + c0];
+    in.p1 = a.P[off + c1];
   } else {
     uint32_t s0 = 0, s1 = 0;
     for (int k0 = 0; k0 < a.nsplit; k0 += 4) {
@@ -148,13 +161,53 @@ __device__ __forceinline__ void qkv_head(const QKVArgs& a, int r, int slotw, int
           s1 += (uint32_t)t1[kk];
         }
     }
-    p0 = (int32_t)s0;
-    p1 = (int32_t)s1;
+    in.p0 = (int32_t)s0;
+    in.p1 = (int32_t)s1;
   }
-  const i64 pos = torch_index(pos_raw, a.max_pos, is_v || lane ? nullptr : a.err,
-                              DI_ERR_POSITION);
-  const i64 cs0 = a.cos_t[pos * 128 + c0], cs1 = a.cos_t[pos * 128 + c1];
-  const i64 sn0 = a.sin_t[pos * 128 + c0], sn1 = a.sin_t[pos * 128 + c1];
+  return in;
+}
+
+// The RoPE table rows of the head's position (loads that depend on the
+// position loaded by qkv_head_load), indexed as torch_index does; an out of
+// range position is reported (DI_ERR_POSITION) by qkv_head_report, after
+// the head's computation: a pending atomic among the loads would make the
+// compiler wait for all of them at the first use of any.
+__device__ __forceinline__ void qkv_head_rope_load(const QKVArgs& a, int slotw, QKVHeadIn& in) {
+  const int lane = threadIdx.x & 63;
+  const int c0 = lane, c1 = lane + 64;
+  in.pos = torch_index(in.pos_raw, a.max_pos, nullptr, DI_ERR_POSITION);
+  const i64 x = in.pos_raw < 0 ? in.pos_raw + a.max_pos : in.pos_raw;
+  in.pos_bad = x < 0 || x >= a.max_pos;
+  in.cs0 = a.cos_t[in.pos * 128 + c0];
+  in.cs1 = a.cos_t[in.pos * 128 + c1];
+  in.sn0 = a.sin_t[in.pos * 128 + c0];
+  in.sn1 = a.sin_t[in.pos * 128 + c1];
+}
+
+// DI_ERR_POSITION for a position out of range (one lane of a Q or K head)
+__device__ __forceinline__ void qkv_head_report(const QKVArgs& a, int slotw, const QKVHeadIn& in) {
+  const bool is_v = slotw >= a.n_q + a.n_kv;
+  if (in.pos_bad && !is_v && (threadIdx.x & 63) == 0 && a.err) atomicOr(a.err, DI_ERR_POSITION);
+}
+
+// The whole wave must be active. K and V go to the cache; a query head's
+// int8 row goes to q8_out[0..128) and its DI-Exp constant to *tpos_out
+// (global memory for the standalone kernel, LDS for the fused one). `in`:
+// qkv_head_load then qkv_head_rope_load of the same (r, slotw).
+__device__ __forceinline__ void qkv_head_compute(const QKVArgs& a, int r, int slotw,
+                                                 const QKVHeadIn& in, int8_t* q8_out,
+                                                 int64_t* tpos_out, int8_t* k_lds = nullptr) {
+  const int lane = threadIdx.x & 63;
+  const int b = r / a.T, t = r - b * a.T;
+  const bool is_q = slotw < a.n_q, is_v = slotw >= a.n_q + a.n_kv;
+  const int h = is_q ? slotw : (is_v ? slotw - a.n_q - a.n_kv : slotw - a.n_q);
+  const int c0 = lane, c1 = lane + 64;
+  const i64 xk = in.xk, xm = in.xm, base = in.base;
+  const i64 wm0 = in.wm0, wm1 = in.wm1, g0 = in.g0, g1 = in.g1, qs0 = in.qs0, qs1 = in.qs1;
+  const i64 kqm0 = in.kqm0, kqm1 = in.kqm1, kqk0 = in.kqk0, kqk1 = in.kqk1;
+  const i64 vqm = in.vqm, vqk = in.vqk, ksm = in.ksm, ksk = in.ksk;
+  const i64 p0 = in.p0, p1 = in.p1;
+  const i64 cs0 = in.cs0, cs1 = in.cs1, sn0 = in.sn0, sn1 = in.sn1;
   const i64 slot = base + t;
 
   if (is_v) {
@@ -260,6 +313,14 @@ __device__ __forceinline__ void qkv_head(const QKVArgs& a, int r, int slotw, int
       a.dbg[qrow * 4 + 3] = sk;
     }
   }
+}
+
+__device__ __forceinline__ void qkv_head(const QKVArgs& a, int r, int slotw, int8_t* q8_out,
+                                         int64_t* tpos_out, int8_t* k_lds = nullptr) {
+  QKVHeadIn in = qkv_head_load(a, r, slotw);
+  qkv_head_rope_load(a, slotw, in);
+  qkv_head_compute(a, r, slotw, in, q8_out, tpos_out, k_lds);
+  qkv_head_report(a, slotw, in);
 }
 
 }  // namespace di

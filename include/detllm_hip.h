@@ -182,8 +182,9 @@ int detllm_merge_rowcol(const int64_t* attn, int nsplit, int64_t split_stride, i
  * page's K rows: n_kv heads x 128 slots x 128 channels) and a V pool
  * [n_pages][n_kv][128][128] (V transposed: channels x slots); table
  * [B][width] int32 gives row b's page for slots [128 j, 128 j + 128)
- * (-1: not mapped; such slots are never written and never read as data).
- * A row holds width * 128 slots. The reference keeps one contiguous
+ * (-1: not mapped; such slots are never written and never read as data:
+ * the kernels mask them, reading page 0's bytes in their place, so a pool
+ * holds at least one page). A row holds width * 128 slots. The reference keeps one contiguous
  * [B, n_kv, CAP, hd] buffer per layer (model.py:67-102): same contents, only
  * the addressing differs, so pages allocated as a cache grows never move
  * earlier slots.
