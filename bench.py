@@ -299,8 +299,12 @@ def split_attention_roofline(model):
     run, nbytes, (chunk, ns) = split_attention_case(model)
     us = _graph_time_us(run, 20, 1)
     achieved = nbytes / (us * 1e-6) / 1e9
+    t1, src = _traffic("k_attn_split_scores")
+    t2, _ = _traffic("k_attn_split_pv")
+    traffic = t1 + t2 if t1 and t2 else None
     return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
+            "traffic_source": src,
             "kernel": "k_attn_split_scores + k_attn_split_pv", "batch": 32, "slots": 4096,
             "chunk": chunk, "nsplit": ns, "bytes_per_call": int(nbytes),
             "avg_call_us": round(us, 3),
