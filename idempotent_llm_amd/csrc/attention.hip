@@ -567,7 +567,7 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, int kvh, int b,
                                             const KPre* pre = nullptr) {
   static_assert(G <= 8, "query heads per kv head");
   __shared__ i64 red_buf[32];
-  BlockRed red{red_buf, 0};
+  BlockRed red{red_buf, 0, 256};
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int l16 = lane & 15, grp = lane >> 4;
   int S = a.S;
@@ -939,7 +939,7 @@ __global__ __launch_bounds__(256) void k_attn_split_scores(SplitArgs sa) {
   const DecodeArgs& a = sa.d;
   __shared__ i64 red_buf[32];
   __shared__ int32_t pg_lds[SPLIT_MAX_PAGES];
-  BlockRed red{red_buf, 0};
+  BlockRed red{red_buf, 0, 256};
   const int kvh = blockIdx.x, b = blockIdx.y, c = blockIdx.z;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, l16 = lane & 15, grp = lane >> 4;
   const int S = scanned_slots(a, kvh == 0 && c == 0);
@@ -1015,7 +1015,7 @@ __global__ __launch_bounds__(256) void k_attn_split_pv(SplitArgs sa) {
   extern __shared__ __attribute__((aligned(16))) int32_t p_lds[];  // [G][chunk] packed p
   __shared__ i64 red_buf[32];
   __shared__ int32_t pg_lds[SPLIT_MAX_PAGES];
-  BlockRed red{red_buf, 0};
+  BlockRed red{red_buf, 0, 256};
   const int kvh = blockIdx.x, b = blockIdx.y, c = blockIdx.z;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, l16 = lane & 15, grp = lane >> 4;
   const int S = scanned_slots(a, false);

@@ -168,7 +168,9 @@ __device__ __forceinline__ i64 isqrt_wave(i64 n) {
   return (i64)lo;
 }
 
-// Block-wide reductions (blockDim.x a multiple of 64, <= 1024), one barrier
+// Block-wide reductions (n = the block's thread count, a multiple of 64,
+// <= 1024, given by the caller: reading blockDim.x costs a dependent load of
+// the launch's hidden arguments), one barrier
 // each: every wave's lane 63 publishes its DPP partial, and calls alternate
 // between two 16-entry slots of `buf`, so a call never overwrites a slot that
 // a slower thread may still be reading (the call in between has a barrier
@@ -177,10 +179,11 @@ __device__ __forceinline__ i64 isqrt_wave(i64 n) {
 struct BlockRed {
   i64* buf;  // __shared__ i64[32]
   int k;
+  int n;     // threads in the block
 
   // the row's threads: the whole block
   __device__ __forceinline__ int tid() const { return (int)threadIdx.x; }
-  __device__ __forceinline__ int nt() const { return (int)blockDim.x; }
+  __device__ __forceinline__ int nt() const { return n; }
 
   template <bool MAX>
   __device__ __forceinline__ i64 reduce(i64 v) {
@@ -189,7 +192,7 @@ struct BlockRed {
     ++k;
     if ((threadIdx.x & 63) == 63) slot[threadIdx.x >> 6] = v;
     __syncthreads();
-    const int nw = blockDim.x >> 6;
+    const int nw = n >> 6;
     i64 r = MAX ? INT64_MIN : 0;
     for (int i = 0; i < nw; i += 4) {
       const i64 a0 = slot[i], a1 = slot[i + 1], a2 = slot[i + 2], a3 = slot[i + 3];
@@ -213,7 +216,7 @@ struct BlockRed {
       slot[8 + (threadIdx.x >> 6)] = b;
     }
     __syncthreads();
-    const int nw = blockDim.x >> 6;
+    const int nw = n >> 6;
     i64 ra = 0, rb = 0;
     for (int i = 0; i < nw; ++i) {
       ra = wadd(ra, slot[i]);
@@ -241,7 +244,7 @@ struct BlockRed {
       slot[16 + (threadIdx.x >> 6)] = b;
     }
     __syncthreads();
-    const int nw = blockDim.x >> 6;
+    const int nw = n >> 6;
     uint32_t ra = 0, rb = 0;
     for (int i = 0; i < nw; i += 4) {  // 4 reads in flight; entries past nw ignored
       const uint32_t a0 = slot[i], a1 = slot[i + 1], a2 = slot[i + 2], a3 = slot[i + 3];

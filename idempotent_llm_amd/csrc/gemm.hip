@@ -277,8 +277,10 @@ __global__ __launch_bounds__(64 * WGM * WGN, MINB) void k_gemm_nt2(const int8_t*
 template <int MB, int KW, int NB>
 __global__ __launch_bounds__(256) void k_gemv_nt(GemvArgs g, Prefetch pf) {
   __shared__ GemvLds<MB, KW> lds;
-  if (blockIdx.y == 0) prefetch_lines(pf, (i64)blockIdx.x * blockDim.x + threadIdx.x);
+  const PrefetchHold ph =
+      prefetch_issue(pf, blockIdx.y == 0 ? (i64)blockIdx.x * 256 + threadIdx.x : (i64)-1);
   gemv_block<MB, KW, NB>(g, blockIdx.x, blockIdx.y, lds);
+  prefetch_keep(pf, ph);
 }
 
 // Skinny GEMM over many columns (the LM head) for M <= 16 rows: the A rows
@@ -296,7 +298,7 @@ __global__ __launch_bounds__(256) void k_gemv_stream(const int8_t* __restrict__ 
                                                      int K, Prefetch pf) {
   extern __shared__ __attribute__((aligned(16))) int8_t sa[];  // [16][K]
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  prefetch_lines(pf, (i64)blockIdx.x * blockDim.x + tid);
+  const PrefetchHold ph = prefetch_issue(pf, (i64)blockIdx.x * 256 + tid);
   for (int i = tid * 16; i < 16 * K; i += 256 * 16)
     *(v4i*)(sa + i) = i / K < M ? *(const v4i*)(A + i) : zero4();
   __syncthreads();
@@ -328,6 +330,7 @@ __global__ __launch_bounds__(256) void k_gemv_stream(const int8_t* __restrict__ 
       if (row < M && col < N) C[(i64)row * N + col] = acc[r];
     }
   }
+  prefetch_keep(pf, ph);
 }
 
 __global__ void k_transpose_i8(const int8_t* __restrict__ src, int8_t* __restrict__ dst, int R,
@@ -415,7 +418,7 @@ __device__ __forceinline__ u64 mix64(u64 z) {
 __global__ __launch_bounds__(1024) void k_logits_digest(const int32_t* __restrict__ rows, int V,
                                                         int64_t* out) {
   __shared__ i64 red_buf[32];
-  BlockRed red{red_buf, 0};
+  BlockRed red{red_buf, 0, 1024};
   const int32_t* row = rows + (i64)blockIdx.x * V;
   i64 acc = 0;
   for (int i = threadIdx.x; i < V; i += blockDim.x)

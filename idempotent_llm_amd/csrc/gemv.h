@@ -132,19 +132,31 @@ struct Prefetch {
   int32_t* sink;
 };
 
-__device__ __forceinline__ void prefetch_lines(const Prefetch& pf, i64 t) {
-  int32_t v = 0;
-  bool hit = false;
+// The touched word, held until the end of the kernel (prefetch_keep): a
+// consumer right after the load, or a register reused while the load is in
+// flight, would make the kernel wait for it before its own loads.
+struct PrefetchHold {
+  int32_t v;
+  bool hit;
+};
+
+__device__ __forceinline__ PrefetchHold prefetch_issue(const Prefetch& pf, i64 t) {
+  const int8_t* q = nullptr;  // thread t's line: the ranges laid end to end
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const i64 lines = (pf.n[i] + 127) >> 7;
-    if (t >= 0 && t < lines) {  // offset 128 t < n, and n is a multiple of 4
-      v = *(const int32_t*)(pf.p[i] + (t << 7));
-      hit = true;
-    }
+    if (q == nullptr && t >= 0 && t < lines) q = pf.p[i] + (t << 7);  // 128 t < n, n % 4 == 0
     t -= lines;
   }
-  if (hit && pf.sink) *pf.sink = v;
+  PrefetchHold h;
+  h.hit = q != nullptr;
+  h.v = 0;
+  if (h.hit) h.v = *(const int32_t*)q;
+  return h;
+}
+
+__device__ __forceinline__ void prefetch_keep(const Prefetch& pf, const PrefetchHold& h) {
+  if (h.hit && pf.sink) *pf.sink = h.v;
 }
 
 // K range per split (a multiple of 64)

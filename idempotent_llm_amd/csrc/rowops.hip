@@ -270,6 +270,7 @@ __device__ __forceinline__ void load_rows_i32_sum(i64 (&v)[NR][VPT], const int32
 
 struct ResNormArgs {
   int C;
+  int nt;    // threads per block (set by the launch)
   int mode;  // 0: embedding gather (residual_from_delta); 1: GEMM residual add;
              // 2: norm-quant of the given rows only
   i64 vocab;
@@ -372,12 +373,13 @@ __device__ __forceinline__ void residual_normq_row(const ResNormArgs& a, int r, 
 template <int VPT, int NT = RT_WIDE>
 __global__ __launch_bounds__(NT) void k_residual_normq(ResNormArgs a) {
   __shared__ i64 red_buf[32];
-  BlockRed red{red_buf, 0};
+  BlockRed red{red_buf, 0, a.nt};
   residual_normq_row<VPT>(a, blockIdx.x, red);
 }
 
 struct SwigluArgs {
   int I;
+  int nt;    // threads per block (set by the launch)
   const int32_t* P;  // [nsplit][R][2I]: gate | up
   int nsplit;
   i64 split_stride;
@@ -445,12 +447,13 @@ template <int VPT, int NT = RT_WIDE>
 __global__ __launch_bounds__(NT, (NT == 256 && VPT >= 8 && VPT <= 12) ? 3 : 1) void k_swiglu_quant(
     SwigluArgs a) {
   __shared__ i64 red_buf[32];
-  BlockRed red{red_buf, 0};
+  BlockRed red{red_buf, 0, a.nt};
   swiglu_quant_row<VPT>(a, blockIdx.x, red);
 }
 
 struct MergeArgs {
   int C;
+  int nt;    // threads per block (set by the launch)
   const int64_t* attn;  // [nsplit][R][C]
   int nsplit;
   i64 split_stride;
@@ -550,7 +553,7 @@ __device__ __forceinline__ void merge_rowcol_row(const MergeArgs& a, int r, Red&
 template <int VPT, int NT = RT_WIDE>
 __global__ __launch_bounds__(NT) void k_merge_rowcol(MergeArgs a) {
   __shared__ i64 red_buf[32];
-  BlockRed red{red_buf, 0};
+  BlockRed red{red_buf, 0, a.nt};
   merge_rowcol_row<VPT>(a, blockIdx.x, red);
 }
 
@@ -621,7 +624,7 @@ __global__ __launch_bounds__(RT) void k_op_quant(const int64_t* x, const int64_t
                                                  const int64_t* k, int C, int8_t* x8,
                                                  int64_t* mo, int64_t* ko) {
   __shared__ i64 red_buf[32];
-  BlockRed red{red_buf, 0};
+  BlockRed red{red_buf, 0, RT};
   const int r = blockIdx.x;
   i64 v[VPT];
   load_row64(v, x, (i64)r * C, C);
@@ -634,7 +637,7 @@ __global__ __launch_bounds__(RT) void k_op_requant_common(const int64_t* P, cons
                                                           int tb, int C, int32_t* y,
                                                           int64_t* ko) {
   __shared__ i64 red_buf[32];
-  BlockRed red{red_buf, 0};
+  BlockRed red{red_buf, 0, RT};
   const int r = blockIdx.x;
   i64 v[VPT];
   load_row64(v, P, (i64)r * C, C);
@@ -655,7 +658,7 @@ __global__ __launch_bounds__(RT) void k_op_rowcol(const int64_t* P, const int64_
                                                   i64 col_k, int C, int8_t* y8, int64_t* mo,
                                                   int64_t* ko) {
   __shared__ i64 red_buf[32];
-  BlockRed red{red_buf, 0};
+  BlockRed red{red_buf, 0, RT};
   const int r = blockIdx.x;
   i64 v[VPT];
   load_row64(v, P, (i64)r * C, C);
@@ -689,7 +692,7 @@ __global__ __launch_bounds__(RT) void k_op_residual(int mode, const int64_t* h_i
                                                     const int64_t* dm, const int64_t* dk, int C,
                                                     int32_t* h_out, int64_t* k_out) {
   __shared__ i64 red_buf[32];
-  BlockRed red{red_buf, 0};
+  BlockRed red{red_buf, 0, RT};
   const int r = blockIdx.x;
   i64 h[VPT];
   load_row64(h, h_in, (i64)r * C, C);
@@ -713,7 +716,7 @@ template <int VPT>
 __global__ __launch_bounds__(RT) void k_op_rmsnorm(const int64_t* x, const int64_t* gamma_m,
                                                    int C, int32_t* y32, int64_t* y64) {
   __shared__ i64 red_buf[32];
-  BlockRed red{red_buf, 0};
+  BlockRed red{red_buf, 0, RT};
   const int r = blockIdx.x;
   i64 v[VPT];
   load_row64(v, x, (i64)r * C, C);
@@ -735,7 +738,7 @@ __global__ __launch_bounds__(RT) void k_op_softmax(const int64_t* x, const int64
                                                    int C, int32_t* probs) {
   // ops/di_softmax.py:33-61
   __shared__ i64 red_buf[32];
-  BlockRed red{red_buf, 0};
+  BlockRed red{red_buf, 0, RT};
   const int r = blockIdx.x;
   const i64 off = (i64)r * C;
   const i64 NEG = INT64_MIN + 1;
@@ -1014,7 +1017,7 @@ __global__ __launch_bounds__(PRO_THREADS) void k_gemv_pro(ProGemv g, ResNormArgs
       b[n][i] = (col < g.N && k < g.K) ? *(const v4i*)(g.B + (i64)col * g.K + k) : zero4();
     }
   }
-  if (by == 0) prefetch_lines(pf, (i64)bx * PRO_THREADS + tid);
+  const PrefetchHold ph = prefetch_issue(pf, by == 0 ? (i64)bx * PRO_THREADS + tid : (i64)-1);
   // 2. the operand rows into LDS
   const bool lead = bx == 0 && by == 0;  // the block that stores the row outputs
   if (PRO == 1) {
@@ -1028,7 +1031,7 @@ __global__ __launch_bounds__(PRO_THREADS) void k_gemv_pro(ProGemv g, ResNormArgs
       a.xk = nullptr;
     }
     if (ONE) {
-      BlockRed red{L.red_buf, 0};
+      BlockRed red{L.red_buf, 0, PRO_THREADS};
       residual_normq_row<CMAX / PRO_THREADS>(a, 0, red);
     } else if (wave < g.R) {
       WaveRed red;
@@ -1043,7 +1046,7 @@ __global__ __launch_bounds__(PRO_THREADS) void k_gemv_pro(ProGemv g, ResNormArgs
       a.ak = nullptr;
     }
     if (ONE) {
-      BlockRed red{L.red_buf, 0};
+      BlockRed red{L.red_buf, 0, PRO_THREADS};
       merge_rowcol_row<CMAX / PRO_THREADS>(a, 0, red);
     } else if (wave < g.R) {
       WaveRed red;
@@ -1082,6 +1085,7 @@ __global__ __launch_bounds__(PRO_THREADS) void k_gemv_pro(ProGemv g, ResNormArgs
       if (row < g.R && col < g.N) g.C[by * g.split_stride + (i64)row * g.N + col] = s;
     }
   }
+  prefetch_keep(pf, ph);
 }
 
 // One launch of k_gemv_pro.
@@ -1127,15 +1131,16 @@ void launch_pro(const ProGemv& g, int ni, int ksplit, const ResNormArgs& ra, con
     default: return DI_ERANGE;                                                            \
   }
 
-#define DI_WIDE_DISPATCH(C, KERNEL, GRID, STREAM, ...)                                       \
+#define DI_WIDE_DISPATCH(C, KERNEL, GRID, STREAM, ARGS)                                      \
   do {                                                                                       \
     int thr_, vpt_;                                                                          \
     if (!wide_shape((C), &thr_, &vpt_)) return DI_ENOSYS;                                    \
+    (ARGS).nt = thr_;                                                                        \
     switch (vpt_) {                                                                          \
-      case 1: hipLaunchKernelGGL(KERNEL<1>, GRID, dim3(thr_), 0, STREAM, __VA_ARGS__); break; \
-      case 2: hipLaunchKernelGGL(KERNEL<2>, GRID, dim3(thr_), 0, STREAM, __VA_ARGS__); break; \
-      case 3: hipLaunchKernelGGL(KERNEL<3>, GRID, dim3(thr_), 0, STREAM, __VA_ARGS__); break; \
-      default: hipLaunchKernelGGL(KERNEL<4>, GRID, dim3(thr_), 0, STREAM, __VA_ARGS__); break; \
+      case 1: hipLaunchKernelGGL(KERNEL<1>, GRID, dim3(thr_), 0, STREAM, ARGS); break;      \
+      case 2: hipLaunchKernelGGL(KERNEL<2>, GRID, dim3(thr_), 0, STREAM, ARGS); break;      \
+      case 3: hipLaunchKernelGGL(KERNEL<3>, GRID, dim3(thr_), 0, STREAM, ARGS); break;      \
+      default: hipLaunchKernelGGL(KERNEL<4>, GRID, dim3(thr_), 0, STREAM, ARGS); break;     \
     }                                                                                        \
   } while (0)
 
@@ -1143,18 +1148,19 @@ void launch_pro(const ProGemv& g, int ni, int ksplit, const ResNormArgs& ra, con
 // to 16 columns per thread: the per-row work (reductions, scale fits,
 // divisors) is then shared by 4 waves instead of up to 16, and more rows fit
 // on a CU at once. Decode-sized calls keep the wide blocks, which shorten
-// the per-row serial chain.
-#define DI_ROWS_DISPATCH(R, C, KERNEL, GRID, STREAM, ...)                                       \
+// the per-row serial chain. ARGS.nt tells the kernel its block size.
+#define DI_ROWS_DISPATCH(R, C, KERNEL, GRID, STREAM, ARGS)                                      \
   do {                                                                                          \
     if ((R) > 64) {                                                                             \
       const int v_ = ((C) + 255) / 256;                                                         \
-      if (v_ <= 4) hipLaunchKernelGGL((KERNEL<4, 256>), GRID, dim3(256), 0, STREAM, __VA_ARGS__);   \
-      else if (v_ <= 8) hipLaunchKernelGGL((KERNEL<8, 256>), GRID, dim3(256), 0, STREAM, __VA_ARGS__); \
-      else if (v_ <= 12) hipLaunchKernelGGL((KERNEL<12, 256>), GRID, dim3(256), 0, STREAM, __VA_ARGS__); \
-      else if (v_ <= 16) hipLaunchKernelGGL((KERNEL<16, 256>), GRID, dim3(256), 0, STREAM, __VA_ARGS__); \
+      (ARGS).nt = 256;                                                                          \
+      if (v_ <= 4) hipLaunchKernelGGL((KERNEL<4, 256>), GRID, dim3(256), 0, STREAM, ARGS);      \
+      else if (v_ <= 8) hipLaunchKernelGGL((KERNEL<8, 256>), GRID, dim3(256), 0, STREAM, ARGS); \
+      else if (v_ <= 12) hipLaunchKernelGGL((KERNEL<12, 256>), GRID, dim3(256), 0, STREAM, ARGS); \
+      else if (v_ <= 16) hipLaunchKernelGGL((KERNEL<16, 256>), GRID, dim3(256), 0, STREAM, ARGS); \
       else return DI_ENOSYS;                                                                    \
     } else {                                                                                    \
-      DI_WIDE_DISPATCH(C, KERNEL, GRID, STREAM, __VA_ARGS__);                                   \
+      DI_WIDE_DISPATCH(C, KERNEL, GRID, STREAM, ARGS);                                          \
     }                                                                                           \
   } while (0)
 
