@@ -542,6 +542,24 @@ __device__ __forceinline__ void store_pv(const v4i (&chi)[2], const v4i (&clo)[2
   }
 }
 
+// The slots a decode block scans: a.S, bounded by the device count when one
+// is given. Without one the load reads `always` (a pointer every launch
+// has) and the value is selected after it: no branch around the load, whose
+// merge would make every earlier load complete first. *over: the device
+// count exceeds a.S; the reference would scan those slots, so the result
+// would differ, and report_slots raises DI_ERR_SLOTS (after the kernel's
+// last load: a pending atomic among loads makes every wait a full one).
+__device__ __forceinline__ int scanned_slots(const DecodeArgs& a, const int64_t* always,
+                                             bool* over) {
+  const int64_t* p = a.s_dev ? a.s_dev : always;
+  const i64 sd = p[0];
+  *over = a.s_dev != nullptr && sd > (i64)a.S;
+  return a.s_dev ? (int)imax(0, imin((i64)a.S, sd)) : a.S;
+}
+__device__ __forceinline__ void report_slots(const DecodeArgs& a, bool over, bool who) {
+  if (over && who && a.err && threadIdx.x == 0) atomicOr(a.err, DI_ERR_SLOTS);
+}
+
 // K rows and validity flags of a wave's first KPRE_IT iterations of 16-slot
 // blocks (the first 16 * 16 * KPRE_IT slots of the row), loaded before the
 // fused kernel's Q/K/V epilogue so that their latency hides behind it; the
@@ -555,13 +573,13 @@ struct KPre {
   i64 new_slot;         // -1: none
 };
 
-// pg_lds: the row's page ids for slots [0, S) (filled by the caller, before
-// a barrier). Slots whose page is not mapped are masked and read page 0. VP:
+// S: the slots to scan (scanned_slots). pg_lds: the row's page ids for
+// slots [0, S) (filled by the caller, before a barrier). Slots whose page is not mapped are masked and read page 0. VP:
 // 64-slot steps of V loaded ahead. SCR: the scores live in the global
 // scratch (a.scratch) instead of LDS (a compile-time choice: LDS-only code
 // never issues flat accesses, which would wait on every outstanding load).
 template <int G, int VP, bool SCR>
-__device__ __forceinline__ void decode_body(const DecodeArgs& a, int kvh, int b,
+__device__ __forceinline__ void decode_body(const DecodeArgs& a, int S, int kvh, int b,
                                             const int8_t* qsrc, const int64_t* tsrc,
                                             int32_t* sh_scores, const int32_t* pg_lds,
                                             const KPre* pre = nullptr) {
@@ -570,14 +588,6 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, int kvh, int b,
   BlockRed red{red_buf, 0, 256};
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int l16 = lane & 15, grp = lane >> 4;
-  int S = a.S;
-  if (a.s_dev) {
-    const i64 sd = a.s_dev[0];
-    // more slots than the launch was sized for: the reference would scan
-    // them, so the result would differ; report instead of truncating
-    if (sd > (i64)S && a.err && threadIdx.x == 0 && kvh == 0) atomicOr(a.err, DI_ERR_SLOTS);
-    S = (int)imax(0, imin((i64)S, sd));
-  }
   const int Spad = (a.S + 15) & ~15;
   int32_t* sc = SCR ? a.scratch + ((i64)b * a.n_q + kvh * G) * Spad : sh_scores;
   const uint8_t* vrow = a.valid + (i64)b * a.valid_stride;
@@ -801,11 +811,14 @@ __global__ __launch_bounds__(256) void k_attn_decode(DecodeArgs a) {
   __shared__ int32_t pg_lds[DEC_MAX_PAGES];
   const int kvh = blockIdx.x, b = blockIdx.y;
   const i64 q0 = (i64)b * a.n_q + kvh * G;
+  bool over;
+  const int S = scanned_slots(a, a.tpos, &over);
   const int npages = (a.S + DI_PAGE - 1) / DI_PAGE;
   for (int i = threadIdx.x; i < npages; i += 256) pg_lds[i] = a.kv.page(b, (i64)i * DI_PAGE);
   if (npages == 0 && threadIdx.x == 0) pg_lds[0] = -1;  // S = 0: loads read page 0
   __syncthreads();
-  decode_body<G, VPRE, SCR>(a, kvh, b, a.q8 + q0 * 128, a.tpos + q0, sh_scores, pg_lds);
+  decode_body<G, VPRE, SCR>(a, S, kvh, b, a.q8 + q0 * 128, a.tpos + q0, sh_scores, pg_lds);
+  report_slots(a, over, kvh == 0);
 }
 
 // Decode step with the Q/K/V epilogue fused in (G <= 2): waves 0..G-1 finish
@@ -821,37 +834,82 @@ __global__ __launch_bounds__(256) void k_qkv_attn_decode(DecodeArgs a, QKVArgs q
   __shared__ int64_t t_lds[G];
   const int kvh = blockIdx.x, b = blockIdx.y;
   const int w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));  // wave-uniform
-  int slotw = -1;
-  if (w < G) slotw = kvh * G + w;
-  else if (w == G) slotw = qa.n_q + kvh;
-  else if (w == G + 1) slotw = qa.n_q + qa.n_kv + kvh;
+  // (kernel arguments pass through opaque_* below: the optimizer would
+  // otherwise fold selects between them into loads from selected argument
+  // addresses, each behind its own wait)
+  const int n_q = opaque_i32(qa.n_q), n_kv = opaque_i32(qa.n_kv);
+  const int slotw = w < G ? kvh * G + w : w == G ? n_q + kvh : w == G + 1 ? n_q + n_kv + kvh : -1;
   __shared__ __attribute__((aligned(16))) int8_t k_new[128];
   __shared__ int32_t pg_lds[DEC_MAX_PAGES];
   const int lane = threadIdx.x & 63, l16 = lane & 15, grp = lane >> 4;
-  // 1. the loads that depend on nothing, together: the row's page ids
-  // (stored to LDS after the epilogue), the pages of the prefetched slots,
-  // the step's slot, then the epilogue's own loads
+  constexpr int NPK = KPRE_SLOTS / DI_PAGE;
+  // 1. loads whose addresses follow from the kernel arguments alone. The
+  // block's scalars come from one vector load (lane i reads word i) and the
+  // pages of the prefetched slots from another, instead of a chain of scalar
+  // loads (a scalar-load wait covers every scalar load in flight).
+  //   word 0 position, 1 xk, 2 xm, 3 the step's slot (device scalar), 4 the
+  //   scanned-slot bound (device scalar), 5-8 vq_m, vq_k, ks_m, ks_k of the
+  //   kv head; other lanes (and absent device scalars) read the position
+  const int64_t* const pos_p = opaque_ptr(qa.positions) + b;
+  const int64_t* const sb_p = opaque_ptr(qa.slot_base_dev);
+  const int64_t* const sd_p = opaque_ptr(a.s_dev);
+  const int64_t* const xk_p = opaque_ptr(qa.xk) + b;
+  const int64_t* const xm_p = opaque_ptr(qa.xm) + b;
+  const int64_t* const vqm_p = opaque_ptr(qa.vq_m) + kvh;
+  const int64_t* const vqk_p = opaque_ptr(qa.vq_k) + kvh;
+  const int64_t* const ksm_p = opaque_ptr(qa.ks_m) + kvh;
+  const int64_t* const ksk_p = opaque_ptr(qa.ks_k) + kvh;
+  const int64_t* wq = pos_p;
+  wq = lane == 1 ? xk_p : wq;
+  wq = lane == 2 ? xm_p : wq;
+  wq = lane == 3 && sb_p ? sb_p : wq;
+  wq = lane == 4 && sd_p ? sd_p : wq;
+  wq = lane == 5 ? vqm_p : wq;
+  wq = lane == 6 ? vqk_p : wq;
+  wq = lane == 7 ? ksm_p : wq;
+  wq = lane == 8 ? ksk_p : wq;
+  const i64 word = ld_global(wq);
+  // page j of the row for lanes j < NPK with slots below a.S (<= width * 128,
+  // so j < width), else page 0's entry (masked below)
+  const bool pk_ok = lane < NPK && lane * DI_PAGE < a.S;
+  const int32_t pword = a.kv.table[(i64)b * a.kv.width + (pk_ok ? lane : 0)];
+  // the row's page ids (stored to LDS after the epilogue)
+  // (npages <= width: each load is in bounds, the ones past npages masked)
   const int npages = (a.S + DI_PAGE - 1) / DI_PAGE;
   int pgv[DEC_MAX_PAGES / 256];
 #pragma unroll
   for (int q = 0; q < DEC_MAX_PAGES / 256; ++q) {
     const int i = (int)threadIdx.x + 256 * q;
-    pgv[q] = i < npages ? a.kv.page(b, (i64)i * DI_PAGE) : -1;
+    pgv[q] = a.kv.table[(i64)b * a.kv.width + (i < npages ? i : 0)];
   }
-  constexpr int NPK = KPRE_SLOTS / DI_PAGE;
-  int pgk[NPK];
-#pragma unroll
-  for (int j = 0; j < NPK; ++j) pgk[j] = j * DI_PAGE < a.S ? a.kv.page(b, (i64)j * DI_PAGE) : -1;
-  const i64 base = qa.slot_base_dev ? qa.slot_base_dev[0] : qa.slot_base;
-  // (unconditional: a wave without a head slot loads slot 0's and ignores
-  // them, so no branch merge forces the loads to complete early)
+  // the head slot's per-channel loads (unconditional: a wave without a head
+  // slot loads slot 0's and ignores them, so no branch merge forces the loads
+  // to complete early)
   const int slotl = slotw >= 0 ? slotw : 0;
-  QKVHeadIn in = qkv_head_load<NS1>(qa, b, slotl);
+  QKVHeadIn in = qkv_head_load<NS1>(qa, b, slotl, QKVScalars{});
+  // (every load above is issued before the wait for the gathered scalars)
+  __builtin_amdgcn_sched_barrier(0);
+  in.pos_raw = readlane64(word, 0);
+  in.xk = readlane64(word, 1);
+  in.xm = readlane64(word, 2);
+  in.base = sb_p ? readlane64(word, 3) : qa.slot_base;
+  in.vqm = readlane64(word, 5);
+  in.vqk = readlane64(word, 6);
+  in.ksm = readlane64(word, 7);
+  in.ksk = readlane64(word, 8);
+  const i64 sdev = readlane64(word, 4);
+  const bool over = sd_p != nullptr && sdev > (i64)a.S;
+  const int S = sd_p ? (int)imax(0, imin((i64)a.S, sdev)) : a.S;
+  const i64 base = in.base;
   qkv_head_rope_load(qa, slotl, in);  // waits for the position only
   // 2. the loads that depend on those: this wave's K rows of the scores
   // pass's first iterations (slots below the host bound a.S <= capacity; the
   // pass masks slots at or past the scanned count and slots of pages that are
   // not mapped)
+  int pgk[NPK];
+#pragma unroll
+  for (int j = 0; j < NPK; ++j)
+    pgk[j] = j * DI_PAGE < a.S ? __builtin_amdgcn_readlane(pword, j) : -1;
   KPre pre;
   int vraw[KPRE_IT][4];
   bool vok[KPRE_IT][4];
@@ -890,10 +948,11 @@ __global__ __launch_bounds__(256) void k_qkv_attn_decode(DecodeArgs a, QKVArgs q
 #pragma unroll
   for (int q = 0; q < DEC_MAX_PAGES / 256; ++q) {
     const int i = (int)threadIdx.x + 256 * q;
-    if (i < npages) pg_lds[i] = pgv[q];
+    if (i < npages) pg_lds[i] = pgv[q];  // (loaded unconditionally above)
   }
   __syncthreads();
-  decode_body<G, 2 * VPRE, SCR>(a, kvh, b, &q_lds[0][0], t_lds, sh_scores, pg_lds, &pre);
+  decode_body<G, 2 * VPRE, SCR>(a, S, kvh, b, &q_lds[0][0], t_lds, sh_scores, pg_lds, &pre);
+  report_slots(a, over, kvh == 0);
 }
 
 // ---------------------------------------------------------------------------
@@ -922,18 +981,6 @@ struct SplitArgs {
   i64 out_stride;   // elements between partials (B * n_q * 128)
 };
 
-// Slots a decode block scans: S, bounded by the device count when given (the
-// count beyond S is reported by one block, as k_attn_decode does).
-__device__ __forceinline__ int scanned_slots(const DecodeArgs& a, bool report) {
-  int S = a.S;
-  if (a.s_dev) {
-    const i64 sd = a.s_dev[0];
-    if (sd > (i64)S && report && a.err && threadIdx.x == 0) atomicOr(a.err, DI_ERR_SLOTS);
-    S = (int)imax(0, imin((i64)S, sd));
-  }
-  return S;
-}
-
 template <int G>
 __global__ __launch_bounds__(256) void k_attn_split_scores(SplitArgs sa) {
   const DecodeArgs& a = sa.d;
@@ -942,7 +989,9 @@ __global__ __launch_bounds__(256) void k_attn_split_scores(SplitArgs sa) {
   BlockRed red{red_buf, 0, 256};
   const int kvh = blockIdx.x, b = blockIdx.y, c = blockIdx.z;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, l16 = lane & 15, grp = lane >> 4;
-  const int S = scanned_slots(a, kvh == 0 && c == 0);
+  bool over;
+  const int S = scanned_slots(a, a.tpos, &over);
+  report_slots(a, over, kvh == 0 && c == 0);  // every later load depends on S anyway
   const int lo = c * sa.chunk, hi = ::min(lo + sa.chunk, S);
   const i64 q0 = (i64)b * a.n_q + kvh * G;
   int32_t* cm = sa.cmax + q0 * sa.ns + c;  // head hh at cm[hh * ns]
@@ -1018,7 +1067,8 @@ __global__ __launch_bounds__(256) void k_attn_split_pv(SplitArgs sa) {
   BlockRed red{red_buf, 0, 256};
   const int kvh = blockIdx.x, b = blockIdx.y, c = blockIdx.z;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, l16 = lane & 15, grp = lane >> 4;
-  const int S = scanned_slots(a, false);
+  bool over;
+  const int S = scanned_slots(a, a.tpos, &over);
   const int lo = c * sa.chunk, hi = ::min(lo + sa.chunk, S);
   const i64 q0 = (i64)b * a.n_q + kvh * G;
   int64_t* outp = a.out + c * sa.out_stride + q0 * 128;
@@ -1233,7 +1283,7 @@ int detllm_qkv_attn_decode(const int32_t* P, int nsplit, int64_t split_stride, i
   if (B <= 0) return DI_OK;
   if (n_q <= 0 || n_kv <= 0 || n_q % n_kv || nsplit < 1 || S < 1 ||
       !kv_ok(kpool, vpool, table, width) || S > (i64)width * DI_PAGE || valid_stride < S ||
-      max_pos <= 0 || !P || !out || !valid)
+      max_pos <= 0 || !P || !positions || !out || !valid)
     return DI_EINVAL;
   if (S > DEC_MAX_S) return DI_ERANGE;  // int32 MFMA accumulators of P.V
   if (!slot_base_dev && (slot_base < 0 || slot_base + 1 > (i64)width * DI_PAGE)) return DI_ERANGE;

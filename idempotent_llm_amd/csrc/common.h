@@ -75,6 +75,26 @@ __device__ __forceinline__ i64 torch_index(i64 x, i64 n, int32_t* err, int bit) 
   return x;
 }
 
+// A wave-uniform value the optimizer cannot trace back to the load it came
+// from (no code: readfirstlane of a scalar register is free). Used on kernel
+// arguments that are selected between, which it would otherwise turn into a
+// load from the selected argument's address.
+__device__ __forceinline__ int opaque_i32(int v) { return __builtin_amdgcn_readfirstlane(v); }
+template <class T>
+__device__ __forceinline__ T* opaque_ptr(T* p) {
+  const u64 u = (u64)p;
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)u);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(u >> 32));
+  return (T*)(((u64)hi << 32) | lo);
+}
+
+// A load through a pointer known to be global memory (a pointer rebuilt from
+// integers, as opaque_ptr returns, would otherwise be loaded as a flat
+// address, which scalar-load waits also cover).
+__device__ __forceinline__ i64 ld_global(const int64_t* p) {
+  return *(const __attribute__((address_space(1))) int64_t*)p;
+}
+
 __device__ __forceinline__ i64 shfl_xor64(i64 v, int mask) {
   int lo = (int)(v & 0xffffffff);
   int hi = (int)((u64)v >> 32);

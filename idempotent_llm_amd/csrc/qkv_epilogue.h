@@ -107,10 +107,54 @@ struct QKVHeadIn {
   int16_t cs0, cs1, sn0, sn1;  // and its RoPE table entries (widened where used)
 };
 
+// The slot of the launch's first token: the device scalar when given, else
+// the argument. The load goes through a pointer that is always valid and the
+// value is selected after it (a select of a kernel-argument address would
+// make the load a flat one, which every later scalar-load wait includes).
+__device__ __forceinline__ i64 slot_base_of(const QKVArgs& a) {
+  const int64_t* bp = a.slot_base_dev ? a.slot_base_dev : a.positions;
+  const i64 bv = bp[0];
+  // the argument as a value that is not a load (else the optimizer folds the
+  // two loads back into one through the selected address)
+  const u64 sb = (u64)a.slot_base;
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)sb);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(sb >> 32));
+  return a.slot_base_dev ? bv : (i64)(((u64)hi << 32) | lo);
+}
+
+// The kv head of head slot slotw
+__device__ __forceinline__ int qkv_kv_head(const QKVArgs& a, int slotw) {
+  const bool is_q = slotw < a.n_q, is_v = slotw >= a.n_q + a.n_kv;
+  return is_q ? slotw / (a.n_q / a.n_kv) : (is_v ? slotw - a.n_q - a.n_kv : slotw - a.n_q);
+}
+
+// The scalars of one (token row r, head slot): the row's position and input
+// scale, the step's slot, the kv head's static V scale and score scale.
+struct QKVScalars {
+  i64 pos_raw, xk, xm, base, vqm, vqk, ksm, ksk;
+};
+
+// QKVScalars by plain loads (base: slot_base_of(a))
+__device__ __forceinline__ QKVScalars qkv_scalars(const QKVArgs& a, int r, int slotw, i64 base) {
+  const int kvh = qkv_kv_head(a, slotw);
+  QKVScalars q;
+  q.pos_raw = a.positions[r];
+  q.xk = a.xk[r];
+  q.xm = a.xm[r];
+  q.base = base;
+  q.vqm = a.vq_m[kvh];
+  q.vqk = a.vq_k[kvh];
+  q.ksm = a.ks_m[kvh];
+  q.ksk = a.ks_k[kvh];
+  return q;
+}
+
+// The per-channel loads of one (token row r, head slot), the scalars given.
 // ONE: the caller guarantees nsplit == 1 (straight-line loads, no branch
 // whose merge would force them to complete early).
 template <bool ONE = false>
-__device__ __forceinline__ QKVHeadIn qkv_head_load(const QKVArgs& a, int r, int slotw) {
+__device__ __forceinline__ QKVHeadIn qkv_head_load(const QKVArgs& a, int r, int slotw,
+                                                   const QKVScalars& sc) {
   const int lane = threadIdx.x & 63;
   const int n_heads = a.n_q + 2 * a.n_kv;
   const int NQKV = n_heads * 128;
@@ -121,10 +165,14 @@ __device__ __forceinline__ QKVHeadIn qkv_head_load(const QKVArgs& a, int r, int 
   const int kvh = is_q ? h / group : h;
   const int c0 = lane, c1 = lane + 64;
   QKVHeadIn in;
-  in.pos_raw = a.positions[r];
-  in.xk = a.xk[r];
-  in.xm = a.xm[r];
-  in.base = a.slot_base_dev ? a.slot_base_dev[0] : a.slot_base;
+  in.pos_raw = sc.pos_raw;
+  in.xk = sc.xk;
+  in.xm = sc.xm;
+  in.base = sc.base;
+  in.vqm = sc.vqm;
+  in.vqk = sc.vqk;
+  in.ksm = sc.ksm;
+  in.ksk = sc.ksk;
   const int64_t* wmp = (is_q ? a.q_m : (is_v ? a.v_m : a.k_m)) + (i64)h * 128;
   in.wm0 = wmp[c0];
   in.wm1 = wmp[c1];
@@ -137,10 +185,6 @@ __device__ __forceinline__ QKVHeadIn qkv_head_load(const QKVArgs& a, int r, int 
   in.kqm1 = a.kq_m[kvh * 128 + c1];
   in.kqk0 = a.kq_k[kvh * 128 + c0];
   in.kqk1 = a.kq_k[kvh * 128 + c1];
-  in.vqm = a.vq_m[kvh];
-  in.vqk = a.vq_k[kvh];
-  in.ksm = a.ks_m[kvh];
-  in.ksk = a.ks_k[kvh];
   if (ONE || a.nsplit == 1) {  // no K split: one load per channel
     in.p0 = a.P[off + c0];
     in.p1 = a.P[off + c1];
@@ -317,7 +361,7 @@ __device__ __forceinline__ void qkv_head_compute(const QKVArgs& a, int r, int sl
 
 __device__ __forceinline__ void qkv_head(const QKVArgs& a, int r, int slotw, int8_t* q8_out,
                                          int64_t* tpos_out, int8_t* k_lds = nullptr) {
-  QKVHeadIn in = qkv_head_load(a, r, slotw);
+  QKVHeadIn in = qkv_head_load(a, r, slotw, qkv_scalars(a, r, slotw, slot_base_of(a)));
   qkv_head_rope_load(a, slotw, in);
   qkv_head_compute(a, r, slotw, in, q8_out, tpos_out, k_lds);
   qkv_head_report(a, slotw, in);
@@ -379,7 +423,7 @@ __device__ __forceinline__ void qkv_rows4(const QKVArgs& a, int R, int r0, int s
   // ---- loads
   const i64 pos_raw = a.positions[r];
   const i64 xk = a.xk[r], xm = a.xm[r];
-  const i64 base = a.slot_base_dev ? a.slot_base_dev[0] : a.slot_base;
+  const i64 base = slot_base_of(a);
   const int64_t* wmp = (is_q ? a.q_m : (is_v ? a.v_m : a.k_m)) + (i64)h * 128;
   i64 wm[8], p[8];
 #pragma unroll

@@ -1359,7 +1359,7 @@ int detllm_qkv_epilogue(const int32_t* P, int nsplit, int64_t split_stride, int 
                         int32_t* err, hipStream_t s) {
   if (B <= 0 || T <= 0) return DI_OK;
   if (n_q <= 0 || n_kv <= 0 || n_q % n_kv != 0 || nsplit < 1 || max_pos <= 0 || !kpool ||
-      !vpool || !table || width <= 0 || width > (1 << 24))
+      !vpool || !table || width <= 0 || width > (1 << 24) || !P || !positions)
     return DI_EINVAL;
   if (!slot_base_dev && (slot_base < 0 || slot_base + T > (i64)width * DI_PAGE)) return DI_ERANGE;
   QKVArgs a{};
