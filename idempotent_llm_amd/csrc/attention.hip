@@ -522,18 +522,18 @@ __device__ __forceinline__ void p_frags(const int32_t* pp, v4i& ahi, v4i& alo) {
 }
 
 // sum_s p_s v_s of the wave's channels from the hi/lo accumulators: lane
-// (grp, l16), element r holds head 4 grp + r, channel 32 wave + 16 nb + l16;
+// (grp, l16), element r holds head 4 grp + r, channel 16 (NB wave + nb) + l16;
 // the colsum of that channel sits in row G (lane 16 (G / 4) + l16, element
 // G % 4). out_heads: the block's first head row of [.][128] int64.
-template <int G>
-__device__ __forceinline__ void store_pv(const v4i (&chi)[2], const v4i (&clo)[2],
+template <int G, int NB = 2>
+__device__ __forceinline__ void store_pv(const v4i (&chi)[NB], const v4i (&clo)[NB],
                                          int64_t* out_heads) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, l16 = lane & 15, grp = lane >> 4;
 #pragma unroll
-  for (int nb = 0; nb < 2; ++nb) {
+  for (int nb = 0; nb < NB; ++nb) {
     const int cs_src = (G / 4) * 16 + l16;
     const int32_t cs = __shfl(chi[nb][G % 4], cs_src, 64);
-    const int d = wave * 32 + nb * 16 + l16;
+    const int d = wave * 16 * NB + nb * 16 + l16;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int hh = grp * 4 + r;
@@ -560,32 +560,39 @@ __device__ __forceinline__ void report_slots(const DecodeArgs& a, bool over, boo
   if (over && who && a.err && threadIdx.x == 0) atomicOr(a.err, DI_ERR_SLOTS);
 }
 
-// K rows and validity flags of a wave's first KPRE_IT iterations of 16-slot
-// blocks (the first 16 * 16 * KPRE_IT slots of the row), loaded before the
-// fused kernel's Q/K/V epilogue so that their latency hides behind it; the
-// slot the epilogue writes is taken from LDS instead.
-constexpr int KPRE_IT = 2;
-constexpr int KPRE_SLOTS = 256 * KPRE_IT;
+// K rows and validity flags of the first KPRE_SLOTS slots of the row, loaded
+// before the fused kernel's Q/K/V epilogue so that their latency hides behind
+// it; the slot the epilogue writes is taken from LDS instead. With NW waves a
+// wave holds IT = KPRE_SLOTS / (64 NW) iterations of four 16-slot blocks.
+constexpr int KPRE_SLOTS = 512;
+template <int IT>
 struct KPre {
-  v4i kb[KPRE_IT][4][2];
-  int vf[KPRE_IT][4];   // 0 for slots of pages that are not mapped
-  const int8_t* k_new;  // LDS, 128 bytes
-  i64 new_slot;         // -1: none
+  v4i kb[IT][4][2];
+  int vf[IT][4];                 // 0 for slots of pages that are not mapped
+  int pg[KPRE_SLOTS / DI_PAGE];  // the pages of those slots (-1: not mapped or past S)
+  const int8_t* k_new;           // LDS, 128 bytes
+  i64 new_slot;                  // -1: none
 };
 
 // S: the slots to scan (scanned_slots). pg_lds: the row's page ids for
-// slots [0, S) (filled by the caller, before a barrier). Slots whose page is not mapped are masked and read page 0. VP:
-// 64-slot steps of V loaded ahead. SCR: the scores live in the global
-// scratch (a.scratch) instead of LDS (a compile-time choice: LDS-only code
-// never issues flat accesses, which would wait on every outstanding load).
-template <int G, int VP, bool SCR>
+// slots [0, S) (filled by the caller, before a barrier). Slots whose page is
+// not mapped are masked and read page 0. VP: 64-slot steps of V loaded ahead.
+// SCR: the scores live in the global scratch (a.scratch) instead of LDS (a
+// compile-time choice: LDS-only code never issues flat accesses, which would
+// wait on every outstanding load). NW: waves of the block (4 or 8): a wave
+// takes every NW-th 16-slot block of the scores and 128 / NW channels of P.V.
+template <int G, int VP, bool SCR, bool PRE = false, int NW = 4>
 __device__ __forceinline__ void decode_body(const DecodeArgs& a, int S, int kvh, int b,
                                             const int8_t* qsrc, const int64_t* tsrc,
                                             int32_t* sh_scores, const int32_t* pg_lds,
-                                            const KPre* pre = nullptr) {
+                                            const KPre<8 / NW>& pre = KPre<8 / NW>{}) {
   static_assert(G <= 8, "query heads per kv head");
+  static_assert(NW == 4 || NW == 8, "waves per block");
+  constexpr int NT = NW * 64;  // threads
+  constexpr int NB = 8 / NW;   // 16-channel blocks of P.V per wave
+  constexpr int IT = 8 / NW;   // prefetched iterations per wave
   __shared__ i64 red_buf[32];
-  BlockRed red{red_buf, 0, 256};
+  BlockRed red{red_buf, 0, NT};
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int l16 = lane & 15, grp = lane >> 4;
   const int Spad = (a.S + 15) & ~15;
@@ -604,7 +611,18 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, int S, int kvh,
   auto vfrag = [&](int st, int nb) -> v4i {
     const int s0 = st * 64 + grp * 16;
     const int sl = s0 < S ? s0 : 0;
-    const int8_t* vch = a.kv.vchan(pg_of(sl), kvh, wave * 32 + nb * 16 + l16);
+    const int8_t* vch = a.kv.vchan(pg_of(sl), kvh, wave * 16 * NB + nb * 16 + l16);
+    return *(const v4i*)(vch + (sl & (DI_PAGE - 1)));
+  };
+  // the same for a step below KPRE_SLOTS with the pages in registers (no LDS
+  // read before the load): slot st * 64 + 16 grp lies in page st / 2 (a group
+  // at or past S reads offset 0 of that page, or of page 0 when it is not
+  // mapped; its A rows are zero)
+  auto vfrag_pre = [&](int st, int nb) -> v4i {
+    const int s0 = st * 64 + grp * 16;
+    const int sl = s0 < S ? s0 : 0;
+    const int pg = pre.pg[st >> 1];
+    const int8_t* vch = a.kv.vchan(pg < 0 ? 0 : pg, kvh, wave * 16 * NB + nb * 16 + l16);
     return *(const v4i*)(vch + (sl & (DI_PAGE - 1)));
   };
 
@@ -625,11 +643,11 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, int S, int kvh,
   // Lane (grp, l16) holds C[4 grp + r][slot l16] in element r.
   int32_t mx[4] = {SCORE_MASKED, SCORE_MASKED, SCORE_MASKED, SCORE_MASKED};
   const int nblk = (S + 15) / 16;
-  // blocks blk0 + 4u (u < 4) from K fragments kb and validity flags vf
+  // blocks blk0 + NW u (u < 4) from K fragments kb and validity flags vf
   auto score4 = [&](int blk0, const v4i (&kb)[4][2], const int (&vf)[4]) {
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
-      const int blk = blk0 + u * 4;
+      const int blk = blk0 + u * NW;
       if (blk < nblk) {  // wave-uniform
         v4i c = mfma16(qa0, kb[u][0], v4i{0, 0, 0, 0});
         c = mfma16(qa1, kb[u][1], c);
@@ -647,34 +665,34 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, int S, int kvh,
     }
   };
   int blk0 = wave;
-  if (pre) {
+  if (PRE) {
 #pragma unroll
-    for (int it = 0; it < KPRE_IT; ++it) {
-      const int bb = wave + 16 * it;
+    for (int it = 0; it < IT; ++it) {
+      const int bb = wave + 4 * NW * it;
       if (bb >= nblk) continue;  // wave-uniform
       v4i kb[4][2];
       int vf[4];
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
-        kb[u][0] = pre->kb[it][u][0];
-        kb[u][1] = pre->kb[it][u][1];
-        if ((bb + u * 4) * 16 + l16 == pre->new_slot) {
-          kb[u][0] = *(const v4i*)(pre->k_new + grp * 16);
-          kb[u][1] = *(const v4i*)(pre->k_new + 64 + grp * 16);
+        kb[u][0] = pre.kb[it][u][0];
+        kb[u][1] = pre.kb[it][u][1];
+        if ((bb + u * NW) * 16 + l16 == pre.new_slot) {
+          kb[u][0] = *(const v4i*)(pre.k_new + grp * 16);
+          kb[u][1] = *(const v4i*)(pre.k_new + 64 + grp * 16);
         }
-        vf[u] = pre->vf[it][u];
+        vf[u] = pre.vf[it][u];
       }
       score4(bb, kb, vf);
     }
-    blk0 = wave + 16 * KPRE_IT;
+    blk0 = wave + 4 * NW * IT;
   }
-  for (; blk0 < nblk; blk0 += 16) {
+  for (; blk0 < nblk; blk0 += 4 * NW) {
     v4i kb[4][2];
     int vraw[4], vf[4];
     bool ok[4];
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
-      const int s = (blk0 + u * 4) * 16 + l16;
+      const int s = (blk0 + u * NW) * 16 + l16;
       const int sc_ = s < S ? s : 0;
       const int8_t* kr = a.kv.krow(pg_of(sc_), kvh, sc_ & (DI_PAGE - 1));
       kb[u][0] = *(const v4i*)(kr + grp * 16);
@@ -688,11 +706,12 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, int S, int kvh,
   }
   // the first VP steps of V, loaded now (the K fragments' registers are
   // free) to overlap the maxima, denominators and probabilities
-  v4i vpre[VP][2];
+  v4i vpre[VP][NB];
 #pragma unroll
   for (int i = 0; i < VP; ++i)
 #pragma unroll
-    for (int nb = 0; nb < 2; ++nb) vpre[i][nb] = vfrag(i, nb);
+    for (int nb = 0; nb < NB; ++nb)
+      vpre[i][nb] = (PRE && i * 64 < KPRE_SLOTS) ? vfrag_pre(i, nb) : vfrag(i, nb);
   // per-head row maxima, two heads per block reduction (int32 scores biased
   // to order-preserving unsigned values)
   i64 hmax[G];
@@ -710,25 +729,55 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, int S, int kvh,
     if (hh + 1 < G) hmax[hh + 1] = r1 == SCORE_MASKED ? 0 : r1;
   }
   __syncthreads();
-  // ---- pass 2: denominators (two heads per block reduction)
+  // ---- pass 2: denominators (two heads per block reduction). When every
+  // head takes the estimate path (the usual case), one loop serves all heads
+  // and two slots per thread, the LDS reads of an iteration issued together.
   i64 den[G];
+  bool allfast = true;
+#pragma unroll
+  for (int hh = 0; hh < G; ++hh) allfast = allfast && tph[hh] < ((i64)1 << 23);
+  ExpEst Ef[G];
+  if (allfast) {
+#pragma unroll
+    for (int hh = 0; hh < G; ++hh) {
+      Ef[hh] = make_expest(tph[hh]);
+      den[hh] = 0;
+    }
+    for (int s0 = tid; s0 < S; s0 += 2 * NT) {
+      const int s1 = s0 + NT;
+      const int s1c = s1 < S ? s1 : s0;
+      int32_t x0[G], x1[G];
+#pragma unroll
+      for (int hh = 0; hh < G; ++hh) {
+        x0[hh] = sc[hh * Spad + s0];
+        x1[hh] = sc[hh * Spad + s1c];
+      }
+#pragma unroll
+      for (int hh = 0; hh < G; ++hh) {
+        if (x0[hh] != SCORE_MASKED) den[hh] += dexp_est((uint32_t)(hmax[hh] - x0[hh]), Ef[hh]);
+        if (s1 < S && x1[hh] != SCORE_MASKED)
+          den[hh] += dexp_est((uint32_t)(hmax[hh] - x1[hh]), Ef[hh]);
+      }
+    }
+  } else {
 #pragma unroll
   for (int hh = 0; hh < G; ++hh) {
     i64 acc = 0;
     if (tph[hh] < ((i64)1 << 23)) {
       const ExpEst Ee = make_expest(tph[hh]);
-      for (int s = tid; s < S; s += 256) {
+      for (int s = tid; s < S; s += NT) {
         const int32_t x = sc[hh * Spad + s];
         if (x != SCORE_MASKED) acc += dexp_est((uint32_t)(hmax[hh] - x), Ee);
       }
     } else {
       const ExpR E = make_exp(tph[hh]);
-      for (int s = tid; s < S; s += 256) {
+      for (int s = tid; s < S; s += NT) {
         const int32_t x = sc[hh * Spad + s];
         if (x != SCORE_MASKED) acc = wadd(acc, di_exp_neg((u64)wsub(hmax[hh], (i64)x), E));
       }
     }
     den[hh] = acc;
+  }
   }
 #pragma unroll
   for (int hh = 0; hh < G; hh += 2) {
@@ -741,6 +790,36 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, int S, int kvh,
   // (0 for masked slots and the padding up to the next multiple of 16, i.e.
   // hi - 64 = -64, lo = 0)
   const int nchunk = (S + 15) / 16;
+  bool pfast = allfast;
+#pragma unroll
+  for (int hh = 0; hh < G; ++hh) pfast = pfast && den[hh] < ((i64)1 << 34);
+  if (pfast) {
+    // as pass 2: every head, two slots per thread, reads first
+    DivEst Df[G];
+#pragma unroll
+    for (int hh = 0; hh < G; ++hh) Df[hh] = make_divest(den[hh], 16384.0);
+    const int lim = nchunk * 16;
+    for (int s0 = tid; s0 < lim; s0 += 2 * NT) {
+      const int s1 = s0 + NT;
+      const int s1c = s1 < lim ? s1 : s0;
+      int32_t x0[G], x1[G];
+#pragma unroll
+      for (int hh = 0; hh < G; ++hh) {
+        x0[hh] = sc[hh * Spad + s0];
+        x1[hh] = sc[hh * Spad + s1c];
+      }
+#pragma unroll
+      for (int hh = 0; hh < G; ++hh) {
+        i64 p0 = 0, p1 = 0;
+        if (s0 < S && x0[hh] != SCORE_MASKED)
+          p0 = rhad_est((double)dexp_est((uint32_t)(hmax[hh] - x0[hh]), Ef[hh]), Df[hh]);
+        if (s1 < S && x1[hh] != SCORE_MASKED)
+          p1 = rhad_est((double)dexp_est((uint32_t)(hmax[hh] - x1[hh]), Ef[hh]), Df[hh]);
+        sc[hh * Spad + s0] = pack_p(p0);
+        if (s1 < lim) sc[hh * Spad + s1] = pack_p(p1);
+      }
+    }
+  } else {
 #pragma unroll
   for (int hh = 0; hh < G; ++hh) {
     auto put = [&](int s, i64 p) { sc[hh * Spad + s] = pack_p(p); };
@@ -748,7 +827,7 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, int S, int kvh,
       // exps below 2^23, den < 2^34: p = rhad(ex 2^14, den) from rhad_est
       const ExpEst Ee = make_expest(tph[hh]);
       const DivEst D = make_divest(den[hh], 16384.0);
-      for (int s = tid; s < nchunk * 16; s += 256) {
+      for (int s = tid; s < nchunk * 16; s += NT) {
         i64 p = 0;
         if (s < S) {
           const int32_t x = sc[hh * Spad + s];
@@ -759,7 +838,7 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, int S, int kvh,
     } else {
       const ExpR E = make_exp(tph[hh]);
       const Recip Rd = make_recip(den[hh]);
-      for (int s = tid; s < nchunk * 16; s += 256) {
+      for (int s = tid; s < nchunk * 16; s += NT) {
         i64 p = 0;
         if (s < S) {
           const int32_t x = sc[hh * Spad + s];
@@ -772,10 +851,13 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, int S, int kvh,
       }
     }
   }
+  }
   __syncthreads();
   // ---- P.V on MFMA
-  v4i chi[2] = {v4i{0, 0, 0, 0}, v4i{0, 0, 0, 0}}, clo[2] = {v4i{0, 0, 0, 0}, v4i{0, 0, 0, 0}};
-  auto pv_step = [&](int st, const v4i (&vb)[2]) {
+  v4i chi[NB], clo[NB];
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) chi[nb] = clo[nb] = v4i{0, 0, 0, 0};
+  auto pv_step = [&](int st, const v4i (&vb)[NB]) {
     v4i ahi = v4i{0, 0, 0, 0}, alo = v4i{0, 0, 0, 0};
     const int s0 = st * 64 + grp * 16;
     if (l16 < G && s0 < S) {
@@ -784,7 +866,7 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, int S, int kvh,
       ahi = v4i{0x01010101, 0x01010101, 0x01010101, 0x01010101};  // colsum row
     }
 #pragma unroll
-    for (int nb = 0; nb < 2; ++nb) {
+    for (int nb = 0; nb < NB; ++nb) {
       chi[nb] = mfma16(ahi, vb[nb], chi[nb]);
       clo[nb] = mfma16(alo, vb[nb], clo[nb]);
     }
@@ -793,16 +875,16 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, int S, int kvh,
   for (int i = 0; i < VP; ++i)
     if (i < nstep) pv_step(i, vpre[i]);
   for (int st0 = VP; st0 < nstep; st0 += 4) {
-    v4i vb[4][2];
+    v4i vb[4][NB];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
-      for (int nb = 0; nb < 2; ++nb) vb[i][nb] = vfrag(st0 + i, nb);
+      for (int nb = 0; nb < NB; ++nb) vb[i][nb] = vfrag(st0 + i, nb);
 #pragma unroll
     for (int i = 0; i < 4; ++i)
       if (st0 + i < nstep) pv_step(st0 + i, vb[i]);
   }
-  store_pv<G>(chi, clo, a.out + (i64)b * a.n_q * 128 + kvh * G * 128);
+  store_pv<G, NB>(chi, clo, a.out + (i64)b * a.n_q * 128 + kvh * G * 128);
 }
 
 template <int G, bool SCR>
@@ -823,12 +905,16 @@ __global__ __launch_bounds__(256) void k_attn_decode(DecodeArgs a) {
 
 // Decode step with the Q/K/V epilogue fused in (G <= 2): waves 0..G-1 finish
 // the block's query heads into LDS, wave G writes the key head and wave G + 1
-// the value head of this step's slot into the cache; after one barrier the
-// block attends over every slot, the new one included. NS1: the Q/K/V
-// product has no K split (qa.nsplit == 1). SCR as in decode_body.
+// the value head of this step's slot into the cache (the other waves only
+// prefetch); after one barrier the block's QAD_WAVES waves attend over every
+// slot, the new one included (two waves per SIMD, each with half the slots
+// and channels of a four-wave block). NS1: the Q/K/V product has no K split
+// (qa.nsplit == 1). SCR as in decode_body.
+constexpr int QAD_WAVES = 8;
 template <int G, bool NS1, bool SCR>
-__global__ __launch_bounds__(256) void k_qkv_attn_decode(DecodeArgs a, QKVArgs qa) {
-  static_assert(G + 2 <= 4, "one wave per head slot");
+__global__ __launch_bounds__(QAD_WAVES * 64) void k_qkv_attn_decode(DecodeArgs a, QKVArgs qa) {
+  constexpr int NW = QAD_WAVES, NT = NW * 64, IT = 8 / NW;
+  static_assert(G + 2 <= NW, "one wave per head slot");
   extern __shared__ __attribute__((aligned(16))) int32_t sh_scores[];
   __shared__ __attribute__((aligned(16))) int8_t q_lds[G][128];
   __shared__ int64_t t_lds[G];
@@ -876,10 +962,10 @@ __global__ __launch_bounds__(256) void k_qkv_attn_decode(DecodeArgs a, QKVArgs q
   // the row's page ids (stored to LDS after the epilogue)
   // (npages <= width: each load is in bounds, the ones past npages masked)
   const int npages = (a.S + DI_PAGE - 1) / DI_PAGE;
-  int pgv[DEC_MAX_PAGES / 256];
+  int pgv[DEC_MAX_PAGES / NT];
 #pragma unroll
-  for (int q = 0; q < DEC_MAX_PAGES / 256; ++q) {
-    const int i = (int)threadIdx.x + 256 * q;
+  for (int q = 0; q < DEC_MAX_PAGES / NT; ++q) {
+    const int i = (int)threadIdx.x + NT * q;
     pgv[q] = a.kv.table[(i64)b * a.kv.width + (i < npages ? i : 0)];
   }
   // the head slot's per-channel loads (unconditional: a wave without a head
@@ -910,16 +996,16 @@ __global__ __launch_bounds__(256) void k_qkv_attn_decode(DecodeArgs a, QKVArgs q
 #pragma unroll
   for (int j = 0; j < NPK; ++j)
     pgk[j] = j * DI_PAGE < a.S ? __builtin_amdgcn_readlane(pword, j) : -1;
-  KPre pre;
-  int vraw[KPRE_IT][4];
-  bool vok[KPRE_IT][4];
+  KPre<IT> pre;
+  int vraw[IT][4];
+  bool vok[IT][4];
   {
     const uint8_t* vrow = a.valid + (i64)b * a.valid_stride;
 #pragma unroll
-    for (int it = 0; it < KPRE_IT; ++it)
+    for (int it = 0; it < IT; ++it)
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
-        const int s = (w + 16 * it + u * 4) * 16 + l16;  // < KPRE_SLOTS
+        const int s = (w + 4 * NW * it + u * NW) * 16 + l16;  // < KPRE_SLOTS
         const int sc_ = s < a.S ? s : 0;
         const int j = sc_ >> 7;
         int pg = pgk[0];
@@ -932,6 +1018,8 @@ __global__ __launch_bounds__(256) void k_qkv_attn_decode(DecodeArgs a, QKVArgs q
         vok[it][u] = pg >= 0;
       }
     pre.k_new = k_new;
+#pragma unroll
+    for (int j = 0; j < NPK; ++j) pre.pg[j] = pgk[j];
   }
   // 3. the epilogue
   if (slotw >= 0)
@@ -939,19 +1027,20 @@ __global__ __launch_bounds__(256) void k_qkv_attn_decode(DecodeArgs a, QKVArgs q
                      w == G ? k_new : nullptr);
   if (slotw >= 0) qkv_head_report(qa, slotw, in);
 #pragma unroll
-  for (int it = 0; it < KPRE_IT; ++it)
+  for (int it = 0; it < IT; ++it)
 #pragma unroll
     for (int u = 0; u < 4; ++u) pre.vf[it][u] = vok[it][u] ? vraw[it][u] : 0;
   // T = 1: the step's slot is base (when its page is not mapped nothing was
   // written, and the slot is masked: the substituted row is never a score)
   pre.new_slot = base;
 #pragma unroll
-  for (int q = 0; q < DEC_MAX_PAGES / 256; ++q) {
-    const int i = (int)threadIdx.x + 256 * q;
+  for (int q = 0; q < DEC_MAX_PAGES / NT; ++q) {
+    const int i = (int)threadIdx.x + NT * q;
     if (i < npages) pg_lds[i] = pgv[q];  // (loaded unconditionally above)
   }
   __syncthreads();
-  decode_body<G, 2 * VPRE, SCR>(a, S, kvh, b, &q_lds[0][0], t_lds, sh_scores, pg_lds, &pre);
+  decode_body<G, 2 * VPRE, SCR, true, NW>(a, S, kvh, b, &q_lds[0][0], t_lds, sh_scores, pg_lds,
+                                          pre);
   report_slots(a, over, kvh == 0);
 }
 
@@ -1311,8 +1400,8 @@ int detllm_qkv_attn_decode(const int32_t* P, int nsplit, int64_t split_stride, i
   DecodeArgs a{nullptr, nullptr, kv, valid, out, scratch, s_dev, S, n_q, n_kv, valid_stride, err};
   const dim3 grid(n_kv, B);
 #define DI_QAD_LAUNCH(G_, NS1_)                                                                 \
-  if (scratch) hipLaunchKernelGGL((k_qkv_attn_decode<G_, NS1_, true>), grid, dim3(256), dyn, s, a, qa); \
-  else hipLaunchKernelGGL((k_qkv_attn_decode<G_, NS1_, false>), grid, dim3(256), dyn, s, a, qa)
+  if (scratch) hipLaunchKernelGGL((k_qkv_attn_decode<G_, NS1_, true>), grid, dim3(QAD_WAVES * 64), dyn, s, a, qa); \
+  else hipLaunchKernelGGL((k_qkv_attn_decode<G_, NS1_, false>), grid, dim3(QAD_WAVES * 64), dyn, s, a, qa)
   if (G == 1) {
     if (nsplit == 1) { DI_QAD_LAUNCH(1, true); }
     else { DI_QAD_LAUNCH(1, false); }
