@@ -198,18 +198,25 @@ DI_HD void fit_dyadic_ratio(i64 num, i64 den, i64* m_out, i64* e_out) {
 // 127 * 2^s use the constant reciprocal floor((2^64 - 1) / 127) whenever no
 // operand of the generic path wraps (num < 2^56, shifts below 56), else the
 // generic path runs.
+// floor(y / 127) for 0 <= y < 2^32 from one fp64 fma: y / 127 has a
+// fractional part that is a multiple of 1/127 (0, or between 1/127 and
+// 126/127), and fma(y, fl(1/127), 2^-12) lies within 2^-19 of
+// y / 127 + 2^-12 (fl(1/127) is within 2^-60 of 1/127, i.e. y 2^-60 < 2^-28
+// absolute, and the one rounding of a result below 2^26 adds at most 2^-27),
+// so its truncation is the integer quotient.
+DI_HD uint32_t floor_div127(uint32_t y) {
+  return (uint32_t)fma((double)y, 1.0 / 127.0, 0x1p-12);
+}
+
 DI_HD i64 srd127(i64 num, i64 e) {
-  // scaled_round_div(num, 127, e) for 0 < num < 2^56, |e| < 56 and no wrap of
-  // num << e: rhad(x, 127 * 2^s) = floor(floor((x + h) / 2^s) / 127) with
-  // h = floor(127 * 2^s / 2).
-  const Recip R127{127ull, 0x0204081020408102ull};
-  if (e >= 0) {
-    const u64 x = (u64)num << e;
-    return (i64)udiv(x + 63, R127);
-  }
+  // scaled_round_div(num, 127, e) for 0 < num < 2^56 when the quotient is
+  // below 2^17 (the callers fit a 16-bit mantissa): rhad(x, 127 * 2^s) =
+  // floor(floor((x + h) / 2^s) / 127) with h = floor(127 * 2^s / 2), and
+  // rhad(x, 127) = floor((x + 63) / 127); either dividend is below 2^24.
+  if (e >= 0) return (i64)floor_div127((uint32_t)(((u64)num << e) + 63));
   const int s = (int)(-e);
   const u64 h = (127ull << s) >> 1;
-  return (i64)udiv(((u64)num + h) >> s, R127);
+  return (i64)floor_div127((uint32_t)(((u64)num + h) >> s));
 }
 
 DI_HD void fit_dyadic_ratio_127(i64 num, i64* m_out, i64* e_out) {

@@ -42,6 +42,7 @@ void di_host_scalar(int op, const int64_t* a, const int64_t* b, const int64_t* c
       case 6: o1[i] = rhad_pow2(a[i], (int)b[i]); break;
       case 7: o1[i] = di_exp_tpos_fast(a[i], b[i]); break;
       case 8: o1[i] = isqrt_est(a[i]); break;
+      case 9: o1[i] = floor_div127((uint32_t)a[i]); break;
       default: o1[i] = scaled_round_div(a[i], b[i], c[i]); break;
     }
   }

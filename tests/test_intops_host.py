@@ -204,6 +204,19 @@ def test_fit127_fast_path_matches_generic_and_golden(lib, golden_dir):
     assert np.array_equal(fm, om) and np.array_equal(fe, oe)
 
 
+def test_floor_div127_estimate(lib):
+    """floor(y / 127) from one fp64 fma (the divisions inside the constant-127
+    fit): every y below 2^20, and around every multiple of 127 up to 2^32 in
+    strides, against integer division."""
+    ks = np.arange(0, (1 << 32) // 127, 997, dtype=I64)
+    y = np.concatenate([np.arange(0, 1 << 20, dtype=I64)] +
+                       [ks * 127 + d for d in (-1, 0, 1, 63, 126)] +
+                       [np.array([(1 << 32) - 1, (1 << 32) - 2, (1 << 24) - 1, 1 << 24], I64)])
+    y = y[(y >= 0) & (y < (1 << 32))]
+    got, _ = _scalar(lib, 9, y)
+    assert np.array_equal(got, y // 127)
+
+
 def test_rhad_pow2_matches_rhad(lib):
     rnd = np.random.default_rng(12)
     a = np.concatenate([rnd.integers(-(1 << 63), (1 << 63) - 1, 40000, dtype=I64, endpoint=True),
