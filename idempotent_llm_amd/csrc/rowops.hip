@@ -209,6 +209,72 @@ __device__ __forceinline__ void prefetch_cols(i64 (&v)[VPT], const int64_t* x, i
     if (red.tid() + j * red.nt() >= C) v[j] = 0;
 }
 
+// x[c] for this thread's columns, 0 past C or when x is null. The load goes
+// through alt (valid for C columns) when x is null and is masked after, so
+// there is no branch around it (a branch merge makes earlier loads complete).
+template <int VPT, class Red>
+__device__ __forceinline__ void load_cols_or0(i64 (&v)[VPT], const int64_t* x, const int64_t* alt,
+                                              int C, const Red& red) {
+  const int64_t* p = x ? x : alt;
+#pragma unroll
+  for (int j = 0; j < VPT; ++j) {
+    const int c = red.tid() + j * red.nt();
+    v[j] = p[c < C ? c : C - 1];
+  }
+#pragma unroll
+  for (int j = 0; j < VPT; ++j)
+    if (red.tid() + j * red.nt() >= C || !x) v[j] = 0;
+}
+
+// The first KF of the nsplit int32 partials P[k * stride + off + c], issued
+// unconditionally (k clamped to nsplit - 1, nsplit >= 1); rows_i32_sum adds
+// them, and the partials past KF, in a fixed order.
+template <int KF, int NR, int VPT, class Red>
+__device__ __forceinline__ void load_rows_i32_first(int32_t (&t)[KF][NR][VPT], const int32_t* P,
+                                                    int nsplit, i64 stride, const i64 (&off)[NR],
+                                                    int C, const Red& red) {
+#pragma unroll
+  for (int kk = 0; kk < KF; ++kk) {
+    const int k = kk < nsplit ? kk : nsplit - 1;
+#pragma unroll
+    for (int q = 0; q < NR; ++q)
+#pragma unroll
+      for (int j = 0; j < VPT; ++j) {
+        const int c = red.tid() + j * red.nt();
+        t[kk][q][j] = P[(i64)k * stride + off[q] + (c < C ? c : C - 1)];
+      }
+  }
+}
+template <int KF, int NR, int VPT, class Red>
+__device__ __forceinline__ void rows_i32_sum(i64 (&v)[NR][VPT], const int32_t (&t)[KF][NR][VPT],
+                                             const int32_t* P, int nsplit, i64 stride,
+                                             const i64 (&off)[NR], int C, const Red& red) {
+  uint32_t s[NR][VPT];
+#pragma unroll
+  for (int q = 0; q < NR; ++q)
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) {
+      uint32_t a = 0;
+#pragma unroll
+      for (int kk = 0; kk < KF; ++kk)
+        if (kk < nsplit) a += (uint32_t)t[kk][q][j];
+      s[q][j] = a;
+    }
+  for (int k = KF; k < nsplit; ++k)  // more partials than KF: one at a time
+#pragma unroll
+    for (int q = 0; q < NR; ++q)
+#pragma unroll
+      for (int j = 0; j < VPT; ++j) {
+        const int c = red.tid() + j * red.nt();
+        s[q][j] += (uint32_t)P[(i64)k * stride + off[q] + (c < C ? c : C - 1)];
+      }
+#pragma unroll
+  for (int q = 0; q < NR; ++q)
+#pragma unroll
+    for (int j = 0; j < VPT; ++j)
+      v[q][j] = red.tid() + j * red.nt() < C ? (i64)(int32_t)s[q][j] : 0;
+}
+
 // Sum of nsplit int32 partials P[k * stride + off + c] (the K-split of the
 // skinny GEMM) in a fixed order, for NR rows at offsets off[0..NR).
 template <int NR, int VPT, class Red>
@@ -306,6 +372,35 @@ __device__ __forceinline__ void residual_normq_row(const ResNormArgs& a, int r, 
   i64 h[VPT], d[VPT], smv[VPT];
   i64 kr, lg = -1;
   const int32_t* h_in = a.h_in ? a.h_in : a.h;
+  if (a.mode == 1) {
+    // the GEMM residual add: every load of the row issued before any is used
+    // (no branch between them; col_m is required in this mode, so it stands
+    // in for a missing sm_m)
+    i64 cm[VPT];
+    load_cols_or0(smv, a.sm_m, a.col_m, C, red);
+    load_cols_or0(cm, a.col_m, a.col_m, C, red);
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) {
+      const int c = red.tid() + j * red.nt();
+      h[j] = h_in[off + (c < C ? c : C - 1)];
+    }
+    const i64 row_k = a.row_k[r], row_m = a.row_m[r];
+    const i64 k_res = (a.k_res_in ? a.k_res_in : a.k_res)[r];
+    constexpr int KF = 4;
+    int32_t t[KF][1][VPT];
+    const i64 offs[1] = {off};
+    load_rows_i32_first<KF, 1, VPT>(t, a.P, a.nsplit, a.split_stride, offs, C, red);
+    __builtin_amdgcn_sched_barrier(0);
+    i64 dd[1][VPT];
+    rows_i32_sum<KF, 1, VPT>(dd, t, a.P, a.nsplit, a.split_stride, offs, C, red);
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) {
+      d[j] = dd[0][j];
+      if (red.tid() + j * red.nt() >= C) h[j] = 0;
+    }
+    const i64 dk = requant_common_row(d, cm, row_k, a.col_k, a.tb, red);
+    kr = residual_add_row(h, k_res, d, row_m, dk, red, &lg);
+  } else {
   prefetch_cols(smv, a.sm_m, C, red);
   if (a.mode == 2) {
     // _norm_quant of a given residual row: h is read, not written
@@ -349,6 +444,7 @@ __device__ __forceinline__ void residual_normq_row(const ResNormArgs& a, int r, 
     }
     const i64 dk = requant_common_row(d, cm, row_k, a.col_k, a.tb, red);
     kr = residual_add_row(h, k_res, d, row_m, dk, red, &lg);
+  }
   }
   if (a.mode != 2 && a.h) {
 #pragma unroll
@@ -405,13 +501,29 @@ __device__ __forceinline__ void swiglu_quant_row(const SwigluArgs& a, int r, Red
   // rows hide the extra load). Decode rows load everything up front.
   constexpr bool kLate = VPT > 4;
   i64 gm[VPT], um[VPT], dsm[VPT];
-  prefetch_cols(gm, a.gate_m, I, red);
-  prefetch_cols(um, a.up_m, I, red);
-  if (!kLate) prefetch_cols(dsm, a.ds_m, I, red);
-  const i64 xm = a.xm[r], xk = a.xk[r];
   i64 gu[2][VPT];
   const i64 offs[2] = {(i64)r * 2 * I, (i64)r * 2 * I + I};
-  load_rows_i32_sum<2, VPT>(gu, a.P, a.nsplit, a.split_stride, offs, I, red);
+  i64 xm, xk;
+  if (!kLate) {
+    // decode rows: every load issued before any is used, no branch between
+    // them (the scale vectors are required: the entry point checks them)
+    load_cols_or0(gm, a.gate_m, a.gate_m, I, red);
+    load_cols_or0(um, a.up_m, a.up_m, I, red);
+    load_cols_or0(dsm, a.ds_m, a.ds_m, I, red);
+    xm = a.xm[r];
+    xk = a.xk[r];
+    constexpr int KF = 1;  // decode gate|up products have no K split
+    int32_t t[KF][2][VPT];
+    load_rows_i32_first<KF, 2, VPT>(t, a.P, a.nsplit, a.split_stride, offs, I, red);
+    __builtin_amdgcn_sched_barrier(0);
+    rows_i32_sum<KF, 2, VPT>(gu, t, a.P, a.nsplit, a.split_stride, offs, I, red);
+  } else {
+    prefetch_cols(gm, a.gate_m, I, red);
+    prefetch_cols(um, a.up_m, I, red);
+    xm = a.xm[r];
+    xk = a.xk[r];
+    load_rows_i32_sum<2, VPT>(gu, a.P, a.nsplit, a.split_stride, offs, I, red);
+  }
   i64 gk, uk;
   requant_common_row2(gu[0], gm, a.gate_k, gu[1], um, a.up_k, xk, 14, red, &gk, &uk);
   // requant_i32_common(14) leaves |g|, |u| <= 2^14 (the shift brings the
@@ -476,24 +588,23 @@ __device__ __forceinline__ void merge_rowcol_row(const MergeArgs& a, int r, Red&
   // per-column factor os_m * col_m (col_m null: os_m already holds the
   // product; int64 multiplication wraps modulo 2^64, so the order of the
   // two factors does not change a bit)
-  prefetch_cols(om, a.os_m, C, red);
+  // every load of the first partial issued before any is used, no branch
+  // between them (os_m stands in for a missing col_m)
+  i64 cm[VPT];
+  load_cols_or0(om, a.os_m, a.os_m, C, red);
+  load_cols_or0(cm, a.col_m, a.os_m, C, red);
+#pragma unroll
+  for (int j = 0; j < VPT; ++j) {
+    const int c = red.tid() + j * red.nt();
+    v[j] = a.attn[off + (c < C ? c : C - 1)];  // partial 0
+  }
+  __builtin_amdgcn_sched_barrier(0);
   if (a.col_m) {
-    i64 cm[VPT];
-    prefetch_cols(cm, a.col_m, C, red);
 #pragma unroll
     for (int j = 0; j < VPT; ++j) om[j] = wmul(om[j], cm[j]);
   }
-#pragma unroll
-  for (int j = 0; j < VPT; ++j) v[j] = 0;
-  if (a.nsplit == 1) {  // one load per element (block-uniform)
-#pragma unroll
-    for (int j = 0; j < VPT; ++j) {
-      const int c = red.tid() + j * red.nt();
-      v[j] = a.attn[off + (c < C ? c : C - 1)];
-    }
-  }
   constexpr int KB = VPT > 16 ? 1 : 2;  // partials per batch of loads (registers)
-  for (int k0 = 0; a.nsplit > 1 && k0 < a.nsplit; k0 += KB) {
+  for (int k0 = 1; k0 < a.nsplit; k0 += KB) {
     i64 t[KB][VPT];
 #pragma unroll
     for (int kk = 0; kk < KB; ++kk) {
