@@ -96,6 +96,7 @@ __device__ __forceinline__ void pf_pack(const uint32_t (&p)[4], int& whi, int& w
 }
 
 __global__ __launch_bounds__(256, 2) void k_attn_prefill(PrefillArgs a) {
+  keep_hidden_args();
   __shared__ __attribute__((aligned(1024))) int8_t ring[PF_RING];
   // PF_CSUM + 8 per 64 slots (tile masks) + 4 per page (page ids)
   extern __shared__ __attribute__((aligned(16))) int8_t dyn[];
@@ -889,6 +890,7 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, int S, int kvh,
 
 template <int G, bool SCR>
 __global__ __launch_bounds__(256) void k_attn_decode(DecodeArgs a) {
+  keep_hidden_args();
   extern __shared__ __attribute__((aligned(16))) int32_t sh_scores[];
   __shared__ int32_t pg_lds[DEC_MAX_PAGES];
   const int kvh = blockIdx.x, b = blockIdx.y;
@@ -913,6 +915,7 @@ __global__ __launch_bounds__(256) void k_attn_decode(DecodeArgs a) {
 constexpr int QAD_WAVES = 8;
 template <int G, bool NS1, bool SCR>
 __global__ __launch_bounds__(QAD_WAVES * 64) void k_qkv_attn_decode(DecodeArgs a, QKVArgs qa) {
+  keep_hidden_args();
   constexpr int NW = QAD_WAVES, NT = NW * 64, IT = 8 / NW;
   static_assert(G + 2 <= NW, "one wave per head slot");
   extern __shared__ __attribute__((aligned(16))) int32_t sh_scores[];
@@ -1072,6 +1075,7 @@ struct SplitArgs {
 
 template <int G>
 __global__ __launch_bounds__(256) void k_attn_split_scores(SplitArgs sa) {
+  keep_hidden_args();
   const DecodeArgs& a = sa.d;
   __shared__ i64 red_buf[32];
   __shared__ int32_t pg_lds[SPLIT_MAX_PAGES];
@@ -1149,6 +1153,7 @@ __global__ __launch_bounds__(256) void k_attn_split_scores(SplitArgs sa) {
 
 template <int G>
 __global__ __launch_bounds__(256) void k_attn_split_pv(SplitArgs sa) {
+  keep_hidden_args();
   const DecodeArgs& a = sa.d;
   extern __shared__ __attribute__((aligned(16))) int32_t p_lds[];  // [G][chunk] packed p
   __shared__ i64 red_buf[32];

@@ -95,6 +95,19 @@ __device__ __forceinline__ i64 ld_global(const int64_t* p) {
   return *(const __attribute__((address_space(1))) int64_t*)p;
 }
 
+// Every kernel starts with this: a reference to its hidden (implicit) launch
+// arguments on a path no launch takes (a workgroup id of 2^31 - 2), so that
+// its argument segment carries the hidden block. rocprofv3's counter
+// collection (ROCm 7.2) reads that block and crashes the profiled process
+// (a host SIGSEGV at the launch) on kernels whose segment ends without it.
+// Costs one scalar compare; the argument segment grows by 256 bytes.
+__device__ __forceinline__ void keep_hidden_args() {
+  if (__builtin_amdgcn_workgroup_id_x() == 0x7ffffffeu) {
+    const int h = *(const int*)__builtin_amdgcn_implicitarg_ptr();
+    asm volatile("" ::"s"(h));
+  }
+}
+
 __device__ __forceinline__ i64 shfl_xor64(i64 v, int mask) {
   int lo = (int)(v & 0xffffffff);
   int hi = (int)((u64)v >> 32);

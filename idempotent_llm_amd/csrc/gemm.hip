@@ -45,6 +45,7 @@ __global__ __launch_bounds__(256) void k_gemm_nt(const int8_t* __restrict__ A,
                                                  const int8_t* __restrict__ B,
                                                  int32_t* __restrict__ C, int M, int N, int K,
                                                  i64 sA, i64 sB, i64 sC, int tiles_n) {
+  keep_hidden_args();
   __shared__ __attribute__((aligned(16))) int8_t As[2][TBM][TBK + TPAD];
   __shared__ __attribute__((aligned(16))) int8_t Bs[2][TBN][TBK + TPAD];
   const int bz = blockIdx.z;
@@ -166,6 +167,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, MINB) void k_gemm_nt2(const int8_t*
                                                         int32_t* __restrict__ C, int M, int N,
                                                         int K, i64 sA, i64 sB, i64 sC,
                                                         int tiles_m, int tiles_n) {
+  keep_hidden_args();
   constexpr int ROWS = BM + BN;       // 128-byte rows per slice: A rows, then B rows
   constexpr int NW = WGM * WGN;       // waves, WGM x WGN over the tile
   constexpr int NI = ROWS / 8;        // load instructions per slice (8 rows each)
@@ -276,6 +278,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, MINB) void k_gemm_nt2(const int8_t*
 // 256-thread block per (column group, K range).
 template <int MB, int KW, int NB>
 __global__ __launch_bounds__(256) void k_gemv_nt(GemvArgs g, Prefetch pf) {
+  keep_hidden_args();
   __shared__ GemvLds<MB, KW> lds;
   const PrefetchHold ph =
       prefetch_issue(pf, blockIdx.y == 0 ? (i64)blockIdx.x * 256 + threadIdx.x : (i64)-1);
@@ -296,6 +299,7 @@ __global__ __launch_bounds__(256) void k_gemv_stream(const int8_t* __restrict__ 
                                                      const int8_t* __restrict__ B,
                                                      int32_t* __restrict__ C, int M, int N,
                                                      int K, Prefetch pf) {
+  keep_hidden_args();
   extern __shared__ __attribute__((aligned(16))) int8_t sa[];  // [16][K]
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const PrefetchHold ph = prefetch_issue(pf, (i64)blockIdx.x * 256 + tid);
@@ -335,6 +339,7 @@ __global__ __launch_bounds__(256) void k_gemv_stream(const int8_t* __restrict__ 
 
 __global__ void k_transpose_i8(const int8_t* __restrict__ src, int8_t* __restrict__ dst, int R,
                                int Cc, i64 sS, i64 sD) {
+  keep_hidden_args();
   __shared__ int8_t tile[64][65];
   src += blockIdx.z * sS;
   dst += blockIdx.z * sD;
@@ -380,6 +385,7 @@ __device__ __forceinline__ Best block_best(Best x, i64* sv, i64* si) {
 __global__ __launch_bounds__(256) void k_argmax_partial(const int32_t* __restrict__ logits,
                                                         const int64_t* __restrict__ head_m, int V,
                                                         int chunk, int64_t* pv, int64_t* pi) {
+  keep_hidden_args();
   __shared__ i64 sv[4], si[4];
   const int r = blockIdx.y, ch = blockIdx.x, nch = gridDim.x;
   const int beg = ch * chunk, end = min(V, beg + chunk);
@@ -397,6 +403,7 @@ __global__ __launch_bounds__(256) void k_argmax_partial(const int32_t* __restric
 
 __global__ __launch_bounds__(256) void k_argmax_final(const int64_t* pv, const int64_t* pi,
                                                       int nch, int64_t* out) {
+  keep_hidden_args();
   __shared__ i64 sv[4], si[4];
   const int r = blockIdx.x;
   Best b{INT64_MIN, INT64_MAX};
@@ -417,6 +424,7 @@ __device__ __forceinline__ u64 mix64(u64 z) {
 
 __global__ __launch_bounds__(1024) void k_logits_digest(const int32_t* __restrict__ rows, int V,
                                                         int64_t* out) {
+  keep_hidden_args();
   __shared__ i64 red_buf[32];
   BlockRed red{red_buf, 0, 1024};
   const int32_t* row = rows + (i64)blockIdx.x * V;

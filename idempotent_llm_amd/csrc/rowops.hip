@@ -468,6 +468,7 @@ __device__ __forceinline__ void residual_normq_row(const ResNormArgs& a, int r, 
 
 template <int VPT, int NT = RT_WIDE>
 __global__ __launch_bounds__(NT) void k_residual_normq(ResNormArgs a) {
+  keep_hidden_args();
   __shared__ i64 red_buf[32];
   BlockRed red{red_buf, 0, a.nt};
   residual_normq_row<VPT>(a, blockIdx.x, red);
@@ -558,6 +559,7 @@ __device__ __forceinline__ void swiglu_quant_row(const SwigluArgs& a, int r, Red
 template <int VPT, int NT = RT_WIDE>
 __global__ __launch_bounds__(NT, (NT == 256 && VPT >= 8 && VPT <= 12) ? 3 : 1) void k_swiglu_quant(
     SwigluArgs a) {
+  keep_hidden_args();
   __shared__ i64 red_buf[32];
   BlockRed red{red_buf, 0, a.nt};
   swiglu_quant_row<VPT>(a, blockIdx.x, red);
@@ -663,12 +665,14 @@ __device__ __forceinline__ void merge_rowcol_row(const MergeArgs& a, int r, Red&
 
 template <int VPT, int NT = RT_WIDE>
 __global__ __launch_bounds__(NT) void k_merge_rowcol(MergeArgs a) {
+  keep_hidden_args();
   __shared__ i64 red_buf[32];
   BlockRed red{red_buf, 0, a.nt};
   merge_rowcol_row<VPT>(a, blockIdx.x, red);
 }
 
 __global__ __launch_bounds__(RT) void k_qkv_epilogue(QKVArgs a) {
+  keep_hidden_args();
   const int slotw = blockIdx.y * 4 + (threadIdx.x >> 6);
   if (slotw >= a.n_q + 2 * a.n_kv) return;
   const int r = blockIdx.x;  // token row = b * T + t
@@ -680,6 +684,7 @@ __global__ __launch_bounds__(RT) void k_qkv_epilogue(QKVArgs a) {
 // Many token rows (prefill): one wave per (head slot, 4 rows), head-major so
 // a block's waves share a head's scale vectors.
 __global__ __launch_bounds__(RT) void k_qkv_epilogue_rows(QKVArgs a, int R, int ngroups) {
+  keep_hidden_args();
   const int heads = a.n_q + 2 * a.n_kv;
   const int wg = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (wg >= heads * ngroups) return;  // whole waves only
@@ -695,6 +700,7 @@ __global__ __launch_bounds__(256) void k_decode_prologue(uint8_t* valid, i64 str
                                                          int64_t* len_idx, int64_t* nslots,
                                                          int64_t* pos, const int64_t* pos0,
                                                          i64 step) {
+  keep_hidden_args();
   for (int b = threadIdx.x; b < B; b += blockDim.x) {
     valid[(i64)b * stride + slot] = 1;
     pos[b] = pos0[b] + step;
@@ -708,6 +714,7 @@ __global__ __launch_bounds__(256) void k_decode_prologue(uint8_t* valid, i64 str
 // kq_channel of every channel: est[i] = {den, up, bits of D.r, bits of D.k}
 __global__ __launch_bounds__(256) void k_kq_est(const int64_t* kq_m, const int64_t* kq_k, i64 n,
                                                 i64 rowk, int64_t* est) {
+  keep_hidden_args();
   const i64 i = blockIdx.x * (i64)blockDim.x + threadIdx.x;
   if (i >= n) return;
   const KqChan q = kq_channel(kq_m[i], kq_k[i], rowk);
@@ -734,6 +741,7 @@ template <int VPT>
 __global__ __launch_bounds__(RT) void k_op_quant(const int64_t* x, const int64_t* m,
                                                  const int64_t* k, int C, int8_t* x8,
                                                  int64_t* mo, int64_t* ko) {
+  keep_hidden_args();
   __shared__ i64 red_buf[32];
   BlockRed red{red_buf, 0, RT};
   const int r = blockIdx.x;
@@ -747,6 +755,7 @@ __global__ __launch_bounds__(RT) void k_op_requant_common(const int64_t* P, cons
                                                           const int64_t* col_m, int G, i64 col_k,
                                                           int tb, int C, int32_t* y,
                                                           int64_t* ko) {
+  keep_hidden_args();
   __shared__ i64 red_buf[32];
   BlockRed red{red_buf, 0, RT};
   const int r = blockIdx.x;
@@ -768,6 +777,7 @@ __global__ __launch_bounds__(RT) void k_op_rowcol(const int64_t* P, const int64_
                                                   const int64_t* row_k, const int64_t* col_m,
                                                   i64 col_k, int C, int8_t* y8, int64_t* mo,
                                                   int64_t* ko) {
+  keep_hidden_args();
   __shared__ i64 red_buf[32];
   BlockRed red{red_buf, 0, RT};
   const int r = blockIdx.x;
@@ -802,6 +812,7 @@ __global__ __launch_bounds__(RT) void k_op_residual(int mode, const int64_t* h_i
                                                     const int64_t* k_res, const int64_t* d,
                                                     const int64_t* dm, const int64_t* dk, int C,
                                                     int32_t* h_out, int64_t* k_out) {
+  keep_hidden_args();
   __shared__ i64 red_buf[32];
   BlockRed red{red_buf, 0, RT};
   const int r = blockIdx.x;
@@ -826,6 +837,7 @@ __global__ __launch_bounds__(RT) void k_op_residual(int mode, const int64_t* h_i
 template <int VPT>
 __global__ __launch_bounds__(RT) void k_op_rmsnorm(const int64_t* x, const int64_t* gamma_m,
                                                    int C, int32_t* y32, int64_t* y64) {
+  keep_hidden_args();
   __shared__ i64 red_buf[32];
   BlockRed red{red_buf, 0, RT};
   const int r = blockIdx.x;
@@ -847,6 +859,7 @@ __global__ __launch_bounds__(RT) void k_op_softmax(const int64_t* x, const int64
                                                    const int64_t* k, const uint8_t* valid,
                                                    int has_clip, i64 clip_c, int p_out_bits,
                                                    int C, int32_t* probs) {
+  keep_hidden_args();
   // ops/di_softmax.py:33-61
   __shared__ i64 red_buf[32];
   BlockRed red{red_buf, 0, RT};
@@ -896,6 +909,7 @@ __global__ __launch_bounds__(RT) void k_op_softmax(const int64_t* x, const int64
 
 __global__ void k_op_di_exp(const int64_t* x, const int64_t* m, const int64_t* k, int C,
                             i64 n, int64_t* res, int64_t* tpos_out) {
+  keep_hidden_args();
   // ops/di_exp.py:21-37, row constants recomputed per element
   for (i64 i = blockIdx.x * (i64)blockDim.x + threadIdx.x; i < n;
        i += (i64)gridDim.x * blockDim.x) {
@@ -909,6 +923,7 @@ __global__ void k_op_di_exp(const int64_t* x, const int64_t* m, const int64_t* k
 __global__ void k_op_swiglu(const int64_t* gate, const int64_t* gm, const int64_t* gk,
                             const int64_t* up, const int64_t* um, const int64_t* uk, int C,
                             i64 n, int64_t* y, int64_t* ym, int64_t* yk) {
+  keep_hidden_args();
   for (i64 i = blockIdx.x * (i64)blockDim.x + threadIdx.x; i < n;
        i += (i64)gridDim.x * blockDim.x) {
     const i64 r = i / C;
@@ -923,6 +938,7 @@ __global__ void k_op_swiglu(const int64_t* gate, const int64_t* gm, const int64_
 __global__ void k_op_rope(const int64_t* x, const int64_t* pos, const int16_t* cos_t,
                           const int16_t* sin_t, i64 max_pos, i64 rows, int64_t* y,
                           int32_t* err) {
+  keep_hidden_args();
   // ops/rope.py:38-55 on rows of 128 channels
   const i64 r = blockIdx.x * 4 + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
@@ -939,6 +955,7 @@ __global__ void k_op_rope(const int64_t* x, const int64_t* pos, const int16_t* c
 __global__ void k_op_static(const int64_t* P, const int64_t* row_m, const int64_t* row_k,
                             const int64_t* col_m, const int64_t* col_k, const int64_t* s_m,
                             const int64_t* s_k, i64 n, int8_t* y8) {
+  keep_hidden_args();
   // dyadic.py:142-163 with every operand materialised per element
   for (i64 i = blockIdx.x * (i64)blockDim.x + threadIdx.x; i < n;
        i += (i64)gridDim.x * blockDim.x) {
@@ -961,6 +978,7 @@ __global__ __launch_bounds__(256) void k_static_cols(const int32_t* __restrict__
                                                      const int64_t* row_m, const int64_t* row_k,
                                                      const int64_t* __restrict__ col_m, i64 col_k,
                                                      i64 s_m, i64 s_k, int8_t* __restrict__ y8) {
+  keep_hidden_args();
   const int cq = (C + 3) / 4;
   const i64 t = (i64)blockIdx.x * blockDim.x + threadIdx.x;
   if (t >= (i64)R * cq) return;
@@ -990,6 +1008,7 @@ __global__ __launch_bounds__(256) void k_static_cols(const int32_t* __restrict__
 // (6, the wave-parallel isqrt, runs in k_op_isqrt_wave)
 __global__ void k_op_scalar(int op, const int64_t* a, const int64_t* b, const int64_t* c, i64 n,
                             int64_t* o1, int64_t* o2) {
+  keep_hidden_args();
   for (i64 i = blockIdx.x * (i64)blockDim.x + threadIdx.x; i < n;
        i += (i64)gridDim.x * blockDim.x) {
     i64 x, y;
@@ -1025,6 +1044,7 @@ __global__ void k_op_scalar(int op, const int64_t* a, const int64_t* b, const in
 // (the search needs the whole wave; indices are clamped so every lane stays
 // active).
 __global__ void k_op_isqrt_wave(const int64_t* a, i64 n, int64_t* o) {
+  keep_hidden_args();
   const i64 lane = threadIdx.x & 63;
   const i64 wave0 = (blockIdx.x * (i64)blockDim.x + threadIdx.x) - lane;
   const i64 stride = (i64)gridDim.x * blockDim.x;
@@ -1113,6 +1133,7 @@ struct ProLds {
 template <int PRO, int CMAX, int NI, int NB, bool ONE>
 __global__ __launch_bounds__(PRO_THREADS) void k_gemv_pro(ProGemv g, ResNormArgs ra, MergeArgs ma,
                                                          Prefetch pf) {
+  keep_hidden_args();
   __shared__ __attribute__((aligned(16))) ProLds<CMAX, NB> L;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int bx = blockIdx.x, by = blockIdx.y;
