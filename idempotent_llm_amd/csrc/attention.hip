@@ -483,7 +483,7 @@ __device__ __forceinline__ int32_t row16_max(int32_t v) {
 
 // Attention of one (batch row b, kv head kvh) over its G query heads, whose
 // int8 rows sit at qsrc[hh * 128] and DI-Exp constants at tsrc[hh] (global
-// memory or LDS). 256 threads = 4 waves.
+// memory or LDS). NW waves (decode_body's template argument, 4 or 8).
 //
 // Scores and P.V run on v_mfma_i32_16x16x64_i8 with the G query heads as the
 // 16 MFMA rows (rows >= G zero):
@@ -496,7 +496,7 @@ __device__ __forceinline__ int32_t row16_max(int32_t v) {
 //     of the hi product holds ones, so C_hi[G][d] = colsum v over exactly the
 //     slots of the B fragments; B-fragment lane l = channel l % 16, slots
 //     16 (l / 16) .. + 15 of V^T (slot-contiguous). Wave w owns channels
-//     32w .. 32w + 31 (two 16-channel blocks).
+//     (128 / NW) w .. + 128 / NW - 1 (8 / NW 16-channel blocks).
 // Slots past S read zero V fragments (16-slot chunks starting at or past S),
 // so their A values do not matter; the p of slots S .. ceil16(S) are 0.
 // |accumulators| <= 128 * 128 * S < 2^31 for S <= 131071.
