@@ -34,6 +34,7 @@ from __future__ import annotations
 
 import argparse
 import hashlib
+import re
 import json
 import os
 import sys
@@ -208,11 +209,21 @@ def _job_bytes(jobs):
     return sum(w.numel() + x.numel() + 4 * x.shape[0] * w.shape[0] for x, w, _, _ in jobs)
 
 
-def _csrc_sha(*names) -> str:
+def _code_text(src: str) -> str:
+    """C++ source without comments and with whitespace collapsed: the part
+    that decides the compiled kernels (string literals in these sources hold
+    no comment markers)."""
+    src = re.sub(r"/\*.*?\*/", " ", src, flags=re.S)
+    src = re.sub(r"//[^\n]*", " ", src)
+    return " ".join(src.split())
+
+
+def _csrc_sha(*names, root: str = ROOT) -> str:
+    """Digest of the kernel sources' code (comments and layout excluded)."""
     h = hashlib.sha256()
     for n in names:
-        with open(os.path.join(ROOT, "idempotent_llm_amd", "csrc", n), "rb") as f:
-            h.update(f.read())
+        with open(os.path.join(root, "idempotent_llm_amd", "csrc", n), encoding="utf-8") as f:
+            h.update(_code_text(f.read()).encode())
     return h.hexdigest()[:16]
 
 
