@@ -363,6 +363,7 @@ struct ResNormArgs {
   int64_t* xm;    // null: (m, k) of x8 not stored
   int64_t* xk;
   int32_t* err;  // optional device error word (DI_ERR_TOKEN)
+  L2Warm warm;   // the next skinny GEMM's weights (extra blocks after the rows)
 };
 
 template <int VPT, class Red>
@@ -466,12 +467,16 @@ __device__ __forceinline__ void residual_normq_row(const ResNormArgs& a, int r, 
             a.xm ? a.xm + r : nullptr, a.xk ? a.xk + r : nullptr);
 }
 
-template <int VPT, int NT = RT_WIDE>
+template <int VPT, int NT = RT_WIDE, bool WARM = false>
 __global__ __launch_bounds__(NT) void k_residual_normq(ResNormArgs a) {
   keep_hidden_args();
   __shared__ i64 red_buf[32];
+  if (WARM && (int)blockIdx.x < L2WARM_BLOCKS) {  // no kernel argument needed to decide
+    l2_warm(a.warm, blockIdx.x, a.nt, red_buf);
+    return;
+  }
   BlockRed red{red_buf, 0, a.nt};
-  residual_normq_row<VPT>(a, blockIdx.x, red);
+  residual_normq_row<VPT>(a, (int)blockIdx.x - (WARM ? L2WARM_BLOCKS : 0), red);
 }
 
 struct SwigluArgs {
@@ -491,6 +496,7 @@ struct SwigluArgs {
   int8_t* y8;
   int64_t* ym;
   int64_t* yk;
+  L2Warm warm;  // the next skinny GEMM's weights (extra blocks after the rows)
 };
 
 template <int VPT, class Red>
@@ -556,13 +562,17 @@ __device__ __forceinline__ void swiglu_quant_row(const SwigluArgs& a, int r, Red
 // per CU (168 VGPRs; 12 columns spill a few registers) beat two unspilled
 // blocks by ~3 % on a 2048-token prefill (measured; four blocks spill more and
 // lose).
-template <int VPT, int NT = RT_WIDE>
+template <int VPT, int NT = RT_WIDE, bool WARM = false>
 __global__ __launch_bounds__(NT, (NT == 256 && VPT >= 8 && VPT <= 12) ? 3 : 1) void k_swiglu_quant(
     SwigluArgs a) {
   keep_hidden_args();
   __shared__ i64 red_buf[32];
+  if (WARM && (int)blockIdx.x < L2WARM_BLOCKS) {  // no kernel argument needed to decide
+    l2_warm(a.warm, blockIdx.x, a.nt, red_buf);
+    return;
+  }
   BlockRed red{red_buf, 0, a.nt};
-  swiglu_quant_row<VPT>(a, blockIdx.x, red);
+  swiglu_quant_row<VPT>(a, (int)blockIdx.x - (WARM ? L2WARM_BLOCKS : 0), red);
 }
 
 struct MergeArgs {
@@ -579,6 +589,7 @@ struct MergeArgs {
   i64 a8_stride;  // row stride of a8 (0: C)
   int64_t* am;    // null: (m, k) of a8 not stored
   int64_t* ak;
+  L2Warm warm;    // the next skinny GEMM's weights (extra blocks after the rows)
 };
 
 template <int VPT, class Red>
@@ -663,12 +674,16 @@ __device__ __forceinline__ void merge_rowcol_row(const MergeArgs& a, int r, Red&
   }
 }
 
-template <int VPT, int NT = RT_WIDE>
+template <int VPT, int NT = RT_WIDE, bool WARM = false>
 __global__ __launch_bounds__(NT) void k_merge_rowcol(MergeArgs a) {
   keep_hidden_args();
   __shared__ i64 red_buf[32];
+  if (WARM && (int)blockIdx.x < L2WARM_BLOCKS) {  // no kernel argument needed to decide
+    l2_warm(a.warm, blockIdx.x, a.nt, red_buf);
+    return;
+  }
   BlockRed red{red_buf, 0, a.nt};
-  merge_rowcol_row<VPT>(a, blockIdx.x, red);
+  merge_rowcol_row<VPT>(a, (int)blockIdx.x - (WARM ? L2WARM_BLOCKS : 0), red);
 }
 
 __global__ __launch_bounds__(RT) void k_qkv_epilogue(QKVArgs a) {
@@ -1296,9 +1311,34 @@ void launch_pro(const ProGemv& g, int ni, int ksplit, const ResNormArgs& ra, con
     }                                                                                           \
   } while (0)
 
+// A decode row launch with the next GEMM's warming blocks in front of the
+// rows (block ids 0 .. L2WARM_BLOCKS - 1: the kernel tells them apart by the
+// block id alone, so the rows' argument loads are not held up by a test on
+// an argument) when ARGS.warm asks for them and the shape takes four columns
+// per thread (every model shape); else the plain row launch.
+#define DI_WARM_OR_ROWS(R, C, KERNEL, STREAM, ARGS)                                          \
+  do {                                                                                       \
+    int thr_, vpt_;                                                                          \
+    if ((ARGS).warm.nwarm > 0 && (R) <= 64 && wide_shape((C), &thr_, &vpt_) && vpt_ == 4) { \
+      (ARGS).nt = thr_;                                                                      \
+      hipLaunchKernelGGL((KERNEL<4, RT_WIDE, true>), dim3(L2WARM_BLOCKS + (R)), dim3(thr_), \
+                         0, STREAM, ARGS);                                                   \
+    } else {                                                                                 \
+      DI_ROWS_DISPATCH(R, C, KERNEL, dim3(R), STREAM, ARGS);                                 \
+    }                                                                                        \
+  } while (0)
+
 extern "C" {
 
 // ---------------------------------------------------------------- model path
+
+// Warming blocks for the skinny GEMM that follows a decode row launch of R
+// rows (none for prefill-sized launches or without a next weight matrix).
+static L2Warm warm_for(int R, const int8_t* next_w, int next_n, int next_k, int next_ksplit) {
+  if (R > 64) return L2Warm{};
+  return make_l2warm(next_w, next_n, next_k, next_ksplit, 0);
+}
+
 
 int detllm_embed_normq(const int64_t* ids, int R, int C, int64_t vocab, const int8_t* e8,
                        const int64_t* em, const int64_t* ek, int32_t* h, int64_t* k_res,
@@ -1318,14 +1358,17 @@ int detllm_embed_normq(const int64_t* ids, int R, int C, int64_t vocab, const in
 int detllm_residual_normq(const int32_t* P, int nsplit, int64_t split_stride, int R, int C,
                           const int64_t* row_m, const int64_t* row_k, const int64_t* col_m,
                           int64_t col_k, int tb, int32_t* h, int64_t* k_res, const int64_t* sm_m,
-                          int64_t sm_k, int8_t* x8, int64_t* xm, int64_t* xk, hipStream_t s) {
+                          int64_t sm_k, int8_t* x8, int64_t* xm, int64_t* xk,
+                          const int8_t* next_w, int next_n, int next_k, int next_ksplit,
+                          hipStream_t s) {
   if (R <= 0) return DI_OK;
   if (C <= 0 || nsplit < 1 || !P || !row_m || !row_k || !col_m || !h || !k_res) return DI_EINVAL;
   ResNormArgs a{};
   a.C = C; a.mode = 1; a.P = P; a.nsplit = nsplit; a.split_stride = split_stride;
   a.row_m = row_m; a.row_k = row_k; a.col_m = col_m; a.col_k = col_k; a.tb = tb;
   a.h = h; a.k_res = k_res; a.sm_m = sm_m; a.sm_k = sm_k; a.x8 = x8; a.xm = xm; a.xk = xk;
-  DI_ROWS_DISPATCH(R, C, k_residual_normq, dim3(R), s, a);
+  a.warm = warm_for(R, next_w, next_n, next_k, next_ksplit);
+  DI_WARM_OR_ROWS(R, C, k_residual_normq, s, a);
   DI_LAUNCH_CHECK();
   return DI_OK;
 }
@@ -1421,7 +1464,9 @@ int detllm_norm_quant(const int32_t* h, int R, int C, const int64_t* sm_m, int64
 int detllm_swiglu_quant(const int32_t* P, int nsplit, int64_t split_stride, int R, int I,
                         const int64_t* xm, const int64_t* xk, const int64_t* gate_m,
                         int64_t gate_k, const int64_t* up_m, int64_t up_k, const int64_t* ds_m,
-                        int64_t ds_k, int8_t* y8, int64_t* ym, int64_t* yk, hipStream_t s) {
+                        int64_t ds_k, int8_t* y8, int64_t* ym, int64_t* yk,
+                        const int8_t* next_w, int next_n, int next_k, int next_ksplit,
+                        hipStream_t s) {
   if (R <= 0) return DI_OK;
   if (I <= 0 || nsplit < 1 || !P || !xm || !xk || !gate_m || !up_m || !ds_m || !y8 || !ym || !yk)
     return DI_EINVAL;
@@ -1429,20 +1474,23 @@ int detllm_swiglu_quant(const int32_t* P, int nsplit, int64_t split_stride, int 
   a.I = I; a.P = P; a.nsplit = nsplit; a.split_stride = split_stride; a.xm = xm; a.xk = xk;
   a.gate_m = gate_m; a.gate_k = gate_k; a.up_m = up_m; a.up_k = up_k; a.ds_m = ds_m;
   a.ds_k = ds_k; a.y8 = y8; a.ym = ym; a.yk = yk;
-  DI_ROWS_DISPATCH(R, I, k_swiglu_quant, dim3(R), s, a);
+  a.warm = warm_for(R, next_w, next_n, next_k, next_ksplit);
+  DI_WARM_OR_ROWS(R, I, k_swiglu_quant, s, a);
   DI_LAUNCH_CHECK();
   return DI_OK;
 }
 
 int detllm_merge_rowcol(const int64_t* attn, int nsplit, int64_t split_stride, int R, int C,
                         const int64_t* os_m, int64_t os_k, const int64_t* col_m, int64_t col_k,
-                        int8_t* a8, int64_t* am, int64_t* ak, hipStream_t s) {
+                        int8_t* a8, int64_t* am, int64_t* ak, const int8_t* next_w,
+                        int next_n, int next_k, int next_ksplit, hipStream_t s) {
   if (R <= 0) return DI_OK;
   if (C <= 0 || nsplit < 1 || !attn || !os_m || !col_m || !a8 || !am || !ak) return DI_EINVAL;
   MergeArgs a{};
   a.C = C; a.attn = attn; a.nsplit = nsplit; a.split_stride = split_stride; a.os_m = os_m;
   a.os_k = os_k; a.col_m = col_m; a.col_k = col_k; a.a8 = a8; a.am = am; a.ak = ak;
-  DI_ROWS_DISPATCH(R, C, k_merge_rowcol, dim3(R), s, a);
+  a.warm = warm_for(R, next_w, next_n, next_k, next_ksplit);
+  DI_WARM_OR_ROWS(R, C, k_merge_rowcol, s, a);
   DI_LAUNCH_CHECK();
   return DI_OK;
 }

@@ -224,12 +224,22 @@ class IntQwen3:
 
     # -- GEMM dispatch ---------------------------------------------------------
     def _ksplit(self, N: int, K: int, M: int = 1) -> int:
-        key = (N, K)
+        key = (N, K, M > 1)  # the plan differs between one row and several
         ks = self._plans.get(key)
         if ks is None:
             ks = gemv_plan(M, N, K)
             self._plans[key] = ks
         return ks
+
+    def _next_gemm(self, w, R: int):
+        """Trailing arguments of a decode row kernel that name the skinny GEMM
+        launched right after it (x . w^T over R rows, _gemm's K split): the
+        row launch pulls w into the L2 caches meanwhile (a hint; results do
+        not depend on it)."""
+        if w is None or R > 64:
+            return (None, 0, 0, 0)
+        N, K = w.shape
+        return (w, N, K, self._ksplit(N, K, R))
 
     def _gemm(self, x: torch.Tensor, w: torch.Tensor, prefetch=(), split: bool = True):
         """x . w^T as int32 partials [ks, R, N] (ks = 1 unless split and the
@@ -459,12 +469,12 @@ class IntQwen3:
                  xm, xk, L.pf_mlp, L.pf_mlp.numel() * 8, None, 0)
             cur = 1 - cur
             call("detllm_swiglu_quant", Pg, nsg, stg, R, I_, xm, xk, L.gate_m, L.gate_k, L.up_m,
-                 L.up_k, L.ds_m, L.ds_k, y8, ym, yk)
+                 L.up_k, L.ds_m, L.ds_k, y8, ym, yk, *self._next_gemm(L.wd, R))
             Pd, nsd, std = self._gemm(y8, L.wd, (L.down_m,) if nxt is None else
                                       (L.down_m, nxt.as_m))
             if nxt is None:
                 call("detllm_residual_normq", Pd, nsd, std, R, H, ym, yk, L.down_m, L.down_k, 20,
-                     hb[cur], kb[cur], None, 0, x8, xm, xk)
+                     hb[cur], kb[cur], None, 0, x8, xm, xk, None, 0, 0, 0)
                 break
             N = nxt.wqkv.shape[0]
             P, ns, st = self._partials(R, N, H)
@@ -562,20 +572,20 @@ class IntQwen3:
         am = torch.empty(R, dtype=I64, device=dev)
         ak = torch.empty(R, dtype=I64, device=dev)
         call("detllm_merge_rowcol", *attn, R, nq * hd, L.os_m, L.os_k, L.attn_out_col_m,
-             L.attn_out_col_k, a8, am, ak)
+             L.attn_out_col_k, a8, am, ak, *self._next_gemm(L.wo, R))
         P, ns, st = self._gemm(a8, L.wo, (L.pf_o,))
         call("detllm_residual_normq", P, ns, st, R, H, am, ak, L.o_m, L.o_k, 20, h, k_res,
-             L.ms_m, L.ms_k, x8, xm, xk)
+             L.ms_m, L.ms_k, x8, xm, xk, *self._next_gemm(L.wgu, R))
         P, ns, st = self._gemm(x8, L.wgu, (L.pf_mlp,))
         y8 = torch.empty(R, I_, dtype=torch.int8, device=dev)
         ym = torch.empty(R, dtype=I64, device=dev)
         yk = torch.empty(R, dtype=I64, device=dev)
         call("detllm_swiglu_quant", P, ns, st, R, I_, xm, xk, L.gate_m, L.gate_k, L.up_m,
-             L.up_k, L.ds_m, L.ds_k, y8, ym, yk)
+             L.up_k, L.ds_m, L.ds_k, y8, ym, yk, *self._next_gemm(L.wd, R))
         P, ns, st = self._gemm(y8, L.wd, (L.down_m,) if nxt is None else (L.down_m, nxt.as_m))
         sm_m, sm_k = (nxt.as_m, nxt.as_k) if nxt is not None else (None, 0)
         call("detllm_residual_normq", P, ns, st, R, H, ym, yk, L.down_m, L.down_k, 20, h, k_res,
-             sm_m, sm_k, x8, xm, xk)
+             sm_m, sm_k, x8, xm, xk, *self._next_gemm(None if nxt is None else nxt.wqkv, R))
 
     # -- decoding (model.py:482-531) ------------------------------------------------
     def greedy_pick(self, logits_row: torch.Tensor) -> torch.Tensor:

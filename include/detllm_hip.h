@@ -115,6 +115,14 @@ int detllm_embed_normq(const int64_t* ids, int R, int C, int64_t vocab, const in
                        const int64_t* sm_m, int64_t sm_k, int8_t* x8, int64_t* xm, int64_t* xk,
                        int32_t* err, hipStream_t s);
 
+/* The next skinny GEMM (next_w, next_n, next_k, next_ksplit), the trailing
+ * arguments of the three row kernels below: the product detllm_igemv_nt
+ * computes right after this launch, W [next_n][next_k] int8 with that K
+ * split. At decode sizes (R <= 64) the launch adds blocks that pull W's
+ * slices into the L2 cache of the XCD whose GEMM blocks will read them. A
+ * performance hint with no counterpart in the reference: results do not
+ * depend on it; next_w null (and zeros) adds nothing. */
+
 /* requant_i32_common(P, row_m, row_k, col_m, col_k, tb) + residual_add +
  * _norm_quant(sm_m, sm_k) — model.py:410-415 / :424-427, :303, :284
  * (dyadic.py:108-120, :193-206; ops/di_rmsnorm.py:33-52; dyadic.py:93-105).
@@ -123,7 +131,8 @@ int detllm_residual_normq(const int32_t* P, int nsplit, int64_t split_stride, in
                           const int64_t* row_m, const int64_t* row_k, const int64_t* col_m,
                           int64_t col_k, int tb, int32_t* h, int64_t* k_res,
                           const int64_t* sm_m, int64_t sm_k, int8_t* x8, int64_t* xm,
-                          int64_t* xk, hipStream_t s);
+                          int64_t* xk, const int8_t* next_w, int next_n, int next_k,
+                          int next_ksplit, hipStream_t s);
 
 /* Decode skinny GEMMs with the row kernel that makes their int8 operand
  * fused in (R <= 8 rows). Results equal the two launches they replace: the
@@ -169,14 +178,17 @@ int detllm_norm_quant(const int32_t* h, int R, int C, const int64_t* sm_m, int64
 int detllm_swiglu_quant(const int32_t* P, int nsplit, int64_t split_stride, int R, int I,
                         const int64_t* xm, const int64_t* xk, const int64_t* gate_m,
                         int64_t gate_k, const int64_t* up_m, int64_t up_k, const int64_t* ds_m,
-                        int64_t ds_k, int8_t* y8, int64_t* ym, int64_t* yk, hipStream_t s);
+                        int64_t ds_k, int8_t* y8, int64_t* ym, int64_t* yk,
+                        const int8_t* next_w, int next_n, int next_k, int next_ksplit,
+                        hipStream_t s);
 
 /* Attention-output merge: requant_i8_rowcol(attn * os_m, 1, os_k, col_m,
  * col_k) — model.py:404-409 (dyadic.py:123-139). attn: [nsplit][R][C] int64
  * partial context sums. */
 int detllm_merge_rowcol(const int64_t* attn, int nsplit, int64_t split_stride, int R, int C,
                         const int64_t* os_m, int64_t os_k, const int64_t* col_m, int64_t col_k,
-                        int8_t* a8, int64_t* am, int64_t* ak, hipStream_t s);
+                        int8_t* a8, int64_t* am, int64_t* ak, const int8_t* next_w,
+                        int next_n, int next_k, int next_ksplit, hipStream_t s);
 
 /* The KV cache is paged. Per layer, a K pool [n_pages][n_kv][128][128] (a
  * page's K rows: n_kv heads x 128 slots x 128 channels) and a V pool

@@ -380,7 +380,7 @@ def test_residual_normq_renorm_branches(C, smooth):
     xm = torch.empty(R, dtype=torch.int64, device="cuda")
     xk = torch.empty(R, dtype=torch.int64, device="cuda")
     call("detllm_residual_normq", g(P), 1, 0, R, C, g(row_m), g(row_k), g(col_m), 20, 20, hg,
-         kg, g(sm_m) if smooth else None, 15, x8, xm, xk)
+         kg, g(sm_m) if smooth else None, 15, x8, xm, xk, None, 0, 0, 0)
     for got, w in zip((hg, kg, x8, xm, xk), want):
         eq(got, w)
     # the rows do take the branches named above

@@ -60,6 +60,11 @@ def test_gemv_plan_host_entry():
         assert (K + chunk - 1) // chunk == ks
     assert gemv_plan(1, 151936, 1024) == 1
     assert gemv_plan(1, 1024, 3072) > 1
+    # several rows split K in two between one and four column groups per CU
+    # (one row keeps one split there: the fused-operand kernels' plan)
+    assert gemv_plan(8, 6144, 1024) == 2
+    assert gemv_plan(1, 6144, 1024) == 1
+    assert gemv_plan(8, 4096, 1024) == 1
     with pytest.raises(RuntimeError):
         gemv_plan(65, 1024, 1024)
 
