@@ -183,7 +183,7 @@ struct L2Warm {
   int nwarm;        // warming blocks, a multiple of 8
 };
 
-constexpr int L2WARM_BLOCKS = 64;
+constexpr int L2WARM_BLOCKS = 32;
 
 // Host side: the warming blocks for the next igemv(A, W, ., M, N, K, ksplit),
 // block ids first .. first + L2WARM_BLOCKS - 1 of a launch (W null: none).
@@ -201,22 +201,23 @@ inline L2Warm make_l2warm(const int8_t* W, int N, int K, int ksplit, int first) 
   return w;
 }
 
-// Block j (>= w.first) of nt threads: one 4-byte direct-to-LDS load per 64
-// bytes of its GEMM blocks' slices (no registers to wait on; the wave ends
-// when they land). `sink`: 256 bytes of this block's LDS, overwritten.
+// Block j (>= w.first) of nt threads: one 4-byte direct-to-LDS load per
+// 128-byte line of its GEMM blocks' slices (as fast for the GEMM as touching
+// every 64 bytes; no registers to wait on: the wave ends when they land).
+// `sink`: 256 bytes of this block's LDS, overwritten.
 constexpr int L2WARM_SLEEP = 0;  // s_sleep units (64 clocks) before the loads
 
 __device__ __forceinline__ void l2_warm(const L2Warm& w, int j, int nt, void* sink) {
   if (L2WARM_SLEEP > 0) __builtin_amdgcn_s_sleep(L2WARM_SLEEP);
   const int t = (j - w.first) >> 3;  // rank among the warming blocks on this XCD
   const int step = w.nwarm;          // 8 x (warming blocks per XCD)
-  const int kc64 = w.kchunk >> 6;
-  const int per = 16 * kc64;
+  const int kl = (w.kchunk + 127) >> 7;  // lines per row of a K range
+  const int per = 16 * kl;
   for (int L = (j & 7) + 8 * t; L < w.nblk; L += step) {
     const int bx = L % w.gx, by = L / w.gx;
     for (int u = (int)threadIdx.x; u < per; u += nt) {
-      const int row = 16 * bx + u / kc64;
-      const int k = by * w.kchunk + (u % kc64) * 64;
+      const int row = 16 * bx + u / kl;
+      const int k = by * w.kchunk + (u % kl) * 128;
       if (row < w.N && k < w.K)
         __builtin_amdgcn_global_load_lds((gbl_ptr_t)(w.W + (i64)row * w.K + k), (lds_ptr_t)sink,
                                          4, 0, 0);
