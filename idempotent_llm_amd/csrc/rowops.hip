@@ -519,7 +519,7 @@ __device__ __forceinline__ void swiglu_quant_row(const SwigluArgs& a, int r, Red
     load_cols_or0(dsm, a.ds_m, a.ds_m, I, red);
     xm = a.xm[r];
     xk = a.xk[r];
-    constexpr int KF = 1;  // decode gate|up products have no K split
+    constexpr int KF = 2;  // decode gate|up products: at most two K splits
     int32_t t[KF][2][VPT];
     load_rows_i32_first<KF, 2, VPT>(t, a.P, a.nsplit, a.split_stride, offs, I, red);
     __builtin_amdgcn_sched_barrier(0);
