@@ -471,6 +471,12 @@ constexpr i64 DECODE_LDS_BYTES = 48 * 1024;
 constexpr int32_t SCORE_MASKED = INT32_MIN;  // |q.k| <= 128*128*128 < 2^31: never a score
 constexpr int DEC_MAX_S = 131071;            // int32 MFMA accumulators of P.V
 constexpr int VPRE = 4;                      // 64-slot steps of V loaded before the scores
+// The same for the fused eight-wave kernel (one 16-channel block per wave):
+// six steps (384 slots) measured fastest at c3's ~320 slots (4: 1.595, 6:
+// 1.561, 8: 1.569 ms per b8 step): loads past the row's steps are wasted
+// traffic through the CU's load path, and the steps past the prefetch cost a
+// round trip in the P.V loop.
+constexpr int VPRE_FUSED = 6;
 
 // DPP max over each aligned row of 16 lanes (result in every lane of the row)
 __device__ __forceinline__ int32_t row16_max(int32_t v) {
@@ -992,9 +998,8 @@ __global__ __launch_bounds__(QAD_WAVES * 64) void k_qkv_attn_decode(DecodeArgs a
   const i64 base = in.base;
   qkv_head_rope_load(qa, slotl, in);  // waits for the position only
   // 2. the loads that depend on those: this wave's K rows of the scores
-  // pass's first iterations (slots below the host bound a.S <= capacity; the
-  // pass masks slots at or past the scanned count and slots of pages that are
-  // not mapped)
+  // pass's first iterations (the pass masks slots at or past the scanned
+  // count and slots of pages that are not mapped)
   int pgk[NPK];
 #pragma unroll
   for (int j = 0; j < NPK; ++j)
@@ -1009,7 +1014,9 @@ __global__ __launch_bounds__(QAD_WAVES * 64) void k_qkv_attn_decode(DecodeArgs a
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
         const int s = (w + 4 * NW * it + u * NW) * 16 + l16;  // < KPRE_SLOTS
-        const int sc_ = s < a.S ? s : 0;
+        // slots at or past the scanned count read slot 0 (one cached line
+        // instead of rows nobody scores; the pass masks them)
+        const int sc_ = s < S ? s : 0;
         const int j = sc_ >> 7;
         int pg = pgk[0];
 #pragma unroll
@@ -1042,8 +1049,8 @@ __global__ __launch_bounds__(QAD_WAVES * 64) void k_qkv_attn_decode(DecodeArgs a
     if (i < npages) pg_lds[i] = pgv[q];  // (loaded unconditionally above)
   }
   __syncthreads();
-  decode_body<G, 2 * VPRE, SCR, true, NW>(a, S, kvh, b, &q_lds[0][0], t_lds, sh_scores, pg_lds,
-                                          pre);
+  decode_body<G, VPRE_FUSED, SCR, true, NW>(a, S, kvh, b, &q_lds[0][0], t_lds, sh_scores,
+                                            pg_lds, pre);
   report_slots(a, over, kvh == 0);
 }
 
