@@ -366,14 +366,17 @@ struct ResNormArgs {
   L2Warm warm;   // the next skinny GEMM's weights (extra blocks after the rows)
 };
 
-template <int VPT, class Red>
+// MODE: the row's mode when the launch fixes it (the kernel then holds that
+// path only: less code to fetch per launch), else -1 (a.mode decides).
+template <int VPT, class Red, int MODE = -1>
 __device__ __forceinline__ void residual_normq_row(const ResNormArgs& a, int r, Red& red) {
+  const int mode = MODE >= 0 ? MODE : a.mode;
   const int C = a.C;
   const i64 off = (i64)r * C;
   i64 h[VPT], d[VPT], smv[VPT];
   i64 kr, lg = -1;
   const int32_t* h_in = a.h_in ? a.h_in : a.h;
-  if (a.mode == 1) {
+  if (mode == 1) {
     // the GEMM residual add: every load of the row issued before any is used
     // (no branch between them; col_m is required in this mode, so it stands
     // in for a missing sm_m)
@@ -403,7 +406,7 @@ __device__ __forceinline__ void residual_normq_row(const ResNormArgs& a, int r, 
     kr = residual_add_row(h, k_res, d, row_m, dk, red, &lg);
   } else {
   prefetch_cols(smv, a.sm_m, C, red);
-  if (a.mode == 2) {
+  if (mode == 2) {
     // _norm_quant of a given residual row: h is read, not written
 #pragma unroll
     for (int j = 0; j < VPT; ++j) {
@@ -414,7 +417,7 @@ __device__ __forceinline__ void residual_normq_row(const ResNormArgs& a, int r, 
     for (int j = 0; j < VPT; ++j)
       if (red.tid() + j * red.nt() >= C) h[j] = 0;
     kr = 0;
-  } else if (a.mode == 0) {
+  } else if (mode == 0) {
     const i64 id = torch_index(a.ids[r], a.vocab, red.tid() ? nullptr : a.err, DI_ERR_TOKEN);
     const i64 dm = a.em[id], ek = a.ek[id];
 #pragma unroll
@@ -447,7 +450,7 @@ __device__ __forceinline__ void residual_normq_row(const ResNormArgs& a, int r, 
     kr = residual_add_row(h, k_res, d, row_m, dk, red, &lg);
   }
   }
-  if (a.mode != 2 && a.h) {
+  if (mode != 2 && a.h) {
 #pragma unroll
     for (int j = 0; j < VPT; ++j) {
       const int c = red.tid() + j * red.nt();
@@ -467,7 +470,7 @@ __device__ __forceinline__ void residual_normq_row(const ResNormArgs& a, int r, 
             a.xm ? a.xm + r : nullptr, a.xk ? a.xk + r : nullptr);
 }
 
-template <int VPT, int NT = RT_WIDE, bool WARM = false>
+template <int VPT, int NT = RT_WIDE, bool WARM = false, int MODE = -1>
 __global__ __launch_bounds__(NT) void k_residual_normq(ResNormArgs a) {
   keep_hidden_args();
   __shared__ i64 red_buf[32];
@@ -476,7 +479,20 @@ __global__ __launch_bounds__(NT) void k_residual_normq(ResNormArgs a) {
     return;
   }
   BlockRed red{red_buf, 0, a.nt};
-  residual_normq_row<VPT>(a, (int)blockIdx.x - (WARM ? L2WARM_BLOCKS : 0), red);
+  residual_normq_row<VPT, BlockRed, MODE>(a, (int)blockIdx.x - (WARM ? L2WARM_BLOCKS : 0), red);
+}
+
+// The GEMM residual add (mode 1) only.
+template <int VPT, int NT = RT_WIDE, bool WARM = false>
+__global__ __launch_bounds__(NT) void k_residual_add_normq(ResNormArgs a) {
+  keep_hidden_args();
+  __shared__ i64 red_buf[32];
+  if (WARM && (int)blockIdx.x < L2WARM_BLOCKS) {  // no kernel argument needed to decide
+    l2_warm(a.warm, blockIdx.x, a.nt, red_buf);
+    return;
+  }
+  BlockRed red{red_buf, 0, a.nt};
+  residual_normq_row<VPT, BlockRed, 1>(a, (int)blockIdx.x - (WARM ? L2WARM_BLOCKS : 0), red);
 }
 
 struct SwigluArgs {
@@ -1179,10 +1195,10 @@ __global__ __launch_bounds__(PRO_THREADS) void k_gemv_pro(ProGemv g, ResNormArgs
     }
     if (ONE) {
       BlockRed red{L.red_buf, 0, PRO_THREADS};
-      residual_normq_row<CMAX / PRO_THREADS>(a, 0, red);
+      residual_normq_row<CMAX / PRO_THREADS, BlockRed, 1>(a, 0, red);
     } else if (wave < g.R) {
       WaveRed red;
-      residual_normq_row<CMAX / 64>(a, wave, red);
+      residual_normq_row<CMAX / 64, WaveRed, 1>(a, wave, red);
     }
   } else {
     MergeArgs a = ma;
@@ -1368,7 +1384,7 @@ int detllm_residual_normq(const int32_t* P, int nsplit, int64_t split_stride, in
   a.row_m = row_m; a.row_k = row_k; a.col_m = col_m; a.col_k = col_k; a.tb = tb;
   a.h = h; a.k_res = k_res; a.sm_m = sm_m; a.sm_k = sm_k; a.x8 = x8; a.xm = xm; a.xk = xk;
   a.warm = warm_for(R, next_w, next_n, next_k, next_ksplit);
-  DI_WARM_OR_ROWS(R, C, k_residual_normq, s, a);
+  DI_WARM_OR_ROWS(R, C, k_residual_add_normq, s, a);
   DI_LAUNCH_CHECK();
   return DI_OK;
 }
