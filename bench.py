@@ -18,7 +18,7 @@ but the capturing first decode) and records the demo checkpoint hashes
 (scripts/demo.py:58-75) of row 0 at batch 8 and of batch 1.
 
 ``roofline`` is the dominant decode kernel, the skinny int8 GEMM
-``k_gemv_nt`` (112 launches per step): algorithmic bytes per launch (weights
+``k_gemv_dec`` (112 launches per step): algorithmic bytes per launch (weights
 + activations + int32 outputs) over its average launch duration, timed with
 HIP events around replays of a graph holding one batch-8 step's 112 launches
 (model weights and K splits) on the stream that launches them; ``traffic`` is
@@ -187,7 +187,7 @@ def _graph_time_us(fn, reps: int, launches: int) -> float:
 def decode_gemv_jobs(model, B: int):
     """The decode step's skinny GEMMs with the model's own weights and K
     splits on random int8 activations: layer jobs (q|k|v, o, gate|up, down
-    per layer: k_gemv_nt) and the LM head (k_gemv_stream)."""
+    per layer: k_gemv_dec) and the LM head (k_gemv_stream)."""
     import torch
     H, I_ = model.hidden, model.inter
     nqd = model.n_q * model.hd
@@ -246,7 +246,7 @@ def _traffic(kernel: str):
 
 
 def gemv_rooflines(model, B: int):
-    """k_gemv_nt (the layer GEMVs) and k_gemv_stream (LM head), each timed
+    """k_gemv_dec (the layer GEMVs) and k_gemv_stream (LM head), each timed
     over a graph of one decode step's launches of that kernel."""
     from idempotent_llm_amd.backends import gemm_nt
     jobs, head = decode_gemv_jobs(model, B)
@@ -258,7 +258,7 @@ def gemv_rooflines(model, B: int):
         return f
 
     res = {}
-    for name, js, reps in (("k_gemv_nt", jobs, 20), ("k_gemv_stream", [head], 50)):
+    for name, js, reps in (("k_gemv_dec", jobs, 20), ("k_gemv_stream", [head], 50)):
         us = _graph_time_us(run(js), reps, len(js))
         per = _job_bytes(js) / len(js)
         achieved = per / (us * 1e-6) / 1e9
@@ -270,7 +270,7 @@ def gemv_rooflines(model, B: int):
                      "avg_launch_us": round(us, 3),
                      "timing": f"HIP events around {reps} replays of a graph of one batch-{B} "
                                f"decode step's {len(js)} {name} launches"}
-    return res["k_gemv_nt"], res["k_gemv_stream"]
+    return res["k_gemv_dec"], res["k_gemv_stream"]
 
 
 def split_attention_case(model, B: int = 32, S: int = 4096, seed: int = 4):
@@ -370,7 +370,7 @@ def kernel_probe(model, B: int, reps: int = 3):
         run()
     torch.cuda.synchronize()
     log(f"kernel probe: copy {n} B x {reps}, {len(jobs) + 1} GEMV launches x {reps} "
-        f"({_job_bytes(jobs) / len(jobs):.0f} algorithmic B per k_gemv_nt launch), "
+        f"({_job_bytes(jobs) / len(jobs):.0f} algorithmic B per k_gemv_dec launch), "
         f"256 eager decode steps at batch {B}, {reps} at batch 1, split-S attention x {reps} "
         f"(plan {plan}, {nbytes} algorithmic B per call)")
 

@@ -744,7 +744,7 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, int S, int kvh,
 #pragma unroll
   for (int hh = 0; hh < G; ++hh) allfast = allfast && tph[hh] < ((i64)1 << 23);
   ExpEst Ef[G];
-  if (allfast) {
+  if (DI_LIKELY(allfast)) {
 #pragma unroll
     for (int hh = 0; hh < G; ++hh) {
       Ef[hh] = make_expest(tph[hh]);
@@ -800,7 +800,7 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, int S, int kvh,
   bool pfast = allfast;
 #pragma unroll
   for (int hh = 0; hh < G; ++hh) pfast = pfast && den[hh] < ((i64)1 << 34);
-  if (pfast) {
+  if (DI_LIKELY(pfast)) {
     // as pass 2: every head, two slots per thread, reads first
     DivEst Df[G];
 #pragma unroll

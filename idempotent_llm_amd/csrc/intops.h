@@ -37,6 +37,12 @@
 #define DI_HD static inline
 #endif
 
+// Branch hints for the exactness fallbacks (operands outside the ranges the
+// fast forms are proven for): the compiler lays the unlikely side out of the
+// hot instruction stream, so a launch fetches fewer instruction lines.
+#define DI_LIKELY(x) __builtin_expect(!!(x), 1)
+#define DI_UNLIKELY(x) __builtin_expect(!!(x), 0)
+
 typedef int64_t i64;
 typedef uint64_t u64;
 
@@ -221,7 +227,7 @@ DI_HD i64 srd127(i64 num, i64 e) {
 
 DI_HD void fit_dyadic_ratio_127(i64 num, i64* m_out, i64* e_out) {
   const i64 lg = ilog2(num);
-  if (num <= 0 || lg >= 56) {
+  if (DI_UNLIKELY(num <= 0 || lg >= 56)) {
     fit_dyadic_ratio(num, 127, m_out, e_out);
     return;
   }
@@ -518,7 +524,7 @@ DI_HD ExpEst make_expest(i64 tpos) {  // 1 <= tpos < 2^23
 // for m_f >= 2^15; smaller m_f takes the integer path); same integer.
 DI_HD i64 di_exp_tpos_fast(i64 m, i64 k) {
   const i64 m_f = wsub(wadd(m, shr(m, 1)), shr(m, 4));
-  if (k >= 0 && k <= 46 && m_f >= ((i64)1 << 15) && m_f < ((i64)1 << 31))
+  if (DI_LIKELY(k >= 0 && k <= 46 && m_f >= ((i64)1 << 15) && m_f < ((i64)1 << 31)))
     return imax((i64)rhad_est((double)((i64)1 << k), make_divest(m_f, 1.0)), 1);
   return di_exp_tpos(m, k);
 }

@@ -84,7 +84,7 @@ __device__ __forceinline__ void wave_rmsnorm128(i64& a, i64& b) {
   b = shl(rshift_round(b, down), up);
   const i64 ss = wave_sum(wadd(wmul(a, a), wmul(b, b)));
   const i64 rms = imax(isqrt_wave(rhad_pow2(ss, 7)), 1);
-  if (rms > ((i64)1 << 16)) {
+  if (DI_LIKELY(rms > ((i64)1 << 16))) {
     // |a|, |b| <= 2^26 after the shift: rhad_est as in rmsnorm_row
     const DivEst D = make_divest(rms, 1048576.0);
     a = rhad_est_signed(a, D);
@@ -265,7 +265,7 @@ __device__ __forceinline__ void qkv_head_compute(const QKVArgs& a, int r, int sl
     const int pg = a.kv.page(b, slot);
     int8_t o0, o1;
     const i64 lim = (i64)1 << 49;  // 2 |n| + den < 2^51 for rhad_est_i8
-    if (den < lim && n0 > -lim && n0 < lim && n1 > -lim && n1 < lim) {
+    if (DI_LIKELY(den < lim && n0 > -lim && n0 < lim && n1 > -lim && n1 < lim)) {
       const DivEst D = make_divest(den, 1.0);
       o0 = (int8_t)rhad_est_i8(n0, D);
       o1 = (int8_t)rhad_est_i8(n1, D);
@@ -309,7 +309,7 @@ __device__ __forceinline__ void qkv_head_compute(const QKVArgs& a, int r, int sl
       if (den <= 0) den = 1;
       const i64 n = shl(rv[q], up);
       const i64 lim = (i64)1 << 49;  // 2 |n| + den < 2^51 for rhad_est_i8
-      if (den < lim && n > -lim && n < lim)
+      if (DI_LIKELY(den < lim && n > -lim && n < lim))
         outv[q] = rhad_est_i8(n, make_divest(den, 1.0));
       else
         outv[q] = clamp_i8(rhad(n, den));
@@ -333,7 +333,7 @@ __device__ __forceinline__ void qkv_head_compute(const QKVArgs& a, int r, int sl
   norm_scale(1, qkk, &m, &k);
   const i64 am = imax(wave_max(imax(wabs(q0), wabs(q1))), 1);
   const i64 qrow = (((i64)b * a.n_q + h) * a.T + t);
-  if (am < ((i64)1 << 43)) {  // as in quant_row: no 127 q wraps, 255 am < 2^51
+  if (DI_LIKELY(am < ((i64)1 << 43))) {  // as in quant_row: no 127 q wraps, 255 am < 2^51
     const DivEst D = make_divest(am, 127.0);
     q8_out[c0] = (int8_t)rhad_est_signed(q0, D);
     q8_out[c1] = (int8_t)rhad_est_signed(q1, D);
@@ -512,7 +512,7 @@ __device__ __forceinline__ void qkv_rows4(const QKVArgs& a, int R, int r0, int s
       ss = wadd(ss, wmul(y[i], y[i]));
     }
     const i64 rms = imax(isqrt_est(rhad_pow2(row16_sum64(ss), 7)), 1);
-    if (rms > ((i64)1 << 16)) {  // |y| <= 2^26 after the shift: rhad_est
+    if (DI_LIKELY(rms > ((i64)1 << 16))) {  // |y| <= 2^26 after the shift: rhad_est
       const DivEst D = make_divest(rms, 1048576.0);
 #pragma unroll
       for (int i = 0; i < 8; ++i) y[i] = rhad_est_signed(y[i], D);
@@ -573,7 +573,7 @@ __device__ __forceinline__ void qkv_rows4(const QKVArgs& a, int R, int r0, int s
   const i64 am = imax(row16_max64(amx), 1);
   const i64 qrow = ((i64)b * a.n_q + h) * a.T + t;
   uint32_t w[2] = {0, 0};
-  if (am < ((i64)1 << 43)) {  // as in quant_row: no 127 q wraps, 255 am < 2^51
+  if (DI_LIKELY(am < ((i64)1 << 43))) {  // as in quant_row: no 127 q wraps, 255 am < 2^51
     const DivEst D = make_divest(am, 127.0);
 #pragma unroll
     for (int i = 0; i < 8; ++i) w[i >> 2] |= (uint32_t)(uint8_t)(int8_t)rhad_est_signed(q[i], D) << (8 * (i & 3));

@@ -70,7 +70,7 @@ __device__ __forceinline__ void rmsnorm_row(i64 (&v)[VPT], int C, Red& red, i64 
   ss = red.sum(ss);
   const i64 mean = (C & (C - 1)) == 0 ? rhad_pow2(ss, (int)ilog2(C)) : rhad(ss, (i64)C);
   const i64 rms = imax(isqrt_wave(mean), 1);
-  if (rms > ((i64)1 << 16)) {
+  if (DI_LIKELY(rms > ((i64)1 << 16))) {
     // the shift leaves |xp| <= 2^26, so 2 |xp| 2^20 + rms < 2^51 and the
     // quotient is below 2^31: rhad_est, and to_i32 keeps it
     const DivEst D = make_divest(rms, 1048576.0);
@@ -92,7 +92,7 @@ __device__ __forceinline__ void quant_row(const i64 (&v)[VPT], i64 m_in, i64 k_i
   i64 m, k;
   norm_scale(m_in, k_in, &m, &k);
   const i64 a = imax(row_absmax(v, red), 1);
-  if (a < ((i64)1 << 43)) {
+  if (DI_LIKELY(a < ((i64)1 << 43))) {
     const DivEst D = make_divest(a, 127.0);
 #pragma unroll
     for (int j = 0; j < VPT; ++j) {
@@ -560,7 +560,7 @@ __device__ __forceinline__ void swiglu_quant_row(const SwigluArgs& a, int r, Red
   if (kLate) prefetch_cols(dsm, a.ds_m, I, red);
   const i64 tp = di_exp_tpos_fast(xm, gk);
   i64 y[VPT];
-  if (tp < ((i64)1 << 23)) {
+  if (DI_LIKELY(tp < ((i64)1 << 23))) {
     const ExpEst Ee = make_expest(tp);
 #pragma unroll
     for (int j = 0; j < VPT; ++j) y[j] = wmul(swiglu_elem_est(g32[j], u32[j], Ee), dsm[j]);
@@ -656,12 +656,12 @@ __device__ __forceinline__ void merge_rowcol_row(const MergeArgs& a, int r, Red&
 #pragma unroll
   for (int j = 0; j < VPT; ++j) v[j] = rshift_round(v[j], sh);
   const i64 a2 = imax(row_absmax(v, red), 1);
-  if (a2 < ((i64)1 << 46)) {
+  if (DI_LIKELY(a2 < ((i64)1 << 46))) {
     // |v| <= a2 < 2^46 (the pre-shift leaves at most 46 bits): 127 |v| does
     // not wrap and 127 |v| + a2 < 2^53; the plain estimate is exact below
     // 2^43, the corrected one above
     const DivEst D = make_divest(a2, 127.0);
-    if (a2 < ((i64)1 << 43)) {
+    if (DI_LIKELY(a2 < ((i64)1 << 43))) {
 #pragma unroll
       for (int j = 0; j < VPT; ++j) {
         const int c = red.tid() + j * red.nt();
