@@ -259,6 +259,27 @@ struct BlockRed {
     b = rb;
   }
 
+  // Block maxima of two values (one barrier; blocks of at most 512 threads)
+  __device__ __forceinline__ void max2(i64& a, i64& b) {
+    a = wave_part<true>(a);
+    b = wave_part<true>(b);
+    i64* slot = buf + (k & 1) * 16;
+    ++k;
+    if ((threadIdx.x & 63) == 63) {
+      slot[threadIdx.x >> 6] = a;
+      slot[8 + (threadIdx.x >> 6)] = b;
+    }
+    __syncthreads();
+    const int nw = n >> 6;
+    i64 ra = INT64_MIN, rb = INT64_MIN;
+    for (int i = 0; i < nw; ++i) {
+      ra = imax(ra, slot[i]);
+      rb = imax(rb, slot[8 + i]);
+    }
+    a = ra;
+    b = rb;
+  }
+
   // Block maxima of one or two 32-bit unsigned values (one barrier). A row
   // shift that depends only on the bit length of max |x| reduces bit lengths
   // (bitlen_abs below) here instead of 64-bit magnitudes.

@@ -22,6 +22,8 @@
 // Op-level kernels (the same device functions, one reference function each)
 // back the op API used by the parity tests.
 
+#include <type_traits>
+
 #include "common.h"
 #include "gemv.h"
 #include "qkv_epilogue.h"
@@ -42,6 +44,21 @@ __device__ __forceinline__ i64 row_absmax(const i64 (&v)[VPT], Red& red) {
 #pragma unroll
   for (int j = 0; j < VPT; ++j) g = imax(g, wabs(v[j]));
   return red.max(g);
+}
+
+// max_j |v_j| over the row as an unsigned value: the same maximum as
+// row_absmax, except that a row holding INT64_MIN (whose wrapped |v| is
+// negative and counts for nothing in dyadic.py's row maximum) returns 2^63.
+// The fp64 quotient estimates need |v| <= max, so such a row takes the
+// exact path, which recomputes the maximum with row_absmax. The unsigned
+// maximum reduces as signed values g - 2^63 (g ^ 2^63 for g <= 2^63).
+template <int VPT, class Red>
+__device__ __forceinline__ u64 row_absmax_u(const i64 (&v)[VPT], Red& red) {
+  u64 g = 0;
+#pragma unroll
+  for (int j = 0; j < VPT; ++j) g = ::max(g, (u64)wabs(v[j]));
+  constexpr u64 top = (u64)1 << 63;
+  return (u64)red.max((i64)(g ^ top)) ^ top;
 }
 
 // ilog2(max(max_j |v_j|, 1)) over the row, from a 32-bit bit-length maximum
@@ -91,8 +108,10 @@ __device__ __forceinline__ void quant_row(const i64 (&v)[VPT], i64 m_in, i64 k_i
                                           Red& red, int8_t* out, i64* m_out, i64* k_out) {
   i64 m, k;
   norm_scale(m_in, k_in, &m, &k);
-  const i64 a = imax(row_absmax(v, red), 1);
-  if (DI_LIKELY(a < ((i64)1 << 43))) {
+  const u64 au = row_absmax_u(v, red);
+  i64 a;
+  if (DI_LIKELY(au < ((u64)1 << 43))) {
+    a = imax((i64)au, 1);
     const DivEst D = make_divest(a, 127.0);
 #pragma unroll
     for (int j = 0; j < VPT; ++j) {
@@ -100,6 +119,7 @@ __device__ __forceinline__ void quant_row(const i64 (&v)[VPT], i64 m_in, i64 k_i
       if (c < C) out[c] = (int8_t)rhad_est_signed(v[j], D);
     }
   } else {
+    a = DI_UNLIKELY(au >> 63) ? imax(row_absmax(v, red), 1) : (i64)au;
     const Recip R = make_recip(a);
 #pragma unroll
     for (int j = 0; j < VPT; ++j) {
@@ -652,11 +672,48 @@ __device__ __forceinline__ void merge_rowcol_row(const MergeArgs& a, int r, Red&
   }
 #pragma unroll
   for (int j = 0; j < VPT; ++j) v[j] = wmul(v[j], om[j]);  // 0 past C
-  const i64 sh = imax(row_ilog2_absmax(v, red) - 45, 0);
+  // Blocks: the pre-shift and the quantisation maximum from one reduction
+  // of the row's largest and smallest value. Both follow from them when
+  // every |v| < 2^62 (then rshift_round(., sh) cannot wrap and does not
+  // decrease, so max_j |rshift_round(v_j, sh)| sits at an extreme, and so
+  // does the bit length of max |v|); else (INT64_MIN or near-overflow
+  // values), and in a single wave, where two reductions cost less than the
+  // extra work, the two reductions of dyadic.py:133-136 run as written.
+  i64 sh, a2;
+  bool exact = false;      // a row holding INT64_MIN after the shift
+  i64 vmax = INT64_MAX, vmin = 0;
+  if constexpr (std::is_same<Red, BlockRed>::value) {
+    vmax = 0;  // columns past C hold 0
 #pragma unroll
-  for (int j = 0; j < VPT; ++j) v[j] = rshift_round(v[j], sh);
-  const i64 a2 = imax(row_absmax(v, red), 1);
-  if (DI_LIKELY(a2 < ((i64)1 << 46))) {
+    for (int j = 0; j < VPT; ++j) {
+      vmax = imax(vmax, v[j]);
+      vmin = imin(vmin, v[j]);
+    }
+    i64 nmin = ~vmin;  // ~ reverses the order without overflow
+    if (red.nt() <= 512) {
+      red.max2(vmax, nmin);
+    } else {
+      vmax = red.max(vmax);
+      nmin = red.max(nmin);
+    }
+    vmin = ~nmin;
+  }
+  const i64 lim = (i64)1 << 62;
+  if (DI_LIKELY(vmax < lim && vmin > -lim)) {
+    const uint32_t L = ::max(bitlen_abs(vmax), bitlen_abs(vmin));
+    sh = imax(ilog2_from_bitlen(L) - 45, 0);
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) v[j] = rshift_round(v[j], sh);
+    a2 = imax(imax(wabs(rshift_round(vmax, sh)), wabs(rshift_round(vmin, sh))), 1);
+  } else {
+    sh = imax(row_ilog2_absmax(v, red) - 45, 0);
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) v[j] = rshift_round(v[j], sh);
+    const u64 au = row_absmax_u(v, red);
+    exact = au >> 63;
+    a2 = DI_UNLIKELY(exact) ? imax(row_absmax(v, red), 1) : imax((i64)au, 1);
+  }
+  if (DI_LIKELY(a2 < ((i64)1 << 46) && !exact)) {
     // |v| <= a2 < 2^46 (the pre-shift leaves at most 46 bits): 127 |v| does
     // not wrap and 127 |v| + a2 < 2^53; the plain estimate is exact below
     // 2^43, the corrected one above

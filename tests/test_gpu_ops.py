@@ -425,3 +425,78 @@ def test_igemv_prefetch_variant_same_product():
         call("detllm_igemv_nt_pf", a, w, ref, M, N, K, ks, M * N, None, 8, None, 0, None, 0,
              None, 0)
 
+
+
+def test_merge_rowcol_extreme_rows():
+    """The attention-output merge (detllm_merge_rowcol) on rows whose scaled
+    values reach every branch of its row maximum: ordinary magnitudes, values
+    in [2^62, 2^63), an exact INT64_MIN in a row that is shifted and in one
+    that is not, products that wrap modulo 2^64, a zero row and a row of
+    INT64_MIN only, against the oracle's requant_i8_rowcol of the same int64
+    products (dyadic.py:123-139)."""
+    from idempotent_llm_amd._lib import call
+    print("[merge_rowcol extreme rows]", flush=True)
+    rng = np.random.default_rng(77)
+    R, C = 6, 2048
+    os_m = rng.integers(1 << 10, 1 << 12, C).astype(I64)
+    col_m = rng.integers(1 << 10, 1 << 12, C).astype(I64)
+    fac = os_m * col_m                        # the per-column factor, below 2^24
+    attn = np.zeros((R, C), I64)
+    attn[0] = rng.integers(-(1 << 30), 1 << 30, C)
+    attn[1] = rng.integers(-(1 << 40), 1 << 40, C)            # |v| up to ~2^63
+    attn[2] = rng.integers(-(1 << 30), 1 << 30, C)
+    j = int(rng.integers(0, C))
+    f2 = int(fac[j]) & -int(fac[j])                           # largest power of two in fac[j]
+    fac[j] = f2 if f2 > 1 else 2
+    attn[2, j] = -(1 << 63) // int(fac[j])                    # attn * fac = INT64_MIN exactly
+    attn[3] = rng.integers(-(1 << 50), 1 << 50, C)            # products wrap modulo 2^64
+    # row 5: small values and one INT64_MIN, which the unshifted row keeps
+    attn[5] = rng.integers(-1000, 1001, C)
+    j5 = (j + 1 + int(rng.integers(0, C - 1))) % C
+    fac[j5] = 1 << 12
+    attn[5, j5] = -(1 << 51)
+    # row 5: INT64_MIN in every column (factor a power of two per column)
+    p2 = np.ones(C, I64) << rng.integers(1, 23, C)
+    attn5 = -(np.ones(C, I64) << (63 - np.log2(p2).astype(I64)))
+    with np.errstate(over="ignore"):
+        v = attn * fac
+    v5 = attn5 * p2
+    assert (v5 == np.iinfo(np.int64).min).all()
+    for attn_r, fac_r, v_r in ((attn, fac, v), (np.stack([attn5] * R), p2, np.stack([v5] * R))):
+        a8 = torch.empty(R, C, dtype=torch.int8, device="cuda")
+        am = torch.empty(R, dtype=torch.int64, device="cuda")
+        ak = torch.empty(R, dtype=torch.int64, device="cuda")
+        call("detllm_merge_rowcol", g(np.ascontiguousarray(attn_r[None])), 1, R * C, R, C,
+             g(fac_r), 7, g(np.ones(C, I64)), 9, a8, am, ak, None, 0, 0, 0)
+        wy, wm, wk = ody.requant_i8_rowcol(v_r, np.ones((R, 1), I64), np.full((R, 1), 7, I64),
+                                           np.ones(C, I64), 9)
+        np.testing.assert_array_equal(a8.cpu().numpy(), wy)
+        np.testing.assert_array_equal(am.cpu().numpy(), wm.reshape(-1))
+        np.testing.assert_array_equal(ak.cpu().numpy(), wk.reshape(-1))
+    assert v[5].min() == np.iinfo(np.int64).min and np.abs(v[5][v[5] > -(1 << 62)]).max() < 1 << 46
+
+
+def test_quant_i8_pertoken_extreme_rows():
+    """detllm_op_quant_i8_pertoken (dyadic.py:93-105) on rows holding
+    INT64_MIN, whose |x| wraps to itself and is skipped by the row maximum:
+    alone among small values, a whole row of it, next to INT64_MAX, and
+    ordinary rows on both quotient paths, against the oracle."""
+    from idempotent_llm_amd import dyadic as dd
+    print("[quant_i8_pertoken extreme rows]", flush=True)
+    rng = np.random.default_rng(78)
+    lo, hi = np.iinfo(np.int64).min, np.iinfo(np.int64).max
+    for C in (1024, 3000):
+        x = np.zeros((6, C), I64)
+        x[0] = rng.integers(-1000, 1001, C)
+        x[0, C // 3] = lo
+        x[1] = lo
+        x[2] = rng.integers(-(1 << 60), 1 << 60, C)
+        x[2, 5], x[2, 7] = lo, hi
+        x[3] = rng.integers(-(1 << 40), 1 << 40, C)               # below 2^43: estimate path
+        x[4] = rng.integers(-(1 << 50), 1 << 50, C)               # above: exact path
+        m = rng.integers(1 << 14, 1 << 16, (6, 1)).astype(I64)
+        k = np.full((6, 1), 20, I64)
+        want = ody.quant_i8_pertoken(x, m, k)
+        got = dd.quant_i8_pertoken(g(x), g(m), g(k))
+        for a, b in zip(got, want):
+            np.testing.assert_array_equal(a.cpu().numpy(), b)
