@@ -507,10 +507,10 @@ def c1_c2_bench():
         call("detllm_norm_quant", h, T, H, ones_h, 0, x8, xm, xk)
         gemm_nt(x8, wgu, out=P1)
         call("detllm_swiglu_quant", P1, 1, 0, T, I, xm, xk, gm, 20, gm, 20, ones_i, 0, y8, ym, yk,
-             None, 0, 0, 0)
+             None, 0, 0, 0, 0)
         gemm_nt(y8, wd, out=P2)
         call("detllm_residual_normq", P2, 1, 0, T, H, ym, yk, dm, 20, 20, h_work, k_res, None, 0,
-             None, None, None, None, 0, 0, 0)
+             None, None, None, None, 0, 0, 0, 0)
 
     us1 = _graph_time_us(mlp, 10, 1)
     ops1 = 2.0 * T * H * I * 3

@@ -31,14 +31,14 @@ SIGNATURES = {
     "detllm_greedy_pick_noalloc": [P, P, I, I, P, S],
     "detllm_logits_digest": [P, I, I, P, S],
     "detllm_embed_normq": [P, I, I, L, P, P, P, P, P, P, L, P, P, P, P, S],
-    "detllm_residual_normq": [P, I, L, I, I, P, P, P, L, I, P, P, P, L, P, P, P, P, I, I, I, S],
+    "detllm_residual_normq": [P, I, L, I, I, P, P, P, L, I, P, P, P, L, P, P, P, P, I, I, I, I, S],
     "detllm_norm_quant": [P, I, I, P, L, P, P, P, S],
     "detllm_attn_decode_split": [P, P, P, P, P, I, P, L, I, I, I, I, P, I, P, P, P, P, S],
     "detllm_igemv_resnormq": [P, P, I, I, I, I, L, P, I, L, P, P, P, L, I, P, P, P, P, P, L, P,
                               P, P, L, P, L, S],
     "detllm_igemv_merge": [P, P, I, I, I, I, L, P, I, L, P, L, P, L, P, P, P, L, P, L, S],
-    "detllm_swiglu_quant": [P, I, L, I, I, P, P, P, L, P, L, P, L, P, P, P, P, I, I, I, S],
-    "detllm_merge_rowcol": [P, I, L, I, I, P, L, P, L, P, P, P, P, I, I, I, S],
+    "detllm_swiglu_quant": [P, I, L, I, I, P, P, P, L, P, L, P, L, P, P, P, P, I, I, I, I, S],
+    "detllm_merge_rowcol": [P, I, L, I, I, P, L, P, L, P, P, P, P, I, I, I, I, S],
     "detllm_qkv_epilogue": [P, I, L, I, I, I, I, P, P, P, P, L, P, L, P, L, P, L, P, L, P, L,
                             P, P, P, P, P, P, P, P, L, P, P, P, P, P, P, I, P, L, P, P, S],
     "detllm_kq_est": [P, P, L, L, P, S],

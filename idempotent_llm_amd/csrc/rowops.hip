@@ -105,7 +105,8 @@ __device__ __forceinline__ void rmsnorm_row(i64 (&v)[VPT], int C, Red& red, i64 
 // 2^51 and no 127 x wraps), else from the 64-bit reciprocal.
 template <int VPT, class Red>
 __device__ __forceinline__ void quant_row(const i64 (&v)[VPT], i64 m_in, i64 k_in, int C,
-                                          Red& red, int8_t* out, i64* m_out, i64* k_out) {
+                                          Red& red, int8_t* out, i64* m_out, i64* k_out,
+                                          bool defer_fit = false) {
   i64 m, k;
   norm_scale(m_in, k_in, &m, &k);
   const u64 au = row_absmax_u(v, red);
@@ -128,10 +129,15 @@ __device__ __forceinline__ void quant_row(const i64 (&v)[VPT], i64 m_in, i64 k_i
     }
   }
   if (red.tid() == 0 && m_out) {
-    i64 mo, e;
-    fit_dyadic_ratio_127(wmul(a, m), &mo, &e);
-    *m_out = mo;
-    *k_out = wadd(k, e);
+    if (defer_fit) {  // the consumer fits: (a m, k) stand for (m, k) = (fit(a m), k + e)
+      *m_out = wmul(a, m);
+      *k_out = k;
+    } else {
+      i64 mo, e;
+      fit_dyadic_ratio_127(wmul(a, m), &mo, &e);
+      *m_out = mo;
+      *k_out = wadd(k, e);
+    }
   }
 }
 
@@ -369,6 +375,7 @@ struct ResNormArgs {
   i64 split_stride;
   const int64_t* row_m;
   const int64_t* row_k;
+  int row_fit;  // mode 1: (row_m, row_k) hold a deferred scale fit (fit_dyadic_ratio_127)
   const int64_t* col_m;
   i64 col_k;
   int tb;
@@ -408,13 +415,21 @@ __device__ __forceinline__ void residual_normq_row(const ResNormArgs& a, int r, 
       const int c = red.tid() + j * red.nt();
       h[j] = h_in[off + (c < C ? c : C - 1)];
     }
-    const i64 row_k = a.row_k[r], row_m = a.row_m[r];
+    i64 row_k = a.row_k[r], row_m = a.row_m[r];
     const i64 k_res = (a.k_res_in ? a.k_res_in : a.k_res)[r];
     constexpr int KF = 4;
     int32_t t[KF][1][VPT];
     const i64 offs[1] = {off};
     load_rows_i32_first<KF, 1, VPT>(t, a.P, a.nsplit, a.split_stride, offs, C, red);
     __builtin_amdgcn_sched_barrier(0);
+    if (a.row_fit) {
+      // the producer of the GEMM's operand left its scale fit to this launch:
+      // every lane fits while the partials are in flight
+      i64 fm, fe;
+      fit_dyadic_ratio_127(row_m, &fm, &fe);
+      row_m = fm;
+      row_k = wadd(row_k, fe);
+    }
     i64 dd[1][VPT];
     rows_i32_sum<KF, 1, VPT>(dd, t, a.P, a.nsplit, a.split_stride, offs, C, red);
 #pragma unroll
@@ -532,6 +547,7 @@ struct SwigluArgs {
   int8_t* y8;
   int64_t* ym;
   int64_t* yk;
+  int defer_fit;  // (ym, yk) left for the consumer to fit (quant_row)
   L2Warm warm;  // the next skinny GEMM's weights (extra blocks after the rows)
 };
 
@@ -591,7 +607,7 @@ __device__ __forceinline__ void swiglu_quant_row(const SwigluArgs& a, int r, Red
   }
   const i64 ym = wmul(xm, xm);
   const i64 yk = wadd(wadd(wadd(gk, uk), 7), a.ds_k);
-  quant_row(y, ym, yk, I, red, a.y8 + (i64)r * I, a.ym + r, a.yk + r);
+  quant_row(y, ym, yk, I, red, a.y8 + (i64)r * I, a.ym + r, a.yk + r, a.defer_fit != 0);
 }
 
 // Prefill (256-thread blocks, 8-12 columns per thread): at least three blocks
@@ -625,6 +641,7 @@ struct MergeArgs {
   i64 a8_stride;  // row stride of a8 (0: C)
   int64_t* am;    // null: (m, k) of a8 not stored
   int64_t* ak;
+  int defer_fit;  // (am, ak) left for the consumer to fit (quant_row)
   L2Warm warm;    // the next skinny GEMM's weights (extra blocks after the rows)
 };
 
@@ -740,10 +757,15 @@ __device__ __forceinline__ void merge_rowcol_row(const MergeArgs& a, int r, Red&
     }
   }
   if (red.tid() == 0 && a.am) {
-    i64 mo, e;
-    fit_dyadic_ratio_127(a2, &mo, &e);
-    a.am[r] = mo;
-    a.ak[r] = wsub(wadd(wadd(a.os_k, a.col_k), e), sh);
+    if (a.defer_fit) {
+      a.am[r] = a2;
+      a.ak[r] = wsub(wadd(a.os_k, a.col_k), sh);
+    } else {
+      i64 mo, e;
+      fit_dyadic_ratio_127(a2, &mo, &e);
+      a.am[r] = mo;
+      a.ak[r] = wsub(wadd(wadd(a.os_k, a.col_k), e), sh);
+    }
   }
 }
 
@@ -1433,12 +1455,15 @@ int detllm_residual_normq(const int32_t* P, int nsplit, int64_t split_stride, in
                           int64_t col_k, int tb, int32_t* h, int64_t* k_res, const int64_t* sm_m,
                           int64_t sm_k, int8_t* x8, int64_t* xm, int64_t* xk,
                           const int8_t* next_w, int next_n, int next_k, int next_ksplit,
-                          hipStream_t s) {
+                          int row_fit, hipStream_t s) {
   if (R <= 0) return DI_OK;
-  if (C <= 0 || nsplit < 1 || !P || !row_m || !row_k || !col_m || !h || !k_res) return DI_EINVAL;
+  if (C <= 0 || nsplit < 1 || !P || !row_m || !row_k || !col_m || !h || !k_res ||
+      (row_fit != 0 && row_fit != 1))
+    return DI_EINVAL;
   ResNormArgs a{};
   a.C = C; a.mode = 1; a.P = P; a.nsplit = nsplit; a.split_stride = split_stride;
-  a.row_m = row_m; a.row_k = row_k; a.col_m = col_m; a.col_k = col_k; a.tb = tb;
+  a.row_m = row_m; a.row_k = row_k; a.row_fit = row_fit;
+  a.col_m = col_m; a.col_k = col_k; a.tb = tb;
   a.h = h; a.k_res = k_res; a.sm_m = sm_m; a.sm_k = sm_k; a.x8 = x8; a.xm = xm; a.xk = xk;
   a.warm = warm_for(R, next_w, next_n, next_k, next_ksplit);
   DI_WARM_OR_ROWS(R, C, k_residual_add_normq, s, a);
@@ -1539,14 +1564,15 @@ int detllm_swiglu_quant(const int32_t* P, int nsplit, int64_t split_stride, int 
                         int64_t gate_k, const int64_t* up_m, int64_t up_k, const int64_t* ds_m,
                         int64_t ds_k, int8_t* y8, int64_t* ym, int64_t* yk,
                         const int8_t* next_w, int next_n, int next_k, int next_ksplit,
-                        hipStream_t s) {
+                        int defer_fit, hipStream_t s) {
   if (R <= 0) return DI_OK;
-  if (I <= 0 || nsplit < 1 || !P || !xm || !xk || !gate_m || !up_m || !ds_m || !y8 || !ym || !yk)
+  if (I <= 0 || nsplit < 1 || !P || !xm || !xk || !gate_m || !up_m || !ds_m || !y8 || !ym ||
+      !yk || (defer_fit != 0 && defer_fit != 1))
     return DI_EINVAL;
   SwigluArgs a{};
   a.I = I; a.P = P; a.nsplit = nsplit; a.split_stride = split_stride; a.xm = xm; a.xk = xk;
   a.gate_m = gate_m; a.gate_k = gate_k; a.up_m = up_m; a.up_k = up_k; a.ds_m = ds_m;
-  a.ds_k = ds_k; a.y8 = y8; a.ym = ym; a.yk = yk;
+  a.ds_k = ds_k; a.y8 = y8; a.ym = ym; a.yk = yk; a.defer_fit = defer_fit;
   a.warm = warm_for(R, next_w, next_n, next_k, next_ksplit);
   DI_WARM_OR_ROWS(R, I, k_swiglu_quant, s, a);
   DI_LAUNCH_CHECK();
@@ -1556,12 +1582,15 @@ int detllm_swiglu_quant(const int32_t* P, int nsplit, int64_t split_stride, int 
 int detllm_merge_rowcol(const int64_t* attn, int nsplit, int64_t split_stride, int R, int C,
                         const int64_t* os_m, int64_t os_k, const int64_t* col_m, int64_t col_k,
                         int8_t* a8, int64_t* am, int64_t* ak, const int8_t* next_w,
-                        int next_n, int next_k, int next_ksplit, hipStream_t s) {
+                        int next_n, int next_k, int next_ksplit, int defer_fit, hipStream_t s) {
   if (R <= 0) return DI_OK;
-  if (C <= 0 || nsplit < 1 || !attn || !os_m || !col_m || !a8 || !am || !ak) return DI_EINVAL;
+  if (C <= 0 || nsplit < 1 || !attn || !os_m || !col_m || !a8 || !am || !ak ||
+      (defer_fit != 0 && defer_fit != 1))
+    return DI_EINVAL;
   MergeArgs a{};
   a.C = C; a.attn = attn; a.nsplit = nsplit; a.split_stride = split_stride; a.os_m = os_m;
   a.os_k = os_k; a.col_m = col_m; a.col_k = col_k; a.a8 = a8; a.am = am; a.ak = ak;
+  a.defer_fit = defer_fit;
   a.warm = warm_for(R, next_w, next_n, next_k, next_ksplit);
   DI_WARM_OR_ROWS(R, C, k_merge_rowcol, s, a);
   DI_LAUNCH_CHECK();

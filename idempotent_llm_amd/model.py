@@ -469,12 +469,12 @@ class IntQwen3:
                  xm, xk, L.pf_mlp, L.pf_mlp.numel() * 8, None, 0)
             cur = 1 - cur
             call("detllm_swiglu_quant", Pg, nsg, stg, R, I_, xm, xk, L.gate_m, L.gate_k, L.up_m,
-                 L.up_k, L.ds_m, L.ds_k, y8, ym, yk, *self._next_gemm(L.wd, R))
+                 L.up_k, L.ds_m, L.ds_k, y8, ym, yk, *self._next_gemm(L.wd, R), 0)
             Pd, nsd, std = self._gemm(y8, L.wd, (L.down_m,) if nxt is None else
                                       (L.down_m, nxt.as_m))
             if nxt is None:
                 call("detllm_residual_normq", Pd, nsd, std, R, H, ym, yk, L.down_m, L.down_k, 20,
-                     hb[cur], kb[cur], None, 0, x8, xm, xk, None, 0, 0, 0)
+                     hb[cur], kb[cur], None, 0, x8, xm, xk, None, 0, 0, 0, 0)
                 break
             N = nxt.wqkv.shape[0]
             P, ns, st = self._partials(R, N, H)
@@ -571,21 +571,24 @@ class IntQwen3:
         a8 = torch.empty(R, nq * hd, dtype=torch.int8, device=dev)
         am = torch.empty(R, dtype=I64, device=dev)
         ak = torch.empty(R, dtype=I64, device=dev)
+        # decode sizes: the merge and the SwiGLU leave their scale fits to the
+        # residual kernel after the next GEMM (same integers)
+        dfit = 1 if R <= 64 else 0
         call("detllm_merge_rowcol", *attn, R, nq * hd, L.os_m, L.os_k, L.attn_out_col_m,
-             L.attn_out_col_k, a8, am, ak, *self._next_gemm(L.wo, R))
+             L.attn_out_col_k, a8, am, ak, *self._next_gemm(L.wo, R), dfit)
         P, ns, st = self._gemm(a8, L.wo, (L.pf_o,))
         call("detllm_residual_normq", P, ns, st, R, H, am, ak, L.o_m, L.o_k, 20, h, k_res,
-             L.ms_m, L.ms_k, x8, xm, xk, *self._next_gemm(L.wgu, R))
+             L.ms_m, L.ms_k, x8, xm, xk, *self._next_gemm(L.wgu, R), dfit)
         P, ns, st = self._gemm(x8, L.wgu, (L.pf_mlp,))
         y8 = torch.empty(R, I_, dtype=torch.int8, device=dev)
         ym = torch.empty(R, dtype=I64, device=dev)
         yk = torch.empty(R, dtype=I64, device=dev)
         call("detllm_swiglu_quant", P, ns, st, R, I_, xm, xk, L.gate_m, L.gate_k, L.up_m,
-             L.up_k, L.ds_m, L.ds_k, y8, ym, yk, *self._next_gemm(L.wd, R))
+             L.up_k, L.ds_m, L.ds_k, y8, ym, yk, *self._next_gemm(L.wd, R), dfit)
         P, ns, st = self._gemm(y8, L.wd, (L.down_m,) if nxt is None else (L.down_m, nxt.as_m))
         sm_m, sm_k = (nxt.as_m, nxt.as_k) if nxt is not None else (None, 0)
         call("detllm_residual_normq", P, ns, st, R, H, ym, yk, L.down_m, L.down_k, 20, h, k_res,
-             sm_m, sm_k, x8, xm, xk, *self._next_gemm(None if nxt is None else nxt.wqkv, R))
+             sm_m, sm_k, x8, xm, xk, *self._next_gemm(None if nxt is None else nxt.wqkv, R), dfit)
 
     # -- decoding (model.py:482-531) ------------------------------------------------
     def greedy_pick(self, logits_row: torch.Tensor) -> torch.Tensor:

@@ -150,7 +150,7 @@ def residual_normq(P: Tensor, row_m: Tensor, row_k: Tensor, col_m: Tensor, col_k
     ns, R, C = P.shape
     x8, xm, xk = _rows_out(R, C, P.device)
     call("detllm_residual_normq", P.contiguous(), ns, R * C, R, C, row_m, row_k, col_m, col_k, tb,
-         h, k_res, sm_m, sm_k, x8, xm, xk, None, 0, 0, 0)
+         h, k_res, sm_m, sm_k, x8, xm, xk, None, 0, 0, 0, 0)
     return x8, xm, xk
 
 
@@ -167,7 +167,7 @@ def swiglu_quant(P: Tensor, xm: Tensor, xk: Tensor, gate_m: Tensor, gate_k: int,
     ns, R, C2 = P.shape
     y8, ym, yk = _rows_out(R, C2 // 2, P.device)
     call("detllm_swiglu_quant", P.contiguous(), ns, R * C2, R, C2 // 2, xm, xk, gate_m, gate_k,
-         up_m, up_k, ds_m, ds_k, y8, ym, yk, None, 0, 0, 0)
+         up_m, up_k, ds_m, ds_k, y8, ym, yk, None, 0, 0, 0, 0)
     return y8, ym, yk
 
 
@@ -184,7 +184,7 @@ def merge_rowcol(attn: Tensor, os_m: Tensor, os_k: int, col_m: Tensor,
     R, C = attn.shape
     a8, am, ak = _rows_out(R, C, attn.device)
     call("detllm_merge_rowcol", attn.contiguous(), 1, 0, R, C, os_m, os_k, col_m, col_k, a8, am,
-         ak, None, 0, 0, 0)
+         ak, None, 0, 0, 0, 0)
     return a8, am, ak
 
 

@@ -121,7 +121,19 @@ int detllm_embed_normq(const int64_t* ids, int R, int C, int64_t vocab, const in
  * split. At decode sizes (R <= 64) the launch adds blocks that pull W's
  * slices into the L2 cache of the XCD whose GEMM blocks will read them. A
  * performance hint with no counterpart in the reference: results do not
- * depend on it; next_w null (and zeros) adds nothing. */
+ * depend on it; next_w null (and zeros) adds nothing.
+ *
+ * Deferred scale fit (the last argument before the stream). A producer of a
+ * GEMM operand (detllm_swiglu_quant, detllm_merge_rowcol) with defer_fit =
+ * 1 does not run the fit (m, e) = fit_dyadic_ratio(num, 127)
+ * (dyadic.py:52-72) that ends quant_i8_pertoken / requant_i8_rowcol
+ * (dyadic.py:104-105, :138-139): it stores num in place of m and the row's
+ * k without e in place of k. The consumer of that GEMM's partials
+ * (detllm_residual_normq with row_fit = 1) runs the fit, on every lane
+ * while its partials are in flight, instead of the producer's one lane at
+ * the end of its launch. The integers are the same either way. This is an
+ * order of operations with no counterpart in the reference; 0 stores and
+ * reads (m, k) as dyadic.py does. */
 
 /* requant_i32_common(P, row_m, row_k, col_m, col_k, tb) + residual_add +
  * _norm_quant(sm_m, sm_k) — model.py:410-415 / :424-427, :303, :284
@@ -132,7 +144,7 @@ int detllm_residual_normq(const int32_t* P, int nsplit, int64_t split_stride, in
                           int64_t col_k, int tb, int32_t* h, int64_t* k_res,
                           const int64_t* sm_m, int64_t sm_k, int8_t* x8, int64_t* xm,
                           int64_t* xk, const int8_t* next_w, int next_n, int next_k,
-                          int next_ksplit, hipStream_t s);
+                          int next_ksplit, int row_fit, hipStream_t s);
 
 /* Decode skinny GEMMs with the row kernel that makes their int8 operand
  * fused in (R <= 8 rows). Results equal the two launches they replace: the
@@ -180,7 +192,7 @@ int detllm_swiglu_quant(const int32_t* P, int nsplit, int64_t split_stride, int 
                         int64_t gate_k, const int64_t* up_m, int64_t up_k, const int64_t* ds_m,
                         int64_t ds_k, int8_t* y8, int64_t* ym, int64_t* yk,
                         const int8_t* next_w, int next_n, int next_k, int next_ksplit,
-                        hipStream_t s);
+                        int defer_fit, hipStream_t s);
 
 /* Attention-output merge: requant_i8_rowcol(attn * os_m, 1, os_k, col_m,
  * col_k) — model.py:404-409 (dyadic.py:123-139). attn: [nsplit][R][C] int64
@@ -188,7 +200,8 @@ int detllm_swiglu_quant(const int32_t* P, int nsplit, int64_t split_stride, int 
 int detllm_merge_rowcol(const int64_t* attn, int nsplit, int64_t split_stride, int R, int C,
                         const int64_t* os_m, int64_t os_k, const int64_t* col_m, int64_t col_k,
                         int8_t* a8, int64_t* am, int64_t* ak, const int8_t* next_w,
-                        int next_n, int next_k, int next_ksplit, hipStream_t s);
+                        int next_n, int next_k, int next_ksplit, int defer_fit,
+                        hipStream_t s);
 
 /* The KV cache is paged. Per layer, a K pool [n_pages][n_kv][128][128] (a
  * page's K rows: n_kv heads x 128 slots x 128 channels) and a V pool

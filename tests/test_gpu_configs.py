@@ -81,11 +81,11 @@ def test_c1_mlp_block_2048_tokens():
     ymg = torch.empty(T, dtype=I64, device="cuda")
     ykg = torch.empty(T, dtype=I64, device="cuda")
     call("detllm_swiglu_quant", P, 1, 0, T, I, xmg, xkg, g(gm), 20, g(um), 20, g(ones_i), 0,
-         y8g, ymg, ykg, None, 0, 0, 0)
+         y8g, ymg, ykg, None, 0, 0, 0, 0)
     eq(y8g, y8, "y8"); eq(ymg, y8m[:, 0], "ym"); eq(ykg, y8k[:, 0], "yk")
     Pd = gemm_nt(y8g, g(Wd.T.copy()))
     call("detllm_residual_normq", Pd, 1, 0, T, H, ymg, ykg, g(dm), 20, 20, hg, kg, None, 0,
-         None, None, None, None, 0, 0, 0)
+         None, None, None, None, 0, 0, 0, 0)
     eq(hg, h_out, "h"); eq(kg, k_out[:, 0], "k_res")
 
 

@@ -86,7 +86,7 @@ def test_igemv_resnormq_equals_two_launches(R, N, K, nsplit, smooth):
     xm = torch.empty(R, dtype=torch.int64, device="cuda")
     xk = torch.empty(R, dtype=torch.int64, device="cuda")
     call("detllm_residual_normq", Pg, nsplit, R * K, R, K, row_m, row_k, col_m, 20, 20, h_ref,
-         k_ref, sm_m, 15, x8, xm, xk, None, 0, 0, 0)
+         k_ref, sm_m, 15, x8, xm, xk, None, 0, 0, 0, 0)
     want = _split_product(x8, w, ks)
     # fused, twice in a row (the second call must not see the first's outputs)
     h_in = g(h)
@@ -132,7 +132,7 @@ def test_igemv_merge_equals_two_launches(R, N, K, nsplit, combined):
     a8 = torch.empty(R, K, dtype=torch.int8, device="cuda")
     am = torch.empty(R, dtype=torch.int64, device="cuda")
     ak = torch.empty(R, dtype=torch.int64, device="cuda")
-    call("detllm_merge_rowcol", ag, nsplit, R * K, R, K, g(os_m), 7, g(col_m), 9, a8, am, ak, None, 0, 0, 0)
+    call("detllm_merge_rowcol", ag, nsplit, R * K, R, K, g(os_m), 7, g(col_m), 9, a8, am, ak, None, 0, 0, 0, 0)
     want = _split_product(a8, w, ks)
     if combined:
         f_os, f_col = g(os_m * col_m), None

@@ -380,7 +380,7 @@ def test_residual_normq_renorm_branches(C, smooth):
     xm = torch.empty(R, dtype=torch.int64, device="cuda")
     xk = torch.empty(R, dtype=torch.int64, device="cuda")
     call("detllm_residual_normq", g(P), 1, 0, R, C, g(row_m), g(row_k), g(col_m), 20, 20, hg,
-         kg, g(sm_m) if smooth else None, 15, x8, xm, xk, None, 0, 0, 0)
+         kg, g(sm_m) if smooth else None, 15, x8, xm, xk, None, 0, 0, 0, 0)
     for got, w in zip((hg, kg, x8, xm, xk), want):
         eq(got, w)
     # the rows do take the branches named above
@@ -467,7 +467,7 @@ def test_merge_rowcol_extreme_rows():
         am = torch.empty(R, dtype=torch.int64, device="cuda")
         ak = torch.empty(R, dtype=torch.int64, device="cuda")
         call("detllm_merge_rowcol", g(np.ascontiguousarray(attn_r[None])), 1, R * C, R, C,
-             g(fac_r), 7, g(np.ones(C, I64)), 9, a8, am, ak, None, 0, 0, 0)
+             g(fac_r), 7, g(np.ones(C, I64)), 9, a8, am, ak, None, 0, 0, 0, 0)
         wy, wm, wk = ody.requant_i8_rowcol(v_r, np.ones((R, 1), I64), np.full((R, 1), 7, I64),
                                            np.ones(C, I64), 9)
         np.testing.assert_array_equal(a8.cpu().numpy(), wy)
@@ -500,3 +500,83 @@ def test_quant_i8_pertoken_extreme_rows():
         got = dd.quant_i8_pertoken(g(x), g(m), g(k))
         for a, b in zip(got, want):
             np.testing.assert_array_equal(a.cpu().numpy(), b)
+
+
+def test_deferred_scale_fit():
+    """detllm_merge_rowcol / detllm_swiglu_quant with defer_fit = 1 store
+    (num, k without e) in place of (m, k), where (m, e) = fit_dyadic_ratio(num,
+    127) (dyadic.py:52-72); detllm_residual_normq with row_fit = 1 finishes
+    that fit. Each producer's int8 rows equal the undeferred launch's, its
+    stored pair fits (by the oracle) to the undeferred (m, k), and the
+    consumer's residual, int8 operand and scales equal the undeferred
+    chain's bit for bit. Flags other than 0 and 1 are refused."""
+    from idempotent_llm_amd._lib import call
+    print("[deferred scale fit]", flush=True)
+    rng = np.random.default_rng(91)
+    R, C, H, I = 8, 2048, 1024, 3072
+
+    def residual(P, rm, rk, fit):
+        h = g(rng_h.copy())
+        kr = g(np.full(R, 24, I64))
+        x8 = torch.empty(R, H, dtype=torch.int8, device="cuda")
+        xm = torch.empty(R, dtype=torch.int64, device="cuda")
+        xk = torch.empty(R, dtype=torch.int64, device="cuda")
+        call("detllm_residual_normq", P, 1, 0, R, H, rm, rk, col_m, 20, 20, h, kr, sm_m, 15,
+             x8, xm, xk, None, 0, 0, 0, fit)
+        return [t.cpu().numpy() for t in (h, kr, x8, xm, xk)]
+
+    def fits_to(num, k_def, m_ref, k_ref):
+        m, e = ody.fit_dyadic_ratio(num.cpu().numpy(), 127)
+        np.testing.assert_array_equal(np.asarray(m).reshape(-1), m_ref.cpu().numpy())
+        np.testing.assert_array_equal(k_def.cpu().numpy() + np.asarray(e).reshape(-1),
+                                      k_ref.cpu().numpy())
+
+    rng_h = rng.integers(-(1 << 29), 1 << 29, (R, H)).astype(np.int32)
+    col_m = g(rng.integers(1 << 15, 1 << 16, H).astype(I64))
+    sm_m = g(rng.integers(1 << 15, 1 << 16, H).astype(I64))
+    P_o = g(rng.integers(-(1 << 19), 1 << 19, (1, R, H)).astype(np.int32))
+    # merge -> (o GEMM partials) -> residual
+    mags = [1 << 20, 1 << 26, 1 << 5, 0, 1 << 23, 1 << 29, 1 << 12, 1 << 27]
+    attn = np.stack([rng.integers(-m, m + 1, C) if m else np.zeros(C, I64) for m in mags])
+    os_m = g(rng.integers(1 << 10, 1 << 12, C).astype(I64))
+    cm = g(rng.integers(1 << 10, 1 << 12, C).astype(I64))
+    outs = []
+    for d in (0, 1):
+        a8 = torch.empty(R, C, dtype=torch.int8, device="cuda")
+        am = torch.empty(R, dtype=torch.int64, device="cuda")
+        ak = torch.empty(R, dtype=torch.int64, device="cuda")
+        call("detllm_merge_rowcol", g(attn[None]), 1, R * C, R, C, os_m, 7, cm, 9, a8, am, ak,
+             None, 0, 0, 0, d)
+        outs.append((a8, am, ak))
+    assert torch.equal(outs[0][0], outs[1][0])
+    fits_to(outs[1][1], outs[1][2], outs[0][1], outs[0][2])
+    for u, v in zip(residual(P_o, outs[0][1], outs[0][2], 0),
+                    residual(P_o, outs[1][1], outs[1][2], 1)):
+        np.testing.assert_array_equal(u, v)
+    # swiglu -> (down GEMM partials) -> residual
+    P_gu = g(rng.integers(-(1 << 20), 1 << 20, (1, R, 2 * I)).astype(np.int32))
+    xm = g(rng.integers(1 << 15, 1 << 16, R).astype(I64))
+    xk = g(np.full(R, 20, I64))
+    gm = g(rng.integers(1 << 14, 1 << 16, I).astype(I64))
+    um = g(rng.integers(1 << 14, 1 << 16, I).astype(I64))
+    dsm = g(rng.integers(1 << 14, 1 << 16, I).astype(I64))
+    outs = []
+    for d in (0, 1):
+        y8 = torch.empty(R, I, dtype=torch.int8, device="cuda")
+        ym = torch.empty(R, dtype=torch.int64, device="cuda")
+        yk = torch.empty(R, dtype=torch.int64, device="cuda")
+        call("detllm_swiglu_quant", P_gu, 1, R * 2 * I, R, I, xm, xk, gm, 20, um, 20, dsm, 15,
+             y8, ym, yk, None, 0, 0, 0, d)
+        outs.append((y8, ym, yk))
+    assert torch.equal(outs[0][0], outs[1][0])
+    fits_to(outs[1][1], outs[1][2], outs[0][1], outs[0][2])
+    for u, v in zip(residual(P_o, outs[0][1], outs[0][2], 0),
+                    residual(P_o, outs[1][1], outs[1][2], 1)):
+        np.testing.assert_array_equal(u, v)
+    # flags other than 0 / 1
+    with pytest.raises(RuntimeError, match="code -22"):
+        call("detllm_merge_rowcol", g(attn[None]), 1, R * C, R, C, os_m, 7, cm, 9,
+             outs[0][0][:, :1].contiguous(), outs[0][1], outs[0][2], None, 0, 0, 0, 2)
+    with pytest.raises(RuntimeError, match="code -22"):
+        residual(P_o, outs[0][1], outs[0][2], 2)
+    torch.cuda.synchronize()
