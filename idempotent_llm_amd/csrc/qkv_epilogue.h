@@ -331,13 +331,21 @@ __device__ __forceinline__ void qkv_head_compute(const QKVArgs& a, int r, int sl
   const i64 qkk = 20 + a.q_norm_k + a.qs_k;
   i64 m, k;
   norm_scale(1, qkk, &m, &k);
-  const i64 am = imax(wave_max(imax(wabs(q0), wabs(q1))), 1);
+  // the head's maximum of |q| as an unsigned value, as in quant_row: a
+  // q of INT64_MIN (|q| wraps to itself, skipped by dyadic.py's maximum)
+  // reads 2^63 and takes the exact path, which recomputes the maximum
+  constexpr u64 top = (u64)1 << 63;
+  const u64 amu =
+      (u64)wave_max((i64)(::max((u64)wabs(q0), (u64)wabs(q1)) ^ top)) ^ top;
   const i64 qrow = (((i64)b * a.n_q + h) * a.T + t);
-  if (DI_LIKELY(am < ((i64)1 << 43))) {  // as in quant_row: no 127 q wraps, 255 am < 2^51
+  i64 am;
+  if (DI_LIKELY(amu < ((u64)1 << 43))) {  // as in quant_row: no 127 q wraps, 255 am < 2^51
+    am = imax((i64)amu, 1);
     const DivEst D = make_divest(am, 127.0);
     q8_out[c0] = (int8_t)rhad_est_signed(q0, D);
     q8_out[c1] = (int8_t)rhad_est_signed(q1, D);
   } else {
+    am = DI_UNLIKELY(amu >> 63) ? imax(wave_max(imax(wabs(q0), wabs(q1))), 1) : (i64)amu;
     const Recip R = make_recip(am);
     q8_out[c0] = (int8_t)clamp_i8(rhad_r(wmul(q0, 127), R));
     q8_out[c1] = (int8_t)clamp_i8(rhad_r(wmul(q1, 127), R));
@@ -561,23 +569,35 @@ __device__ __forceinline__ void qkv_rows4(const QKVArgs& a, int R, int r0, int s
     return;
   }
   // Q: QK smoothing (model.py:317-320) then quant_i8_pertoken (model.py:322-323)
-  i64 q[8], amx = 0;
+  i64 q[8];
+  u64 amx = 0;  // unsigned: a q of INT64_MIN reads 2^63 (see the one-token form)
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     q[i] = wmul(rv[i], a.qs_m[kvh * 128 + c[i]]);
-    amx = imax(amx, wabs(q[i]));
+    amx = ::max(amx, (u64)wabs(q[i]));
   }
   const i64 qkk = 20 + a.q_norm_k + a.qs_k;
   i64 m, k;
   norm_scale(1, qkk, &m, &k);
-  const i64 am = imax(row16_max64(amx), 1);
+  constexpr u64 top = (u64)1 << 63;
+  const u64 amu = (u64)row16_max64((i64)(amx ^ top)) ^ top;
   const i64 qrow = ((i64)b * a.n_q + h) * a.T + t;
   uint32_t w[2] = {0, 0};
-  if (DI_LIKELY(am < ((i64)1 << 43))) {  // as in quant_row: no 127 q wraps, 255 am < 2^51
+  i64 am;
+  if (DI_LIKELY(amu < ((u64)1 << 43))) {  // as in quant_row: no 127 q wraps, 255 am < 2^51
+    am = imax((i64)amu, 1);
     const DivEst D = make_divest(am, 127.0);
 #pragma unroll
     for (int i = 0; i < 8; ++i) w[i >> 2] |= (uint32_t)(uint8_t)(int8_t)rhad_est_signed(q[i], D) << (8 * (i & 3));
   } else {
+    if (DI_UNLIKELY(amu >> 63)) {  // uniform over the row's 16 lanes
+      i64 sx = 0;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) sx = imax(sx, wabs(q[i]));
+      am = imax(row16_max64(sx), 1);
+    } else {
+      am = (i64)amu;
+    }
     const Recip Rr = make_recip(am);
 #pragma unroll
     for (int i = 0; i < 8; ++i)

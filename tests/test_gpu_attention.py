@@ -388,3 +388,58 @@ def test_prefill_epilogue_kq_estimates(T):
     for a, b in zip(*outs):
         assert torch.equal(a, b)
     assert outs[0][2].abs().sum().item() > 0
+
+
+@pytest.mark.parametrize("B,T", [(4, 1), (1, 100)])
+def test_qkv_epilogue_q_int64_min(B, T):
+    """Q quantisation (model.py:317-323: QK smoothing, then quant_i8_pertoken)
+    on heads holding a q of exactly INT64_MIN: QK smoothing scale 2^62 on
+    channel 0 of every kv head, 1 elsewhere, so channel 0's q = r * 2^62
+    wraps to 0, +-2^62 or INT64_MIN while the other channels stay below
+    2^43. dyadic.py's head maximum skips the wrapped |INT64_MIN|, so such a
+    head's quotients must come from the exact path. The q8 of both the
+    one-token (B, T = 1) and the rows (R > 64) layouts against the oracle's
+    composition of the same steps (oracle/model.py _qk_head_pipeline)."""
+    from idempotent_llm_amd._lib import call
+    from oracle import dyadic as ody, ops as oops
+    print(f"[qkv epilogue q INT64_MIN B={B} T={T}]", flush=True)
+    dims = art.MID
+    prm = _layer_params(dims, 4)
+    nq, nkv, hd = dims["n_q_heads"], dims["n_kv_heads"], 128
+    rnd = torch.Generator().manual_seed(40 + T)
+    P = torch.randint(-(1 << 19), 1 << 19, (1, B * T, (nq + 2 * nkv) * hd), generator=rnd,
+                      dtype=torch.int32).cuda()
+    xm = torch.randint(1 << 15, 1 << 16, (B * T,), generator=rnd, dtype=I64).cuda()
+    xk = torch.randint(22, 30, (B * T,), generator=rnd, dtype=I64).cuda()
+    pos = torch.randint(0, dims["max_pos"], (B * T,), generator=rnd, dtype=I64).cuda()
+    qs = np.ones((nkv, hd), np.int64)
+    qs[:, 0] = 1 << 62
+    qs_m = torch.from_numpy(qs.reshape(-1)).cuda()
+    common = (prm["q_m"], prm["q_k"], prm["k_m"], prm["k_k"], prm["v_m"], prm["v_k"],
+              prm["q_norm_m"], prm["q_norm_k"], prm["k_norm_m"], prm["k_norm_k"], qs_m,
+              prm["qs_k"], prm["kq_m"], prm["kq_k"], prm["ks_m"], prm["ks_k"], prm["vq_m"],
+              prm["vq_k"], prm["cos"], prm["sin"], prm["cos"].shape[0])
+    q8 = torch.empty(B, nq, T, hd, dtype=torch.int8, device="cuda")
+    tpos = torch.empty(B, nq, T, dtype=I64, device="cuda")
+    kc, vc, table, width = paged(torch.zeros(B, nkv, 256, hd, dtype=torch.int8),
+                                 torch.zeros(B, nkv, hd, 256, dtype=torch.int8), seed=T)
+    call("detllm_qkv_epilogue", P, 1, B * T * P.shape[2], B, T, nq, nkv, xm, xk, pos, *common,
+         q8, tpos, None, kc, vc, table, width, None, 0, None, None)
+    torch.cuda.synchronize()
+    # the oracle's Q steps on the same inputs
+    n = lambda t: t.cpu().numpy()
+    Pq = n(P)[0][:, :nq * hd].astype(np.int64).reshape(B, T, nq, hd)
+    y, _, _ = ody.requant_i32_common(Pq, n(xm).reshape(B, T, 1, 1), n(xk).reshape(B, T, 1, 1),
+                                     n(prm["q_m"]).reshape(nq, hd), prm["q_k"], target_bits=16)
+    yn, qkk = oops.di_rmsnorm_gamma(y, n(prm["q_norm_m"]), prm["q_norm_k"])
+    yn = yn.transpose(0, 2, 1, 3)
+    pb = np.broadcast_to(n(pos).reshape(B, 1, T), (B, nq, T))
+    yr = oops.apply_int_rope(yn, n(prm["cos"]), n(prm["sin"]), pb)
+    with np.errstate(over="ignore"):
+        q = yr * np.repeat(qs, nq // nkv, axis=0)[None, :, None, :]
+    one = np.ones((B, nq, T, 1), np.int64)
+    want, _, _ = ody.quant_i8_pertoken(q, one, np.zeros_like(one) + qkk + prm["qs_k"])
+    hit = (q == np.iinfo(np.int64).min).any(axis=-1)
+    small = (np.abs(np.where(q == np.iinfo(np.int64).min, 0, q)).max(axis=-1) < (1 << 43))
+    assert (hit & small).any()      # some heads take INT64_MIN with a maximum below 2^43
+    np.testing.assert_array_equal(n(q8), want)
