@@ -43,6 +43,16 @@
 #define DI_LIKELY(x) __builtin_expect(!!(x), 1)
 #define DI_UNLIKELY(x) __builtin_expect(!!(x), 0)
 
+// Precondition checks of the fast forms, active in the CPU build that the
+// tests run (intops_host.cpp): a violated bound aborts there. Device code
+// and the host pass of the HIP library compile them away.
+#if defined(__HIPCC__) || defined(__HIP__)
+#define DI_HOST_CHECK(x) ((void)0)
+#else
+#include <stdlib.h>
+#define DI_HOST_CHECK(x) ((x) ? (void)0 : abort())
+#endif
+
 typedef int64_t i64;
 typedef uint64_t u64;
 
@@ -200,10 +210,11 @@ DI_HD void fit_dyadic_ratio(i64 num, i64 den, i64* m_out, i64* e_out) {
 }
 
 // fit_dyadic_ratio(num, 127): every requantisation to int8 fits its output
-// scale against 127. Same integer as the generic routine; the divisions by
-// 127 * 2^s use the constant reciprocal floor((2^64 - 1) / 127) whenever no
-// operand of the generic path wraps (num < 2^56, shifts below 56), else the
-// generic path runs.
+// scale against 127. Same integer as the generic routine. For 0 < num < 2^56
+// the divisions by 127 * 2^s go through srd127 / floor_div127 below (one fp64
+// fma each), whose dividends stay below 2^24 for the exponents this routine
+// tries (e = 21 - ilog2(num), then one step of +-1); any other num takes the
+// generic integer path.
 // floor(y / 127) for 0 <= y < 2^32 from one fp64 fma: y / 127 has a
 // fractional part that is a multiple of 1/127 (0, or between 1/127 and
 // 126/127), and fma(y, fl(1/127), 2^-12) lies within 2^-19 of
@@ -215,14 +226,23 @@ DI_HD uint32_t floor_div127(uint32_t y) {
 }
 
 DI_HD i64 srd127(i64 num, i64 e) {
-  // scaled_round_div(num, 127, e) for 0 < num < 2^56 when the quotient is
-  // below 2^17 (the callers fit a 16-bit mantissa): rhad(x, 127 * 2^s) =
+  // scaled_round_div(num, 127, e), valid ONLY for the (num, e) pairs that
+  // fit_dyadic_ratio_127 passes: 0 < num < 2^56 and e = 21 - ilog2(num) or
+  // one step from it, so num * 2^e < 2^23. Then rhad(x, 127 * 2^s) =
   // floor(floor((x + h) / 2^s) / 127) with h = floor(127 * 2^s / 2), and
-  // rhad(x, 127) = floor((x + 63) / 127); either dividend is below 2^24.
-  if (e >= 0) return (i64)floor_div127((uint32_t)(((u64)num << e) + 63));
-  const int s = (int)(-e);
-  const u64 h = (127ull << s) >> 1;
-  return (i64)floor_div127((uint32_t)(((u64)num + h) >> s));
+  // rhad(x, 127) = floor((x + 63) / 127); either dividend is below 2^24
+  // (the uint32_t cast below would truncate a larger one, and floor_div127
+  // is proven for dividends below 2^32 only).
+  u64 y;
+  if (e >= 0) {
+    y = ((u64)num << e) + 63;
+  } else {
+    const int s = (int)(-e);
+    const u64 h = (127ull << s) >> 1;
+    y = ((u64)num + h) >> s;
+  }
+  DI_HOST_CHECK(y < (1ull << 24));
+  return (i64)floor_div127((uint32_t)y);
 }
 
 DI_HD void fit_dyadic_ratio_127(i64 num, i64* m_out, i64* e_out) {

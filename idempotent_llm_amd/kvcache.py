@@ -30,6 +30,13 @@ import torch
 PAGE = 128   # slots per page (csrc/common.h DI_PAGE)
 
 
+class CacheRowsMismatch(RuntimeError, ValueError):
+    """A batch whose row count differs from the rows the cache holds. The
+    reference fails the same call in ``torch.cat([cache.valid, chunk_valid])``
+    (a RuntimeError); here the check runs on the host before any kernel
+    would index the page tables past their rows."""
+
+
 class KVCache:
     def __init__(self):
         self.k_pools: list = []     # per layer [n_pages, n_kv, PAGE, hd] int8
@@ -140,7 +147,15 @@ class KVCache:
             self.table.copy_(torch.from_numpy(self._table_host))
         self.mapped = need_w * PAGE
 
+    def check_rows(self, B: int):
+        """Raise CacheRowsMismatch unless the cache is empty or holds B rows."""
+        if self._table_host is not None and self._table_host.shape[0] != B:
+            raise CacheRowsMismatch(
+                f"a batch of {B} rows cannot use a KV cache of "
+                f"{self._table_host.shape[0]} rows")
+
     def _init(self, model, B: int):
+        self.check_rows(B)
         if self._dims is None:
             self._dims = (model.n_layers, model.n_kv, model.hd, model.device)
             self._ensure_width(B, 1)

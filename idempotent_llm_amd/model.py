@@ -91,6 +91,41 @@ class LayerWeights:
     # int64 (detllm_kq_est): layer constants computed once at load
     kq_est: torch.Tensor | None = None
 
+    # the reference's field names (model.py:41-64) as views of the kernel
+    # layout, for code written against the reference class (seam overrides)
+    @property
+    def q_w8t(self) -> torch.Tensor:
+        return self.wqkv[:self.q_m.numel()].t()
+
+    @property
+    def k_w8t(self) -> torch.Tensor:
+        nq = self.q_m.numel()
+        return self.wqkv[nq:nq + self.k_m.numel()].t()
+
+    @property
+    def v_w8t(self) -> torch.Tensor:
+        return self.wqkv[self.q_m.numel() + self.k_m.numel():].t()
+
+    @property
+    def o_w8t(self) -> torch.Tensor:
+        return self.wo.t()
+
+    @property
+    def gate_w8t(self) -> torch.Tensor:
+        return self.wgu[:self.gate_m.numel()].t()
+
+    @property
+    def up_w8t(self) -> torch.Tensor:
+        return self.wgu[self.gate_m.numel():].t()
+
+    @property
+    def down_w8t(self) -> torch.Tensor:
+        return self.wd.t()
+
+    @property
+    def k_rowk(self) -> int:
+        return OUT_FRAC_BITS + self.k_norm_k
+
 
 def _pack(L: LayerWeights, names) -> torch.Tensor:
     """Move the named int64 tensors of L into one buffer (views keep their
@@ -196,6 +231,9 @@ class IntQwen3:
         # host (IndexError from embed_e8[ids] / cos_t[positions]); the
         # kernels OR bits into it, raise_if_device_error() reads it
         self._err = torch.zeros(1, dtype=torch.int32, device=dev)
+        # reference attributes (model.py:177-183) that seam overrides read
+        self._one1 = torch.ones(1, dtype=I64, device=dev)
+        self._layer_compiled = None
 
     def raise_if_device_error(self):
         """Synchronise on the error word and raise IndexError (as the
@@ -278,6 +316,7 @@ class IntQwen3:
         B, T = ids.shape
         if cache is None:
             cache = KVCache()
+        cache.check_rows(B)
         static = cache.static_cap > 0
         S_past = cache.length
         if static:
@@ -346,6 +385,28 @@ class IntQwen3:
         """Seam (model.py:476-478): 15-bit probabilities x int8 V, exact
         hi/lo split (backends.py:152-164)."""
         return int_gemm_u16i8(probs, V8r, self.backend)
+
+    def _norm_quant(self, h: torch.Tensor, k_res: torch.Tensor,
+                    sm_m: torch.Tensor | None = None, sm_k: int = 0):
+        """model.py:187-198 on the op kernels: RMSNorm (scale (1, 20)), the
+        optional smoothing multiply, per-token int8 quantisation. The layer
+        kernels fuse the same integers; this form serves code written
+        against the reference class."""
+        y = ops.di_rmsnorm(h)
+        kq = torch.full_like(k_res, OUT_FRAC_BITS)
+        if sm_m is not None:
+            y = y.to(I64) * sm_m
+            kq = kq + sm_k
+        return dy.quant_i8_pertoken(y, torch.ones_like(k_res), kq)
+
+    def enable_layer_compile(self):
+        """model.py:452-467 compiles the per-layer function with inductor;
+        every layer here is already a fixed sequence of hand-fused kernels,
+        so there is nothing to compile (kept for the same API)."""
+
+    def enable_layer_cudagraphs(self):
+        """model.py:434-450; see enable_layer_compile. The whole decode step
+        is one HIP graph (GraphedDecode)."""
 
     def _seams_overridden(self) -> bool:
         cls = type(self)
@@ -616,12 +677,6 @@ class IntQwen3:
         chunk_valid). Returns (tokens [B, max_new], step_logits list of [B, V])."""
         dev = self.device
         B, T0 = ids.shape
-        # the last decode step runs at position <= T0 + max_new - 2; the
-        # reference's cos_t[positions] raises IndexError there, so refuse up
-        # front rather than after max_pos steps
-        if T0 + max_new - 1 > self.max_pos:
-            raise IndexError(f"prompt of {T0} tokens + {max_new} new tokens reaches position "
-                             f"{T0 + max_new - 2}, outside the RoPE tables (size {self.max_pos})")
         self._check_host_indices(ids, torch.zeros(1, dtype=I64))
         ids = ids.to(dev)
         if chunk_valid is None:
@@ -629,6 +684,14 @@ class IntQwen3:
         chunk_valid = chunk_valid.to(dev)
         positions = torch.arange(T0, device=dev).expand(B, T0)
         lens = chunk_valid.sum(dim=1)
+        # prefill reads positions 0 .. T0 - 1 and decode step s (1 <= s <
+        # max_new) position lens + s - 1; the reference's cos_t[positions]
+        # raises IndexError at the first position >= max_pos, so refuse up
+        # front rather than after that many steps
+        last_pos = max(T0 - 1, int(lens.max()) + max_new - 2 if max_new > 1 else -1)
+        if last_pos >= self.max_pos:
+            raise IndexError(f"generation reaches position {last_pos}, outside the RoPE "
+                             f"tables (size {self.max_pos})")
         last = (lens - 1).clamp(min=0)
         # the cache is sized for the whole generation up front: decoding then
         # only maps pages (no reallocation, no copy, one graph capture)

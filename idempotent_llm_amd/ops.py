@@ -98,15 +98,21 @@ def apply_int_rope(x: torch.Tensor, cos_t: torch.Tensor, sin_t: torch.Tensor,
     return y
 
 
-def di_linear(x8: torch.Tensor, xm, xk, w8_t: torch.Tensor, wm, wk):
-    """ops/di_matmul.py:22-31: exact int8 GEMM, scales passed through."""
-    from .backends import int_gemm
+def di_linear(x8: torch.Tensor, xm, xk, w8_t: torch.Tensor, wm, wk, backend: str = "rocm"):
+    """ops/di_matmul.py:22-31: exact int8 GEMM (x8 [..., T, K] against
+    w8_t [K, N], shared over the leading dims: the reference expands it, a
+    2-D operand folds into the rows here, same integers), scales passed
+    through."""
+    from .backends import _require_rocm, canonical_backend, int_gemm
+    _require_rocm(canonical_backend(backend))
     return int_gemm(x8, w8_t, "rocm"), xm, xk, wm, wk
 
 
-def di_matmul(x: torch.Tensor, xm, xk, w8_t: torch.Tensor, wm, wk):
+def di_matmul(x: torch.Tensor, xm, xk, w8_t: torch.Tensor, wm, wk, backend: str = "rocm"):
     """ops/di_matmul.py:34-40: quantise per token, GEMM, requantise to int8."""
+    from .backends import _require_rocm, canonical_backend
     from .dyadic import quant_i8_pertoken, requant_i8_rowcol
+    _require_rocm(canonical_backend(backend))
     x8, qm, qk = quant_i8_pertoken(x, xm, xk)
     P, rm, rk, cm, ck = di_linear(x8, qm, qk, w8_t, wm, wk)
     return requant_i8_rowcol(P, rm, rk, cm, ck)

@@ -100,7 +100,7 @@ def test_plugin_routes_reference_api(tmp_path):
     plugin.install(pkg)
     try:
         m = pkg.model.IntQwen3(d, "rocm")
-        assert isinstance(m, RocmIntQwen3)
+        assert isinstance(m, RocmIntQwen3) and isinstance(m, pkg.model.IntQwen3)
         direct = RocmIntQwen3(d, "rocm")
         ids = torch.from_numpy(art.prompt_ids(110, 24, art.TINY["vocab"]))[None].cuda()
         pos = torch.arange(24, device="cuda")[None]
@@ -120,3 +120,94 @@ def test_plugin_routes_reference_api(tmp_path):
         m.raise_if_device_error()
     finally:
         plugin.uninstall(pkg)
+
+
+class _Dispatched(__import__("torch.utils._python_dispatch", fromlist=["x"]).TorchDispatchMode):
+    """Records the namespace of every operator dispatched while active."""
+
+    def __init__(self):
+        super().__init__()
+        self.namespaces = set()
+
+    def __torch_dispatch__(self, func, types, args=(), kwargs=None):
+        self.namespaces.add(getattr(func, "namespace", ""))
+        return func(*args, **(kwargs or {}))
+
+
+def test_plugin_reference_routes_reach_the_hip_kernels(tmp_path):
+    """Through the reference package's unchanged API (stand-in layout, see
+    test_plugin_cpu.py), with the plugin installed:
+    * ops.di_matmul(..., "rocm") (ops/di_matmul.py:34-40, which imports
+      int_gemm by name) equals the oracle's composition and dispatches none
+      of the reference package's operators;
+    * a subclass of the reference IntQwen3 overriding _lm_head with zeros
+      (a ZeroHead diagnostic) runs this runtime: zero logits at every step
+      of a graphed generation, greedy picks of id 0 (lowest-id tie-break);
+    * a seam override that calls super() and a reference primitive on the
+      device gets this runtime's bits, and the primitive runs this package's
+      HIP kernel instead of the reference's Triton kernel (its stand-in
+      counts launches: none while installed, one after uninstall)."""
+    import sys
+
+    from idempotent_llm_amd import plugin
+    from idempotent_llm_amd.model import IntQwen3 as RocmIntQwen3
+    from oracle import ops as oops
+    sys.path.insert(0, __import__("os").path.dirname(__file__))
+    from test_plugin_cpu import _standin
+    name = "detllm_standin_routes"
+    pkg = _standin(name)
+    state = pkg.ops.int_prims.STATE
+    d = str(tmp_path)
+    art.make_artifact(d, art.TINY, seed=11)
+    ids = torch.from_numpy(art.prompt_ids(110, 24, art.TINY["vocab"]))[None].cuda()
+    pos = torch.arange(24, device="cuda")[None]
+    plugin.install(pkg)
+    try:
+        rnd = np.random.default_rng(21)
+        x = rnd.integers(-(1 << 30), 1 << 30, (37, 256)).astype(np.int64)
+        xm = rnd.integers(1 << 15, 1 << 16, (37, 1)).astype(np.int64)
+        xk = rnd.integers(20, 40, (37, 1)).astype(np.int64)
+        w = rnd.integers(-127, 128, (256, 96)).astype(np.int8)
+        wm = rnd.integers(1 << 14, 1 << 16, (96,)).astype(np.int64)
+        cu = lambda a: torch.from_numpy(a).cuda()
+        with _Dispatched() as rec:
+            y8, m8, k8 = pkg.ops.di_matmul(cu(x), cu(xm), cu(xk), cu(w), cu(wm), 24, "rocm")
+        oy, om, ok = oops.di_matmul(x, xm, xk, w, wm, 24)
+        assert np.array_equal(y8.cpu().numpy(), oy)
+        assert np.array_equal(m8.cpu().numpy(), om) and np.array_equal(k8.cpu().numpy(), ok)
+        assert name not in rec.namespaces and "detllm_rocm" in rec.namespaces
+
+        class ZeroHead(pkg.model.IntQwen3):
+            def _lm_head(self, x8, xm, xk):
+                return torch.zeros(*x8.shape[:-1], self.vocab, dtype=torch.int32,
+                                   device=x8.device)
+
+        z = ZeroHead(d, "rocm")
+        assert isinstance(z, RocmIntQwen3) and isinstance(z, ZeroHead)
+        with _Dispatched() as rec:
+            lg = z.forward(ids, pos)[0]
+        assert name not in rec.namespaces
+        assert lg.shape == (1, 24, art.TINY["vocab"]) and not lg.any()
+        toks, steps = z.generate(ids, 5, use_graph=True)
+        assert toks.tolist() == [[0] * 5] and not any(s.any() for s in steps)
+
+        class Probe(pkg.model.IntQwen3):
+            calls = 0
+
+            def _attn_scores(self, q8, qm, qk, K8r, L, group, aux=None):
+                type(self).calls += 1
+                lg2 = pkg.ops.int_prims.ilog2_i64(qm.clamp(min=1))
+                want = [v.bit_length() - 1 for v in qm.clamp(min=1).reshape(-1).tolist()]
+                assert lg2.is_cuda and lg2.reshape(-1).tolist() == want
+                return super()._attn_scores(q8, qm, qk, K8r, L, group, aux)
+
+        probe = Probe(d, "rocm")
+        direct = RocmIntQwen3(d, "rocm")
+        assert torch.equal(probe.forward(ids, pos)[0], direct.forward(ids, pos)[0])
+        assert Probe.calls == art.TINY["n_layers"]
+        assert state.TRITON_CALLS == 0
+        probe.raise_if_device_error()
+    finally:
+        plugin.uninstall(pkg)
+    pkg.ops.int_prims.ilog2_i64(torch.ones(3, dtype=torch.int64, device="cuda"))
+    assert state.TRITON_CALLS == 1

@@ -232,6 +232,25 @@ def test_out_of_range_indices_raise_like_the_reference(case):
         m.forward(torch.tensor([[1]]), torch.tensor([[P]]))
     with pytest.raises(IndexError):
         m.generate(ids, P)                 # runs past the RoPE table
+    # right-padded rows decode at their own lengths (pos = lens + step - 1),
+    # so the last position is max(lens) + max_new - 2, not T0 + max_new - 2:
+    # a run ending at position P - 1 completes, one step more raises
+    ids2 = ids.expand(2, T).contiguous()
+    cv = torch.ones(2, T, dtype=torch.bool, device="cuda")
+    cv[0, T - 3:] = False
+    cv[1, T - 5:] = False
+    n_ok = P - (T - 3) + 1
+    toks, _ = m.generate(ids2, n_ok, chunk_valid=cv, use_graph=True)
+    assert toks.shape == (2, n_ok)
+    with pytest.raises(IndexError, match="position"):
+        m.generate(ids2, n_ok + 1, chunk_valid=cv, use_graph=True)
+    # a cache holds a fixed number of rows: another batch size is refused on
+    # the host before any kernel could index its page tables past their rows
+    _, _, _, cache = m.forward(ids2, pos.expand(2, T))
+    with pytest.raises(ValueError, match="rows"):
+        m.forward(ids.expand(3, T).contiguous(), pos.expand(3, T) + T, cache)
+    with pytest.raises(RuntimeError, match="rows"):
+        m.forward(ids[:, :1], pos[:, :1] + T, cache)
     # device tensors: flagged by the kernels, raised at the next check
     bad = ids.clone()
     bad[0, 3] = V + 5
