@@ -221,6 +221,17 @@ def calibration_maxima(model, calib_ids: torch.Tensor, device) -> dict:
     return acc
 
 
+# smoothing factors (activation and QK) are clamped to [1/SMOOTH_CLAMP,
+# SMOOTH_CLAMP] (prepare.py:297, :387)
+SMOOTH_CLAMP = 64.0
+
+
+def _relative(s: torch.Tensor) -> torch.Tensor:
+    """Activation smoothing keeps only the relative scale of its factors:
+    they are divided by their median (prepare.py:296)."""
+    return s / s.median()
+
+
 def _act_smoothing(act_max: torch.Tensor, weights: list, alpha: float = 0.5):
     """Analytic SmoothQuant factors for one linear-input site (prepare.py:
     285-302): s_c = amax_c^alpha / wmax_c^(1-alpha), normalised by the median,
@@ -229,7 +240,7 @@ def _act_smoothing(act_max: torch.Tensor, weights: list, alpha: float = 0.5):
     (inv_m int64, inv_k int, s used [C] float64)."""
     wmax = torch.stack([w.to(F64).abs().amax(dim=0) for w in weights]).amax(dim=0)
     s = act_max.to(F64).clamp(min=1e-5).pow(alpha) / wmax.clamp(min=1e-5).pow(1 - alpha)
-    s = (s / s.median()).clamp(1 / 64.0, 64.0)
+    s = _relative(s).clamp(1 / SMOOTH_CLAMP, SMOOTH_CLAMP)
     inv_m, inv_k, inv = _smooth_dyadic(1.0 / s)
     return inv_m, inv_k, 1.0 / inv
 
@@ -344,7 +355,7 @@ def prepare(out_dir: str, model, calib_ids, kv_margin: float = 1.05, device=None
         # scale is c_d sK_h with one base scale per kv head
         kc = mx["k"][i].to(F64).clamp(min=1e-6)
         qc = mx["q"][i].to(F64).clamp(min=1e-6)
-        c = (kc.pow(qk_alpha) / qc.pow(1 - qk_alpha)).clamp(1 / 64.0, 64.0)
+        c = (kc.pow(qk_alpha) / qc.pow(1 - qk_alpha)).clamp(1 / SMOOTH_CLAMP, SMOOTH_CLAMP)
         qs_m, qs_k, c_used = _smooth_dyadic(c)
         tensors[p + "qs_m"] = qs_m
         Lc["qs_k"] = qs_k

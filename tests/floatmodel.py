@@ -4,9 +4,12 @@ quantiser tests."""
 import torch
 
 
-def small_float_model(seed=0):
+def small_float_model(seed=0, outliers=False):
     """A 2-layer Qwen3 (hidden 256, 4/2 heads, vocab 1000) with random weights
-    and non-trivial norm gains and per-channel activation scales."""
+    and non-trivial norm gains and per-channel activation scales. outliers:
+    a few channels scaled up by orders of magnitude at every smoothing site
+    (the RMSNorm inputs, K after its norm, the inputs of o and down), so the
+    smoothing factors reach their clamp."""
     from transformers import Qwen3Config, Qwen3ForCausalLM
     torch.manual_seed(seed)
     cfg = Qwen3Config(vocab_size=1000, hidden_size=256, intermediate_size=512,
@@ -26,4 +29,13 @@ def small_float_model(seed=0):
                 lin.weight.mul_(3.0)
         m.model.norm.weight.mul_(1 + 0.3 * torch.randn_like(m.model.norm.weight))
         m.model.embed_tokens.weight.mul_(torch.exp(torch.randn(1, 256)))
+        if outliers:
+            m.model.embed_tokens.weight[:, :3].mul_(1e6)
+            for layer in m.model.layers:
+                layer.self_attn.k_norm.weight[:4].mul_(3e3)
+                layer.self_attn.q_norm.weight[4:6].mul_(3e3)
+                layer.self_attn.v_proj.weight[:2].mul_(1e4)
+                layer.mlp.up_proj.weight[:2].mul_(1e4)
+                layer.mlp.gate_proj.weight[:, 5:8].mul_(1e-4)
+                layer.mlp.up_proj.weight[:, 5:8].mul_(1e-4)
     return m

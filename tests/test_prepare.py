@@ -3,17 +3,18 @@ the reference's src/detllm/prepare.py):
 
 * the fitting helpers against vectors the reference's own helpers wrote
   (tests/golden/prepare_helpers.npz, make_prepare_golden.py) — exact;
-* a whole quantisation of a small random Qwen3 float model (transformers,
-  offline): the artifact has the runtime schema (names, dtypes, shapes and
-  config keys of the random-init generator), loads in the integer oracle, and
-  the integer model's logits track the float model's (a sign error, a dropped
-  gamma fold or a misapplied smoothing factor breaks the correlation).
+* the whole quantisation of a small random Qwen3 float model with fixed
+  calibration ids against the artifact the reference's prepare() wrote for
+  the same model and ids (tests/golden/prepare_artifact.json,
+  make_prepare_artifact.py): every tensor byte-identical (SHA-256, and the
+  values of the int64 scale tensors) and an equal config, with and without
+  smoothing; a planted change to the smoothing's median normalisation or to
+  its clamp fails that comparison;
+* the artifact has the runtime schema (names, dtypes, shapes and config keys
+  of the random-init generator), loads in the integer oracle, and the
+  integer model's logits track the float model's."""
 
-The calibration and smoothing formulas inside the reference's prepare() are
-not importable on their own and its end-to-end run needs a Hub tokenizer and
-a dataset: at bit level those parts are parity unpinned, and pinned instead
-by the float/integer agreement below."""
-
+import contextlib
 import json
 import os
 
@@ -21,6 +22,7 @@ import numpy as np
 import pytest
 import torch
 
+from artifact_record import describe, differences
 from floatmodel import small_float_model
 from idempotent_llm_amd import prepare as P
 
@@ -61,6 +63,62 @@ def test_embedding_and_gamma(G):
     assert np.array_equal(em.numpy(), G["em"]) and np.array_equal(ek.numpy(), G["ek"])
     gm, gk = P.fit_gamma_dyadic(torch.from_numpy(G["gamma"]))
     assert np.array_equal(gm.numpy(), G["gamma_m"]) and gk == int(G["gamma_k"])
+
+
+@pytest.fixture(scope="module")
+def ref_artifact():
+    with open(os.path.join(HERE, "golden", "prepare_artifact.json")) as f:
+        return json.load(f)
+
+
+@contextlib.contextmanager
+def _one_thread():
+    # the reference's artifact was written with one CPU thread: the float
+    # calibration pass then sums in the same order here
+    n = torch.get_num_threads()
+    torch.set_num_threads(1)
+    try:
+        yield
+    finally:
+        torch.set_num_threads(n)
+
+
+def _quantise(out_dir, rec):
+    calib = np.random.default_rng(5).integers(0, 1000, (4, 64), dtype=np.int64)
+    with _one_thread():
+        P.prepare(out_dir, small_float_model(seed=0, **rec["model_options"]), calib,
+                  device="cpu", model_id="test-small-qwen3", **rec["options"])
+    return describe(out_dir)
+
+
+@pytest.mark.parametrize("variant", ["default", "no_smoothing_qk_alpha_0p5",
+                                     "outlier_channels"])
+def test_artifact_identical_to_the_reference(ref_artifact, variant, tmp_path):
+    """prepare() writes the reference's artifact bit for bit (prepare.py:
+    120-434: calibration maxima, activation and QK smoothing, static K/V
+    scales, every fit)."""
+    want = ref_artifact["variants"][variant]
+    got = _quantise(str(tmp_path), want)
+    assert len(got["tensors"]) == len(want["tensors"]) == 61
+    assert differences(got, want) == []
+
+
+@pytest.mark.parametrize("plant", ["mean_normalisation", "clamp_32", "clamp_128"])
+def test_planted_smoothing_change_fails(ref_artifact, plant, tmp_path, monkeypatch):
+    """A plausible slip in the smoothing formulas (mean instead of median
+    normalisation, another clamp bound) changes the artifact: the comparison
+    above catches it (the outlier-channel model drives factors past the
+    clamp at every smoothing site)."""
+    if plant == "mean_normalisation":
+        monkeypatch.setattr(P, "_relative", lambda s: s / s.mean())
+    else:
+        monkeypatch.setattr(P, "SMOOTH_CLAMP", float(plant.split("_")[1]))
+    want = ref_artifact["variants"]["outlier_channels"]
+    diff = differences(_quantise(str(tmp_path), want), want)
+    sites = {d.rsplit(".", 1)[-1] for d in diff}
+    assert {"as_m", "ms_m", "ds_m", "os_m"} <= sites, diff
+    if plant != "mean_normalisation":          # QK smoothing shares the clamp
+        assert "qs_m" in sites, diff
 
 
 @pytest.fixture(scope="module")
