@@ -112,7 +112,12 @@ class IntQwen3Oracle:
         return yr, k_out
 
     # -- forward (model.py:220-286) -----------------------------------------
-    def forward(self, ids, positions, cache: OracleKV | None = None, chunk_valid=None):
+    def forward(self, ids, positions, cache: OracleKV | None = None, chunk_valid=None,
+                head_rows=None):
+        """model.py:220-286. head_rows (int [B], optional): the LM head only at
+        position head_rows[b] of each row, logits [B, vocab] (the final norm,
+        quantisation and head GEMM act row by row, so this is the same rows
+        the full [B, T, vocab] logits hold; generate() keeps only those)."""
         ids = np.asarray(ids, dtype=I64)
         positions = np.asarray(positions, dtype=I64)
         B, T = ids.shape
@@ -136,8 +141,13 @@ class IntQwen3Oracle:
         for li, L in enumerate(self.layers):
             h, k_res = self._layer(li, L, h, k_res, mask, positions, cache, S_past, S)
         cache.length = S
+        if head_rows is not None:
+            sel = (np.arange(B), np.asarray(head_rows, dtype=I64))
+            h, k_res = h[sel][:, None], k_res[sel][:, None]
         x8, xm, xk = self._norm_quant(h, k_res)
         logits = self._gemm_w(x8, "head", self.head_w8t)
+        if head_rows is not None:
+            return logits[:, 0], xm[:, 0], xk[:, 0], cache
         return logits, xm, xk, cache
 
     def _layer(self, li, L, h, k_res, mask, positions, cache, S_past, S):

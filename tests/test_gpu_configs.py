@@ -12,6 +12,7 @@ import pytest
 import torch
 
 from idempotent_llm_amd import artifact as art
+from idempotent_llm_amd.hashchain import chain_hashes
 from oracle import dyadic as ody
 from oracle import gemm as ogemm
 from oracle import ops as oops
@@ -302,6 +303,80 @@ def test_c4_batch32_to_4096_slots(full_model):
 
     _graphed_run(m, torch.from_numpy(ids).cuda(), torch.from_numpy(valid).cuda(), steps, check)
     assert not bad, bad[:10]
+
+
+def _c4_prompts():
+    lens = art.uniform_int(4, "c4.lens", (32,), 16, 1025)
+    return [art.uniform_int(4, f"c4.prompt.{i}", (int(n),), 100, 50000)
+            for i, n in enumerate(lens)]
+
+
+@pytest.mark.parametrize("graphed", [True, False], ids=["graphed", "eager"])
+def test_c4_prefix_vs_oracle_fixture(full_model, graphed):
+    """Config c4's batch of 32 ragged prompts (seeded lengths in [16, 1024],
+    right-padded) against the CPU oracle on a prefix of the run: the prefill
+    and the first decodes of every row (the full run to 4096 slots would take
+    the oracle days). Tokens and the demo chain hashes of the logits at every
+    step of every row equal tests/golden/c4_prefix.json (make_c4_fixture.py)."""
+    import json
+    import os
+    d, m = full_model
+    with open(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden",
+                           "c4_prefix.json")) as f:
+        fx = json.load(f)
+    assert art.artifact_digest(d) == fx["artifact_sha256"], "artifact generator drifted"
+    prompts = _c4_prompts()
+    assert [len(p) for p in prompts] == fx["lens"]
+    ids, valid = art.right_pad(prompts)
+    assert ids.shape[1] == fx["padded_len"]
+    steps = fx["steps"]
+    print(f"[c4 prefix vs oracle: B=32 T={ids.shape[1]} steps={steps} graphed={graphed}]",
+          flush=True)
+    toks, lg = m.generate(torch.from_numpy(ids).cuda(), steps, use_graph=graphed,
+                          chunk_valid=torch.from_numpy(valid).cuda())
+    rows = [[r.cpu().numpy() for r in step] for step in lg]
+    for b, w in enumerate(fx["rows"]):
+        assert toks[b].tolist() == w["tokens"], f"row {b}: tokens"
+        assert chain_hashes([rows[s][b] for s in range(steps)]) == w["logit_chain"], f"row {b}"
+
+
+def test_4k_prompt_long_context(full_model):
+    """tests/test_determinism.py:127-161 on the full-size model with a
+    4096-token prompt (seeded ids: the reference tokenises wikitext, a
+    network fetch): run-to-run equality of 5 greedy steps (eager, and the
+    graphed decode equal to it); batch invariance at bs 2 with a 100-token
+    co-prompt; and prefill of 4095 tokens then one decode equal to the full
+    prefill's last row (the decode scans 4096 slots: split-S attention)."""
+    _, m = full_model
+    V = art.QWEN3_0_6B["vocab"]
+    ids = torch.from_numpy(art.prompt_ids(40, 4096, V)).cuda()
+    T = ids.shape[0]
+    print("[4k prompt: run-to-run]", flush=True)
+    t1, l1 = m.generate(ids[None], 5)
+    t2, l2 = m.generate(ids[None], 5)
+    tg, lgr = m.generate(ids[None], 5, use_graph=True)
+    assert torch.equal(t1, t2) and torch.equal(t1, tg)
+    for a, b, c in zip(l1, l2, lgr):
+        assert torch.equal(a, b) and torch.equal(a, c)
+    print("[4k prompt: bs-2 batch invariance]", flush=True)
+    bids = torch.zeros(2, T, dtype=torch.int64, device="cuda")
+    valid = torch.zeros(2, T, dtype=torch.bool, device="cuda")
+    bids[0] = ids
+    valid[0] = True
+    bids[1, :100] = ids[:100]
+    valid[1, :100] = True
+    tb, lb = m.generate(bids, 5, chunk_valid=valid)
+    assert torch.equal(tb[0], t1[0])
+    for a, b in zip(lb, l1):
+        assert torch.equal(a[0], b[0])
+    print("[4k prompt: prefill 4095 + decode 1 == full prefill]", flush=True)
+    pos = torch.arange(T, device="cuda")[None]
+    full, _, _, _ = m.forward(ids[None], pos)
+    _, _, _, c = m.forward(ids[None, :-1], pos[:, :-1])
+    lg2, _, _, c = m.forward(ids[None, -1:], pos[:, -1:], c)
+    assert torch.equal(full[0, -1], lg2[0, 0])
+    assert torch.equal(full[0, -1], l1[0][0])
+    m.raise_if_device_error()
 
 
 def test_c4_split_prefill_batch32(full_model):

@@ -106,6 +106,26 @@ def test_generate_padded_batch(case):
     assert rec["batch_row_chains"][0] == rec["b1_logit_chain"]   # batch invariance
 
 
+def test_head_rows_select_the_full_logits_rows(case):
+    """forward(head_rows=r) computes the LM head at position r[b] of each row
+    only: the same rows (and row scales) as the full [B, T, vocab] logits
+    against the reference-written padded-batch goldens."""
+    rec, m = case
+    ids = np.array(rec["batch_ids"], dtype=I64)
+    valid = np.array(rec["batch_valid"], dtype=bool)
+    B, T = ids.shape
+    pos = np.broadcast_to(np.arange(T, dtype=I64), (B, T))
+    full, fxm, fxk, _ = m.forward(ids, pos, None, valid)
+    last = np.maximum(valid.sum(axis=1) - 1, 0)
+    sel, sxm, sxk, _ = m.forward(ids, pos, None, valid, head_rows=last)
+    rows = np.arange(B)
+    assert sel.shape == (B, full.shape[-1])
+    assert np.array_equal(sel, full[rows, last])
+    assert np.array_equal(sxm, fxm[rows, last]) and np.array_equal(sxk, fxk[rows, last])
+    for b in range(B):    # the first step of the reference's padded-batch chains
+        assert chain_hashes([sel[b]])[0] == rec["batch_row_chains"][b][0]
+
+
 def test_split_prefill(case):
     rec, m = case
     ids = np.array(rec["prompt"], dtype=I64)
