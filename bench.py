@@ -73,16 +73,20 @@ def c3_inputs(B: int, vocab: int):
 
 def _c3_start(model, B: int):
     """Prefill of the c3 batch, graph capture with the first decode.
-    Returns (GraphedDecode, padded prompt length)."""
+    Returns (GraphedDecode, padded prompt length). The cache is planned for
+    the whole run up front, as IntQwen3.generate plans it: the decodes then
+    only map pages (no pool regrowth, no graph recapture)."""
     import torch
     from idempotent_llm_amd.graphed import GraphedDecode
+    from idempotent_llm_amd.kvcache import KVCache
     ids, valid = c3_inputs(B, model.vocab)
     ids = torch.from_numpy(ids).cuda()
     valid = torch.from_numpy(valid).cuda()
     T = ids.shape[1]
     pos = torch.arange(T, device="cuda").expand(B, T)
     lens = valid.sum(dim=1)
-    first, _, _, cache = model._forward(ids, pos, None, valid, (lens - 1).clamp(min=0))
+    cache = KVCache().plan(model, B, T + C3_STEPS)
+    first, _, _, cache = model._forward(ids, pos, cache, valid, (lens - 1).clamp(min=0))
     gd = GraphedDecode(model, cache, lens)
     gd.step_greedy(model.greedy_pick(first))      # decode 1 (captures the step graph)
     return gd, T
@@ -379,24 +383,21 @@ def kernel_probe(model, B: int, reps: int = 3):
 
 def c0_bench():
     """Config c0: A int8 [64, 1024] x W int8 [1024, 3072] (seed 0) then
-    requant_i8_static(P, 1, 0, m, 20, 1, 0) to int8: the skinny GEMM (K
-    split) and the fused static epilogue, timed over graph replays."""
+    requant_i8_static(P, 1, 0, m, 20, 1, 0) to int8, in one launch
+    (detllm_igemv_requant_static: the int32 product stays in registers),
+    timed over graph replays."""
     import torch
     from idempotent_llm_amd import artifact as art
-    from idempotent_llm_amd._lib import call, gemv_plan
-    from idempotent_llm_amd.backends import gemm_nt
+    from idempotent_llm_amd._lib import call
     M, K, N = 64, 1024, 3072
     A = torch.from_numpy(art.rand_i8(0, "c0.A", (M, K))).cuda()
     Wt = torch.from_numpy(art.rand_i8(0, "c0.W", (K, N)).T.copy()).cuda()
     m = torch.from_numpy(art.uniform_int(0, "c0.m", (N,), 1 << 14, 1 << 15)).cuda()
-    ks = gemv_plan(M, N, K)
-    P = torch.empty(ks, M, N, dtype=torch.int32, device="cuda")
     y8 = torch.empty(M, N, dtype=torch.int8, device="cuda")
 
     def run():
         for _ in range(10):
-            gemm_nt(A, Wt, out=P, ksplit=ks)
-            call("detllm_requant_static_cols", P, ks, M * N, M, N, None, None, m, 20, 1, 0, y8)
+            call("detllm_igemv_requant_static", A, Wt, M, N, K, None, None, m, 20, 1, 0, y8)
 
     us = _graph_time_us(run, 20, 10)
     ops = 2.0 * M * N * K
@@ -405,8 +406,8 @@ def c0_bench():
             "frac_mfma_peak": round(ops / (us * 1e-6) / 1e12 / I8_PEAK_TOPS, 5),
             "hbm_gbs": round(nbytes / (us * 1e-6) / 1e9, 1),
             "frac_hbm_peak": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
-            "algorithmic_bytes": nbytes, "ksplit": ks,
-            "kernels": "k_gemv_nt + k_static_cols (one launch pair)"}
+            "algorithmic_bytes": nbytes, "ksplit": 1,
+            "kernels": "k_gemv_static (one launch: GEMV + requant_i8_static epilogue)"}
 
 
 def prefill_bench(model, T: int):
@@ -590,6 +591,18 @@ def gemm_tops(T: int = PREFILL_LEN):
 
 # ------------------------------------------------------------- CPU baseline
 
+def _cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    import platform
+    return platform.processor() or "unknown"
+
+
 def _cores() -> int:
     cores = len(os.sched_getaffinity(0))
     omp = os.environ.get("OMP_NUM_THREADS")
@@ -674,7 +687,8 @@ def cpu_baseline(art_dir: str, steps: int = 3):
     o.forward(cur4[:, None], np.full((32, 1), 16), c4c, np.ones((32, 1), dtype=bool))
     cfg["c4"] = {"s": round(time.perf_counter() - t0, 3),
                  "sample": "prefix: batch 32, prompts cut to 16 tokens, prefill + 1 decode step"}
-    head = {"value": round(steps / dt, 4), "unit": "tok/s", "cores": _cores(), "kind": "port",
+    head = {"value": round(steps / dt, 4), "unit": "tok/s", "cores": _cores(),
+            "cpu_model": _cpu_model(), "kind": "port",
             "sample": f"c3 batch 1: {steps} decode steps after the 64-token prefill (prefill "
                       f"untimed), full 28-layer model, numpy oracle"}
     return head, cfg

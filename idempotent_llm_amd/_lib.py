@@ -43,6 +43,7 @@ SIGNATURES = {
                             P, P, P, P, P, P, P, P, L, P, P, P, P, P, P, I, P, L, P, P, S],
     "detllm_kq_est": [P, P, L, L, P, S],
     "detllm_requant_static_cols": [P, I, L, I, I, P, P, P, L, L, L, P, S],
+    "detllm_igemv_requant_static": [P, P, I, I, I, P, P, P, L, L, L, P, S],
     "detllm_attn_prefill": [P, P, P, P, P, I, P, L, I, I, I, I, I, P, S],
     "detllm_attn_decode": [P, P, P, P, P, I, P, L, I, I, I, I, P, P, P, P, S],
     "detllm_qkv_attn_decode": [P, I, L, I, I, I, P, P, P, P, L, P, L, P, L, P, L, P, L, P, L,

@@ -343,6 +343,67 @@ __global__ __launch_bounds__(256) void k_gemv_dec(GemvArgs g, Prefetch pf) {
   keep_hidden_args();
 }
 
+// requant_i8_static of a skinny GEMM's product (M <= 64 rows), applied in
+// the GEMV's epilogue so the int32 product never leaves registers: config
+// c0's int_gemm + requant (dyadic.py:142-163, canonical form (P, 1, 0, m, 20,
+// 1, 0)). The per-row constants (row_m, the shift split into up / down, the
+// divisor s_m << down and its fp64 estimate) are computed once per block into
+// LDS; each element is y = clamp_i8(rhad((P col_m row_m) << up, den)), by the
+// fp64 estimate when 0 < den < 2^49 and |n| < 2^49 (then 2 |n| + den < 2^51,
+// as rhad_est_i8 requires), else by the integer division (torch's floor
+// division also for a divisor that wrapped negative). Same integers as
+// k_static_cols after the GEMV.
+struct StaticRows {
+  i64 rm[64], up[64], den[64];
+  double dr[64], dk[64];
+  int fast[64];
+};
+
+struct StaticEpi {
+  const StaticRows* rows;
+  i64 cm;
+  int8_t* y8;
+  __device__ __forceinline__ void operator()(const GemvArgs& g, int, int row, int col,
+                                             int32_t v) const {
+    const i64 n = shl(wmul(wmul((i64)v, cm), rows->rm[row]), rows->up[row]);
+    constexpr i64 lim = (i64)1 << 49;
+    const DivEst D{rows->dr[row], rows->dk[row]};
+    y8[(i64)row * g.N + col] = (int8_t)((rows->fast[row] && n > -lim && n < lim)
+                                            ? rhad_est_i8(n, D)
+                                            : clamp_i8(rhad(n, rows->den[row])));
+  }
+};
+
+__global__ __launch_bounds__(256) void k_gemv_static(GemvArgs g, const int64_t* row_m,
+                                                     const int64_t* row_k,
+                                                     const int64_t* __restrict__ col_m, i64 col_k,
+                                                     i64 s_m, i64 s_k, int8_t* __restrict__ y8) {
+  keep_hidden_args();
+  __shared__ GemvLds<4, 4> lds;
+  __shared__ StaticRows sr;
+  const int col = blockIdx.x * 16 + (threadIdx.x & 15);
+  const i64 cm = col_m[col < g.N ? col : g.N - 1];
+  const int t = threadIdx.x;
+  if (t < g.M) {
+    const i64 rk = row_k ? row_k[t] : 0;
+    const i64 shift = wsub(wadd(rk, col_k), s_k);
+    const i64 down = imax(shift, 0);
+    i64 den = shl(s_m, down);
+    if (den == 0) den = 1;  // the reference's division raises there
+    const int fast = den > 0 && den < ((i64)1 << 49);
+    const DivEst D = make_divest(fast ? den : 1, 1.0);
+    sr.rm[t] = row_m ? row_m[t] : 1;
+    sr.up[t] = imax(wneg(shift), 0);
+    sr.den[t] = den;
+    sr.dr[t] = D.r;
+    sr.dk[t] = D.k;
+    sr.fast[t] = fast;
+  }
+  // gemv_block's cross-wave barrier (four waves split K) orders these LDS
+  // writes before the epilogue reads them
+  gemv_block<4, 4, 1>(g, blockIdx.x, 0, lds, StaticEpi{&sr, cm, y8});
+}
+
 // Skinny GEMM over many columns (the LM head) for M <= 16 rows: the A rows
 // are staged in LDS once per block, and each wave walks its own 16-column
 // groups over the whole K range (grid-stride), with all of a group's weight
@@ -626,6 +687,21 @@ int detllm_igemm_nt(const int8_t* A, const int8_t* B, int32_t* C, int M, int N, 
   if ((i64)tiles_m * tiles_n > 0x7fffffff) return DI_ERANGE;
   hipLaunchKernelGGL(k_gemm_nt, dim3(tiles_m * tiles_n, 1, batch), dim3(256), 0, s, A, B, C, M,
                      N, K, (i64)sA, (i64)sB, (i64)sC, tiles_n);
+  DI_LAUNCH_CHECK();
+  return DI_OK;
+}
+
+// int_gemm + requant_i8_static for M <= 64 rows in one launch (k_gemv_static).
+int detllm_igemv_requant_static(const int8_t* A, const int8_t* B, int M, int N, int K,
+                                const int64_t* row_m, const int64_t* row_k,
+                                const int64_t* col_m, int64_t col_k, int64_t s_m, int64_t s_k,
+                                int8_t* y8, hipStream_t s) {
+  if (M <= 0 || N <= 0) return DI_OK;
+  if (M > 64 || K <= 0 || (K % 16) != 0 || K > 131071 || !A || !B || !col_m || !y8)
+    return DI_EINVAL;
+  GemvArgs g{A, B, nullptr, M, N, K, K, 0};
+  hipLaunchKernelGGL(k_gemv_static, dim3((N + 15) / 16), dim3(256), 0, s, g, row_m, row_k, col_m,
+                     (i64)col_k, (i64)s_m, (i64)s_k, y8);
   DI_LAUNCH_CHECK();
   return DI_OK;
 }

@@ -41,9 +41,20 @@ struct GemvLds {
   int32_t red[KW > 1 ? (KW - 1) * (4 / KW) : 1][MB * 4][64];
 };
 
-// One 256-thread GEMV block: column group(s) `bx`, K range `by`.
-template <int MB, int KW, int NB>
-__device__ __forceinline__ void gemv_block(const GemvArgs& g, int bx, int by, GemvLds<MB, KW>& L) {
+// The default epilogue of gemv_block: the int32 product (or K-split
+// partial) to C.
+struct GemvStore {
+  __device__ __forceinline__ void operator()(const GemvArgs& g, int by, int row, int col,
+                                             int32_t v) const {
+    g.C[by * g.split_stride + (i64)row * g.N + col] = v;
+  }
+};
+
+// One 256-thread GEMV block: column group(s) `bx`, K range `by`; every
+// in-range (row, col) result goes to epi(g, by, row, col, value).
+template <int MB, int KW, int NB, class Epi = GemvStore>
+__device__ __forceinline__ void gemv_block(const GemvArgs& g, int bx, int by, GemvLds<MB, KW>& L,
+                                           const Epi& epi = Epi()) {
   constexpr int U = 4;           // 16-byte slices per lane per iteration
   constexpr int CG = 4 / KW;     // column groups per block
   constexpr int KSTEP = 64 * U;  // K covered by one wave-iteration
@@ -116,7 +127,7 @@ __device__ __forceinline__ void gemv_block(const GemvArgs& g, int bx, int by, Ge
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int row = mb * 16 + grp * 4 + r;
-      if (row < M && colok) g.C[by * g.split_stride + (i64)row * g.N + col] = acc[mb][r];
+      if (row < M && colok) epi(g, by, row, col, acc[mb][r]);
     }
 }
 

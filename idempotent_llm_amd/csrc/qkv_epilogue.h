@@ -52,8 +52,10 @@ struct QKVArgs {
 
 // The static K requantisation's divisor of one channel (model.py:326-329,
 // requant_i8_static with row scale (1, rowk)): den = kq_m << max(rowk - kq_k,
-// 0) (1 if not positive), the numerator's up-shift max(kq_k - rowk, 0), and
-// DivEst(den, 1) for rhad_est_i8. Every input is a layer constant, so the
+// 0) (wrapping as torch's shift does; 1 if it is 0, where the reference's
+// division raises), the numerator's up-shift max(kq_k - rowk, 0), and
+// DivEst(den, 1) for rhad_est_i8 (used for 0 < den < 2^49 only; a negative
+// wrapped divisor takes the generic floor division, as torch computes it). Every input is a layer constant, so the
 // estimate can be computed once per channel (kq_est) instead of per element.
 struct KqChan {
   i64 den, up;
@@ -65,8 +67,8 @@ __device__ __forceinline__ KqChan kq_channel(i64 km, i64 kk, i64 rowk) {
   KqChan q;
   q.up = imax(wneg(shift), 0);
   q.den = shl(km, imax(shift, 0));
-  if (q.den <= 0) q.den = 1;
-  q.D = make_divest(q.den < ((i64)1 << 49) ? q.den : 1, 1.0);
+  if (q.den == 0) q.den = 1;
+  q.D = make_divest(q.den > 0 && q.den < ((i64)1 << 49) ? q.den : 1, 1.0);
   return q;
 }
 
@@ -259,20 +261,23 @@ __device__ __forceinline__ void qkv_head_compute(const QKVArgs& a, int r, int sl
     const i64 shift = wsub(wadd(xk, a.v_k), vqk);
     const i64 up = imax(wneg(shift), 0), down = imax(shift, 0);
     i64 den = shl(vqm, down);
-    if (den <= 0) den = 1;  // static scales are positive mantissas in artifacts
+    if (den == 0) den = 1;  // the reference's division raises there
     const i64 n0 = shl(wmul(wmul(p0, wm0), xm), up);
     const i64 n1 = shl(wmul(wmul(p1, wm1), xm), up);
     const int pg = a.kv.page(b, slot);
     int8_t o0, o1;
     const i64 lim = (i64)1 << 49;  // 2 |n| + den < 2^51 for rhad_est_i8
-    if (DI_LIKELY(den < lim && n0 > -lim && n0 < lim && n1 > -lim && n1 < lim)) {
+    if (DI_LIKELY(den > 0 && den < lim && n0 > -lim && n0 < lim && n1 > -lim && n1 < lim)) {
       const DivEst D = make_divest(den, 1.0);
       o0 = (int8_t)rhad_est_i8(n0, D);
       o1 = (int8_t)rhad_est_i8(n1, D);
-    } else {
+    } else if (DI_LIKELY(den > 0)) {
       const Recip R = make_recip(den);
       o0 = (int8_t)clamp_i8(rhad_r(n0, R));
       o1 = (int8_t)clamp_i8(rhad_r(n1, R));
+    } else {  // a wrapped, negative divisor: torch's floor division
+      o0 = (int8_t)clamp_i8(rhad(n0, den));
+      o1 = (int8_t)clamp_i8(rhad(n1, den));
     }
     if (pg >= 0) {
       a.kv.vchan(pg, h, c0)[slot & (DI_PAGE - 1)] = o0;
@@ -306,10 +311,10 @@ __device__ __forceinline__ void qkv_head_compute(const QKVArgs& a, int r, int sl
       const i64 shift = wsub(rowk, kk[q]);
       const i64 up = imax(wneg(shift), 0), down = imax(shift, 0);
       i64 den = shl(km[q], down);
-      if (den <= 0) den = 1;
+      if (den == 0) den = 1;  // the reference's division raises there
       const i64 n = shl(rv[q], up);
       const i64 lim = (i64)1 << 49;  // 2 |n| + den < 2^51 for rhad_est_i8
-      if (DI_LIKELY(den < lim && n > -lim && n < lim))
+      if (DI_LIKELY(den > 0 && den < lim && n > -lim && n < lim))
         outv[q] = rhad_est_i8(n, make_divest(den, 1.0));
       else
         outv[q] = clamp_i8(rhad(n, den));
@@ -458,9 +463,9 @@ __device__ __forceinline__ void qkv_rows4(const QKVArgs& a, int R, int r0, int s
     const i64 shift = wsub(wadd(xk, a.v_k), vqk);
     const i64 up = imax(wneg(shift), 0), down = imax(shift, 0);
     i64 den = shl(vqm, down);
-    if (den <= 0) den = 1;
+    if (den == 0) den = 1;  // the reference's division raises there
     i64 n[8];
-    bool fast = den < ((i64)1 << 49);
+    bool fast = den > 0 && den < ((i64)1 << 49);
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       n[i] = shl(wmul(wmul(p[i], wm[i]), xm), up);
@@ -471,10 +476,13 @@ __device__ __forceinline__ void qkv_rows4(const QKVArgs& a, int R, int r0, int s
       const DivEst D = make_divest(den, 1.0);
 #pragma unroll
       for (int i = 0; i < 8; ++i) o[i] = (int8_t)rhad_est_i8(n[i], D);
-    } else {
+    } else if (DI_LIKELY(den > 0)) {
       const Recip Rr = make_recip(den);
 #pragma unroll
       for (int i = 0; i < 8; ++i) o[i] = (int8_t)clamp_i8(rhad_r(n[i], Rr));
+    } else {  // a wrapped, negative divisor: torch's floor division
+#pragma unroll
+      for (int i = 0; i < 8; ++i) o[i] = (int8_t)clamp_i8(rhad(n[i], den));
     }
     if (sok) {
 #pragma unroll
@@ -557,7 +565,7 @@ __device__ __forceinline__ void qkv_rows4(const QKVArgs& a, int R, int r0, int s
       }
       const i64 n = shl(rv[i], q.up);
       const i64 lim = (i64)1 << 49;  // 2 |n| + den < 2^51 for rhad_est_i8
-      const int o = (q.den < lim && n > -lim && n < lim) ? rhad_est_i8(n, q.D)
+      const int o = (q.den > 0 && q.den < lim && n > -lim && n < lim) ? rhad_est_i8(n, q.D)
                                                          : (int)clamp_i8(rhad(n, q.den));
       w[i >> 2] |= (uint32_t)(uint8_t)(int8_t)o << (8 * (i & 3));
     }

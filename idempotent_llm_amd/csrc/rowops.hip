@@ -1073,7 +1073,7 @@ __global__ void k_op_static(const int64_t* P, const int64_t* row_m, const int64_
     const i64 shift = wsub(wadd(row_k[i], col_k[i]), s_k[i]);
     const i64 up = imax(wneg(shift), 0), down = imax(shift, 0);
     i64 den = shl(s_m[i], down);
-    if (den <= 0) den = 1;
+    if (den == 0) den = 1;  // the reference's division raises there
     y8[i] = (int8_t)clamp_i8(rhad(shl(num, up), den));
   }
 }
@@ -1097,8 +1097,8 @@ __global__ __launch_bounds__(256) void k_static_cols(const int32_t* __restrict__
   const i64 shift = wsub(wadd(rk, col_k), s_k);
   const i64 up = imax(wneg(shift), 0), down = imax(shift, 0);
   i64 den = shl(s_m, down);
-  if (den <= 0) den = 1;
-  const bool fast_den = den < ((i64)1 << 49);
+  if (den == 0) den = 1;  // the reference's division raises there
+  const bool fast_den = den > 0 && den < ((i64)1 << 49);
   const DivEst D = make_divest(fast_den ? den : 1, 1.0);
   const i64 off = (i64)r * C + c0;
 #pragma unroll

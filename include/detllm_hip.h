@@ -46,7 +46,9 @@ extern "C" {
 /* int_gemm(a, b, backend) — src/detllm/backends.py:88-135 (batched form
  * :127-134). C[b] = A[b] . B[b]^T: A [batch][M][K], B [batch][N][K] (the
  * artifact's [K][N] w8t transposed), C [batch][M][N] int32; batch strides in
- * elements. K % 16 == 0, K <= 131071. i8 MFMA, 128x128 block tiles. */
+ * elements. K % 16 == 0, K <= 131071. i8 MFMA: 32x32x32 tiles of 256x256,
+ * 128x192, 128x128 or 128x64 elements per block by tile count when K % 128
+ * == 0 (a direct-to-LDS operand ring), else 128x128 blocks of 16x16x64. */
 int detllm_igemm_nt(const int8_t* A, const int8_t* B, int32_t* C, int M, int N, int K,
                     int batch, int64_t sA, int64_t sB, int64_t sC, hipStream_t s);
 
@@ -241,7 +243,7 @@ int detllm_qkv_epilogue(const int32_t* P, int nsplit, int64_t split_stride, int 
 /* The static K requantisation's per-channel divisors for one layer
  * (requant_i8_static of model.py:326-329 with row scale (1, rowk), rowk =
  * 20 + k_norm_k), computed once at model load: est [n][4] = {den = kq_m <<
- * max(rowk - kq_k, 0) (1 if not positive), up = max(kq_k - rowk, 0), the bits
+ * max(rowk - kq_k, 0) (wrapping; 1 if 0), up = max(kq_k - rowk, 0), the bits
  * of fl(1/den) and of fl((floor(den/2) + 1/2) / den)}. detllm_qkv_epilogue
  * reads them through kq_est (nullable: then it derives them per element). */
 int detllm_kq_est(const int64_t* kq_m, const int64_t* kq_k, int64_t n, int64_t rowk,
@@ -256,6 +258,19 @@ int detllm_requant_static_cols(const int32_t* P, int nsplit, int64_t split_strid
                                const int64_t* row_m, const int64_t* row_k, const int64_t* col_m,
                                int64_t col_k, int64_t s_m, int64_t s_k, int8_t* y8,
                                hipStream_t s);
+
+/* int_gemm followed by requant_i8_static, for M <= 64 rows, in one launch —
+ * src/detllm/backends.py:88-135 then dyadic.py:142-163 (config c0: A int8
+ * [64][1024] x the [1024][3072] weight, (P, 1, 0, m, 20, 1, 0)). A [M][K], B
+ * [N][K] (the weight transposed, as detllm_igemv_nt takes it); the int32
+ * product stays in registers and y8 [M][N] = clamp_i8(rhad(P col_m row_m <<
+ * up, s_m << down)), shift = row_k + col_k - s_k; row_m / row_k nullable (1,
+ * 0). Same integers as detllm_igemv_nt + detllm_requant_static_cols.
+ * K % 16 == 0, K <= 131071. */
+int detllm_igemv_requant_static(const int8_t* A, const int8_t* B, int M, int N, int K,
+                                const int64_t* row_m, const int64_t* row_k,
+                                const int64_t* col_m, int64_t col_k, int64_t s_m, int64_t s_k,
+                                int8_t* y8, hipStream_t s);
 
 /* ------------------------------------------------------------ attention -- */
 

@@ -298,6 +298,41 @@ def test_config0_gemm_requant():
     eq(y8s, ody.requant_i8_static(Pw, 1, 0, m, 20, 1, 0))
 
 
+def test_igemv_requant_static_c0_and_general():
+    """detllm_igemv_requant_static (int_gemm + requant_i8_static in one
+    launch, the product kept in registers): config c0 against the oracle
+    (backends.py:88-135, dyadic.py:142-163), then ragged shapes (M = 1, 17,
+    64; N not a multiple of 16; K not a multiple of 256) with per-row scales,
+    up- and down-shifts, numerators past the fp64 estimate's bound (the
+    exact integer path) and divisors that wrap negative (rows with row_k
+    22: torch's floor division by the wrapped value), each equal to the
+    oracle."""
+    from idempotent_llm_amd import artifact as art
+    from idempotent_llm_amd._lib import call
+    A = art.rand_i8(0, "c0.A", (64, 1024))
+    W = art.rand_i8(0, "c0.W", (1024, 3072))
+    m = art.uniform_int(0, "c0.m", (3072,), 1 << 14, 1 << 15)
+    y8 = torch.empty(64, 3072, dtype=torch.int8, device="cuda")
+    call("detllm_igemv_requant_static", g(A), g(W.T.copy()), 64, 3072, 1024, None, None, g(m),
+         20, 1, 0, y8)
+    eq(y8, ody.requant_i8_static(ogemm.int_gemm(A, W), 1, 0, m, 20, 1, 0))
+    rnd = np.random.default_rng(44)
+    for M, N, K in ((1, 301, 272), (17, 4100, 1024), (64, 48, 1040)):
+        A = rnd.integers(-128, 128, (M, K)).astype(np.int8)
+        W = rnd.integers(-128, 128, (K, N)).astype(np.int8)
+        Pw = ogemm.int_gemm(A, W)
+        row_m = rnd.integers(1, 1 << 16, (M, 1)).astype(I64)
+        row_k = rnd.integers(0, 30, (M, 1)).astype(I64)
+        col_m = rnd.integers(1 << 14, 1 << 16, (N,)).astype(I64)
+        col_m[::7] = rnd.integers(1 << 30, 1 << 40, col_m[::7].shape)   # |n| past 2^49
+        for col_k, s_m, s_k in ((20, 1, 0), (5, 40000, 60), (24, (1 << 20) + 7, 3)):
+            want = ody.requant_i8_static(Pw, row_m, row_k, col_m, col_k, s_m, s_k)
+            y8 = torch.empty(M, N, dtype=torch.int8, device="cuda")
+            call("detllm_igemv_requant_static", g(A), g(W.T.copy()), M, N, K, g(row_m[:, 0]),
+                 g(row_k[:, 0]), g(col_m), col_k, s_m, s_k, y8)
+            eq(y8, want)
+
+
 @pytest.mark.parametrize("seed", [0, 1])
 def test_requant_static_cols_general(seed):
     """detllm_requant_static_cols with per-row scales, up- and down-shifts
@@ -311,6 +346,10 @@ def test_requant_static_cols_general(seed):
     Pw = ((Pw + (1 << 31)) % (1 << 32) - (1 << 31)).astype(np.int32)   # int32 wrap of the sum
     row_m = rnd.integers(1, 1 << 16, (R, 1)).astype(I64)
     row_k = rnd.integers(0, 30, (R, 1)).astype(I64)
+    # rows whose divisor s_m << shift wraps negative at the third target
+    # ((2^20 + 7) << 43 and << 61 pass 2^63): torch's floor division by the
+    # wrapped value, as the reference's tensor rhad computes it
+    row_k[0, 0], row_k[1, 0] = 22, 40
     col_m = rnd.integers(1 << 14, 1 << 16, (C,)).astype(I64)
     for col_k, s_m, s_k in ((20, 1, 0), (5, 40000, 60), (24, (1 << 20) + 7, 3)):
         want = ody.requant_i8_static(Pw, row_m, row_k, col_m, col_k, s_m, s_k)
