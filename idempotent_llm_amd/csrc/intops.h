@@ -582,6 +582,50 @@ DI_HD i64 isqrt_est(i64 n) {
   return r;
 }
 
+// ---- exact integers carried as fp64 values ----------------------------
+//
+// An integer of magnitude below 2^53 is an exact double, and fp64 multiply,
+// fma and floor are correctly rounded (IEEE), so a product of two such
+// integers whose true value is below 2^53 comes out exact. The row kernels
+// keep their int32 x mantissa products in this form where the operands are
+// bounded (a 64-bit integer multiply costs four quarter-rate instructions on
+// gfx950, an fp64 multiply one full-rate instruction); the bounds each use
+// needs are checked per row, with the integer routines as the fallback.
+
+// Bit length of an integer-valued double (0 for 0): e with 2^(e-1) <= |x| <
+// 2^e, the exponent frexp returns (v_frexp_exp_i32_f64 on the device).
+DI_HD uint32_t bitlen_f64(double x) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  return x == 0.0 ? 0u : (uint32_t)__builtin_amdgcn_frexp_exp(x);
+#else
+  int e = 0;
+  frexp(x, &e);
+  return x == 0.0 ? 0u : (uint32_t)e;
+#endif
+}
+
+// rshift_round(x, sh) (intmath.py:120-147: (x + 2^(sh-1)) >> sh, floor) for an
+// integer-valued double with |x| < 2^52 and 0 <= sh < 1000: x 2^-sh is exact
+// (a power-of-two scaling), a multiple of 2^-sh below 2^(52-sh) in magnitude,
+// so adding 1/2 in the fma stays exact (the sum is below 2^(53-sh) and a
+// multiple of 2^-sh), and floor gives the integer.
+DI_HD double rshift_round_f64(double x, int sh) {
+  return sh == 0 ? x : floor(fma(x, ldexp(1.0, -sh), 0.5));
+}
+
+// The bit pattern of a non-negative double as an int64 orders like the
+// double, so a block maximum of magnitudes reduces these patterns.
+DI_HD i64 f64_bits(double x) {
+  i64 b;
+  __builtin_memcpy(&b, &x, 8);
+  return b;
+}
+DI_HD double f64_from_bits(i64 b) {
+  double x;
+  __builtin_memcpy(&x, &b, 8);
+  return x;
+}
+
 // ops/di_swiglu.py:39-58 on one element for |g|, |u| <= 2^14 (gate and up
 // after requant_i32_common(14)) and tpos < 2^23: |g| < 2^22 for dexp_est,
 // E <= tpos and den = tpos + E < 2^24 for sigmoid_est24, g * sig (sig <= 128)
@@ -590,6 +634,13 @@ DI_HD i64 swiglu_elem_est(int32_t g, int32_t u, const ExpEst& E) {
   const uint32_t e = dexp_est((uint32_t)(g < 0 ? -g : g), E);
   const uint32_t sig = sigmoid_est24(g >= 0 ? E.t : e, E.t + e);
   return (i64)(g * (int32_t)sig) * (i64)u;
+}
+
+// g * sig of swiglu_elem_est (|g| <= 2^14, sig <= 128: an int32 product)
+DI_HD int32_t swiglu_gsig_est(int32_t g, const ExpEst& E) {
+  const uint32_t e = dexp_est((uint32_t)(g < 0 ? -g : g), E);
+  const uint32_t sig = sigmoid_est24(g >= 0 ? E.t : e, E.t + e);
+  return g * (int32_t)sig;
 }
 
 }  // namespace di

@@ -47,6 +47,14 @@ void di_host_scalar(int op, const int64_t* a, const int64_t* b, const int64_t* c
     }
   }
 }
+// bitlen_f64 / rshift_round_f64 on integer inputs: out[i] = bit length of
+// a[i] (op 0) or rshift_round_f64(a[i], b[i]) converted back (op 1)
+void di_host_f64_int_op(int op, const int64_t* a, const int64_t* b, int64_t n, int64_t* out) {
+  for (int64_t i = 0; i < n; ++i) {
+    if (op == 0) out[i] = (int64_t)bitlen_f64((double)a[i]);
+    else out[i] = (int64_t)rshift_round_f64((double)a[i], (int)b[i]);
+  }
+}
 void di_host_di_exp_neg(const int64_t* neg, const int64_t* tpos, int64_t n, int64_t* out) {
   for (int64_t i = 0; i < n; ++i) out[i] = di_exp_neg((u64)neg[i], make_exp(tpos[i]));
 }

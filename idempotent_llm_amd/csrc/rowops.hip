@@ -141,6 +141,56 @@ __device__ __forceinline__ void quant_row(const i64 (&v)[VPT], i64 m_in, i64 k_i
   }
 }
 
+// quant_row on exact integer values carried as doubles (|v| < 2^53), for a
+// row whose every element this thread holds is exact (ok): the row maximum
+// reduces the doubles' bit patterns (non-negative doubles order like their
+// bits), and a thread whose values are not exact enters +inf, which sends
+// the whole row back to the caller (returns false: the caller recomputes
+// the values as int64 and runs quant_row). With a = max(max |v|, 1) below
+// 2^43 the quotients rhad(127 |v|, a) come from the fp64 estimate, exactly
+// as quant_row's (2 * 127 |v| + a < 2^51); a larger maximum converts the
+// values (exact below 2^53) and runs quant_row. Same integers and (m, k).
+template <int VPT, class Red>
+__device__ __forceinline__ bool quant_row_f64(const double (&v)[VPT], bool ok, i64 m_in, i64 k_in,
+                                              int C, Red& red, int8_t* out, i64* m_out,
+                                              i64* k_out, bool defer_fit = false) {
+  double g = 0.0;
+#pragma unroll
+  for (int j = 0; j < VPT; ++j) g = fmax(g, fabs(v[j]));
+  const i64 bits = red.max(ok ? f64_bits(g) : f64_bits(__builtin_inf()));
+  if (DI_UNLIKELY(bits >= f64_bits(__builtin_inf()))) return false;
+  const double au = f64_from_bits(bits);
+  if (DI_UNLIKELY(au >= 0x1p43)) {
+    i64 w[VPT];
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) w[j] = (i64)v[j];
+    quant_row(w, m_in, k_in, C, red, out, m_out, k_out, defer_fit);
+    return true;
+  }
+  i64 m, k;
+  norm_scale(m_in, k_in, &m, &k);
+  const i64 a = imax((i64)au, 1);
+  const DivEst D = make_divest(a, 127.0);
+#pragma unroll
+  for (int j = 0; j < VPT; ++j) {
+    const int c = red.tid() + j * red.nt();
+    const uint32_t q = rhad_est(fabs(v[j]), D);
+    if (c < C) out[c] = (int8_t)(v[j] < 0 ? -(int32_t)q : (int32_t)q);
+  }
+  if (red.tid() == 0 && m_out) {
+    if (defer_fit) {
+      *m_out = wmul(a, m);
+      *k_out = k;
+    } else {
+      i64 mo, e;
+      fit_dyadic_ratio_127(wmul(a, m), &mo, &e);
+      *m_out = mo;
+      *k_out = wadd(k, e);
+    }
+  }
+  return true;
+}
+
 // dyadic.py:108-120: v holds P on entry, y (int32 values) on exit; cm holds
 // col_m of this thread's columns (0 past C); returns k_out
 template <int VPT, class Red>
@@ -583,39 +633,103 @@ __device__ __forceinline__ void swiglu_quant_row(const SwigluArgs& a, int r, Red
     xk = a.xk[r];
     load_rows_i32_sum<2, VPT>(gu, a.P, a.nsplit, a.split_stride, offs, I, red);
   }
+  // requant_i32_common(14) of gate and up (dyadic.py:108-120) on fp64: with
+  // |col_m| < 2^21 every product P col_m (|P| < 2^31) is an exact double
+  // below 2^52, its bit length is the fp64 exponent and rshift_round_f64
+  // applies. A thread holding a larger col_m enters bit length 64, which no
+  // exact product reaches, and the row takes the integer routine. Only the
+  // doubles stay live across the reduction: the integer routines reload
+  // their operands (a rare path), which keeps the registers of the common
+  // one free.
+  constexpr i64 CM_LIM = (i64)1 << 21;
+  double vg[VPT], vu[VPT];
+  uint32_t L0 = 0, L1 = 0;
+  {
+    bool ok = true;
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) {
+      ok = ok && gm[j] > -CM_LIM && gm[j] < CM_LIM && um[j] > -CM_LIM && um[j] < CM_LIM;
+      vg[j] = (double)(int32_t)gu[0][j] * (double)(int32_t)gm[j];
+      vu[j] = (double)(int32_t)gu[1][j] * (double)(int32_t)um[j];
+      L0 = ::max(L0, bitlen_f64(vg[j]));
+      L1 = ::max(L1, bitlen_f64(vu[j]));
+    }
+    if (!ok) L0 = L1 = 64u;
+  }
+  red.max2_u32(L0, L1);
   i64 gk, uk;
-  requant_common_row2(gu[0], gm, a.gate_k, gu[1], um, a.up_k, xk, 14, red, &gk, &uk);
+  int32_t g32[VPT], u32[VPT];
+  if (DI_LIKELY(L0 < 64u && L1 < 64u)) {
+    const i64 sh0 = imax(ilog2_from_bitlen(L0) - 13, 0);
+    const i64 sh1 = imax(ilog2_from_bitlen(L1) - 13, 0);
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) {
+      g32[j] = (int32_t)rshift_round_f64(vg[j], (int)sh0);
+      u32[j] = (int32_t)rshift_round_f64(vu[j], (int)sh1);
+    }
+    gk = wsub(wadd(xk, a.gate_k), sh0);
+    uk = wsub(wadd(xk, a.up_k), sh1);
+  } else {
+    i64 cg[VPT], cu[VPT], v[2][VPT];
+    prefetch_cols(cg, a.gate_m, I, red);
+    prefetch_cols(cu, a.up_m, I, red);
+    load_rows_i32_sum<2, VPT>(v, a.P, a.nsplit, a.split_stride, offs, I, red);
+    requant_common_row2(v[0], cg, a.gate_k, v[1], cu, a.up_k, xk, 14, red, &gk, &uk);
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) {
+      g32[j] = (int32_t)v[0][j];
+      u32[j] = (int32_t)v[1][j];
+    }
+  }
   // requant_i32_common(14) leaves |g|, |u| <= 2^14 (the shift brings the
   // row's largest magnitude to at most 2^14)
-  int32_t g32[VPT], u32[VPT];
-#pragma unroll
-  for (int j = 0; j < VPT; ++j) {
-    g32[j] = (int32_t)gu[0][j];
-    u32[j] = (int32_t)gu[1][j];
-  }
   if (kLate) prefetch_cols(dsm, a.ds_m, I, red);
   const i64 tp = di_exp_tpos_fast(xm, gk);
-  i64 y[VPT];
-  if (DI_LIKELY(tp < ((i64)1 << 23))) {
-    const ExpEst Ee = make_expest(tp);
-#pragma unroll
-    for (int j = 0; j < VPT; ++j) y[j] = wmul(swiglu_elem_est(g32[j], u32[j], Ee), dsm[j]);
-  } else {
-    const ExpR E = make_exp(tp);
-#pragma unroll
-    for (int j = 0; j < VPT; ++j) y[j] = wmul(swiglu_elem_e(g32[j], u32[j], E), dsm[j]);
-  }
   const i64 ym = wmul(xm, xm);
   const i64 yk = wadd(wadd(wadd(gk, uk), 7), a.ds_k);
-  quant_row(y, ym, yk, I, red, a.y8 + (i64)r * I, a.ym + r, a.yk + r, a.defer_fit != 0);
+  int8_t* const y8 = a.y8 + (i64)r * I;
+  if (DI_LIKELY(tp < ((i64)1 << 23))) {
+    // y = g sig u ds_m on fp64: |g sig| <= 2^21 (an int32 product), |g sig u|
+    // <= 2^35, and with |ds_m| < 2^18 the last product is an exact double
+    // below 2^53 (no int64 step wraps); otherwise the thread reports its
+    // values inexact and the row quantises int64 values (ds_m reloaded)
+    constexpr i64 DS_LIM = (i64)1 << 18;
+    const ExpEst Ee = make_expest(tp);
+    double yd[VPT];
+    bool ok = true;
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) {
+      ok = ok && dsm[j] > -DS_LIM && dsm[j] < DS_LIM;
+      yd[j] = (double)(int32_t)swiglu_gsig_est(g32[j], Ee) * (double)u32[j] *
+              (double)(int32_t)dsm[j];
+    }
+    if (DI_LIKELY(quant_row_f64(yd, ok, ym, yk, I, red, y8, a.ym + r, a.yk + r,
+                                a.defer_fit != 0)))
+      return;
+    i64 ds[VPT], y[VPT];
+    prefetch_cols(ds, a.ds_m, I, red);
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) y[j] = wmul(swiglu_elem_est(g32[j], u32[j], Ee), ds[j]);
+    quant_row(y, ym, yk, I, red, y8, a.ym + r, a.yk + r, a.defer_fit != 0);
+  } else {
+    const ExpR E = make_exp(tp);
+    i64 y[VPT];
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) y[j] = wmul(swiglu_elem_e(g32[j], u32[j], E), dsm[j]);
+    quant_row(y, ym, yk, I, red, y8, a.ym + r, a.yk + r, a.defer_fit != 0);
+  }
 }
+
+#ifndef SWIGLU_MINB
+#define SWIGLU_MINB 3
+#endif
 
 // Prefill (256-thread blocks, 8-12 columns per thread): at least three blocks
 // per CU (168 VGPRs; 12 columns spill a few registers) beat two unspilled
 // blocks by ~3 % on a 2048-token prefill (measured; four blocks spill more and
 // lose).
 template <int VPT, int NT = RT_WIDE, bool WARM = false>
-__global__ __launch_bounds__(NT, (NT == 256 && VPT >= 8 && VPT <= 12) ? 3 : 1) void k_swiglu_quant(
+__global__ __launch_bounds__(NT, (NT == 256 && VPT >= 8 && VPT <= 12) ? SWIGLU_MINB : 1) void k_swiglu_quant(
     SwigluArgs a) {
   keep_hidden_args();
   __shared__ i64 red_buf[32];
@@ -1574,6 +1688,13 @@ int detllm_swiglu_quant(const int32_t* P, int nsplit, int64_t split_stride, int 
   a.gate_m = gate_m; a.gate_k = gate_k; a.up_m = up_m; a.up_k = up_k; a.ds_m = ds_m;
   a.ds_k = ds_k; a.y8 = y8; a.ym = ym; a.yk = yk; a.defer_fit = defer_fit;
   a.warm = warm_for(R, next_w, next_n, next_k, next_ksplit);
+#ifdef SWIGLU_PREFILL_WIDE
+  if (R > 64) {
+    DI_WIDE_DISPATCH(I, k_swiglu_quant, dim3(R), s, a);
+    DI_LAUNCH_CHECK();
+    return DI_OK;
+  }
+#endif
   DI_WARM_OR_ROWS(R, I, k_swiglu_quant, s, a);
   DI_LAUNCH_CHECK();
   return DI_OK;

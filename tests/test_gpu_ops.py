@@ -619,3 +619,46 @@ def test_deferred_scale_fit():
     with pytest.raises(RuntimeError, match="code -22"):
         residual(P_o, outs[0][1], outs[0][2], 2)
     torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("R", [3, 100])
+def test_swiglu_quant_every_path(R):
+    """detllm_swiglu_quant (model.py:416-423: requant_i32_common(14) of gate
+    and up, di_swiglu, the ds_m smoothing multiply, quant_i8_pertoken)
+    against the oracle's composition, at decode (3 rows) and prefill (100
+    rows) sizes, on inputs that take each path of the kernel: ordinary
+    mantissas (fp64 chain); a gate mantissa of 2^21 or more (integer
+    requantisation); a ds_m of 2^18 or more (integer quantisation); ds_m
+    near 2^17 with large products (a row maximum of 2^43 or more); a row
+    scale giving tpos >= 2^23 (64-bit DI-Exp); and a zero row."""
+    from idempotent_llm_amd._lib import call
+    rng = np.random.default_rng(93)
+    I = 3072
+    base = dict(gm=rng.integers(1 << 14, 1 << 16, I), um=rng.integers(1 << 14, 1 << 16, I),
+                dsm=rng.integers(1 << 12, 1 << 14, I))
+    cases = {"fp64": {}, "big_gate_m": {"gm_big": True}, "big_ds_m": {"ds_big": True},
+             "row_max_2^43": {"ds_near": True}, "big_tpos": {"xk": 50}}
+    for name, c in cases.items():
+        gm, um, dsm = base["gm"].copy(), base["um"].copy(), base["dsm"].copy()
+        if c.get("gm_big"):
+            gm[17] = 1 << 22
+        if c.get("ds_big"):
+            dsm[5] = (1 << 18) + 3
+        if c.get("ds_near"):
+            dsm[:] = rng.integers((1 << 17) - 1000, 1 << 17, I)
+        P = rng.integers(-(1 << 24), 1 << 24, (R, 2 * I)).astype(np.int32)
+        P[0] = 0
+        xm = rng.integers(1 << 15, 1 << 16, (R, 1)).astype(I64)
+        xk = np.full((R, 1), c.get("xk", 20), I64)
+        gate, ogm, ogk = ody.requant_i32_common(P[:, :I], xm, xk, gm.astype(I64), 20, 14)
+        up, oum, ouk = ody.requant_i32_common(P[:, I:], xm, xk, um.astype(I64), 20, 14)
+        ys, ym, yk = oops.di_swiglu(gate, ogm, ogk, up, oum, ouk)
+        wy, wm, wk = ody.quant_i8_pertoken(ys * dsm.astype(I64), ym, yk + 15)
+        y8 = torch.empty(R, I, dtype=torch.int8, device="cuda")
+        gym = torch.empty(R, dtype=torch.int64, device="cuda")
+        gyk = torch.empty(R, dtype=torch.int64, device="cuda")
+        print(f"[swiglu_quant R={R} {name}]", flush=True)
+        call("detllm_swiglu_quant", g(P[None]), 1, R * 2 * I, R, I, g(xm[:, 0]), g(xk[:, 0]),
+             g(gm.astype(I64)), 20, g(um.astype(I64)), 20, g(dsm.astype(I64)), 15, y8, gym, gyk,
+             None, 0, 0, 0, 0)
+        eq(y8, wy); eq(gym, wm[:, 0]); eq(gyk, wk[:, 0])

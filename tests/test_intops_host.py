@@ -507,3 +507,30 @@ def test_isqrt_est_matches_oracle(lib):
     v = v[(v < (1 << 62))]
     got, _ = _scalar(lib, 8, v)
     assert np.array_equal(got, oim.isqrt(v))
+
+
+def test_f64_integer_helpers(lib):
+    """bitlen_f64 (the fp64 exponent) equals int.bit_length of |x|, and
+    rshift_round_f64 equals rshift_round (intmath.py:120-147, (x + 2^(sh-1))
+    >> sh with floor) for |x| < 2^52 and every shift from 0 to 70, on random
+    magnitudes of every size, exact powers of two and their neighbours, and
+    the halfway cases x = (2j + 1) 2^(sh-1)."""
+    rnd = np.random.default_rng(77)
+    mags = np.concatenate([rnd.integers(0, 1 << 52, 20000),
+                           (1 << rnd.integers(0, 52, 2000)).astype(np.int64)])
+    mags = np.concatenate([mags, np.maximum(mags - 1, 0), np.minimum(mags + 1, (1 << 52) - 1)])
+    sign = np.where(rnd.integers(0, 2, mags.size) == 1, -1, 1)
+    x = (mags * sign).astype(np.int64)
+    out = np.empty_like(x)
+    lib.di_host_f64_int_op(ctypes.c_int(0), _p(x), _p(x), ctypes.c_int64(x.size), _p(out))
+    assert [int(v) for v in out] == [abs(int(v)).bit_length() for v in x]
+    for sh in range(0, 71):
+        xs = x.copy()
+        if 1 <= sh <= 51:   # halfway cases
+            j = rnd.integers(-(1 << (51 - sh)), 1 << (51 - sh), 500)
+            xs = np.concatenate([xs[:5000], ((2 * j + 1) << (sh - 1)).astype(np.int64)])
+        k = np.full(xs.size, sh, dtype=np.int64)
+        lib.di_host_f64_int_op(ctypes.c_int(1), _p(xs), _p(k), ctypes.c_int64(xs.size),
+                               _p(out[:xs.size]))
+        want = [int(v) if sh == 0 else (int(v) + (1 << (sh - 1))) >> sh for v in xs]
+        assert [int(v) for v in out[:xs.size]] == want, sh
