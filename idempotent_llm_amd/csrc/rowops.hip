@@ -264,6 +264,69 @@ __device__ __forceinline__ i64 residual_add_row(i64 (&h)[VPT], i64 k_res, const 
   return residual_renorm_row(h, k_res, red, lg_out);
 }
 
+// requant_i32_common(tb) of a GEMM product, residual_add and the renorm
+// (dyadic.py:108-120, :193-206, :174-184) on exact fp64 values. P holds the
+// product sums (int32 values), cm the column mantissas, h the residual (int32
+// values); on success h holds the renormalised residual, *kr its k and *lg
+// what residual_renorm_row reports. Bounds, each making every intermediate an
+// exact double and matching the int64 steps (no wrap anywhere):
+//  * tb <= 20, |row_m| < 2^31, |col_m| < 2^21: P col_m is below 2^52, the
+//    requantised d below 2^20 + 1, d row_m below 2^52 (rshift_round_f64);
+//  * the alignment shift down <= 63 (rshift_round of |x| < 2^52 by 53..63
+//    gives 0 both ways; from 64 on the int64 form differs) and up <= 52,
+//    with the aligned delta below 2^51, so h + delta is below 2^52 and its
+//    renormalisation is rshift_round_f64 and an exact power-of-two scaling.
+// A row outside them returns false with h untouched (every test is
+// block-uniform: row scalars, or a flag folded into a reduction), and the
+// caller runs the integer routines.
+template <int VPT, class Red>
+__device__ __forceinline__ bool requant_residual_f64(i64 (&h)[VPT], const i64 (&P)[VPT],
+                                                     const i64 (&cm)[VPT], i64 row_m, i64 row_k,
+                                                     i64 col_k, int tb, i64 k_res, Red& red,
+                                                     i64* kr, i64* lg_out) {
+  if (tb > 20 || row_m <= -((i64)1 << 31) || row_m >= ((i64)1 << 31)) return false;
+  constexpr i64 CM_LIM = (i64)1 << 21;
+  double vd[VPT];
+  uint32_t L = 0;
+  bool ok = true;
+#pragma unroll
+  for (int j = 0; j < VPT; ++j) {
+    ok = ok && cm[j] > -CM_LIM && cm[j] < CM_LIM;
+    vd[j] = (double)(int32_t)P[j] * (double)(int32_t)cm[j];
+    L = ::max(L, bitlen_f64(vd[j]));
+  }
+  L = red.max_u32(ok ? L : 64u);
+  if (DI_UNLIKELY(L >= 64u)) return false;
+  const i64 sh = imax(ilog2_from_bitlen(L) - (tb - 1), 0);
+  const i64 dk = wsub(wadd(row_k, col_k), sh);
+  const i64 rel = wsub(dk, k_res);
+  const i64 down = imax(rel, 0), up = imax(wneg(rel), 0);
+  if (down > 63 || up > 52) return false;
+  const double rmd = (double)(int32_t)row_m, upf = ldexp(1.0, (int)up);
+  double hn[VPT];
+  uint32_t L2 = 0;
+  ok = true;
+#pragma unroll
+  for (int j = 0; j < VPT; ++j) {
+    const double d = rshift_round_f64(vd[j], (int)sh);
+    const double al = rshift_round_f64(d * rmd, (int)down) * upf;
+    ok = ok && fabs(al) < 0x1p51;
+    hn[j] = (double)(int32_t)h[j] + al;
+    L2 = ::max(L2, bitlen_f64(hn[j]));
+  }
+  L2 = red.max_u32(ok ? L2 : 64u);
+  if (DI_UNLIKELY(L2 >= 64u)) return false;
+  const i64 lg = ilog2_from_bitlen(L2);
+  const i64 sh_down = imax(lg - 29, 0);
+  const i64 sh_up = sh_down > 0 ? 0 : (L2 > 0 ? imax(26 - lg, 0) : 0);
+  const double upf2 = ldexp(1.0, (int)sh_up);
+#pragma unroll
+  for (int j = 0; j < VPT; ++j) h[j] = (i64)(int32_t)(rshift_round_f64(hn[j], (int)sh_down) * upf2);
+  *kr = wadd(wsub(k_res, sh_down), sh_up);
+  *lg_out = sh_down > 0 ? -1 : ilog2_from_bitlen(L2 > 0 ? L2 + (uint32_t)sh_up : 0u);
+  return true;
+}
+
 // Latency, not bandwidth, bounds these kernels at decode (one block per
 // token row): every helper below issues all of its global loads before the
 // first use, so a kernel waits for one memory round trip instead of one per
@@ -487,8 +550,11 @@ __device__ __forceinline__ void residual_normq_row(const ResNormArgs& a, int r, 
       d[j] = dd[0][j];
       if (red.tid() + j * red.nt() >= C) h[j] = 0;
     }
-    const i64 dk = requant_common_row(d, cm, row_k, a.col_k, a.tb, red);
-    kr = residual_add_row(h, k_res, d, row_m, dk, red, &lg);
+    if (DI_UNLIKELY(!requant_residual_f64(h, d, cm, row_m, row_k, a.col_k, a.tb, k_res, red,
+                                          &kr, &lg))) {
+      const i64 dk = requant_common_row(d, cm, row_k, a.col_k, a.tb, red);
+      kr = residual_add_row(h, k_res, d, row_m, dk, red, &lg);
+    }
   } else {
   prefetch_cols(smv, a.sm_m, C, red);
   if (mode == 2) {

@@ -433,6 +433,69 @@ def test_residual_normq_renorm_branches(C, smooth):
     assert ((top >= 2 ** 26) & (top < 2 ** 30)).any() and (top == 0).any()
 
 
+@pytest.mark.parametrize("big_col", [False, True])
+def test_residual_normq_every_path(big_col):
+    """The GEMM residual add (requant_i32_common(20) + residual_add + renorm)
+    runs on exact doubles for rows whose operands keep every product below
+    2^52 and on int64 routines otherwise. Rows here take each side: an
+    alignment down-shift of 58 (the delta rounds to 0 both ways) and of 70
+    (past 63 torch's shift clamps differ from a rounding: int64 side), an
+    up-shift of 25 (doubles), of 40 (delta above 2^51: int64) and of 60 (the
+    int64 shift wraps), a row mantissa of 2^33 and of -2^31 (int64 side).
+    With big_col one column mantissa is 2^21 (every row on the int64 side);
+    without, one is -(2^21 - 1) (the doubles' limit). Both the row kernel and
+    the decode GEMV with the row kernel fused in are checked against the
+    oracle."""
+    from idempotent_llm_amd._lib import call
+    print(f"[residual_normq every path big_col={big_col}]", flush=True)
+    rng = np.random.default_rng(11 + big_col)
+    R, C, N = 8, 1024, 1024
+    col_m = rng.integers(1 << 15, 1 << 16, C).astype(I64)
+    col_m[C // 2] = (1 << 21) if big_col else -((1 << 21) - 1)
+    k_res = np.full(R, 24, I64)
+    # (row_m, P magnitude, target rel = dk - k_res; None: row_k 20)
+    rows = [(40000, 1 << 20, None), (40000, 1 << 20, 58), (40000, 1 << 20, 70),
+            (3, 4, -25), (3, 4, -40), (3, 4, -60), (1 << 33, 1 << 20, None),
+            (-(1 << 31), 1 << 20, None)]
+    P = np.stack([rng.integers(-p, p + 1, C) for _, p, _ in rows]).astype(np.int32)
+    row_m = np.array([m for m, _, _ in rows], I64)
+    _, _, dk0 = ody.requant_i32_common(P, row_m[:, None], np.zeros((R, 1), I64), col_m, 20,
+                                       target_bits=20)
+    row_k = np.array([20 if rel is None else k_res[i] + rel - dk0[i, 0]
+                      for i, (_, _, rel) in enumerate(rows)], I64)
+    h = rng.integers(-(1 << 26), 1 << 26, (R, C)).astype(np.int32)
+    sm_m = rng.integers(1 << 15, 1 << 16, C).astype(I64)
+    want = _normq_oracle(P, row_m, row_k, col_m, 20, h, k_res, sm_m, 15)
+    # the rows take the shifts named above
+    _, _, dk = ody.requant_i32_common(P, row_m[:, None], row_k[:, None], col_m, 20, 20)
+    rel = dk[:, 0] - k_res
+    assert list(rel[1:6]) == [58, 70, -25, -40, -60]
+    hg, kg = g(h), g(k_res.copy())
+    x8 = torch.empty(R, C, dtype=torch.int8, device="cuda")
+    xm = torch.empty(R, dtype=torch.int64, device="cuda")
+    xk = torch.empty(R, dtype=torch.int64, device="cuda")
+    call("detllm_residual_normq", g(P), 1, 0, R, C, g(row_m), g(row_k), g(col_m), 20, 20, hg,
+         kg, g(sm_m), 15, x8, xm, xk, None, 0, 0, 0, 0)
+    for got, w in zip((hg, kg, x8, xm, xk), want):
+        eq(got, w)
+    # the decode GEMV with this row kernel fused in (partials split in two)
+    w8 = rng.integers(-128, 128, (N, C)).astype(np.int8)
+    P2 = np.stack([P, np.zeros_like(P)]).astype(np.int32)
+    P2[1] = rng.integers(-50, 51, (R, C))
+    P2[0] -= P2[1]
+    ks = 1
+    h_out = torch.full((R, C), -1, dtype=torch.int32, device="cuda")
+    k_out = torch.full((R,), -1, dtype=torch.int64, device="cuda")
+    fm = torch.full((R,), -1, dtype=torch.int64, device="cuda")
+    fk = torch.full((R,), -1, dtype=torch.int64, device="cuda")
+    Cg = torch.full((ks, R, N), -7, dtype=torch.int32, device="cuda")
+    call("detllm_igemv_resnormq", g(w8), Cg, R, N, C, ks, R * N, g(P2), 2, R * C, g(row_m),
+         g(row_k), g(col_m), 20, 20, g(h), g(k_res), h_out, k_out, g(sm_m), 15, fm, fk,
+         None, 0, None, 0)
+    eq(h_out, want[0]); eq(k_out, want[1]); eq(fm, want[3]); eq(fk, want[4])
+    eq(Cg.sum(0), ogemm.int_gemm(want[2], w8.T))
+
+
 def test_igemv_prefetch_variant_same_product():
     """detllm_igemv_nt_pf (skinny GEMM + prefetch hint) gives the product of
     detllm_igemv_nt, with 0-4 ranges of any multiple-of-4 size; bad ranges are
