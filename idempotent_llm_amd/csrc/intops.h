@@ -472,6 +472,20 @@ DI_HD int rhad_est_i8(i64 n, const DivEst& D) {
   return sq < -128 ? -128 : (sq > 127 ? 127 : sq);
 }
 
+// rhad_est_signed and rhad_est_i8 of an integer-valued double (the same
+// integers: the two helpers above convert their int64 operand's magnitude to
+// this double, exactly under their bounds)
+DI_HD int32_t rhad_est_signed_f64(double a, const DivEst& D) {
+  const uint32_t q = rhad_est(fabs(a), D);
+  return a < 0 ? -(int32_t)q : (int32_t)q;
+}
+DI_HD int rhad_est_i8_f64(double n, const DivEst& D) {
+  const double e = fmin(fma(fabs(n), D.r, D.k), 255.0);
+  const int q = (int)(uint32_t)e;
+  const int sq = n < 0 ? -q : q;
+  return sq < -128 ? -128 : (sq > 127 ? 127 : sq);
+}
+
 // rhad(s |a|, d) signed, for s |a| + d < 2^53 and quotients below 2^31: the
 // estimate may be one off once 2 s |a| + d reaches 2^51, so its truncation
 // q0 is corrected with the exact remainder s |a| + floor(d/2) - q0 d (all

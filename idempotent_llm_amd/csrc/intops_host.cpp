@@ -52,7 +52,9 @@ void di_host_scalar(int op, const int64_t* a, const int64_t* b, const int64_t* c
 void di_host_f64_int_op(int op, const int64_t* a, const int64_t* b, int64_t n, int64_t* out) {
   for (int64_t i = 0; i < n; ++i) {
     if (op == 0) out[i] = (int64_t)bitlen_f64((double)a[i]);
-    else out[i] = (int64_t)rshift_round_f64((double)a[i], (int)b[i]);
+    else if (op == 1) out[i] = (int64_t)rshift_round_f64((double)a[i], (int)b[i]);
+    else if (op == 2) out[i] = rhad_est_i8_f64((double)a[i], make_divest(b[i], 1.0));
+    else out[i] = rhad_est_signed_f64((double)a[i], make_divest(b[i], 127.0));
   }
 }
 void di_host_di_exp_neg(const int64_t* neg, const int64_t* tpos, int64_t n, int64_t* out) {

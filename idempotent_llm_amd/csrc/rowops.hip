@@ -973,7 +973,10 @@ __global__ __launch_bounds__(RT) void k_qkv_epilogue(QKVArgs a) {
 
 // Many token rows (prefill): one wave per (head slot, 4 rows), head-major so
 // a block's waves share a head's scale vectors.
-__global__ __launch_bounds__(RT) void k_qkv_epilogue_rows(QKVArgs a, int R, int ngroups) {
+#ifndef QKV_ROWS_MINW
+#define QKV_ROWS_MINW 1
+#endif
+__global__ __launch_bounds__(RT, QKV_ROWS_MINW) void k_qkv_epilogue_rows(QKVArgs a, int R, int ngroups) {
   keep_hidden_args();
   const int heads = a.n_q + 2 * a.n_kv;
   const int wg = blockIdx.x * 4 + (threadIdx.x >> 6);

@@ -11,7 +11,7 @@ import pytest
 import torch
 
 from idempotent_llm_amd import artifact as art
-from pagedcache import paged
+from pagedcache import paged, unpaged
 
 pytestmark = pytest.mark.gpu
 I64 = torch.int64
@@ -443,3 +443,150 @@ def test_qkv_epilogue_q_int64_min(B, T):
     small = (np.abs(np.where(q == np.iinfo(np.int64).min, 0, q)).max(axis=-1) < (1 << 43))
     assert (hit & small).any()      # some heads take INT64_MIN with a maximum below 2^43
     np.testing.assert_array_equal(n(q8), want)
+
+
+def _qkv_oracle(P, xm, xk, pos, prm, B, T, nq, nkv):
+    """model.py:303-358 on the oracle: q8 and tpos of the Q heads, the K and
+    V cache rows (k8, v8 [B, n_kv, T, 128]) of one Q/K/V product."""
+    from oracle import dyadic as ody, ops as oops
+    n = lambda t: t.cpu().numpy() if torch.is_tensor(t) else np.asarray(t)
+    hd, g = 128, nq // nkv
+    Pn = n(P)[0].astype(np.int64).reshape(B, T, nq + 2 * nkv, hd)
+    xm4, xk4 = n(xm).reshape(B, T, 1, 1), n(xk).reshape(B, T, 1, 1)
+    pos = n(pos).reshape(B, T)
+
+    def head_pipeline(Ph, wm, wk, gm, gk, nh):
+        y, _, _ = ody.requant_i32_common(Ph, xm4, xk4, n(wm).reshape(nh, hd), wk,
+                                         target_bits=16)
+        yn, kout = oops.di_rmsnorm_gamma(y, n(gm), gk)
+        yn = yn.transpose(0, 2, 1, 3)
+        pb = np.broadcast_to(pos[:, None, :], (B, nh, T))
+        return oops.apply_int_rope(yn, n(prm["cos"]), n(prm["sin"]), pb), kout
+
+    with np.errstate(over="ignore"):
+        yq, qkk = head_pipeline(Pn[:, :, :nq], prm["q_m"], prm["q_k"], prm["q_norm_m"],
+                                prm["q_norm_k"], nq)
+        q = yq * np.repeat(n(prm["qs_m"]).reshape(nkv, hd), g, axis=0)[None, :, None, :]
+        one = np.ones((B, nq, T, 1), np.int64)
+        q8, qm, qk = ody.quant_i8_pertoken(q, one, np.zeros_like(one) + qkk + prm["qs_k"])
+        ks_m = np.repeat(n(prm["ks_m"]), g).reshape(1, nq, 1, 1)
+        ks_k = np.repeat(n(prm["ks_k"]), g).reshape(1, nq, 1, 1)
+        sm, sk = ody.norm_scale(qm * ks_m, qk + ks_k)
+        tpos = oops.di_exp_tpos(sm, sk)[..., 0]
+        yk, _ = head_pipeline(Pn[:, :, nq:nq + nkv], prm["k_m"], prm["k_k"], prm["k_norm_m"],
+                              prm["k_norm_k"], nkv)
+        k8 = ody.requant_i8_static(yk, 1, 20 + prm["k_norm_k"], 1, 0,
+                                   n(prm["kq_m"]).reshape(1, nkv, 1, hd),
+                                   n(prm["kq_k"]).reshape(1, nkv, 1, hd))
+        v8 = ody.requant_i8_static(Pn[:, :, nq + nkv:], xm4, xk4, n(prm["v_m"]).reshape(nkv, hd),
+                                   prm["v_k"], n(prm["vq_m"]).reshape(1, 1, nkv, 1),
+                                   n(prm["vq_k"]).reshape(1, 1, nkv, 1))
+    return q8, tpos, k8, v8.transpose(0, 2, 1, 3), q
+
+
+def _plant(prm, variant, nq, nkv):
+    """Channel constants that send heads or lanes to the integer routines of
+    the Q/K/V epilogue ("ranges"), or every Q head ("gamma"); "none" keeps the
+    artifact's (the fp64 paths, with about a third of the Q heads above the
+    2^43 maximum)."""
+    prm = dict(prm)
+    hd = 128
+    cl = lambda k: prm[k].clone()
+    if variant == "ranges":
+        q_m, k_m, v_m, qs_m, kq_m, kq_k = (cl(k) for k in ("q_m", "k_m", "v_m", "qs_m", "kq_m",
+                                                           "kq_k"))
+        q_m[1 * hd + 5] = 1 << 21               # Q head 1: P w_m beyond the doubles
+        k_m[0 * hd + 70] = -(1 << 21)           # K head 0
+        v_m[1 * hd + 3] = 1 << 22               # V head 1: one lane per row
+        qs_m[2 * hd + 0] = 1 << 15              # Q heads of kv head 2: smoothing too large
+        qs_m[3 * hd:4 * hd] = (1 << 14) + 3     # Q heads of kv head 3: maxima near 2^50
+        kq_k[4 * hd + 7] = 20 + prm["k_norm_k"] + 20   # K head 4 channel 7: n above 2^49
+        kq_m[5 * hd + 9] = 1 << 50              # K head 5 channel 9: divisor above 2^49
+        prm.update(q_m=q_m, k_m=k_m, v_m=v_m, qs_m=qs_m, kq_m=kq_m, kq_k=kq_k)
+    elif variant == "gamma":
+        g = cl("q_norm_m")
+        g[9] = 1 << 12                          # every Q head: gamma beyond the doubles
+        prm["q_norm_m"] = g
+    return prm
+
+
+@pytest.mark.parametrize("variant", ["none", "ranges", "gamma"])
+@pytest.mark.parametrize("B,T", [(4, 1), (2, 40), (1, 100)])
+def test_qkv_epilogue_every_path(variant, B, T):
+    """The Q/K/V epilogue's exact fp64 paths and their integer fallbacks
+    against the oracle (model.py:303-358: _qk_head_pipeline, QK smoothing,
+    quant_i8_pertoken, the score scale's tpos, requant_i8_static of K and V),
+    in the one-token layout (B, T = 1: one wave per head) and the rows layout
+    (R > 64: four rows per wave), with the K divisor estimates derived per
+    element and precomputed; zero product heads (the normalisation's zero
+    case), rows with a row mantissa beyond 2^40 (V numerators that wrap) and
+    the planted channels of _plant. The fused decode kernel writes the same
+    cache bytes and attention output as the separate launches."""
+    from idempotent_llm_amd._lib import call
+    print(f"[qkv epilogue every path {variant} B={B} T={T}]", flush=True)
+    dims = art.MID
+    nq, nkv, hd = dims["n_q_heads"], dims["n_kv_heads"], 128
+    prm = _plant(_layer_params(dims, 6), variant, nq, nkv)
+    rnd = torch.Generator().manual_seed(B * 1000 + T)
+    R = B * T
+    P = torch.randint(-(1 << 19), 1 << 19, (1, R, (nq + 2 * nkv) * hd), generator=rnd,
+                      dtype=torch.int32)
+    P[0, 0, 9 * hd:10 * hd] = 0                 # Q head 9 of row 0: a zero head
+    P[0, R - 1, (nq + 6) * hd:(nq + 7) * hd] = 0   # K head 6 of the last row
+    P = P.cuda()
+    xm = torch.randint(1 << 15, 1 << 16, (R,), generator=rnd, dtype=I64)
+    xm[R // 2] = (1 << 40) + 7                  # V numerators of this row wrap
+    xm = xm.cuda()
+    xk = torch.randint(22, 30, (R,), generator=rnd, dtype=I64).cuda()
+    pos = torch.randint(0, dims["max_pos"], (R,), generator=rnd, dtype=I64).cuda()
+    want_q8, want_tpos, want_k, want_v, q = _qkv_oracle(P, xm, xk, pos, prm, B, T, nq, nkv)
+    big = np.abs(q).max(axis=-1) >= (1 << 43)   # the Q maxima take both quotient forms
+    if variant == "ranges" or R >= 64:
+        assert big.any() and (~big).any()
+    common = (prm["q_m"], prm["q_k"], prm["k_m"], prm["k_k"], prm["v_m"], prm["v_k"],
+              prm["q_norm_m"], prm["q_norm_k"], prm["k_norm_m"], prm["k_norm_k"], prm["qs_m"],
+              prm["qs_k"], prm["kq_m"], prm["kq_k"], prm["ks_m"], prm["ks_k"], prm["vq_m"],
+              prm["vq_k"], prm["cos"], prm["sin"], prm["cos"].shape[0])
+    est = torch.empty(prm["kq_m"].numel(), 4, dtype=I64, device="cuda")
+    call("detllm_kq_est", prm["kq_m"], prm["kq_k"], prm["kq_m"].numel(),
+         20 + prm["k_norm_k"], est)
+    cap = 128
+    for e in (None, est):
+        q8 = torch.full((B, nq, T, hd), 99, dtype=torch.int8, device="cuda")
+        tpos = torch.full((B, nq, T), -1, dtype=I64, device="cuda")
+        kc, vc, table, width = paged(torch.zeros(B, nkv, cap, hd, dtype=torch.int8),
+                                     torch.zeros(B, nkv, hd, cap, dtype=torch.int8), seed=T)
+        call("detllm_qkv_epilogue", P, 1, R * P.shape[2], B, T, nq, nkv, xm, xk, pos, *common,
+             q8, tpos, None, kc, vc, table, width, None, 0, e, None)
+        torch.cuda.synchronize()
+        k, v = unpaged(kc, vc, table, T)
+        np.testing.assert_array_equal(q8.cpu().numpy(), want_q8)
+        np.testing.assert_array_equal(tpos.cpu().numpy(), want_tpos)
+        np.testing.assert_array_equal(k.cpu().numpy(), want_k)
+        np.testing.assert_array_equal(v.cpu().numpy(), want_v)
+    if T == 1:
+        # the fused decode kernel (Q/K/V epilogue + attention) on the same
+        # product, against the separate launches over a random cache
+        slot, S = 50, 51
+        k0 = torch.randint(-128, 128, (B, nkv, cap, hd), generator=rnd, dtype=torch.int8)
+        v0 = torch.randint(-128, 128, (B, nkv, hd, cap), generator=rnd, dtype=torch.int8)
+        valid = torch.ones(B, cap, dtype=torch.bool)
+        k0, v0, table, width, valid = paged(k0, v0, valid, seed=3)
+        vbytes = valid.view(torch.uint8)
+        ka, va = k0.clone(), v0.clone()
+        q8 = torch.empty(B, nq, 1, hd, dtype=torch.int8, device="cuda")
+        tpos = torch.empty(B, nq, 1, dtype=I64, device="cuda")
+        out_a = torch.empty(B, nq * hd, dtype=I64, device="cuda")
+        call("detllm_qkv_epilogue", P, 1, R * P.shape[2], B, 1, nq, nkv, xm, xk, pos, *common,
+             q8, tpos, None, ka, va, table, width, None, slot, None, None)
+        call("detllm_attn_decode", q8, tpos, ka, va, table, width, vbytes, width * 128, B, S,
+             nq, nkv, None, None, out_a, None)
+        kb, vb = k0.clone(), v0.clone()
+        out_b = torch.empty(B, nq * hd, dtype=I64, device="cuda")
+        call("detllm_qkv_attn_decode", P, 1, R * P.shape[2], B, nq, nkv, xm, xk, pos, *common,
+             kb, vb, table, width, None, slot, vbytes, width * 128, S, None, None, out_b, None)
+        torch.cuda.synchronize()
+        assert torch.equal(ka, kb) and torch.equal(va, vb) and torch.equal(out_a, out_b)
+        k, v = unpaged(ka, va, table, S)
+        np.testing.assert_array_equal(k[:, :, slot].cpu().numpy(), want_k[:, :, 0])
+        np.testing.assert_array_equal(v[:, :, slot].cpu().numpy(), want_v[:, :, 0])

@@ -534,3 +534,31 @@ def test_f64_integer_helpers(lib):
                                _p(out[:xs.size]))
         want = [int(v) if sh == 0 else (int(v) + (1 << (sh - 1))) >> sh for v in xs]
         assert [int(v) for v in out[:xs.size]] == want, sh
+
+
+def test_f64_division_estimates(lib):
+    """rhad_est_i8_f64 equals clamp_i8(rhad(n, d)) and rhad_est_signed_f64
+    equals sign(a) rhad(127 |a|, d) (intmath.py:60-80 rhad, :150-153 clamp)
+    on integer-valued doubles within the estimates' bounds (2 |n| + d and
+    2 127 |a| + d below 2^51): random magnitudes of every size, exact
+    multiples of the divisor, the halfway cases, and every divisor size."""
+    rnd = np.random.default_rng(78)
+    n = 40000
+    d = np.concatenate([rnd.integers(1, 64, n // 4), (1 << rnd.integers(0, 48, n // 4)),
+                        rnd.integers(1, 1 << 48, n // 2)]).astype(np.int64)
+    rnd.shuffle(d)
+    # clamp_i8(rhad(n, d)): quotients around the clamp and far beyond it
+    q = rnd.integers(-300, 301, n)
+    r = np.where(rnd.integers(0, 3, n) == 0, d // 2, rnd.integers(0, np.maximum(d, 1)))
+    num = q * d + np.where(q < 0, -r, r)
+    num = np.where(np.abs(num) < (1 << 49), num, rnd.integers(-(1 << 40), 1 << 40, n))
+    out = np.empty_like(num)
+    lib.di_host_f64_int_op(ctypes.c_int(2), _p(num), _p(d), ctypes.c_int64(n), _p(out))
+    want = [max(-128, min(127, _py_rhad(int(a), int(b)))) for a, b in zip(num, d)]
+    assert [int(v) for v in out] == want
+    # sign(a) rhad(127 |a|, d) with |a| <= d (quantiser quotients <= 127)
+    a = (rnd.random(n) * d).astype(np.int64) * np.where(rnd.integers(0, 2, n) == 1, -1, 1)
+    a = np.where(rnd.integers(0, 4, n) == 0, np.sign(a) * d, a).astype(np.int64)
+    lib.di_host_f64_int_op(ctypes.c_int(3), _p(a), _p(d), ctypes.c_int64(n), _p(out))
+    want = [(-1 if v < 0 else 1) * _py_rhad(127 * abs(int(v)), int(b)) for v, b in zip(a, d)]
+    assert [int(v) for v in out] == want
