@@ -140,6 +140,11 @@ def _pack(L: LayerWeights, names) -> torch.Tensor:
 
 
 class IntQwen3:
+    # decode steps of at most this many rows run the fused-operand GEMVs
+    # (the skinny GEMM's operand row kernel inside it, one launch fewer per
+    # row kernel); more rows run the separate row kernels
+    fused_decode_rows = 1
+
     def __init__(self, artifact_dir: str, backend: str = "rocm"):
         from safetensors.torch import load_file
         self.backend = canonical_backend(backend)
@@ -222,11 +227,12 @@ class IntQwen3:
         # decode rows run the fused-operand GEMVs where their shapes allow
         L0 = self.layers[0]
         nqkv, nqh = L0.wqkv.shape[0], self.n_q * self.hd
-        self._fused_decode = (
-            self.hidden <= 1024 and nqh <= 2048
-            and pro_fits(self.hidden, self._ksplit(nqkv, self.hidden))
-            and pro_fits(nqh, self._ksplit(self.hidden, nqh))
-            and pro_fits(self.hidden, self._ksplit(2 * self.inter, self.hidden)))
+        self._fused_decode = {
+            M: (self.hidden <= 1024 and nqh <= 2048
+                and pro_fits(self.hidden, self._ksplit(nqkv, self.hidden, M))
+                and pro_fits(nqh, self._ksplit(self.hidden, nqh, M))
+                and pro_fits(self.hidden, self._ksplit(2 * self.inter, self.hidden, M)))
+            for M in (1, 2)}
         # device error word of the index checks the reference does on the
         # host (IndexError from embed_e8[ids] / cos_t[positions]); the
         # kernels OR bits into it, raise_if_device_error() reads it
@@ -332,10 +338,11 @@ class IntQwen3:
                 cache.valid_buf[:, S_past:S] = chunk_valid.to(dev)
         H, R = self.hidden, B * T
         # one decode row: the GEMVs run their operand's row kernel themselves
-        # (at 2+ rows the fused prologue gives each row one wave, whose
-        # 64-bit chain over 16+ columns per lane outlasts the separate
-        # launches: c3 b8 2.35 vs 1.94 ms per step, b1 1.64 vs 1.80)
-        fused = T == 1 and R == 1 and self._fused_decode
+        # (at 2+ rows the fused prologue gives each row one wave, whose chain
+        # over 16+ columns per lane outlasts the separate launches: c3 b8
+        # 2.38 vs 1.53 ms per step, b1 1.30 vs 1.64 the other way round)
+        fused = (T == 1 and R <= self.fused_decode_rows
+                 and self._fused_decode[1 if R == 1 else 2])
         # the fused decode stack double-buffers the residual (h = buffer 0)
         hb = torch.empty(2 if fused else 1, R, H, dtype=torch.int32, device=dev)
         kb = torch.empty(2 if fused else 1, R, dtype=I64, device=dev)
