@@ -191,6 +191,57 @@ __device__ __forceinline__ bool quant_row_f64(const double (&v)[VPT], bool ok, i
   return true;
 }
 
+// rmsnorm_row, the smoothing product (sm: the row's smoothing mantissas when
+// smooth) and quant_row(., 1, kq) of an int32-valued row h, on exact fp64
+// values: the normalisation shift is a power-of-two scaling plus
+// rshift_round_f64, the shifted values (|x| <= 2^26) square in int64 exactly
+// as rmsnorm_row's (wrapping) sum does, and with rms > 2^16 the quotients
+// rhad(x 2^20, rms) come from the same fp64 estimate, below 2^30 in
+// magnitude; a smoothing mantissa below 2^21 keeps each product an exact
+// double below 2^51 for quant_row_f64. Returns false (block-uniform, h
+// untouched, nothing stored) when rms <= 2^16 (a zero row, or a sum of
+// squares that wrapped): the caller runs the integer routines. A smoothing
+// mantissa out of range makes the quantiser run on int64 products.
+template <int VPT, class Red>
+__device__ __forceinline__ bool norm_quant_row_f64(const i64 (&h)[VPT], int C, Red& red, i64 lg,
+                                                   const i64 (&sm)[VPT], bool smooth, i64 kq,
+                                                   int8_t* out, i64* m_out, i64* k_out) {
+  if (lg < 0) lg = row_ilog2_absmax(h, red);
+  const i64 sh = 25 - lg;
+  const int up = (int)imax(sh, 0), down = (int)imax(-sh, 0);
+  const double su = ldexp(1.0, up);
+  double x[VPT];
+  i64 ss = 0;
+#pragma unroll
+  for (int j = 0; j < VPT; ++j) {
+    x[j] = rshift_round_f64((double)(int32_t)h[j], down) * su;
+    const int32_t xi = (int32_t)x[j];
+    ss = wadd(ss, (i64)xi * xi);
+  }
+  ss = red.sum(ss);
+  const i64 mean = (C & (C - 1)) == 0 ? rhad_pow2(ss, (int)ilog2(C)) : rhad(ss, (i64)C);
+  const i64 rms = imax(isqrt_wave(mean), 1);
+  if (DI_UNLIKELY(rms <= ((i64)1 << 16))) return false;
+  const DivEst D = make_divest(rms, 1048576.0);
+  constexpr i64 SM_LIM = (i64)1 << 21;
+  bool ok = true;
+#pragma unroll
+  for (int j = 0; j < VPT; ++j) {
+    x[j] = (double)rhad_est_signed_f64(x[j], D);
+    if (smooth) {
+      ok = ok && sm[j] > -SM_LIM && sm[j] < SM_LIM;
+      x[j] *= (double)(int32_t)sm[j];
+    }
+  }
+  if (DI_LIKELY(quant_row_f64(x, ok, 1, kq, C, red, out, m_out, k_out))) return true;
+  i64 y[VPT];
+#pragma unroll
+  for (int j = 0; j < VPT; ++j) y[j] = wmul((i64)rhad_est_signed_f64(
+      rshift_round_f64((double)(int32_t)h[j], down) * su, D), sm[j]);
+  quant_row(y, 1, kq, C, red, out, m_out, k_out);
+  return true;
+}
+
 // dyadic.py:108-120: v holds P on entry, y (int32 values) on exit; cm holds
 // col_m of this thread's columns (0 past C); returns k_out
 template <int VPT, class Red>
@@ -610,15 +661,17 @@ __device__ __forceinline__ void residual_normq_row(const ResNormArgs& a, int r, 
     if (red.tid() == 0) a.k_res[r] = kr;
   }
   if (a.x8 == nullptr) return;
+  const i64 kq = a.sm_m != nullptr ? wadd(20, a.sm_k) : 20;
+  int8_t* const x8 = a.x8 + (i64)r * (a.x8_stride ? a.x8_stride : C);
+  if (DI_LIKELY(norm_quant_row_f64(h, C, red, lg, smv, a.sm_m != nullptr, kq, x8,
+                                   a.xm ? a.xm + r : nullptr, a.xk ? a.xk + r : nullptr)))
+    return;
   rmsnorm_row(h, C, red, lg);
-  i64 kq = 20;
   if (a.sm_m != nullptr) {
 #pragma unroll
     for (int j = 0; j < VPT; ++j) h[j] = wmul(h[j], smv[j]);
-    kq += a.sm_k;
   }
-  quant_row(h, 1, kq, C, red, a.x8 + (i64)r * (a.x8_stride ? a.x8_stride : C),
-            a.xm ? a.xm + r : nullptr, a.xk ? a.xk + r : nullptr);
+  quant_row(h, 1, kq, C, red, x8, a.xm ? a.xm + r : nullptr, a.xk ? a.xk + r : nullptr);
 }
 
 template <int VPT, int NT = RT_WIDE, bool WARM = false, int MODE = -1>

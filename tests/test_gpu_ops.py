@@ -725,3 +725,39 @@ def test_swiglu_quant_every_path(R):
              g(gm.astype(I64)), 20, g(um.astype(I64)), 20, g(dsm.astype(I64)), 15, y8, gym, gyk,
              None, 0, 0, 0, 0)
         eq(y8, wy); eq(gym, wm[:, 0]); eq(gyk, wk[:, 0])
+
+
+@pytest.mark.parametrize("C", [1024, 3072])
+@pytest.mark.parametrize("big_sm", [False, True])
+def test_norm_quant_every_path(C, big_sm):
+    """_norm_quant (model.py:187-198: di_rmsnorm, the smoothing product,
+    quant_i8_pertoken) through detllm_norm_quant against the oracle, on rows
+    that take each side of the row kernel's fp64 path: random rows of every
+    magnitude (up- and down-shifts of the normalisation), a zero row (rms 1:
+    the integer routines), a one-hot row, and at 3072 columns a row of
+    near-maximal values whose sum of squares passes 2^63 and wraps as
+    torch's does. With big_sm one smoothing mantissa is 2^21 (the quantiser
+    on int64 products); without, one is -(2^21 - 1)."""
+    from idempotent_llm_amd._lib import call
+    print(f"[norm_quant every path C={C} big_sm={big_sm}]", flush=True)
+    rng = np.random.default_rng(C + 5 * big_sm)
+    scale = [2 ** 12, 2 ** 20, 2 ** 29 - 3, 2 ** 30, 0, 0, 2 ** 25, 7]
+    R = len(scale)
+    h = np.stack([rng.integers(-s, s + 1, C) if s else np.zeros(C, I64) for s in scale])
+    h[5, C // 2] = -3                                  # one-hot
+    if C == 3072:
+        h[3] = np.where(rng.integers(0, 2, C) == 1, 1, -1) * ((1 << 30) - 1)
+    h = h.astype(np.int32)
+    sm_m = rng.integers(1 << 15, 1 << 16, C).astype(I64)
+    sm_m[C // 3] = (1 << 21) if big_sm else -((1 << 21) - 1)
+    y = oops.di_rmsnorm(h).astype(I64) * sm_m
+    if C == 3072:
+        xp = oim.rshift_round(h[3].astype(I64), 4)       # the shift to [2^25, 2^26]
+        assert sum(int(v) * int(v) for v in xp) >= 1 << 63  # the sum of squares wraps
+    kq = np.full((R, 1), 20 + 15, I64)
+    want = ody.quant_i8_pertoken(y, np.ones_like(kq), kq)
+    x8 = torch.empty(R, C, dtype=torch.int8, device="cuda")
+    xm = torch.empty(R, dtype=torch.int64, device="cuda")
+    xk = torch.empty(R, dtype=torch.int64, device="cuda")
+    call("detllm_norm_quant", g(h), R, C, g(sm_m), 15, x8, xm, xk)
+    eq(x8, want[0]); eq(xm, want[1][:, 0]); eq(xk, want[2][:, 0])
