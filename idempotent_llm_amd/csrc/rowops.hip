@@ -699,6 +699,18 @@ __global__ __launch_bounds__(NT) void k_residual_add_normq(ResNormArgs a) {
   residual_normq_row<VPT, BlockRed, 1>(a, (int)blockIdx.x - (WARM ? L2WARM_BLOCKS : 0), red);
 }
 
+// Many rows (prefill): one wave per row, four rows per block, every
+// reduction a DPP reduction within the wave (no LDS round trip, no barrier),
+// so more rows are in flight per CU than with a block per row.
+template <int VPT, int MODE>
+__global__ __launch_bounds__(256) void k_residual_normq_w(ResNormArgs a, int R) {
+  keep_hidden_args();
+  const int r = (int)blockIdx.x * 4 + (int)(threadIdx.x >> 6);
+  if (r >= R) return;  // whole waves
+  WaveRed red;
+  residual_normq_row<VPT, WaveRed, MODE>(a, r, red);
+}
+
 struct SwigluArgs {
   int I;
   int nt;    // threads per block (set by the launch)
@@ -1659,6 +1671,22 @@ void launch_pro(const ProGemv& g, int ni, int ksplit, const ResNormArgs& ra, con
     }                                                                                        \
   } while (0)
 
+// The wave-per-row launch of a prefill-sized residual / norm-quant call
+// (R > 64 rows of C = 512 or 1024 columns); false: the caller launches the
+// block-per-row kernel.
+template <int MODE>
+static bool rows_wave_launch(int R, int C, hipStream_t s, ResNormArgs& a) {
+#ifdef ROWS_BLOCK
+  return false;
+#endif
+  if (R <= 64 || (C != 512 && C != 1024)) return false;
+  a.nt = 64;
+  const dim3 grid((unsigned)((R + 3) / 4));
+  if (C == 1024) hipLaunchKernelGGL((k_residual_normq_w<16, MODE>), grid, dim3(256), 0, s, a, R);
+  else hipLaunchKernelGGL((k_residual_normq_w<8, MODE>), grid, dim3(256), 0, s, a, R);
+  return true;
+}
+
 extern "C" {
 
 // ---------------------------------------------------------------- model path
@@ -1702,7 +1730,7 @@ int detllm_residual_normq(const int32_t* P, int nsplit, int64_t split_stride, in
   a.col_m = col_m; a.col_k = col_k; a.tb = tb;
   a.h = h; a.k_res = k_res; a.sm_m = sm_m; a.sm_k = sm_k; a.x8 = x8; a.xm = xm; a.xk = xk;
   a.warm = warm_for(R, next_w, next_n, next_k, next_ksplit);
-  DI_WARM_OR_ROWS(R, C, k_residual_add_normq, s, a);
+  if (!rows_wave_launch<1>(R, C, s, a)) DI_WARM_OR_ROWS(R, C, k_residual_add_normq, s, a);
   DI_LAUNCH_CHECK();
   return DI_OK;
 }
@@ -1790,7 +1818,7 @@ int detllm_norm_quant(const int32_t* h, int R, int C, const int64_t* sm_m, int64
   ResNormArgs a{};
   a.C = C; a.mode = 2; a.h = const_cast<int32_t*>(h); a.sm_m = sm_m; a.sm_k = sm_k;
   a.x8 = x8; a.xm = xm; a.xk = xk;
-  DI_ROWS_DISPATCH(R, C, k_residual_normq, dim3(R), s, a);
+  if (!rows_wave_launch<2>(R, C, s, a)) DI_ROWS_DISPATCH(R, C, k_residual_normq, dim3(R), s, a);
   DI_LAUNCH_CHECK();
   return DI_OK;
 }
