@@ -618,15 +618,6 @@ DI_HD uint32_t bitlen_f64(double x) {
 #endif
 }
 
-// rshift_round(x, sh) (intmath.py:120-147: (x + 2^(sh-1)) >> sh, floor) for an
-// integer-valued double with |x| < 2^52 and 0 <= sh < 1000: x 2^-sh is exact
-// (a power-of-two scaling), a multiple of 2^-sh below 2^(52-sh) in magnitude,
-// so adding 1/2 in the fma stays exact (the sum is below 2^(53-sh) and a
-// multiple of 2^-sh), and floor gives the integer.
-DI_HD double rshift_round_f64(double x, int sh) {
-  return sh == 0 ? x : floor(fma(x, ldexp(1.0, -sh), 0.5));
-}
-
 // The bit pattern of a non-negative double as an int64 orders like the
 // double, so a block maximum of magnitudes reduces these patterns.
 DI_HD i64 f64_bits(double x) {
@@ -639,6 +630,29 @@ DI_HD double f64_from_bits(i64 b) {
   __builtin_memcpy(&x, &b, 8);
   return x;
 }
+
+// rshift_round(x, sh) (intmath.py:120-147: (x + 2^(sh-1)) >> sh, floor) for an
+// integer-valued double with |x| < 2^52 and 0 <= sh < 1000: x 2^-sh is exact
+// (a power-of-two scaling), a multiple of 2^-sh below 2^(52-sh) in magnitude,
+// so adding 1/2 in the fma stays exact (the sum is below 2^(53-sh) and a
+// multiple of 2^-sh), and floor gives the integer. At sh = 0 that is
+// floor(x + 1/2) = x, the identity rshift_round keeps for a zero shift.
+DI_HD double rshift_round_f64(double x, int sh) {
+  return floor(fma(x, ldexp(1.0, -sh), 0.5));
+}
+
+// The bit length of max |x| over integer-valued doubles (|x| < 2^53) from the
+// high words of their bit patterns: the high word of |x| (sign bit cleared)
+// orders like |x| up to ties within one exponent, so the maximum of the high
+// words over a row holds the largest biased exponent e, and the bit length
+// is e - 1022 (0 for a row of zeros). One AND and one 32-bit maximum per
+// element. The high word of +inf (0x7FF00000) reads 1025: a row that enters
+// it is marked inexact (any bit length of 64 or more).
+DI_HD uint32_t f64_hiword_abs(double x) {
+  return (uint32_t)((uint64_t)f64_bits(x) >> 32) & 0x7FFFFFFFu;
+}
+DI_HD uint32_t bitlen_from_hiword(uint32_t hw) { return hw == 0u ? 0u : (hw >> 20) - 1022u; }
+
 
 // ops/di_swiglu.py:39-58 on one element for |g|, |u| <= 2^14 (gate and up
 // after requant_i32_common(14)) and tpos < 2^23: |g| < 2^22 for dexp_est,

@@ -54,6 +54,7 @@ void di_host_f64_int_op(int op, const int64_t* a, const int64_t* b, int64_t n, i
     if (op == 0) out[i] = (int64_t)bitlen_f64((double)a[i]);
     else if (op == 1) out[i] = (int64_t)rshift_round_f64((double)a[i], (int)b[i]);
     else if (op == 2) out[i] = rhad_est_i8_f64((double)a[i], make_divest(b[i], 1.0));
+    else if (op == 4) out[i] = (int64_t)bitlen_from_hiword(f64_hiword_abs((double)a[i]));
     else out[i] = rhad_est_signed_f64((double)a[i], make_divest(b[i], 127.0));
   }
 }

@@ -174,28 +174,28 @@ __device__ __forceinline__ bool qk_head_f64(bool is_q, const int32_t (&p)[N],
   constexpr i64 WM_LIM = (i64)1 << 21, G_LIM = (i64)1 << 12, QS_LIM = (i64)1 << 15;
   const HeadRed<WAVE> red;
   double y[N];
-  uint32_t L = 0;
+  uint32_t pm = 0u;
   bool ok = true;
 #pragma unroll
   for (int i = 0; i < N; ++i) {
     ok = ok && wm[i] > -WM_LIM && wm[i] < WM_LIM && gm[i] > -G_LIM && gm[i] < G_LIM &&
          (!is_q || (qs[i] > -QS_LIM && qs[i] < QS_LIM));
     y[i] = (double)p[i] * (double)(int32_t)wm[i];
-    L = ::max(L, bitlen_f64(y[i]));
+    pm = ::max(pm, f64_hiword_abs(y[i]));
   }
-  L = red.max_u32(ok ? L : 64u);
+  const uint32_t L = bitlen_from_hiword(red.max_u32(ok ? pm : 0x7FF00000u));
   if (DI_UNLIKELY(L >= 64u)) return false;
   // requant_i32_common(tb = 16) per (token, head)
   const int sh = (int)imax(ilog2_from_bitlen(L) - 15, 0);
-  uint32_t L2 = 0;
+  uint32_t ym = 0u;
   double ss = 0.0;
 #pragma unroll
   for (int i = 0; i < N; ++i) {
     y[i] = rshift_round_f64(y[i], sh);
-    L2 = ::max(L2, bitlen_f64(y[i]));
+    ym = ::max(ym, f64_hiword_abs(y[i]));
     ss = fma(y[i], y[i], ss);
   }
-  L2 = red.max_u32(L2);
+  const uint32_t L2 = bitlen_from_hiword(red.max_u32(ym));
   ss = red.sum(ss);
   // di_rmsnorm (ops/di_rmsnorm.py:33-52) with the up-shift u
   const int u = 25 - (int)ilog2_from_bitlen(L2);

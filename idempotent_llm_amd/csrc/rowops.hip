@@ -338,15 +338,15 @@ __device__ __forceinline__ bool requant_residual_f64(i64 (&h)[VPT], const i64 (&
   if (tb > 20 || row_m <= -((i64)1 << 31) || row_m >= ((i64)1 << 31)) return false;
   constexpr i64 CM_LIM = (i64)1 << 21;
   double vd[VPT];
-  uint32_t L = 0;
+  uint32_t am = 0u;
   bool ok = true;
 #pragma unroll
   for (int j = 0; j < VPT; ++j) {
     ok = ok && cm[j] > -CM_LIM && cm[j] < CM_LIM;
     vd[j] = (double)(int32_t)P[j] * (double)(int32_t)cm[j];
-    L = ::max(L, bitlen_f64(vd[j]));
+    am = ::max(am, f64_hiword_abs(vd[j]));
   }
-  L = red.max_u32(ok ? L : 64u);
+  const uint32_t L = bitlen_from_hiword(red.max_u32(ok ? am : 0x7FF00000u));
   if (DI_UNLIKELY(L >= 64u)) return false;
   const i64 sh = imax(ilog2_from_bitlen(L) - (tb - 1), 0);
   const i64 dk = wsub(wadd(row_k, col_k), sh);
@@ -355,7 +355,7 @@ __device__ __forceinline__ bool requant_residual_f64(i64 (&h)[VPT], const i64 (&
   if (down > 63 || up > 52) return false;
   const double rmd = (double)(int32_t)row_m, upf = ldexp(1.0, (int)up);
   double hn[VPT];
-  uint32_t L2 = 0;
+  uint32_t hm = 0u;
   ok = true;
 #pragma unroll
   for (int j = 0; j < VPT; ++j) {
@@ -363,9 +363,9 @@ __device__ __forceinline__ bool requant_residual_f64(i64 (&h)[VPT], const i64 (&
     const double al = rshift_round_f64(d * rmd, (int)down) * upf;
     ok = ok && fabs(al) < 0x1p51;
     hn[j] = (double)(int32_t)h[j] + al;
-    L2 = ::max(L2, bitlen_f64(hn[j]));
+    hm = ::max(hm, f64_hiword_abs(hn[j]));
   }
-  L2 = red.max_u32(ok ? L2 : 64u);
+  const uint32_t L2 = bitlen_from_hiword(red.max_u32(ok ? hm : 0x7FF00000u));
   if (DI_UNLIKELY(L2 >= 64u)) return false;
   const i64 lg = ilog2_from_bitlen(L2);
   const i64 sh_down = imax(lg - 29, 0);
@@ -774,20 +774,24 @@ __device__ __forceinline__ void swiglu_quant_row(const SwigluArgs& a, int r, Red
   // one free.
   constexpr i64 CM_LIM = (i64)1 << 21;
   double vg[VPT], vu[VPT];
-  uint32_t L0 = 0, L1 = 0;
+  uint32_t L0, L1;
   {
     bool ok = true;
+    L0 = L1 = 0u;
 #pragma unroll
     for (int j = 0; j < VPT; ++j) {
       ok = ok && gm[j] > -CM_LIM && gm[j] < CM_LIM && um[j] > -CM_LIM && um[j] < CM_LIM;
       vg[j] = (double)(int32_t)gu[0][j] * (double)(int32_t)gm[j];
       vu[j] = (double)(int32_t)gu[1][j] * (double)(int32_t)um[j];
-      L0 = ::max(L0, bitlen_f64(vg[j]));
-      L1 = ::max(L1, bitlen_f64(vu[j]));
+      L0 = ::max(L0, f64_hiword_abs(vg[j]));
+      L1 = ::max(L1, f64_hiword_abs(vu[j]));
     }
-    if (!ok) L0 = L1 = 64u;
+    // the bit lengths of the row maxima from the high words
+    if (!ok) L0 = L1 = 0x7FF00000u;
   }
   red.max2_u32(L0, L1);
+  L0 = bitlen_from_hiword(L0);
+  L1 = bitlen_from_hiword(L1);
   i64 gk, uk;
   int32_t g32[VPT], u32[VPT];
   if (DI_LIKELY(L0 < 64u && L1 < 64u)) {

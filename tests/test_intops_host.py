@@ -510,7 +510,8 @@ def test_isqrt_est_matches_oracle(lib):
 
 
 def test_f64_integer_helpers(lib):
-    """bitlen_f64 (the fp64 exponent) equals int.bit_length of |x|, and
+    """bitlen_f64 (the fp64 exponent) and bitlen_from_hiword (the exponent in
+    the high word of |x|) equal int.bit_length of |x|, and
     rshift_round_f64 equals rshift_round (intmath.py:120-147, (x + 2^(sh-1))
     >> sh with floor) for |x| < 2^52 and every shift from 0 to 70, on random
     magnitudes of every size, exact powers of two and their neighbours, and
@@ -523,6 +524,9 @@ def test_f64_integer_helpers(lib):
     x = (mags * sign).astype(np.int64)
     out = np.empty_like(x)
     lib.di_host_f64_int_op(ctypes.c_int(0), _p(x), _p(x), ctypes.c_int64(x.size), _p(out))
+    assert [int(v) for v in out] == [abs(int(v)).bit_length() for v in x]
+    # the same bit length from the high word of |x| (bitlen_from_hiword)
+    lib.di_host_f64_int_op(ctypes.c_int(4), _p(x), _p(x), ctypes.c_int64(x.size), _p(out))
     assert [int(v) for v in out] == [abs(int(v)).bit_length() for v in x]
     for sh in range(0, 71):
         xs = x.copy()
