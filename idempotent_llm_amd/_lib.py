@@ -38,6 +38,8 @@ SIGNATURES = {
                               P, P, L, P, L, S],
     "detllm_igemv_merge": [P, P, I, I, I, I, L, P, I, L, P, L, P, L, P, P, P, L, P, L, S],
     "detllm_swiglu_quant": [P, I, L, I, I, P, P, P, L, P, L, P, L, P, P, P, P, I, I, I, I, S],
+    "detllm_igemv_swiglu": [P, P, I, I, I, L, P, I, L, P, P, P, L, P, L, P, L, P, P, I, P, L, P,
+                            L, S],
     "detllm_merge_rowcol": [P, I, L, I, I, P, L, P, L, P, P, P, P, I, I, I, I, S],
     "detllm_qkv_epilogue": [P, I, L, I, I, I, I, P, P, P, P, L, P, L, P, L, P, L, P, L, P, L,
                             P, P, P, P, P, P, P, P, L, P, P, P, P, P, P, I, P, L, P, P, S],

@@ -1489,12 +1489,13 @@ struct ProLds {
 };
 
 // PRO 1: residual_normq (ResNormArgs, mode 1, C = K <= CMAX); 2: merge_rowcol
-// (MergeArgs, C = K <= CMAX). ONE: a single row, computed by the whole block
-// (else one wave per row); separate instantiations keep the one-row kernel
-// free of the wave path's registers.
+// (MergeArgs, C = K <= CMAX); 3: swiglu_quant (SwigluArgs, I = K <= CMAX, one
+// row only). ONE: a single row, computed by the whole block (else one wave
+// per row); separate instantiations keep the one-row kernel free of the wave
+// path's registers.
 template <int PRO, int CMAX, int NI, int NB, bool ONE>
 __global__ __launch_bounds__(PRO_THREADS) void k_gemv_pro(ProGemv g, ResNormArgs ra, MergeArgs ma,
-                                                         Prefetch pf) {
+                                                         SwigluArgs sa, Prefetch pf) {
   keep_hidden_args();
   __shared__ __attribute__((aligned(16))) ProLds<CMAX, NB> L;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
@@ -1530,6 +1531,17 @@ __global__ __launch_bounds__(PRO_THREADS) void k_gemv_pro(ProGemv g, ResNormArgs
     } else if (wave < g.R) {
       WaveRed red;
       residual_normq_row<CMAX / 64, WaveRed, 1>(a, wave, red);
+    }
+  } else if (PRO == 3) {
+    SwigluArgs a = sa;
+    a.y8 = &L.a[0][0];  // row 0 (the entry point takes one row)
+    if (!lead) {
+      a.ym = nullptr;
+      a.yk = nullptr;
+    }
+    if (ONE) {
+      BlockRed red{L.red_buf, 0, PRO_THREADS};
+      swiglu_quant_row<CMAX / PRO_THREADS>(a, 0, red);
     }
   } else {
     MergeArgs a = ma;
@@ -1585,10 +1597,10 @@ __global__ __launch_bounds__(PRO_THREADS) void k_gemv_pro(ProGemv g, ResNormArgs
 // One launch of k_gemv_pro.
 template <int PRO, int CMAX, bool ONE>
 void launch_pro1(const ProGemv& g, int ni, int nb, dim3 grid, const ResNormArgs& ra,
-                 const MergeArgs& ma, const Prefetch& pf, hipStream_t s) {
+                 const MergeArgs& ma, const SwigluArgs& sa, const Prefetch& pf, hipStream_t s) {
   const dim3 block(PRO_THREADS);
 #define DI_PRO_LAUNCH(NI_, NB_) \
-  hipLaunchKernelGGL((k_gemv_pro<PRO, CMAX, NI_, NB_, ONE>), grid, block, 0, s, g, ra, ma, pf)
+  hipLaunchKernelGGL((k_gemv_pro<PRO, CMAX, NI_, NB_, ONE>), grid, block, 0, s, g, ra, ma, sa, pf)
   if (nb == 1) {
     if (ni == 1) DI_PRO_LAUNCH(1, 1);
     else DI_PRO_LAUNCH(2, 1);
@@ -1601,15 +1613,18 @@ void launch_pro1(const ProGemv& g, int ni, int nb, dim3 grid, const ResNormArgs&
 
 template <int PRO, int CMAX>
 void launch_pro(const ProGemv& g, int ni, int ksplit, const ResNormArgs& ra, const MergeArgs& ma,
-                const Prefetch& pf, hipStream_t s) {
+                const SwigluArgs& sa, const Prefetch& pf, hipStream_t s) {
   // NB = 2 when one column group per block would need more blocks than the
   // chip has CUs (measured at one row, c3 b1: 1.635 ms per step against
   // 1.670 with one group per block and 1.677 with up to four)
   const int groups = (g.N + 15) / 16;
   const int nb = (long)groups * ksplit > 256 ? 2 : 1;
   const dim3 grid((groups + nb - 1) / nb, ksplit);
-  if (g.R == 1) launch_pro1<PRO, CMAX, true>(g, ni, nb, grid, ra, ma, pf, s);
-  else launch_pro1<PRO, CMAX, false>(g, ni, nb, grid, ra, ma, pf, s);
+  if (g.R == 1) {
+    launch_pro1<PRO, CMAX, true>(g, ni, nb, grid, ra, ma, sa, pf, s);
+  } else {
+    if constexpr (PRO != 3) launch_pro1<PRO, CMAX, false>(g, ni, nb, grid, ra, ma, sa, pf, s);
+  }
 }
 
 }  // namespace
@@ -1787,7 +1802,7 @@ int detllm_igemv_resnormq(const int8_t* W, int32_t* C, int R, int N, int K, int 
   a.h_in = h_in; a.k_res_in = k_res_in; a.h = h_out; a.k_res = k_res_out; a.sm_m = sm_m;
   a.sm_k = sm_k; a.xm = xm; a.xk = xk;
   const ProGemv g{W, C, R, N, K, kchunk, (i64)split_stride};
-  launch_pro<1, 1024>(g, ni, ksplit, a, MergeArgs{}, pf, s);
+  launch_pro<1, 1024>(g, ni, ksplit, a, MergeArgs{}, SwigluArgs{}, pf, s);
   DI_LAUNCH_CHECK();
   return DI_OK;
 }
@@ -1810,7 +1825,33 @@ int detllm_igemv_merge(const int8_t* W, int32_t* C, int R, int N, int K, int ksp
   m.C = K; m.attn = attn; m.nsplit = nsplit; m.split_stride = a_split_stride; m.os_m = os_m;
   m.os_k = os_k; m.col_m = col_m; m.col_k = col_k; m.am = am; m.ak = ak;
   const ProGemv g{W, C, R, N, K, kchunk, (i64)split_stride};
-  launch_pro<2, 2048>(g, ni, ksplit, ResNormArgs{}, m, pf, s);
+  launch_pro<2, 2048>(g, ni, ksplit, ResNormArgs{}, m, SwigluArgs{}, pf, s);
+  DI_LAUNCH_CHECK();
+  return DI_OK;
+}
+
+int detllm_igemv_swiglu(const int8_t* W, int32_t* C, int N, int K, int ksplit,
+                        int64_t split_stride, const int32_t* P, int nsplit, int64_t p_split_stride,
+                        const int64_t* xm, const int64_t* xk, const int64_t* gate_m,
+                        int64_t gate_k, const int64_t* up_m, int64_t up_k, const int64_t* ds_m,
+                        int64_t ds_k, int64_t* ym, int64_t* yk, int defer_fit, const void* pf0,
+                        int64_t n0, const void* pf1, int64_t n1, hipStream_t s) {
+  if (N <= 0) return DI_OK;
+  if (K <= 0 || K > 3072 || K % 512 != 0 || !W || !C || !P || nsplit < 1 || !xm || !xk ||
+      !gate_m || !up_m || !ds_m || !ym || !yk || (defer_fit != 0 && defer_fit != 1) ||
+      (ksplit > 1 && split_stride < (int64_t)N))
+    return DI_EINVAL;
+  int kchunk = 0;
+  const int ni = pro_steps(K, ksplit, &kchunk);
+  if (ni == 0) return DI_ENOSYS;
+  Prefetch pf;
+  if (!pro_prefetch(pf0, n0, pf1, n1, &pf)) return DI_EINVAL;
+  SwigluArgs a{};
+  a.I = K; a.nt = PRO_THREADS; a.P = P; a.nsplit = nsplit; a.split_stride = p_split_stride;
+  a.xm = xm; a.xk = xk; a.gate_m = gate_m; a.gate_k = gate_k; a.up_m = up_m; a.up_k = up_k;
+  a.ds_m = ds_m; a.ds_k = ds_k; a.ym = ym; a.yk = yk; a.defer_fit = defer_fit;
+  const ProGemv g{W, C, 1, N, K, kchunk, (i64)split_stride};
+  launch_pro<3, 3072>(g, ni, ksplit, ResNormArgs{}, MergeArgs{}, a, pf, s);
   DI_LAUNCH_CHECK();
   return DI_OK;
 }

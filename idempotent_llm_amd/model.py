@@ -144,6 +144,9 @@ class IntQwen3:
     # (the skinny GEMM's operand row kernel inside it, one launch fewer per
     # row kernel); more rows run the separate row kernels
     fused_decode_rows = 1
+    # K split of the one-row down GEMV with the SwiGLU row fused in
+    # (detllm_igemv_swiglu); 0 runs the SwiGLU row kernel and the GEMV apart
+    fused_swiglu_ksplit = 3
 
     def __init__(self, artifact_dir: str, backend: str = "rocm"):
         from safetensors.torch import load_file
@@ -508,9 +511,10 @@ class IntQwen3:
     def _layers_fused(self, B, hb, kb, x8, xm, xk, pos, cache, S_past, S, static):
         """The decoder stack for a decode row (T == 1, B == 1) with each
         skinny GEMM's operand row kernel fused into it (detllm_igemv_merge,
-        detllm_igemv_resnormq): per layer QKV-GEMM(+residual_normq of the
-        previous layer's down product) -> attention -> o-GEMM(+merge) ->
-        gate|up-GEMM(+residual_normq of the o product) -> SwiGLU -> down-GEMM;
+        detllm_igemv_resnormq, detllm_igemv_swiglu): per layer
+        QKV-GEMM(+residual_normq of the previous layer's down product) ->
+        attention -> o-GEMM(+merge) -> gate|up-GEMM(+residual_normq of the o
+        product) -> down-GEMM(+SwiGLU);
         the same integers as _layer's sequence. The residual alternates
         between two buffers (a fused launch reads one while its lead block
         writes the other): hb [2, B, H], kb [2, B] with the embedding's
@@ -536,10 +540,22 @@ class IntQwen3:
                  L.o_m, L.o_k, 20, hb[cur], kb[cur], hb[1 - cur], kb[1 - cur], L.ms_m, L.ms_k,
                  xm, xk, L.pf_mlp, L.pf_mlp.numel() * 8, None, 0)
             cur = 1 - cur
-            call("detllm_swiglu_quant", Pg, nsg, stg, R, I_, xm, xk, L.gate_m, L.gate_k, L.up_m,
-                 L.up_k, L.ds_m, L.ds_k, y8, ym, yk, *self._next_gemm(L.wd, R), 0)
-            Pd, nsd, std = self._gemm(y8, L.wd, (L.down_m,) if nxt is None else
-                                      (L.down_m, nxt.as_m))
+            pfd = (L.down_m,) if nxt is None else (L.down_m, nxt.as_m)
+            ksd = self.fused_swiglu_ksplit
+            if ksd and I_ % 512 == 0 and I_ <= 3072 and pro_fits(I_, ksd):
+                # the down GEMV computes its SwiGLU operand row itself
+                Pd = torch.empty(ksd, R, H, dtype=torch.int32, device=dev)
+                nsd, std = ksd, R * H
+                pf = []
+                for t in pfd:
+                    pf += [t, t.numel() * t.element_size()]
+                pf += [None, 0] * (2 - len(pfd))
+                call("detllm_igemv_swiglu", L.wd, Pd, H, I_, ksd, std, Pg, nsg, stg, xm, xk,
+                     L.gate_m, L.gate_k, L.up_m, L.up_k, L.ds_m, L.ds_k, ym, yk, 0, *pf)
+            else:
+                call("detllm_swiglu_quant", Pg, nsg, stg, R, I_, xm, xk, L.gate_m, L.gate_k,
+                     L.up_m, L.up_k, L.ds_m, L.ds_k, y8, ym, yk, *self._next_gemm(L.wd, R), 0)
+                Pd, nsd, std = self._gemm(y8, L.wd, pfd)
             if nxt is None:
                 call("detllm_residual_normq", Pd, nsd, std, R, H, ym, yk, L.down_m, L.down_k, 20,
                      hb[cur], kb[cur], None, 0, x8, xm, xk, None, 0, 0, 0, 0)

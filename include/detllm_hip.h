@@ -180,6 +180,19 @@ int detllm_igemv_merge(const int8_t* W, int32_t* C, int R, int N, int K, int ksp
                        const int64_t* col_m, int64_t col_k, int64_t* am, int64_t* ak,
                        const void* pf0, int64_t n0, const void* pf1, int64_t n1, hipStream_t s);
 
+/* detllm_igemv_swiglu: operand = detllm_swiglu_quant of ONE decode row's
+ * gate|up product (P [nsplit][1][2K], p_split_stride apart) — model.py:416-423
+ * (dyadic.py:108-120 twice, ops/di_swiglu.py:39-58, dyadic.py:93-105) — whose
+ * row scale goes to ym / yk (fitted unless defer_fit, as detllm_swiglu_quant);
+ * K = the intermediate size, a multiple of 512, at most 3072; W [N][K] the
+ * down projection's weights. The int8 row itself stays in LDS. */
+int detllm_igemv_swiglu(const int8_t* W, int32_t* C, int N, int K, int ksplit,
+                        int64_t split_stride, const int32_t* P, int nsplit, int64_t p_split_stride,
+                        const int64_t* xm, const int64_t* xk, const int64_t* gate_m,
+                        int64_t gate_k, const int64_t* up_m, int64_t up_k, const int64_t* ds_m,
+                        int64_t ds_k, int64_t* ym, int64_t* yk, int defer_fit, const void* pf0,
+                        int64_t n0, const void* pf1, int64_t n1, hipStream_t s);
+
 /* IntQwen3._norm_quant — model.py:187-198: di_rmsnorm(h) (ops/di_rmsnorm.py:33-52),
  * optional smoothing multiply by sm_m (null: none) with k 20 + sm_k, then
  * quant_i8_pertoken (dyadic.py:93-105). h [R][C] int32 is only read. */

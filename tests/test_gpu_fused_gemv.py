@@ -187,3 +187,52 @@ def test_fused_gemv_argument_errors():
     assert pro_fits(2048, 4) and pro_fits(2048, 2) and not pro_fits(2048, 1)
     rn(8, 2, h2, kr2)              # covered: runs
     torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("I,ks", [(3072, 3), (3072, 6), (1024, 1), (1024, 2)])
+@pytest.mark.parametrize("case", ["fp64", "big_gate_m", "big_ds_m", "big_tpos"])
+def test_igemv_swiglu_equals_two_launches(I, ks, case):
+    """The one-row down GEMV with its SwiGLU operand fused in
+    (detllm_igemv_swiglu) against the two launches it replaces
+    (detllm_swiglu_quant, then detllm_igemv_nt with the same K split): equal
+    partials and row scale, with the scale fit done and deferred, summed
+    gate|up partials, and inputs that take each path of the SwiGLU row (fp64
+    chain, a gate mantissa of 2^22: integer requantisation, a ds_m of
+    2^18 + 3: integer quantisation, tpos >= 2^23: 64-bit DI-Exp). The
+    product is checked against the oracle's int_gemm of the row kernel's
+    int8 operand, whose parity with the oracle test_gpu_ops pins."""
+    from idempotent_llm_amd._lib import call
+    print(f"[igemv_swiglu I={I} ks={ks} {case}]", flush=True)
+    rng = np.random.default_rng(I + 31 * ks + len(case))
+    N, nsplit = 1024, 2
+    gm = rng.integers(1 << 14, 1 << 16, I).astype(I64)
+    um = rng.integers(1 << 14, 1 << 16, I).astype(I64)
+    dsm = rng.integers(1 << 12, 1 << 14, I).astype(I64)
+    if case == "big_gate_m":
+        gm[17] = 1 << 22
+    if case == "big_ds_m":
+        dsm[5] = (1 << 18) + 3
+    P = rng.integers(-(1 << 23), 1 << 23, (nsplit, 1, 2 * I)).astype(np.int32)
+    xm = g(rng.integers(1 << 15, 1 << 16, 1).astype(I64))
+    xk = g(np.full(1, 50 if case == "big_tpos" else 20, I64))
+    w = g(rng.integers(-128, 128, (N, I)).astype(np.int8))
+    Pg = g(P)
+    for defer in (0, 1):
+        y8 = torch.empty(1, I, dtype=torch.int8, device="cuda")
+        ym = torch.full((1,), -1, dtype=torch.int64, device="cuda")
+        yk = torch.full((1,), -1, dtype=torch.int64, device="cuda")
+        call("detllm_swiglu_quant", Pg, nsplit, 2 * I, 1, I, xm, xk, g(gm), 20, g(um), 20, g(dsm),
+             15, y8, ym, yk, None, 0, 0, 0, defer)
+        want = _split_product(y8, w, ks)
+        for rep in range(2):
+            C = torch.full((ks, 1, N), -7, dtype=torch.int32, device="cuda")
+            fm = torch.full((1,), -1, dtype=torch.int64, device="cuda")
+            fk = torch.full((1,), -1, dtype=torch.int64, device="cuda")
+            pf = g(rng.integers(0, 9, 4096).astype(I64))
+            call("detllm_igemv_swiglu", w, C, N, I, ks, N, Pg, nsplit, 2 * I, xm, xk, g(gm), 20,
+                 g(um), 20, g(dsm), 15, fm, fk, defer, pf if rep else None,
+                 pf.numel() * 8 if rep else 0, None, 0)
+            assert torch.equal(C, want)
+            assert torch.equal(fm, ym) and torch.equal(fk, yk)
+        prod = ogemm.int_gemm(y8.cpu().numpy(), w.cpu().numpy().T)
+        assert np.array_equal(want.sum(0).cpu().numpy().astype(I64), prod.astype(I64))
