@@ -730,7 +730,7 @@ def main():
     from idempotent_llm_amd.model import IntQwen3
     assert torch.cuda.is_available(), "bench.py needs a GPU"
     if args.gemm_probe:
-        print(json.dumps(gemm_tops()), flush=True)
+        print(json.dumps({"2048": gemm_tops(), "c4": gemm_tops(32 * 1021)}), flush=True)
         return
     if args.attn_probe:
         print(json.dumps({"c2_attention_prefill_2048": c2_bench()}), flush=True)
@@ -781,6 +781,10 @@ def main():
             log(f"prefill 2048: {extras['prefill_tok_s_2048']} tok/s")
             extras["int8_gemm_prefill"] = gemm_tops()
             log(f"gemm: {extras['int8_gemm_prefill']['all']}")
+            # the same four products at c4's prefill size (32 rows padded to
+            # 1,021 tokens: M = 32,672), where the 256x256 tiles run
+            extras["int8_gemm_prefill_c4"] = gemm_tops(32 * 1021)
+            log(f"gemm c4: {extras['int8_gemm_prefill_c4']['all']}")
             c1, c2 = c1_c2_bench()
             extras["c1_mlp_block_2048"] = c1
             extras["c2_attention_prefill_2048"] = c2
