@@ -134,7 +134,7 @@ def attn_split_plan(B: int, S: int, n_q: int, n_kv: int):
 
 def pro_fits(K: int, ksplit: int) -> bool:
     """True when the fused decode GEMVs (detllm_igemv_resnormq /
-    detllm_igemv_merge) cover a K split of ``ksplit``: each split a whole
+    detllm_igemv_merge / detllm_igemv_swiglu) cover a K split of ``ksplit``: each split a whole
     number of 512-byte chunks, at most two (the check those entry points make
     before returning -38)."""
     if K <= 0 or K % 16 or ksplit < 1:
