@@ -95,6 +95,35 @@ __device__ __forceinline__ i64 ld_global(const int64_t* p) {
   return *(const __attribute__((address_space(1))) int64_t*)p;
 }
 
+// Raw buffer views. A descriptor of n bytes at p (stride 0, unswizzled): a
+// load at a byte offset at or past n reads 0 and a store there is dropped
+// (the buffer unit's range check on the VGPR + instruction offset), and the
+// offset is one 32-bit VGPR. Row kernels read and write a row's columns
+// through them: no index clamp, no 64-bit address arithmetic and no select
+// that zeroes the columns past the row's end. A null p with n = 0 reads 0
+// everywhere. p and n must be uniform across the wave (row scalars), n below
+// 2^32, offsets multiples of the access size.
+typedef __amdgpu_buffer_rsrc_t bufv_t;
+__device__ __forceinline__ bufv_t buf_view(const void* p, i64 nbytes) {
+  return __builtin_amdgcn_make_buffer_rsrc((void*)p, (short)0, (int)(uint32_t)nbytes, 0x00020000);
+}
+__device__ __forceinline__ i64 buf_ld_i64(bufv_t r, uint32_t off) {
+  const auto v = __builtin_amdgcn_raw_buffer_load_b64(r, (int)off, 0, 0);
+  return (i64)(((u64)v[1] << 32) | v[0]);
+}
+__device__ __forceinline__ int32_t buf_ld_i32(bufv_t r, uint32_t off) {
+  return (int32_t)__builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 0);
+}
+__device__ __forceinline__ int32_t buf_ld_i8(bufv_t r, uint32_t off) {
+  return (int32_t)(int8_t)__builtin_amdgcn_raw_buffer_load_b8(r, (int)off, 0, 0);
+}
+__device__ __forceinline__ void buf_st_i8(bufv_t r, uint32_t off, int32_t v) {
+  __builtin_amdgcn_raw_buffer_store_b8((uint8_t)v, r, (int)off, 0, 0);
+}
+__device__ __forceinline__ void buf_st_i32(bufv_t r, uint32_t off, int32_t v) {
+  __builtin_amdgcn_raw_buffer_store_b32((uint32_t)v, r, (int)off, 0, 0);
+}
+
 // Every kernel starts with this: a reference to its hidden (implicit) launch
 // arguments on a path no launch takes (a workgroup id of 2^31 - 2), so that
 // its argument segment carries the hidden block. rocprofv3's counter

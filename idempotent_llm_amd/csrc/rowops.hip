@@ -381,39 +381,38 @@ __device__ __forceinline__ bool requant_residual_f64(i64 (&h)[VPT], const i64 (&
 // Latency, not bandwidth, bounds these kernels at decode (one block per
 // token row): every helper below issues all of its global loads before the
 // first use, so a kernel waits for one memory round trip instead of one per
-// load. Indices are clamped instead of branched on, so each load is
-// unconditional and in bounds; out-of-range lanes are zeroed after the load.
+// load. The loads go through buffer views of the row (buf_view): a column
+// past C reads 0, so each load is unconditional, needs no index clamp and no
+// select after it, and its address is one 32-bit offset.
+
+// Byte offset of this thread's column j (c = tid + j * nt) for elements of E bytes
+template <int E, class Red>
+__device__ __forceinline__ uint32_t col_off(const Red& red, int j) {
+  return (uint32_t)(red.tid() + j * red.nt()) * (uint32_t)E;
+}
 
 // x[c] for the columns c = threadIdx.x + j * blockDim.x this thread owns (0 past C or
 // when x is null).
 template <int VPT, class Red>
 __device__ __forceinline__ void prefetch_cols(i64 (&v)[VPT], const int64_t* x, int C,
                                               const Red& red) {
+  const bufv_t xb = buf_view(x, x ? (i64)C * 8 : 0);
 #pragma unroll
-  for (int j = 0; j < VPT; ++j) {
-    const int c = red.tid() + j * red.nt();
-    v[j] = x ? x[c < C ? c : C - 1] : 0;
-  }
-#pragma unroll
-  for (int j = 0; j < VPT; ++j)
-    if (red.tid() + j * red.nt() >= C) v[j] = 0;
+  for (int j = 0; j < VPT; ++j) v[j] = buf_ld_i64(xb, col_off<8>(red, j));
 }
 
-// x[c] for this thread's columns, 0 past C or when x is null. The load goes
-// through alt (valid for C columns) when x is null and is masked after, so
-// there is no branch around it (a branch merge makes earlier loads complete).
+// x[c] for this thread's columns, 0 past C or when x is null (alt: unused,
+// kept for the callers that name a stand-in vector).
 template <int VPT, class Red>
 __device__ __forceinline__ void load_cols_or0(i64 (&v)[VPT], const int64_t* x, const int64_t* alt,
                                               int C, const Red& red) {
-  const int64_t* p = x ? x : alt;
-#pragma unroll
-  for (int j = 0; j < VPT; ++j) {
-    const int c = red.tid() + j * red.nt();
-    v[j] = p[c < C ? c : C - 1];
-  }
-#pragma unroll
-  for (int j = 0; j < VPT; ++j)
-    if (red.tid() + j * red.nt() >= C || !x) v[j] = 0;
+  (void)alt;
+  prefetch_cols(v, x, C, red);
+}
+
+// Row q of int32 partial k: P[k * stride + off[q] + c] for c < C
+__device__ __forceinline__ bufv_t part_view(const int32_t* P, int k, i64 stride, i64 off, int C) {
+  return buf_view(P + (i64)k * stride + off, (i64)C * 4);
 }
 
 // The first KF of the nsplit int32 partials P[k * stride + off + c], issued
@@ -427,12 +426,11 @@ __device__ __forceinline__ void load_rows_i32_first(int32_t (&t)[KF][NR][VPT], c
   for (int kk = 0; kk < KF; ++kk) {
     const int k = kk < nsplit ? kk : nsplit - 1;
 #pragma unroll
-    for (int q = 0; q < NR; ++q)
+    for (int q = 0; q < NR; ++q) {
+      const bufv_t pb = part_view(P, k, stride, off[q], C);
 #pragma unroll
-      for (int j = 0; j < VPT; ++j) {
-        const int c = red.tid() + j * red.nt();
-        t[kk][q][j] = P[(i64)k * stride + off[q] + (c < C ? c : C - 1)];
-      }
+      for (int j = 0; j < VPT; ++j) t[kk][q][j] = buf_ld_i32(pb, col_off<4>(red, j));
+    }
   }
 }
 template <int KF, int NR, int VPT, class Red>
@@ -452,17 +450,15 @@ __device__ __forceinline__ void rows_i32_sum(i64 (&v)[NR][VPT], const int32_t (&
     }
   for (int k = KF; k < nsplit; ++k)  // more partials than KF: one at a time
 #pragma unroll
-    for (int q = 0; q < NR; ++q)
+    for (int q = 0; q < NR; ++q) {
+      const bufv_t pb = part_view(P, k, stride, off[q], C);
 #pragma unroll
-      for (int j = 0; j < VPT; ++j) {
-        const int c = red.tid() + j * red.nt();
-        s[q][j] += (uint32_t)P[(i64)k * stride + off[q] + (c < C ? c : C - 1)];
-      }
+      for (int j = 0; j < VPT; ++j) s[q][j] += (uint32_t)buf_ld_i32(pb, col_off<4>(red, j));
+    }
 #pragma unroll
   for (int q = 0; q < NR; ++q)
 #pragma unroll
-    for (int j = 0; j < VPT; ++j)
-      v[q][j] = red.tid() + j * red.nt() < C ? (i64)(int32_t)s[q][j] : 0;
+    for (int j = 0; j < VPT; ++j) v[q][j] = (i64)(int32_t)s[q][j];
 }
 
 // Sum of nsplit int32 partials P[k * stride + off + c] (the K-split of the
@@ -473,17 +469,11 @@ __device__ __forceinline__ void load_rows_i32_sum(i64 (&v)[NR][VPT], const int32
                                                   int C, const Red& red) {
   if (nsplit == 1) {  // no K split (block-uniform): one load per element
 #pragma unroll
-    for (int q = 0; q < NR; ++q)
+    for (int q = 0; q < NR; ++q) {
+      const bufv_t pb = part_view(P, 0, 0, off[q], C);
 #pragma unroll
-      for (int j = 0; j < VPT; ++j) {
-        const int c = red.tid() + j * red.nt();
-        v[q][j] = P[off[q] + (c < C ? c : C - 1)];
-      }
-#pragma unroll
-    for (int q = 0; q < NR; ++q)
-#pragma unroll
-      for (int j = 0; j < VPT; ++j)
-        if (red.tid() + j * red.nt() >= C) v[q][j] = 0;
+      for (int j = 0; j < VPT; ++j) v[q][j] = buf_ld_i32(pb, col_off<4>(red, j));
+    }
     return;
   }
   constexpr int KU = NR * VPT > 8 ? 2 : 4;  // partials per batch of loads
@@ -498,12 +488,11 @@ __device__ __forceinline__ void load_rows_i32_sum(i64 (&v)[NR][VPT], const int32
     for (int kk = 0; kk < KU; ++kk) {
       const int k = k0 + kk < nsplit ? k0 + kk : nsplit - 1;
 #pragma unroll
-      for (int q = 0; q < NR; ++q)
+      for (int q = 0; q < NR; ++q) {
+        const bufv_t pb = part_view(P, k, stride, off[q], C);
 #pragma unroll
-        for (int j = 0; j < VPT; ++j) {
-          const int c = red.tid() + j * red.nt();
-          t[kk][q][j] = P[(i64)k * stride + off[q] + (c < C ? c : C - 1)];
-        }
+        for (int j = 0; j < VPT; ++j) t[kk][q][j] = buf_ld_i32(pb, col_off<4>(red, j));
+      }
     }
 #pragma unroll
     for (int kk = 0; kk < KU; ++kk)
@@ -516,8 +505,7 @@ __device__ __forceinline__ void load_rows_i32_sum(i64 (&v)[NR][VPT], const int32
 #pragma unroll
   for (int q = 0; q < NR; ++q)
 #pragma unroll
-    for (int j = 0; j < VPT; ++j)
-      v[q][j] = red.tid() + j * red.nt() < C ? (i64)(int32_t)s[q][j] : 0;
+    for (int j = 0; j < VPT; ++j) v[q][j] = (i64)(int32_t)s[q][j];
 }
 
 // =====================================================================
@@ -574,10 +562,10 @@ __device__ __forceinline__ void residual_normq_row(const ResNormArgs& a, int r, 
     i64 cm[VPT];
     load_cols_or0(smv, a.sm_m, a.col_m, C, red);
     load_cols_or0(cm, a.col_m, a.col_m, C, red);
+    {
+      const bufv_t hb = buf_view(h_in + off, (i64)C * 4);
 #pragma unroll
-    for (int j = 0; j < VPT; ++j) {
-      const int c = red.tid() + j * red.nt();
-      h[j] = h_in[off + (c < C ? c : C - 1)];
+      for (int j = 0; j < VPT; ++j) h[j] = buf_ld_i32(hb, col_off<4>(red, j));
     }
     i64 row_k = a.row_k[r], row_m = a.row_m[r];
     const i64 k_res = (a.k_res_in ? a.k_res_in : a.k_res)[r];
@@ -597,10 +585,7 @@ __device__ __forceinline__ void residual_normq_row(const ResNormArgs& a, int r, 
     i64 dd[1][VPT];
     rows_i32_sum<KF, 1, VPT>(dd, t, a.P, a.nsplit, a.split_stride, offs, C, red);
 #pragma unroll
-    for (int j = 0; j < VPT; ++j) {
-      d[j] = dd[0][j];
-      if (red.tid() + j * red.nt() >= C) h[j] = 0;
-    }
+    for (int j = 0; j < VPT; ++j) d[j] = dd[0][j];
     if (DI_UNLIKELY(!requant_residual_f64(h, d, cm, row_m, row_k, a.col_k, a.tb, k_res, red,
                                           &kr, &lg))) {
       const i64 dk = requant_common_row(d, cm, row_k, a.col_k, a.tb, red);
@@ -610,33 +595,24 @@ __device__ __forceinline__ void residual_normq_row(const ResNormArgs& a, int r, 
   prefetch_cols(smv, a.sm_m, C, red);
   if (mode == 2) {
     // _norm_quant of a given residual row: h is read, not written
+    const bufv_t hb = buf_view(h_in + off, (i64)C * 4);
 #pragma unroll
-    for (int j = 0; j < VPT; ++j) {
-      const int c = red.tid() + j * red.nt();
-      h[j] = h_in[off + (c < C ? c : C - 1)];
-    }
-#pragma unroll
-    for (int j = 0; j < VPT; ++j)
-      if (red.tid() + j * red.nt() >= C) h[j] = 0;
+    for (int j = 0; j < VPT; ++j) h[j] = buf_ld_i32(hb, col_off<4>(red, j));
     kr = 0;
   } else if (mode == 0) {
     const i64 id = torch_index(a.ids[r], a.vocab, red.tid() ? nullptr : a.err, DI_ERR_TOKEN);
     const i64 dm = a.em[id], ek = a.ek[id];
+    const bufv_t eb = buf_view(a.e8 + id * C, C);
 #pragma unroll
-    for (int j = 0; j < VPT; ++j) {
-      const int c = red.tid() + j * red.nt();
-      h[j] = a.e8[id * C + (c < C ? c : C - 1)];
-    }
-#pragma unroll
-    for (int j = 0; j < VPT; ++j) h[j] = red.tid() + j * red.nt() < C ? wmul(h[j], dm) : 0;
+    for (int j = 0; j < VPT; ++j) h[j] = wmul((i64)buf_ld_i8(eb, col_off<1>(red, j)), dm);
     kr = residual_renorm_row(h, ek, red, &lg);
   } else {
     i64 cm[VPT];
     prefetch_cols(cm, a.col_m, C, red);
+    {
+      const bufv_t hb = buf_view(h_in + off, (i64)C * 4);
 #pragma unroll
-    for (int j = 0; j < VPT; ++j) {
-      const int c = red.tid() + j * red.nt();
-      h[j] = h_in[off + (c < C ? c : C - 1)];
+      for (int j = 0; j < VPT; ++j) h[j] = buf_ld_i32(hb, col_off<4>(red, j));
     }
     const i64 row_k = a.row_k[r], row_m = a.row_m[r];
     const i64 k_res = (a.k_res_in ? a.k_res_in : a.k_res)[r];
@@ -644,10 +620,7 @@ __device__ __forceinline__ void residual_normq_row(const ResNormArgs& a, int r, 
     const i64 offs[1] = {off};
     load_rows_i32_sum<1, VPT>(dd, a.P, a.nsplit, a.split_stride, offs, C, red);
 #pragma unroll
-    for (int j = 0; j < VPT; ++j) {
-      d[j] = dd[0][j];
-      if (red.tid() + j * red.nt() >= C) h[j] = 0;
-    }
+    for (int j = 0; j < VPT; ++j) d[j] = dd[0][j];
     const i64 dk = requant_common_row(d, cm, row_k, a.col_k, a.tb, red);
     kr = residual_add_row(h, k_res, d, row_m, dk, red, &lg);
   }
@@ -705,7 +678,8 @@ __global__ __launch_bounds__(NT) void k_residual_add_normq(ResNormArgs a) {
 template <int VPT, int MODE>
 __global__ __launch_bounds__(256) void k_residual_normq_w(ResNormArgs a, int R) {
   keep_hidden_args();
-  const int r = (int)blockIdx.x * 4 + (int)(threadIdx.x >> 6);
+  // (wave-uniform: the row's buffer views live in scalar registers)
+  const int r = __builtin_amdgcn_readfirstlane((int)blockIdx.x * 4 + (int)(threadIdx.x >> 6));
   if (r >= R) return;  // whole waves
   WaveRed red;
   residual_normq_row<VPT, WaveRed, MODE>(a, r, red);
@@ -908,10 +882,10 @@ __device__ __forceinline__ void merge_rowcol_row(const MergeArgs& a, int r, Red&
   i64 cm[VPT];
   load_cols_or0(om, a.os_m, a.os_m, C, red);
   load_cols_or0(cm, a.col_m, a.os_m, C, red);
+  {
+    const bufv_t ab = buf_view(a.attn + off, (i64)C * 8);
 #pragma unroll
-  for (int j = 0; j < VPT; ++j) {
-    const int c = red.tid() + j * red.nt();
-    v[j] = a.attn[off + (c < C ? c : C - 1)];  // partial 0
+    for (int j = 0; j < VPT; ++j) v[j] = buf_ld_i64(ab, col_off<8>(red, j));  // partial 0
   }
   __builtin_amdgcn_sched_barrier(0);
   if (a.col_m) {
@@ -924,11 +898,9 @@ __device__ __forceinline__ void merge_rowcol_row(const MergeArgs& a, int r, Red&
 #pragma unroll
     for (int kk = 0; kk < KB; ++kk) {
       const int k = k0 + kk < a.nsplit ? k0 + kk : a.nsplit - 1;
+      const bufv_t ab = buf_view(a.attn + (i64)k * a.split_stride + off, (i64)C * 8);
 #pragma unroll
-      for (int j = 0; j < VPT; ++j) {
-        const int c = red.tid() + j * red.nt();
-        t[kk][j] = a.attn[(i64)k * a.split_stride + off + (c < C ? c : C - 1)];
-      }
+      for (int j = 0; j < VPT; ++j) t[kk][j] = buf_ld_i64(ab, col_off<8>(red, j));
     }
 #pragma unroll
     for (int kk = 0; kk < KB; ++kk)
