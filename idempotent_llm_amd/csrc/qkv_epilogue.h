@@ -341,12 +341,16 @@ __device__ __forceinline__ QKVHeadIn qkv_head_load(const QKVArgs& a, int r, int 
   in.vqk = sc.vqk;
   in.ksm = sc.ksm;
   in.ksk = sc.ksk;
-  const int64_t* wmp = (is_q ? a.q_m : (is_v ? a.v_m : a.k_m)) + (i64)h * 128;
-  in.wm0 = wmp[c0];
-  in.wm1 = wmp[c1];
-  const int64_t* gam = is_q ? a.q_norm_m : a.k_norm_m;
-  in.g0 = gam[c0];
-  in.g1 = gam[c1];
+  // (each candidate pointer through opaque_ptr: a select between kernel
+  // arguments would become a scalar load from the selected argument's
+  // address, one more round trip before the loads below)
+  const int64_t* wmp =
+      (is_q ? opaque_ptr(a.q_m) : (is_v ? opaque_ptr(a.v_m) : opaque_ptr(a.k_m))) + (i64)h * 128;
+  in.wm0 = ld_global(wmp + c0);
+  in.wm1 = ld_global(wmp + c1);
+  const int64_t* gam = is_q ? opaque_ptr(a.q_norm_m) : opaque_ptr(a.k_norm_m);
+  in.g0 = ld_global(gam + c0);
+  in.g1 = ld_global(gam + c1);
   in.qs0 = a.qs_m[kvh * 128 + c0];
   in.qs1 = a.qs_m[kvh * 128 + c1];
   in.kqm0 = a.kq_m[kvh * 128 + c0];
@@ -602,12 +606,14 @@ __device__ __forceinline__ void qkv_rows4(const QKVArgs& a, int R, int r0, int s
   const i64 pos_raw = a.positions[r];
   const i64 xk = a.xk[r], xm = a.xm[r];
   const i64 base = slot_base_of(a);
-  const int64_t* wmp = (is_q ? a.q_m : (is_v ? a.v_m : a.k_m)) + (i64)h * 128;
+  // (candidates through opaque_ptr, as in qkv_head_load)
+  const int64_t* wmp =
+      (is_q ? opaque_ptr(a.q_m) : (is_v ? opaque_ptr(a.v_m) : opaque_ptr(a.k_m))) + (i64)h * 128;
   // the head's column mantissas and product sums (loaded again by the
   // integer routines, so the fp64 path does not keep them live)
   auto load_wp = [&](i64 (&wm)[8], i64 (&p)[8]) {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) wm[i] = wmp[c[i]];
+    for (int i = 0; i < 8; ++i) wm[i] = ld_global(wmp + c[i]);
     uint32_t s[8] = {0, 0, 0, 0, 0, 0, 0, 0};
     for (int k = 0; k < a.nsplit; ++k) {
       const int32_t* pk = a.P + (i64)k * a.split_stride + off;
@@ -668,7 +674,7 @@ __device__ __forceinline__ void qkv_rows4(const QKVArgs& a, int R, int r0, int s
     }
     return;
   }
-  const int64_t* gam = is_q ? a.q_norm_m : a.k_norm_m;
+  const int64_t* gam = is_q ? opaque_ptr(a.q_norm_m) : opaque_ptr(a.k_norm_m);
   const i64 pos = torch_index(pos_raw, a.max_pos, (j == 0 && rok) ? a.err : nullptr,
                               DI_ERR_POSITION);
   // the head's gamma, RoPE and smoothing entries (loaded again by the
@@ -676,7 +682,7 @@ __device__ __forceinline__ void qkv_rows4(const QKVArgs& a, int R, int r0, int s
   auto load_ch = [&](i64 (&gm)[8], int32_t (&cs)[8], int32_t (&sn)[8], i64 (&qs)[8]) {
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      gm[i] = gam[c[i]];
+      gm[i] = ld_global(gam + c[i]);
       cs[i] = a.cos_t[pos * 128 + c[i]];
       sn[i] = a.sin_t[pos * 128 + c[i]];
       qs[i] = is_q ? a.qs_m[kvh * 128 + c[i]] : 0;

@@ -1020,7 +1020,8 @@ __global__ __launch_bounds__(RT) void k_qkv_epilogue(QKVArgs a) {
 __global__ __launch_bounds__(RT, QKV_ROWS_MINW) void k_qkv_epilogue_rows(QKVArgs a, int R, int ngroups) {
   keep_hidden_args();
   const int heads = a.n_q + 2 * a.n_kv;
-  const int wg = blockIdx.x * 4 + (threadIdx.x >> 6);
+  // (wave-uniform, so the head slot's pointer and scale selects stay scalar)
+  const int wg = __builtin_amdgcn_readfirstlane((int)(blockIdx.x * 4 + (threadIdx.x >> 6)));
   if (wg >= heads * ngroups) return;  // whole waves only
   const int slotw = wg / ngroups, grp = wg - slotw * ngroups;
   qkv_rows4(a, R, grp * 4, slotw);
