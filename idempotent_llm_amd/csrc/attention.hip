@@ -599,7 +599,7 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, int S, int kvh,
   constexpr int NB = 8 / NW;   // 16-channel blocks of P.V per wave
   constexpr int IT = 8 / NW;   // prefetched iterations per wave
   __shared__ i64 red_buf[32];
-  BlockRed red{red_buf, 0, NT};
+  BlockRedT<NT / 64> red{red_buf, 0, NT};
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int l16 = lane & 15, grp = lane >> 4;
   const int Spad = (a.S + 15) & ~15;
@@ -1086,7 +1086,7 @@ __global__ __launch_bounds__(256) void k_attn_split_scores(SplitArgs sa) {
   const DecodeArgs& a = sa.d;
   __shared__ i64 red_buf[32];
   __shared__ int32_t pg_lds[SPLIT_MAX_PAGES];
-  BlockRed red{red_buf, 0, 256};
+  BlockRedT<4> red{red_buf, 0, 256};
   const int kvh = blockIdx.x, b = blockIdx.y, c = blockIdx.z;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, l16 = lane & 15, grp = lane >> 4;
   bool over;
@@ -1165,7 +1165,7 @@ __global__ __launch_bounds__(256) void k_attn_split_pv(SplitArgs sa) {
   extern __shared__ __attribute__((aligned(16))) int32_t p_lds[];  // [G][chunk] packed p
   __shared__ i64 red_buf[32];
   __shared__ int32_t pg_lds[SPLIT_MAX_PAGES];
-  BlockRed red{red_buf, 0, 256};
+  BlockRedT<4> red{red_buf, 0, 256};
   const int kvh = blockIdx.x, b = blockIdx.y, c = blockIdx.z;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, l16 = lane & 15, grp = lane >> 4;
   bool over;

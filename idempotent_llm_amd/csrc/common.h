@@ -238,14 +238,21 @@ __device__ __forceinline__ i64 isqrt_wave(i64 n) {
 // a slower thread may still be reading (the call in between has a barrier
 // that every thread passes only after its reads). Max and wrapping sum are
 // associative and commutative: any combine order gives the same integer.
-struct BlockRed {
+// NWS > 0: the launch fixes the block at NWS waves (n = 64 NWS), so the
+// combine of the wave partials is straight-line code over exactly NWS slots
+// instead of a loop over up to 16 with masked entries.
+template <int NWS = 0>
+struct BlockRedT {
+  static_assert(NWS >= 0 && NWS <= 16, "waves per block");
+  static constexpr bool kBlock = true;
   i64* buf;  // __shared__ i64[32]
   int k;
-  int n;     // threads in the block
+  int n;     // threads in the block (64 NWS when NWS > 0)
 
   // the row's threads: the whole block
   __device__ __forceinline__ int tid() const { return (int)threadIdx.x; }
-  __device__ __forceinline__ int nt() const { return n; }
+  __device__ __forceinline__ int nt() const { return NWS ? 64 * NWS : n; }
+  __device__ __forceinline__ int waves() const { return NWS ? NWS : n >> 6; }
 
   template <bool MAX>
   __device__ __forceinline__ i64 reduce(i64 v) {
@@ -254,7 +261,7 @@ struct BlockRed {
     ++k;
     if ((threadIdx.x & 63) == 63) slot[threadIdx.x >> 6] = v;
     __syncthreads();
-    const int nw = n >> 6;
+    const int nw = waves();
     i64 r = MAX ? INT64_MIN : 0;
     for (int i = 0; i < nw; i += 4) {
       const i64 a0 = slot[i], a1 = slot[i + 1], a2 = slot[i + 2], a3 = slot[i + 3];
@@ -278,7 +285,7 @@ struct BlockRed {
       slot[8 + (threadIdx.x >> 6)] = b;
     }
     __syncthreads();
-    const int nw = n >> 6;
+    const int nw = waves();
     i64 ra = 0, rb = 0;
     for (int i = 0; i < nw; ++i) {
       ra = wadd(ra, slot[i]);
@@ -299,7 +306,7 @@ struct BlockRed {
       slot[8 + (threadIdx.x >> 6)] = b;
     }
     __syncthreads();
-    const int nw = n >> 6;
+    const int nw = waves();
     i64 ra = INT64_MIN, rb = INT64_MIN;
     for (int i = 0; i < nw; ++i) {
       ra = imax(ra, slot[i]);
@@ -327,7 +334,7 @@ struct BlockRed {
       slot[16 + (threadIdx.x >> 6)] = b;
     }
     __syncthreads();
-    const int nw = n >> 6;
+    const int nw = waves();
     uint32_t ra = 0, rb = 0;
     for (int i = 0; i < nw; i += 4) {  // 4 reads in flight; entries past nw ignored
       const uint32_t a0 = slot[i], a1 = slot[i + 1], a2 = slot[i + 2], a3 = slot[i + 3];
@@ -374,10 +381,13 @@ struct BlockRed {
   }
 };
 
+using BlockRed = BlockRedT<0>;
+
 // Reductions over one wave's 64 lanes (DPP, no LDS, no barrier): a row
 // handled by a single wave, several rows per block side by side. Same
 // integers as BlockRed (max and wrapping sum are order-independent).
 struct WaveRed {
+  static constexpr bool kBlock = false;
   __device__ __forceinline__ int tid() const { return (int)(threadIdx.x & 63); }
   __device__ __forceinline__ int nt() const { return 64; }
   __device__ __forceinline__ i64 max(i64 v) { return wave_max(v); }

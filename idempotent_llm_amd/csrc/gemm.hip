@@ -620,7 +620,7 @@ __global__ __launch_bounds__(1024) void k_logits_digest(const int32_t* __restric
                                                         int64_t* out) {
   keep_hidden_args();
   __shared__ i64 red_buf[32];
-  BlockRed red{red_buf, 0, 1024};
+  BlockRedT<16> red{red_buf, 0, 1024};
   const int32_t* row = rows + (i64)blockIdx.x * V;
   i64 acc = 0;
   for (int i = threadIdx.x; i < V; i += blockDim.x)

@@ -37,6 +37,12 @@ constexpr int RT = DI_ROW_THREADS;
 // (at most 4 columns per thread), shortening the per-element part of the
 // serial per-row chain that bounds them at decode.
 constexpr int RT_WIDE = 1024;
+// The block reducer of a row kernel launched with NT threads: launches at
+// NT < RT_WIDE run exactly NT threads (prefill rows at 256, decode rows at
+// the width their shape picks), so the reducer knows its wave count; the
+// RT_WIDE instantiation runs the thread count in the args' nt.
+template <int NT>
+using RowRed = BlockRedT<NT < RT_WIDE ? NT / 64 : 0>;
 
 template <int VPT, class Red>
 __device__ __forceinline__ i64 row_absmax(const i64 (&v)[VPT], Red& red) {
@@ -655,8 +661,8 @@ __global__ __launch_bounds__(NT) void k_residual_normq(ResNormArgs a) {
     l2_warm(a.warm, blockIdx.x, a.nt, red_buf);
     return;
   }
-  BlockRed red{red_buf, 0, a.nt};
-  residual_normq_row<VPT, BlockRed, MODE>(a, (int)blockIdx.x - (WARM ? L2WARM_BLOCKS : 0), red);
+  RowRed<NT> red{red_buf, 0, a.nt};
+  residual_normq_row<VPT, decltype(red), MODE>(a, (int)blockIdx.x - (WARM ? L2WARM_BLOCKS : 0), red);
 }
 
 // The GEMM residual add (mode 1) only.
@@ -668,8 +674,8 @@ __global__ __launch_bounds__(NT) void k_residual_add_normq(ResNormArgs a) {
     l2_warm(a.warm, blockIdx.x, a.nt, red_buf);
     return;
   }
-  BlockRed red{red_buf, 0, a.nt};
-  residual_normq_row<VPT, BlockRed, 1>(a, (int)blockIdx.x - (WARM ? L2WARM_BLOCKS : 0), red);
+  RowRed<NT> red{red_buf, 0, a.nt};
+  residual_normq_row<VPT, decltype(red), 1>(a, (int)blockIdx.x - (WARM ? L2WARM_BLOCKS : 0), red);
 }
 
 // Many rows (prefill): one wave per row, four rows per block, every
@@ -846,7 +852,7 @@ __global__ __launch_bounds__(NT, (NT == 256 && VPT >= 8 && VPT <= 12) ? SWIGLU_M
     l2_warm(a.warm, blockIdx.x, a.nt, red_buf);
     return;
   }
-  BlockRed red{red_buf, 0, a.nt};
+  RowRed<NT> red{red_buf, 0, a.nt};
   swiglu_quant_row<VPT>(a, (int)blockIdx.x - (WARM ? L2WARM_BLOCKS : 0), red);
 }
 
@@ -920,7 +926,7 @@ __device__ __forceinline__ void merge_rowcol_row(const MergeArgs& a, int r, Red&
   i64 sh, a2;
   bool exact = false;      // a row holding INT64_MIN after the shift
   i64 vmax = INT64_MAX, vmin = 0;
-  if constexpr (std::is_same<Red, BlockRed>::value) {
+  if constexpr (Red::kBlock) {
     vmax = 0;  // columns past C hold 0
 #pragma unroll
     for (int j = 0; j < VPT; ++j) {
@@ -998,7 +1004,7 @@ __global__ __launch_bounds__(NT) void k_merge_rowcol(MergeArgs a) {
     l2_warm(a.warm, blockIdx.x, a.nt, red_buf);
     return;
   }
-  BlockRed red{red_buf, 0, a.nt};
+  RowRed<NT> red{red_buf, 0, a.nt};
   merge_rowcol_row<VPT>(a, (int)blockIdx.x - (WARM ? L2WARM_BLOCKS : 0), red);
 }
 
@@ -1078,7 +1084,7 @@ __global__ __launch_bounds__(RT) void k_op_quant(const int64_t* x, const int64_t
                                                  int64_t* mo, int64_t* ko) {
   keep_hidden_args();
   __shared__ i64 red_buf[32];
-  BlockRed red{red_buf, 0, RT};
+  BlockRedT<RT / 64> red{red_buf, 0, RT};
   const int r = blockIdx.x;
   i64 v[VPT];
   load_row64(v, x, (i64)r * C, C);
@@ -1092,7 +1098,7 @@ __global__ __launch_bounds__(RT) void k_op_requant_common(const int64_t* P, cons
                                                           int64_t* ko) {
   keep_hidden_args();
   __shared__ i64 red_buf[32];
-  BlockRed red{red_buf, 0, RT};
+  BlockRedT<RT / 64> red{red_buf, 0, RT};
   const int r = blockIdx.x;
   i64 v[VPT];
   load_row64(v, P, (i64)r * C, C);
@@ -1114,7 +1120,7 @@ __global__ __launch_bounds__(RT) void k_op_rowcol(const int64_t* P, const int64_
                                                   int64_t* ko) {
   keep_hidden_args();
   __shared__ i64 red_buf[32];
-  BlockRed red{red_buf, 0, RT};
+  BlockRedT<RT / 64> red{red_buf, 0, RT};
   const int r = blockIdx.x;
   i64 v[VPT];
   load_row64(v, P, (i64)r * C, C);
@@ -1149,7 +1155,7 @@ __global__ __launch_bounds__(RT) void k_op_residual(int mode, const int64_t* h_i
                                                     int32_t* h_out, int64_t* k_out) {
   keep_hidden_args();
   __shared__ i64 red_buf[32];
-  BlockRed red{red_buf, 0, RT};
+  BlockRedT<RT / 64> red{red_buf, 0, RT};
   const int r = blockIdx.x;
   i64 h[VPT];
   load_row64(h, h_in, (i64)r * C, C);
@@ -1174,7 +1180,7 @@ __global__ __launch_bounds__(RT) void k_op_rmsnorm(const int64_t* x, const int64
                                                    int C, int32_t* y32, int64_t* y64) {
   keep_hidden_args();
   __shared__ i64 red_buf[32];
-  BlockRed red{red_buf, 0, RT};
+  BlockRedT<RT / 64> red{red_buf, 0, RT};
   const int r = blockIdx.x;
   i64 v[VPT];
   load_row64(v, x, (i64)r * C, C);
@@ -1197,7 +1203,7 @@ __global__ __launch_bounds__(RT) void k_op_softmax(const int64_t* x, const int64
   keep_hidden_args();
   // ops/di_softmax.py:33-61
   __shared__ i64 red_buf[32];
-  BlockRed red{red_buf, 0, RT};
+  BlockRedT<RT / 64> red{red_buf, 0, RT};
   const int r = blockIdx.x;
   const i64 off = (i64)r * C;
   const i64 NEG = INT64_MIN + 1;
@@ -1499,8 +1505,8 @@ __global__ __launch_bounds__(PRO_THREADS) void k_gemv_pro(ProGemv g, ResNormArgs
       a.xk = nullptr;
     }
     if (ONE) {
-      BlockRed red{L.red_buf, 0, PRO_THREADS};
-      residual_normq_row<CMAX / PRO_THREADS, BlockRed, 1>(a, 0, red);
+      BlockRedT<PRO_THREADS / 64> red{L.red_buf, 0, PRO_THREADS};
+      residual_normq_row<CMAX / PRO_THREADS, decltype(red), 1>(a, 0, red);
     } else if (wave < g.R) {
       WaveRed red;
       residual_normq_row<CMAX / 64, WaveRed, 1>(a, wave, red);
@@ -1513,7 +1519,7 @@ __global__ __launch_bounds__(PRO_THREADS) void k_gemv_pro(ProGemv g, ResNormArgs
       a.yk = nullptr;
     }
     if (ONE) {
-      BlockRed red{L.red_buf, 0, PRO_THREADS};
+      BlockRedT<PRO_THREADS / 64> red{L.red_buf, 0, PRO_THREADS};
       swiglu_quant_row<CMAX / PRO_THREADS>(a, 0, red);
     }
   } else {
@@ -1525,7 +1531,7 @@ __global__ __launch_bounds__(PRO_THREADS) void k_gemv_pro(ProGemv g, ResNormArgs
       a.ak = nullptr;
     }
     if (ONE) {
-      BlockRed red{L.red_buf, 0, PRO_THREADS};
+      BlockRedT<PRO_THREADS / 64> red{L.red_buf, 0, PRO_THREADS};
       merge_rowcol_row<CMAX / PRO_THREADS>(a, 0, red);
     } else if (wave < g.R) {
       WaveRed red;
@@ -1656,8 +1662,14 @@ void launch_pro(const ProGemv& g, int ni, int ksplit, const ResNormArgs& ra, con
     int thr_, vpt_;                                                                          \
     if ((ARGS).warm.nwarm > 0 && (R) <= 64 && wide_shape((C), &thr_, &vpt_) && vpt_ == 4) { \
       (ARGS).nt = thr_;                                                                      \
-      hipLaunchKernelGGL((KERNEL<4, RT_WIDE, true>), dim3(L2WARM_BLOCKS + (R)), dim3(thr_), \
-                         0, STREAM, ARGS);                                                   \
+      const dim3 g_(L2WARM_BLOCKS + (R));                                                    \
+      switch (thr_) { /* the model's widths at their exact thread count */                   \
+        case 256: hipLaunchKernelGGL((KERNEL<4, 256, true>), g_, dim3(256), 0, STREAM, ARGS); break; \
+        case 512: hipLaunchKernelGGL((KERNEL<4, 512, true>), g_, dim3(512), 0, STREAM, ARGS); break; \
+        case 768: hipLaunchKernelGGL((KERNEL<4, 768, true>), g_, dim3(768), 0, STREAM, ARGS); break; \
+        default:                                                                             \
+          hipLaunchKernelGGL((KERNEL<4, RT_WIDE, true>), g_, dim3(thr_), 0, STREAM, ARGS);   \
+      }                                                                                      \
     } else {                                                                                 \
       DI_ROWS_DISPATCH(R, C, KERNEL, dim3(R), STREAM, ARGS);                                 \
     }                                                                                        \
