@@ -114,6 +114,14 @@ __device__ __forceinline__ i64 buf_ld_i64(bufv_t r, uint32_t off) {
 __device__ __forceinline__ int32_t buf_ld_i32(bufv_t r, uint32_t off) {
   return (int32_t)__builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 0);
 }
+// 16 bytes; an offset of BUF_OOB (beyond any view, no 32-bit wrap with the
+// access size added) reads 0, so a lane masks its load with a select
+constexpr uint32_t BUF_OOB = 0x7FFFFFF0u;
+template <class V4>
+__device__ __forceinline__ V4 buf_ld_16(bufv_t r, uint32_t off) {
+  const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0);
+  return V4{(int)v[0], (int)v[1], (int)v[2], (int)v[3]};
+}
 __device__ __forceinline__ int32_t buf_ld_i8(bufv_t r, uint32_t off) {
   return (int32_t)(int8_t)__builtin_amdgcn_raw_buffer_load_b8(r, (int)off, 0, 0);
 }

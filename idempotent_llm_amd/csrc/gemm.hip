@@ -304,22 +304,28 @@ __global__ __launch_bounds__(256) void k_gemv_dec(GemvArgs g, Prefetch pf) {
   const int r16 = lane & 15, grp = lane >> 4;
   const int col = blockIdx.x * 16 + r16;
   const bool colok = col < g.N;
-  const bool rowok = r16 < g.M;
   const int kbeg = blockIdx.y * g.kchunk;
   const int kend = min(g.K, kbeg + g.kchunk);
   const int k0 = kbeg + wave * 256 + grp * 64;
-  const int8_t* brow = g.B + (i64)(colok ? col : 0) * g.K;
-  const int8_t* arow = g.A + (i64)(rowok ? r16 : 0) * g.K;
+  // buffer views of the block's 16 weight rows (those below N) and of the M
+  // operand rows: a lane's row past either end reads 0 by the range check,
+  // and a slice past the block's K range gets an offset beyond both views,
+  // so every load is unconditional (no branch around it) and addressed by
+  // one 32-bit offset (16 K < 2^21)
+  const int ncols = min(16, g.N - (int)blockIdx.x * 16);
+  const bufv_t bv = buf_view(g.B + (i64)blockIdx.x * 16 * g.K, (i64)ncols * g.K);
+  const bufv_t av = buf_view(g.A, (i64)g.M * g.K);
+  const uint32_t rowoff = (uint32_t)(r16 * g.K);
   v4i b[4], a[4];
 #pragma unroll
   for (int u = 0; u < 4; ++u) {
     const int kk = k0 + u * 16;
-    b[u] = (colok && kk < kend) ? *(const v4i*)(brow + kk) : zero4();
+    b[u] = buf_ld_16<v4i>(bv, kk < kend ? rowoff + (uint32_t)kk : BUF_OOB);
   }
 #pragma unroll
   for (int u = 0; u < 4; ++u) {
     const int kk = k0 + u * 16;
-    a[u] = (rowok && kk < kend) ? *(const v4i*)(arow + kk) : zero4();
+    a[u] = buf_ld_16<v4i>(av, kk < kend ? rowoff + (uint32_t)kk : BUF_OOB);
   }
   const PrefetchHold ph =
       prefetch_issue(pf, blockIdx.y == 0 ? (i64)blockIdx.x * 256 + tid : (i64)-1);
@@ -391,8 +397,12 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_static(GemvArgs g, const int64
   const int col = blockIdx.x * 16 + r16;
   const bool colok = col < g.N;
   const int M = g.M, K = g.K;
-  const int8_t* brow = g.B + (i64)(colok ? col : 0) * K;
   const i64 cm = col_m[colok ? col : 0];
+  // buffer views of the block's weight rows below N and of the M operand
+  // rows (rows past either end read 0; a slice past K gets an offset beyond
+  // both views): unconditional loads on 32-bit offsets (64 K < 2^23)
+  const bufv_t bv = buf_view(g.B + (i64)blockIdx.x * 16 * K, (i64)min(16, g.N - (int)blockIdx.x * 16) * K);
+  const bufv_t av = buf_view(g.A, (i64)M * K);
   v4i acc[4];
 #pragma unroll
   for (int mb = 0; mb < 4; ++mb) acc[mb] = zero4();
@@ -403,7 +413,7 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_static(GemvArgs g, const int64
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int kk = k0 + grp * 16 * U + u * 16;
-      b[u] = (colok && kk < K) ? *(const v4i*)(brow + kk) : zero4();
+      b[u] = buf_ld_16<v4i>(bv, kk < K ? (uint32_t)(r16 * K + kk) : BUF_OOB);
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
@@ -411,7 +421,7 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_static(GemvArgs g, const int64
 #pragma unroll
       for (int mb = 0; mb < 4; ++mb) {
         const int row = mb * 16 + r16;
-        a[u][mb] = (row < M && kk < K) ? *(const v4i*)(g.A + (i64)row * K + kk) : zero4();
+        a[u][mb] = buf_ld_16<v4i>(av, kk < K ? (uint32_t)(row * K + kk) : BUF_OOB);
       }
     }
   };

@@ -1480,15 +1480,21 @@ __global__ __launch_bounds__(PRO_THREADS) void k_gemv_pro(ProGemv g, ResNormArgs
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int bx = blockIdx.x, by = blockIdx.y;
   const int kbeg = by * g.kchunk;
-  // 1. this wave's weight fragments, loaded before anything else
+  // 1. this wave's weight fragments, loaded before anything else: a buffer
+  // view of the block's weight rows below N (a row past N reads 0, a slice
+  // past K gets an offset beyond the view), so the loads are unconditional
   v4i b[NB][NI];
+  {
+    const int c0 = bx * NB * 16;
+    const bufv_t bv = buf_view(g.B + (i64)c0 * g.K, (i64)min(NB * 16, g.N - c0) * g.K);
 #pragma unroll
-  for (int n = 0; n < NB; ++n) {
-    const int col = (bx * NB + n) * 16 + (lane & 15);
+    for (int n = 0; n < NB; ++n) {
+      const uint32_t rowoff = (uint32_t)((n * 16 + (lane & 15)) * g.K);
 #pragma unroll
-    for (int i = 0; i < NI; ++i) {
-      const int k = kbeg + (wave * NI + i) * 64 + (lane >> 4) * 16;
-      b[n][i] = (col < g.N && k < g.K) ? *(const v4i*)(g.B + (i64)col * g.K + k) : zero4();
+      for (int i = 0; i < NI; ++i) {
+        const int k = kbeg + (wave * NI + i) * 64 + (lane >> 4) * 16;
+        b[n][i] = buf_ld_16<v4i>(bv, k < g.K ? rowoff + (uint32_t)k : BUF_OOB);
+      }
     }
   }
   const PrefetchHold ph = prefetch_issue(pf, by == 0 ? (i64)bx * PRO_THREADS + tid : (i64)-1);
