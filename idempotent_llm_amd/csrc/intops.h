@@ -210,7 +210,7 @@ DI_HD void fit_dyadic_ratio(i64 num, i64 den, i64* m_out, i64* e_out) {
 }
 
 // fit_dyadic_ratio(num, 127): every requantisation to int8 fits its output
-// scale against 127. Same integer as the generic routine. For 0 < num < 2^56
+// scale against 127. Same integer as the generic routine. For 0 < num < 2^62
 // the divisions by 127 * 2^s go through srd127 / floor_div127 below (one fp64
 // fma each), whose dividends stay below 2^24 for the exponents this routine
 // tries (e = 21 - ilog2(num), then one step of +-1); any other num takes the
@@ -227,12 +227,13 @@ DI_HD uint32_t floor_div127(uint32_t y) {
 
 DI_HD i64 srd127(i64 num, i64 e) {
   // scaled_round_div(num, 127, e), valid ONLY for the (num, e) pairs that
-  // fit_dyadic_ratio_127 passes: 0 < num < 2^56 and e = 21 - ilog2(num) or
+  // fit_dyadic_ratio_127 passes: 0 < num < 2^62 and e = 21 - ilog2(num) or
   // one step from it, so num * 2^e < 2^23. Then rhad(x, 127 * 2^s) =
-  // floor(floor((x + h) / 2^s) / 127) with h = floor(127 * 2^s / 2), and
-  // rhad(x, 127) = floor((x + 63) / 127); either dividend is below 2^24
-  // (the uint32_t cast below would truncate a larger one, and floor_div127
-  // is proven for dividends below 2^32 only).
+  // floor(floor((x + h) / 2^s) / 127) with h = floor(127 * 2^s / 2) (s <= 42,
+  // h < 2^48, so the generic routine's x + h stays below 2^63 and does not
+  // wrap), and rhad(x, 127) = floor((x + 63) / 127); either dividend is below
+  // 2^24 (the uint32_t cast below would truncate a larger one, and
+  // floor_div127 is proven for dividends below 2^32 only).
   u64 y;
   if (e >= 0) {
     y = ((u64)num << e) + 63;
@@ -247,11 +248,11 @@ DI_HD i64 srd127(i64 num, i64 e) {
 
 DI_HD void fit_dyadic_ratio_127(i64 num, i64* m_out, i64* e_out) {
   const i64 lg = ilog2(num);
-  if (DI_UNLIKELY(num <= 0 || lg >= 56)) {
+  if (DI_UNLIKELY(num <= 0 || lg >= 62)) {
     fit_dyadic_ratio(num, 127, m_out, e_out);
     return;
   }
-  // e = 15 - (lg - 6) in [-34, 21]; num << e < 2^(lg + e + 1) <= 2^22: no wrap
+  // e = 15 - (lg - 6) in [-40, 21]; num << e < 2^(lg + e + 1) <= 2^22: no wrap
   i64 e = 21 - lg;
   i64 m = srd127(num, e);
   const i64 adj = (m >= 65536 ? -1 : 0) + (m < 32768 ? 1 : 0);

@@ -184,7 +184,7 @@ def test_scalar_ops_match_oracle(lib, golden_dir):
 def test_fit127_fast_path_matches_generic_and_golden(lib, golden_dir):
     """fit_dyadic_ratio(num, 127) through the constant-127 reciprocal path
     (what every fused kernel runs) equals the generic routine and the
-    reference's golden vectors, across the fast-path boundary (2^56) and at
+    reference's golden vectors, across the fast-path boundary (2^62) and at
     the adjustment edges (mantissas near 2^15 and 2^16)."""
     D = dict(np.load(os.path.join(golden_dir, "dyadic.npz")))
     m, e = _scalar(lib, 5, D["fit_num"])
@@ -195,7 +195,9 @@ def test_fit127_fast_path_matches_generic_and_golden(lib, golden_dir):
         (I64(1) << rnd.integers(0, 62, 20000).astype(I64)) + rnd.integers(-3, 4, 20000),
         np.arange(1, 5000, dtype=I64),
         np.array([(1 << 56) - 1, 1 << 56, (1 << 56) + 1, (1 << 55) + 12345, 127, 254, 127 << 20,
-                  (127 << 20) - 1, (1 << 63) - 1], I64)])
+                  (127 << 20) - 1, (1 << 63) - 1, (1 << 62) - 1, 1 << 62, (1 << 62) + 1,
+                  (1 << 62) - (127 << 40), (1 << 61) + (127 << 39) - 1], I64),
+        rnd.integers(1 << 56, 1 << 62, 20000, dtype=I64)])
     num = num[num > 0]
     fm, fe = _scalar(lib, 5, num)
     gm, ge = _scalar(lib, 3, num, np.full_like(num, 127))
