@@ -487,10 +487,13 @@ DI_HD int rhad_est_i8_f64(double n, const DivEst& D) {
   return sq < -128 ? -128 : (sq > 127 ? 127 : sq);
 }
 
-// rhad(s |a|, d) signed, for s |a| + d < 2^53 and quotients below 2^31: the
-// estimate may be one off once 2 s |a| + d reaches 2^51, so its truncation
-// q0 is corrected with the exact remainder s |a| + floor(d/2) - q0 d (all
-// terms below 2^54 as int64).
+// rhad(s |a|, d) signed, for s |a| + d < 2^53 and quotients below 2^31, or
+// for |a| <= d < 2^53 and 1 <= s <= 127: the estimate may be one off once
+// 2 s |a| + d reaches 2^51, so its truncation q0 is corrected with the exact
+// remainder n - q0 d, n = s |a| + floor(d/2). In the second case |a| is an
+// exact double, the fma's value (below 128.5) lies within 2^-44 of
+// (n + 1/2) / d, whose floor is floor(n / d), so q0 is within one of it, and
+// n < 2^60, q0 d <= 2^60 as int64.
 DI_HD int32_t rhad_est_corr_signed(i64 a, int s, i64 d, const DivEst& D) {
   const i64 n = (a < 0 ? -a : a) * (i64)s + (d >> 1);
   i64 q = (i64)(uint32_t)fma((double)(a < 0 ? -a : a), D.r, D.k);

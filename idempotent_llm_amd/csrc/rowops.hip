@@ -108,7 +108,9 @@ __device__ __forceinline__ void rmsnorm_row(i64 (&v)[VPT], int C, Red& red, i64 
 
 // dyadic.py:93-105. The quotients rhad(127 x, a) with |x| <= a come from the
 // fp64 estimate (intops.h rhad_est) when a < 2^43 (then 2 * 127 |x| + a <
-// 2^51 and no 127 x wraps), else from the 64-bit reciprocal.
+// 2^51 and no 127 x wraps), from the estimate corrected by its exact
+// remainder (rhad_est_corr_signed) when a < 2^53, else from the 64-bit
+// reciprocal.
 template <int VPT, class Red>
 __device__ __forceinline__ void quant_row(const i64 (&v)[VPT], i64 m_in, i64 k_in, int C,
                                           Red& red, int8_t* out, i64* m_out, i64* k_out,
@@ -124,6 +126,14 @@ __device__ __forceinline__ void quant_row(const i64 (&v)[VPT], i64 m_in, i64 k_i
     for (int j = 0; j < VPT; ++j) {
       const int c = red.tid() + j * red.nt();
       if (c < C) out[c] = (int8_t)rhad_est_signed(v[j], D);
+    }
+  } else if (DI_LIKELY(au < ((u64)1 << 53))) {
+    a = (i64)au;
+    const DivEst D = make_divest(a, 127.0);
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) {
+      const int c = red.tid() + j * red.nt();
+      if (c < C) out[c] = (int8_t)rhad_est_corr_signed(v[j], 127, a, D);
     }
   } else {
     a = DI_UNLIKELY(au >> 63) ? imax(row_absmax(v, red), 1) : (i64)au;
@@ -154,8 +164,9 @@ __device__ __forceinline__ void quant_row(const i64 (&v)[VPT], i64 m_in, i64 k_i
 // the whole row back to the caller (returns false: the caller recomputes
 // the values as int64 and runs quant_row). With a = max(max |v|, 1) below
 // 2^43 the quotients rhad(127 |v|, a) come from the fp64 estimate, exactly
-// as quant_row's (2 * 127 |v| + a < 2^51); a larger maximum converts the
-// values (exact below 2^53) and runs quant_row. Same integers and (m, k).
+// as quant_row's (2 * 127 |v| + a < 2^51); a maximum in [2^43, 2^53) takes
+// the same estimate corrected by its exact int64 remainder
+// (rhad_est_corr_signed). Same integers and (m, k) as quant_row.
 template <int VPT, class Red>
 __device__ __forceinline__ bool quant_row_f64(const double (&v)[VPT], bool ok, i64 m_in, i64 k_in,
                                               int C, Red& red, int8_t* out, i64* m_out,
@@ -166,7 +177,7 @@ __device__ __forceinline__ bool quant_row_f64(const double (&v)[VPT], bool ok, i
   const i64 bits = red.max(ok ? f64_bits(g) : f64_bits(__builtin_inf()));
   if (DI_UNLIKELY(bits >= f64_bits(__builtin_inf()))) return false;
   const double au = f64_from_bits(bits);
-  if (DI_UNLIKELY(au >= 0x1p43)) {
+  if (DI_UNLIKELY(au >= 0x1p53)) {  // (exact values stay below 2^53)
     i64 w[VPT];
 #pragma unroll
     for (int j = 0; j < VPT; ++j) w[j] = (i64)v[j];
@@ -177,11 +188,20 @@ __device__ __forceinline__ bool quant_row_f64(const double (&v)[VPT], bool ok, i
   norm_scale(m_in, k_in, &m, &k);
   const i64 a = imax((i64)au, 1);
   const DivEst D = make_divest(a, 127.0);
+  if (DI_LIKELY(au < 0x1p43)) {
 #pragma unroll
-  for (int j = 0; j < VPT; ++j) {
-    const int c = red.tid() + j * red.nt();
-    const uint32_t q = rhad_est(fabs(v[j]), D);
-    if (c < C) out[c] = (int8_t)(v[j] < 0 ? -(int32_t)q : (int32_t)q);
+    for (int j = 0; j < VPT; ++j) {
+      const int c = red.tid() + j * red.nt();
+      const uint32_t q = rhad_est(fabs(v[j]), D);
+      if (c < C) out[c] = (int8_t)(v[j] < 0 ? -(int32_t)q : (int32_t)q);
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) {
+      const int c = red.tid() + j * red.nt();
+      const int32_t q = rhad_est_corr_signed((i64)v[j], 127, a, D);
+      if (c < C) out[c] = (int8_t)q;
+    }
   }
   if (red.tid() == 0 && m_out) {
     if (defer_fit) {

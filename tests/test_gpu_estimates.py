@@ -114,7 +114,8 @@ def test_rhad_est_i8_saturation_edges():
 
 def test_rhad_est_corr_signed_near_2p53():
     """op 11 sign(a) rhad(|a| s, d) with the remainder step: s |a| + d up to
-    just below 2^53, quotients below 2^31 (the merge's 46-bit rows)."""
+    just below 2^53, quotients below 2^31 (the merge's 46-bit rows), and
+    |a| <= d < 2^53 at s = 127 (the fp64 row quantiser's large rows)."""
     rng = random.Random(7)
     A, B, C = [], [], []
     for s in (1, 127):
@@ -124,6 +125,16 @@ def test_rhad_est_corr_signed_near_2p53():
             for a in _boundary_operands(rng, d, s, a_max, 8) + [a_max, a_max - 1]:
                 for sg in (1, -1):
                     A.append(sg * a); B.append(d); C.append(s)
+    # the fp64 row quantiser's large rows: s = 127, |a| <= d < 2^53
+    for e in (43, 46, 50, 52):
+        d = (1 << e) + rng.randrange(1, 1 << 20)
+        for a in _boundary_operands(rng, d, 127, d, 8) + [d, d - 1]:
+            for sg in (1, -1):
+                A.append(sg * a); B.append(d); C.append(127)
+    for d in ((1 << 53) - 1, (1 << 53) - 3):
+        for a in (d, d - 1, d // 2, d // 127):
+            for sg in (1, -1):
+                A.append(sg * a); B.append(d); C.append(127)
     want = [rhad(a * c if a >= 0 else -((-a) * c), b) for a, b, c in zip(A, B, C)]
     assert run(11, A, B, C) == want
 

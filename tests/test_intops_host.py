@@ -439,7 +439,8 @@ def test_rhad_est_signed_i8_and_corrected(lib):
     divisions of the row kernels against exact rhad (Python integers) at
     their stated bounds: quantisation (s = 127, |a| <= d < 2^43), RMSNorm
     (s = 2^20, |a| <= 2^26), static requant (s = 1, |a|, d < 2^49, clamped),
-    merge (s = 127, |a| <= d < 2^46, corrected)."""
+    merge (s = 127, |a| <= d < 2^46, corrected), large-row quantisation
+    (s = 127, |a| <= d < 2^53, corrected)."""
     rnd = random.Random(23)
 
     def rh(a, d):
@@ -490,6 +491,20 @@ def test_rhad_est_signed_i8_and_corrected(lib):
     for _ in range(6000):
         d = rnd.randrange(1 << 40, 1 << 46)
         for a in near_ties(d, 127, d, 3) + [rnd.randrange(-d, d + 1), d, -d]:
+            A.append(a)
+            D.append(d)
+    got = _est_op(lib, 2, A, D, [127] * len(A))
+    assert got.tolist() == [rh(127 * a, d) for a, d in zip(A, D)]
+    # quantisation of rows with a maximum in [2^43, 2^53): |a| <= d < 2^53
+    # with the correction step (the fp64 row quantiser's large-row path)
+    A, D = [], []
+    for _ in range(8000):
+        d = rnd.randrange(1 << 43, 1 << rnd.randrange(44, 54))
+        for a in near_ties(d, 127, d, 3) + [rnd.randrange(-d, d + 1), d, -d]:
+            A.append(a)
+            D.append(d)
+    for d in ((1 << 53) - 1, (1 << 53) - 2, (1 << 52) + 1, 1 << 43):
+        for a in (d, -d, d - 1, (d - 1) // 2, d // 127, -(d // 127) - 1, 0):
             A.append(a)
             D.append(d)
     got = _est_op(lib, 2, A, D, [127] * len(A))
