@@ -65,6 +65,10 @@ DI_HD i64 wneg(i64 a) { return (i64)(0ull - (u64)a); }
 DI_HD i64 wabs(i64 a) { return a < 0 ? wneg(a) : a; }  // |INT64_MIN| stays INT64_MIN
 DI_HD i64 imax(i64 a, i64 b) { return a > b ? a : b; }
 DI_HD i64 imin(i64 a, i64 b) { return a < b ? a : b; }
+// -lim < x < lim (lim >= 1) as one unsigned comparison (x + lim - 1 taken
+// modulo 2^64), so a chain of operand bounds combines with & into one
+// branch-free mask instead of a short-circuit branch per operand
+DI_HD bool in_range(i64 x, i64 lim) { return (u64)x + (u64)(lim - 1) < (u64)(2 * lim - 1); }
 
 // torch.bitwise_left_shift / bitwise_right_shift on int64
 DI_HD i64 shl(i64 a, i64 k) { return (k < 0 || k >= 64) ? 0 : (i64)((u64)a << k); }

@@ -48,13 +48,15 @@ void di_host_scalar(int op, const int64_t* a, const int64_t* b, const int64_t* c
   }
 }
 // bitlen_f64 / rshift_round_f64 on integer inputs: out[i] = bit length of
-// a[i] (op 0) or rshift_round_f64(a[i], b[i]) converted back (op 1)
+// a[i] (op 0) or rshift_round_f64(a[i], b[i]) converted back (op 1); op 5:
+// in_range(a[i], b[i])
 void di_host_f64_int_op(int op, const int64_t* a, const int64_t* b, int64_t n, int64_t* out) {
   for (int64_t i = 0; i < n; ++i) {
     if (op == 0) out[i] = (int64_t)bitlen_f64((double)a[i]);
     else if (op == 1) out[i] = (int64_t)rshift_round_f64((double)a[i], (int)b[i]);
     else if (op == 2) out[i] = rhad_est_i8_f64((double)a[i], make_divest(b[i], 1.0));
     else if (op == 4) out[i] = (int64_t)bitlen_from_hiword(f64_hiword_abs((double)a[i]));
+    else if (op == 5) out[i] = in_range(a[i], b[i]) ? 1 : 0;
     else out[i] = rhad_est_signed_f64((double)a[i], make_divest(b[i], 127.0));
   }
 }

@@ -178,8 +178,7 @@ __device__ __forceinline__ bool qk_head_f64(bool is_q, const int32_t (&p)[N],
   bool ok = true;
 #pragma unroll
   for (int i = 0; i < N; ++i) {
-    ok = ok && wm[i] > -WM_LIM && wm[i] < WM_LIM && gm[i] > -G_LIM && gm[i] < G_LIM &&
-         (!is_q || (qs[i] > -QS_LIM && qs[i] < QS_LIM));
+    ok = ok & in_range(wm[i], WM_LIM) & in_range(gm[i], G_LIM) & (!is_q | in_range(qs[i], QS_LIM));
     y[i] = (double)p[i] * (double)(int32_t)wm[i];
     pm = ::max(pm, f64_hiword_abs(y[i]));
   }
@@ -648,7 +647,7 @@ __device__ __forceinline__ void qkv_rows4(const QKVArgs& a, int R, int r0, int s
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       nd[i] = (double)(int32_t)p[i] * (double)(int32_t)wm[i] * xs;
-      fast = fast && wm[i] > -WM_LIM && wm[i] < WM_LIM && fabs(nd[i]) < 0x1p49;
+      fast = fast & in_range(wm[i], WM_LIM) & (fabs(nd[i]) < 0x1p49);
     }
     int8_t o[8];
     if (DI_LIKELY(fast)) {
@@ -685,7 +684,7 @@ __device__ __forceinline__ void qkv_rows4(const QKVArgs& a, int R, int r0, int s
       gm[i] = ld_global(gam + c[i]);
       cs[i] = a.cos_t[pos * 128 + c[i]];
       sn[i] = a.sin_t[pos * 128 + c[i]];
-      qs[i] = is_q ? a.qs_m[kvh * 128 + c[i]] : 0;
+      qs[i] = a.qs_m[kvh * 128 + c[i]];  // (unconditional: K heads ignore it)
     }
   };
   i64 gm[8], qs[8];

@@ -255,7 +255,7 @@ __device__ __forceinline__ bool norm_quant_row_f64(const i64 (&h)[VPT], int C, R
   for (int j = 0; j < VPT; ++j) {
     x[j] = (double)rhad_est_signed_f64(x[j], D);
     if (smooth) {
-      ok = ok && sm[j] > -SM_LIM && sm[j] < SM_LIM;
+      ok = ok & in_range(sm[j], SM_LIM);
       x[j] *= (double)(int32_t)sm[j];
     }
   }
@@ -368,7 +368,7 @@ __device__ __forceinline__ bool requant_residual_f64(i64 (&h)[VPT], const i64 (&
   bool ok = true;
 #pragma unroll
   for (int j = 0; j < VPT; ++j) {
-    ok = ok && cm[j] > -CM_LIM && cm[j] < CM_LIM;
+    ok = ok & in_range(cm[j], CM_LIM);
     vd[j] = (double)(int32_t)P[j] * (double)(int32_t)cm[j];
     am = ::max(am, f64_hiword_abs(vd[j]));
   }
@@ -387,7 +387,7 @@ __device__ __forceinline__ bool requant_residual_f64(i64 (&h)[VPT], const i64 (&
   for (int j = 0; j < VPT; ++j) {
     const double d = rshift_round_f64(vd[j], (int)sh);
     const double al = rshift_round_f64(d * rmd, (int)down) * upf;
-    ok = ok && fabs(al) < 0x1p51;
+    ok = ok & (fabs(al) < 0x1p51);
     hn[j] = (double)(int32_t)h[j] + al;
     hm = ::max(hm, f64_hiword_abs(hn[j]));
   }
@@ -780,7 +780,7 @@ __device__ __forceinline__ void swiglu_quant_row(const SwigluArgs& a, int r, Red
     L0 = L1 = 0u;
 #pragma unroll
     for (int j = 0; j < VPT; ++j) {
-      ok = ok && gm[j] > -CM_LIM && gm[j] < CM_LIM && um[j] > -CM_LIM && um[j] < CM_LIM;
+      ok = ok & in_range(gm[j], CM_LIM) & in_range(um[j], CM_LIM);
       vg[j] = (double)(int32_t)gu[0][j] * (double)(int32_t)gm[j];
       vu[j] = (double)(int32_t)gu[1][j] * (double)(int32_t)um[j];
       L0 = ::max(L0, f64_hiword_abs(vg[j]));
@@ -834,7 +834,7 @@ __device__ __forceinline__ void swiglu_quant_row(const SwigluArgs& a, int r, Red
     bool ok = true;
 #pragma unroll
     for (int j = 0; j < VPT; ++j) {
-      ok = ok && dsm[j] > -DS_LIM && dsm[j] < DS_LIM;
+      ok = ok & in_range(dsm[j], DS_LIM);
       yd[j] = (double)(int32_t)swiglu_gsig_est(g32[j], Ee) * (double)u32[j] *
               (double)(int32_t)dsm[j];
     }

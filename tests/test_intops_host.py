@@ -526,6 +526,25 @@ def test_isqrt_est_matches_oracle(lib):
     assert np.array_equal(got, oim.isqrt(v))
 
 
+def test_in_range_bounds(lib):
+    """in_range(x, lim) (the row kernels' branch-free operand bounds) is
+    -lim < x < lim, at both edges and the int64 extremes, for every limit
+    the kernels use and random others."""
+    rnd = np.random.default_rng(78)
+    lims = [1 << 12, 1 << 15, 1 << 18, 1 << 21, 1, 2, 3] + [int(v) for v in rnd.integers(1, 1 << 40, 20)]
+    xs, ls = [], []
+    for lim in lims:
+        for x in (-lim - 1, -lim, -lim + 1, -1, 0, 1, lim - 1, lim, lim + 1,
+                  -(1 << 63), (1 << 63) - 1, -(1 << 62), (1 << 62)):
+            xs.append(x); ls.append(lim)
+        for x in rnd.integers(-(2 * lim), 2 * lim + 1, 50):
+            xs.append(int(x)); ls.append(lim)
+    x = np.array(xs, dtype=np.int64); b = np.array(ls, dtype=np.int64)
+    out = np.empty_like(x)
+    lib.di_host_f64_int_op(ctypes.c_int(5), _p(x), _p(b), ctypes.c_int64(x.size), _p(out))
+    assert [int(v) for v in out] == [int(-l < v < l) for v, l in zip(xs, ls)]
+
+
 def test_f64_integer_helpers(lib):
     """bitlen_f64 (the fp64 exponent) and bitlen_from_hiword (the exponent in
     the high word of |x|) equal int.bit_length of |x|, and
