@@ -37,6 +37,7 @@ SIGNATURES = {
     "detllm_igemv_resnormq": [P, P, I, I, I, I, L, P, I, L, P, P, P, L, I, P, P, P, P, P, L, P,
                               P, P, L, P, L, S],
     "detllm_igemv_merge": [P, P, I, I, I, I, L, P, I, L, P, L, P, L, P, P, P, L, P, L, S],
+    "detllm_igemv_merge_ext": [P, P, I, I, I, I, L, P, P, L, L, P, I, P, P, I, P, L, P, L, S],
     "detllm_swiglu_quant": [P, I, L, I, I, P, P, P, L, P, L, P, L, P, P, P, P, I, I, I, I, S],
     "detllm_igemv_swiglu": [P, P, I, I, I, L, P, I, L, P, P, P, L, P, L, P, L, P, P, I, P, L, P,
                             L, S],
@@ -50,6 +51,9 @@ SIGNATURES = {
     "detllm_attn_decode": [P, P, P, P, P, I, P, L, I, I, I, I, P, P, P, P, S],
     "detllm_qkv_attn_decode": [P, I, L, I, I, I, P, P, P, P, L, P, L, P, L, P, L, P, L, P, L,
                                P, P, P, P, P, P, P, P, L, P, P, P, I, P, L, P, L, I, P, P, P, P, S],
+    "detllm_qkv_attn_decode_ext": [P, I, L, I, I, I, P, P, P, P, L, P, L, P, L, P, L, P, L, P,
+                                   L, P, P, P, P, P, P, P, P, L, P, P, P, I, P, L, P, L, I, P,
+                                   P, P, P, P, P, S],
     "detllm_decode_prologue": [P, L, I, L, P, P, P, P, L, S],
     "detllm_op_quant_i8_pertoken": [P, P, P, I, I, P, P, P, S],
     "detllm_op_requant_i32_common": [P, P, P, I, L, I, I, I, P, P, S],

@@ -461,6 +461,12 @@ struct DecodeArgs {
   int S, n_q, n_kv;
   i64 valid_stride;
   int32_t* err;          // optional device error word (DI_ERR_SLOTS)
+  // optional (both or neither): the attention-output merge's per-column
+  // factor om [n_q * 128] and its row statistics ext [B][n_kv][2] — per
+  // (row, kv head) block the largest v and the largest ~v over the block's
+  // outputs v = out * om (int64, wrapping) and 0
+  const int64_t* om;
+  int64_t* ext;
 };
 
 constexpr int DEC_MAX_PAGES = 1024;  // ceil(131071 / DI_PAGE)
@@ -532,9 +538,10 @@ __device__ __forceinline__ void p_frags(const int32_t* pp, v4i& ahi, v4i& alo) {
 // (grp, l16), element r holds head 4 grp + r, channel 16 (NB wave + nb) + l16;
 // the colsum of that channel sits in row G (lane 16 (G / 4) + l16, element
 // G % 4). out_heads: the block's first head row of [.][128] int64.
-template <int G, int NB = 2>
+// each(nb, r, value) sees every stored value.
+template <int G, int NB = 2, class Each>
 __device__ __forceinline__ void store_pv(const v4i (&chi)[NB], const v4i (&clo)[NB],
-                                         int64_t* out_heads) {
+                                         int64_t* out_heads, Each&& each) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, l16 = lane & 15, grp = lane >> 4;
 #pragma unroll
   for (int nb = 0; nb < NB; ++nb) {
@@ -544,9 +551,18 @@ __device__ __forceinline__ void store_pv(const v4i (&chi)[NB], const v4i (&clo)[
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int hh = grp * 4 + r;
-      if (hh < G) out_heads[hh * 128 + d] = ((i64)chi[nb][r] + 64 * (i64)cs) * 128 + (i64)clo[nb][r];
+      if (hh < G) {
+        const i64 o = ((i64)chi[nb][r] + 64 * (i64)cs) * 128 + (i64)clo[nb][r];
+        out_heads[hh * 128 + d] = o;
+        each(nb, r, o);
+      }
     }
   }
+}
+template <int G, int NB = 2>
+__device__ __forceinline__ void store_pv(const v4i (&chi)[NB], const v4i (&clo)[NB],
+                                         int64_t* out_heads) {
+  store_pv<G, NB>(chi, clo, out_heads, [](int, int, i64) {});
 }
 
 // The slots a decode block scans: a.S, bounded by the device count when one
@@ -588,11 +604,34 @@ struct KPre {
 // compile-time choice: LDS-only code never issues flat accesses, which would
 // wait on every outstanding load). NW: waves of the block (4 or 8): a wave
 // takes every NW-th 16-slot block of the scores and 128 / NW channels of P.V.
-template <int G, int VP, bool SCR, bool PRE = false, int NW = 4>
+// The merge factors of a lane's outputs (store_pv's layout: head 4 grp + r,
+// channel 16 (NB wave + nb) + l16; heads past G read entry 0), loaded where
+// the caller's first loads issue.
+template <int G, int NB>
+struct OmPre {
+  static constexpr int RG = G < 4 ? G : 4;
+  i64 v[NB][RG];
+  __device__ __forceinline__ void load(const DecodeArgs& a, int kvh) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, l16 = lane & 15, grp = lane >> 4;
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+      for (int r = 0; r < RG; ++r) {
+        const int hh = grp * 4 + r;
+        const int d = wave * 16 * NB + nb * 16 + l16;
+        v[nb][r] = a.om[hh < G ? (kvh * G + hh) * 128 + d : 0];
+      }
+  }
+};
+
+// OMP: omp holds the merge factors (else decode_body loads them when a.ext
+// is set).
+template <int G, int VP, bool SCR, bool PRE = false, int NW = 4, bool OMP = false>
 __device__ __forceinline__ void decode_body(const DecodeArgs& a, int S, int kvh, int b,
                                             const int8_t* qsrc, const int64_t* tsrc,
                                             int32_t* sh_scores, const int32_t* pg_lds,
-                                            const KPre<8 / NW>& pre = KPre<8 / NW>{}) {
+                                            const KPre<8 / NW>& pre = KPre<8 / NW>{},
+                                            const OmPre<G, 8 / NW>& omp = OmPre<G, 8 / NW>{}) {
   static_assert(G <= 8, "query heads per kv head");
   static_assert(NW == 4 || NW == 8, "waves per block");
   constexpr int NT = NW * 64;  // threads
@@ -632,6 +671,12 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, int S, int kvh,
     const int8_t* vch = a.kv.vchan(pg < 0 ? 0 : pg, kvh, wave * 16 * NB + nb * 16 + l16);
     return *(const v4i*)(vch + (sl & (DI_PAGE - 1)));
   };
+
+  // the merge factors of this lane's outputs, used after P.V
+  constexpr int RG = OmPre<G, NB>::RG;
+  OmPre<G, NB> oml;
+  if (!OMP && a.ext != nullptr) oml.load(a, kvh);
+  const OmPre<G, NB>& omv = OMP ? omp : oml;
 
   // query fragments (row l16 = head) and the heads' DI-Exp constants
   v4i qa0 = v4i{0, 0, 0, 0}, qa1 = v4i{0, 0, 0, 0};
@@ -891,7 +936,24 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, int S, int kvh,
     for (int i = 0; i < 4; ++i)
       if (st0 + i < nstep) pv_step(st0 + i, vb[i]);
   }
-  store_pv<G, NB>(chi, clo, a.out + (i64)b * a.n_q * 128 + kvh * G * 128);
+  if (a.ext == nullptr) {
+    store_pv<G, NB>(chi, clo, a.out + (i64)b * a.n_q * 128 + kvh * G * 128);
+    return;
+  }
+  // with the merge's row statistics of the block's outputs (0 included, as
+  // merge_rowcol_row starts its extremes from 0)
+  i64 vmx = 0, nmn = -1;
+  store_pv<G, NB>(chi, clo, a.out + (i64)b * a.n_q * 128 + kvh * G * 128,
+                  [&](int nb, int r, i64 o) {
+                    const i64 v = wmul(o, omv.v[nb][r < RG ? r : 0]);
+                    vmx = imax(vmx, v);
+                    nmn = imax(nmn, ~v);
+                  });
+  red.max2(vmx, nmn);
+  if (tid == 0) {
+    a.ext[((i64)b * a.n_kv + kvh) * 2] = vmx;
+    a.ext[((i64)b * a.n_kv + kvh) * 2 + 1] = nmn;
+  }
 }
 
 template <int G, bool SCR>
@@ -982,6 +1044,9 @@ __global__ __launch_bounds__(QAD_WAVES * 64) void k_qkv_attn_decode(DecodeArgs a
   // to complete early)
   const int slotl = slotw >= 0 ? slotw : 0;
   QKVHeadIn in = qkv_head_load<NS1>(qa, b, slotl, QKVScalars{});
+  // the merge factors of this wave's outputs (for the row statistics)
+  OmPre<G, 8 / NW> omp;
+  if (a.ext != nullptr) omp.load(a, kvh);
   // (every load above is issued before the wait for the gathered scalars)
   __builtin_amdgcn_sched_barrier(0);
   in.pos_raw = readlane64(word, 0);
@@ -1049,8 +1114,8 @@ __global__ __launch_bounds__(QAD_WAVES * 64) void k_qkv_attn_decode(DecodeArgs a
     if (i < npages) pg_lds[i] = pgv[q];  // (loaded unconditionally above)
   }
   __syncthreads();
-  decode_body<G, VPRE_FUSED, SCR, true, NW>(a, S, kvh, b, &q_lds[0][0], t_lds, sh_scores,
-                                            pg_lds, pre);
+  decode_body<G, VPRE_FUSED, SCR, true, NW, true>(a, S, kvh, b, &q_lds[0][0], t_lds, sh_scores,
+                                                  pg_lds, pre, omp);
   report_slots(a, over, kvh == 0);
 }
 
@@ -1367,7 +1432,7 @@ int detllm_attn_decode(const int8_t* q8, const int64_t* tpos, const int8_t* kpoo
 
 // Fused decode step for one query token per row: the Q/K/V epilogue of
 // detllm_qkv_epilogue (T = 1) followed by detllm_attn_decode, one launch.
-int detllm_qkv_attn_decode(const int32_t* P, int nsplit, int64_t split_stride, int B, int n_q,
+static int qkv_attn_decode_launch(const int32_t* P, int nsplit, int64_t split_stride, int B, int n_q,
                            int n_kv, const int64_t* xm, const int64_t* xk,
                            const int64_t* positions, const int64_t* q_m, int64_t q_k,
                            const int64_t* k_m, int64_t k_k, const int64_t* v_m, int64_t v_k,
@@ -1380,7 +1445,7 @@ int detllm_qkv_attn_decode(const int32_t* P, int nsplit, int64_t split_stride, i
                            const int64_t* slot_base_dev, int64_t slot_base,
                            const uint8_t* valid, int64_t valid_stride, int S,
                            const int64_t* s_dev, int32_t* scratch, int64_t* out, int32_t* err,
-                           hipStream_t s) {
+                           const int64_t* om, int64_t* ext, hipStream_t s) {
   if (B <= 0) return DI_OK;
   if (n_q <= 0 || n_kv <= 0 || n_q % n_kv || nsplit < 1 || S < 1 ||
       !kv_ok(kpool, vpool, table, width) || S > (i64)width * DI_PAGE || valid_stride < S ||
@@ -1409,7 +1474,9 @@ int detllm_qkv_attn_decode(const int32_t* P, int nsplit, int64_t split_stride, i
   qa.ks_m = ks_m; qa.ks_k = ks_k; qa.vq_m = vq_m; qa.vq_k = vq_k; qa.cos_t = cos_t;
   qa.sin_t = sin_t; qa.max_pos = max_pos; qa.q8 = nullptr; qa.tpos = nullptr; qa.dbg = nullptr;
   qa.kv = kv; qa.slot_base_dev = slot_base_dev; qa.slot_base = slot_base; qa.err = err;
-  DecodeArgs a{nullptr, nullptr, kv, valid, out, scratch, s_dev, S, n_q, n_kv, valid_stride, err};
+  if ((om == nullptr) != (ext == nullptr)) return DI_EINVAL;
+  DecodeArgs a{nullptr, nullptr, kv, valid, out, scratch, s_dev, S, n_q, n_kv, valid_stride, err,
+               om, ext};
   const dim3 grid(n_kv, B);
 #define DI_QAD_LAUNCH(G_, NS1_)                                                                 \
   if (scratch) hipLaunchKernelGGL((k_qkv_attn_decode<G_, NS1_, true>), grid, dim3(QAD_WAVES * 64), dyn, s, a, qa); \
@@ -1424,6 +1491,49 @@ int detllm_qkv_attn_decode(const int32_t* P, int nsplit, int64_t split_stride, i
 #undef DI_QAD_LAUNCH
   DI_LAUNCH_CHECK();
   return DI_OK;
+}
+
+int detllm_qkv_attn_decode(const int32_t* P, int nsplit, int64_t split_stride, int B, int n_q,
+                           int n_kv, const int64_t* xm, const int64_t* xk,
+                           const int64_t* positions, const int64_t* q_m, int64_t q_k,
+                           const int64_t* k_m, int64_t k_k, const int64_t* v_m, int64_t v_k,
+                           const int64_t* q_norm_m, int64_t q_norm_k, const int64_t* k_norm_m,
+                           int64_t k_norm_k, const int64_t* qs_m, int64_t qs_k,
+                           const int64_t* kq_m, const int64_t* kq_k, const int64_t* ks_m,
+                           const int64_t* ks_k, const int64_t* vq_m, const int64_t* vq_k,
+                           const int16_t* cos_t, const int16_t* sin_t, int64_t max_pos,
+                           int8_t* kpool, int8_t* vpool, const int32_t* table, int width,
+                           const int64_t* slot_base_dev, int64_t slot_base,
+                           const uint8_t* valid, int64_t valid_stride, int S,
+                           const int64_t* s_dev, int32_t* scratch, int64_t* out, int32_t* err,
+                           hipStream_t s) {
+  return qkv_attn_decode_launch(
+      P, nsplit, split_stride, B, n_q, n_kv, xm, xk, positions, q_m, q_k, k_m, k_k, v_m, v_k,
+      q_norm_m, q_norm_k, k_norm_m, k_norm_k, qs_m, qs_k, kq_m, kq_k, ks_m, ks_k, vq_m, vq_k,
+      cos_t, sin_t, max_pos, kpool, vpool, table, width, slot_base_dev, slot_base, valid,
+      valid_stride, S, s_dev, scratch, out, err, nullptr, nullptr, s);
+}
+
+int detllm_qkv_attn_decode_ext(const int32_t* P, int nsplit, int64_t split_stride, int B, int n_q,
+                           int n_kv, const int64_t* xm, const int64_t* xk,
+                           const int64_t* positions, const int64_t* q_m, int64_t q_k,
+                           const int64_t* k_m, int64_t k_k, const int64_t* v_m, int64_t v_k,
+                           const int64_t* q_norm_m, int64_t q_norm_k, const int64_t* k_norm_m,
+                           int64_t k_norm_k, const int64_t* qs_m, int64_t qs_k,
+                           const int64_t* kq_m, const int64_t* kq_k, const int64_t* ks_m,
+                           const int64_t* ks_k, const int64_t* vq_m, const int64_t* vq_k,
+                           const int16_t* cos_t, const int16_t* sin_t, int64_t max_pos,
+                           int8_t* kpool, int8_t* vpool, const int32_t* table, int width,
+                           const int64_t* slot_base_dev, int64_t slot_base,
+                           const uint8_t* valid, int64_t valid_stride, int S,
+                           const int64_t* s_dev, int32_t* scratch, int64_t* out, int32_t* err,
+                               const int64_t* om, int64_t* ext, hipStream_t s) {
+  if (!om || !ext) return DI_EINVAL;
+  return qkv_attn_decode_launch(
+      P, nsplit, split_stride, B, n_q, n_kv, xm, xk, positions, q_m, q_k, k_m, k_k, v_m, v_k,
+      q_norm_m, q_norm_k, k_norm_m, k_norm_k, qs_m, qs_k, kq_m, kq_k, ks_m, ks_k, vq_m, vq_k,
+      cos_t, sin_t, max_pos, kpool, vpool, table, width, slot_base_dev, slot_base, valid,
+      valid_stride, S, s_dev, scratch, out, err, om, ext, s);
 }
 
 // Chunking of the split-S decode attention: enough chunks that the launch has

@@ -892,7 +892,40 @@ struct MergeArgs {
   int64_t* ak;
   int defer_fit;  // (am, ak) left for the consumer to fit (quant_row)
   L2Warm warm;    // the next skinny GEMM's weights (extra blocks after the rows)
+  // k_gemv_pro PRO 4: the rows' statistics [R][n_ext][2] (per part of a row
+  // the largest v and the largest ~v, v = attn * os_m * col_m; the parts
+  // cover the row)
+  const int64_t* ext;
+  int n_ext;
 };
+
+// The merge's pre-shift sh and quantisation maximum a2 of a row from its
+// largest and smallest value (each taken together with 0), valid when every
+// |v| < 2^62: rshift_round(., sh) then cannot wrap and does not decrease, so
+// max |rshift_round(v, sh)| sits at an extreme, and so does the bit length
+// of max |v|. False (sh, a2 unset) outside that range.
+__device__ __forceinline__ bool merge_shift_ext(i64 vmax, i64 vmin, i64* sh, i64* a2) {
+  const i64 lim = (i64)1 << 62;
+  if (!(vmax < lim && vmin > -lim)) return false;
+  const uint32_t L = ::max(bitlen_abs(vmax), bitlen_abs(vmin));
+  *sh = imax(ilog2_from_bitlen(L) - 45, 0);
+  *a2 = imax(imax(wabs(rshift_round(vmax, *sh)), wabs(rshift_round(vmin, *sh))), 1);
+  return true;
+}
+
+// (am, ak) of a merged row: the fit of a2 / 127 (dyadic.py:137-139), or a2
+// itself for the consumer to fit (defer)
+__device__ __forceinline__ void merge_row_scale(const MergeArgs& a, int r, i64 a2, i64 sh) {
+  if (a.defer_fit) {
+    a.am[r] = a2;
+    a.ak[r] = wsub(wadd(a.os_k, a.col_k), sh);
+  } else {
+    i64 mo, e;
+    fit_dyadic_ratio_127(a2, &mo, &e);
+    a.am[r] = mo;
+    a.ak[r] = wsub(wadd(wadd(a.os_k, a.col_k), e), sh);
+  }
+}
 
 template <int VPT, class Red>
 __device__ __forceinline__ void merge_rowcol_row(const MergeArgs& a, int r, Red& red) {
@@ -962,13 +995,9 @@ __device__ __forceinline__ void merge_rowcol_row(const MergeArgs& a, int r, Red&
     }
     vmin = ~nmin;
   }
-  const i64 lim = (i64)1 << 62;
-  if (DI_LIKELY(vmax < lim && vmin > -lim)) {
-    const uint32_t L = ::max(bitlen_abs(vmax), bitlen_abs(vmin));
-    sh = imax(ilog2_from_bitlen(L) - 45, 0);
+  if (DI_LIKELY(merge_shift_ext(vmax, vmin, &sh, &a2))) {
 #pragma unroll
     for (int j = 0; j < VPT; ++j) v[j] = rshift_round(v[j], sh);
-    a2 = imax(imax(wabs(rshift_round(vmax, sh)), wabs(rshift_round(vmin, sh))), 1);
   } else {
     sh = imax(row_ilog2_absmax(v, red) - 45, 0);
 #pragma unroll
@@ -1003,17 +1032,7 @@ __device__ __forceinline__ void merge_rowcol_row(const MergeArgs& a, int r, Red&
       if (c < C) a8[c] = (int8_t)clamp_i8(rhad_r(wmul(v[j], 127), R));
     }
   }
-  if (red.tid() == 0 && a.am) {
-    if (a.defer_fit) {
-      a.am[r] = a2;
-      a.ak[r] = wsub(wadd(a.os_k, a.col_k), sh);
-    } else {
-      i64 mo, e;
-      fit_dyadic_ratio_127(a2, &mo, &e);
-      a.am[r] = mo;
-      a.ak[r] = wsub(wadd(wadd(a.os_k, a.col_k), e), sh);
-    }
-  }
+  if (red.tid() == 0 && a.am) merge_row_scale(a, r, a2, sh);
 }
 
 template <int VPT, int NT = RT_WIDE, bool WARM = false>
@@ -1487,11 +1506,108 @@ struct ProLds {
   i64 red_buf[32];
 };
 
+constexpr int PRO_MAX_EXT = 8;  // statistics entries per row (MergeArgs::n_ext)
+
+// PRO 4: the operand rows of the merge (merge_rowcol_row's integers, nsplit
+// 1) over the block's K range [kbeg, kbeg + 512 NI) only, their row
+// statistics taken from a.ext instead of row reductions, so every value is
+// elementwise: lane r < R reduces row r's entries and fits its divisor once,
+// each wave then quantises 64 NI columns of every row. A row outside the
+// estimate tiers (extremes beyond merge_shift_ext's range, or a2 = 2^46) is
+// merged in full by merge_rowcol_row over the whole block. Lead: (am, ak)
+// stored.
+template <int NI, bool ONE, int CMAX>
+__device__ __forceinline__ void merge_rows_ext(const MergeArgs& a, int R, int kbeg, int8_t* a8,
+                                               int stride, i64* red_buf) {
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int K = a.C;
+  // this lane's columns and their factors; every row's values, loaded first
+  // (buffer views: rows >= R and columns >= K read 0)
+  constexpr int RMAX = ONE ? 1 : PRO_ROWS;  // rows the launch may hold
+  int col[NI];
+  i64 om[NI];
+  i64 x[RMAX][NI];
+  {
+    const bufv_t ov = buf_view(a.os_m, (i64)K * 8);
+    const bufv_t av = buf_view(a.attn, (i64)R * K * 8);
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+      col[i] = kbeg + (wave * NI + i) * 64 + lane;
+      om[i] = buf_ld_i64(ov, col[i] < K ? (uint32_t)col[i] * 8 : BUF_OOB);
+#pragma unroll
+      for (int r = 0; r < RMAX; ++r)
+        x[r][i] = buf_ld_i64(av, (r < R && col[i] < K) ? (uint32_t)(r * K + col[i]) * 8 : BUF_OOB);
+    }
+  }
+  // row statistics: lane r < R takes row r (other lanes row 0, unused);
+  // one view of the whole array (a descriptor must be wave-uniform: a
+  // per-lane base would make the compiler loop over the lanes' values)
+  v4i q[PRO_MAX_EXT];
+  {
+    const int rr = lane < R ? lane : 0;
+    const bufv_t ev = buf_view(a.ext, (i64)R * a.n_ext * 16);
+    const uint32_t rowoff = (uint32_t)(rr * a.n_ext) * 16;
+#pragma unroll
+    for (int e = 0; e < PRO_MAX_EXT; ++e)
+      q[e] = buf_ld_16<v4i>(ev, e < a.n_ext ? rowoff + (uint32_t)e * 16 : BUF_OOB);
+  }
+  // (every load above is issued before any is used)
+  __builtin_amdgcn_sched_barrier(0);
+  i64 vmax = 0, nmin = -1;
+#pragma unroll
+  for (int e = 0; e < PRO_MAX_EXT; ++e) {
+    const i64 hi = (i64)(((u64)(uint32_t)q[e][1] << 32) | (uint32_t)q[e][0]);
+    const i64 nm = (i64)(((u64)(uint32_t)q[e][3] << 32) | (uint32_t)q[e][2]);
+    vmax = imax(vmax, hi);
+    nmin = imax(nmin, e < a.n_ext ? nm : (i64)-1);
+  }
+  // the estimate tiers of merge_rowcol_row (a2 < 2^46: rhad_est, plain
+  // below 2^43, corrected above); a row past them (a2 = 2^46 after rounding,
+  // or extremes beyond 2^62) takes the fallback below
+  i64 sh = 0, a2 = 1;
+  const bool fast = merge_shift_ext(vmax, ~nmin, &sh, &a2) && a2 < ((i64)1 << 46);
+  const uint32_t fastm = (uint32_t)__ballot(fast) & ((1u << R) - 1u);
+  const DivEst D = make_divest(fast ? a2 : 1, 127.0);
+  if (a.am && lane < R && fast) merge_row_scale(a, lane, a2, sh);
+#pragma unroll
+  for (int r = 0; r < RMAX; ++r) {
+    if (r >= R || !((fastm >> r) & 1u)) continue;  // wave-uniform
+    // one row: every lane computed row 0's values; else lane r's
+    const i64 shr = ONE ? sh : readlane64(sh, r), a2r = ONE ? a2 : readlane64(a2, r);
+    DivEst Dr = D;
+    if (!ONE) {
+      Dr.r = __longlong_as_double(readlane64(__double_as_longlong(D.r), r));
+      Dr.k = __longlong_as_double(readlane64(__double_as_longlong(D.k), r));
+    }
+    int8_t* const row = a8 + r * stride;
+    if (DI_LIKELY(a2r < ((i64)1 << 43))) {
+#pragma unroll
+      for (int i = 0; i < NI; ++i)
+        if (col[i] < K) row[col[i]] = (int8_t)rhad_est_signed(rshift_round(wmul(x[r][i], om[i]), shr), Dr);
+    } else {
+#pragma unroll
+      for (int i = 0; i < NI; ++i)
+        if (col[i] < K)
+          row[col[i]] = (int8_t)rhad_est_corr_signed(rshift_round(wmul(x[r][i], om[i]), shr), 127, a2r, Dr);
+    }
+  }
+  if (DI_UNLIKELY(fastm != (1u << R) - 1u)) {
+    // rows past the estimate tiers: the row kernel's own reductions, one row
+    // at a time over the whole block (few registers per thread)
+    MergeArgs m = a;
+    m.a8 = a8;
+    m.a8_stride = stride;
+    BlockRedT<PRO_THREADS / 64> red{red_buf, 0, PRO_THREADS};
+    for (int r = 0; r < R; ++r)
+      if (!((fastm >> r) & 1u)) merge_rowcol_row<CMAX / PRO_THREADS>(m, r, red);  // uniform
+  }
+}
+
 // PRO 1: residual_normq (ResNormArgs, mode 1, C = K <= CMAX); 2: merge_rowcol
 // (MergeArgs, C = K <= CMAX); 3: swiglu_quant (SwigluArgs, I = K <= CMAX, one
-// row only). ONE: a single row, computed by the whole block (else one wave
-// per row); separate instantiations keep the one-row kernel free of the wave
-// path's registers.
+// row only); 4: merge_rows_ext (MergeArgs with ext). ONE: a single row,
+// computed by the whole block (else one wave per row); separate
+// instantiations keep the one-row kernel free of the wave path's registers.
 template <int PRO, int CMAX, int NI, int NB, bool ONE>
 __global__ __launch_bounds__(PRO_THREADS) void k_gemv_pro(ProGemv g, ResNormArgs ra, MergeArgs ma,
                                                          SwigluArgs sa, Prefetch pf) {
@@ -1548,6 +1664,13 @@ __global__ __launch_bounds__(PRO_THREADS) void k_gemv_pro(ProGemv g, ResNormArgs
       BlockRedT<PRO_THREADS / 64> red{L.red_buf, 0, PRO_THREADS};
       swiglu_quant_row<CMAX / PRO_THREADS>(a, 0, red);
     }
+  } else if constexpr (PRO == 4) {
+    MergeArgs a = ma;
+    if (!lead) {
+      a.am = nullptr;
+      a.ak = nullptr;
+    }
+    merge_rows_ext<NI, ONE, CMAX>(a, g.R, kbeg, &L.a[0][0], CMAX + 16, L.red_buf);
   } else {
     MergeArgs a = ma;
     a.a8 = &L.a[0][0];
@@ -1837,6 +1960,31 @@ int detllm_igemv_merge(const int8_t* W, int32_t* C, int R, int N, int K, int ksp
   m.os_k = os_k; m.col_m = col_m; m.col_k = col_k; m.am = am; m.ak = ak;
   const ProGemv g{W, C, R, N, K, kchunk, (i64)split_stride};
   launch_pro<2, 2048>(g, ni, ksplit, ResNormArgs{}, m, SwigluArgs{}, pf, s);
+  DI_LAUNCH_CHECK();
+  return DI_OK;
+}
+
+int detllm_igemv_merge_ext(const int8_t* W, int32_t* C, int R, int N, int K, int ksplit,
+                           int64_t split_stride, const int64_t* attn, const int64_t* om,
+                           int64_t os_k, int64_t col_k, const int64_t* ext, int n_ext,
+                           int64_t* am, int64_t* ak, int defer_fit, const void* pf0, int64_t n0,
+                           const void* pf1, int64_t n1, hipStream_t s) {
+  if (R <= 0 || N <= 0) return DI_OK;
+  if (R > PRO_ROWS || K > 2048 || !W || !C || !attn || !om || !ext || n_ext < 1 ||
+      n_ext > PRO_MAX_EXT || !am || !ak || (defer_fit != 0 && defer_fit != 1) ||
+      (ksplit > 1 && split_stride < (int64_t)R * N))
+    return DI_EINVAL;
+  int kchunk = 0;
+  const int ni = pro_steps(K, ksplit, &kchunk);
+  if (ni == 0) return DI_ENOSYS;
+  Prefetch pf;
+  if (!pro_prefetch(pf0, n0, pf1, n1, &pf)) return DI_EINVAL;
+  MergeArgs m{};
+  m.C = K; m.attn = attn; m.nsplit = 1; m.split_stride = 0; m.os_m = om; m.os_k = os_k;
+  m.col_m = nullptr; m.col_k = col_k; m.am = am; m.ak = ak; m.defer_fit = defer_fit;
+  m.ext = ext; m.n_ext = n_ext;
+  const ProGemv g{W, C, R, N, K, kchunk, (i64)split_stride};
+  launch_pro<4, 2048>(g, ni, ksplit, ResNormArgs{}, m, SwigluArgs{}, pf, s);
   DI_LAUNCH_CHECK();
   return DI_OK;
 }

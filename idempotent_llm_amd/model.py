@@ -52,6 +52,12 @@ GREEDY_CHUNK = 2048
 DEC_MAX_SLOTS = 131071
 # decode rows scanning at least this many slots use the split-S attention
 SPLIT_MIN_SLOTS = 2048
+# decode batches up to this many rows take the o-GEMV that quantises its own
+# K range of the merged rows (detllm_igemv_merge_ext, which covers 8 rows):
+# at one row it replaces the fused merge's row reductions (c3 b1 1.136 ->
+# 1.126 ms per step); at eight rows every block quantising all eight rows of
+# its range outlasts the separate merge launch (1.408 -> 1.418)
+MERGE_EXT_ROWS = 1
 
 
 @dataclass
@@ -462,8 +468,10 @@ class IntQwen3:
     def _attend(self, L: LayerWeights, B, T, P, ns, st, xm, xk, pos, cache: KVCache, S_past, S,
                 static):
         """Q/K/V epilogue (cache write) and attention of one layer from the
-        QKV partials P. Returns (attn, nsplit, split_stride): int64 context
-        partials [nsplit][B * T][n_q * hd] whose sum is the context."""
+        QKV partials P. Returns (attn, nsplit, split_stride, ext): int64
+        context partials [nsplit][B * T][n_q * hd] whose sum is the context,
+        and the merge statistics [B][n_kv][2] of a decode step's context
+        (detllm_qkv_attn_decode_ext), else None."""
         dev = self.device
         R, nq, nkv, hd = B * T, self.n_q, self.n_kv, self.hd
         li = L.idx
@@ -486,23 +494,30 @@ class IntQwen3:
             call("detllm_attn_decode_split", q8, tpos, *cache.layer_args(li), valid, cache.cap,
                  B, S, nq, nkv, cache.nslots if static else None, chunk, scores, cmax, attn,
                  self._err)
-            return attn, nsp, R * nq * hd
+            return attn, nsp, R * nq * hd, None
         attn = torch.empty(R, nq * hd, dtype=I64, device=dev)
         if T == 1 and nq // nkv <= 2:
             # decode: Q/K/V epilogue and attention in one launch
             scratch = self._decode_scratch(B, S)
-            call("detllm_qkv_attn_decode", P, ns, st, B, nq, nkv, xm, xk, pos,
-                 L.q_m, L.q_k, L.k_m, L.k_k, L.v_m, L.v_k, L.q_norm_m, L.q_norm_k,
-                 L.k_norm_m, L.k_norm_k, L.qs_m, L.qs_k, L.kq_m, L.kq_k, L.ks_m, L.ks_k,
-                 L.vq_m, L.vq_k, self.rope_cos, self.rope_sin, self.max_pos,
-                 *cache.layer_args(li), cache.len_idx if static else None,
-                 0 if static else S_past, valid, cache.cap, S,
-                 cache.nslots if static else None, scratch, attn, self._err)
+            args = (P, ns, st, B, nq, nkv, xm, xk, pos,
+                    L.q_m, L.q_k, L.k_m, L.k_k, L.v_m, L.v_k, L.q_norm_m, L.q_norm_k,
+                    L.k_norm_m, L.k_norm_k, L.qs_m, L.qs_k, L.kq_m, L.kq_k, L.ks_m, L.ks_k,
+                    L.vq_m, L.vq_k, self.rope_cos, self.rope_sin, self.max_pos,
+                    *cache.layer_args(li), cache.len_idx if static else None,
+                    0 if static else S_past, valid, cache.cap, S,
+                    cache.nslots if static else None, scratch, attn, self._err)
+            if B <= MERGE_EXT_ROWS and nq * hd <= 2048 and nkv <= 8:
+                # with the merge's row statistics, for the o-GEMV that
+                # quantises its own K range of the operand
+                ext = torch.empty(B, nkv, 2, dtype=I64, device=dev)
+                call("detllm_qkv_attn_decode_ext", *args, L.osc_m, ext)
+                return attn, 1, 0, ext
+            call("detllm_qkv_attn_decode", *args)
         elif T > 1 and self._seams_overridden():
             self._attention_seams(L, B, T, P, ns, st, xm, xk, pos, cache, S_past, S, attn)
         else:
             self._attention(L, B, T, P, ns, st, xm, xk, pos, cache, S_past, S, static, attn)
-        return attn, 1, 0
+        return attn, 1, 0, None
 
     def _partials(self, R: int, N: int, K: int):
         ks = self._ksplit(N, K, R)
@@ -533,8 +548,14 @@ class IntQwen3:
             nxt = self.layers[li + 1] if li + 1 < self.n_layers else None
             attn = self._attend(L, B, 1, P, ns, st, xm, xk, pos, cache, S_past, S, static)
             Po, nso, sto = self._partials(R, H, nq * hd)
-            call("detllm_igemv_merge", L.wo, Po, R, H, nq * hd, nso, sto, *attn, L.osc_m,
-                 L.os_k, None, L.attn_out_col_k, am, ak, L.pf_o, L.pf_o.numel() * 8, None, 0)
+            if attn[3] is not None:
+                call("detllm_igemv_merge_ext", L.wo, Po, R, H, nq * hd, nso, sto, attn[0],
+                     L.osc_m, L.os_k, L.attn_out_col_k, attn[3], self.n_kv, am, ak, 0,
+                     L.pf_o, L.pf_o.numel() * 8, None, 0)
+            else:
+                call("detllm_igemv_merge", L.wo, Po, R, H, nq * hd, nso, sto, *attn[:3],
+                     L.osc_m, L.os_k, None, L.attn_out_col_k, am, ak, L.pf_o,
+                     L.pf_o.numel() * 8, None, 0)
             Pg, nsg, stg = self._partials(R, 2 * I_, H)
             call("detllm_igemv_resnormq", L.wgu, Pg, R, 2 * I_, H, nsg, stg, Po, nso, sto, am, ak,
                  L.o_m, L.o_k, 20, hb[cur], kb[cur], hb[1 - cur], kb[1 - cur], L.ms_m, L.ms_k,
@@ -658,9 +679,19 @@ class IntQwen3:
         # decode sizes: the merge and the SwiGLU leave their scale fits to the
         # residual kernel after the next GEMM (same integers)
         dfit = 1 if R <= 64 else 0
-        call("detllm_merge_rowcol", *attn, R, nq * hd, L.os_m, L.os_k, L.attn_out_col_m,
-             L.attn_out_col_k, a8, am, ak, *self._next_gemm(L.wo, R), dfit)
-        P, ns, st = self._gemm(a8, L.wo, (L.pf_o,))
+        ks = self._ksplit(H, nq * hd, R) if attn[3] is not None else 0
+        if attn[3] is not None and pro_fits(nq * hd, ks):
+            # the o-GEMV quantises its own K range of the merged rows from the
+            # attention's row statistics (no merge launch)
+            P = torch.empty(ks, R, H, dtype=torch.int32, device=dev)
+            ns, st = ks, R * H
+            call("detllm_igemv_merge_ext", L.wo, P, R, H, nq * hd, ks, st, attn[0], L.osc_m,
+                 L.os_k, L.attn_out_col_k, attn[3], self.n_kv, am, ak, dfit, L.pf_o,
+                 L.pf_o.numel() * 8, None, 0)
+        else:
+            call("detllm_merge_rowcol", *attn[:3], R, nq * hd, L.os_m, L.os_k,
+                 L.attn_out_col_m, L.attn_out_col_k, a8, am, ak, *self._next_gemm(L.wo, R), dfit)
+            P, ns, st = self._gemm(a8, L.wo, (L.pf_o,))
         call("detllm_residual_normq", P, ns, st, R, H, am, ak, L.o_m, L.o_k, 20, h, k_res,
              L.ms_m, L.ms_k, x8, xm, xk, *self._next_gemm(L.wgu, R), dfit)
         P, ns, st = self._gemm(x8, L.wgu, (L.pf_mlp,))

@@ -170,6 +170,19 @@ int detllm_igemv_resnormq(const int8_t* W, int32_t* C, int R, int N, int K, int 
                           const void* pf0, int64_t n0, const void* pf1, int64_t n1,
                           hipStream_t s);
 
+/* detllm_igemv_merge_ext: detllm_igemv_merge (one partial of attn [R][K])
+ * whose merge statistics come from ext [R][n_ext][2] as
+ * detllm_qkv_attn_decode_ext writes them (n_ext = n_kv), so each block
+ * quantises only its K range of the operand rows, every value elementwise —
+ * the same integers as requant_i8_rowcol (dyadic.py:123-139, model.py:
+ * 404-409). om [K]: the per-column product os_m * col_m; n_ext <= 8;
+ * defer_fit as in detllm_merge_rowcol. */
+int detllm_igemv_merge_ext(const int8_t* W, int32_t* C, int R, int N, int K, int ksplit,
+                           int64_t split_stride, const int64_t* attn, const int64_t* om,
+                           int64_t os_k, int64_t col_k, const int64_t* ext, int n_ext,
+                           int64_t* am, int64_t* ak, int defer_fit, const void* pf0, int64_t n0,
+                           const void* pf1, int64_t n1, hipStream_t s);
+
 /* detllm_igemv_merge: operand = the attention-output merge
  * requant_i8_rowcol(attn * os_m, 1, os_k, col_m, col_k) — model.py:404-409 —
  * of int64 attn [nsplit][R][K], K <= 2048; col_m may be null when os_m holds
@@ -361,6 +374,27 @@ int detllm_qkv_attn_decode(const int32_t* P, int nsplit, int64_t split_stride, i
                            const uint8_t* valid, int64_t valid_stride, int S,
                            const int64_t* s_dev, int32_t* scratch, int64_t* out, int32_t* err,
                            hipStream_t s);
+
+/* detllm_qkv_attn_decode, and the merge statistics of its output for
+ * detllm_igemv_merge_ext: om [n_q * 128] the merge's per-column factor
+ * os_m * col_m (model.py:404-409); ext [B][n_kv][2] int64: for row b and kv
+ * head h, the largest v and the largest ~v over v = out[b][c] * om[c]
+ * (int64, wrapping) for the columns c of h's query heads, and 0 — the
+ * extremes dyadic.py:133-136 reduces over the row. */
+int detllm_qkv_attn_decode_ext(const int32_t* P, int nsplit, int64_t split_stride, int B,
+                               int n_q, int n_kv, const int64_t* xm, const int64_t* xk,
+                               const int64_t* positions, const int64_t* q_m, int64_t q_k,
+                               const int64_t* k_m, int64_t k_k, const int64_t* v_m, int64_t v_k,
+                               const int64_t* q_norm_m, int64_t q_norm_k,
+                               const int64_t* k_norm_m, int64_t k_norm_k, const int64_t* qs_m,
+                               int64_t qs_k, const int64_t* kq_m, const int64_t* kq_k,
+                               const int64_t* ks_m, const int64_t* ks_k, const int64_t* vq_m,
+                               const int64_t* vq_k, const int16_t* cos_t, const int16_t* sin_t,
+                               int64_t max_pos, int8_t* kpool, int8_t* vpool,
+                               const int32_t* table, int width, const int64_t* slot_base_dev,
+                               int64_t slot_base, const uint8_t* valid, int64_t valid_stride,
+                               int S, const int64_t* s_dev, int32_t* scratch, int64_t* out,
+                               int32_t* err, const int64_t* om, int64_t* ext, hipStream_t s);
 
 /* ------------------------------------------- operator-level entry points -- */
 /* One reference function each (rows = leading dims flattened, C = last dim). */

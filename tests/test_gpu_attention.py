@@ -82,10 +82,26 @@ def _run(dims, B, cap, S, slot, device_bounds, seed):
     out_b = torch.empty(B, nq * hd, dtype=I64, device="cuda")
     call("detllm_qkv_attn_decode", P, ns, B * P.shape[2], B, nq, nkv, xm, xk, pos, *common,
          kb, vb, table, width, slot_dev, slot, vbytes, cap, S_host, s_dev, scratch, out_b, None)
+    # with the merge statistics (detllm_qkv_attn_decode_ext): the same
+    # cache and context, and per (row, kv head) the largest v and ~v over
+    # v = context * om of the kv head's query heads (and 0), om spanning
+    # products that wrap
+    om = torch.randint(-(1 << 40), 1 << 40, (nq * hd,), generator=rnd, dtype=I64).cuda()
+    kc, vc = k0.clone(), v0.clone()
+    out_c = torch.empty(B, nq * hd, dtype=I64, device="cuda")
+    ext = torch.full((B, nkv, 2), 99, dtype=I64, device="cuda")
+    call("detllm_qkv_attn_decode_ext", P, ns, B * P.shape[2], B, nq, nkv, xm, xk, pos, *common,
+         kc, vc, table, width, slot_dev, slot, vbytes, cap, S_host, s_dev, scratch, out_c, None,
+         om, ext)
     torch.cuda.synchronize()
     assert torch.equal(ka, kb)
     assert torch.equal(va, vb)
     assert torch.equal(out_a, out_b)
+    assert torch.equal(kc, kb) and torch.equal(vc, vb) and torch.equal(out_c, out_b)
+    vv = (out_b.cpu() * om.cpu()).view(B, nkv, G * hd)   # int64 products wrap
+    hi = torch.clamp(vv.max(dim=2).values, min=0)
+    nm = torch.clamp((~vv).max(dim=2).values, min=-1)
+    assert torch.equal(ext.cpu(), torch.stack([hi, nm], dim=2))
     assert not torch.equal(ka, k0)          # the step's K slot was written
     assert out_a.abs().sum().item() > 0
 

@@ -156,6 +156,69 @@ def test_igemv_merge_equals_two_launches(R, N, K, nsplit, combined):
         assert ((top >= 2 ** 43) & (top < 2 ** 46)).any()
 
 
+def _merge_stats(v, n_ext):
+    """detllm_qkv_attn_decode_ext's statistics of rows v [R][K] (int64): per
+    part of K / n_ext columns the largest v and the largest ~v, each taken
+    together with 0 (for v) and ~0 (for ~v)."""
+    R, K = v.shape
+    parts = v.reshape(R, n_ext, K // n_ext)
+    hi = np.maximum(parts.max(axis=2), 0)
+    nm = np.maximum((~parts).max(axis=2), -1)
+    return np.stack([hi, nm], axis=2).astype(I64)
+
+
+@pytest.mark.parametrize("R", [1, 3, 8])
+@pytest.mark.parametrize("N,ks_pick,defer", [(1024, "plan", 1), (1024, 4, 0), (2000, 2, 1)])
+def test_igemv_merge_ext_equals_two_launches(R, N, ks_pick, defer):
+    """The o-GEMV that quantises only its own K range of the merged rows
+    from their statistics (detllm_igemv_merge_ext) against detllm_merge_rowcol
+    then detllm_igemv_nt: equal partials and row scales (fitted and deferred),
+    rows in every tier of the int8 quantiser, a zero row, and rows with values
+    at or beyond 2^62 (wrapping products included) that take the full-row
+    fallback."""
+    from idempotent_llm_amd._lib import call, pro_fits
+    K, n_ext = 2048, 8
+    ks = _fused_split(R, N, K) if ks_pick == "plan" else ks_pick
+    assert pro_fits(K, ks)
+    print(f"[igemv_merge_ext R={R} N={N} ks={ks} defer={defer}]", flush=True)
+    rng = np.random.default_rng(R * 31337 + N + ks + defer)
+    mags = [1 << 20, 1 << 39, 1 << 5, 0, 1 << 23, 1 << 29, 1 << 12, 1 << 38][:R]
+    if R == 1:
+        mags = [1 << 39] if defer else [1 << 26]
+    attn = np.stack([rng.integers(-m, m + 1, K) if m else np.zeros(K, I64) for m in mags]).astype(I64)
+    os_m = rng.integers(1 << 10, 1 << 12, K).astype(I64)
+    col_m = rng.integers(1 << 10, 1 << 12, K).astype(I64)
+    om = os_m * col_m
+    with np.errstate(over="ignore"):
+        v = attn * om
+    ext = _merge_stats(v, n_ext)
+    ag = g(attn)
+    w = g(rng.integers(-128, 128, (N, K)).astype(np.int8))
+    a8 = torch.empty(R, K, dtype=torch.int8, device="cuda")
+    am = torch.empty(R, dtype=torch.int64, device="cuda")
+    ak = torch.empty(R, dtype=torch.int64, device="cuda")
+    call("detllm_merge_rowcol", ag, 1, R * K, R, K, g(os_m), 7, g(col_m), 9, a8, am, ak, None, 0,
+         0, 0, defer)
+    want = _split_product(a8, w, ks)
+    for rep in range(2):
+        fm = torch.full((R,), -1, dtype=torch.int64, device="cuda")
+        fk = torch.full((R,), -1, dtype=torch.int64, device="cuda")
+        C = torch.full((ks, R, N), -7, dtype=torch.int32, device="cuda")
+        call("detllm_igemv_merge_ext", w, C, R, N, K, ks, R * N, ag, g(om), 7, 9, g(ext), n_ext,
+             fm, fk, defer, None, 0, None, 0)
+        assert torch.equal(C, want)
+        assert torch.equal(fm, am) and torch.equal(fk, ak)
+    prod = ogemm.int_gemm(a8.cpu().numpy(), w.cpu().numpy().T)
+    assert np.array_equal(want.sum(0).cpu().numpy().astype(I64), prod.astype(I64))
+    if R == 8:
+        # the rows reach every tier and the fallback
+        top = np.abs(v).max(axis=1)
+        assert (top >= 2 ** 62).any() and (top < 2 ** 43).any()
+    with pytest.raises(RuntimeError, match="code -22"):
+        call("detllm_igemv_merge_ext", w, C, R, N, K, ks, R * N, ag, g(om), 7, 9, g(ext), 9,
+             fm, fk, defer, None, 0, None, 0)
+
+
 def test_fused_gemv_argument_errors():
     """Rows beyond 8, aliased residual buffers and shapes the fused kernel
     does not cover are refused before any launch (the last with -38, the
