@@ -687,9 +687,13 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, int S, int kvh,
   // per head: the fp64-estimate DI-Exp (intops.h dexp_est) when tpos < 2^23
   // (every score difference is below 2^22: |q8 . k8| <= 2^21), else the
   // integer form
+  // (the fused kernel's constants are written during the score pass and
+  // read after the maxima's barrier)
   i64 tph[G];
+  if (!PRE) {
 #pragma unroll
-  for (int hh = 0; hh < G; ++hh) tph[hh] = tsrc[hh];
+    for (int hh = 0; hh < G; ++hh) tph[hh] = tsrc[hh];
+  }
 
   // ---- pass 1: scores on MFMA; masked slots marked; per-head row max.
   // Lane (grp, l16) holds C[4 grp + r][slot l16] in element r.
@@ -781,6 +785,10 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, int S, int kvh,
     if (hh + 1 < G) hmax[hh + 1] = r1 == SCORE_MASKED ? 0 : r1;
   }
   __syncthreads();
+  if (PRE) {
+#pragma unroll
+    for (int hh = 0; hh < G; ++hh) tph[hh] = tsrc[hh];
+  }
   // ---- pass 2: denominators (two heads per block reduction). When every
   // head takes the estimate path (the usual case), one loop serves all heads
   // and two slots per thread, the LDS reads of an iteration issued together.
@@ -989,6 +997,7 @@ __global__ __launch_bounds__(QAD_WAVES * 64) void k_qkv_attn_decode(DecodeArgs a
   extern __shared__ __attribute__((aligned(16))) int32_t sh_scores[];
   __shared__ __attribute__((aligned(16))) int8_t q_lds[G][128];
   __shared__ int64_t t_lds[G];
+  __shared__ int64_t am_lds[G];
   const int kvh = blockIdx.x, b = blockIdx.y;
   const int w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));  // wave-uniform
   // (kernel arguments pass through opaque_* below: the optimizer would
@@ -1098,8 +1107,8 @@ __global__ __launch_bounds__(QAD_WAVES * 64) void k_qkv_attn_decode(DecodeArgs a
   }
   // 3. the epilogue
   if (slotw >= 0)
-    qkv_head_compute(qa, b, slotw, in, w < G ? q_lds[w] : nullptr, w < G ? &t_lds[w] : nullptr,
-                     w == G ? k_new : nullptr);
+    qkv_head_compute(qa, b, slotw, in, w < G ? q_lds[w] : nullptr, nullptr,
+                     w == G ? k_new : nullptr, w < G ? &am_lds[w] : nullptr);
   if (slotw >= 0) qkv_head_report(qa, slotw, in);
 #pragma unroll
   for (int it = 0; it < IT; ++it)
@@ -1114,6 +1123,11 @@ __global__ __launch_bounds__(QAD_WAVES * 64) void k_qkv_attn_decode(DecodeArgs a
     if (i < npages) pg_lds[i] = pgv[q];  // (loaded unconditionally above)
   }
   __syncthreads();
+  // the query heads' DI-Exp constants (one lane's serial chain per head) on
+  // the last wave, while the others start the scores; decode_body reads
+  // them after its maxima's barrier
+  if (w == NW - 1 && lane < G)
+    t_lds[lane] = q_head_tpos(qa, am_lds[lane], in.ksm, in.ksk, nullptr);
   decode_body<G, VPRE_FUSED, SCR, true, NW, true>(a, S, kvh, b, &q_lds[0][0], t_lds, sh_scores,
                                                   pg_lds, pre, omp);
   report_slots(a, over, kvh == 0);

@@ -405,13 +405,39 @@ __device__ __forceinline__ void qkv_head_report(const QKVArgs& a, int slotw, con
   if (in.pos_bad && !is_v && (threadIdx.x & 63) == 0 && a.err) atomicOr(a.err, DI_ERR_POSITION);
 }
 
+// A query head's DI-Exp constant from its int8 row's quantisation maximum
+// am: the scale fit of am * 2^-20-normalised (m, k) (quant_i8_pertoken's
+// (m, k)), the score scale norm_scale(qm * ks_m, qk + ks_k) (model.py:
+// 351-353) and di_exp_tpos of it. One lane's serial chain.
+__device__ __forceinline__ i64 q_head_tpos(const QKVArgs& a, i64 am, i64 ksm, i64 ksk,
+                                           i64* dbg4) {
+  const i64 qkk = 20 + a.q_norm_k + a.qs_k;
+  i64 m, k;
+  norm_scale(1, qkk, &m, &k);
+  i64 qm, e;
+  fit_dyadic_ratio_127(wmul(am, m), &qm, &e);
+  const i64 qk = wadd(k, e);
+  // score scale: norm_scale(qm * ks_m[h//g], qk + ks_k[h//g])   (model.py:351-353)
+  i64 sm, sk;
+  norm_scale(wmul(qm, ksm), wadd(qk, ksk), &sm, &sk);
+  if (dbg4) {
+    dbg4[0] = qm;
+    dbg4[1] = qk;
+    dbg4[2] = sm;
+    dbg4[3] = sk;
+  }
+  return di_exp_tpos_fast(sm, sk);
+}
+
 // The whole wave must be active. K and V go to the cache; a query head's
 // int8 row goes to q8_out[0..128) and its DI-Exp constant to *tpos_out
-// (global memory for the standalone kernel, LDS for the fused one). `in`:
-// qkv_head_load then qkv_head_rope_load of the same (r, slotw).
+// (global memory for the standalone kernel, LDS for the fused one), or,
+// with am_out, its quantisation maximum am to *am_out for q_head_tpos
+// later. `in`: qkv_head_load then qkv_head_rope_load of the same (r, slotw).
 __device__ __forceinline__ void qkv_head_compute(const QKVArgs& a, int r, int slotw,
                                                  const QKVHeadIn& in, int8_t* q8_out,
-                                                 int64_t* tpos_out, int8_t* k_lds = nullptr) {
+                                                 int64_t* tpos_out, int8_t* k_lds = nullptr,
+                                                 int64_t* am_out = nullptr) {
   const int lane = threadIdx.x & 63;
   const int b = r / a.T, t = r - b * a.T;
   const bool is_q = slotw < a.n_q, is_v = slotw >= a.n_q + a.n_kv;
@@ -538,24 +564,10 @@ __device__ __forceinline__ void qkv_head_compute(const QKVArgs& a, int r, int sl
   }
   q8_out[c0] = (int8_t)o[0];
   q8_out[c1] = (int8_t)o[1];
-  const i64 qkk = 20 + a.q_norm_k + a.qs_k;
-  i64 m, k;
-  norm_scale(1, qkk, &m, &k);
   const i64 qrow = (((i64)b * a.n_q + h) * a.T + t);
   if (lane == 0) {
-    i64 qm, e;
-    fit_dyadic_ratio_127(wmul(am, m), &qm, &e);
-    const i64 qk = wadd(k, e);
-    // score scale: norm_scale(qm * ks_m[h//g], qk + ks_k[h//g])   (model.py:351-353)
-    i64 sm, sk;
-    norm_scale(wmul(qm, ksm), wadd(qk, ksk), &sm, &sk);
-    *tpos_out = di_exp_tpos_fast(sm, sk);
-    if (a.dbg) {
-      a.dbg[qrow * 4 + 0] = qm;
-      a.dbg[qrow * 4 + 1] = qk;
-      a.dbg[qrow * 4 + 2] = sm;
-      a.dbg[qrow * 4 + 3] = sk;
-    }
+    if (am_out) *am_out = am;
+    else *tpos_out = q_head_tpos(a, am, ksm, ksk, a.dbg ? a.dbg + qrow * 4 : nullptr);
   }
 }
 
