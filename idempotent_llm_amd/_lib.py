@@ -42,6 +42,7 @@ SIGNATURES = {
     "detllm_igemv_swiglu": [P, P, I, I, I, L, P, I, L, P, P, P, L, P, L, P, L, P, P, I, P, L, P,
                             L, S],
     "detllm_merge_rowcol": [P, I, L, I, I, P, L, P, L, P, P, P, P, I, I, I, I, S],
+    "detllm_merge_ext": [P, I, I, P, L, L, P, I, P, P, P, P, I, I, I, I, S],
     "detllm_qkv_epilogue": [P, I, L, I, I, I, I, P, P, P, P, L, P, L, P, L, P, L, P, L, P, L,
                             P, P, P, P, P, P, P, P, L, P, P, P, P, P, P, I, P, L, P, P, S],
     "detllm_kq_est": [P, P, L, L, P, S],

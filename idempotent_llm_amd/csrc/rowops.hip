@@ -1035,6 +1035,65 @@ __device__ __forceinline__ void merge_rowcol_row(const MergeArgs& a, int r, Red&
   if (red.tid() == 0 && a.am) merge_row_scale(a, r, a2, sh);
 }
 
+// The merge of decode rows from the attention's row statistics (a.ext,
+// a.n_ext <= 8 entries per row): every value is elementwise once the row's
+// pre-shift and maximum are known, so each row is cut into 256-column
+// pieces, one block each (one column per thread, no reduction), after the
+// L2-warming blocks of the next GEMV. A row outside the estimate tiers is
+// merged in full by each of its piece blocks (the same bytes; piece 0 stores
+// the scale). C <= 2048.
+constexpr int MEXT_MAX = 8;  // statistics entries per row
+template <bool WARM>
+__global__ __launch_bounds__(256) void k_merge_ext(MergeArgs a, int pieces) {
+  keep_hidden_args();
+  __shared__ i64 red_buf[32];
+  if (WARM && (int)blockIdx.x < L2WARM_BLOCKS) {  // no kernel argument needed to decide
+    l2_warm(a.warm, blockIdx.x, 256, red_buf);
+    return;
+  }
+  const int bid = (int)blockIdx.x - (WARM ? L2WARM_BLOCKS : 0);
+  const int r = bid / pieces, piece = bid - r * pieces;
+  const int C = a.C;
+  const int c = piece * 256 + (int)threadIdx.x;
+  // the value, its factor and the row's statistics (the same entries on
+  // every lane), all issued before any is used
+  const i64 x = buf_ld_i64(buf_view(a.attn + (i64)r * C, (i64)C * 8), c < C ? (uint32_t)c * 8 : BUF_OOB);
+  const i64 om = buf_ld_i64(buf_view(a.os_m, (i64)C * 8), c < C ? (uint32_t)c * 8 : BUF_OOB);
+  v4i q[MEXT_MAX];
+  {
+    const bufv_t ev = buf_view(a.ext + (i64)r * a.n_ext * 2, (i64)a.n_ext * 16);
+#pragma unroll
+    for (int e = 0; e < MEXT_MAX; ++e) q[e] = buf_ld_16<v4i>(ev, e < a.n_ext ? (uint32_t)e * 16 : BUF_OOB);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  i64 vmax = 0, nmin = -1;
+#pragma unroll
+  for (int e = 0; e < MEXT_MAX; ++e) {
+    const i64 hi = (i64)(((u64)(uint32_t)q[e][1] << 32) | (uint32_t)q[e][0]);
+    const i64 nm = (i64)(((u64)(uint32_t)q[e][3] << 32) | (uint32_t)q[e][2]);
+    vmax = imax(vmax, hi);
+    nmin = imax(nmin, e < a.n_ext ? nm : (i64)-1);
+  }
+  i64 sh = 0, a2 = 1;
+  const bool fast = merge_shift_ext(vmax, ~nmin, &sh, &a2) && a2 < ((i64)1 << 46);
+  int8_t* const a8 = a.a8 + (i64)r * (a.a8_stride ? a.a8_stride : C);
+  if (DI_LIKELY(fast)) {  // uniform: the row's statistics
+    const DivEst D = make_divest(a2, 127.0);
+    const i64 v = rshift_round(wmul(x, om), sh);
+    const int qv = a2 < ((i64)1 << 43) ? rhad_est_signed(v, D) : rhad_est_corr_signed(v, 127, a2, D);
+    if (c < C) a8[c] = (int8_t)qv;
+    if (piece == 0 && threadIdx.x == 0 && a.am) merge_row_scale(a, r, a2, sh);
+    return;
+  }
+  MergeArgs m = a;
+  if (piece != 0) {
+    m.am = nullptr;
+    m.ak = nullptr;
+  }
+  BlockRedT<4> red{red_buf, 0, 256};
+  merge_rowcol_row<8>(m, r, red);
+}
+
 template <int VPT, int NT = RT_WIDE, bool WARM = false>
 __global__ __launch_bounds__(NT) void k_merge_rowcol(MergeArgs a) {
   keep_hidden_args();
@@ -2068,6 +2127,29 @@ int detllm_merge_rowcol(const int64_t* attn, int nsplit, int64_t split_stride, i
   a.defer_fit = defer_fit;
   a.warm = warm_for(R, next_w, next_n, next_k, next_ksplit);
   DI_WARM_OR_ROWS(R, C, k_merge_rowcol, s, a);
+  DI_LAUNCH_CHECK();
+  return DI_OK;
+}
+
+int detllm_merge_ext(const int64_t* attn, int R, int C, const int64_t* om, int64_t os_k,
+                     int64_t col_k, const int64_t* ext, int n_ext, int8_t* a8, int64_t* am,
+                     int64_t* ak, const int8_t* next_w, int next_n, int next_k, int next_ksplit,
+                     int defer_fit, hipStream_t s) {
+  if (R <= 0) return DI_OK;
+  if (C <= 0 || C > 2048 || R > 64 || !attn || !om || !ext || n_ext < 1 || n_ext > MEXT_MAX ||
+      !a8 || !am || !ak || (defer_fit != 0 && defer_fit != 1))
+    return DI_EINVAL;
+  MergeArgs a{};
+  a.C = C; a.nt = 256; a.attn = attn; a.nsplit = 1; a.split_stride = 0; a.os_m = om;
+  a.os_k = os_k; a.col_m = nullptr; a.col_k = col_k; a.a8 = a8; a.am = am; a.ak = ak;
+  a.defer_fit = defer_fit; a.ext = ext; a.n_ext = n_ext;
+  a.warm = warm_for(R, next_w, next_n, next_k, next_ksplit);
+  const int pieces = (C + 255) / 256;
+  if (a.warm.nwarm > 0)
+    hipLaunchKernelGGL(k_merge_ext<true>, dim3(L2WARM_BLOCKS + R * pieces), dim3(256), 0, s, a,
+                       pieces);
+  else
+    hipLaunchKernelGGL(k_merge_ext<false>, dim3(R * pieces), dim3(256), 0, s, a, pieces);
   DI_LAUNCH_CHECK();
   return DI_OK;
 }

@@ -52,12 +52,11 @@ GREEDY_CHUNK = 2048
 DEC_MAX_SLOTS = 131071
 # decode rows scanning at least this many slots use the split-S attention
 SPLIT_MIN_SLOTS = 2048
-# decode batches up to this many rows take the o-GEMV that quantises its own
-# K range of the merged rows (detllm_igemv_merge_ext, which covers 8 rows):
-# at one row it replaces the fused merge's row reductions (c3 b1 1.136 ->
-# 1.126 ms per step); at eight rows every block quantising all eight rows of
-# its range outlasts the separate merge launch (1.408 -> 1.418)
-MERGE_EXT_ROWS = 1
+# decode batches up to this many rows have the attention write the merge's
+# row statistics: one row takes the o-GEMV that quantises its own K range of
+# the merged row (detllm_igemv_merge_ext: c3 b1 1.136 -> 1.126 ms per step),
+# more rows the merge launch cut into 256-column pieces (detllm_merge_ext)
+MERGE_EXT_ROWS = 8
 
 
 @dataclass
@@ -679,19 +678,15 @@ class IntQwen3:
         # decode sizes: the merge and the SwiGLU leave their scale fits to the
         # residual kernel after the next GEMM (same integers)
         dfit = 1 if R <= 64 else 0
-        ks = self._ksplit(H, nq * hd, R) if attn[3] is not None else 0
-        if attn[3] is not None and pro_fits(nq * hd, ks):
-            # the o-GEMV quantises its own K range of the merged rows from the
-            # attention's row statistics (no merge launch)
-            P = torch.empty(ks, R, H, dtype=torch.int32, device=dev)
-            ns, st = ks, R * H
-            call("detllm_igemv_merge_ext", L.wo, P, R, H, nq * hd, ks, st, attn[0], L.osc_m,
-                 L.os_k, L.attn_out_col_k, attn[3], self.n_kv, am, ak, dfit, L.pf_o,
-                 L.pf_o.numel() * 8, None, 0)
+        if attn[3] is not None:
+            # the merge from the attention's row statistics: elementwise, in
+            # 256-column pieces (no row reduction)
+            call("detllm_merge_ext", attn[0], R, nq * hd, L.osc_m, L.os_k, L.attn_out_col_k,
+                 attn[3], self.n_kv, a8, am, ak, *self._next_gemm(L.wo, R), dfit)
         else:
             call("detllm_merge_rowcol", *attn[:3], R, nq * hd, L.os_m, L.os_k,
                  L.attn_out_col_m, L.attn_out_col_k, a8, am, ak, *self._next_gemm(L.wo, R), dfit)
-            P, ns, st = self._gemm(a8, L.wo, (L.pf_o,))
+        P, ns, st = self._gemm(a8, L.wo, (L.pf_o,))
         call("detllm_residual_normq", P, ns, st, R, H, am, ak, L.o_m, L.o_k, 20, h, k_res,
              L.ms_m, L.ms_k, x8, xm, xk, *self._next_gemm(L.wgu, R), dfit)
         P, ns, st = self._gemm(x8, L.wgu, (L.pf_mlp,))

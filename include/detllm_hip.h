@@ -170,6 +170,17 @@ int detllm_igemv_resnormq(const int8_t* W, int32_t* C, int R, int N, int K, int 
                           const void* pf0, int64_t n0, const void* pf1, int64_t n1,
                           hipStream_t s);
 
+/* detllm_merge_rowcol of decode rows (one partial of attn [R][C], C <= 2048,
+ * R <= 64) from the row statistics detllm_qkv_attn_decode_ext writes (ext
+ * [R][n_ext][2], n_ext = n_kv <= 8): every value elementwise — the same
+ * integers as requant_i8_rowcol (dyadic.py:123-139, model.py:404-409) — in
+ * 256-column pieces, one block each. om [C]: the per-column product
+ * os_m * col_m; the other arguments as detllm_merge_rowcol's. */
+int detllm_merge_ext(const int64_t* attn, int R, int C, const int64_t* om, int64_t os_k,
+                     int64_t col_k, const int64_t* ext, int n_ext, int8_t* a8, int64_t* am,
+                     int64_t* ak, const int8_t* next_w, int next_n, int next_k, int next_ksplit,
+                     int defer_fit, hipStream_t s);
+
 /* detllm_igemv_merge_ext: detllm_igemv_merge (one partial of attn [R][K])
  * whose merge statistics come from ext [R][n_ext][2] as
  * detllm_qkv_attn_decode_ext writes them (n_ext = n_kv), so each block

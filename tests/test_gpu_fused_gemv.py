@@ -219,6 +219,47 @@ def test_igemv_merge_ext_equals_two_launches(R, N, ks_pick, defer):
              fm, fk, defer, None, 0, None, 0)
 
 
+@pytest.mark.parametrize("R,C,n_ext", [(1, 2048, 8), (3, 1000, 5), (8, 2048, 8), (17, 2048, 8)])
+@pytest.mark.parametrize("defer", [0, 1])
+def test_merge_ext_equals_merge_rowcol(R, C, n_ext, defer):
+    """detllm_merge_ext (the merge from the attention's row statistics, in
+    256-column pieces) against detllm_merge_rowcol: equal int8 rows and row
+    scales, fitted and deferred, with rows in every quantiser tier, a zero
+    row, ragged columns, and rows at or beyond 2^62 (wrapping products) that
+    each piece block merges in full."""
+    from idempotent_llm_amd._lib import call
+    print(f"[merge_ext R={R} C={C} n_ext={n_ext} defer={defer}]", flush=True)
+    rng = np.random.default_rng(R * 131 + C + n_ext + defer)
+    base = [1 << 20, 1 << 39, 1 << 5, 0, 1 << 23, 1 << 29, 1 << 12, 1 << 38]
+    mags = [base[i % 8] for i in range(R)] if R > 1 else [1 << 26]
+    attn = np.stack([rng.integers(-m, m + 1, C) if m else np.zeros(C, I64) for m in mags]).astype(I64)
+    os_m = rng.integers(1 << 10, 1 << 12, C).astype(I64)
+    col_m = rng.integers(1 << 10, 1 << 12, C).astype(I64)
+    om = os_m * col_m
+    with np.errstate(over="ignore"):
+        v = attn * om
+    ext = _merge_stats(v, n_ext)
+    ag = g(attn)
+    want8 = torch.full((R, C), 99, dtype=torch.int8, device="cuda")
+    wm = torch.empty(R, dtype=torch.int64, device="cuda")
+    wk = torch.empty(R, dtype=torch.int64, device="cuda")
+    call("detllm_merge_rowcol", ag, 1, R * C, R, C, g(os_m), 7, g(col_m), 9, want8, wm, wk, None,
+         0, 0, 0, defer)
+    w = torch.zeros(4096, C, dtype=torch.int8, device="cuda")   # warming blocks' target
+    for rep in range(2):
+        a8 = torch.full((R, C), 99, dtype=torch.int8, device="cuda")
+        am = torch.full((R,), -1, dtype=torch.int64, device="cuda")
+        ak = torch.full((R,), -1, dtype=torch.int64, device="cuda")
+        call("detllm_merge_ext", ag, R, C, g(om), 7, 9, g(ext), n_ext, a8, am, ak,
+             w if rep else None, 4096 if rep else 0, C if rep else 0, 1, defer)
+        torch.cuda.synchronize()
+        assert torch.equal(a8, want8)
+        assert torch.equal(am, wm) and torch.equal(ak, wk)
+    if R == 8:
+        top = np.abs(v).max(axis=1)
+        assert (top >= 2 ** 62).any() and (top < 2 ** 43).any()
+
+
 def test_fused_gemv_argument_errors():
     """Rows beyond 8, aliased residual buffers and shapes the fused kernel
     does not cover are refused before any launch (the last with -38, the
