@@ -147,7 +147,7 @@ def c3_hashes(model):
 
 
 def c3_step_bytes(model, B: int, mean_slots: float) -> float:
-    """Bytes one decode step must move (SURVEY-style count): every weight
+    """Bytes one decode step must move (an algorithmic count): every weight
     matrix and LM head once, the per-channel scale vectors, and per row the
     embedding row, the new K/V rows, the int32 logits and the K/V of the
     scanned slots."""
