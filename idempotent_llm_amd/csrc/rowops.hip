@@ -856,13 +856,13 @@ __device__ __forceinline__ void swiglu_quant_row(const SwigluArgs& a, int r, Red
 }
 
 #ifndef SWIGLU_MINB
-#define SWIGLU_MINB 3
+#define SWIGLU_MINB 4
 #endif
 
-// Prefill (256-thread blocks, 8-12 columns per thread): at least three blocks
-// per CU (168 VGPRs; 12 columns spill a few registers) beat two unspilled
-// blocks by ~3 % on a 2048-token prefill (measured; four blocks spill more and
-// lose).
+// Prefill (256-thread blocks, 8-12 columns per thread): at least four blocks
+// per CU (128 VGPRs; 12 columns spill some registers to scratch) — measured
+// on the 2048-token MLP block: 80.7 us against 82.2 at three blocks (168
+// VGPRs) and 86.7 at two.
 template <int VPT, int NT = RT_WIDE, bool WARM = false>
 __global__ __launch_bounds__(NT, (NT == 256 && VPT >= 8 && VPT <= 12) ? SWIGLU_MINB : 1) void k_swiglu_quant(
     SwigluArgs a) {
